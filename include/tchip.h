@@ -1,0 +1,307 @@
+/*
+ * tchip.h — the C ABI of the MI355X `Hip` storage and kernel backend for
+ * tensorcrate.
+ *
+ * Every entry point takes plain device pointers, element counts and small
+ * plain-old-data layout structs; nothing here names a C++ or torch type, so a
+ * Rust `extern "C"` block (or ctypes, or cgo) binds it directly.  Each
+ * declaration cites the reference interface it stands in for, as
+ * `<file>:<line>` under arthurmburke/tensorcrate's `src/`.
+ *
+ * Conventions
+ *  - Every function returns a `tc_status`.  On failure `tc_last_error()` holds
+ *    a message for the calling thread, worded like the reference's panic for
+ *    the same mistake ("strided copy: shape [..] ... reaches past N
+ *    elements").  Layout checks run on the host before any launch, so a bad
+ *    layout never reaches the GPU.
+ *  - All work is queued asynchronously on one HIP stream per host thread and
+ *    ordered on it; `tc_sync` waits for it.  Host pointers passed to
+ *    `tc_upload` / `tc_download` are done with when the call returns.
+ *  - Element counts and strides are in elements of the operand's type, not
+ *    bytes, as the reference's `Strided`/`Region` are (backend.rs:199-213).
+ *  - Storage is not shared between threads: a pointer is allocated, used and
+ *    freed on one thread, as the reference's Metal tensors are not `Send`.
+ */
+#ifndef TCHIP_H
+#define TCHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The deepest layout a strided operation takes: `MAX_RANK` (tensors/layout.rs:16). */
+#define TC_MAX_RANK 6
+/* Registers, inputs, outputs, instructions and loads of one fused program
+ * (tensors/fused/mod.rs:119-132, :483). */
+#define TC_FUSED_REGISTERS 16
+#define TC_FUSED_MAX_INPUTS 16
+#define TC_FUSED_MAX_OUTPUTS 8
+#define TC_FUSED_MAX_INSTRUCTIONS 256
+#define TC_FUSED_MAX_LOADS 64
+/* Row axes a fused program's place folds together (fused/mod.rs:3236). */
+#define TC_FUSED_LEAD 5
+
+typedef enum tc_status {
+    TC_OK = 0,
+    TC_INVALID = 1,     /* a shape, layout or argument the reference would panic on */
+    TC_UNSUPPORTED = 2, /* a type or operation with no kernel: never a silent fallback */
+    TC_DEVICE = 3,      /* a HIP runtime error */
+    TC_OUT_OF_MEMORY = 4
+} tc_status;
+
+/* Storage and arithmetic types: `fused::DType` (fused/mod.rs:145-150). */
+typedef enum tc_dtype { TC_F32 = 0, TC_F16 = 1, TC_BF16 = 2, TC_F64 = 3 } tc_dtype;
+
+/* `BinaryOp` (tensors/kernels.rs:32-38). */
+typedef enum tc_binary_op { TC_ADD = 0, TC_SUB = 1, TC_MUL = 2, TC_DIV = 3, TC_REM = 4 } tc_binary_op;
+
+/* `Compare` (tensors/kernels.rs:106-122). */
+typedef enum tc_compare_op {
+    TC_MIN = 0, TC_MAX = 1, TC_MAX_SHARE = 2,
+    TC_LESS = 3, TC_LESS_EQUAL = 4, TC_GREATER = 5, TC_GREATER_EQUAL = 6
+} tc_compare_op;
+
+/* `Reduce` (tensors/kernels.rs:183-187). */
+typedef enum tc_reduce_op { TC_REDUCE_SUM = 0, TC_REDUCE_MIN = 1, TC_REDUCE_MAX = 2 } tc_reduce_op;
+
+/* `Pairwise` (tensors/kernels.rs:411-415): the kind, then the `BinaryOp` or
+ * `Compare` code in a separate argument. */
+typedef enum tc_pairwise { TC_PAIR_ARITHMETIC = 0, TC_PAIR_COMPARE = 1, TC_PAIR_POWER = 2 } tc_pairwise;
+
+/* `AxisReduction` (tensors/kernels.rs:449-457): `Fold(Reduce)`, `Mean`, or
+ * `Variance { divisor }`. */
+typedef enum tc_axis_reduction { TC_AXIS_FOLD = 0, TC_AXIS_MEAN = 1, TC_AXIS_VARIANCE = 2 } tc_axis_reduction;
+
+/* `Transposed` (tensors/kernels.rs:462-467), with `TC_PLAIN` for neither. */
+typedef enum tc_transposed { TC_PLAIN = 0, TC_LEFT = 1, TC_RIGHT = 2 } tc_transposed;
+
+/* One side of a strided copy: element [i0..] of a shape is storage element
+ * `offset + sum(i_k * strides[k])` (`Strided`, tensors/backend.rs:199-202). */
+typedef struct tc_strided {
+    uint64_t offset;
+    uint64_t strides[TC_MAX_RANK];
+} tc_strided;
+
+/* One block of an assemble or a strided write: `shape` copied from `source`
+ * (holding `source_len` elements) at `from` to the target at `to`
+ * (`Region`, tensors/backend.rs:208-213). */
+typedef struct tc_region {
+    const void* source;
+    uint64_t source_len;
+    uint32_t rank;
+    uint64_t shape[TC_MAX_RANK];
+    tc_strided from;
+    tc_strided to;
+} tc_region;
+
+/* A layout split for a reduction (`Split`, tensors/layout.rs:370-376): result
+ * [k..] folds storage elements `offset + sum(k_i kept_strides[i]) +
+ * sum(f_j folded_strides[j])` over every index [f..] of `folded`. */
+typedef struct tc_split {
+    uint64_t offset;
+    uint32_t kept_rank;
+    uint64_t kept[TC_MAX_RANK];
+    uint64_t kept_strides[TC_MAX_RANK];
+    uint32_t folded_rank;
+    uint64_t folded[TC_MAX_RANK];
+    uint64_t folded_strides[TC_MAX_RANK];
+} tc_split;
+
+/* One instruction of a fused program as the kernels read it, twelve bytes
+ * (`Encoded`, tensors/fused/mod.rs:1391-1410):
+ *   kind 0 load  : op = load index, dst, a = input slot, b = storage dtype
+ *   kind 1 const : dst, value
+ *   kind 2 binary: op = BinaryOp, dst, a, b
+ *   kind 3 unary : op = Analytic, dst, a
+ *   kind 4 cmp   : op = Compare, dst, a, b
+ *   kind 5 store : a = source register, b = storage dtype, aux = output slot */
+typedef struct tc_encoded {
+    uint16_t kind;
+    uint16_t op;
+    uint8_t dst;
+    uint8_t a;
+    uint8_t b;
+    uint8_t aux;
+    float value;
+} tc_encoded;
+
+/* Where element (row, col) of a rows x cols walk reads a load: storage
+ * element `offset + col*col_step`, plus the row split over the `lead` axes
+ * it folds together, outermost first (`Place`, fused/mod.rs:3229-3268). */
+typedef struct tc_place {
+    uint64_t offset;
+    uint64_t col_step;
+    uint32_t lead;
+    uint64_t dims[TC_FUSED_LEAD];
+    uint64_t steps[TC_FUSED_LEAD];
+} tc_place;
+
+/* ---- context, stream, errors ------------------------------------------- */
+
+/* Select the device for the calling thread and create its stream.  Every
+ * other entry point calls it for device 0 if the thread has not.  Replaces
+ * the thread-local Metal device (metal/device.rs:309-313). */
+int tc_init(int device);
+
+/* The last failure's message on this thread ("" when none).  The Rust side
+ * maps it onto the panic `require_metal` raises (tensors/backend.rs:422-426). */
+const char* tc_last_error(void);
+
+/* Wait for all work queued by this thread, and report any asynchronous
+ * failure — the HIP form of `sync` (metal/sync.rs:225-259). */
+int tc_sync(void);
+
+/* The calling thread's HIP stream (a `hipStream_t`), for callers that order
+ * their own work against this library's. */
+int tc_stream(void** stream);
+
+/* The device's marketing name and architecture string, e.g. "gfx950". */
+int tc_device_info(char* name, size_t name_len, char* arch, size_t arch_len);
+
+/* GPU time between `tc_timer_begin` and `tc_timer_end` on this thread's
+ * stream, in milliseconds; `tc_timer_end` waits for the stream. */
+int tc_timer_begin(void);
+int tc_timer_end(float* milliseconds);
+
+/* ---- storage (Backend, tensors/backend.rs:86-111) ---------------------- */
+
+/* Device storage of `bytes` from this thread's stream-ordered cache.
+ * `Backend::store` / `from_vec` allocate with this and then upload. */
+int tc_alloc(size_t bytes, void** out);
+/* Return storage to the calling thread's cache; work already queued that
+ * reads it still completes first (the pool fence of metal/pool.rs:34-48). */
+int tc_free(void* pointer);
+/* Give every cached, unused block back to the device. */
+int tc_empty_cache(void);
+/* Host to device, device to host (`as_slice`, backend.rs:99; the download
+ * waits for queued work), and device to device (`duplicate`, backend.rs:111). */
+int tc_upload(void* device_dst, const void* host_src, size_t bytes);
+int tc_download(void* host_dst, const void* device_src, size_t bytes);
+int tc_copy(void* device_dst, const void* device_src, size_t bytes);
+/* `count` elements of `width` bytes set to `*value` on the device: the
+ * device-side `Vector::filled` / `Matrix::filled` (vector.rs:101,
+ * matrix.rs:112), so a zero adjoint is never a host upload. */
+int tc_fill(void* dst, uint64_t count, uint32_t width, const void* value);
+
+/* ---- strided copies (Backend, tensors/backend.rs:141-173) --------------- */
+
+/* `Backend::strided_copy` (backend.rs:141-145; Host backend.rs:255-274):
+ * the `rank`-axis layout `from` of `src` (holding `src_len` elements of
+ * `width` bytes, width 1/2/4/8/16) copied row-major into `dst`, which holds
+ * the product of `shape` elements. */
+int tc_strided_copy(uint32_t width, const void* src, uint64_t src_len, uint32_t rank,
+                    const uint64_t* shape, const tc_strided* from, void* dst);
+
+/* `Backend::assemble` (backend.rs:157-160; Host backend.rs:303-323): each
+ * region copied into `dst` of `len` elements.  Elements no region writes are
+ * left as they were (the reference leaves them unspecified). */
+int tc_assemble(uint32_t width, void* dst, uint64_t len, const tc_region* regions, uint32_t count);
+
+/* `Backend::strided_write` (backend.rs:170-173; Host backend.rs:277-300):
+ * `region` copied into `target` (holding `target_len` elements) in place. */
+int tc_strided_write(uint32_t width, void* target, uint64_t target_len, const tc_region* region);
+
+/* ---- elementwise (Kernels, tensors/kernels.rs:832-863, :912-938) -------- */
+
+/* `vector_elementwise` / `matrix_elementwise` (kernels.rs:832, :912):
+ * out[i] = a[i] op b[i], one rounding to `dtype`. */
+int tc_elementwise(uint32_t dtype, uint32_t op, const void* a, const void* b, void* out, uint64_t n);
+/* `vector_broadcast` / `matrix_broadcast` (kernels.rs:838, :918):
+ * out[i] = a[i] op s, or s op a[i] when `scalar_left`.  `scalar` is a value
+ * of `dtype`, which float holds exactly. */
+int tc_broadcast(uint32_t dtype, uint32_t op, const void* a, float scalar, int scalar_left,
+                 void* out, uint64_t n);
+/* `vector_compare` / `matrix_compare` (kernels.rs:846, :926). */
+int tc_compare(uint32_t dtype, uint32_t op, const void* a, const void* b, void* out, uint64_t n);
+/* `vector_compare_scalar` / `matrix_compare_scalar` (kernels.rs:849, :929). */
+int tc_compare_scalar(uint32_t dtype, uint32_t op, const void* a, float scalar, int scalar_left,
+                      void* out, uint64_t n);
+/* `vector_clamp` / `matrix_clamp` (kernels.rs:863, :938): fails unless
+ * low <= high. */
+int tc_clamp(uint32_t dtype, const void* a, float low, float high, void* out, uint64_t n);
+
+/* `Kernels::strided_binary` (kernels.rs:1162-1166; Host strided.rs:29-78):
+ * op(a, b) over `shape`, each operand read in place through its own layout
+ * (a zero stride repeats an element, as a broadcast does), into the
+ * row-major `out`.  `kind` is a `tc_pairwise`; `op` its BinaryOp or Compare. */
+int tc_strided_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank,
+                      const uint64_t* shape, const void* a, uint64_t a_len, const tc_strided* a_at,
+                      const void* b, uint64_t b_len, const tc_strided* b_at, void* out);
+
+/* ---- reductions (kernels.rs:867, :1175, :1187) -------------------------- */
+
+/* `Kernels::reduce_axes` (kernels.rs:1175-1179; Host strided.rs:105-162):
+ * one result per kept index, folded over `split->folded`, accumulated in f32
+ * and rounded to `dtype` once.  `kind` is a `tc_axis_reduction`; `op` the
+ * `Reduce` of a fold; `divisor` the variance's divisor
+ * (statistics/mod.rs:96-101).  Every slice holds at least one element. */
+int tc_reduce_axes(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split,
+                   uint32_t kind, uint32_t op, uint64_t divisor, void* out);
+
+/* `Kernels::arg_reduce` (kernels.rs:1187; Host strided.rs:186-225): the
+ * u32 position along the one folded axis of each slice's first maximum
+ * (`op` TC_REDUCE_MAX) or minimum (TC_REDUCE_MIN); NaNs are passed over and
+ * an all-NaN slice answers 0.  `split` folds exactly one axis. */
+int tc_arg_reduce(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split,
+                  uint32_t op, uint32_t* out);
+
+/* `Kernels::vector_reduce` (kernels.rs:867): the whole buffer folded; the
+ * f32 accumulator is written to the device scalar `result`, unrounded, as
+ * Metal's `reduce` returns it (tensors/backend.rs:813-818). */
+int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result);
+
+/* `Kernels::dot` (kernels.rs:897): sum a[i]*b[i] into the device f32 scalar
+ * `result`, unrounded. */
+int tc_dot(uint32_t dtype, const void* a, const void* b, uint64_t n, float* result);
+
+/* ---- products (kernels.rs:897-908, :956-987) ---------------------------- */
+
+/* `Kernels::matmul` / `matmul_add` / `matmul_transposed_add`
+ * (kernels.rs:956, :963, :975; Host matrix.rs:580-667, compact.rs:232-253):
+ *   transposed TC_PLAIN: C[m x n] (+)= A[m x k] . B[k x n]
+ *   transposed TC_LEFT : C (+)= A^T . B with A stored k x m
+ *   transposed TC_RIGHT: C (+)= A . B^T with B stored n x k
+ * all row-major.  `accumulate` adds to C (the addend the reference consumes
+ * as its accumulator) instead of overwriting it.  A and B are `in_dtype`,
+ * accumulation is f32, and C is `out_dtype`: `in_dtype` itself, or TC_F32
+ * for the compact types' `matmul_f32`.  k == 0 gives zeros (or the addend). */
+int tc_matmul(uint32_t in_dtype, uint32_t out_dtype, uint32_t transposed, int accumulate,
+              uint64_t m, uint64_t k, uint64_t n, const void* a, const void* b, void* c);
+
+/* `Kernels::matvec` / `matvec_add` (kernels.rs:901-908; Host matrix.rs:675-737):
+ * y[rows] (+)= M[rows x cols] . v[cols]. */
+int tc_matvec(uint32_t dtype, int accumulate, uint64_t rows, uint64_t cols,
+              const void* matrix, const void* vector, void* out);
+
+/* `Kernels::vecmat` (kernels.rs:899; vector.rs:491): y[cols] = v[rows] . M[rows x cols]. */
+int tc_vecmat(uint32_t dtype, uint64_t rows, uint64_t cols, const void* vector,
+              const void* matrix, void* out);
+
+/* `Kernels::transpose` (kernels.rs:987; matrix.rs:740, :1173-1206): the
+ * cols x rows transpose of a rows x cols matrix of `width`-byte elements. */
+int tc_transpose(uint32_t width, uint64_t rows, uint64_t cols, const void* src, void* dst);
+
+/* ---- fused programs (kernels.rs:1077-1082; fused/mod.rs:959-1011) ------- */
+
+/* `Kernels::fused`: run `count` encoded instructions for every element of a
+ * rows x cols space, computing in `dtype`.  Load `k` reads through
+ * `places[k]` from `inputs[slot]`; a store writes element row*cols + col of
+ * `outputs[slot]`.  An in-place tensor is both an input and an output, and
+ * is loaded unremapped before it is stored, so every element is read by the
+ * thread that writes it.  `code`, `places` and the two length arrays are
+ * host arrays; `input_lens[k]` / `output_lens[k]` count the elements of
+ * each buffer, and a load or store that would reach past one is refused
+ * before launch (`Program::run`'s checks, fused/mod.rs:978-986). */
+int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+             uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+             uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
+             uint32_t output_count, uint64_t rows, uint64_t cols);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TCHIP_H */

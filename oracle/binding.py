@@ -1,0 +1,245 @@
+"""ctypes binding of ``liboracle.so``, the CPU restatement of the Host backend.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg, as the checker and the timed CPU
+baseline.  The product (``tensorcrate_amd``) never imports it.  Each wrapper
+takes numpy arrays in the element type's host form (bf16 as uint16 bits) and
+returns numpy arrays.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / "liboracle.so"
+
+F32, F16, BF16 = 0, 1, 2
+NUMPY = {F32: np.float32, F16: np.float16, BF16: np.uint16}
+MAX_RANK = 6
+
+u32, u64, vp, f32, i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
+
+
+class Encoded(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_uint16), ("op", ctypes.c_uint16), ("dst", ctypes.c_uint8), ("a", ctypes.c_uint8),
+                ("b", ctypes.c_uint8), ("aux", ctypes.c_uint8), ("value", ctypes.c_float)]
+
+
+class Place(ctypes.Structure):
+    _fields_ = [("offset", u64), ("col_step", u64), ("lead", u32), ("dims", u64 * 5), ("steps", u64 * 5)]
+
+
+_SIGNATURES = {
+    "or_bf16_from_f32": ([f32], ctypes.c_uint16),
+    "or_f16_from_f32": ([f32], ctypes.c_uint16),
+    "or_f16_to_f32": ([ctypes.c_uint16], f32),
+    "or_narrow": ([u32, vp, vp, u64], None),
+    "or_widen": ([u32, vp, vp, u64], None),
+    "or_strided_copy": ([u32, vp, u32, vp, u64, vp, vp], u64),
+    "or_strided_write": ([u32, vp, vp, u32, vp, u64, vp, u64, vp], None),
+    "or_binary": ([u32, u32, u32, u32, vp, vp, u64, vp, vp, u64, vp, vp], None),
+    "or_elementwise": ([u32, u32, u32, vp, vp, vp, u64], None),
+    "or_scalar": ([u32, u32, u32, vp, f32, i32, vp, u64], None),
+    "or_clamp": ([u32, vp, f32, f32, vp, u64], None),
+    "or_reduce": ([u32, vp, u32, vp, u64, vp, u32, vp, u32, u32, u64, vp], None),
+    "or_arg_reduce": ([u32, vp, u32, vp, u64, vp, u32, u32, vp], None),
+    "or_matmul_f32": ([vp, vp, u64, u64, u64, vp, i32], None),
+    "or_matmul": ([u32, u32, vp, vp, u64, u64, u64, vp, i32], None),
+    "or_transpose": ([u32, vp, u64, u64, vp], None),
+    "or_dot": ([u32, vp, vp, u64], f32),
+    "or_matvec": ([u32, vp, vp, u64, u64, vp, i32], None),
+    "or_vecmat": ([u32, vp, vp, u64, u64, vp], None),
+    "or_fold": ([u32, vp, u64, u32], f32),
+    "or_fused": ([u32, vp, u32, vp, vp, vp, u64, u64], None),
+}
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIBRARY
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            build()
+        lib = ctypes.CDLL(str(LIBRARY))
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes, fn.restype = args, res
+        _lib = lib
+    return _lib
+
+
+def _p(array: np.ndarray) -> int:
+    return array.ctypes.data
+
+
+def _dims(values) -> np.ndarray:
+    out = np.zeros(MAX_RANK, np.uint64)
+    out[: len(values)] = values
+    return out
+
+
+def bf16_from_f32(values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.empty(values.shape, np.uint16)
+    load().or_narrow(BF16, _p(values), _p(out), values.size)
+    return out
+
+
+def f16_from_f32(values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.empty(values.shape, np.uint16)
+    load().or_narrow(F16, _p(values), _p(out), values.size)
+    return out.view(np.float16)
+
+
+def widen(dtype: int, values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values)
+    out = np.empty(values.shape, np.float32)
+    load().or_widen(dtype, _p(values), _p(out), values.size)
+    return out
+
+
+def narrow(dtype: int, values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.empty(values.shape, NUMPY[dtype])
+    load().or_narrow(dtype, _p(values), _p(out), values.size)
+    return out
+
+
+def strided_copy(src: np.ndarray, shape, offset, strides) -> np.ndarray:
+    src = np.ascontiguousarray(src).reshape(-1)
+    count = int(np.prod(shape, dtype=np.int64)) if len(shape) else 1
+    out = np.empty(count, src.dtype)
+    d_shape, d_strides = _dims(shape), _dims(strides)
+    load().or_strided_copy(src.itemsize, _p(src), len(shape), _p(d_shape), offset, _p(d_strides), _p(out))
+    return out.reshape(shape)
+
+
+def strided_write(src: np.ndarray, target: np.ndarray, shape, from_offset, from_strides, to_offset, to_strides):
+    src = np.ascontiguousarray(src).reshape(-1)
+    assert target.flags.c_contiguous and target.dtype == src.dtype
+    d_shape, d_from, d_to = _dims(shape), _dims(from_strides), _dims(to_strides)
+    load().or_strided_write(src.itemsize, _p(src), _p(target), len(shape), _p(d_shape), from_offset, _p(d_from),
+                            to_offset, _p(d_to))
+
+
+def binary(dtype, kind, op, shape, a, a_offset, a_strides, b, b_offset, b_strides) -> np.ndarray:
+    a = np.ascontiguousarray(a).reshape(-1)
+    b = np.ascontiguousarray(b).reshape(-1)
+    count = int(np.prod(shape, dtype=np.int64)) if len(shape) else 1
+    out = np.empty(count, NUMPY[dtype])
+    d_shape, d_a, d_b = _dims(shape), _dims(a_strides), _dims(b_strides)
+    load().or_binary(dtype, kind, op, len(shape), _p(d_shape), _p(a), a_offset, _p(d_a), _p(b), b_offset, _p(d_b),
+                     _p(out))
+    return out.reshape(shape)
+
+
+def elementwise(dtype, kind, op, a, b) -> np.ndarray:
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    out = np.empty(a.shape, NUMPY[dtype])
+    load().or_elementwise(dtype, kind, op, _p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def scalar(dtype, kind, op, a, value, scalar_left) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.empty(a.shape, NUMPY[dtype])
+    load().or_scalar(dtype, kind, op, _p(a), value, int(scalar_left), _p(out), a.size)
+    return out
+
+
+def clamp(dtype, a, low, high) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.empty(a.shape, NUMPY[dtype])
+    load().or_clamp(dtype, _p(a), low, high, _p(out), a.size)
+    return out
+
+
+def reduce(dtype, values, shape, offset, strides, axes, kind, op=0, divisor=0) -> np.ndarray:
+    values = np.ascontiguousarray(values).reshape(-1)
+    kept = [shape[k] for k in range(len(shape)) if k not in axes]
+    count = int(np.prod(kept, dtype=np.int64)) if kept else 1
+    out = np.empty(count, NUMPY[dtype])
+    axes_array = np.array(sorted(axes), np.uint32)
+    d_shape, d_strides = _dims(shape), _dims(strides)
+    load().or_reduce(dtype, _p(values), len(shape), _p(d_shape), offset, _p(d_strides), len(axes), _p(axes_array),
+                     kind, op, divisor, _p(out))
+    return out.reshape(kept)
+
+
+def arg_reduce(dtype, values, shape, offset, strides, axis, op) -> np.ndarray:
+    values = np.ascontiguousarray(values).reshape(-1)
+    kept = [shape[k] for k in range(len(shape)) if k != axis]
+    count = int(np.prod(kept, dtype=np.int64)) if kept else 1
+    out = np.empty(count, np.uint32)
+    d_shape, d_strides = _dims(shape), _dims(strides)
+    load().or_arg_reduce(dtype, _p(values), len(shape), _p(d_shape), offset, _p(d_strides), axis, op, _p(out))
+    return out.reshape(kept)
+
+
+def matmul(in_dtype, a, b, m, k, n, out_dtype=None, addend=None) -> np.ndarray:
+    out_dtype = in_dtype if out_dtype is None else out_dtype
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    out = (np.array(addend, NUMPY[out_dtype]).reshape(-1).copy() if addend is not None
+           else np.empty(m * n, NUMPY[out_dtype]))
+    load().or_matmul(in_dtype, out_dtype, _p(a), _p(b), m, k, n, _p(out), int(addend is not None))
+    return out.reshape(m, n)
+
+
+def transpose(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    rows, cols = a.shape
+    out = np.empty((cols, rows), a.dtype)
+    load().or_transpose(a.itemsize, _p(a), rows, cols, _p(out))
+    return out
+
+
+def dot(dtype, a, b) -> float:
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    return load().or_dot(dtype, _p(a), _p(b), a.size)
+
+
+def matvec(dtype, m, v, addend=None) -> np.ndarray:
+    m, v = np.ascontiguousarray(m), np.ascontiguousarray(v)
+    rows, cols = m.shape
+    out = np.array(addend, NUMPY[dtype]).copy() if addend is not None else np.empty(rows, NUMPY[dtype])
+    load().or_matvec(dtype, _p(m), _p(v), rows, cols, _p(out), int(addend is not None))
+    return out
+
+
+def vecmat(dtype, v, m) -> np.ndarray:
+    m, v = np.ascontiguousarray(m), np.ascontiguousarray(v)
+    rows, cols = m.shape
+    out = np.empty(cols, NUMPY[dtype])
+    load().or_vecmat(dtype, _p(v), _p(m), rows, cols, _p(out))
+    return out
+
+
+def fold(dtype, a, op) -> float:
+    a = np.ascontiguousarray(a)
+    return load().or_fold(dtype, _p(a), a.size, op)
+
+
+def fused(dtype, code, places, inputs, outputs, rows, cols) -> None:
+    """Run an encoded program; ``code`` is a list of (kind, op, dst, a, b, aux,
+    value) and ``places`` of (offset, col_step, lead, dims, steps)."""
+    enc = (Encoded * max(len(code), 1))(*[Encoded(*c) for c in code])
+    pl = (Place * max(len(places), 1))()
+    for k, (offset, col_step, lead, dims, steps) in enumerate(places):
+        pl[k].offset, pl[k].col_step, pl[k].lead = offset, col_step, lead
+        for d in range(len(dims)):
+            pl[k].dims[d], pl[k].steps[d] = dims[d], steps[d]
+    ins = (vp * max(len(inputs), 1))(*[_p(x) for x in inputs])
+    outs = (vp * max(len(outputs), 1))(*[_p(x) for x in outputs])
+    load().or_fused(dtype, enc, len(code), pl, ins, outs, rows, cols)

@@ -1,0 +1,771 @@
+/*
+ * CPU restatement of tensorcrate's Host backend for the Hip backend's hot
+ * path.  TEST INFRASTRUCTURE: the checker the GPU results are compared with
+ * and the timed CPU baseline, never part of the product (see oracle.h).
+ *
+ * Each function follows the reference's own loop structure and arithmetic
+ * order, cited per function as src/<file>:<line> of arthurmburke/tensorcrate,
+ * so that where the Host backend is deterministic (copies, elementwise ops,
+ * sequential folds, the f32 FMA-chain product, the fused interpreter) this
+ * gives its bits.  Built with -ffp-contract=off: every multiply and add the
+ * reference writes separately stays separate, and FMA appears only where the
+ * reference calls one (_mm256_fmadd_ps, restated with fmaf).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+
+#define MAX_RANK 6
+
+enum { F32 = 0, F16 = 1, BF16 = 2 };
+
+/* ---- conversions (half 2.7.1, called at compact.rs:40-57) ---------------- */
+
+static uint32_t bits_of(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    return x;
+}
+
+static float float_of(uint32_t x) {
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* Round-to-nearest-even with NaN quieting; the rule metal/common.h:153-165
+ * restates from `half::bf16::from_f32`. */
+uint16_t or_bf16_from_f32(float value) {
+    uint32_t x = bits_of(value);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+    uint32_t round_bit = 0x00008000u;
+    if ((x & round_bit) != 0 && (x & (3u * round_bit - 1u)) != 0) return (uint16_t)((x >> 16) + 1);
+    return (uint16_t)(x >> 16);
+}
+
+static float bf16_to_f32(uint16_t bits) { return float_of((uint32_t)bits << 16); }
+
+/* `value >> shift` rounded to nearest, ties to even. */
+static uint32_t shift_rne(uint32_t value, uint32_t shift) {
+    if (shift == 0) return value;
+    if (shift > 31) return 0;
+    uint32_t q = value >> shift;
+    uint32_t rem = value & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return q;
+}
+
+/* IEEE binary32 -> binary16, round to nearest even; NaNs keep their top
+ * payload bits and are quieted, as `half::f16::from_f32` does. */
+uint16_t or_f16_from_f32(float value) {
+    uint32_t x = bits_of(value);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xffu) {
+        if (man != 0) return (uint16_t)(sign | 0x7e00u | (man >> 13));
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    int e = (int)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        /* A subnormal half: the value over 2^-24, rounded. */
+        if (exp == 0) return (uint16_t)sign; /* f32 subnormals are far below half's */
+        uint32_t significand = man | 0x800000u;
+        uint32_t shift = (uint32_t)(126 - (int)exp);
+        return (uint16_t)(sign | shift_rne(significand, shift));
+    }
+    /* Adding a rounded-up mantissa carries into the exponent, and from the
+     * largest exponent into infinity, as it should. */
+    uint32_t rounded = shift_rne(man, 13);
+    return (uint16_t)(sign + ((uint32_t)e << 10) + rounded);
+}
+
+float or_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0x1fu) return float_of(sign | 0x7f800000u | (man << 13));
+    if (exp == 0) {
+        if (man == 0) return float_of(sign);
+        /* subnormal: man * 2^-24, exact in f32 */
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    return float_of(sign | ((exp - 15 + 127) << 23) | (man << 13));
+}
+
+static float widen_one(uint32_t dtype, const void* p, uint64_t i) {
+    switch (dtype) {
+        case F16: return or_f16_to_f32(((const uint16_t*)p)[i]);
+        case BF16: return bf16_to_f32(((const uint16_t*)p)[i]);
+        default: return ((const float*)p)[i];
+    }
+}
+
+static void narrow_one(uint32_t dtype, void* p, uint64_t i, float v) {
+    switch (dtype) {
+        case F16: ((uint16_t*)p)[i] = or_f16_from_f32(v); break;
+        case BF16: ((uint16_t*)p)[i] = or_bf16_from_f32(v); break;
+        default: ((float*)p)[i] = v; break;
+    }
+}
+
+/* A value rounded to the element type and back. */
+static float in_type(uint32_t dtype, float v) {
+    switch (dtype) {
+        case F16: return or_f16_to_f32(or_f16_from_f32(v));
+        case BF16: return bf16_to_f32(or_bf16_from_f32(v));
+        default: return v;
+    }
+}
+
+void or_narrow(uint32_t dtype, const float* in, void* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) narrow_one(dtype, out, i, in[i]);
+}
+
+void or_widen(uint32_t dtype, const void* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = widen_one(dtype, in, i);
+}
+
+/* ---- layout walk (layout.rs:419-498) --------------------------------------- */
+
+typedef struct walk {
+    uint32_t rank;
+    uint64_t shape[MAX_RANK];
+    uint64_t strides[3][MAX_RANK];
+} walk;
+
+/* `coalesce` (layout.rs:419-449) over n operands. */
+static walk coalesce(uint32_t rank, const uint64_t* shape, uint32_t n, const uint64_t* const* strides) {
+    walk w;
+    memset(&w, 0, sizeof w);
+    for (uint32_t axis = 0; axis < rank; axis++) {
+        uint64_t extent = shape[axis];
+        if (extent == 1) continue;
+        uint32_t r = w.rank;
+        int joins = r > 0;
+        for (uint32_t o = 0; joins && o < n; o++) joins = w.strides[o][r - 1] == strides[o][axis] * extent;
+        if (joins) {
+            w.shape[r - 1] *= extent;
+            for (uint32_t o = 0; o < n; o++) w.strides[o][r - 1] = strides[o][axis];
+        } else {
+            w.shape[r] = extent;
+            for (uint32_t o = 0; o < n; o++) w.strides[o][r] = strides[o][axis];
+            w.rank++;
+        }
+    }
+    return w;
+}
+
+typedef void (*run_fn)(void* context, const uint64_t* starts, uint64_t len, const uint64_t* steps);
+
+/* `for_each_run` (layout.rs:457-498): one call per innermost run, in
+ * row-major order; none for an empty shape, one of one element for a scalar. */
+static void for_each_run(uint32_t rank, const uint64_t* shape, uint32_t n, const uint64_t* offsets,
+                         const uint64_t* const* strides, run_fn run, void* context) {
+    for (uint32_t k = 0; k < rank; k++)
+        if (shape[k] == 0) return;
+    walk w = coalesce(rank, shape, n, strides);
+    uint64_t at[3] = {0, 0, 0};
+    for (uint32_t o = 0; o < n; o++) at[o] = offsets[o];
+    if (w.rank == 0) {
+        uint64_t zero[3] = {0, 0, 0};
+        run(context, at, 1, zero);
+        return;
+    }
+    uint64_t inner = w.shape[w.rank - 1];
+    uint64_t steps[3] = {0, 0, 0};
+    for (uint32_t o = 0; o < n; o++) steps[o] = w.strides[o][w.rank - 1];
+    uint64_t index[MAX_RANK] = {0};
+    for (;;) {
+        run(context, at, inner, steps);
+        uint32_t axis = w.rank - 1;
+        for (;;) {
+            if (axis == 0) return;
+            axis--;
+            index[axis]++;
+            for (uint32_t o = 0; o < n; o++) at[o] += w.strides[o][axis];
+            if (index[axis] < w.shape[axis]) break;
+            for (uint32_t o = 0; o < n; o++) at[o] -= w.strides[o][axis] * w.shape[axis];
+            index[axis] = 0;
+        }
+    }
+}
+
+/* ---- strided copies (backend.rs:255-300) ----------------------------------- */
+
+typedef struct copy_ctx {
+    uint32_t width;
+    const uint8_t* src;
+    uint8_t* out;
+    uint64_t written;
+} copy_ctx;
+
+static void copy_run(void* c, const uint64_t* starts, uint64_t len, const uint64_t* steps) {
+    copy_ctx* ctx = (copy_ctx*)c;
+    uint32_t w = ctx->width;
+    if (steps[0] == 1) {
+        memcpy(ctx->out + ctx->written * w, ctx->src + starts[0] * w, len * w);
+    } else {
+        for (uint64_t i = 0; i < len; i++)
+            memcpy(ctx->out + (ctx->written + i) * w, ctx->src + (starts[0] + i * steps[0]) * w, w);
+    }
+    ctx->written += len;
+}
+
+uint64_t or_strided_copy(uint32_t width, const void* src, uint32_t rank, const uint64_t* shape, uint64_t offset,
+                         const uint64_t* strides, void* out) {
+    copy_ctx ctx = {width, (const uint8_t*)src, (uint8_t*)out, 0};
+    const uint64_t* s[1] = {strides};
+    uint64_t offsets[1] = {offset};
+    for_each_run(rank, shape, 1, offsets, s, copy_run, &ctx);
+    return ctx.written;
+}
+
+typedef struct write_ctx {
+    uint32_t width;
+    const uint8_t* src;
+    uint8_t* target;
+} write_ctx;
+
+static void write_run(void* c, const uint64_t* starts, uint64_t len, const uint64_t* steps) {
+    write_ctx* ctx = (write_ctx*)c;
+    uint32_t w = ctx->width;
+    for (uint64_t i = 0; i < len; i++)
+        memcpy(ctx->target + (starts[1] + i * steps[1]) * w, ctx->src + (starts[0] + i * steps[0]) * w, w);
+}
+
+void or_strided_write(uint32_t width, const void* src, void* target, uint32_t rank, const uint64_t* shape,
+                      uint64_t from_offset, const uint64_t* from_strides, uint64_t to_offset,
+                      const uint64_t* to_strides) {
+    write_ctx ctx = {width, (const uint8_t*)src, (uint8_t*)target};
+    const uint64_t* s[2] = {from_strides, to_strides};
+    uint64_t offsets[2] = {from_offset, to_offset};
+    for_each_run(rank, shape, 2, offsets, s, write_run, &ctx);
+}
+
+/* ---- elementwise (kernels.rs:98-153, :431-441) ---------------------------- */
+
+/* `Compare::value` (kernels.rs:138-153). */
+static float compare_value(uint32_t op, float a, float b) {
+    switch (op) {
+        case 0: return fminf(a, b);
+        case 1: return fmaxf(a, b);
+        case 2: return a > b ? 1.0f : (a < b ? 0.0f : 0.5f);
+        case 3: return a < b ? 1.0f : 0.0f;
+        case 4: return a <= b ? 1.0f : 0.0f;
+        case 5: return a > b ? 1.0f : 0.0f;
+        default: return a >= b ? 1.0f : 0.0f;
+    }
+}
+
+static float arithmetic_value(uint32_t op, float a, float b) {
+    switch (op) {
+        case 0: return a + b;
+        case 1: return a - b;
+        case 2: return a * b;
+        case 3: return a / b;
+        default: return fmodf(a, b); /* Rust `%` on floats: the truncated remainder */
+    }
+}
+
+/* `Pairwise::value` (kernels.rs:431-441) for T of `dtype`: the f32 result
+ * rounded to T once, which for f16 and bf16 is the correctly rounded value
+ * `half`'s operators give; a power is f32 `powf` then one rounding
+ * (numbers/primitive.rs:131-156). */
+static float pairwise(uint32_t dtype, uint32_t kind, uint32_t op, float a, float b) {
+    float v;
+    if (kind == 0) v = arithmetic_value(op, a, b);
+    else if (kind == 1) v = compare_value(op, a, b);
+    else v = powf(a, b);
+    return in_type(dtype, v);
+}
+
+typedef struct binary_ctx {
+    uint32_t dtype, kind, op;
+    const void *a, *b;
+    void* out;
+    uint64_t written;
+} binary_ctx;
+
+static void binary_run(void* c, const uint64_t* starts, uint64_t len, const uint64_t* steps) {
+    binary_ctx* ctx = (binary_ctx*)c;
+    for (uint64_t k = 0; k < len; k++) {
+        float x = widen_one(ctx->dtype, ctx->a, starts[0] + k * steps[0]);
+        float y = widen_one(ctx->dtype, ctx->b, starts[1] + k * steps[1]);
+        narrow_one(ctx->dtype, ctx->out, ctx->written + k, pairwise(ctx->dtype, ctx->kind, ctx->op, x, y));
+    }
+    ctx->written += len;
+}
+
+void or_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank, const uint64_t* shape, const void* a,
+               uint64_t a_offset, const uint64_t* a_strides, const void* b, uint64_t b_offset,
+               const uint64_t* b_strides, void* out) {
+    binary_ctx ctx = {dtype, kind, op, a, b, out, 0};
+    const uint64_t* s[2] = {a_strides, b_strides};
+    uint64_t offsets[2] = {a_offset, b_offset};
+    for_each_run(rank, shape, 2, offsets, s, binary_run, &ctx);
+}
+
+void or_elementwise(uint32_t dtype, uint32_t kind, uint32_t op, const void* a, const void* b, void* out,
+                    uint64_t n) {
+    for (uint64_t i = 0; i < n; i++)
+        narrow_one(dtype, out, i, pairwise(dtype, kind, op, widen_one(dtype, a, i), widen_one(dtype, b, i)));
+}
+
+void or_scalar(uint32_t dtype, uint32_t kind, uint32_t op, const void* a, float scalar, int scalar_left, void* out,
+               uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) {
+        float x = widen_one(dtype, a, i);
+        float v = scalar_left ? pairwise(dtype, kind, op, scalar, x) : pairwise(dtype, kind, op, x, scalar);
+        narrow_one(dtype, out, i, v);
+    }
+}
+
+/* `clamp` (kernels.rs:856-863): the pair of comparisons in one pass. */
+void or_clamp(uint32_t dtype, const void* a, float low, float high, void* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) narrow_one(dtype, out, i, fminf(fmaxf(widen_one(dtype, a, i), low), high));
+}
+
+/* ---- reductions (strided.rs:80-225) ---------------------------------------- */
+
+static int in_axes(uint32_t axis, uint32_t naxes, const uint32_t* axes) {
+    for (uint32_t k = 0; k < naxes; k++)
+        if (axes[k] == axis) return 1;
+    return 0;
+}
+
+/* `result_strides` (strided.rs:83-100). */
+static void result_strides(uint32_t rank, const uint64_t* shape, uint32_t naxes, const uint32_t* axes,
+                           uint64_t* out) {
+    uint64_t kept[MAX_RANK];
+    uint32_t nkept = 0;
+    for (uint32_t a = 0; a < rank; a++)
+        if (!in_axes(a, naxes, axes)) kept[nkept++] = shape[a];
+    uint64_t kept_strides[MAX_RANK];
+    uint64_t step = 1;
+    for (int k = (int)nkept - 1; k >= 0; k--) {
+        kept_strides[k] = step;
+        step *= kept[k];
+    }
+    uint32_t next = 0;
+    for (uint32_t a = 0; a < rank; a++) out[a] = in_axes(a, naxes, axes) ? 0 : kept_strides[next++];
+}
+
+enum { FOLD_SUM, FOLD_MIN, FOLD_MAX, FOLD_DEVIATION };
+
+typedef struct fold_ctx {
+    uint32_t dtype, mode;
+    const void* input;
+    float* acc;
+    const float* means;
+} fold_ctx;
+
+/* `Reduce::combine` (kernels.rs:205-211) and the deviation fold of
+ * strided.rs:150-153, into accumulator `slot`. */
+static void fold_run(void* c, const uint64_t* starts, uint64_t len, const uint64_t* steps) {
+    fold_ctx* ctx = (fold_ctx*)c;
+    for (uint64_t k = 0; k < len; k++) {
+        uint64_t slot = starts[1] + k * steps[1];
+        float x = widen_one(ctx->dtype, ctx->input, starts[0] + k * steps[0]);
+        float t = ctx->acc[slot];
+        switch (ctx->mode) {
+            case FOLD_SUM: t = t + x; break;
+            case FOLD_MIN: t = fminf(t, x); break;
+            case FOLD_MAX: t = fmaxf(t, x); break;
+            default: {
+                float d = x - ctx->means[slot];
+                t = t + d * d;
+            }
+        }
+        ctx->acc[slot] = t;
+    }
+}
+
+static void fold_all(uint32_t dtype, const void* input, uint32_t rank, const uint64_t* shape, uint64_t offset,
+                     const uint64_t* strides, const uint64_t* to, uint32_t mode, float* acc, const float* means) {
+    fold_ctx ctx = {dtype, mode, input, acc, means};
+    const uint64_t* s[2] = {strides, to};
+    uint64_t offsets[2] = {offset, 0};
+    for_each_run(rank, shape, 2, offsets, s, fold_run, &ctx);
+}
+
+/* `reduce_in` with the f32 accumulator (strided.rs:119-162). */
+void or_reduce(uint32_t dtype, const void* input, uint32_t rank, const uint64_t* shape, uint64_t offset,
+               const uint64_t* strides, uint32_t naxes, const uint32_t* axes, uint32_t kind, uint32_t op,
+               uint64_t divisor, void* out) {
+    uint64_t to[MAX_RANK];
+    result_strides(rank, shape, naxes, axes, to);
+    uint64_t results = 1, depth = 1;
+    for (uint32_t a = 0; a < rank; a++) {
+        if (in_axes(a, naxes, axes)) depth *= shape[a];
+        else results *= shape[a];
+    }
+    float count = (float)(double)depth;
+    float* totals = (float*)malloc((results ? results : 1) * sizeof(float));
+    if (kind == 0) {
+        float identity = op == 0 ? 0.0f : (op == 1 ? INFINITY : -INFINITY);
+        for (uint64_t r = 0; r < results; r++) totals[r] = identity;
+        fold_all(dtype, input, rank, shape, offset, strides, to, op == 0 ? FOLD_SUM : (op == 1 ? FOLD_MIN : FOLD_MAX),
+                 totals, NULL);
+    } else {
+        for (uint64_t r = 0; r < results; r++) totals[r] = 0.0f;
+        fold_all(dtype, input, rank, shape, offset, strides, to, FOLD_SUM, totals, NULL);
+        for (uint64_t r = 0; r < results; r++) totals[r] = totals[r] / count;
+        if (kind == 2) {
+            float* means = totals;
+            float* deviations = (float*)malloc((results ? results : 1) * sizeof(float));
+            for (uint64_t r = 0; r < results; r++) deviations[r] = 0.0f;
+            fold_all(dtype, input, rank, shape, offset, strides, to, FOLD_DEVIATION, deviations, means);
+            float d = (float)(double)divisor;
+            for (uint64_t r = 0; r < results; r++) totals[r] = deviations[r] / d;
+            free(deviations);
+        }
+    }
+    for (uint64_t r = 0; r < results; r++) narrow_one(dtype, out, r, totals[r]);
+    free(totals);
+}
+
+typedef struct arg_ctx {
+    uint32_t dtype, op;
+    const void* input;
+    float* best;
+    uint32_t* positions;
+} arg_ctx;
+
+/* `replaces` (strided.rs:188-197): a number that beats the best so far, or
+ * any number over a NaN best. */
+static int replaces(uint32_t op, float x, float best) {
+    if (isnan(x)) return 0;
+    return isnan(best) || (op == 1 ? x < best : x > best);
+}
+
+static void arg_run(void* c, const uint64_t* starts, uint64_t len, const uint64_t* steps) {
+    arg_ctx* ctx = (arg_ctx*)c;
+    for (uint64_t k = 0; k < len; k++) {
+        uint64_t slot = starts[1] + k * steps[1];
+        float x = widen_one(ctx->dtype, ctx->input, starts[0] + k * steps[0]);
+        if (replaces(ctx->op, x, ctx->best[slot])) {
+            ctx->best[slot] = x;
+            ctx->positions[slot] = (uint32_t)(starts[2] + k * steps[2]);
+        }
+    }
+}
+
+void or_arg_reduce(uint32_t dtype, const void* input, uint32_t rank, const uint64_t* shape, uint64_t offset,
+                   const uint64_t* strides, uint32_t axis, uint32_t op, uint32_t* out) {
+    uint64_t to[MAX_RANK], along[MAX_RANK] = {0};
+    uint32_t axes[1] = {axis};
+    result_strides(rank, shape, 1, axes, to);
+    along[axis] = 1;
+    uint64_t results = 1;
+    for (uint32_t a = 0; a < rank; a++)
+        if (a != axis) results *= shape[a];
+    float* best = (float*)malloc((results ? results : 1) * sizeof(float));
+    for (uint64_t r = 0; r < results; r++) {
+        best[r] = NAN;
+        out[r] = 0;
+    }
+    arg_ctx ctx = {dtype, op, input, best, out};
+    const uint64_t* s[3] = {strides, to, along};
+    uint64_t offsets[3] = {offset, 0, 0};
+    for_each_run(rank, shape, 3, offsets, s, arg_run, &ctx);
+    free(best);
+}
+
+/* ---- products (matrix.rs:580-745, simd_x86.rs:57-101, :1261-1327) --------- */
+
+#define HOST_MATMUL_DISPATCH_OPS 512 /* tensors/mod.rs:167 */
+
+static int has_avx2_fma(void) {
+#if defined(__x86_64__)
+    static int known = -1;
+    if (known < 0) known = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    return known;
+#else
+    return 0;
+#endif
+}
+
+#if defined(__x86_64__)
+__attribute__((target("avx2,fma"))) static void matmul_accumulate_avx(const float* a, const float* b, uint64_t m,
+                                                                      uint64_t k, uint64_t n, float* out) {
+    for (uint64_t i = 0; i < m; i++) {
+        const uint64_t arow = i * k, orow = i * n;
+        for (uint64_t p = 0; p < k; p++) {
+            const float value = a[arow + p];
+            const __m256 broadcast = _mm256_set1_ps(value);
+            const uint64_t brow = p * n;
+            uint64_t j = 0;
+            for (; j + 8 <= n; j += 8) {
+                __m256 rhs = _mm256_loadu_ps(b + brow + j);
+                __m256 current = _mm256_loadu_ps(out + orow + j);
+                _mm256_storeu_ps(out + orow + j, _mm256_fmadd_ps(broadcast, rhs, current));
+            }
+            for (; j < n; j++) out[orow + j] += value * b[brow + j];
+        }
+    }
+}
+#endif
+
+/* `matmul_avx` (simd_x86.rs:1302-1327): i, p, j; each eight-lane block is one
+ * FMA per element, the tail a separate multiply and add.  `fmaf` is the
+ * same single rounding as `_mm256_fmadd_ps`. */
+static void matmul_accumulate(const float* a, const float* b, uint64_t m, uint64_t k, uint64_t n, float* out) {
+#if defined(__x86_64__)
+    if (has_avx2_fma()) {
+        matmul_accumulate_avx(a, b, m, k, n, out);
+        return;
+    }
+#endif
+    for (uint64_t i = 0; i < m; i++) {
+        for (uint64_t p = 0; p < k; p++) {
+            const float value = a[i * k + p];
+            uint64_t j = 0;
+            for (; j + 8 <= n; j += 8)
+                for (uint64_t l = 0; l < 8; l++) out[i * n + j + l] = fmaf(value, b[p * n + j + l], out[i * n + j + l]);
+            for (; j < n; j++) out[i * n + j] += value * b[p * n + j];
+        }
+    }
+}
+
+void or_matmul_f32(const float* a, const float* b, uint64_t m, uint64_t k, uint64_t n, float* out,
+                   int accumulate) {
+    if (m * k * n < HOST_MATMUL_DISPATCH_OPS) {
+        if (accumulate) {
+            /* matrix.rs:658-665: i, p, j onto the addend. */
+            for (uint64_t i = 0; i < m; i++)
+                for (uint64_t p = 0; p < k; p++)
+                    for (uint64_t j = 0; j < n; j++) out[i * n + j] = out[i * n + j] + a[i * k + p] * b[p * n + j];
+        } else {
+            /* matrix.rs:601-609: i, j, then the sum over p from zero. */
+            for (uint64_t i = 0; i < m; i++)
+                for (uint64_t j = 0; j < n; j++) {
+                    float sum = 0.0f;
+                    for (uint64_t p = 0; p < k; p++) sum = sum + a[i * k + p] * b[p * n + j];
+                    out[i * n + j] = sum;
+                }
+        }
+        return;
+    }
+    if (!accumulate) memset(out, 0, m * n * sizeof(float)); /* f32k::matmul fills with zero */
+    matmul_accumulate(a, b, m, k, n, out);
+}
+
+void or_matmul(uint32_t in_dtype, uint32_t out_dtype, const void* a, const void* b, uint64_t m, uint64_t k,
+               uint64_t n, void* out, int accumulate) {
+    if (in_dtype == F32) {
+        or_matmul_f32((const float*)a, (const float*)b, m, k, n, (float*)out, accumulate);
+        return;
+    }
+    float* wa = (float*)malloc((m * k + 1) * sizeof(float));
+    float* wb = (float*)malloc((k * n + 1) * sizeof(float));
+    float* wc = (float*)malloc((m * n + 1) * sizeof(float));
+    or_widen(in_dtype, a, wa, m * k);
+    or_widen(in_dtype, b, wb, k * n);
+    if (accumulate) or_widen(out_dtype, out, wc, m * n);
+    or_matmul_f32(wa, wb, m, k, n, wc, accumulate);
+    or_narrow(out_dtype, wc, out, m * n);
+    free(wa);
+    free(wb);
+    free(wc);
+}
+
+void or_transpose(uint32_t width, const void* src, uint64_t rows, uint64_t cols, void* out) {
+    const uint8_t* s = (const uint8_t*)src;
+    uint8_t* o = (uint8_t*)out;
+    for (uint64_t j = 0; j < cols; j++)
+        for (uint64_t i = 0; i < rows; i++) memcpy(o + (j * rows + i) * width, s + (i * cols + j) * width, width);
+}
+
+#if defined(__x86_64__)
+__attribute__((target("avx2,fma"))) static float dot_avx(const float* a, const float* b, uint64_t n) {
+    uint64_t i = 0;
+    __m256 acc[4] = {_mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps()};
+    while (i + 32 <= n) {
+        for (int lane = 0; lane < 4; lane++) {
+            uint64_t offset = i + (uint64_t)lane * 8;
+            acc[lane] = _mm256_fmadd_ps(_mm256_loadu_ps(a + offset), _mm256_loadu_ps(b + offset), acc[lane]);
+        }
+        i += 32;
+    }
+    __m256 total = _mm256_add_ps(_mm256_add_ps(acc[0], acc[1]), _mm256_add_ps(acc[2], acc[3]));
+    float lanes[8];
+    _mm256_storeu_ps(lanes, total);
+    float sum = 0.0f;
+    for (int l = 0; l < 8; l++) sum += lanes[l];
+    while (i + 8 <= n) {
+        __m256 product = _mm256_mul_ps(_mm256_loadu_ps(a + i), _mm256_loadu_ps(b + i));
+        _mm256_storeu_ps(lanes, product);
+        float part = 0.0f;
+        for (int l = 0; l < 8; l++) part += lanes[l];
+        sum += part;
+        i += 8;
+    }
+    while (i < n) {
+        sum += a[i] * b[i];
+        i++;
+    }
+    return sum;
+}
+#endif
+
+/* `f32k::dot` = `dot_avx` (simd_x86.rs:57-101), with the same association in
+ * the scalar fallback. */
+static float dot_simd(const float* a, const float* b, uint64_t n) {
+#if defined(__x86_64__)
+    if (has_avx2_fma()) return dot_avx(a, b, n);
+#endif
+    uint64_t i = 0;
+    float acc[4][8] = {{0}};
+    while (i + 32 <= n) {
+        for (int lane = 0; lane < 4; lane++)
+            for (int l = 0; l < 8; l++) acc[lane][l] = fmaf(a[i + lane * 8 + l], b[i + lane * 8 + l], acc[lane][l]);
+        i += 32;
+    }
+    float sum = 0.0f;
+    for (int l = 0; l < 8; l++) sum += (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+    while (i + 8 <= n) {
+        float part = 0.0f;
+        for (int l = 0; l < 8; l++) part += a[i + l] * b[i + l];
+        sum += part;
+        i += 8;
+    }
+    for (; i < n; i++) sum += a[i] * b[i];
+    return sum;
+}
+
+/* `Vector::dot` (vector.rs:468-483): the SIMD dot from 16 elements
+ * (simd_dispatch.rs:77-91), the plain loop below. */
+static float dot_f32(const float* a, const float* b, uint64_t n) {
+    if (n < 16) {
+        float sum = 0.0f;
+        for (uint64_t i = 0; i < n; i++) sum = sum + a[i] * b[i];
+        return sum;
+    }
+    return dot_simd(a, b, n);
+}
+
+float or_dot(uint32_t dtype, const void* a, const void* b, uint64_t n) {
+    if (dtype == F32) return dot_f32((const float*)a, (const float*)b, n);
+    float total = 0.0f; /* compact.rs:177-179: each product exact, one rounding per term */
+    for (uint64_t i = 0; i < n; i++) total = total + widen_one(dtype, a, i) * widen_one(dtype, b, i);
+    return total;
+}
+
+void or_matvec(uint32_t dtype, const void* m, const void* v, uint64_t rows, uint64_t cols, void* out,
+               int accumulate) {
+    if (dtype != F32) {
+        or_matmul(dtype, dtype, m, v, rows, cols, 1, out, accumulate);
+        return;
+    }
+    const float* mm = (const float*)m;
+    const float* vv = (const float*)v;
+    float* o = (float*)out;
+    int simd = rows * cols >= HOST_MATMUL_DISPATCH_OPS;
+    for (uint64_t r = 0; r < rows; r++) {
+        float sum;
+        if (simd) {
+            sum = dot_simd(mm + r * cols, vv, cols);
+        } else {
+            sum = 0.0f;
+            for (uint64_t c = 0; c < cols; c++) sum = sum + mm[r * cols + c] * vv[c];
+        }
+        o[r] = accumulate ? o[r] + sum : sum;
+    }
+}
+
+void or_vecmat(uint32_t dtype, const void* v, const void* m, uint64_t rows, uint64_t cols, void* out) {
+    if (dtype != F32) {
+        or_matmul(dtype, dtype, v, m, 1, rows, cols, out, 0);
+        return;
+    }
+    const float* vv = (const float*)v;
+    const float* mm = (const float*)m;
+    float* o = (float*)out;
+    if (rows * cols >= HOST_MATMUL_DISPATCH_OPS) {
+        or_matmul_f32(vv, mm, 1, rows, cols, o, 0);
+        return;
+    }
+    for (uint64_t j = 0; j < cols; j++) {
+        float sum = 0.0f;
+        for (uint64_t p = 0; p < rows; p++) sum = sum + vv[p] * mm[p * cols + j];
+        o[j] = sum;
+    }
+}
+
+float or_fold(uint32_t dtype, const void* a, uint64_t n, uint32_t op) {
+    float t = op == 0 ? 0.0f : (op == 1 ? INFINITY : -INFINITY);
+    for (uint64_t i = 0; i < n; i++) {
+        float x = widen_one(dtype, a, i);
+        t = op == 0 ? t + x : (op == 1 ? fminf(t, x) : fmaxf(t, x));
+    }
+    return t;
+}
+
+/* ---- fused programs (fused/mod.rs:62-70, :3254-3268) ------------------------ */
+
+static uint64_t place_at(const or_place* p, uint64_t row, uint64_t col) {
+    uint64_t at = p->offset + col * p->col_step;
+    if (p->lead > 0) {
+        for (int k = (int)p->lead - 1; k > 0; k--) {
+            at += (row % p->dims[k]) * p->steps[k];
+            row /= p->dims[k];
+        }
+        at += row * p->steps[0];
+    }
+    return at;
+}
+
+/* `Analytic::value` (kernels.rs:334-354) in f32 libm; only `Sqrt`, which
+ * is IEEE, is pinned bit for bit. */
+static float analytic(uint32_t op, float x) {
+    switch (op) {
+        case 0: return sinf(x);
+        case 1: return cosf(x);
+        case 2: return tanf(x);
+        case 3: return 1.0f / cosf(x);
+        case 4: return 1.0f / sinf(x);
+        case 5: return asinf(x);
+        case 6: return acosf(x);
+        case 7: return atanf(x);
+        case 8: return expf(x);
+        case 9: return logf(x);
+        case 10: return sinhf(x);
+        case 11: return coshf(x);
+        case 12: return tanhf(x);
+        case 13: return sqrtf(x);
+        default: return NAN;
+    }
+}
+
+void or_fused(uint32_t dtype, const or_encoded* code, uint32_t count, const or_place* places,
+              const void* const* inputs, void* const* outputs, uint64_t rows, uint64_t cols) {
+    float r[16] = {0};
+    for (uint64_t row = 0; row < rows; row++) {
+        for (uint64_t col = 0; col < cols; col++) {
+            uint64_t element = row * cols + col;
+            for (uint32_t pc = 0; pc < count; pc++) {
+                const or_encoded* in = &code[pc];
+                switch (in->kind) {
+                    case 0:
+                        r[in->dst] = in_type(dtype, widen_one(in->b, inputs[in->a], place_at(&places[in->op], row, col)));
+                        break;
+                    case 1: r[in->dst] = in->value; break;
+                    case 2: r[in->dst] = in_type(dtype, arithmetic_value(in->op, r[in->a], r[in->b])); break;
+                    case 3: r[in->dst] = in_type(dtype, analytic(in->op, r[in->a])); break;
+                    case 4: r[in->dst] = in_type(dtype, compare_value(in->op, r[in->a], r[in->b])); break;
+                    default: narrow_one(in->b, outputs[in->aux], element, r[in->a]); break;
+                }
+            }
+        }
+    }
+}

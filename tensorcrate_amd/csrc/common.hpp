@@ -1,0 +1,286 @@
+// Shared by every translation unit of libtchip: the runtime hooks the entry
+// points use (error state, the calling thread's stream, launch checks), the
+// element types and their conversions, and the index arithmetic the strided
+// kernels run on.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/tchip.h"
+
+namespace tc {
+
+constexpr int kMaxRank = TC_MAX_RANK;
+
+// ---- runtime hooks (runtime.hip) -------------------------------------------
+
+// Record `message` as this thread's last error and return `status`.
+int fail(int status, const std::string& message);
+// The calling thread's stream, initialising device 0 on first use; nullptr
+// (with the error recorded) if the device cannot be set up.
+hipStream_t stream();
+// TC_OK, or the HIP error from the launch just made, recorded under `what`.
+int check_launch(const char* what);
+// Shorthand: set up the thread's stream or return its failure.
+#define TC_STREAM(var)                                \
+    hipStream_t var = ::tc::stream();                 \
+    if (var == nullptr) return TC_DEVICE
+
+// Number of compute units, for sizing persistent and split grids.
+int compute_units();
+
+std::string shape_text(const uint64_t* values, uint32_t rank);
+
+// ---- element types ----------------------------------------------------------
+
+// bf16 is the top half of an f32, so widening is a shift.
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t bits) {
+    return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+// Round to nearest, ties to even, with NaNs quieted: the rule of
+// `half::bf16::from_f32` that the reference narrows with.  Adding 0x7fff plus
+// the kept bit's lowest bit carries into the kept half exactly when the
+// dropped half is above one half, or exactly one half with an odd kept half.
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float value) {
+    uint32_t x = __float_as_uint(value);
+    if ((x & 0x7fffffffu) > 0x7f800000u) {
+        return static_cast<uint16_t>((x >> 16) | 0x0040u);
+    }
+    return static_cast<uint16_t>((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+}
+
+struct bf16_t {
+    uint16_t bits;
+};
+
+// How a storage type widens to the f32 the kernels compute in, and rounds
+// back once.  f32 is the identity; f16 uses the hardware conversion, which
+// rounds to nearest even.
+template <typename S>
+struct Elem;
+
+template <>
+struct Elem<float> {
+    static constexpr int dtype = TC_F32;
+    __device__ static float widen(float v) { return v; }
+    __device__ static float narrow(float v) { return v; }
+};
+
+template <>
+struct Elem<_Float16> {
+    static constexpr int dtype = TC_F16;
+    __device__ static float widen(_Float16 v) { return static_cast<float>(v); }
+    __device__ static _Float16 narrow(float v) { return static_cast<_Float16>(v); }
+};
+
+template <>
+struct Elem<bf16_t> {
+    static constexpr int dtype = TC_BF16;
+    __device__ static float widen(bf16_t v) { return bf16_bits_to_f32(v.bits); }
+    __device__ static bf16_t narrow(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+};
+
+inline size_t dtype_size(uint32_t dtype) {
+    switch (dtype) {
+        case TC_F32: return 4;
+        case TC_F16:
+        case TC_BF16: return 2;
+        case TC_F64: return 8;
+        default: return 0;
+    }
+}
+
+inline const char* dtype_name(uint32_t dtype) {
+    switch (dtype) {
+        case TC_F32: return "f32";
+        case TC_F16: return "f16";
+        case TC_BF16: return "bf16";
+        case TC_F64: return "f64";
+        default: return "unknown";
+    }
+}
+
+// Call `body` with a value of the storage type `dtype` names (only its type
+// matters); unsupported types are reported, never computed some other way.
+#define TC_DISPATCH_FLOAT(dtype, what, S, ...)                                        \
+    switch (dtype) {                                                                  \
+        case TC_F32: { using S = float; __VA_ARGS__; break; }                         \
+        case TC_F16: { using S = _Float16; __VA_ARGS__; break; }                      \
+        case TC_BF16: { using S = ::tc::bf16_t; __VA_ARGS__; break; }                 \
+        default:                                                                      \
+            return ::tc::fail(TC_UNSUPPORTED, std::string(what) + ": no kernel for " + \
+                                                  ::tc::dtype_name(dtype));           \
+    }
+
+// ---- the scalar operations every kernel shares -----------------------------
+
+// `BinaryOp` in f32 (kernels.rs:431-437); the caller rounds to the element
+// type once.  `Rem` is Rust's `%`, the truncated remainder `fmod`, which is
+// exact.
+__device__ inline float binary_value(uint32_t op, float a, float b) {
+    switch (op) {
+        case TC_ADD: return a + b;
+        case TC_SUB: return a - b;
+        case TC_MUL: return a * b;
+        case TC_DIV: return a / b;
+        default: return fmodf(a, b);
+    }
+}
+
+// `Compare::value` (kernels.rs:138-153): minNum/maxNum, the ½-at-ties share,
+// and predicates that are false on NaN.
+__device__ inline float compare_value(uint32_t op, float a, float b) {
+    switch (op) {
+        case TC_MIN: return fminf(a, b);
+        case TC_MAX: return fmaxf(a, b);
+        case TC_MAX_SHARE: return a > b ? 1.0f : (a < b ? 0.0f : 0.5f);
+        case TC_LESS: return a < b ? 1.0f : 0.0f;
+        case TC_LESS_EQUAL: return a <= b ? 1.0f : 0.0f;
+        case TC_GREATER: return a > b ? 1.0f : 0.0f;
+        default: return a >= b ? 1.0f : 0.0f;
+    }
+}
+
+// `Pairwise::value` (kernels.rs:431-441); a power is f32 `powf`
+// (numbers/primitive.rs:131-156).
+__device__ inline float pairwise_value(uint32_t kind, uint32_t op, float a, float b) {
+    if (kind == TC_PAIR_ARITHMETIC) return binary_value(op, a, b);
+    if (kind == TC_PAIR_COMPARE) return compare_value(op, a, b);
+    return powf(a, b);
+}
+
+// ---- index arithmetic -------------------------------------------------------
+
+// Unsigned 32-bit division by an invariant divisor as a multiply and a shift
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(m, n) + n) >> l for every
+// n < 2^32.
+struct DivMod {
+    uint32_t divisor = 1;
+    uint32_t multiplier = 0;
+    uint32_t shift = 0;
+
+    DivMod() = default;
+    explicit DivMod(uint32_t d) : divisor(d) {
+        uint32_t l = 0;
+        while (l < 32 && (uint64_t{1} << l) < d) l++;
+        shift = l;
+        multiplier = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+    }
+    __device__ __forceinline__ uint32_t div(uint32_t n) const {
+        uint32_t t = __umulhi(n, multiplier);
+        return static_cast<uint32_t>((static_cast<uint64_t>(t) + n) >> shift);
+    }
+};
+
+// Division by an extent in index type I: multiply-shift for 32-bit indices,
+// a plain divide for 64-bit ones.
+template <typename I>
+struct Div;
+template <>
+struct Div<uint32_t> {
+    DivMod dm;
+    void set(uint64_t d) { dm = DivMod(static_cast<uint32_t>(d)); }
+    __device__ __forceinline__ uint32_t div(uint32_t n) const { return dm.div(n); }
+};
+template <>
+struct Div<uint64_t> {
+    uint64_t d = 1;
+    void set(uint64_t v) { d = v; }
+    __device__ __forceinline__ uint64_t div(uint64_t n) const { return n / d; }
+};
+
+inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// A joint layout of up to `kMaxRank` axes over `N` operands, after
+// coalescing: the extents, a divider per axis, and each operand's strides.
+template <int N>
+struct Walk {
+    int rank = 0;
+    uint64_t shape[kMaxRank] = {};
+    uint64_t strides[N][kMaxRank] = {};
+    uint64_t offsets[N] = {};
+};
+
+// `coalesce` (tensors/layout.rs:419-449): axes of one element dropped, and an
+// axis merged into the one before it wherever every operand steps across the
+// pair as across one axis.  The row-major walk order is unchanged.
+template <int N>
+Walk<N> coalesce(uint32_t rank, const uint64_t* shape, const uint64_t* const* strides,
+                 const uint64_t* offsets) {
+    Walk<N> walk;
+    for (int n = 0; n < N; n++) walk.offsets[n] = offsets[n];
+    for (uint32_t axis = 0; axis < rank; axis++) {
+        uint64_t extent = shape[axis];
+        if (extent == 1) continue;
+        int r = walk.rank;
+        bool joins = r > 0;
+        for (int n = 0; joins && n < N; n++) {
+            joins = walk.strides[n][r - 1] == strides[n][axis] * extent;
+        }
+        if (joins) {
+            walk.shape[r - 1] *= extent;
+            for (int n = 0; n < N; n++) walk.strides[n][r - 1] = strides[n][axis];
+        } else {
+            walk.shape[r] = extent;
+            for (int n = 0; n < N; n++) walk.strides[n][r] = strides[n][axis];
+            walk.rank++;
+        }
+    }
+    return walk;
+}
+
+// The number of elements of `shape`, or false on overflow (layout.rs:96-103).
+inline bool element_count(uint32_t rank, const uint64_t* shape, uint64_t* count) {
+    uint64_t total = 1;
+    for (uint32_t k = 0; k < rank; k++) {
+        if (shape[k] != 0 && total > UINT64_MAX / shape[k]) return false;
+        total *= shape[k];
+    }
+    *count = total;
+    return true;
+}
+
+// One past the last element a layout reads, 0 if it reads none, or false on
+// overflow (`reach`, layout.rs:138-149).
+inline bool reach(uint32_t rank, const uint64_t* shape, uint64_t offset, const uint64_t* strides,
+                  uint64_t* end) {
+    for (uint32_t k = 0; k < rank; k++) {
+        if (shape[k] == 0) {
+            *end = 0;
+            return true;
+        }
+    }
+    uint64_t at = offset;
+    for (uint32_t k = 0; k < rank; k++) {
+        uint64_t extent = shape[k] - 1;
+        if (strides[k] != 0 && extent > (UINT64_MAX - at) / strides[k]) return false;
+        at += extent * strides[k];
+    }
+    if (at == UINT64_MAX) return false;
+    *end = at + 1;
+    return true;
+}
+
+// `check_strided` (tensors/backend.rs:226-252): TC_OK with the element count,
+// or TC_INVALID with the reference's message.
+int check_strided(uint64_t len, uint32_t rank, const uint64_t* shape, uint64_t offset,
+                  const uint64_t* strides, const char* operation, uint64_t* count);
+
+// Blocks for a grid-stride kernel over `work` items of `per_block` each,
+// capped so the grid stays a few waves deep on every CU.
+inline uint32_t grid_for(uint64_t work, uint32_t per_block, uint32_t cap_per_cu = 16) {
+    uint64_t blocks = (work + per_block - 1) / per_block;
+    uint64_t cap = static_cast<uint64_t>(compute_units()) * cap_per_cu;
+    if (blocks > cap) blocks = cap;
+    if (blocks == 0) blocks = 1;
+    return static_cast<uint32_t>(blocks);
+}
+
+}  // namespace tc

@@ -1,0 +1,206 @@
+// Matrix-vector products: `Kernels::matvec` / `matvec_add` (tensors/kernels.rs:901-908,
+// matrix.rs:675-737) and `Kernels::vecmat` (kernels.rs:899, vector.rs:491).
+//
+// Both stream the matrix once from HBM, so both are bandwidth kernels:
+//  - matvec: one wave per row, lanes reading 16 bytes of the row at a time,
+//    a 64-lane shuffle tree for the dot product.  The vector stays hot in L2.
+//  - vecmat: lanes on neighbouring columns, 16 bytes of a row each, so every
+//    row read is one coalesced run; four row groups split the rows inside a
+//    block, and tall matrices split their rows across blocks, combined in
+//    order by a second pass, so the result does not depend on timing.
+// Accumulation is f32, rounded once to the element type (compact.rs:223-231).
+
+#include "common.hpp"
+
+namespace tc {
+namespace {
+
+template <typename S>
+struct alignas(16) Pack {
+    static constexpr int N = 16 / sizeof(S);
+    S v[N];
+};
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+template <typename S, bool PACKED>
+__global__ void __launch_bounds__(256) matvec_kernel(const S* __restrict__ m, const S* __restrict__ v,
+                                                     S* __restrict__ y, uint64_t rows, uint64_t cols,
+                                                     bool accumulate) {
+    using E = Elem<S>;
+    constexpr int N = Pack<S>::N;
+    const int lane = threadIdx.x % 64;
+    const uint64_t waves = static_cast<uint64_t>(gridDim.x) * (blockDim.x / 64);
+    for (uint64_t r = static_cast<uint64_t>(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64; r < rows;
+         r += waves) {
+        const S* row = m + r * cols;
+        float total = 0.0f;
+        if (PACKED) {
+            const Pack<S>* pr = reinterpret_cast<const Pack<S>*>(row);
+            const Pack<S>* pv = reinterpret_cast<const Pack<S>*>(v);
+            for (uint64_t p = lane; p < cols / N; p += 64) {
+                Pack<S> a = pr[p], b = pv[p];
+#pragma unroll
+                for (int k = 0; k < N; k++) total += E::widen(a.v[k]) * E::widen(b.v[k]);
+            }
+        } else {
+            for (uint64_t c = lane; c < cols; c += 64) total += E::widen(row[c]) * E::widen(v[c]);
+        }
+        total = wave_sum(total);
+        if (lane == 0) {
+            if (accumulate) total += E::widen(y[r]);
+            y[r] = E::narrow(total);
+        }
+    }
+}
+
+constexpr int kGroups = 4;
+
+// Block: 64 lanes x kGroups row groups over `V`-column packs; `split` picks
+// the rows.  With one split the block finishes its columns; otherwise it
+// writes f32 partial sums to `partial[split][col]`.
+template <typename S, int V>
+__global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, const S* __restrict__ m,
+                                                     S* __restrict__ y, float* __restrict__ partial,
+                                                     uint64_t rows, uint64_t cols, uint64_t tiles,
+                                                     uint64_t splits, uint64_t per_split) {
+    using E = Elem<S>;
+    __shared__ float stage[kGroups][64 * V];
+    const int lane = threadIdx.x % 64;
+    const int group = threadIdx.x / 64;
+    const uint64_t tile = blockIdx.x % tiles;
+    const uint64_t split = blockIdx.x / tiles;
+    const uint64_t col0 = (tile * 64 + lane) * V;
+    const uint64_t begin = split * per_split;
+    const uint64_t end = min(begin + per_split, rows);
+    const uint64_t span = end > begin ? end - begin : 0;
+    const uint64_t per_group = (span + kGroups - 1) / kGroups;
+    const uint64_t first = min(begin + group * per_group, end);
+    const uint64_t last = min(first + per_group, end);
+    float acc[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) acc[k] = 0.0f;
+    if (col0 < cols) {
+        for (uint64_t r = first; r < last; r++) {
+            const float w = E::widen(v[r]);
+            if (V > 1) {
+                Pack<S> p = *reinterpret_cast<const Pack<S>*>(m + r * cols + col0);
+#pragma unroll
+                for (int k = 0; k < V; k++) acc[k] += w * E::widen(p.v[k]);
+            } else {
+                acc[0] += w * E::widen(m[r * cols + col0]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < V; k++) stage[group][lane * V + k] = acc[k];
+    __syncthreads();
+    if (group == 0 && col0 < cols) {
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            float total = stage[0][lane * V + k];
+#pragma unroll
+            for (int g = 1; g < kGroups; g++) total += stage[g][lane * V + k];
+            if (splits == 1) {
+                y[col0 + k] = E::narrow(total);
+            } else {
+                partial[split * cols + col0 + k] = total;
+            }
+        }
+    }
+}
+
+template <typename S>
+__global__ void __launch_bounds__(256) vecmat_combine_kernel(const float* __restrict__ partial, S* __restrict__ y,
+                                                             uint64_t cols, uint64_t splits) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t c = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < cols; c += stride) {
+        float total = partial[c];
+        for (uint64_t k = 1; k < splits; k++) total += partial[k * cols + c];
+        y[c] = Elem<S>::narrow(total);
+    }
+}
+
+template <typename S>
+int matvec_typed(bool accumulate, uint64_t rows, uint64_t cols, const void* m, const void* v, void* y) {
+    TC_STREAM(s);
+    if (rows == 0) return TC_OK;
+    const S* pm = static_cast<const S*>(m);
+    const S* pv = static_cast<const S*>(v);
+    S* py = static_cast<S*>(y);
+    const bool packed = cols % Pack<S>::N == 0 && aligned16(m) && aligned16(v);
+    const uint32_t blocks = grid_for(rows, 4, 32);
+    if (packed) {
+        matvec_kernel<S, true><<<blocks, 256, 0, s>>>(pm, pv, py, rows, cols, accumulate);
+    } else {
+        matvec_kernel<S, false><<<blocks, 256, 0, s>>>(pm, pv, py, rows, cols, accumulate);
+    }
+    return check_launch("matvec");
+}
+
+template <typename S, int V>
+int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, hipStream_t s) {
+    const uint64_t tiles = (cols + 64 * V - 1) / (64 * V);
+    const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
+    uint64_t splits = 1;
+    if (tiles < want) {
+        splits = (want + tiles - 1) / tiles;
+        const uint64_t most = rows / (kGroups * 16);
+        if (splits > most) splits = most;
+        if (splits < 1) splits = 1;
+    }
+    const uint64_t per_split = (rows + splits - 1) / splits;
+    splits = rows == 0 ? 1 : (rows + per_split - 1) / per_split;
+    float* partial = nullptr;
+    if (splits > 1) {
+        void* scratch = nullptr;
+        int status = tc_alloc(splits * cols * sizeof(float), &scratch);
+        if (status != TC_OK) return status;
+        partial = static_cast<float*>(scratch);
+    }
+    vecmat_kernel<S, V><<<static_cast<uint32_t>(tiles * splits), 256, 0, s>>>(v, m, y, partial, rows, cols, tiles,
+                                                                              splits, per_split);
+    int status = check_launch("vecmat");
+    if (status == TC_OK && splits > 1) {
+        vecmat_combine_kernel<S><<<grid_for(cols, 256), 256, 0, s>>>(partial, y, cols, splits);
+        status = check_launch("vecmat");
+    }
+    if (partial != nullptr) tc_free(partial);
+    return status;
+}
+
+template <typename S>
+int vecmat_typed(uint64_t rows, uint64_t cols, const void* v, const void* m, void* y) {
+    TC_STREAM(s);
+    if (cols == 0) return TC_OK;
+    const S* pv = static_cast<const S*>(v);
+    const S* pm = static_cast<const S*>(m);
+    S* py = static_cast<S*>(y);
+    constexpr int V = Pack<S>::N;
+    if (cols % V == 0 && aligned16(m)) return launch_vecmat<S, V>(pv, pm, py, rows, cols, s);
+    return launch_vecmat<S, 1>(pv, pm, py, rows, cols, s);
+}
+
+}  // namespace
+}  // namespace tc
+
+using namespace tc;
+
+extern "C" {
+
+int tc_matvec(uint32_t dtype, int accumulate, uint64_t rows, uint64_t cols, const void* matrix, const void* vector,
+              void* out) {
+    TC_DISPATCH_FLOAT(dtype, "matvec", S, return matvec_typed<S>(accumulate != 0, rows, cols, matrix, vector, out));
+    return TC_OK;
+}
+
+int tc_vecmat(uint32_t dtype, uint64_t rows, uint64_t cols, const void* vector, const void* matrix, void* out) {
+    TC_DISPATCH_FLOAT(dtype, "vecmat", S, return vecmat_typed<S>(rows, cols, vector, matrix, out));
+    return TC_OK;
+}
+
+}  // extern "C"

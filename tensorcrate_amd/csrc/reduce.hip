@@ -1,0 +1,692 @@
+// Reductions: `Kernels::reduce_axes` (tensors/kernels.rs:1175-1179),
+// `Kernels::arg_reduce` (kernels.rs:1187), and the whole-buffer
+// `vector_reduce` and `dot` (kernels.rs:867, :897).
+//
+// Every slice accumulates in f32 and rounds to the element type once, as the
+// host's `reduce_in` does (strided.rs:102-162).  Min and max are minNum /
+// maxNum, exact in any order; a sum is a tree here where the host folds left
+// to right, so sums, means and variances agree with the host within rounding,
+// as the reference's own Metal kernels do (kernels.rs:170-180).  The variance
+// is single-pass: each thread folds exact two-pass moments of the values it
+// holds in registers, and threads combine (count, mean, M2) triples with
+// Chan, Golub and LeVeque's pairwise update, so no slice is read from HBM
+// twice.  Argmax/argmin carry (value, index) pairs ordered by value and then
+// by smaller index, which picks the first extreme whatever the tree's shape;
+// NaNs never win, and a slice of NaNs answers index 0 (strided.rs:186-225).
+//
+// The host coalesces the kept and the folded axes separately and picks:
+//  - rows: the folded axes are one contiguous run; one wave per slice, lanes
+//    reading 16 bytes at a time, combined by a 64-lane shuffle tree;
+//  - columns: the innermost kept axis is contiguous and the folded axes are
+//    one strided axis; lanes take neighbouring columns so each row read is
+//    coalesced, four row groups split the depth inside a block, and long
+//    depths split across blocks with a second, ordered combining pass;
+//  - general: one thread per slice walking its elements in row-major order.
+
+#include <math.h>
+
+#include "common.hpp"
+
+namespace tc {
+namespace {
+
+// ---- accumulator policies ---------------------------------------------------
+
+// Sum, Min, Max and Mean fold one f32.
+template <uint32_t OP>
+struct Fold {
+    using State = float;
+    __device__ static State init() {
+        return OP == TC_REDUCE_SUM ? 0.0f : (OP == TC_REDUCE_MIN ? INFINITY : -INFINITY);
+    }
+    __device__ static State combine(State a, float x) {
+        return OP == TC_REDUCE_SUM ? a + x : (OP == TC_REDUCE_MIN ? fminf(a, x) : fmaxf(a, x));
+    }
+    __device__ static void add(State& s, float x, uint32_t) { s = combine(s, x); }
+    template <int N>
+    __device__ static void add_chunk(State& s, const float (&x)[N], uint32_t) {
+        State c = init();
+#pragma unroll
+        for (int k = 0; k < N; k++) c = combine(c, x[k]);
+        s = combine(s, c);
+    }
+    __device__ static State merge(State a, State b) { return combine(a, b); }
+    __device__ static State shuffle(State s, int lane) { return __shfl(s, lane, 64); }
+};
+
+struct Moments {
+    float n, mean, m2;
+};
+
+// Chan, Golub and LeVeque (1979): the moments of two disjoint sets.
+__device__ inline Moments merge_moments(Moments a, Moments b) {
+    if (a.n == 0.0f) return b;
+    if (b.n == 0.0f) return a;
+    const float n = a.n + b.n;
+    const float share = b.n / n;
+    const float d = b.mean - a.mean;
+    return Moments{n, a.mean + d * share, a.m2 + b.m2 + d * d * a.n * share};
+}
+
+struct Var {
+    using State = Moments;
+    __device__ static State init() { return Moments{0.0f, 0.0f, 0.0f}; }
+    __device__ static void add(State& s, float x, uint32_t) { s = merge_moments(s, Moments{1.0f, x, 0.0f}); }
+    // A chunk's own moments are exact two-pass ones from registers.
+    template <int N>
+    __device__ static void add_chunk(State& s, const float (&x)[N], uint32_t) {
+        float total = 0.0f;
+#pragma unroll
+        for (int k = 0; k < N; k++) total += x[k];
+        const float mean = total / static_cast<float>(N);
+        float m2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < N; k++) {
+            const float d = x[k] - mean;
+            m2 += d * d;
+        }
+        s = merge_moments(s, Moments{static_cast<float>(N), mean, m2});
+    }
+    __device__ static State merge(State a, State b) { return merge_moments(a, b); }
+    __device__ static State shuffle(State s, int lane) {
+        return Moments{__shfl(s.n, lane, 64), __shfl(s.mean, lane, 64), __shfl(s.m2, lane, 64)};
+    }
+};
+
+struct Arg {
+    float value;  // NaN until the slice's first number
+    uint32_t index;
+};
+
+// The later-or-better pair under "largest (or smallest) value, then smallest
+// index, NaNs never": associative and commutative, so any tree finds the
+// first extreme.
+template <uint32_t OP>
+struct ArgFold {
+    using State = Arg;
+    __device__ static State init() { return Arg{NAN, 0u}; }
+    __device__ static bool better(Arg b, Arg a) {
+        if (isnan(b.value)) return false;
+        if (isnan(a.value)) return true;
+        const bool past = OP == TC_REDUCE_MIN ? b.value < a.value : b.value > a.value;
+        return past || (b.value == a.value && b.index < a.index);
+    }
+    __device__ static void add(State& s, float x, uint32_t index) {
+        Arg c{x, index};
+        if (better(c, s)) s = c;
+    }
+    template <int N>
+    __device__ static void add_chunk(State& s, const float (&x)[N], uint32_t first) {
+#pragma unroll
+        for (int k = 0; k < N; k++) add(s, x[k], first + k);
+    }
+    __device__ static State merge(State a, State b) { return better(b, a) ? b : a; }
+    __device__ static State shuffle(State s, int lane) {
+        return Arg{__shfl(s.value, lane, 64), static_cast<uint32_t>(__shfl(static_cast<int>(s.index), lane, 64))};
+    }
+};
+
+// What a finished slice writes.
+struct Finish {
+    uint32_t kind;     // tc_axis_reduction
+    float depth;       // the mean's count
+    float divisor;     // the variance's divisor
+};
+
+template <typename S>
+__device__ inline void write_result(S* out, uint64_t at, float value) {
+    out[at] = Elem<S>::narrow(value);
+}
+
+template <typename P, typename S>
+__device__ inline void finish(const typename P::State& s, const Finish& f, S* out, uint64_t at);
+
+template <typename P>
+struct Finisher {
+    template <typename S>
+    __device__ static void write(const typename P::State& s, const Finish& f, S* out, uint64_t at) {
+        // Fold and Mean share the f32 state; the mean divides in f32.
+        const float v = f.kind == TC_AXIS_MEAN ? s / f.depth : s;
+        write_result(out, at, v);
+    }
+};
+template <>
+struct Finisher<Var> {
+    template <typename S>
+    __device__ static void write(const Moments& s, const Finish& f, S* out, uint64_t at) {
+        write_result(out, at, s.m2 / f.divisor);
+    }
+};
+template <uint32_t OP>
+struct Finisher<ArgFold<OP>> {
+    template <typename S>
+    __device__ static void write(const Arg& s, const Finish&, S*, uint64_t) {}
+    __device__ static void write(const Arg& s, const Finish&, uint32_t* out, uint64_t at) { out[at] = s.index; }
+};
+
+template <typename P>
+__device__ inline typename P::State wave_reduce(typename P::State s) {
+    const int lane = threadIdx.x % 64;
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        typename P::State other = P::shuffle(s, lane ^ offset);
+        // The lower lane's state is the left operand, so the tree's order is
+        // fixed and the result deterministic.
+        s = (lane & offset) ? P::merge(other, s) : P::merge(s, other);
+    }
+    return s;
+}
+
+// ---- layouts ----------------------------------------------------------------
+
+template <typename I>
+struct Kept {
+    int rank;
+    I shape[kMaxRank];
+    Div<I> div[kMaxRank];
+    I strides[kMaxRank];
+};
+
+template <typename I>
+__device__ __forceinline__ I kept_offset(const Kept<I>& kept, I index) {
+    I at = 0;
+    for (int k = kept.rank - 1; k > 0; k--) {
+        I q = kept.div[k].div(index);
+        at += (index - q * kept.shape[k]) * kept.strides[k];
+        index = q;
+    }
+    if (kept.rank > 0) at += index * kept.strides[0];
+    return at;
+}
+
+template <typename I>
+struct Folded {
+    int rank;
+    I shape[kMaxRank];
+    I strides[kMaxRank];
+};
+
+template <typename S>
+struct alignas(16) Pack {
+    static constexpr int N = 16 / sizeof(S);
+    S v[N];
+};
+
+// ---- rows: one wave per contiguous slice ------------------------------------
+
+template <typename S, typename P, typename O, bool PACKED, typename I>
+__global__ void __launch_bounds__(256) rows_kernel(const S* __restrict__ in, O* __restrict__ out,
+                                                   Kept<I> kept, I results, I depth, Finish f) {
+    using E = Elem<S>;
+    constexpr int V = Pack<S>::N;
+    const int lane = threadIdx.x % 64;
+    const I waves = static_cast<I>(gridDim.x) * (blockDim.x / 64);
+    for (I r = static_cast<I>(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64; r < results; r += waves) {
+        const S* slice = in + kept_offset(kept, r);
+        typename P::State s = P::init();
+        if (PACKED) {
+            const Pack<S>* packs = reinterpret_cast<const Pack<S>*>(slice);
+            const I count = depth / V;
+            I p = lane;
+            // Two packs in flight per lane per step.
+            for (; p + 64 < count; p += 128) {
+                Pack<S> a = packs[p], b = packs[p + 64];
+                float x[V], y[V];
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    x[k] = E::widen(a.v[k]);
+                    y[k] = E::widen(b.v[k]);
+                }
+                P::add_chunk(s, x, static_cast<uint32_t>(p * V));
+                P::add_chunk(s, y, static_cast<uint32_t>((p + 64) * V));
+            }
+            if (p < count) {
+                Pack<S> a = packs[p];
+                float x[V];
+#pragma unroll
+                for (int k = 0; k < V; k++) x[k] = E::widen(a.v[k]);
+                P::add_chunk(s, x, static_cast<uint32_t>(p * V));
+            }
+        } else {
+            for (I i = lane; i < depth; i += 64) P::add(s, E::widen(slice[i]), static_cast<uint32_t>(i));
+        }
+        s = wave_reduce<P>(s);
+        if (lane == 0) Finisher<P>::write(s, f, out, r);
+    }
+}
+
+// ---- columns: lanes on neighbouring kept columns ----------------------------
+
+constexpr int kColumns = 64;
+constexpr int kGroups = 4;
+
+// The columns' layout: results are [outer, columns] with the columns
+// contiguous in the input; each column folds `depth` elements `step` apart.
+template <typename I>
+struct ColumnWalk {
+    Kept<I> outer;  // the kept axes before the column axis
+    I columns;
+    I depth, step;
+    I tiles;        // column tiles per outer index
+    Div<I> tiles_div;
+    I splits;       // depth splits across blocks
+    I per_split;    // rows per split (the last may hold fewer)
+};
+
+// One block: kColumns columns x kGroups row groups over one split's rows.
+// With splits == 1 it finishes the results; otherwise it writes its states
+// to `partial[split][result]` for `combine_kernel`.
+template <typename S, typename P, typename O, typename I>
+__global__ void __launch_bounds__(256) columns_kernel(const S* __restrict__ in, O* __restrict__ out,
+                                                      typename P::State* __restrict__ partial,
+                                                      ColumnWalk<I> w, I blocks, Finish f) {
+    using E = Elem<S>;
+    using State = typename P::State;
+    __shared__ State stage[kGroups][kColumns];
+    const int lane = threadIdx.x % kColumns;
+    const int group = threadIdx.x / kColumns;
+    const I results = w.columns;  // per outer index
+    for (I block = blockIdx.x; block < blocks; block += gridDim.x) {
+        // block -> (split, outer, tile), split outermost so neighbouring
+        // blocks share rows.
+        const I per_split_blocks = blocks / w.splits;
+        const I split = block / per_split_blocks;
+        const I rest = block - split * per_split_blocks;
+        const I outer = w.tiles_div.div(rest);
+        const I tile = rest - outer * w.tiles;
+        const I column = tile * kColumns + lane;
+        const I row_begin = split * w.per_split;
+        I row_end = row_begin + w.per_split;
+        if (row_end > w.depth) row_end = w.depth;
+        // Contiguous row ranges per group, so group order is index order.
+        const I span = row_end - row_begin;
+        const I per_group = (span + kGroups - 1) / kGroups;
+        I first = row_begin + group * per_group;
+        I last = first + per_group;
+        if (last > row_end) last = row_end;
+        if (first > row_end) first = row_end;
+        State s = P::init();
+        if (column < w.columns) {
+            const S* base = in + kept_offset(w.outer, outer) + column;
+            I row = first;
+            constexpr int U = 8;
+            for (; row + U <= last; row += U) {
+                float x[U];
+#pragma unroll
+                for (int k = 0; k < U; k++) x[k] = E::widen(base[(row + k) * w.step]);
+                P::add_chunk(s, x, static_cast<uint32_t>(row));
+            }
+            for (; row < last; row++) P::add(s, E::widen(base[row * w.step]), static_cast<uint32_t>(row));
+        }
+        stage[group][lane] = s;
+        __syncthreads();
+        if (group == 0 && column < w.columns) {
+#pragma unroll
+            for (int g = 1; g < kGroups; g++) s = P::merge(s, stage[g][lane]);
+            const I result = outer * results + column;
+            if (w.splits == 1) {
+                Finisher<P>::write(s, f, out, result);
+            } else {
+                const I total = blocks / w.splits / w.tiles * results;  // outer count x columns
+                partial[split * total + result] = s;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Merge each result's split states in split order and finish it.
+template <typename P, typename O, typename I>
+__global__ void __launch_bounds__(256) combine_kernel(const typename P::State* __restrict__ partial,
+                                                      O* __restrict__ out, I results, I splits, Finish f) {
+    const I stride = static_cast<I>(gridDim.x) * blockDim.x;
+    for (I r = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; r < results; r += stride) {
+        typename P::State s = partial[r];
+        for (I k = 1; k < splits; k++) s = P::merge(s, partial[k * results + r]);
+        Finisher<P>::write(s, f, out, r);
+    }
+}
+
+// ---- general: one thread per slice -------------------------------------------
+
+template <typename S, typename P, typename O, typename I>
+__global__ void __launch_bounds__(256) general_kernel(const S* __restrict__ in, O* __restrict__ out,
+                                                      Kept<I> kept, Folded<I> folded, I results, I depth,
+                                                      Finish f) {
+    using E = Elem<S>;
+    const I stride = static_cast<I>(gridDim.x) * blockDim.x;
+    for (I r = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; r < results; r += stride) {
+        const S* slice = in + kept_offset(kept, r);
+        typename P::State s = P::init();
+        I index[kMaxRank] = {};
+        I at = 0;
+        for (I i = 0; i < depth; i++) {
+            P::add(s, E::widen(slice[at]), static_cast<uint32_t>(i));
+            // Advance the folded axes like an odometer (layout.rs:476-496).
+            for (int k = folded.rank - 1; k >= 0; k--) {
+                index[k]++;
+                at += folded.strides[k];
+                if (index[k] < folded.shape[k]) break;
+                at -= folded.strides[k] * folded.shape[k];
+                index[k] = 0;
+            }
+        }
+        Finisher<P>::write(s, f, out, r);
+    }
+}
+
+// ---- host-side planning -------------------------------------------------------
+
+// One operand's axes with extent-one axes dropped and mergeable neighbours
+// merged (layout.rs:419-449 for a single operand).
+struct Axes {
+    int rank = 0;
+    uint64_t shape[kMaxRank] = {};
+    uint64_t strides[kMaxRank] = {};
+};
+
+Axes coalesce_axes(uint32_t rank, const uint64_t* shape, const uint64_t* strides) {
+    Axes axes;
+    for (uint32_t k = 0; k < rank; k++) {
+        if (shape[k] == 1) continue;
+        if (axes.rank > 0 && axes.strides[axes.rank - 1] == strides[k] * shape[k]) {
+            axes.shape[axes.rank - 1] *= shape[k];
+            axes.strides[axes.rank - 1] = strides[k];
+        } else {
+            axes.shape[axes.rank] = shape[k];
+            axes.strides[axes.rank] = strides[k];
+            axes.rank++;
+        }
+    }
+    return axes;
+}
+
+template <typename I>
+Kept<I> make_kept(const Axes& axes, int rank) {
+    Kept<I> kept{};
+    kept.rank = rank;
+    for (int k = 0; k < rank; k++) {
+        kept.shape[k] = static_cast<I>(axes.shape[k]);
+        kept.div[k].set(axes.shape[k]);
+        kept.strides[k] = static_cast<I>(axes.strides[k]);
+    }
+    return kept;
+}
+
+struct Plan {
+    Axes kept, folded;
+    uint64_t results, depth;
+};
+
+template <typename S, typename P, typename O, typename I>
+int launch_reduce(const S* in, O* out, const Plan& plan, const Finish& f, hipStream_t s, const char* what) {
+    const Axes& kept = plan.kept;
+    const Axes& folded = plan.folded;
+    const uint64_t results = plan.results, depth = plan.depth;
+    // Rows: the slice is one contiguous run long enough to share a wave.
+    if (folded.rank == 1 && folded.strides[0] == 1 && depth >= 64) {
+        constexpr int V = Pack<S>::N;
+        bool packed = depth % V == 0 && aligned16(in);
+        for (int k = 0; packed && k < kept.rank; k++) packed = (kept.strides[k] * sizeof(S)) % 16 == 0;
+        Kept<I> k = make_kept<I>(kept, kept.rank);
+        const uint32_t blocks = grid_for(results, 4, 32);
+        if (packed) {
+            rows_kernel<S, P, O, true, I><<<blocks, 256, 0, s>>>(in, out, k, static_cast<I>(results),
+                                                                 static_cast<I>(depth), f);
+        } else {
+            rows_kernel<S, P, O, false, I><<<blocks, 256, 0, s>>>(in, out, k, static_cast<I>(results),
+                                                                  static_cast<I>(depth), f);
+        }
+        return check_launch(what);
+    }
+    // Columns: contiguous neighbouring results, one strided folded axis.
+    if (folded.rank == 1 && kept.rank >= 1 && kept.strides[kept.rank - 1] == 1 &&
+        kept.shape[kept.rank - 1] >= 16) {
+        ColumnWalk<I> w{};
+        w.outer = make_kept<I>(kept, kept.rank - 1);
+        const uint64_t columns = kept.shape[kept.rank - 1];
+        const uint64_t outer = results / columns;
+        const uint64_t tiles = (columns + kColumns - 1) / kColumns;
+        w.columns = static_cast<I>(columns);
+        w.depth = static_cast<I>(depth);
+        w.step = static_cast<I>(folded.strides[0]);
+        w.tiles = static_cast<I>(tiles);
+        w.tiles_div.set(tiles);
+        // Enough blocks to put four on every CU, each split keeping at least
+        // 32 rows per row group.
+        const uint64_t base_blocks = outer * tiles;
+        const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
+        uint64_t splits = 1;
+        if (base_blocks < want) {
+            splits = (want + base_blocks - 1) / base_blocks;
+            const uint64_t most = depth / (kGroups * 32);
+            if (splits > most) splits = most;
+            if (splits < 1) splits = 1;
+        }
+        const uint64_t per_split = (depth + splits - 1) / splits;
+        splits = (depth + per_split - 1) / per_split;
+        w.splits = static_cast<I>(splits);
+        w.per_split = static_cast<I>(per_split);
+        const uint64_t blocks = base_blocks * splits;
+        typename P::State* partial = nullptr;
+        if (splits > 1) {
+            void* scratch = nullptr;
+            int status = tc_alloc(splits * results * sizeof(typename P::State), &scratch);
+            if (status != TC_OK) return status;
+            partial = static_cast<typename P::State*>(scratch);
+        }
+        columns_kernel<S, P, O, I><<<grid_for(blocks, 1, 64), 256, 0, s>>>(in, out, partial, w,
+                                                                             static_cast<I>(blocks), f);
+        int status = check_launch(what);
+        if (status == TC_OK && splits > 1) {
+            combine_kernel<P, O, I><<<grid_for(results, 256), 256, 0, s>>>(partial, out, static_cast<I>(results),
+                                                                          static_cast<I>(splits), f);
+            status = check_launch(what);
+        }
+        // Stream order keeps the block alive until both kernels have run.
+        if (partial != nullptr) tc_free(partial);
+        return status;
+    }
+    Kept<I> k = make_kept<I>(kept, kept.rank);
+    Folded<I> fo{};
+    fo.rank = folded.rank;
+    for (int a = 0; a < folded.rank; a++) {
+        fo.shape[a] = static_cast<I>(folded.shape[a]);
+        fo.strides[a] = static_cast<I>(folded.strides[a]);
+    }
+    general_kernel<S, P, O, I><<<grid_for(results, 256), 256, 0, s>>>(in, out, k, fo, static_cast<I>(results),
+                                                                      static_cast<I>(depth), f);
+    return check_launch(what);
+}
+
+template <typename S, typename P, typename O>
+int reduce_typed(const void* input, void* out, uint64_t offset, const Plan& plan, const Finish& f,
+                 uint64_t input_len, const char* what) {
+    TC_STREAM(s);
+    const S* in = static_cast<const S*>(input) + offset;
+    if (plan.results == 0) return TC_OK;
+    bool small = plan.results <= UINT32_MAX && plan.depth <= UINT32_MAX && input_len <= UINT32_MAX;
+    if (small) return launch_reduce<S, P, O, uint32_t>(in, static_cast<O*>(out), plan, f, s, what);
+    return launch_reduce<S, P, O, uint64_t>(in, static_cast<O*>(out), plan, f, s, what);
+}
+
+int check_split(const tc_split* split, uint64_t input_len, const char* what, Plan* plan) {
+    if (split->kept_rank + split->folded_rank > static_cast<uint32_t>(kMaxRank)) {
+        return fail(TC_INVALID, std::string(what) + ": more than " + std::to_string(kMaxRank) + " axes");
+    }
+    uint64_t shape[kMaxRank], strides[kMaxRank];
+    uint32_t rank = 0;
+    for (uint32_t k = 0; k < split->kept_rank; k++, rank++) {
+        shape[rank] = split->kept[k];
+        strides[rank] = split->kept_strides[k];
+    }
+    for (uint32_t k = 0; k < split->folded_rank; k++, rank++) {
+        shape[rank] = split->folded[k];
+        strides[rank] = split->folded_strides[k];
+    }
+    uint64_t count = 0;
+    int status = check_strided(input_len, rank, shape, split->offset, strides, what, &count);
+    if (status != TC_OK) return status;
+    if (!element_count(split->kept_rank, split->kept, &plan->results) ||
+        !element_count(split->folded_rank, split->folded, &plan->depth)) {
+        return fail(TC_INVALID, std::string(what) + ": too many elements");
+    }
+    plan->kept = coalesce_axes(split->kept_rank, split->kept, split->kept_strides);
+    plan->folded = coalesce_axes(split->folded_rank, split->folded, split->folded_strides);
+    return TC_OK;
+}
+
+template <typename S>
+int reduce_axes_typed(const void* input, uint64_t input_len, const tc_split* split, uint32_t kind,
+                      uint32_t op, uint64_t divisor, void* out) {
+    Plan plan;
+    int status = check_split(split, input_len, "reduce_axes", &plan);
+    if (status != TC_OK) return status;
+    Finish f{kind, static_cast<float>(plan.depth), static_cast<float>(divisor)};
+    const char* what = "reduce_axes";
+    if (kind == TC_AXIS_VARIANCE) {
+        return reduce_typed<S, Var, S>(input, out, split->offset, plan, f, input_len, what);
+    }
+    if (kind == TC_AXIS_MEAN) {
+        return reduce_typed<S, Fold<TC_REDUCE_SUM>, S>(input, out, split->offset, plan, f, input_len, what);
+    }
+    if (kind != TC_AXIS_FOLD) return fail(TC_INVALID, "reduce_axes: no AxisReduction " + std::to_string(kind));
+    switch (op) {
+        case TC_REDUCE_SUM:
+            return reduce_typed<S, Fold<TC_REDUCE_SUM>, S>(input, out, split->offset, plan, f, input_len, what);
+        case TC_REDUCE_MIN:
+            return reduce_typed<S, Fold<TC_REDUCE_MIN>, S>(input, out, split->offset, plan, f, input_len, what);
+        case TC_REDUCE_MAX:
+            return reduce_typed<S, Fold<TC_REDUCE_MAX>, S>(input, out, split->offset, plan, f, input_len, what);
+        default:
+            return fail(TC_INVALID, "reduce_axes: no Reduce " + std::to_string(op));
+    }
+}
+
+template <typename S>
+int arg_reduce_typed(const void* input, uint64_t input_len, const tc_split* split, uint32_t op,
+                     uint32_t* out) {
+    const char* what = "arg_reduce";
+    if (split->folded_rank != 1) {
+        return fail(TC_INVALID, "arg_reduce: folds " + std::to_string(split->folded_rank) +
+                                    " axes, not one");
+    }
+    if (split->folded[0] == 0) return fail(TC_INVALID, "arg_reduce: the axis is empty");
+    if (split->folded[0] > UINT32_MAX) {
+        return fail(TC_INVALID, "arg_reduce: the axis's extent " + std::to_string(split->folded[0]) +
+                                    " does not fit a u32");
+    }
+    Plan plan;
+    int status = check_split(split, input_len, what, &plan);
+    if (status != TC_OK) return status;
+    Finish f{TC_AXIS_FOLD, 0.0f, 0.0f};
+    switch (op) {
+        case TC_REDUCE_MIN:
+            return reduce_typed<S, ArgFold<TC_REDUCE_MIN>, uint32_t>(input, out, split->offset, plan, f, input_len, what);
+        case TC_REDUCE_MAX:
+            return reduce_typed<S, ArgFold<TC_REDUCE_MAX>, uint32_t>(input, out, split->offset, plan, f, input_len, what);
+        default:
+            return fail(TC_INVALID, "arg_reduce: Reduce " + std::to_string(op) + " is not Min or Max");
+    }
+}
+
+// ---- whole buffers ------------------------------------------------------------
+
+// Stage one: each block folds a strided share into `partial[block]`; stage
+// two: one block folds the partials in order into `result`.
+template <typename S, uint32_t OP, bool DOT>
+__global__ void __launch_bounds__(256) total_kernel(const S* __restrict__ a, const S* __restrict__ b,
+                                                    uint64_t n, float* __restrict__ partial) {
+    using E = Elem<S>;
+    using P = Fold<OP>;
+    __shared__ float stage[4];
+    float s = P::init();
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float x = E::widen(a[i]);
+        P::add(s, DOT ? x * E::widen(b[i]) : x, 0);
+    }
+    s = wave_reduce<P>(s);
+    if (threadIdx.x % 64 == 0) stage[threadIdx.x / 64] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = stage[0];
+        for (int w = 1; w < 4; w++) t = P::merge(t, stage[w]);
+        partial[blockIdx.x] = t;
+    }
+}
+
+template <uint32_t OP>
+__global__ void __launch_bounds__(64) finish_total_kernel(const float* __restrict__ partial, uint32_t count,
+                                                          float* __restrict__ result) {
+    using P = Fold<OP>;
+    float s = P::init();
+    for (uint32_t i = threadIdx.x; i < count; i += 64) P::add(s, partial[i], 0);
+    s = wave_reduce<P>(s);
+    if (threadIdx.x == 0) *result = s;
+}
+
+template <typename S, uint32_t OP, bool DOT>
+int total(const void* a, const void* b, uint64_t n, float* result, const char* what) {
+    TC_STREAM(s);
+    const uint32_t blocks = grid_for(n, 256 * 8, 4);
+    void* scratch = nullptr;
+    int status = tc_alloc(blocks * sizeof(float), &scratch);
+    if (status != TC_OK) return status;
+    float* partial = static_cast<float*>(scratch);
+    total_kernel<S, OP, DOT><<<blocks, 256, 0, s>>>(static_cast<const S*>(a), static_cast<const S*>(b), n, partial);
+    status = check_launch(what);
+    if (status == TC_OK) {
+        finish_total_kernel<OP><<<1, 64, 0, s>>>(partial, blocks, result);
+        status = check_launch(what);
+    }
+    tc_free(scratch);
+    return status;
+}
+
+}  // namespace
+}  // namespace tc
+
+using namespace tc;
+
+extern "C" {
+
+int tc_reduce_axes(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split,
+                   uint32_t kind, uint32_t op, uint64_t divisor, void* out) {
+    TC_DISPATCH_FLOAT(dtype, "reduce_axes", S,
+                      return reduce_axes_typed<S>(input, input_len, split, kind, op, divisor, out));
+    return TC_OK;
+}
+
+int tc_arg_reduce(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split,
+                  uint32_t op, uint32_t* out) {
+    TC_DISPATCH_FLOAT(dtype, "arg_reduce", S, return arg_reduce_typed<S>(input, input_len, split, op, out));
+    return TC_OK;
+}
+
+int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result) {
+    switch (op) {
+        case TC_REDUCE_SUM:
+            TC_DISPATCH_FLOAT(dtype, "vector_reduce", S,
+                              return total<S, TC_REDUCE_SUM, false>(a, nullptr, n, result, "vector_reduce"));
+            break;
+        case TC_REDUCE_MIN:
+            TC_DISPATCH_FLOAT(dtype, "vector_reduce", S,
+                              return total<S, TC_REDUCE_MIN, false>(a, nullptr, n, result, "vector_reduce"));
+            break;
+        case TC_REDUCE_MAX:
+            TC_DISPATCH_FLOAT(dtype, "vector_reduce", S,
+                              return total<S, TC_REDUCE_MAX, false>(a, nullptr, n, result, "vector_reduce"));
+            break;
+        default:
+            return fail(TC_INVALID, "vector_reduce: no Reduce " + std::to_string(op));
+    }
+    return TC_OK;
+}
+
+int tc_dot(uint32_t dtype, const void* a, const void* b, uint64_t n, float* result) {
+    TC_DISPATCH_FLOAT(dtype, "dot", S, return total<S, TC_REDUCE_SUM, true>(a, b, n, result, "dot"));
+    return TC_OK;
+}
+
+}  // extern "C"

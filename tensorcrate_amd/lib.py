@@ -1,0 +1,277 @@
+"""ctypes binding of ``libtchip.so``, the C ABI declared in ``include/tchip.h``.
+
+This is the thin driver the parity tests and the benchmark use to reach the
+HIP kernels.  Loading fails loudly when the library has not been built: there
+is no other implementation behind these calls to fall back on.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PACKAGE = Path(__file__).resolve().parent
+LIBRARY = PACKAGE / "libtchip.so"
+
+MAX_RANK = 6
+FUSED_LEAD = 5
+
+# Status codes (tc_status).
+OK, INVALID, UNSUPPORTED, DEVICE, OUT_OF_MEMORY = range(5)
+# Element types (fused::DType, fused/mod.rs:145-150).
+F32, F16, BF16, F64 = range(4)
+# BinaryOp (kernels.rs:32-38).
+ADD, SUB, MUL, DIV, REM = range(5)
+# Compare (kernels.rs:106-122).
+MIN, MAX, MAX_SHARE, LESS, LESS_EQUAL, GREATER, GREATER_EQUAL = range(7)
+# Reduce (kernels.rs:183-187).
+SUM, RMIN, RMAX = range(3)
+# Pairwise kinds (kernels.rs:411-415).
+ARITHMETIC, COMPARE, POWER = range(3)
+# AxisReduction (kernels.rs:449-457).
+FOLD, MEAN, VARIANCE = range(3)
+# Transposed (kernels.rs:462-467), plus PLAIN.
+PLAIN, LEFT, RIGHT = range(3)
+
+DTYPE_SIZE = {F32: 4, F16: 2, BF16: 2}
+# How each element type is held on the host: bf16 as its raw bits.
+NUMPY_TYPE = {F32: np.float32, F16: np.float16, BF16: np.uint16}
+
+
+class Strided(ctypes.Structure):
+    _fields_ = [("offset", ctypes.c_uint64), ("strides", ctypes.c_uint64 * MAX_RANK)]
+
+
+class Region(ctypes.Structure):
+    _fields_ = [
+        ("source", ctypes.c_void_p),
+        ("source_len", ctypes.c_uint64),
+        ("rank", ctypes.c_uint32),
+        ("shape", ctypes.c_uint64 * MAX_RANK),
+        ("src", Strided),
+        ("dst", Strided),
+    ]
+
+
+class Split(ctypes.Structure):
+    _fields_ = [
+        ("offset", ctypes.c_uint64),
+        ("kept_rank", ctypes.c_uint32),
+        ("kept", ctypes.c_uint64 * MAX_RANK),
+        ("kept_strides", ctypes.c_uint64 * MAX_RANK),
+        ("folded_rank", ctypes.c_uint32),
+        ("folded", ctypes.c_uint64 * MAX_RANK),
+        ("folded_strides", ctypes.c_uint64 * MAX_RANK),
+    ]
+
+
+class Encoded(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_uint16),
+        ("op", ctypes.c_uint16),
+        ("dst", ctypes.c_uint8),
+        ("a", ctypes.c_uint8),
+        ("b", ctypes.c_uint8),
+        ("aux", ctypes.c_uint8),
+        ("value", ctypes.c_float),
+    ]
+
+
+class Place(ctypes.Structure):
+    _fields_ = [
+        ("offset", ctypes.c_uint64),
+        ("col_step", ctypes.c_uint64),
+        ("lead", ctypes.c_uint32),
+        ("dims", ctypes.c_uint64 * FUSED_LEAD),
+        ("steps", ctypes.c_uint64 * FUSED_LEAD),
+    ]
+
+
+class HipError(RuntimeError):
+    """A failed call: the status code and the library's message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+_lib: ctypes.CDLL | None = None
+
+u32, u64, vp, i32, f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+
+# Every entry point of include/tchip.h with its argument types.
+SIGNATURES = {
+    "tc_init": [i32],
+    "tc_last_error": [],
+    "tc_sync": [],
+    "tc_stream": [ctypes.POINTER(vp)],
+    "tc_device_info": [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t],
+    "tc_timer_begin": [],
+    "tc_timer_end": [ctypes.POINTER(f32)],
+    "tc_alloc": [ctypes.c_size_t, ctypes.POINTER(vp)],
+    "tc_free": [vp],
+    "tc_empty_cache": [],
+    "tc_upload": [vp, vp, ctypes.c_size_t],
+    "tc_download": [vp, vp, ctypes.c_size_t],
+    "tc_copy": [vp, vp, ctypes.c_size_t],
+    "tc_fill": [vp, u64, u32, vp],
+    "tc_strided_copy": [u32, vp, u64, u32, ctypes.POINTER(u64), ctypes.POINTER(Strided), vp],
+    "tc_assemble": [u32, vp, u64, ctypes.POINTER(Region), u32],
+    "tc_strided_write": [u32, vp, u64, ctypes.POINTER(Region)],
+    "tc_elementwise": [u32, u32, vp, vp, vp, u64],
+    "tc_broadcast": [u32, u32, vp, f32, i32, vp, u64],
+    "tc_compare": [u32, u32, vp, vp, vp, u64],
+    "tc_compare_scalar": [u32, u32, vp, f32, i32, vp, u64],
+    "tc_clamp": [u32, vp, f32, f32, vp, u64],
+    "tc_strided_binary": [u32, u32, u32, u32, ctypes.POINTER(u64), vp, u64, ctypes.POINTER(Strided), vp, u64,
+                          ctypes.POINTER(Strided), vp],
+    "tc_reduce_axes": [u32, vp, u64, ctypes.POINTER(Split), u32, u32, u64, vp],
+    "tc_arg_reduce": [u32, vp, u64, ctypes.POINTER(Split), u32, vp],
+    "tc_vector_reduce": [u32, vp, u64, u32, vp],
+    "tc_dot": [u32, vp, vp, u64, vp],
+    "tc_matmul": [u32, u32, u32, i32, u64, u64, u64, vp, vp, vp],
+    "tc_matvec": [u32, i32, u64, u64, vp, vp, vp],
+    "tc_vecmat": [u32, u64, u64, vp, vp, vp],
+    "tc_transpose": [u32, u64, u64, vp, vp],
+    "tc_fused": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, ctypes.POINTER(vp),
+                 ctypes.POINTER(u64), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32, u64, u64],
+}
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library, with every signature set; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("TCHIP_LIBRARY", LIBRARY))
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is not built: run __graft_entry__.build() first; the Hip backend has no "
+            "other implementation to fall back on"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p if name == "tc_last_error" else ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def check(status: int) -> None:
+    if status != OK:
+        message = load().tc_last_error().decode()
+        raise HipError(status, message)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))
+
+
+def sync() -> None:
+    call("tc_sync")
+
+
+def device_info() -> tuple[str, str]:
+    name = ctypes.create_string_buffer(256)
+    arch = ctypes.create_string_buffer(64)
+    call("tc_device_info", name, 256, arch, 64)
+    return name.value.decode(), arch.value.decode()
+
+
+class Buffer:
+    """Device storage from the library's stream-ordered cache."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        pointer = vp()
+        call("tc_alloc", max(self.nbytes, 1), ctypes.byref(pointer))
+        self.ptr = pointer.value
+
+    @classmethod
+    def of(cls, array: np.ndarray) -> "Buffer":
+        array = np.ascontiguousarray(array)
+        buffer = cls(array.nbytes)
+        if array.nbytes:
+            call("tc_upload", buffer.ptr, array.ctypes.data, array.nbytes)
+        return buffer
+
+    def download(self, dtype, count: int | None = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype)
+        if out.nbytes:
+            call("tc_download", out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+    def free(self) -> None:
+        if self.ptr is not None:
+            load().tc_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def strided(offset: int, strides) -> Strided:
+    s = Strided()
+    s.offset = offset
+    for k, v in enumerate(strides):
+        s.strides[k] = v
+    return s
+
+
+def dims(values) -> ctypes.Array:
+    array = (u64 * MAX_RANK)()
+    for k, v in enumerate(values):
+        array[k] = v
+    return array
+
+
+def split(offset: int, kept, kept_strides, folded, folded_strides) -> Split:
+    s = Split()
+    s.offset = offset
+    s.kept_rank = len(kept)
+    s.folded_rank = len(folded)
+    for k, (e, st) in enumerate(zip(kept, kept_strides)):
+        s.kept[k], s.kept_strides[k] = e, st
+    for k, (e, st) in enumerate(zip(folded, folded_strides)):
+        s.folded[k], s.folded_strides[k] = e, st
+    return s
+
+
+def fused(dtype: int, code, places, inputs, outputs, rows: int, cols: int) -> None:
+    """``tc_fused`` over Python lists: ``code`` of (kind, op, dst, a, b, aux,
+    value) tuples, ``places`` of (offset, col_step, lead, dims, steps), and
+    ``inputs``/``outputs`` of (Buffer, element count) pairs."""
+    enc = (Encoded * max(len(code), 1))(*[Encoded(*c) for c in code])
+    pl = (Place * max(len(places), 1))()
+    for k, (offset, col_step, lead, dims_, steps) in enumerate(places):
+        pl[k].offset, pl[k].col_step, pl[k].lead = offset, col_step, lead
+        for d in range(len(dims_)):
+            pl[k].dims[d], pl[k].steps[d] = dims_[d], steps[d]
+    ins = (vp * max(len(inputs), 1))(*[b.ptr for b, _ in inputs])
+    in_lens = (u64 * max(len(inputs), 1))(*[n for _, n in inputs])
+    outs = (vp * max(len(outputs), 1))(*[b.ptr for b, _ in outputs])
+    out_lens = (u64 * max(len(outputs), 1))(*[n for _, n in outputs])
+    call("tc_fused", dtype, enc, len(code), pl, len(places), ins, in_lens, len(inputs), outs, out_lens, len(outputs),
+         rows, cols)
+
+
+def region(source: Buffer | int, source_len: int, shape, src_offset, src_strides, dst_offset,
+           dst_strides) -> Region:
+    r = Region()
+    r.source = source.ptr if isinstance(source, Buffer) else source
+    r.source_len = source_len
+    r.rank = len(shape)
+    for k, v in enumerate(shape):
+        r.shape[k] = v
+    r.src = strided(src_offset, src_strides)
+    r.dst = strided(dst_offset, dst_strides)
+    return r

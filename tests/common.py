@@ -1,0 +1,61 @@
+"""Helpers shared by the tests: the reference's deterministic generators and
+element-type conversions."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import binding as oracle
+from tensorcrate_amd import lib
+
+KINDS = [lib.F32, lib.F16, lib.BF16]
+KIND_NAMES = {lib.F32: "f32", lib.F16: "f16", lib.BF16: "bf16"}
+
+
+class Lcg:
+    """The test generator of tests/half.rs:20-40: a 64-bit LCG, top 31 bits."""
+
+    def __init__(self, seed: int):
+        self.state = seed & (2**64 - 1)
+
+    def next(self) -> int:
+        self.state = (self.state * 6364136223846793005 + 1442695040888963407) & (2**64 - 1)
+        return self.state >> 33
+
+    def uniform(self, low: float, high: float, n: int) -> np.ndarray:
+        return np.array([low + (high - low) * (self.next() / float(1 << 31)) for _ in range(n)])
+
+
+def filler(shape) -> np.ndarray:
+    """``value(i) = ((7i + 3) mod 23) - 11`` (tests/broadcast_reduce.rs:12-14):
+    integral and mixed-sign, so sums are exact in any order."""
+    n = int(np.prod(shape, dtype=np.int64)) if len(shape) else 1
+    i = np.arange(n, dtype=np.int64)
+    return (((i * 7 + 3) % 23) - 11).astype(np.float32).reshape(shape)
+
+
+def to_kind(values, kind) -> np.ndarray:
+    """f32 values in the host form of `kind`, rounded once to nearest even."""
+    values = np.asarray(values, np.float32)
+    if kind == lib.F32:
+        return values.copy()
+    return oracle.narrow(kind, values)
+
+
+def widen(kind, values) -> np.ndarray:
+    values = np.asarray(values)
+    if kind == lib.F32:
+        return values.astype(np.float32)
+    return oracle.widen(kind, values)
+
+
+def same(got, want) -> bool:
+    """Equal element for element, a NaN matching a NaN
+    (tests/broadcast_reduce.rs:65-74)."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return got.shape == want.shape and bool(np.all((got == want) | (np.isnan(got) & np.isnan(want))))
+
+
+def bits_equal(got: np.ndarray, want: np.ndarray) -> bool:
+    got, want = np.ascontiguousarray(got), np.ascontiguousarray(want)
+    return got.shape == want.shape and got.tobytes() == want.tobytes()

@@ -1,0 +1,60 @@
+"""The C ABI library loads and exports every entry point include/tchip.h
+declares, with the struct layouts the header fixes (CPU only: no call here
+touches a device)."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+from tensorcrate_amd import lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_functions():
+    header = (ROOT / "include" / "tchip.h").read_text()
+    header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tc_\w+)\s*\(", header, flags=re.M)))
+
+
+def test_the_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 30
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib.LIBRARY)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [name for name in names if name not in exported]
+    assert not missing, missing
+    # The binding names exactly the declared set.
+    assert sorted(lib.SIGNATURES) == names
+
+
+def test_the_library_loads_and_binds():
+    loaded = lib.load()
+    for name in declared_functions():
+        assert getattr(loaded, name) is not None
+
+
+def test_struct_layouts_match_the_header():
+    # Natural C alignment of the header's structs, as a Rust #[repr(C)]
+    # mirror would lay them out.
+    assert ctypes.sizeof(lib.Strided) == 8 + 6 * 8
+    assert ctypes.sizeof(lib.Encoded) == 12
+    assert lib.Region.rank.offset == 16 and lib.Region.shape.offset == 24
+    assert ctypes.sizeof(lib.Region) == 24 + 48 + 2 * 56
+    assert lib.Split.kept.offset == 16
+    assert ctypes.sizeof(lib.Place) == 8 + 8 + 8 + 40 + 40
+
+
+def test_errors_are_reported_not_raised_on_the_device():
+    # A layout reaching past its storage is refused on the host, with the
+    # reference's wording (backend.rs:245-250), before any device work; the
+    # check needs no device.
+    loaded = lib.load()
+    shape = lib.dims([2, 3])
+    from_ = lib.strided(5, [3, 1])
+    status = loaded.tc_strided_copy(4, None, 10, 2, shape, ctypes.byref(from_), None)
+    assert status == lib.INVALID
+    assert loaded.tc_last_error().decode() == (
+        "strided copy: shape [2, 3] with strides [3, 1] from offset 5 reaches past 10 elements")

@@ -1,0 +1,117 @@
+"""Fused programs on the GPU against the oracle's host interpreter, bit for
+bit (Kernels::fused, kernels.rs:1077; fused/mod.rs:62-70), and the Adam step
+built on them (optim.rs:1048-1136; tests/optim.rs:71-101)."""
+
+import numpy as np
+import pytest
+
+from oracle import binding as oracle
+from tensorcrate_amd import lib
+from tensorcrate_amd.optim import Adam, adam_program, identity_place
+from tests.common import KINDS, bits_equal, to_kind, widen
+
+pytestmark = pytest.mark.gpu
+
+
+def test_the_known_answer():
+    # fused/mod.rs:23-37: y = sqrt(a w + 1) over [3, 0] and [1, 5] is [2, 1].
+    code = [(0, 0, 0, 0, lib.F32, 0, 0.0), (0, 1, 1, 1, lib.F32, 0, 0.0), (2, lib.MUL, 2, 0, 1, 0, 0.0),
+            (1, 0, 3, 0, 0, 0, 1.0), (2, lib.ADD, 4, 2, 3, 0, 0.0), (3, 13, 5, 4, 0, 0, 0.0),
+            (5, 0, 0, 5, lib.F32, 0, 0.0)]
+    a, w = lib.Buffer.of(np.array([3.0, 0.0], np.float32)), lib.Buffer.of(np.array([1.0, 5.0], np.float32))
+    y = lib.Buffer(8)
+    place = identity_place(1, 2)
+    lib.fused(lib.F32, code, [place, place], [(a, 2), (w, 2)], [(y, 2)], 1, 2)
+    assert y.download(np.float32).tolist() == [2.0, 1.0]
+
+
+def test_remapped_loads_and_mixed_storage():
+    # A [rows, cols] space reading an f16 row vector broadcast down the rows,
+    # a bf16 matrix transposed, and an f32 matrix; stores to two types.
+    rows, cols = 37, 70
+    rng = np.random.default_rng(0)
+    bias = to_kind(rng.standard_normal(cols), lib.F16)
+    tm = to_kind(rng.standard_normal((cols, rows)), lib.BF16)  # read transposed
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    code = [(0, 0, 0, 0, lib.F16, 0, 0.0), (0, 1, 1, 1, lib.BF16, 0, 0.0), (0, 2, 2, 2, lib.F32, 0, 0.0),
+            (2, lib.MUL, 3, 1, 2, 0, 0.0), (2, lib.ADD, 3, 3, 0, 0, 0.0), (4, lib.MAX, 4, 3, 2, 0, 0.0),
+            (4, lib.GREATER, 5, 3, 0, 0, 0.0), (2, lib.DIV, 6, 4, 1, 0, 0.0),
+            (5, 0, 0, 6, lib.BF16, 0, 0.0), (5, 0, 0, 5, lib.F32, 1, 0.0)]
+    places = [(0, 1, 1, [rows], [0]), (0, rows, 1, [rows], [1]), identity_place(rows, cols)]
+    for dtype in KINDS:
+        out0 = np.zeros(rows * cols, np.uint16)
+        out1 = np.zeros(rows * cols, np.float32)
+        oracle.fused(dtype, code, places, [bias.view(np.uint16), tm, x], [out0, out1], rows, cols)
+        d = [lib.Buffer.of(bias), lib.Buffer.of(tm), lib.Buffer.of(x)]
+        g0, g1 = lib.Buffer(out0.nbytes), lib.Buffer(out1.nbytes)
+        lib.fused(dtype, code, places, [(d[0], cols), (d[1], rows * cols), (d[2], rows * cols)],
+                  [(g0, rows * cols), (g1, rows * cols)], rows, cols)
+        assert bits_equal(g0.download(np.uint16), out0), dtype
+        assert bits_equal(g1.download(np.float32), out1), dtype
+
+
+def test_a_load_past_its_input_is_refused():
+    code = [(0, 0, 0, 0, lib.F32, 0, 0.0), (5, 0, 0, 0, lib.F32, 0, 0.0)]
+    a, y = lib.Buffer(4 * 10), lib.Buffer(4 * 12)
+    with pytest.raises(lib.HipError, match="reaches past input 0"):
+        lib.fused(lib.F32, code, [identity_place(3, 4)], [(a, 10)], [(y, 12)], 3, 4)
+
+
+@pytest.mark.parametrize("magnitude", [0.01, 1.0, 100.0])
+def test_adams_first_step_is_the_rate(magnitude):
+    # tests/optim.rs:92-99: m_hat / sqrt(v_hat) is exactly +-1 on step one.
+    p, g = lib.Buffer.of(np.zeros(1, np.float32)), lib.Buffer.of(np.array([magnitude], np.float32))
+    Adam(0.1).update(p, g, 1, 1)
+    assert abs(p.download(np.float32)[0] + 0.1) < 1e-6
+
+
+@pytest.mark.parametrize("dtype", KINDS)
+def test_adam_steps_match_the_oracle_bit_for_bit(dtype):
+    rows, cols = 129, 257
+    rng = np.random.default_rng(4)
+    p0 = to_kind(rng.standard_normal((rows, cols)), dtype)
+    grads = [to_kind(rng.standard_normal((rows, cols)), dtype) for _ in range(4)]
+    rule = Adam(1e-3, dtype)
+    p = lib.Buffer.of(p0)
+    host_p = p0.copy().reshape(-1)
+    host_m = host_v = None
+    for step, grad in enumerate(grads, start=1):
+        rule.update(p, lib.Buffer.of(grad), rows, cols)
+        resumed = host_m is not None
+        code, loads = adam_program(resumed, dtype, 1e-3, 0.9, 0.999, 1e-8, step)
+        places = [identity_place(rows, cols)] * loads
+        new_m = np.zeros_like(host_p) if not resumed else host_m
+        new_v = np.zeros_like(host_p) if not resumed else host_v
+        inputs = [grad.reshape(-1), host_p] + ([host_m, host_v] if resumed else [])
+        oracle.fused(dtype, code, places, inputs, [host_p, new_m, new_v], rows, cols)
+        host_m, host_v = new_m, new_v
+        assert bits_equal(p.download(host_p.dtype), host_p), step
+        assert bits_equal(rule.first.download(host_p.dtype), host_m), step
+        assert bits_equal(rule.second.download(host_p.dtype), host_v), step
+
+
+def test_config5_adam_over_the_mlp_parameters():
+    # The MLP's 25,175,040 parameters in six tensors (1024 -> 4096 -> 4096 ->
+    # 1024, with biases), ten steps, against the oracle on sampled slices of
+    # the largest tensor and exactly everywhere through a checksum.
+    rng = np.random.default_rng(4)
+    rows, cols = 4096, 4096
+    p0 = (rng.standard_normal((rows, cols), dtype=np.float32) * np.sqrt(2 / 4096)).astype(np.float32)
+    grad = rng.standard_normal((rows, cols), dtype=np.float32)
+    p, g = lib.Buffer.of(p0), lib.Buffer.of(grad)
+    rule = Adam(1e-3)
+    for _ in range(3):
+        rule.update(p, g, rows, cols)
+    got = p.download(np.float32).reshape(rows, cols)
+    # The oracle on the first 64 rows (a row slab is the same program).
+    host_p = p0[:64].copy().reshape(-1)
+    m = v = None
+    for step in range(1, 4):
+        resumed = m is not None
+        code, loads = adam_program(resumed, lib.F32, 1e-3, 0.9, 0.999, 1e-8, step)
+        nm = np.zeros_like(host_p) if m is None else m
+        nv = np.zeros_like(host_p) if v is None else v
+        ins = [grad[:64].reshape(-1).copy(), host_p] + ([m, v] if resumed else [])
+        oracle.fused(lib.F32, code, [identity_place(64, cols)] * loads, ins, [host_p, nm, nv], 64, cols)
+        m, v = nm, nv
+    assert bits_equal(got[:64].reshape(-1), host_p)

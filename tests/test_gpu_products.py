@@ -1,0 +1,150 @@
+"""Matrix products on the GPU's matrix cores against the oracle and f64
+(Kernels::matmul / matmul_add / matmul_transposed_add / matvec / vecmat,
+kernels.rs:897-987; tests/backend.rs:221-334 and tests/simd.rs:89-119 are the
+reference's versions).
+
+Tolerances (per element, relative to sum_k |a_ik b_kj|, which cancellation
+cannot shrink): f32 1e-5 sqrt(K); f16 and bf16 inputs, compared with the f64
+product of the same rounded inputs, 2^-7 sqrt(K) for a 16-bit output and
+1e-5 sqrt(K) for the f32 (`matmul_f32`) output.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import binding as oracle
+from tensorcrate_amd import lib
+from tests.common import to_kind, widen
+
+pytestmark = pytest.mark.gpu
+
+HOST = {lib.F32: np.float32, lib.F16: np.float16, lib.BF16: np.uint16}
+
+
+def error(got, a, b, want):
+    scale = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))
+    return np.max(np.abs(got.astype(np.float64) - want) / np.maximum(scale, 1e-30))
+
+
+def product(in_kind, out_kind, transposed, a, b, m, k, n, addend=None):
+    da, db = lib.Buffer.of(a), lib.Buffer.of(b)
+    size = 4 if out_kind == lib.F32 else 2
+    dc = lib.Buffer.of(addend) if addend is not None else lib.Buffer(m * n * size)
+    lib.call("tc_matmul", in_kind, out_kind, transposed, int(addend is not None), m, k, n, da.ptr, db.ptr, dc.ptr)
+    return dc.download(HOST[out_kind], m * n).reshape(m, n)
+
+
+def tolerance(in_kind, out_kind, k):
+    return (1e-5 if out_kind == lib.F32 else 2.0 ** -7) * np.sqrt(max(k, 1))
+
+
+SHAPES = [(1, 1, 1), (5, 6, 7), (96, 96, 96), (33, 70, 65), (256, 128, 64), (300, 257, 129), (17, 1000, 3),
+          (512, 512, 512)]
+
+
+@pytest.mark.parametrize("in_kind,out_kind", [(lib.F32, lib.F32), (lib.BF16, lib.BF16), (lib.BF16, lib.F32),
+                                              (lib.F16, lib.F16), (lib.F16, lib.F32)])
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_matmul_against_the_oracle(in_kind, out_kind, m, k, n):
+    rng = np.random.default_rng(m * 10000 + k * 100 + n)
+    a = to_kind(rng.uniform(-1, 1, (m, k)), in_kind)
+    b = to_kind(rng.uniform(-1, 1, (k, n)), in_kind)
+    wa, wb = widen(in_kind, a), widen(in_kind, b)
+    exact = wa.astype(np.float64) @ wb.astype(np.float64)
+    tol = tolerance(in_kind, out_kind, k)
+    got = widen(out_kind, product(in_kind, out_kind, lib.PLAIN, a, b, m, k, n))
+    assert error(got, wa, wb, exact) <= tol
+    want = widen(out_kind, oracle.matmul(in_kind, a, b, m, k, n, out_dtype=out_kind))
+    assert error(got, wa, wb, want) <= 2 * tol
+
+
+@pytest.mark.parametrize("kind", [lib.F32, lib.BF16])
+@pytest.mark.parametrize("m,k,n", [(64, 48, 80), (130, 257, 33), (4, 4, 4)])
+def test_transposed_products_accumulate(kind, m, k, n):
+    # C + A^T B (A stored k x m) and C + A B^T (B stored n x k): the matmul
+    # backward's two products (tape/mod.rs:1199-1214).
+    rng = np.random.default_rng(k)
+    at = to_kind(rng.uniform(-1, 1, (k, m)), kind)
+    b = to_kind(rng.uniform(-1, 1, (k, n)), kind)
+    bt = to_kind(rng.uniform(-1, 1, (n, k)), kind)
+    a = to_kind(rng.uniform(-1, 1, (m, k)), kind)
+    c = to_kind(rng.uniform(-1, 1, (m, n)), kind)
+    tol = tolerance(kind, kind, k) + (2.0 ** -8 if kind == lib.BF16 else 0)
+    got = widen(kind, product(kind, kind, lib.LEFT, at, b, m, k, n, addend=c))
+    want = widen(kind, c) + widen(kind, at).T.astype(np.float64) @ widen(kind, b)
+    assert error(got, widen(kind, at).T, widen(kind, b), want) <= tol * 2
+    got = widen(kind, product(kind, kind, lib.RIGHT, a, bt, m, k, n, addend=c))
+    want = widen(kind, c) + widen(kind, a).astype(np.float64) @ widen(kind, bt).T
+    assert error(got, widen(kind, a), widen(kind, bt).T, want) <= tol * 2
+    got = widen(kind, product(kind, kind, lib.PLAIN, a, b, m, k, n, addend=c))
+    want = oracle.matmul(kind, a, b, m, k, n, addend=c)
+    assert error(got, widen(kind, a), widen(kind, b), widen(kind, want)) <= tol * 2
+
+
+def test_an_empty_inner_dimension_gives_zeros_or_the_addend():
+    # ops.rs:163-168, tests/backend.rs:259-266.
+    a = np.zeros((3, 0), np.float32)
+    b = np.zeros((0, 4), np.float32)
+    assert np.array_equal(product(lib.F32, lib.F32, lib.PLAIN, a, b, 3, 0, 4), np.zeros((3, 4)))
+    c = np.arange(12, dtype=np.float32).reshape(3, 4)
+    assert np.array_equal(product(lib.F32, lib.F32, lib.PLAIN, a, b, 3, 0, 4, addend=c), c)
+
+
+def test_matvec_vecmat():
+    rng = np.random.default_rng(13)
+    for kind in [lib.F32, lib.BF16, lib.F16]:
+        for rows, cols in [(1, 1), (37, 53), (1000, 64), (8, 8192), (513, 1031)]:
+            m = to_kind(rng.uniform(-1, 1, (rows, cols)), kind)
+            v = to_kind(rng.uniform(-1, 1, cols), kind)
+            w = to_kind(rng.uniform(-1, 1, rows), kind)
+            dm, dv, dw = lib.Buffer.of(m), lib.Buffer.of(v), lib.Buffer.of(w)
+            out = lib.Buffer(rows * 4)
+            lib.call("tc_matvec", kind, 0, rows, cols, dm.ptr, dv.ptr, out.ptr)
+            got = widen(kind, out.download(HOST[kind], rows))
+            wm, wv, ww = widen(kind, m), widen(kind, v), widen(kind, w)
+            want = wm.astype(np.float64) @ wv
+            scale = np.abs(wm).astype(np.float64) @ np.abs(wv)
+            unit = 2.0 ** -24 if kind == lib.F32 else (2.0 ** -11 if kind == lib.F16 else 2.0 ** -8)
+            assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(cols) * scale + unit * np.abs(want) + 1e-30)
+            lib.call("tc_matvec", kind, 1, rows, cols, dm.ptr, dv.ptr, dw.ptr)
+            got = widen(kind, dw.download(HOST[kind], rows))
+            assert np.all(np.abs(got - (want + ww)) <= 1e-5 * np.sqrt(cols) * scale + unit * (np.abs(want) + 1) + 1e-30)
+            out = lib.Buffer(cols * 4)
+            lib.call("tc_vecmat", kind, rows, cols, dw.ptr, dm.ptr, out.ptr)
+            got = widen(kind, out.download(HOST[kind], cols))
+            w2 = widen(kind, dw.download(HOST[kind], rows))
+            want = w2.astype(np.float64) @ wm
+            scale = np.abs(w2).astype(np.float64) @ np.abs(wm)
+            assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(rows) * scale + unit * np.abs(want) + 1e-30)
+
+
+def test_config1_f32_512_cubed():
+    # f32 C = A @ B, A and B 512 x 512 U(-1, 1), seed 0, against the oracle.
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    b = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    got = product(lib.F32, lib.F32, lib.PLAIN, a, b, 512, 512, 512)
+    want = oracle.matmul(lib.F32, a, b, 512, 512, 512)
+    assert error(got, a, b, want) <= 1e-5 * np.sqrt(512)
+    assert error(got, a, b, a.astype(np.float64) @ b) <= 1e-5 * np.sqrt(512)
+
+
+@pytest.mark.parametrize("in_kind,m,k,n", [(lib.BF16, 8192, 8192, 8192), (lib.F32, 4096, 4096, 4096),
+                                           (lib.F16, 16384, 4096, 1024)])
+def test_config4_sweep_on_sampled_entries(in_kind, m, k, n):
+    # The dense sweep at full size, seed 3: bf16 A, B ~ N(0, 1/sqrt(K)) (the
+    # second parameter read as the standard deviation), f32 U(-1, 1), f16
+    # N(0, 1/sqrt(K)); 64 sampled rows against the f64 product.
+    rng = np.random.default_rng(3)
+    if in_kind == lib.F32:
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    else:
+        sigma = 1 / np.sqrt(k)
+        a = to_kind((rng.standard_normal((m, k), dtype=np.float32) * sigma), in_kind)
+        b = to_kind((rng.standard_normal((k, n), dtype=np.float32) * sigma), in_kind)
+    got = product(in_kind, in_kind, lib.PLAIN, a, b, m, k, n)
+    rows = np.sort(rng.choice(m, 64, replace=False))
+    wa, wb = widen(in_kind, a[rows]), widen(in_kind, b)
+    want = wa.astype(np.float64) @ wb.astype(np.float64)
+    assert error(widen(in_kind, got[rows]), wa, wb, want) <= tolerance(in_kind, in_kind, k)
