@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X `Hip` backend's hot path on one GPU.
+
+The headline line is BASELINE.json's first metric on the configuration its
+target names: a dense bf16 GEMM, M = N = K = 8192, through the C ABI's
+`tc_matmul` (Kernels::matmul), in TFLOP/s.  A "step" is one such product over
+one batch of synthetic input already resident in HBM.  The same JSON line
+carries the other configurations' measurements under "workloads": the f32
+and f16 GEMMs of the sweep, the axis reductions of configuration 2 (at the
+stated [64,128,1024] and at the 512 MiB size its text quotes), the broadcast
+chain and strided copies of configuration 3 — each with the roofline that
+bounds it.
+
+Timing: W untimed warmup steps, then exactly K steps between two HIP events
+recorded on the library's own stream (the stream every kernel is launched
+on), the stream synchronised on both sides.  The roofline's `achieved` is the
+algorithmic work per launch of the dominant kernel over that kernel's own
+event-timed duration.  The CPU baseline is the oracle's C restatement of the
+reference Host (simd) algorithm, timed on a bounded sample on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from tensorcrate_amd import halfconv, lib  # noqa: E402
+from tensorcrate_amd.tensor import Tensor  # noqa: E402
+
+HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
+MFMA_PEAK = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}  # dense TFLOP/s
+KIND = {"bf16": lib.BF16, "f16": lib.F16, "f32": lib.F32}
+METRIC = "GEMM TFLOP/s & %MFMA peak; reduce/elementwise/copy GB/s & %HBM peak"
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps: int, warmup: int) -> float:
+    """Milliseconds per call of `fn` over `steps` calls after `warmup`."""
+    for _ in range(warmup):
+        fn()
+    lib.sync()
+    lib.call("tc_timer_begin")
+    for _ in range(steps):
+        fn()
+    ms = ctypes.c_float()
+    lib.call("tc_timer_end", ctypes.byref(ms))
+    lib.sync()
+    return ms.value / steps
+
+
+def host_matrix(kind: str, rows: int, cols: int, rng, sigma=None) -> np.ndarray:
+    if sigma is None:
+        values = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+    else:
+        values = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(sigma)
+    if kind == "bf16":
+        return halfconv.bf16_bits(values)
+    if kind == "f16":
+        return halfconv.f16(values)
+    return values
+
+
+def gemm(kind: str, m: int, k: int, n: int, seed: int, sigma, steps: int, warmup: int) -> dict:
+    rng = np.random.default_rng(seed)
+    a = lib.Buffer.of(host_matrix(kind, m, k, rng, sigma))
+    b_host = host_matrix(kind, k, n, rng, sigma)
+    b = lib.Buffer.of(b_host)
+    del b_host
+    size = 4 if kind == "f32" else 2
+    c = lib.Buffer(m * n * size)
+    code = KIND[kind]
+    op = lambda: lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
+    ms = timed(op, steps, warmup)
+    # The matrix-core kernel alone: the product reads B as N x K, so hand it
+    # B^T directly (`matmul_transposed_add` Right, same kernel, same shapes).
+    bt = lib.Buffer(k * n * size)
+    lib.call("tc_transpose", size, k, n, b.ptr, bt.ptr)
+    kernel = lambda: lib.call("tc_matmul", code, code, lib.RIGHT, 0, m, k, n, a.ptr, bt.ptr, c.ptr)
+    kernel_ms = timed(kernel, steps, warmup)
+    flops = 2.0 * m * n * k
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    for buffer in (a, b, bt, c):
+        buffer.free()
+    return {
+        "workload": f"{kind} GEMM {m}x{k}x{n}",
+        "value": flops / (ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "ms": ms,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind], "unit": "TFLOP/s",
+                     "frac": achieved / MFMA_PEAK[kind], "traffic": None, "kernel_ms": kernel_ms},
+    }
+
+
+def hbm_line(workload: str, nbytes: float, ms: float) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": workload, "value": gbs, "unit": "GB/s", "ms": ms,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK, "unit": "GB/s", "frac": gbs / HBM_PEAK,
+                         "traffic": None}}
+
+
+def reductions(shape, seed: int, steps: int, warmup: int) -> list[dict]:
+    rng = np.random.default_rng(seed)
+    x = Tensor.from_numpy(rng.standard_normal(shape, dtype=np.float32))
+    n = int(np.prod(shape))
+    lines = []
+    tag = "x".join(map(str, shape))
+    for name, axes, results in [("sum", [2], n // shape[2]), ("max", [2], n // shape[2]),
+                                ("min", [2], n // shape[2]), ("mean", [2], n // shape[2]), ("var", [2], n // shape[2]),
+                                ("sum", [0, 1], shape[2]), ("max", [0, 1], shape[2]), ("var", [0, 1], shape[2])]:
+        fn = getattr(x, f"{name}_axes")
+        ms = timed(lambda: fn(axes), steps, warmup)
+        lines.append(hbm_line(f"{name}_axes {axes} of f32 [{tag}]", 4 * (n + results), ms))
+    for name in ("argmax", "argmin"):
+        fn = getattr(x, name)
+        ms = timed(lambda: fn(1), steps, warmup)
+        lines.append(hbm_line(f"{name} axis 1 of f32 [{tag}]", 4 * n + 4 * (n // shape[1]), ms))
+    return lines
+
+
+def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
+    rng = np.random.default_rng(2)
+    shape = (256, 512, 512)
+    x = Tensor.from_numpy(rng.standard_normal(shape, dtype=np.float32))
+    y = Tensor.from_numpy(rng.uniform(-1, 1, (1, 512, 1)).astype(np.float32))
+    z = Tensor.from_numpy(rng.uniform(-1, 1, (256, 1, 512)).astype(np.float32))
+    n = 256 * 512 * 512
+    mib = 4 * n
+    lines = []
+    ms = timed(lambda: x * y, steps, warmup)
+    lines.append(hbm_line("x*y, f32 [256,512,512] x [1,512,1]", 2 * mib + 4 * 512, ms))
+    t = x * y
+    ms = timed(lambda: t + z, steps, warmup)
+    lines.append(hbm_line("t+z, f32 [256,512,512] + [256,1,512]", 2 * mib + 4 * 256 * 512, ms))
+    out = t + z
+    ms = timed(lambda: out.permute([0, 2, 1]).contiguous(), steps, warmup)
+    lines.append(hbm_line("permute(0,2,1).contiguous, f32 [256,512,512]", 2 * mib, ms))
+    p = out.permute([0, 2, 1]).contiguous()
+    ms = timed(lambda: p.slice(1, 128, 384).contiguous(), steps, warmup)
+    lines.append(hbm_line("slice [:,128:384,:].contiguous, f32", mib, ms))
+    halves = p.chunk(1, 2)
+    ms = timed(lambda: Tensor.concat(halves, 1), steps, warmup)
+    lines.append(hbm_line("concat of two [256,256,512] halves on axis 1, f32", 2 * mib, ms))
+    a, b = x.storage, t.storage
+    dst = lib.Buffer(mib)
+    ms = timed(lambda: lib.call("tc_elementwise", lib.F32, lib.ADD, a.ptr, b.ptr, dst.ptr, n), steps, warmup)
+    lines.append(hbm_line("same-shape add, f32 64 Mi elements", 3 * mib, ms))
+    return lines
+
+
+def cpu_baseline(m: int, k: int, n: int) -> dict:
+    """The oracle's restatement of the Host (simd) bf16 product —
+    widen, i-p-j AVX2 FMA on one thread, round once (compact.rs:232-253,
+    simd_x86.rs:1302-1327) — on a band of rows of A against all of B, scaled
+    linearly in M (the i-p-j loop is linear in rows)."""
+    from oracle import binding as oracle
+
+    rng = np.random.default_rng(3)
+    sigma = 1 / np.sqrt(k)
+    b = halfconv.bf16_bits(rng.standard_normal((k, n), dtype=np.float32) * np.float32(sigma))
+    rows = 2
+    while True:
+        a = halfconv.bf16_bits(rng.standard_normal((rows, k), dtype=np.float32) * np.float32(sigma))
+        start = time.perf_counter()
+        oracle.matmul(oracle.BF16, a, b, rows, k, n)
+        seconds = time.perf_counter() - start
+        if seconds >= 10.0 or rows >= m:
+            break
+        rows = min(m, max(rows * 2, int(rows * 12.0 / max(seconds, 1e-3))))
+    flops = 2.0 * rows * k * n
+    return {"value": flops / seconds / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"rows 0..{rows} of A ({rows} of {m}) times all of B, bf16 {m}x{k}x{n}: the oracle's "
+                      f"widen + single-thread AVX2 i-p-j FMA + round-once, {seconds:.1f} s, scaled linearly in M"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--quick", action="store_true", help="headline only, no secondary workloads or CPU baseline")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path, so --gpus must be 1", file=sys.stderr)
+        return 2
+    lib.call("tc_init", 0)
+    name, arch = lib.device_info()
+    log(f"device {name} {arch}")
+
+    m = k = n = 8192
+    log("bf16 GEMM 8192^3 ...")
+    head = gemm("bf16", m, k, n, 3, 1 / np.sqrt(k), args.steps, args.warmup)
+    log(f"  {head['value']:.1f} TFLOP/s ({head['ms']:.3f} ms/step), kernel {head['roofline']['achieved']:.1f}")
+    workloads = []
+    if not args.quick:
+        log("f32 GEMM 4096^3 ...")
+        workloads.append(gemm("f32", 4096, 4096, 4096, 3, None, args.steps, args.warmup))
+        log("f16 GEMM 16384x4096x1024 ...")
+        workloads.append(gemm("f16", 16384, 1024, 4096, 3, 1 / np.sqrt(1024), args.steps, args.warmup))
+        log("reductions ...")
+        workloads += reductions((64, 128, 1024), 1, args.steps, args.warmup)
+        workloads += reductions((1024, 128, 1024), 1, max(args.steps // 2, 5), args.warmup)
+        log("broadcast chain and copies ...")
+        workloads += broadcast_and_copies(args.steps, args.warmup)
+        for line in workloads:
+            log(f"  {line['workload']}: {line['value']:.1f} {line['unit']} ({line['roofline']['frac'] * 100:.1f}%)")
+    baseline = None
+    if not args.quick and not args.no_cpu:
+        log("CPU baseline ...")
+        baseline = cpu_baseline(m, k, n)
+        log(f"  {baseline['value'] * 1e3:.2f} GFLOP/s on one core")
+    line = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: A, B ~ N(0, 1/sqrt(K)) bf16, seed 3, numpy PCG64",
+        "config": {"workload": "dense GEMM bf16 M=N=K=8192, f32 accumulate, bf16 out (configs[3])",
+                   "m": m, "n": n, "k": k, "device": f"{name} {arch}"},
+        "roofline": head["roofline"],
+        "cpu_baseline": baseline,
+        "workloads": workloads,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -19,7 +19,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import lib
+from . import halfconv, lib
 
 MAX_RANK = lib.MAX_RANK
 
@@ -95,7 +95,10 @@ class Storage:
     def filled(cls, kind, length: int, value) -> "Storage":
         """``Vector::filled`` (vector.rs:101) without a host upload."""
         out = cls(kind, length)
-        scalar = np.array([value], dtype=_NUMPY[kind])
+        if kind == lib.BF16:
+            scalar = halfconv.bf16_bits(np.array([value], np.float32))
+        else:
+            scalar = np.array([value], dtype=_NUMPY[kind])
         lib.call("tc_fill", out.ptr, out.len, out.width, scalar.ctypes.data)
         return out
 

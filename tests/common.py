@@ -59,3 +59,26 @@ def same(got, want) -> bool:
 def bits_equal(got: np.ndarray, want: np.ndarray) -> bool:
     got, want = np.ascontiguousarray(got), np.ascontiguousarray(want)
     return got.shape == want.shape and got.tobytes() == want.tobytes()
+
+
+def _nan_mask(values: np.ndarray, kind) -> np.ndarray:
+    bits = values.view(np.uint32 if kind == lib.F32 else np.uint16).astype(np.uint64)
+    if kind == lib.F32:
+        return (bits & 0x7FFFFFFF) > 0x7F800000
+    if kind == lib.F16:
+        return (bits & 0x7FFF) > 0x7C00
+    return (bits & 0x7FFF) > 0x7F80
+
+
+def same_bits(got: np.ndarray, want: np.ndarray, kind) -> bool:
+    """Bit for bit, except that any NaN matches any NaN: a NaN's sign and
+    payload are not pinned (x86 produces a negative default NaN where the
+    GPU's is positive), as the reference's own `assert_same` allows
+    (tests/broadcast_reduce.rs:65-74)."""
+    got, want = np.ascontiguousarray(got).reshape(-1), np.ascontiguousarray(want).reshape(-1)
+    if got.shape != want.shape:
+        return False
+    gn, wn = _nan_mask(got, kind), _nan_mask(want, kind)
+    if not np.array_equal(gn, wn):
+        return False
+    return got[~gn].tobytes() == want[~wn].tobytes()

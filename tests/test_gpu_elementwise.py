@@ -9,7 +9,7 @@ import pytest
 from oracle import binding as oracle
 from tensorcrate_amd import lib
 from tensorcrate_amd.tensor import Tensor
-from tests.common import KINDS, bits_equal, filler, same, to_kind, widen
+from tests.common import KINDS, bits_equal, filler, same, same_bits, to_kind, widen
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def test_same_shape_operations_are_bit_exact(kind, n):
     host = a.dtype
     for op in ARITH:
         lib.call("tc_elementwise", kind, op, da.ptr, db.ptr, out.ptr, n)
-        assert bits_equal(out.download(host, n), oracle.elementwise(kind, lib.ARITHMETIC, op, a, b)), op
+        assert same_bits(out.download(host, n), oracle.elementwise(kind, lib.ARITHMETIC, op, a, b), kind), op
     for op in CMP:
         lib.call("tc_compare", kind, op, da.ptr, db.ptr, out.ptr, n)
         got = widen(kind, out.download(host, n))
@@ -43,7 +43,7 @@ def test_same_shape_operations_are_bit_exact(kind, n):
     for left in (0, 1):
         for op in ARITH:
             lib.call("tc_broadcast", kind, op, da.ptr, 1.5, left, out.ptr, n)
-            assert bits_equal(out.download(host, n), oracle.scalar(kind, lib.ARITHMETIC, op, a, 1.5, left)), op
+            assert same_bits(out.download(host, n), oracle.scalar(kind, lib.ARITHMETIC, op, a, 1.5, left), kind), op
         for op in CMP:
             lib.call("tc_compare_scalar", kind, op, da.ptr, 0.0, left, out.ptr, n)
             got = widen(kind, out.download(host, n))

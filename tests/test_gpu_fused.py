@@ -8,7 +8,7 @@ import pytest
 from oracle import binding as oracle
 from tensorcrate_amd import lib
 from tensorcrate_amd.optim import Adam, adam_program, identity_place
-from tests.common import KINDS, bits_equal, to_kind, widen
+from tests.common import KINDS, bits_equal, same_bits, to_kind, widen
 
 pytestmark = pytest.mark.gpu
 
@@ -85,9 +85,9 @@ def test_adam_steps_match_the_oracle_bit_for_bit(dtype):
         inputs = [grad.reshape(-1), host_p] + ([host_m, host_v] if resumed else [])
         oracle.fused(dtype, code, places, inputs, [host_p, new_m, new_v], rows, cols)
         host_m, host_v = new_m, new_v
-        assert bits_equal(p.download(host_p.dtype), host_p), step
-        assert bits_equal(rule.first.download(host_p.dtype), host_m), step
-        assert bits_equal(rule.second.download(host_p.dtype), host_v), step
+        assert same_bits(p.download(host_p.dtype), host_p, dtype), step
+        assert same_bits(rule.first.download(host_p.dtype), host_m, dtype), step
+        assert same_bits(rule.second.download(host_p.dtype), host_v, dtype), step
 
 
 def test_config5_adam_over_the_mlp_parameters():
