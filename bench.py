@@ -86,15 +86,20 @@ def gemm(kind: str, m: int, k: int, n: int, seed: int, sigma, steps: int, warmup
     code = KIND[kind]
     op = lambda: lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
     ms = timed(op, steps, warmup)
-    # The matrix-core kernel alone: the product reads B as N x K, so hand it
+    # A 16-bit product is one kernel launch, so the call's event time is the
+    # kernel's; an f32 product first transposes B, so its kernel is timed on
     # B^T directly (`matmul_transposed_add` Right, same kernel, same shapes).
-    bt = lib.Buffer(k * n * size)
-    lib.call("tc_transpose", size, k, n, b.ptr, bt.ptr)
-    kernel = lambda: lib.call("tc_matmul", code, code, lib.RIGHT, 0, m, k, n, a.ptr, bt.ptr, c.ptr)
-    kernel_ms = timed(kernel, steps, warmup)
+    kernel_ms = ms
+    extra = []
+    if kind == "f32":
+        bt = lib.Buffer(k * n * size)
+        lib.call("tc_transpose", size, k, n, b.ptr, bt.ptr)
+        kernel = lambda: lib.call("tc_matmul", code, code, lib.RIGHT, 0, m, k, n, a.ptr, bt.ptr, c.ptr)
+        kernel_ms = timed(kernel, steps, warmup)
+        extra.append(bt)
     flops = 2.0 * m * n * k
     achieved = flops / (kernel_ms * 1e-3) / 1e12
-    for buffer in (a, b, bt, c):
+    for buffer in (a, b, c, *extra):
         buffer.free()
     return {
         "workload": f"{kind} GEMM {m}x{k}x{n}",

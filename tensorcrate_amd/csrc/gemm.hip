@@ -8,26 +8,28 @@
 // matrix cores', not the host's left-to-right FMA chain, so results agree
 // with the host within the f32 tolerance the reference's Metal products keep.
 //
-// One kernel shape carries every product: C[M x N] (+)= A[M x K] . Bt[N x K]^T
-// with both operands K-contiguous, which is how a matrix core wants its
-// operands (each lane feeds it consecutive k).  A product whose operand is
-// stored the other way round is first transposed into a scratch block with
-// the LDS tile transpose.
+// 16-bit operands (the tiled kernel below, v_mfma_f32_32x32x16_{bf16,f16})
+// are read in whatever orientation they are stored in: a K-contiguous
+// operand's LDS tile is read with ds_read_b128, a row-contiguous one's with
+// gfx950's transposing ds_read_tr16_b64, so `matmul`, `matmul_add` and both
+// `matmul_transposed_add` forms run the same kernel with no transpose pass.
+// Blocks own 256 x 256 tiles of C over eight waves (128 x 128 over four for
+// small products), walk K 64 at a time with double-buffered LDS, stage HBM
+// through buffer loads whose out-of-range reads return zeros, and weave each
+// step's loads, LDS traffic and matrix-core steps with scheduling groups.
 //
-//  - 16-bit operands: v_mfma_f32_32x32x16_{bf16,f16}.  A 256 x 128 block tile
-//    and 64-deep k steps; four waves, each owning a 128 x 64 sub-tile as
-//    4 x 2 matrix-core tiles (128 f32 accumulators per lane).
-//  - f32 operands: v_mfma_f32_16x16x4_f32, the same block tile with 32-deep k
-//    steps and 8 x 4 tiles of 16 x 16 per wave.  One 16-byte LDS read feeds
-//    four consecutive matrix-core steps, since the sum over k does not care
-//    which lane holds which k as long as both operands agree.
+// f32 operands (v_mfma_f32_16x16x4_f32) and 16-bit operands whose rows are
+// not 16-byte aligned take the general kernels: both operands K-contiguous,
+// a product whose operand is stored the other way round first transposed
+// into a scratch block with the LDS tile transpose; 256 x 128 tiles, 64-deep
+// (16-bit) or 32-deep (f32) k steps, operands global -> registers -> LDS,
+// double-buffered, LDS rows padded by 16 bytes.  One 16-byte LDS read of f32
+// feeds four consecutive matrix-core steps, since the sum over k does not
+// care which lane holds which k as long as both operands agree.
 //
-// Operands travel global -> registers -> LDS, double-buffered so the next k
-// step's loads are in flight while the matrix cores work on this one; LDS
-// rows are padded by 16 bytes so a wave's 16-byte operand reads spread over
-// the banks.  Block tiles are ordered in groups of rows, and the linear
-// block index is first spread so that the blocks one XCD runs are
-// neighbours, which keeps each XCD's L2 working on a few A and B panels.
+// Block tiles are ordered in groups of rows, and the linear block index is
+// first spread so that the blocks one XCD runs are neighbours, which keeps
+// each XCD's L2 working on a few A and B panels.
 
 #include "common.hpp"
 
@@ -308,6 +310,284 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
     }
 }
 
+// ---- 16-bit operands in place: the tiled kernel ---------------------------------------
+//
+// C[M x N] (+)= A . B with each operand read in the layout it is stored in:
+// "K-contiguous" (A stored M x K, B stored N x K) or "row-contiguous" (A
+// stored K x M, B stored K x N — B's ordinary row-major form).  Each block
+// owns a BM x BN tile of C and walks K in 64-deep steps; the waves split the
+// tile WM x WN, each owning (BM/WM) x (BN/WN) as 32 x 32 matrix-core tiles.
+//
+// LDS holds each operand's tile in its HBM orientation, double-buffered:
+//  - K-contiguous: [rows][64 + 8] — a lane's 16-byte ds_read_b128 feeds one
+//    matrix-core step (row lane % 32, k (lane / 32) * 8 .. + 8); the 144-byte
+//    row stride puts each 16-lane phase on 16 distinct 4-bank groups.
+//  - row-contiguous: [64][rows + 32] — read with gfx950's transposing
+//    ds_read_tr16_b64, which hands each lane of a 16-lane group four
+//    k-consecutive values of one column: when lane j of the group addresses
+//    (k0 + j / 4, c0 + 4 (j % 4)), lane i receives rows k0 .. k0 + 3 of column
+//    c0 + i.  Two such reads give a lane the same (column, 8 k) fragment the
+//    K-contiguous read does, so no operand is ever transposed in HBM.  The
+//    (rows + 32)-element row stride keeps the four rows of a phase on
+//    distinct banks.
+// Requirements (checked by the host): 16-byte aligned operands, K a multiple
+// of 8 for K-contiguous operands, and the contiguous extent a multiple of 8
+// for row-contiguous ones.  M and N edges clamp the rows a block loads (the
+// extra rows only feed results that are never stored), and the K tail loads
+// zeros, so any M, N and K with those alignments run here.
+
+constexpr int kTileK = 64;
+constexpr int kPadK = 8;    // elements after each K-contiguous LDS row
+constexpr int kPadRow = 32;  // elements after each row-contiguous LDS row
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+template <int ROWS, bool KC>
+struct LdsTile {
+    // Elements of one buffer of the operand's LDS tile.
+    static constexpr int kElems = KC ? ROWS * (kTileK + kPadK) : kTileK * (ROWS + kPadRow);
+};
+
+__device__ __forceinline__ short4v read_tr16(const void* lds_addr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) short4v*)(const_cast<void*>(lds_addr)));
+}
+
+// The descriptor word that makes a gfx9-family buffer resource a plain,
+// untyped byte range (32-bit data format, no swizzle, no stride).
+constexpr int kBufferFlags = 0x00020000;
+
+// One operand's global -> register -> LDS staging for a block: `ROWS` rows
+// (M for A, N for B) of the tile, 64 deep in K, `THREADS` threads.  Loads go
+// through a buffer resource over the operand, which answers zeros past its
+// end: rows past M or N at the bottom of a K-contiguous operand, and the K
+// tail of a row-contiguous one, load zeros with no test in the loop.  Every
+// chunk a thread stages sits a block-uniform distance from its first, so the
+// only per-thread state is one byte offset into HBM and one into LDS.
+template <typename S, int ROWS, bool KC, int THREADS>
+struct Stager {
+    static constexpr int kChunks = ROWS * kTileK / 8;  // 16-byte chunks per tile
+    static constexpr int kPer = kChunks / THREADS;
+    static_assert(kChunks % THREADS == 0, "tile chunks must divide among the threads");
+    // Threads per tile row and the tile rows one pass of them covers.
+    static constexpr int kRowThreads = KC ? kTileK / 8 : ROWS / 8;
+    static_assert(THREADS % kRowThreads == 0, "a pass of the threads must cover whole tile rows");
+    static constexpr int kPassRows = THREADS / kRowThreads;
+    static constexpr int kLdsRow = KC ? kTileK + kPadK : ROWS + kPadRow;
+
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t offset;      // this thread's first chunk, in bytes from the resource's base
+    uint32_t pass_bytes;  // bytes between a thread's consecutive chunks
+    uint32_t k_bytes;     // bytes per step of k
+    uint32_t lds_at;      // this thread's first chunk in the LDS tile, in elements
+    uint32_t k_in;        // the k of a K-contiguous thread's chunks within a step
+
+    // `rows` and `ld` are the operand's extent along the tile's rows and its
+    // stored row length; `first` the tile's first row; `depth` is K.
+    __device__ void init(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int t) {
+        const uint32_t row = t / kRowThreads, part = (t % kRowThreads) * 8;
+        if (KC) {
+            // Based at the tile's first row: rows past the operand's last
+            // fall beyond the resource.
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + static_cast<uint64_t>(first) * ld), 0,
+                                                     (rows - first) * ld * sizeof(S), kBufferFlags);
+            offset = (row * ld + part) * sizeof(S);
+            pass_bytes = kPassRows * ld * sizeof(S);
+            k_bytes = sizeof(S);
+            k_in = part;
+        } else {
+            // Based at the tile's first column: k rows past K fall beyond
+            // the resource; columns past the last only feed results that
+            // are never stored.
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + first), 0,
+                                                     (depth * ld - first) * sizeof(S), kBufferFlags);
+            offset = (row * ld + part) * sizeof(S);
+            pass_bytes = kPassRows * ld * sizeof(S);
+            k_bytes = ld * sizeof(S);
+            k_in = 0;
+        }
+        lds_at = row * kLdsRow + part;
+    }
+    // The step at `k0`; `full` says all 64 k are inside K.  Past K a
+    // K-contiguous operand's chunks are the next row's, so they are pointed
+    // past the resource's end (2^31 and more; operands are smaller), where
+    // they load zeros.
+    __device__ __forceinline__ void fetch(uint4 (&stage)[kPer], uint32_t k0, uint32_t K, bool full) const {
+        const uint32_t at = (full || !KC || k0 + k_in < K) ? offset : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, at, i * pass_bytes + k0 * k_bytes, 0);
+            stage[i] = __builtin_bit_cast(uint4, v);
+        }
+    }
+    __device__ __forceinline__ void commit(const uint4 (&stage)[kPer], S* lds) const {
+        uint4* to = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+        for (int i = 0; i < kPer; i++) to[(lds_at + i * kPassRows * kLdsRow) / 8] = stage[i];
+    }
+};
+
+// A lane's 8-element matrix-core fragment of tile row `row` (the tile's M or
+// N index) at k `k` (a multiple of 8) from an LDS tile.
+template <typename S, int ROWS, bool KC>
+__device__ __forceinline__ uint4 fragment(const S* lds, int row_base, int k_base, int lane) {
+    if (KC) {
+        // Indexed in 16-byte units, so the read is a single ds_read_b128.
+        constexpr int kRow16 = (kTileK + kPadK) / 8;
+        return reinterpret_cast<const uint4*>(lds)[(row_base + lane % 32) * kRow16 + k_base / 8 + lane / 32];
+    } else {
+        const int g = lane / 16, j = lane % 16;
+        const int k = k_base + (g / 2) * 8 + j / 4;
+        const int col = row_base + (g % 2) * 16 + 4 * (j % 4);
+        const S* at = lds + k * (ROWS + kPadRow) + col;
+        short4v lo = read_tr16(at);
+        short4v hi = read_tr16(at + 4 * (ROWS + kPadRow));
+        uint4 out;
+        out.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
+        out.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
+        out.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
+        out.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
+        return out;
+    }
+}
+
+// The order the scheduler is asked to keep within one step: F matrix-core
+// steps per slice, each followed by its share of the next step's HBM loads
+// (first slice), of the next slice's LDS reads (all but the last) or of the
+// staged step's LDS writes (last slice).
+template <int F, int LOADS, int READS, int SLICES, int Q = 0, int R = 0>
+__device__ __forceinline__ void weave() {
+    if constexpr (Q < SLICES) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // a matrix-core step
+        constexpr int loads = LOADS * (R + 1) / F - LOADS * R / F;
+        constexpr int reads = READS * (R + 1) / F - READS * R / F;
+        if constexpr (Q == 0 && loads > 0) __builtin_amdgcn_sched_group_barrier(0x020, loads, 0);  // HBM loads
+        if constexpr (Q + 1 < SLICES && reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);  // LDS reads
+        if constexpr (Q + 1 == SLICES && loads > 0) __builtin_amdgcn_sched_group_barrier(0x200, loads, 0);  // LDS writes
+        if constexpr (R + 1 < F) {
+            weave<F, LOADS, READS, SLICES, Q, R + 1>();
+        } else {
+            weave<F, LOADS, READS, SLICES, Q + 1, 0>();
+        }
+    }
+}
+
+template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(const S* __restrict__ A, const S* __restrict__ B,
+                                                               O* __restrict__ C, uint32_t M, uint32_t N,
+                                                               uint32_t K, bool accumulate) {
+    constexpr int kThreadsT = WM * WN * 64;
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+    constexpr int kA = LdsTile<BM, A_KC>::kElems, kB = LdsTile<BN, B_KC>::kElems;
+    __shared__ __attribute__((aligned(16))) S lds_a[2 * kA];
+    __shared__ __attribute__((aligned(16))) S lds_b[2 * kB];
+
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    uint32_t tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x;
+    const int lane = t % 64;
+    const int wave = t / 64;
+    const int wm = wave / WN, wn = wave % WN;
+
+    Stager<S, BM, A_KC, kThreadsT> sa;
+    Stager<S, BN, B_KC, kThreadsT> sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, t);
+    sb.init(B, n0, N, B_KC ? K : N, K, t);
+    uint4 stage_a[Stager<S, BM, A_KC, kThreadsT>::kPer];
+    uint4 stage_b[Stager<S, BN, B_KC, kThreadsT>::kPer];
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
+
+    const uint32_t steps = (K + kTileK - 1) / kTileK;
+    if (steps > 0) {
+        const bool full = kTileK <= K;
+        sa.fetch(stage_a, 0, K, full);
+        sb.fetch(stage_b, 0, K, full);
+        sa.commit(stage_a, lds_a);
+        sb.commit(stage_b, lds_b);
+        __syncthreads();
+    }
+    // Fragments are double-buffered in registers: the reads for the next
+    // 16-deep slice are issued before the matrix-core steps of this one.
+    uint4 fa[2][TM], fb[2][TN];
+    auto read_fragments = [&](int slot, const S* la, const S* lb, int kk) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) fa[slot][i] = fragment<S, BM, A_KC>(la, wm * (BM / WM) + i * 32, kk, lane);
+#pragma unroll
+        for (int j = 0; j < TN; j++) fb[slot][j] = fragment<S, BN, B_KC>(lb, wn * (BN / WN) + j * 32, kk, lane);
+    };
+    if (steps > 0) read_fragments(0, lds_a, lds_b, 0);
+    // One step is one basic block, so the scheduler can weave it: the next
+    // step's HBM loads go out with the first slice's matrix-core steps, each
+    // slice's steps carry the next slice's LDS reads, and the last slice's
+    // carry the LDS writes of the staged step.  The last step re-loads
+    // itself rather than branch, and writes a buffer no one reads again.
+    constexpr int kSlices = kTileK / 16;
+    constexpr int kSteps = TM * TN;  // matrix-core steps per slice
+    constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);  // LDS reads per slice
+    constexpr int kLoads = Stager<S, BM, A_KC, kThreadsT>::kPer + Stager<S, BN, B_KC, kThreadsT>::kPer;
+    for (uint32_t step = 0; step < steps; step++) {
+        const int buffer = step & 1;
+        const uint32_t k0 = (step + 1 < steps ? step + 1 : step) * kTileK;
+        const bool full = k0 + kTileK <= K;
+        sa.fetch(stage_a, k0, K, full);
+        sb.fetch(stage_b, k0, K, full);
+        const S* la = lds_a + buffer * kA;
+        const S* lb = lds_b + buffer * kB;
+#pragma unroll
+        for (int q = 0; q < kSlices; q++) {
+            if (q + 1 < kSlices) read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[q & 1][i], fb[q & 1][j], acc[i][j]);
+        }
+        sa.commit(stage_a, lds_a + (buffer ^ 1) * kA);
+        sb.commit(stage_b, lds_b + (buffer ^ 1) * kB);
+        weave<kSteps, kLoads, kReads, kSlices>();
+        __syncthreads();
+        read_fragments(0, lds_a + (buffer ^ 1) * kA, lds_b + (buffer ^ 1) * kB, 0);
+    }
+
+    // A 32 x 32 result tile: lane holds column lane % 32, and rows
+    // 8 (e / 4) + 4 (lane / 32) + e % 4 for its 16 values e.
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const uint32_t col = n0 + wn * (BN / WN) + j * 32 + lane % 32;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const uint32_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
+            }
+        }
+    }
+}
+
+// The tiled kernel's shapes: a 256 x 256 tile over eight waves of 128 x 64
+// (two waves per SIMD, so one's waits overlap the other's matrix-core
+// steps), and a 128 x 128 tile over four waves of 64 x 64 for products too
+// small to give every CU a few large tiles.
+template <typename S, typename O, bool A_KC, bool B_KC>
+void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
+                    hipStream_t s) {
+    const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
+    if (large >= static_cast<uint32_t>(compute_units())) {
+        tiled16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+    } else {
+        const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);
+        tiled16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+    }
+}
+
 // ---- host side ---------------------------------------------------------------------
 
 // A K-contiguous copy of an operand stored the other way round, in a block
@@ -348,10 +628,30 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
     }
     const S* pa = static_cast<const S*>(a);
     const S* pb = static_cast<const S*>(b);
+    if constexpr (!std::is_same<S, float>::value) {
+        // 16-bit operands read in place whenever their rows are 16-byte
+        // aligned: A is K-contiguous unless LEFT, B only when RIGHT.
+        const bool a_kc = transposed != TC_LEFT, b_kc = transposed == TC_RIGHT;
+        const bool in_place = aligned16(a) && aligned16(b) && (a_kc ? k % 8 == 0 : m % 8 == 0) &&
+                              (b_kc ? k % 8 == 0 : n % 8 == 0);
+        if (in_place) {
+            const uint32_t m32 = static_cast<uint32_t>(m), k32 = static_cast<uint32_t>(k),
+                           n32 = static_cast<uint32_t>(n);
+            O* pc = static_cast<O*>(c);
+            if (a_kc && b_kc) {
+                launch_tiled16<S, O, true, true>(pa, pb, pc, m32, k32, n32, accumulate, s);
+            } else if (a_kc) {
+                launch_tiled16<S, O, true, false>(pa, pb, pc, m32, k32, n32, accumulate, s);
+            } else {
+                launch_tiled16<S, O, false, false>(pa, pb, pc, m32, k32, n32, accumulate, s);
+            }
+            return check_launch("matmul");
+        }
+    }
     void* made_a = nullptr;
     void* made_b = nullptr;
     int status = TC_OK;
-    // The kernel wants A as M x K and B as N x K.
+    // The general kernels want A as M x K and B as N x K.
     if (transposed == TC_LEFT) {  // A stored K x M
         status = transposed_copy(a, k, m, sizeof(S), &made_a);
         if (status != TC_OK) return status;
