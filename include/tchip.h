@@ -219,8 +219,9 @@ int tc_compare(uint32_t dtype, uint32_t op, const void* a, const void* b, void* 
 /* `vector_compare_scalar` / `matrix_compare_scalar` (kernels.rs:849, :929). */
 int tc_compare_scalar(uint32_t dtype, uint32_t op, const void* a, float scalar, int scalar_left,
                       void* out, uint64_t n);
-/* `vector_clamp` / `matrix_clamp` (kernels.rs:863, :938): fails unless
- * low <= high. */
+/* `vector_clamp` / `matrix_clamp` (kernels.rs:863, :938): min(max(x, low),
+ * high).  Fails when low > high (shape.rs:30-43); a NaN bound passes and is
+ * inert. */
 int tc_clamp(uint32_t dtype, const void* a, float low, float high, void* out, uint64_t n);
 
 /* `Kernels::strided_binary` (kernels.rs:1162-1166; Host strided.rs:29-78):

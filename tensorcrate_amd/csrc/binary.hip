@@ -349,10 +349,9 @@ int tc_compare_scalar(uint32_t dtype, uint32_t op, const void* a, float scalar, 
 }
 
 int tc_clamp(uint32_t dtype, const void* a, float low, float high, void* out, uint64_t n) {
-    if (!(low <= high)) {
-        return fail(TC_INVALID, "clamp: low " + std::to_string(low) + " is above high " +
-                                    std::to_string(high));
-    }
+    // Only an ordered pair the wrong way round is refused: a NaN bound is
+    // inert, since max(x, NaN) and min(x, NaN) are x (shape.rs:30-43).
+    if (low > high) return fail(TC_INVALID, "clamp: the lower bound exceeds the upper one");
     TC_STREAM(s);
     TC_DISPATCH_FLOAT(dtype, "clamp", S, return launch_map<S>(a, nullptr, out, n, ClampTo{low, high}, s, "clamp"));
     return TC_OK;

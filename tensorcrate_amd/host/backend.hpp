@@ -1,0 +1,306 @@
+// The host side of the `Hip` backend in C++: tensorcrate's `Backend` storage
+// and the `Kernels<T>` operations the tape and the optimizers are written in
+// (src/tensors/backend.rs:77-178, src/tensors/kernels.rs:829-1188), as types
+// over the C ABI of include/tchip.h.
+//
+// The reference's host code is Rust and reaches a device backend through
+// `B: Kernels<T>`; this mirror keeps its names, argument meanings and error
+// behaviour so the code above it (tape.hpp, optim.hpp) reads like the
+// reference's own.  Shape mistakes throw `std::invalid_argument` with the
+// reference's panic wording before anything reaches the device
+// (tensors/shape.rs:9-60); a failed device call throws `hip::Error` with the
+// library's message, the analogue of `require_metal`'s panic
+// (backend.rs:422-426).  Nothing here computes on the host: every operation
+// is one or two calls into libtchip.
+#pragma once
+
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "tchip.h"
+
+namespace tensorcrate {
+namespace hip {
+
+struct Error : std::runtime_error {
+    int status;
+    Error(int s, const std::string& message) : std::runtime_error(message), status(s) {}
+};
+
+inline void check(int status) {
+    if (status != TC_OK) throw Error(status, tc_last_error());
+}
+
+// `BinaryOp`, `Compare`, `Reduce`, `Transposed` (kernels.rs:30-187, :461).
+enum class BinaryOp : uint32_t { Add = TC_ADD, Sub = TC_SUB, Mul = TC_MUL, Div = TC_DIV, Rem = TC_REM };
+enum class Compare : uint32_t {
+    Min = TC_MIN, Max = TC_MAX, MaxShare = TC_MAX_SHARE,
+    Less = TC_LESS, LessEqual = TC_LESS_EQUAL, Greater = TC_GREATER, GreaterEqual = TC_GREATER_EQUAL
+};
+enum class Reduce : uint32_t { Sum = TC_REDUCE_SUM, Min = TC_REDUCE_MIN, Max = TC_REDUCE_MAX };
+enum class Transposed : uint32_t { Left = TC_LEFT, Right = TC_RIGHT };
+
+// The element types a kernel computes in; only f32 is instantiated here.
+template <typename T>
+struct DType;
+template <>
+struct DType<float> {
+    static constexpr uint32_t code = TC_F32;
+};
+
+// `Backend::Storage<T>` for Hip (backend.rs:86-111): one device allocation
+// from the calling thread's stream-ordered cache, freed back to it.  Like a
+// Metal tensor it belongs to the thread that made it.
+template <typename T>
+class Storage {
+   public:
+    explicit Storage(size_t len) : len_(len) { check(tc_alloc(len * sizeof(T), &ptr_)); }
+    ~Storage() {
+        if (ptr_ != nullptr) tc_free(ptr_);
+    }
+    Storage(const Storage&) = delete;
+    Storage& operator=(const Storage&) = delete;
+    Storage(Storage&& other) noexcept : ptr_(other.ptr_), len_(other.len_) {
+        other.ptr_ = nullptr;
+        other.len_ = 0;
+    }
+    Storage& operator=(Storage&& other) noexcept {
+        std::swap(ptr_, other.ptr_);
+        std::swap(len_, other.len_);
+        return *this;
+    }
+
+    // `Backend::store` (backend.rs:89): one upload.
+    static Storage store(const T* values, size_t len) {
+        Storage s(len);
+        check(tc_upload(s.ptr_, values, len * sizeof(T)));
+        return s;
+    }
+    // `Vector::filled` on the device: a fill kernel, not an upload of a
+    // host vector as the reference's generic `filled` makes (vector.rs:101-106).
+    static Storage filled(size_t len, T value) {
+        Storage s(len);
+        check(tc_fill(s.ptr_, len, sizeof(T), &value));
+        return s;
+    }
+    // `Backend::duplicate` (backend.rs:111): a device-to-device copy.
+    Storage duplicate() const {
+        Storage s(len_);
+        check(tc_copy(s.ptr_, ptr_, len_ * sizeof(T)));
+        return s;
+    }
+    // `Backend::as_slice` (backend.rs:99): waits for queued work, downloads.
+    std::vector<T> to_host() const {
+        std::vector<T> out(len_);
+        check(tc_download(out.data(), ptr_, len_ * sizeof(T)));
+        return out;
+    }
+
+    void* ptr() { return ptr_; }
+    const void* ptr() const { return ptr_; }
+    size_t len() const { return len_; }
+
+   private:
+    void* ptr_ = nullptr;
+    size_t len_ = 0;
+};
+
+// `Vector<T, Hip>` (tensors/vector.rs).
+template <typename T>
+class Vector {
+   public:
+    explicit Vector(Storage<T> s) : storage_(std::move(s)) {}
+    static Vector filled(size_t len, T value) { return Vector(Storage<T>::filled(len, value)); }
+    static Vector from_host(const std::vector<T>& values) { return Vector(Storage<T>::store(values.data(), values.size())); }
+    Vector duplicate() const { return Vector(storage_.duplicate()); }
+    std::vector<T> to_host() const { return storage_.to_host(); }
+    size_t len() const { return storage_.len(); }
+    Storage<T>& storage() { return storage_; }
+    const Storage<T>& storage() const { return storage_; }
+    Storage<T> into_storage() && { return std::move(storage_); }
+
+   private:
+    Storage<T> storage_;
+};
+
+// `Matrix<T, Hip>` (tensors/matrix.rs:23): row-major `rows x cols`.
+template <typename T>
+class Matrix {
+   public:
+    Matrix(size_t rows, size_t cols, Storage<T> s) : rows_(rows), cols_(cols), storage_(std::move(s)) {
+        if (storage_.len() != rows * cols) {
+            throw std::invalid_argument("from_storage: " + std::to_string(storage_.len()) + " elements for a " +
+                                        std::to_string(rows) + "×" + std::to_string(cols) + " matrix");
+        }
+    }
+    static Matrix filled(size_t rows, size_t cols, T value) {
+        return Matrix(rows, cols, Storage<T>::filled(rows * cols, value));
+    }
+    static Matrix from_host(size_t rows, size_t cols, const std::vector<T>& values) {
+        return Matrix(rows, cols, Storage<T>::store(values.data(), values.size()));
+    }
+    Matrix duplicate() const { return Matrix(rows_, cols_, storage_.duplicate()); }
+    std::vector<T> to_host() const { return storage_.to_host(); }
+    size_t rows() const { return rows_; }
+    size_t cols() const { return cols_; }
+    std::pair<size_t, size_t> shape() const { return {rows_, cols_}; }
+    size_t len() const { return rows_ * cols_; }
+    Storage<T>& storage() { return storage_; }
+    const Storage<T>& storage() const { return storage_; }
+    Storage<T> into_storage() && { return std::move(storage_); }
+
+   private:
+    size_t rows_, cols_;
+    Storage<T> storage_;
+};
+
+// ---- the reference's shape checks (tensors/shape.rs:9-60) ----------------------
+
+inline std::string dims(std::pair<size_t, size_t> s) {
+    return std::to_string(s.first) + "×" + std::to_string(s.second);
+}
+
+inline void assert_same_len(size_t left, size_t right, const char* operation) {
+    if (left != right) {
+        throw std::invalid_argument(std::string(operation) + ": vector lengths differ, " + std::to_string(left) +
+                                    " and " + std::to_string(right));
+    }
+}
+
+inline void assert_same_shape(std::pair<size_t, size_t> left, std::pair<size_t, size_t> right, const char* operation) {
+    if (left != right) {
+        throw std::invalid_argument(std::string(operation) + ": matrix shapes differ, " + dims(left) + " and " +
+                                    dims(right));
+    }
+}
+
+inline void assert_inner(std::pair<size_t, size_t> left, std::pair<size_t, size_t> right, const char* operation) {
+    if (left.second != right.first) {
+        throw std::invalid_argument(std::string(operation) + ": inner dimensions differ, " + dims(left) + " times " +
+                                    dims(right));
+    }
+}
+
+// ---- Kernels<T> for Hip (kernels.rs:829-1188) -----------------------------------
+
+template <typename T>
+struct Kernels {
+    static constexpr uint32_t dtype = DType<T>::code;
+
+    // `vector_elementwise` (kernels.rs:832).
+    static Vector<T> vector_elementwise(const Vector<T>& a, const Vector<T>& b, BinaryOp op) {
+        assert_same_len(a.len(), b.len(), "elementwise");
+        Storage<T> out(a.len());
+        check(tc_elementwise(dtype, static_cast<uint32_t>(op), a.storage().ptr(), b.storage().ptr(), out.ptr(), a.len()));
+        return Vector<T>(std::move(out));
+    }
+    // `matrix_elementwise` (kernels.rs:912).
+    static Matrix<T> matrix_elementwise(const Matrix<T>& a, const Matrix<T>& b, BinaryOp op) {
+        assert_same_shape(a.shape(), b.shape(), "elementwise");
+        Storage<T> out(a.len());
+        check(tc_elementwise(dtype, static_cast<uint32_t>(op), a.storage().ptr(), b.storage().ptr(), out.ptr(), a.len()));
+        return Matrix<T>(a.rows(), a.cols(), std::move(out));
+    }
+    // `vector_broadcast` / `matrix_broadcast` (kernels.rs:838, :918):
+    // x op s, or s op x when `scalar_left`.
+    static Vector<T> vector_broadcast(const Vector<T>& a, T scalar, BinaryOp op, bool scalar_left) {
+        Storage<T> out(a.len());
+        check(tc_broadcast(dtype, static_cast<uint32_t>(op), a.storage().ptr(), scalar, scalar_left, out.ptr(), a.len()));
+        return Vector<T>(std::move(out));
+    }
+    static Matrix<T> matrix_broadcast(const Matrix<T>& a, T scalar, BinaryOp op, bool scalar_left) {
+        Storage<T> out(a.len());
+        check(tc_broadcast(dtype, static_cast<uint32_t>(op), a.storage().ptr(), scalar, scalar_left, out.ptr(), a.len()));
+        return Matrix<T>(a.rows(), a.cols(), std::move(out));
+    }
+    // `matrix_compare` / `matrix_compare_scalar` (kernels.rs:926, :929).
+    static Matrix<T> matrix_compare(const Matrix<T>& a, const Matrix<T>& b, Compare op) {
+        assert_same_shape(a.shape(), b.shape(), "compare");
+        Storage<T> out(a.len());
+        check(tc_compare(dtype, static_cast<uint32_t>(op), a.storage().ptr(), b.storage().ptr(), out.ptr(), a.len()));
+        return Matrix<T>(a.rows(), a.cols(), std::move(out));
+    }
+    static Matrix<T> matrix_compare_scalar(const Matrix<T>& a, T scalar, Compare op, bool scalar_left) {
+        Storage<T> out(a.len());
+        check(tc_compare_scalar(dtype, static_cast<uint32_t>(op), a.storage().ptr(), scalar, scalar_left, out.ptr(),
+                                a.len()));
+        return Matrix<T>(a.rows(), a.cols(), std::move(out));
+    }
+    // `matmul` (kernels.rs:956): (R×K)·(K×C).
+    static Matrix<T> matmul(const Matrix<T>& a, const Matrix<T>& b) {
+        assert_inner(a.shape(), b.shape(), "matmul");
+        Storage<T> out(a.rows() * b.cols());
+        check(tc_matmul(dtype, dtype, TC_PLAIN, 0, a.rows(), a.cols(), b.cols(), a.storage().ptr(), b.storage().ptr(),
+                        out.ptr()));
+        return Matrix<T>(a.rows(), b.cols(), std::move(out));
+    }
+    // `matmul_add` (kernels.rs:963): the addend is consumed as the accumulator.
+    static Matrix<T> matmul_add(const Matrix<T>& a, const Matrix<T>& b, Matrix<T> addend) {
+        assert_inner(a.shape(), b.shape(), "matmul_add");
+        assert_same_shape(addend.shape(), {a.rows(), b.cols()}, "matmul_add");
+        check(tc_matmul(dtype, dtype, TC_PLAIN, 1, a.rows(), a.cols(), b.cols(), a.storage().ptr(), b.storage().ptr(),
+                        addend.storage().ptr()));
+        return addend;
+    }
+    // `matmul_transposed_add` (kernels.rs:975-985): addend + Aᵀ·B (Left) or
+    // addend + A·Bᵀ (Right), the transposed operand read in place.
+    static Matrix<T> matmul_transposed_add(const Matrix<T>& a, const Matrix<T>& b, Transposed which, Matrix<T> addend) {
+        size_t m, k, n;
+        if (which == Transposed::Left) {
+            assert_inner({a.cols(), a.rows()}, b.shape(), "matmul_transposed_add");
+            m = a.cols(), k = a.rows(), n = b.cols();
+        } else {
+            assert_inner(a.shape(), {b.cols(), b.rows()}, "matmul_transposed_add");
+            m = a.rows(), k = a.cols(), n = b.rows();
+        }
+        assert_same_shape(addend.shape(), {m, n}, "matmul_transposed_add");
+        check(tc_matmul(dtype, dtype, static_cast<uint32_t>(which), 1, m, k, n, a.storage().ptr(), b.storage().ptr(),
+                        addend.storage().ptr()));
+        return addend;
+    }
+    // `matvec` (kernels.rs:901): M·v.
+    static Vector<T> matvec(const Matrix<T>& m, const Vector<T>& v) {
+        if (m.cols() != v.len()) {
+            throw std::invalid_argument("matvec: a " + dims(m.shape()) + " matrix times a length-" +
+                                        std::to_string(v.len()) + " vector");
+        }
+        Storage<T> out(m.rows());
+        check(tc_matvec(dtype, 0, m.rows(), m.cols(), m.storage().ptr(), v.storage().ptr(), out.ptr()));
+        return Vector<T>(std::move(out));
+    }
+    // `vecmat` (kernels.rs:899): vᵀ·M.
+    static Vector<T> vecmat(const Vector<T>& v, const Matrix<T>& m) {
+        if (m.rows() != v.len()) {
+            throw std::invalid_argument("vecmat: a length-" + std::to_string(v.len()) + " vector times a " +
+                                        dims(m.shape()) + " matrix");
+        }
+        Storage<T> out(m.cols());
+        check(tc_vecmat(dtype, m.rows(), m.cols(), v.storage().ptr(), m.storage().ptr(), out.ptr()));
+        return Vector<T>(std::move(out));
+    }
+    // `transpose` (kernels.rs:987).
+    static Matrix<T> transpose(const Matrix<T>& m) {
+        Storage<T> out(m.len());
+        check(tc_transpose(sizeof(T), m.rows(), m.cols(), m.storage().ptr(), out.ptr()));
+        return Matrix<T>(m.cols(), m.rows(), std::move(out));
+    }
+    // `vector_reduce` (kernels.rs:867): the whole buffer folded; reading the
+    // value waits for the device.
+    static T reduce(const Storage<T>& values, Reduce op) {
+        float* result = nullptr;
+        check(tc_alloc(sizeof(float), reinterpret_cast<void**>(&result)));
+        int status = tc_vector_reduce(dtype, values.ptr(), values.len(), static_cast<uint32_t>(op), result);
+        float host = 0.0f;
+        if (status == TC_OK) status = tc_download(&host, result, sizeof(float));
+        tc_free(result);
+        check(status);
+        return static_cast<T>(host);
+    }
+};
+
+}  // namespace hip
+}  // namespace tensorcrate

@@ -275,3 +275,94 @@ def region(source: Buffer | int, source_len: int, shape, src_offset, src_strides
     r.src = strided(src_offset, src_strides)
     r.dst = strided(dst_offset, dst_strides)
     return r
+
+
+# ---- the C++ host mirror (include/tchip_host.h) -------------------------------
+
+HOST_LIBRARY = PACKAGE / "libtchip_host.so"
+
+HOST_SIGNATURES = {
+    "tch_last_error": [],
+    "tch_mlp_create": [u32, ctypes.POINTER(u64), u64, ctypes.POINTER(vp), ctypes.POINTER(vp), vp, vp, f32,
+                       ctypes.POINTER(vp)],
+    "tch_mlp_step": [vp, i32],
+    "tch_mlp_loss": [vp, ctypes.POINTER(f32)],
+    "tch_mlp_parameters": [vp, u32, vp, vp],
+    "tch_mlp_gradients": [vp, u32, vp, vp],
+    "tch_mlp_destroy": [vp],
+}
+
+_host: ctypes.CDLL | None = None
+
+
+def load_host() -> ctypes.CDLL:
+    """``libtchip_host.so``, after ``libtchip.so`` (which it links, so both
+    share one runtime state); raises if it is not built."""
+    global _host
+    if _host is not None:
+        return _host
+    load()
+    if not HOST_LIBRARY.exists():
+        raise RuntimeError(f"{HOST_LIBRARY} is not built: run __graft_entry__.build() first")
+    host = ctypes.CDLL(str(HOST_LIBRARY))
+    for name, argtypes in HOST_SIGNATURES.items():
+        fn = getattr(host, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p if name == "tch_last_error" else (None if name == "tch_mlp_destroy" else ctypes.c_int)
+    _host = host
+    return host
+
+
+def host_call(name: str, *args) -> None:
+    status = getattr(load_host(), name)(*args)
+    if status != OK:
+        raise HipError(status, load_host().tch_last_error().decode())
+
+
+class Mlp:
+    """The training step of tensorcrate's benchmark harness (``mlp_step``,
+    benches/nn_ops.rs:875-921) on the C++ tape, through ``tch_mlp_*``."""
+
+    def __init__(self, widths, batch: int, weights, biases, inputs, targets, rate: float):
+        self.widths, self.batch = list(widths), int(batch)
+        layers = len(self.widths) - 1
+        keep = [np.ascontiguousarray(a, np.float32) for a in (*weights, *biases, inputs, targets)]
+        ws, bs, x, y = keep[:layers], keep[layers:2 * layers], keep[-2], keep[-1]
+        dims = (u64 * (layers + 1))(*self.widths)
+        wp = (vp * layers)(*[a.ctypes.data for a in ws])
+        bp = (vp * layers)(*[a.ctypes.data for a in bs])
+        handle = vp()
+        host_call("tch_mlp_create", layers, dims, self.batch, wp, bp, x.ctypes.data, y.ctypes.data, rate,
+                  ctypes.byref(handle))
+        self.handle = handle.value
+
+    def step(self, update: bool = True) -> None:
+        host_call("tch_mlp_step", self.handle, int(update))
+
+    def loss(self) -> float:
+        value = f32()
+        host_call("tch_mlp_loss", self.handle, ctypes.byref(value))
+        return value.value
+
+    def _read(self, name: str, layer: int):
+        w = np.empty((self.widths[layer + 1], self.widths[layer]), np.float32)
+        b = np.empty(self.widths[layer + 1], np.float32)
+        host_call(name, self.handle, layer, w.ctypes.data, b.ctypes.data)
+        return w, b
+
+    def parameters(self, layer: int):
+        return self._read("tch_mlp_parameters", layer)
+
+    def gradients(self, layer: int):
+        return self._read("tch_mlp_gradients", layer)
+
+    def close(self) -> None:
+        if self.handle is not None:
+            load_host().tch_mlp_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -12,10 +12,11 @@ from tensorcrate_amd import lib
 ROOT = Path(__file__).resolve().parent.parent
 
 
-def declared_functions():
-    header = (ROOT / "include" / "tchip.h").read_text()
+def declared_functions(name="tchip.h", prefix="tc_"):
+    header = (ROOT / "include" / name).read_text()
     header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tc_\w+)\s*\(", header, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|void|const char\*)\s+(" + prefix + r"\w+)\s*\(", header,
+                                 flags=re.M)))
 
 
 def test_the_library_exports_every_declared_symbol():
@@ -28,6 +29,17 @@ def test_the_library_exports_every_declared_symbol():
     assert not missing, missing
     # The binding names exactly the declared set.
     assert sorted(lib.SIGNATURES) == names
+
+
+def test_the_host_mirror_exports_every_declared_symbol():
+    names = declared_functions("tchip_host.h", "tch_")
+    assert len(names) >= 7
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib.HOST_LIBRARY)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert not [name for name in names if name not in exported]
+    assert sorted(lib.HOST_SIGNATURES) == names
+    lib.load_host()
 
 
 def test_the_library_loads_and_binds():

@@ -139,3 +139,15 @@ def test_fill_and_duplicate():
     b = lib.Buffer(400)
     lib.call("tc_copy", b.ptr, a.ptr, 400)
     assert np.array_equal(b.download(np.float32), np.arange(100, dtype=np.float32))
+
+
+def test_clamp_bounds_follow_the_reference():
+    # A NaN bound is inert and only low > high is refused (shape.rs:30-43).
+    a = np.array([-3.0, -0.5, 0.0, 0.5, 3.0, np.nan], np.float32)
+    da, out = lib.Buffer.of(a), lib.Buffer(a.nbytes)
+    lib.call("tc_clamp", lib.F32, da.ptr, float("nan"), 1.0, out.ptr, a.size)
+    assert same(out.download(np.float32), np.fmin(np.fmax(a, np.nan), np.float32(1.0)))
+    lib.call("tc_clamp", lib.F32, da.ptr, -1.0, float("nan"), out.ptr, a.size)
+    assert same(out.download(np.float32), oracle.clamp(lib.F32, a, -1.0, float("nan")))
+    with pytest.raises(lib.HipError, match="lower bound exceeds the upper"):
+        lib.call("tc_clamp", lib.F32, da.ptr, 2.0, 1.0, out.ptr, a.size)
