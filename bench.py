@@ -37,6 +37,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from tensorcrate_amd import halfconv, lib  # noqa: E402
+from tensorcrate_amd.optim import Adam  # noqa: E402
 from tensorcrate_amd.tensor import Tensor  # noqa: E402
 
 HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
@@ -167,6 +168,66 @@ def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
     return lines
 
 
+def mlp_step(steps: int, warmup: int) -> list[dict]:
+    """Configuration 5: the training step of the reference's harness
+    (``mlp_step``, benches/nn_ops.rs:875-921) at 1024 -> 4096 -> 4096 -> 1024,
+    batch 4096, on the C++ tape: forward, backward and an Adam update of
+    every parameter, with nothing read back.  Its work is the 618.5 GFLOP of
+    its nine f32 products; the Adam step alone is timed as its own line."""
+    from oracle import mlp  # the synthetic network's generator only
+
+    widths, batch = (1024, 4096, 4096, 1024), 4096
+    weights, biases = mlp.he_init(widths, 4)
+    x, y = mlp.batch_of(widths, batch, 4)
+    net = lib.Mlp(widths, batch, weights, biases, x, y, 1e-3)
+    del weights, biases, x, y
+    ms = timed(net.step, steps, warmup)
+    flops = sum(2.0 * widths[l] * widths[l + 1] * batch for l in range(3)) * 3
+    net.close()
+    achieved = flops / (ms * 1e-3) / 1e12
+    lines = [{"workload": "MLP training step 1024-4096-4096-1024, batch 4096, f32, tape + Adam (configs[4])",
+              "value": 1e3 / ms, "unit": "steps/s", "ms": ms,
+              "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK["f32"], "unit": "TFLOP/s",
+                           "frac": achieved / MFMA_PEAK["f32"], "traffic": None}}]
+    # The Adam step over all 25,175,040 parameters as one tensor: reads the
+    # gradient, parameters and both moments, writes the last three.
+    n = sum(widths[l] * widths[l + 1] + widths[l + 1] for l in range(3))
+    params, grads = lib.Buffer(4 * n), lib.Buffer(4 * n)
+    lib.call("tc_fill", params.ptr, n, 4, ctypes.byref(ctypes.c_float(0.5)))
+    lib.call("tc_fill", grads.ptr, n, 4, ctypes.byref(ctypes.c_float(0.25)))
+    rule = Adam(1e-3)
+    rule.update(params, grads, 1, n)
+    ms = timed(lambda: rule.update(params, grads, 1, n), steps, warmup)
+    lines.append(hbm_line(f"Adam update, {n} f32 parameters (fused program)", 7 * 4 * n, ms))
+    return lines
+
+
+def traffic_probe() -> None:
+    """A short run for ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``: three
+    plain contiguous copies of 1 GiB through ``tc_strided_copy`` (the rows
+    kernel; 1 GiB read and 1 GiB written each, the counters' calibration),
+    then three launches of the headline product."""
+    n = 1 << 28
+    src, dst = lib.Buffer(4 * n), lib.Buffer(4 * n)
+    lib.call("tc_fill", src.ptr, n, 4, ctypes.byref(ctypes.c_float(1.0)))
+    shape = lib.dims([n])
+    at = lib.strided(0, [1])
+    for _ in range(3):
+        lib.call("tc_strided_copy", 4, src.ptr, n, 1, shape, ctypes.byref(at), dst.ptr)
+    lib.sync()
+    src.free()
+    dst.free()
+    m = k = n = 8192
+    rng = np.random.default_rng(3)
+    a = lib.Buffer.of(host_matrix("bf16", m, k, rng, 1 / np.sqrt(k)))
+    b = lib.Buffer.of(host_matrix("bf16", k, n, rng, 1 / np.sqrt(k)))
+    c = lib.Buffer(m * n * 2)
+    for _ in range(3):
+        lib.call("tc_matmul", lib.BF16, lib.BF16, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
+    lib.sync()
+    log("traffic probe done")
+
+
 def cpu_baseline(m: int, k: int, n: int) -> dict:
     """The oracle's restatement of the Host (simd) bf16 product —
     widen, i-p-j AVX2 FMA on one thread, round once (compact.rs:232-253,
@@ -199,6 +260,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--quick", action="store_true", help="headline only, no secondary workloads or CPU baseline")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--traffic-probe", action="store_true",
+                        help="only the short copy + product run that HBM-traffic counters are read over")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path, so --gpus must be 1", file=sys.stderr)
@@ -206,6 +269,9 @@ def main() -> int:
     lib.call("tc_init", 0)
     name, arch = lib.device_info()
     log(f"device {name} {arch}")
+    if args.traffic_probe:
+        traffic_probe()
+        return 0
 
     m = k = n = 8192
     log("bf16 GEMM 8192^3 ...")
@@ -222,6 +288,8 @@ def main() -> int:
         workloads += reductions((1024, 128, 1024), 1, max(args.steps // 2, 5), args.warmup)
         log("broadcast chain and copies ...")
         workloads += broadcast_and_copies(args.steps, args.warmup)
+        log("MLP training step and Adam ...")
+        workloads += mlp_step(max(args.steps // 4, 3), 2)
         for line in workloads:
             log(f"  {line['workload']}: {line['value']:.1f} {line['unit']} ({line['roofline']['frac'] * 100:.1f}%)")
     baseline = None

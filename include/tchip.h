@@ -301,6 +301,15 @@ int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_pl
              uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
              uint32_t output_count, uint64_t rows, uint64_t cols);
 
+/* How many fused programs this process has compiled into kernels of their
+ * own.  A dense program (every load in element order, every load before any
+ * store) is compiled on its second appearance and cached by its source, as
+ * the reference's Metal backend does (metal/codegen.rs:1-40); others, and
+ * any that fail to compile, run on the interpreter.  No counterpart in the
+ * reference's interface: a diagnostic in the manner of its `counters`
+ * feature (counters.rs:1-110), for tests and profiling. */
+int tc_fused_compiled(uint64_t* count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,7 @@ then one link.  Nothing here runs at import time.
 from __future__ import annotations
 
 import concurrent.futures
+import json
 import os
 import shutil
 import subprocess
@@ -64,14 +65,29 @@ def _compile(source: Path, flags: list[str]) -> Path:
     return target
 
 
+def _embedded_sources() -> Path:
+    """``scalar_ops.h`` as the C string ``tc_scalar_ops_source``: the header
+    the fused-program compiler hands hiprtc with every generated kernel."""
+    OBJECTS.mkdir(exist_ok=True)
+    text = (CSRC / "scalar_ops.h").read_text()
+    target = OBJECTS / "scalar_ops_source.cpp"
+    body = "".join(f"    {json.dumps(line + chr(10))}\n" for line in text.splitlines())
+    target.write_text('extern "C" const char tc_scalar_ops_source[] =\n' + body + "    ;\n")
+    return target
+
+
 def build_library(jobs: int | None = None) -> Path:
-    """Compile every ``csrc/*.hip`` for gfx950 and link ``libtchip.so``."""
+    """Compile every ``csrc/*.hip`` for gfx950 and link ``libtchip.so``
+    (with hiprtc, which compiles fused programs at run time)."""
     sources = sorted(CSRC.glob("*.hip"))
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
         objects = list(pool.map(lambda s: _compile(s, HIP_FLAGS), sources))
+    embedded = OBJECTS / "scalar_ops_source.o"
+    _run(["g++", "-O2", "-fPIC", "-c", str(_embedded_sources()), "-o", str(embedded)])
     staged = LIBRARY.with_suffix(".so.tmp")
-    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(staged)])
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), str(embedded), "-lhiprtc",
+          "-o", str(staged)])
     os.replace(staged, LIBRARY)
     return LIBRARY
 

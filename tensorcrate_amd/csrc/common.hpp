@@ -11,6 +11,18 @@
 #include <vector>
 
 #include "../../include/tchip.h"
+#include "scalar_ops.h"
+
+// The codes scalar_ops.h (which the runtime compiler also reads) uses are
+// the C ABI's.
+static_assert(tc_ops::ADD == TC_ADD && tc_ops::SUB == TC_SUB && tc_ops::MUL == TC_MUL && tc_ops::DIV == TC_DIV &&
+                  tc_ops::REM == TC_REM,
+              "BinaryOp codes");
+static_assert(tc_ops::MIN == TC_MIN && tc_ops::MAX == TC_MAX && tc_ops::MAX_SHARE == TC_MAX_SHARE &&
+                  tc_ops::LESS == TC_LESS && tc_ops::LESS_EQUAL == TC_LESS_EQUAL && tc_ops::GREATER == TC_GREATER &&
+                  tc_ops::GREATER_EQUAL == TC_GREATER_EQUAL,
+              "Compare codes");
+static_assert(tc_ops::F32 == TC_F32 && tc_ops::F16 == TC_F16 && tc_ops::BF16 == TC_BF16, "DType codes");
 
 namespace tc {
 
@@ -37,22 +49,8 @@ std::string shape_text(const uint64_t* values, uint32_t rank);
 
 // ---- element types ----------------------------------------------------------
 
-// bf16 is the top half of an f32, so widening is a shift.
-__host__ __device__ inline float bf16_bits_to_f32(uint16_t bits) {
-    return __uint_as_float(static_cast<uint32_t>(bits) << 16);
-}
-
-// Round to nearest, ties to even, with NaNs quieted: the rule of
-// `half::bf16::from_f32` that the reference narrows with.  Adding 0x7fff plus
-// the kept bit's lowest bit carries into the kept half exactly when the
-// dropped half is above one half, or exactly one half with an odd kept half.
-__host__ __device__ inline uint16_t f32_to_bf16_bits(float value) {
-    uint32_t x = __float_as_uint(value);
-    if ((x & 0x7fffffffu) > 0x7f800000u) {
-        return static_cast<uint16_t>((x >> 16) | 0x0040u);
-    }
-    return static_cast<uint16_t>((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
-}
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t bits) { return tc_bf16_to_f32(bits); }
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float value) { return tc_f32_to_bf16(value); }
 
 struct bf16_t {
     uint16_t bits;
@@ -119,32 +117,8 @@ inline const char* dtype_name(uint32_t dtype) {
 
 // ---- the scalar operations every kernel shares -----------------------------
 
-// `BinaryOp` in f32 (kernels.rs:431-437); the caller rounds to the element
-// type once.  `Rem` is Rust's `%`, the truncated remainder `fmod`, which is
-// exact.
-__device__ inline float binary_value(uint32_t op, float a, float b) {
-    switch (op) {
-        case TC_ADD: return a + b;
-        case TC_SUB: return a - b;
-        case TC_MUL: return a * b;
-        case TC_DIV: return a / b;
-        default: return fmodf(a, b);
-    }
-}
-
-// `Compare::value` (kernels.rs:138-153): minNum/maxNum, the ½-at-ties share,
-// and predicates that are false on NaN.
-__device__ inline float compare_value(uint32_t op, float a, float b) {
-    switch (op) {
-        case TC_MIN: return fminf(a, b);
-        case TC_MAX: return fmaxf(a, b);
-        case TC_MAX_SHARE: return a > b ? 1.0f : (a < b ? 0.0f : 0.5f);
-        case TC_LESS: return a < b ? 1.0f : 0.0f;
-        case TC_LESS_EQUAL: return a <= b ? 1.0f : 0.0f;
-        case TC_GREATER: return a > b ? 1.0f : 0.0f;
-        default: return a >= b ? 1.0f : 0.0f;
-    }
-}
+__device__ inline float binary_value(uint32_t op, float a, float b) { return tc_binary(op, a, b); }
+__device__ inline float compare_value(uint32_t op, float a, float b) { return tc_compare(op, a, b); }
 
 // `Pairwise::value` (kernels.rs:431-441); a power is f32 `powf`
 // (numbers/primitive.rs:131-156).

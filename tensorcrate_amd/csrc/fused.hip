@@ -3,11 +3,14 @@
 //
 // A program is a short register program over a rows x cols space, encoded
 // twelve bytes an instruction (fused/mod.rs:1387-1410), and each element runs
-// it in order.  The program and its load places are copied into LDS once per
-// block; every wave then walks them in lockstep, so each instruction's
-// operands are wave-uniform, and the register file is a small array indexed
-// by those uniform numbers.  Each thread runs four elements 64 apart, so
-// every load and store instruction of a wave touches one contiguous run.
+// it in order.  Every wave walks the program in lockstep, fetching each
+// instruction and load place with scalar loads (from the kernel's argument
+// segment for programs of up to 48 instructions, such as Adam's, from a
+// device block otherwise), so the opcode and register numbers are SGPRs,
+// each instruction is dispatched once per wave, and the register file — one
+// 16-wide vector per element — is indexed with indexed VGPR moves, never
+// scratch memory.  Each thread runs four elements 64 apart, so every load
+// and store instruction of a wave touches one contiguous run.
 //
 // A program computes in its own type T (f32, f16 or bf16): loads convert
 // their storage type to T, every operation rounds to T, and stores convert T
@@ -16,8 +19,13 @@
 // f32 and rounded once is T's own correctly rounded result.  No
 // multiply-add is ever contracted.
 
+#include <hip/hiprtc.h>
 #include <math.h>
 #include <string.h>
+
+#include <mutex>
+#include <sstream>
+#include <unordered_map>
 
 #include "common.hpp"
 
@@ -35,12 +43,9 @@ struct DevicePlace {
     uint64_t steps[TC_FUSED_LEAD];
 };
 
-// Round an f32 value to the program's type T and back.
 template <int T>
 __device__ __forceinline__ float round_to(float v) {
-    if (T == TC_F16) return static_cast<float>(static_cast<_Float16>(v));
-    if (T == TC_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
-    return v;
+    return tc_round<T>(v);
 }
 
 __device__ __forceinline__ float load_as(const void* base, uint32_t dtype, uint64_t index) {
@@ -59,27 +64,7 @@ __device__ __forceinline__ void store_as(void* base, uint32_t dtype, uint64_t in
     }
 }
 
-// `Analytic::value` (kernels.rs:334-354), in f32; the program rounds the
-// result to T.
-__device__ __forceinline__ float analytic_value(uint32_t op, float x) {
-    switch (op) {
-        case 0: return sinf(x);
-        case 1: return cosf(x);
-        case 2: return tanf(x);
-        case 3: return 1.0f / cosf(x);
-        case 4: return 1.0f / sinf(x);
-        case 5: return asinf(x);
-        case 6: return acosf(x);
-        case 7: return atanf(x);
-        case 8: return expf(x);
-        case 9: return logf(x);
-        case 10: return sinhf(x);
-        case 11: return coshf(x);
-        case 12: return tanhf(x);
-        case 13: return sqrtf(x);
-        default: return NAN;
-    }
-}
+__device__ __forceinline__ float analytic_value(uint32_t op, float x) { return tc_analytic(op, x); }
 
 // The storage element element (row, col) reads through `place`
 // (fused/mod.rs:3254-3268).
@@ -101,17 +86,110 @@ struct Buffers {
     void* outputs[TC_FUSED_MAX_OUTPUTS];
 };
 
+// A program small enough to travel in the kernel's argument segment, where
+// the scalar unit reads it directly; larger ones are read from a device
+// block.  Either way every instruction and place is fetched by scalar loads
+// at a wave-uniform index, so the opcode, the register numbers and the
+// place are SGPR values and every lane runs the same instruction.
+constexpr int kInlineCode = 48;
+constexpr int kInlinePlaces = 8;
+
+struct Inline {
+    tc_encoded code[kInlineCode];
+    DevicePlace places[kInlinePlaces];
+};
+
+// The interpreter's register file: one 16-wide vector register per element
+// a thread runs, indexed only by uniform register numbers, so each stays in
+// VGPRs (indexed moves) rather than going to scratch memory.
+typedef float Regs16 __attribute__((ext_vector_type(TC_FUSED_REGISTERS)));
+
+struct Registers {
+    Regs16 r[kLanesPerThread];
+    template <int V>
+    __device__ __forceinline__ float get(uint32_t i) const {
+        return r[V][i];
+    }
+    template <int V>
+    __device__ __forceinline__ void set(uint32_t i, float v) {
+        r[V][i] = v;
+    }
+};
+
+// The rare analytic functions, kept out of line so the interpreter's hot
+// path stays small; `Sqrt`, the one Adam runs, is inline.
+__device__ __noinline__ float analytic_slow(uint32_t op, float x) { return analytic_value(op, x); }
+
+// Every element of one instruction, dispatched once on the (uniform) kind and
+// operation, then applied to each of a thread's elements.
+#define TC_EACH(body)                        \
+    {                                        \
+        constexpr int V = 0;                 \
+        body;                                \
+    }                                        \
+    {                                        \
+        constexpr int V = 1;                 \
+        body;                                \
+    }                                        \
+    {                                        \
+        constexpr int V = 2;                 \
+        body;                                \
+    }                                        \
+    {                                        \
+        constexpr int V = 3;                 \
+        body;                                \
+    }
+
 template <int T>
-__global__ void __launch_bounds__(256) fused_kernel(const tc_encoded* __restrict__ code, uint32_t count,
-                                                    const DevicePlace* __restrict__ places, uint32_t place_count,
+__device__ __forceinline__ void run(Registers& regs, const tc_encoded& in, const DevicePlace* place,
+                                    const Buffers& buffers, const bool (&live)[kLanesPerThread],
+                                    const uint64_t (&row)[kLanesPerThread], const uint64_t (&col)[kLanesPerThread],
+                                    const uint64_t (&element)[kLanesPerThread]) {
+    static_assert(kLanesPerThread == 4, "TC_EACH covers four elements");
+    switch (in.kind) {
+        case 0: {  // load
+            const void* src = buffers.inputs[in.a];
+            TC_EACH(regs.set<V>(in.dst, live[V] ? round_to<T>(load_as(src, in.b, place_at(*place, row[V], col[V])))
+                                                : 0.0f));
+            break;
+        }
+        case 1:  // const: a T value, which f32 holds exactly
+            TC_EACH(regs.set<V>(in.dst, in.value));
+            break;
+        case 2:
+            switch (in.op) {
+                case TC_ADD: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) + regs.get<V>(in.b)))); break;
+                case TC_SUB: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) - regs.get<V>(in.b)))); break;
+                case TC_MUL: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) * regs.get<V>(in.b)))); break;
+                case TC_DIV: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) / regs.get<V>(in.b)))); break;
+                default: TC_EACH(regs.set<V>(in.dst, round_to<T>(fmodf(regs.get<V>(in.a), regs.get<V>(in.b))))); break;
+            }
+            break;
+        case 3:
+            if (in.op == 13) {
+                TC_EACH(regs.set<V>(in.dst, round_to<T>(sqrtf(regs.get<V>(in.a)))));
+            } else {
+                TC_EACH(regs.set<V>(in.dst, round_to<T>(analytic_slow(in.op, regs.get<V>(in.a)))));
+            }
+            break;
+        case 4:
+            TC_EACH(regs.set<V>(in.dst, round_to<T>(compare_value(in.op, regs.get<V>(in.a), regs.get<V>(in.b)))));
+            break;
+        default: {  // store
+            void* dst = buffers.outputs[in.aux];
+            TC_EACH(if (live[V]) store_as(dst, in.b, element[V], regs.get<V>(in.a)));
+            break;
+        }
+    }
+}
+
+#undef TC_EACH
+
+template <int T, bool INLINE>
+__global__ void __launch_bounds__(256) fused_kernel(Inline small_program, const tc_encoded* __restrict__ code,
+                                                    const DevicePlace* __restrict__ places, uint32_t count,
                                                     Buffers buffers, uint64_t rows, uint64_t cols, DivMod cols_div,
                                                     bool small) {
-    __shared__ tc_encoded lds_code[TC_FUSED_MAX_INSTRUCTIONS];
-    __shared__ DevicePlace lds_places[TC_FUSED_MAX_LOADS];
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) lds_code[i] = code[i];
-    for (uint32_t i = threadIdx.x; i < place_count; i += blockDim.x) lds_places[i] = places[i];
-    __syncthreads();
-
     const uint64_t total = rows * cols;
     const uint64_t per_block = static_cast<uint64_t>(blockDim.x) * kLanesPerThread;
     const int lane = threadIdx.x % 64;
@@ -135,50 +213,313 @@ __global__ void __launch_bounds__(256) fused_kernel(const tc_encoded* __restrict
                 col[v] = element[v] - row[v] * cols;
             }
         }
-        float r0[TC_FUSED_REGISTERS], r1[TC_FUSED_REGISTERS], r2[TC_FUSED_REGISTERS], r3[TC_FUSED_REGISTERS];
-        float* regs[kLanesPerThread] = {r0, r1, r2, r3};
+        Registers regs;
         for (uint32_t pc = 0; pc < count; pc++) {
-            const tc_encoded in = lds_code[pc];
-            switch (in.kind) {
-                case 0: {  // load
-                    const DevicePlace& p = lds_places[in.op];
-                    const void* src = buffers.inputs[in.a];
+            const tc_encoded in = INLINE ? small_program.code[pc] : code[pc];
+            const DevicePlace* place = nullptr;
+            if (in.kind == 0) place = INLINE ? &small_program.places[in.op] : &places[in.op];
+            run<T>(regs, in, place, buffers, live, row, col, element);
+        }
+    }
+}
+
+// ---- the dense path ------------------------------------------------------
+//
+// A program whose every load reads its tensor in element order and whose
+// loads all come before its stores — a whole-tensor update such as Adam —
+// runs four consecutive elements per thread: all of a chunk's loads are
+// issued first, as one 16-byte (f32) or 8-byte (16-bit) vector load each, so
+// every thread has its whole working set in flight at once, and each store
+// writes its four elements with one vector store.  Load instruction j of the
+// program reads staging slot j.
+
+constexpr int kDenseLoads = 8;
+typedef float Stage __attribute__((ext_vector_type(4 * kDenseLoads)));
+
+struct DenseLoads {
+    const void* base[kDenseLoads];  // the input with the place's offset applied
+    uint32_t dtype[kDenseLoads];
+};
+
+__device__ __forceinline__ void load4(const void* base, uint32_t dtype, uint64_t first, float (&out)[4]) {
+    if (dtype == TC_F32) {
+        const float4 v = reinterpret_cast<const float4*>(base)[first / 4];
+        out[0] = v.x, out[1] = v.y, out[2] = v.z, out[3] = v.w;
+    } else {
+        const uint2 v = reinterpret_cast<const uint2*>(base)[first / 4];
+        const uint16_t h[4] = {static_cast<uint16_t>(v.x), static_cast<uint16_t>(v.x >> 16),
+                               static_cast<uint16_t>(v.y), static_cast<uint16_t>(v.y >> 16)};
 #pragma unroll
-                    for (int v = 0; v < kLanesPerThread; v++) {
-                        regs[v][in.dst] = live[v] ? round_to<T>(load_as(src, in.b, place_at(p, row[v], col[v]))) : 0.0f;
-                    }
-                    break;
-                }
-                case 1:  // const: a T value, which f32 holds exactly
+        for (int e = 0; e < 4; e++) {
+            out[e] = dtype == TC_F16 ? static_cast<float>(__builtin_bit_cast(_Float16, h[e])) : bf16_bits_to_f32(h[e]);
+        }
+    }
+}
+
+__device__ __forceinline__ void store4(void* base, uint32_t dtype, uint64_t first, const float (&v)[4]) {
+    if (dtype == TC_F32) {
+        reinterpret_cast<float4*>(base)[first / 4] = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+        uint16_t h[4];
 #pragma unroll
-                    for (int v = 0; v < kLanesPerThread; v++) regs[v][in.dst] = in.value;
-                    break;
-                case 2:
+        for (int e = 0; e < 4; e++) {
+            h[e] = dtype == TC_F16 ? __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[e])) : f32_to_bf16_bits(v[e]);
+        }
+        reinterpret_cast<uint2*>(base)[first / 4] =
+            make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+    }
+}
+
+template <int T>
+__global__ void __launch_bounds__(256) fused_dense_kernel(Inline program, uint32_t count, DenseLoads loads,
+                                                          uint32_t load_count, Buffers buffers, uint64_t chunks) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t chunk = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; chunk < chunks;
+         chunk += stride) {
+        const uint64_t first = chunk * 4;
+        Stage stage;
+        for (uint32_t j = 0; j < load_count; j++) {
+            float v[4];
+            load4(loads.base[j], loads.dtype[j], first, v);
 #pragma unroll
-                    for (int v = 0; v < kLanesPerThread; v++)
-                        regs[v][in.dst] = round_to<T>(binary_value(in.op, regs[v][in.a], regs[v][in.b]));
-                    break;
-                case 3:
-#pragma unroll
-                    for (int v = 0; v < kLanesPerThread; v++)
-                        regs[v][in.dst] = round_to<T>(analytic_value(in.op, regs[v][in.a]));
-                    break;
-                case 4:
-#pragma unroll
-                    for (int v = 0; v < kLanesPerThread; v++)
-                        regs[v][in.dst] = round_to<T>(compare_value(in.op, regs[v][in.a], regs[v][in.b]));
-                    break;
-                default: {  // store
-                    void* dst = buffers.outputs[in.aux];
-#pragma unroll
-                    for (int v = 0; v < kLanesPerThread; v++) {
-                        if (live[v]) store_as(dst, in.b, element[v], regs[v][in.a]);
-                    }
-                    break;
-                }
+            for (int e = 0; e < 4; e++) stage[4 * j + e] = v[e];
+        }
+        Registers regs;
+        uint32_t next_load = 0;
+        for (uint32_t pc = 0; pc < count; pc++) {
+            const tc_encoded in = program.code[pc];
+            if (in.kind == 0) {
+                const uint32_t j = next_load++;
+                regs.set<0>(in.dst, round_to<T>(stage[4 * j + 0]));
+                regs.set<1>(in.dst, round_to<T>(stage[4 * j + 1]));
+                regs.set<2>(in.dst, round_to<T>(stage[4 * j + 2]));
+                regs.set<3>(in.dst, round_to<T>(stage[4 * j + 3]));
+            } else if (in.kind == 5) {
+                const float v[4] = {regs.get<0>(in.a), regs.get<1>(in.a), regs.get<2>(in.a), regs.get<3>(in.a)};
+                store4(buffers.outputs[in.aux], in.b, first, v);
+            } else {
+                const bool live[4] = {true, true, true, true};
+                const uint64_t none[4] = {0, 0, 0, 0};
+                run<T>(regs, in, nullptr, buffers, live, none, none, none);
             }
         }
     }
+}
+
+// Whether `code` runs on the dense path over a rows x cols space, and if so
+// the staging it reads.
+bool dense_plan(const tc_encoded* code, uint32_t count, const tc_place* places, const void* const* inputs,
+                void* const* outputs, uint64_t rows, uint64_t cols, DenseLoads* plan, uint32_t* load_count) {
+    if (count > static_cast<uint32_t>(kInlineCode) || (rows * cols) % 4 != 0) return false;
+    uint32_t loads = 0;
+    bool stored = false;
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        const size_t size = in.b == TC_F32 ? 4 : 2;
+        if (in.kind == 0) {
+            if (stored || loads == static_cast<uint32_t>(kDenseLoads)) return false;
+            const tc_place& p = places[in.op];
+            // Element order: (row, col) reads offset + row * cols + col.
+            const bool in_order = p.col_step == 1 && (rows == 1 || (p.lead == 1 && p.steps[0] == cols));
+            const uint8_t* base = static_cast<const uint8_t*>(inputs[in.a]) + p.offset * size;
+            if (!in_order || reinterpret_cast<uintptr_t>(base) % (4 * size) != 0) return false;
+            plan->base[loads] = base;
+            plan->dtype[loads] = in.b;
+            loads++;
+        } else if (in.kind == 5) {
+            stored = true;
+            if (reinterpret_cast<uintptr_t>(outputs[in.aux]) % (4 * size) != 0) return false;
+        }
+    }
+    *load_count = loads;
+    return true;
+}
+
+// ---- compiled programs -----------------------------------------------------
+//
+// A dense program that runs more than once is compiled into a kernel of its
+// own, as the reference's Metal backend compiles its fused programs
+// (metal/codegen.rs:1-40): straight-line code, one local per value, every
+// opcode and storage type a constant the compiler folds away, calling the
+// same scalar functions the interpreter does (scalar_ops.h, embedded in the
+// generated source).  Constants travel in the kernel's arguments, so
+// programs that differ only in their constants — an optimizer's, rebuilt
+// every step — share one compiled kernel.  A program is compiled on its
+// second appearance, so one run once never waits for the compiler, and
+// kernels are cached by their source for the life of the process.  The
+// runtime compiler is hiprtc, with this library's own code-generation flags.
+
+extern "C" const char tc_scalar_ops_source[];  // scalar_ops.h, embedded by the build
+
+constexpr int kCompiledConstants = kInlineCode;
+
+struct CompiledArgs {
+    const void* in[kDenseLoads];
+    void* out[TC_FUSED_MAX_OUTPUTS];
+    float constants[kCompiledConstants];
+    uint64_t chunks;
+};
+
+// The generated source of a dense program, and the order its constants
+// take in `CompiledArgs::constants`.
+std::string dense_source(const tc_encoded* code, uint32_t count, uint32_t dtype, std::vector<float>* constants) {
+    static const char* const kRound[] = {"tc_round<0>", "tc_round<1>", "tc_round<2>"};
+    static const char* const kBinary[] = {"+", "-", "*", "/"};
+    const char* round = kRound[dtype];
+    std::ostringstream src;
+    src << "#include \"scalar_ops.h\"\n"
+        << "struct Args { const void* in[" << kDenseLoads << "]; void* out[" << TC_FUSED_MAX_OUTPUTS
+        << "]; float constants[" << kCompiledConstants << "]; unsigned long long chunks; };\n"
+        << "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_program(Args a) {\n"
+        << "  const unsigned long long stride = (unsigned long long)gridDim.x * blockDim.x;\n"
+        << "  for (unsigned long long chunk = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;"
+        << " chunk < a.chunks; chunk += stride) {\n";
+    std::string reg[TC_FUSED_REGISTERS];
+    uint32_t loads = 0;
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        const std::string v = "v" + std::to_string(pc);
+        auto at = [&](uint8_t r) { return reg[r].empty() ? std::string("0.0f") : reg[r] + "[e]"; };
+        if (in.kind == 5) {
+            const std::string value = reg[in.a].empty() ? "zero" : reg[in.a];
+            if (reg[in.a].empty()) src << "    const float zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};\n";
+            if (in.b == TC_F32) {
+                src << "    ((float4*)a.out[" << int(in.aux) << "])[chunk] = make_float4(" << value << "[0], " << value
+                    << "[1], " << value << "[2], " << value << "[3]);\n";
+            } else {
+                const std::string narrow = in.b == TC_F16 ? "__builtin_bit_cast(unsigned short, (_Float16)(" : "tc_f32_to_bf16((";
+                src << "    { unsigned short h[4]; for (int e = 0; e < 4; e++) h[e] = " << narrow << value << "[e]));\n"
+                    << "      ((uint2*)a.out[" << int(in.aux) << "])[chunk] = make_uint2(h[0] | ((unsigned)h[1] << 16),"
+                    << " h[2] | ((unsigned)h[3] << 16)); }\n";
+            }
+            continue;
+        }
+        src << "    float " << v << "[4];\n";
+        switch (in.kind) {
+            case 0: {
+                const uint32_t j = loads++;
+                if (in.b == TC_F32) {
+                    src << "    { const float4 w = ((const float4*)a.in[" << j << "])[chunk]; " << v << "[0] = " << round
+                        << "(w.x); " << v << "[1] = " << round << "(w.y); " << v << "[2] = " << round << "(w.z); " << v
+                        << "[3] = " << round << "(w.w); }\n";
+                } else {
+                    const std::string widen = in.b == TC_F16 ? "(float)__builtin_bit_cast(_Float16, (unsigned short)(" : "tc_bf16_to_f32((unsigned short)(";
+                    src << "    { const uint2 w = ((const uint2*)a.in[" << j << "])[chunk];\n"
+                        << "      const unsigned hw[4] = {w.x & 0xffffu, w.x >> 16, w.y & 0xffffu, w.y >> 16};\n"
+                        << "      for (int e = 0; e < 4; e++) " << v << "[e] = " << round << "(" << widen << "hw[e]))); }\n";
+                }
+                break;
+            }
+            case 1: {
+                src << "    for (int e = 0; e < 4; e++) " << v << "[e] = a.constants[" << constants->size() << "];\n";
+                constants->push_back(in.value);
+                break;
+            }
+            case 2:
+                if (in.op == TC_REM) {
+                    src << "    for (int e = 0; e < 4; e++) " << v << "[e] = " << round << "(fmodf(" << at(in.a) << ", "
+                        << at(in.b) << "));\n";
+                } else {
+                    src << "    for (int e = 0; e < 4; e++) " << v << "[e] = " << round << "(" << at(in.a) << " "
+                        << kBinary[in.op] << " " << at(in.b) << ");\n";
+                }
+                break;
+            case 3:
+                src << "    for (int e = 0; e < 4; e++) " << v << "[e] = " << round << "(tc_analytic(" << in.op << "u, "
+                    << at(in.a) << "));\n";
+                break;
+            default:  // compare
+                src << "    for (int e = 0; e < 4; e++) " << v << "[e] = " << round << "(tc_compare(" << in.op << "u, "
+                    << at(in.a) << ", " << at(in.b) << "));\n";
+                break;
+        }
+        reg[in.dst] = v;
+    }
+    src << "  }\n}\n";
+    return src.str();
+}
+
+struct Compiled {
+    uint32_t seen = 0;
+    bool failed = false;
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;
+};
+
+std::mutex compiled_mutex;
+std::unordered_map<std::string, Compiled> compiled_programs;
+uint64_t compiled_count = 0;
+
+// hiprtc's flags: the library's own (see _build.py).
+const char* const kCompileFlags[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                                     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+
+bool compile_program(const std::string& source, Compiled* out) {
+    hiprtcProgram program;
+    const char* headers[] = {tc_scalar_ops_source};
+    const char* names[] = {"scalar_ops.h"};
+    if (hiprtcCreateProgram(&program, source.c_str(), "tc_fused_program.hip", 1, headers, names) != HIPRTC_SUCCESS) {
+        return false;
+    }
+    bool ok = hiprtcCompileProgram(program, sizeof(kCompileFlags) / sizeof(kCompileFlags[0]), kCompileFlags) ==
+              HIPRTC_SUCCESS;
+    std::vector<char> binary;
+    if (ok) {
+        size_t size = 0;
+        ok = hiprtcGetCodeSize(program, &size) == HIPRTC_SUCCESS && size > 0;
+        if (ok) {
+            binary.resize(size);
+            ok = hiprtcGetCode(program, binary.data()) == HIPRTC_SUCCESS;
+        }
+    }
+    hiprtcDestroyProgram(&program);
+    if (!ok) return false;
+    if (hipModuleLoadData(&out->module, binary.data()) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (hipModuleGetFunction(&out->function, out->module, "tc_fused_program") != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return true;
+}
+
+// Run `code` compiled when it has been seen before and compiles; false when
+// the interpreter should run it instead.
+bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const DenseLoads& loads,
+                  uint32_t load_count, const Buffers& buffers, uint64_t chunks, hipStream_t s, int* status) {
+    std::vector<float> constants;
+    int device = 0;
+    (void)hipGetDevice(&device);
+    const std::string source = dense_source(code, count, dtype, &constants);
+    if (constants.size() > static_cast<size_t>(kCompiledConstants)) return false;
+    hipFunction_t function = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(compiled_mutex);
+        Compiled& entry = compiled_programs["device " + std::to_string(device) + "\n" + source];
+        if (entry.failed) return false;
+        if (entry.function == nullptr) {
+            if (++entry.seen < 2) return false;
+            if (!compile_program(source, &entry)) {
+                entry.failed = true;
+                return false;
+            }
+            compiled_count++;
+        }
+        function = entry.function;
+    }
+    CompiledArgs args{};
+    for (uint32_t j = 0; j < load_count; j++) args.in[j] = loads.base[j];
+    for (int k = 0; k < TC_FUSED_MAX_OUTPUTS; k++) args.out[k] = buffers.outputs[k];
+    for (size_t k = 0; k < constants.size(); k++) args.constants[k] = constants[k];
+    args.chunks = chunks;
+    size_t size = sizeof(args);
+    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+    const uint32_t blocks = grid_for(chunks, 256, 8);
+    hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, nullptr, config);
+    *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused program: ") + hipGetErrorString(error));
+    return true;
 }
 
 // Host-side validation of what the kernel would otherwise trust.
@@ -263,14 +604,28 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
                                         std::to_string(rows * cols));
         }
     }
-    // The program and its places travel in one block of device memory,
-    // freed once the kernel has been queued (stream order keeps it alive).
-    const size_t code_bytes = (count * sizeof(tc_encoded) + 15) / 16 * 16;
-    const size_t place_bytes = place_count * sizeof(DevicePlace);
-    std::vector<uint8_t> host(code_bytes + place_bytes);
-    memcpy(host.data(), code, count * sizeof(tc_encoded));
+    Buffers buffers{};
+    for (uint32_t k = 0; k < input_count; k++) buffers.inputs[k] = inputs[k];
+    for (uint32_t k = 0; k < output_count; k++) buffers.outputs[k] = outputs[k];
+    DenseLoads dense{};
+    uint32_t dense_loads = 0;
+    if (dense_plan(code, count, places, inputs, outputs, rows, cols, &dense, &dense_loads)) {
+        const uint64_t chunks = rows * cols / 4;
+        if (run_compiled(code, count, dtype, dense, dense_loads, buffers, chunks, s, &status)) return status;
+        Inline program{};
+        memcpy(program.code, code, count * sizeof(tc_encoded));
+        const uint32_t blocks = grid_for(chunks, 256, 8);
+        switch (dtype) {
+            case TC_F32: fused_dense_kernel<TC_F32><<<blocks, 256, 0, s>>>(program, count, dense, dense_loads, buffers, chunks); break;
+            case TC_F16: fused_dense_kernel<TC_F16><<<blocks, 256, 0, s>>>(program, count, dense, dense_loads, buffers, chunks); break;
+            default: fused_dense_kernel<TC_BF16><<<blocks, 256, 0, s>>>(program, count, dense, dense_loads, buffers, chunks); break;
+        }
+        return check_launch("fused program");
+    }
+    std::vector<DevicePlace> device_places(place_count);
     for (uint32_t k = 0; k < place_count; k++) {
-        DevicePlace p{};
+        DevicePlace& p = device_places[k];
+        p = DevicePlace{};
         p.offset = places[k].offset;
         p.col_step = places[k].col_step;
         p.lead = places[k].lead;
@@ -282,31 +637,62 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
                 return fail(TC_INVALID, "fused program: a place has an empty axis");
             }
         }
-        memcpy(host.data() + code_bytes + k * sizeof(DevicePlace), &p, sizeof(DevicePlace));
     }
-    void* device = nullptr;
-    status = tc_alloc(host.size(), &device);
-    if (status != TC_OK) return status;
-    hipError_t error = hipMemcpyAsync(device, host.data(), host.size(), hipMemcpyHostToDevice, s);
-    if (error != hipSuccess) {
-        tc_free(device);
-        return fail(TC_DEVICE, std::string("fused program upload: ") + hipGetErrorString(error));
-    }
-    Buffers buffers{};
-    for (uint32_t k = 0; k < input_count; k++) buffers.inputs[k] = inputs[k];
-    for (uint32_t k = 0; k < output_count; k++) buffers.outputs[k] = outputs[k];
     const uint64_t total = rows * cols;
     const bool small = total <= UINT32_MAX && cols <= UINT32_MAX;
     DivMod cols_div(small ? static_cast<uint32_t>(cols) : 1u);
     const uint32_t blocks = grid_for(total, 256 * kLanesPerThread, 8);
-    const tc_encoded* dcode = static_cast<const tc_encoded*>(device);
-    const DevicePlace* dplaces = reinterpret_cast<const DevicePlace*>(static_cast<uint8_t*>(device) + code_bytes);
-    switch (dtype) {
-        case TC_F32: fused_kernel<TC_F32><<<blocks, 256, 0, s>>>(dcode, count, dplaces, place_count, buffers, rows, cols, cols_div, small); break;
-        case TC_F16: fused_kernel<TC_F16><<<blocks, 256, 0, s>>>(dcode, count, dplaces, place_count, buffers, rows, cols, cols_div, small); break;
-        default: fused_kernel<TC_BF16><<<blocks, 256, 0, s>>>(dcode, count, dplaces, place_count, buffers, rows, cols, cols_div, small); break;
+    Inline program{};
+    const bool inline_program = count <= static_cast<uint32_t>(kInlineCode) &&
+                                place_count <= static_cast<uint32_t>(kInlinePlaces);
+    void* device = nullptr;
+    const tc_encoded* dcode = nullptr;
+    const DevicePlace* dplaces = nullptr;
+    if (inline_program) {
+        memcpy(program.code, code, count * sizeof(tc_encoded));
+        if (place_count) memcpy(program.places, device_places.data(), place_count * sizeof(DevicePlace));
+    } else {
+        // A larger program and its places travel in one block of device
+        // memory, freed once the kernel has been queued (stream order keeps
+        // it alive until the kernel has run).
+        const size_t code_bytes = (count * sizeof(tc_encoded) + 15) / 16 * 16;
+        std::vector<uint8_t> host(code_bytes + place_count * sizeof(DevicePlace));
+        memcpy(host.data(), code, count * sizeof(tc_encoded));
+        if (place_count) memcpy(host.data() + code_bytes, device_places.data(), place_count * sizeof(DevicePlace));
+        status = tc_alloc(host.size(), &device);
+        if (status != TC_OK) return status;
+        hipError_t error = hipMemcpyAsync(device, host.data(), host.size(), hipMemcpyHostToDevice, s);
+        if (error != hipSuccess) {
+            tc_free(device);
+            return fail(TC_DEVICE, std::string("fused program upload: ") + hipGetErrorString(error));
+        }
+        dcode = static_cast<const tc_encoded*>(device);
+        dplaces = reinterpret_cast<const DevicePlace*>(static_cast<uint8_t*>(device) + code_bytes);
     }
+#define TC_FUSED_LAUNCH(T, INLINE)                                                                  \
+    fused_kernel<T, INLINE><<<blocks, 256, 0, s>>>(program, dcode, dplaces, count, buffers, rows, cols, \
+                                                   cols_div, small)
+    if (inline_program) {
+        switch (dtype) {
+            case TC_F32: TC_FUSED_LAUNCH(TC_F32, true); break;
+            case TC_F16: TC_FUSED_LAUNCH(TC_F16, true); break;
+            default: TC_FUSED_LAUNCH(TC_BF16, true); break;
+        }
+    } else {
+        switch (dtype) {
+            case TC_F32: TC_FUSED_LAUNCH(TC_F32, false); break;
+            case TC_F16: TC_FUSED_LAUNCH(TC_F16, false); break;
+            default: TC_FUSED_LAUNCH(TC_BF16, false); break;
+        }
+    }
+#undef TC_FUSED_LAUNCH
     status = check_launch("fused program");
-    tc_free(device);
+    if (device != nullptr) tc_free(device);
     return status;
+}
+
+extern "C" int tc_fused_compiled(uint64_t* count) {
+    std::lock_guard<std::mutex> lock(compiled_mutex);
+    *count = compiled_count;
+    return TC_OK;
 }

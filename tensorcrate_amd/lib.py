@@ -138,6 +138,7 @@ SIGNATURES = {
     "tc_transpose": [u32, u64, u64, vp, vp],
     "tc_fused": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, ctypes.POINTER(vp),
                  ctypes.POINTER(u64), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32, u64, u64],
+    "tc_fused_compiled": [ctypes.POINTER(u64)],
 }
 
 

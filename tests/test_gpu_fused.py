@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import binding as oracle
+from oracle import mlp
 from tensorcrate_amd import lib
 from tensorcrate_amd.optim import Adam, adam_program, identity_place
 from tests.common import KINDS, bits_equal, same_bits, to_kind, widen
@@ -115,3 +116,29 @@ def test_config5_adam_over_the_mlp_parameters():
         oracle.fused(lib.F32, code, [identity_place(64, cols)] * loads, ins, [host_p, nm, nv], 64, cols)
         m, v = nm, nv
     assert bits_equal(got[:64].reshape(-1), host_p)
+
+
+def test_a_repeated_program_runs_compiled_and_stays_exact():
+    # Dense programs compile on their second appearance (metal/codegen.rs:24);
+    # the compiled kernel must give the interpreter's (and the oracle's) bits.
+    import ctypes
+
+    def compiled():
+        count = ctypes.c_uint64()
+        lib.call("tc_fused_compiled", ctypes.byref(count))
+        return count.value
+
+    rng = np.random.default_rng(12)
+    n = 4096 * 3
+    p0 = rng.standard_normal(n).astype(np.float32)
+    grads = [rng.standard_normal(n).astype(np.float32) for _ in range(4)]
+    before = compiled()
+    params, moments = lib.Buffer.of(p0), None
+    rule = Adam(1e-2)
+    want = mlp.Adam(1e-2)
+    expected = p0.copy()
+    for g in grads:
+        rule.update(params, lib.Buffer.of(g), 1, n)
+        expected = want.update(expected, g)
+        assert np.array_equal(params.download(np.float32), expected)
+    assert compiled() > before
