@@ -10,9 +10,10 @@
 // (compact.rs:5-13).  The sources build with -ffp-contract=off, so no
 // multiply and add are ever fused across two operations.
 //
-// Each thread moves 16 bytes of every unit-stride operand per step (4 f32 or
-// 8 f16/bf16 elements) with vector loads and stores; grids stride over the
-// work and are capped at a few waves per CU.
+// Each thread moves 16 bytes of every unit-stride operand (4 f32 or 8
+// f16/bf16 elements) with vector loads and stores, in one pass over a grid
+// that covers the work; launches whose traffic exceeds the Infinity Cache
+// stream with nontemporal accesses.
 
 #include "common.hpp"
 
@@ -59,37 +60,55 @@ struct ClampTo {
 };
 
 // out[i] = f(a[i], b[i]) over n contiguous elements; `b` may be null when f
-// ignores it.  PACKED kernels move 16-byte packs (all pointers aligned) and
-// finish the last partial pack element by element.
-template <typename S, typename F, bool PACKED>
+// ignores it.  PACKED kernels move 16-byte packs (all pointers aligned), U
+// packs a thread in one pass with every load issued before any store, and
+// block 0 finishes the last partial pack element by element; NT marks a
+// streaming launch.
+template <typename S, typename F, bool PACKED, bool NT, int U>
 __global__ void __launch_bounds__(256) map_kernel(const S* __restrict__ a, const S* __restrict__ b,
                                                   S* __restrict__ out, uint64_t n, F f) {
     using E = Elem<S>;
     constexpr int N = Pack<S>::N;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    const uint64_t first = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    uint64_t done = 0;
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * 256 * U + threadIdx.x;
     if (PACKED) {
         const uint64_t packs = n / N;
-        const Pack<S>* pa = reinterpret_cast<const Pack<S>*>(a);
-        const Pack<S>* pb = reinterpret_cast<const Pack<S>*>(b);
-        Pack<S>* po = reinterpret_cast<Pack<S>*>(out);
-        for (uint64_t i = first; i < packs; i += stride) {
-            Pack<S> x = pa[i], z;
-            Pack<S> y;
-            if (b != nullptr) y = pb[i];
+        Pack<S> x[U], y[U];
 #pragma unroll
-            for (int k = 0; k < N; k++) {
-                float yv = b != nullptr ? E::widen(y.v[k]) : 0.0f;
-                z.v[k] = E::narrow(f(E::widen(x.v[k]), yv));
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + u * 256;
+            if (i < packs) {
+                x[u] = __builtin_bit_cast(Pack<S>, load_word<NT>(a + i * N));
+                if (b != nullptr) y[u] = __builtin_bit_cast(Pack<S>, load_word<NT>(b + i * N));
             }
-            po[i] = z;
         }
-        done = packs * N;
-    }
-    for (uint64_t i = done + first; i < n; i += stride) {
-        float yv = b != nullptr ? E::widen(b[i]) : 0.0f;
-        out[i] = E::narrow(f(E::widen(a[i]), yv));
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + u * 256;
+            if (i < packs) {
+                Pack<S> z;
+#pragma unroll
+                for (int k = 0; k < N; k++) {
+                    const float yv = b != nullptr ? E::widen(y[u].v[k]) : 0.0f;
+                    z.v[k] = E::narrow(f(E::widen(x[u].v[k]), yv));
+                }
+                store_word<NT>(out + i * N, __builtin_bit_cast(uint4, z));
+            }
+        }
+        const uint64_t tail = n - packs * N;
+        if (blockIdx.x == 0 && threadIdx.x < tail) {
+            const uint64_t i = packs * N + threadIdx.x;
+            const float yv = b != nullptr ? E::widen(b[i]) : 0.0f;
+            out[i] = E::narrow(f(E::widen(a[i]), yv));
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + u * 256;
+            if (i < n) {
+                const float yv = b != nullptr ? E::widen(b[i]) : 0.0f;
+                out[i] = E::narrow(f(E::widen(a[i]), yv));
+            }
+        }
     }
 }
 
@@ -99,10 +118,16 @@ int launch_map(const void* a, const void* b, void* out, uint64_t n, F f, hipStre
     const S* pa = static_cast<const S*>(a);
     const S* pb = static_cast<const S*>(b);
     S* po = static_cast<S*>(out);
+    const uint64_t bytes = n * sizeof(S) * (b == nullptr ? 2 : 3);
     if (aligned16(a) && (b == nullptr || aligned16(b)) && aligned16(out)) {
-        map_kernel<S, F, true><<<grid_for(n / Pack<S>::N + 1, 256 * 2), 256, 0, s>>>(pa, pb, po, n, f);
+        const uint64_t packs = n / Pack<S>::N;
+        if (bytes > kStreamBytes) {
+            map_kernel<S, F, true, true, 4><<<blocks_for(packs, 4), 256, 0, s>>>(pa, pb, po, n, f);
+        } else {
+            map_kernel<S, F, true, false, 1><<<blocks_for(packs, 1), 256, 0, s>>>(pa, pb, po, n, f);
+        }
     } else {
-        map_kernel<S, F, false><<<grid_for(n, 256 * 4), 256, 0, s>>>(pa, pb, po, n, f);
+        map_kernel<S, F, false, false, 4><<<blocks_for(n, 4), 256, 0, s>>>(pa, pb, po, n, f);
     }
     return check_launch(what);
 }
@@ -175,15 +200,15 @@ struct BinaryWalk {
 
 // Work items are groups of V consecutive elements of one run (V divides the
 // run).  The output is the row-major layout of the walk's shape.
-template <typename S, typename Op, int V, typename I>
+template <typename S, typename Op, int V, bool NT, typename I>
 __global__ void __launch_bounds__(256) strided_binary_kernel(const S* __restrict__ a,
                                                              const S* __restrict__ b,
                                                              S* __restrict__ out, BinaryWalk<I> w,
                                                              I groups, Div<I> per_run, I run_groups) {
     using E = Elem<S>;
     const int last = w.rank - 1;
-    const I stride = static_cast<I>(gridDim.x) * blockDim.x;
-    for (I g = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; g < groups; g += stride) {
+    const I g = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g < groups) {
         const I row = per_run.div(g);
         const I col = (g - row * run_groups) * V;
         // The run's start in each operand, from the row's coordinates.
@@ -202,7 +227,7 @@ __global__ void __launch_bounds__(256) strided_binary_kernel(const S* __restrict
         }
         float x[V], y[V];
         if (V > 1 && w.step_a == kUnit && w.vec_a) {
-            Pack<S> p = *reinterpret_cast<const Pack<S>*>(a + at_a + col);
+            Pack<S> p = __builtin_bit_cast(Pack<S>, load_word<NT>(a + at_a + col));
 #pragma unroll
             for (int k = 0; k < V; k++) x[k] = E::widen(p.v[k]);
         } else if (w.step_a == kRepeat) {
@@ -214,7 +239,7 @@ __global__ void __launch_bounds__(256) strided_binary_kernel(const S* __restrict
             for (int k = 0; k < V; k++) x[k] = E::widen(a[at_a + (col + k) * w.a[last]]);
         }
         if (V > 1 && w.step_b == kUnit && w.vec_b) {
-            Pack<S> p = *reinterpret_cast<const Pack<S>*>(b + at_b + col);
+            Pack<S> p = __builtin_bit_cast(Pack<S>, load_word<NT>(b + at_b + col));
 #pragma unroll
             for (int k = 0; k < V; k++) y[k] = E::widen(p.v[k]);
         } else if (w.step_b == kRepeat) {
@@ -230,7 +255,7 @@ __global__ void __launch_bounds__(256) strided_binary_kernel(const S* __restrict
             Pack<S> z;
 #pragma unroll
             for (int k = 0; k < V; k++) z.v[k] = E::narrow(Op::apply(x[k], y[k]));
-            *reinterpret_cast<Pack<S>*>(out + o) = z;
+            store_word<NT>(out + o, __builtin_bit_cast(uint4, z));
         } else {
             out[o] = E::narrow(Op::apply(x[0], y[0]));
         }
@@ -249,7 +274,7 @@ int launch_strided_binary(const S* a, const S* b, S* out, const Walk<3>& walk, u
         w.step_a = w.step_b = kRepeat;
         Div<I> one;
         one.set(1);
-        strided_binary_kernel<S, Op, 1, I><<<1, 64, 0, s>>>(a, b, out, w, I{1}, one, I{1});
+        strided_binary_kernel<S, Op, 1, false, I><<<1, 64, 0, s>>>(a, b, out, w, I{1}, one, I{1});
         return check_launch("strided binary");
     }
     BinaryWalk<I> w{};
@@ -280,12 +305,18 @@ int launch_strided_binary(const S* a, const S* b, S* out, const Walk<3>& walk, u
         const uint64_t groups = count / V;
         Div<I> per_run;
         per_run.set(run_groups);
-        strided_binary_kernel<S, Op, V, I><<<grid_for(groups, 256 * 2), 256, 0, s>>>(
-            a, b, out, w, static_cast<I>(groups), per_run, static_cast<I>(run_groups));
+        // Streaming when the output alone exceeds the Infinity Cache.
+        if (count * sizeof(S) > kStreamBytes) {
+            strided_binary_kernel<S, Op, V, true, I><<<blocks_for(groups, 1), 256, 0, s>>>(
+                a, b, out, w, static_cast<I>(groups), per_run, static_cast<I>(run_groups));
+        } else {
+            strided_binary_kernel<S, Op, V, false, I><<<blocks_for(groups, 1), 256, 0, s>>>(
+                a, b, out, w, static_cast<I>(groups), per_run, static_cast<I>(run_groups));
+        }
     } else {
         Div<I> per_run;
         per_run.set(run);
-        strided_binary_kernel<S, Op, 1, I><<<grid_for(count, 256 * 4), 256, 0, s>>>(
+        strided_binary_kernel<S, Op, 1, false, I><<<blocks_for(count, 1), 256, 0, s>>>(
             a, b, out, w, static_cast<I>(count), per_run, static_cast<I>(run));
     }
     return check_launch("strided binary");

@@ -89,17 +89,23 @@ __global__ void __launch_bounds__(256) gather_kernel(const T* __restrict__ src, 
 }
 
 // Rows of `run` words each, a word being one element or 16 bytes of them.
-// `rows_div` divides a flat (row, word) index by the words per row.
-template <typename T, typename I>
+// `rows_div` divides a flat (row, word) index by the words per row.  One
+// word a thread, over a grid that covers them; NT (16-byte words only) marks
+// a copy that streams past the Infinity Cache.
+template <typename T, bool NT, typename I>
 __global__ void __launch_bounds__(256) rows_kernel(const T* __restrict__ src, T* __restrict__ dst,
                                                    Layout2<I> layout, Div<I> run_div, I run, I total) {
-    I stride = static_cast<I>(gridDim.x) * blockDim.x;
-    for (I i = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const I i = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < total) {
         I row = run_div.div(i);
         I word = i - row * run;
         I from, to;
         locate(layout, layout.rank - 1, row, from, to);
-        dst[to + word] = src[from + word];
+        if constexpr (NT) {
+            store_word<true>(dst + to + word, load_word<true>(src + from + word));
+        } else {
+            dst[to + word] = src[from + word];
+        }
     }
 }
 
@@ -170,6 +176,59 @@ __global__ void __launch_bounds__(256) tile_kernel(const T* __restrict__ src, T*
     }
 }
 
+// The same transpose for 4-byte elements moving 16 bytes a lane on both
+// sides: a lane reads four elements along `a` and, after the LDS exchange,
+// writes four along `b`.  The 65-word row pitch keeps both the row writes and
+// the column reads of a wave on 64 distinct banks.  Needs every extent,
+// offset and stride that steps along a vector to be a multiple of 4, which
+// the host checks; NT marks a transpose that streams past the Infinity Cache.
+template <typename I, bool NT>
+__global__ void __launch_bounds__(256) tile4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                                    TileLayout<I> t) {
+    __shared__ uint32_t tile[kTile][kTile + 1];
+    const int quad = threadIdx.x % 16;  // which four elements of a 64-element row
+    const int row = threadIdx.x / 16;   // 16 rows a pass, four passes
+    I block = blockIdx.x;
+    I rest = t.tiles_a_div.div(block);
+    const I tile_a = block - rest * t.tiles_a;
+    I batch = t.tiles_b_div.div(rest);
+    const I tile_b = rest - batch * t.tiles_b;
+    I from = 0, to = 0;
+    for (int k = t.batch_rank - 1; k > 0; k--) {
+        I q = t.batch_div[k].div(batch);
+        I c = batch - q * t.batch_shape[k];
+        from += c * t.batch_src[k];
+        to += c * t.batch_dst[k];
+        batch = q;
+    }
+    if (t.batch_rank > 0) {
+        from += batch * t.batch_src[0];
+        to += batch * t.batch_dst[0];
+    }
+    const I a0 = tile_a * kTile, b0 = tile_b * kTile;
+    const I a = a0 + quad * 4;
+#pragma unroll
+    for (int pass = 0; pass < kTile / 16; pass++) {
+        const I b = b0 + row + pass * 16;
+        if (a < t.extent_a && b < t.extent_b) {
+            const uint4 v = load_word<NT>(src + from + a + b * t.src_b);
+            uint32_t* at = &tile[row + pass * 16][quad * 4];
+            at[0] = v.x, at[1] = v.y, at[2] = v.z, at[3] = v.w;
+        }
+    }
+    __syncthreads();
+    const I b = b0 + quad * 4;
+#pragma unroll
+    for (int pass = 0; pass < kTile / 16; pass++) {
+        const I aa = a0 + row + pass * 16;
+        if (aa < t.extent_a && b < t.extent_b) {
+            const int c = row + pass * 16;
+            const uint4 v{tile[quad * 4][c], tile[quad * 4 + 1][c], tile[quad * 4 + 2][c], tile[quad * 4 + 3][c]};
+            store_word<NT>(dst + to + b + aa * t.dst_a, v);
+        }
+    }
+}
+
 bool fits32(const Walk<2>& walk, uint64_t count) {
     if (count > UINT32_MAX) return false;
     for (int n = 0; n < 2; n++) {
@@ -211,13 +270,19 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, hipSt
             Div<I> run_div;
             run_div.set(run_words);
             const uint64_t total = rows * run_words;
-            rows_kernel<uint4, I><<<grid_for(total, 256 * 4), 256, 0, s>>>(
-                reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), words, run_div,
-                static_cast<I>(run_words), static_cast<I>(total));
+            if (2 * total * 16 > kStreamBytes) {
+                rows_kernel<uint4, true, I><<<blocks_for(total, 1), 256, 0, s>>>(
+                    reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), words, run_div,
+                    static_cast<I>(run_words), static_cast<I>(total));
+            } else {
+                rows_kernel<uint4, false, I><<<blocks_for(total, 1), 256, 0, s>>>(
+                    reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), words, run_div,
+                    static_cast<I>(run_words), static_cast<I>(total));
+            }
         } else {
             Div<I> run_div;
             run_div.set(run);
-            rows_kernel<T, I><<<grid_for(count, 256 * 4), 256, 0, s>>>(
+            rows_kernel<T, false, I><<<blocks_for(count, 1), 256, 0, s>>>(
                 src, dst, layout, run_div, static_cast<I>(run), static_cast<I>(count));
         }
         return check_launch("strided copy");
@@ -253,6 +318,22 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, hipSt
             batches *= walk.shape[k];
         }
         const uint64_t blocks = tiles_a * tiles_b * batches;
+        // Four-byte elements whose rows start on 16-byte boundaries move 16
+        // bytes a lane.
+        bool wide = sizeof(T) == 4 && blocks <= 0x7fffffffu && walk.shape[axis_a] % 4 == 0 &&
+                    walk.shape[axis_b] % 4 == 0 && walk.strides[0][axis_b] % 4 == 0 &&
+                    walk.strides[1][axis_a] % 4 == 0 && aligned16(src) && aligned16(dst);
+        for (int k = 0; wide && k < t.batch_rank; k++) wide = t.batch_src[k] % 4 == 0 && t.batch_dst[k] % 4 == 0;
+        if (wide) {
+            const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+            uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+            if (2 * count * sizeof(T) > kStreamBytes) {
+                tile4_kernel<I, true><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
+            } else {
+                tile4_kernel<I, false><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
+            }
+            return check_launch("strided copy");
+        }
         tile_kernel<T, I><<<grid_for(blocks, 1, 64), 256, 0, s>>>(src, dst, t, static_cast<I>(blocks));
         return check_launch("strided copy");
     }

@@ -20,7 +20,8 @@
 //  - columns: the innermost kept axis is contiguous and the folded axes are
 //    one strided axis; lanes take neighbouring columns so each row read is
 //    coalesced, four row groups split the depth inside a block, and long
-//    depths split across blocks with a second, ordered combining pass;
+//    depths split across blocks, each result's splits then merged by one
+//    wave in a fixed order;
 //  - general: one thread per slice walking its elements in row-major order.
 
 #include <math.h>
@@ -275,7 +276,7 @@ struct ColumnWalk {
 
 // One block: kColumns columns x kGroups row groups over one split's rows.
 // With splits == 1 it finishes the results; otherwise it writes its states
-// to `partial[split][result]` for `combine_kernel`.
+// to `partial[result][split]` for `combine_kernel`.
 template <typename S, typename P, typename O, typename I>
 __global__ void __launch_bounds__(256) columns_kernel(const S* __restrict__ in, O* __restrict__ out,
                                                       typename P::State* __restrict__ partial,
@@ -327,23 +328,28 @@ __global__ void __launch_bounds__(256) columns_kernel(const S* __restrict__ in, 
             if (w.splits == 1) {
                 Finisher<P>::write(s, f, out, result);
             } else {
-                const I total = blocks / w.splits / w.tiles * results;  // outer count x columns
-                partial[split * total + result] = s;
+                partial[result * w.splits + split] = s;
             }
         }
         __syncthreads();
     }
 }
 
-// Merge each result's split states in split order and finish it.
+// Merge each result's split states and finish it: one wave per result,
+// lanes taking the splits k = lane, lane + 64, ... in order and the wave's
+// fixed shuffle tree merging the lanes, so the order is the same every run.
+// A result's states are contiguous (`partial[result * splits + split]`), so
+// each wave's loads are one run.
 template <typename P, typename O, typename I>
 __global__ void __launch_bounds__(256) combine_kernel(const typename P::State* __restrict__ partial,
                                                       O* __restrict__ out, I results, I splits, Finish f) {
-    const I stride = static_cast<I>(gridDim.x) * blockDim.x;
-    for (I r = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; r < results; r += stride) {
-        typename P::State s = partial[r];
-        for (I k = 1; k < splits; k++) s = P::merge(s, partial[k * results + r]);
-        Finisher<P>::write(s, f, out, r);
+    const int lane = threadIdx.x % 64;
+    const I waves = static_cast<I>(gridDim.x) * (blockDim.x / 64);
+    for (I r = static_cast<I>(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64; r < results; r += waves) {
+        typename P::State s = P::init();
+        for (I k = lane; k < splits; k += 64) s = P::merge(s, partial[r * splits + k]);
+        s = wave_reduce<P>(s);
+        if (lane == 0) Finisher<P>::write(s, f, out, r);
     }
 }
 
@@ -479,8 +485,8 @@ int launch_reduce(const S* in, O* out, const Plan& plan, const Finish& f, hipStr
                                                                              static_cast<I>(blocks), f);
         int status = check_launch(what);
         if (status == TC_OK && splits > 1) {
-            combine_kernel<P, O, I><<<grid_for(results, 256), 256, 0, s>>>(partial, out, static_cast<I>(results),
-                                                                          static_cast<I>(splits), f);
+            combine_kernel<P, O, I><<<grid_for(results, 4, 64), 256, 0, s>>>(partial, out, static_cast<I>(results),
+                                                                            static_cast<I>(splits), f);
             status = check_launch(what);
         }
         // Stream order keeps the block alive until both kernels have run.

@@ -23,9 +23,11 @@ def test_permute_matches_the_reference_known_answer():
 
 
 @pytest.mark.parametrize("axes", [[0, 2, 1], [2, 1, 0], [1, 0, 2], [2, 0, 1]])
-def test_permutes_of_every_width(axes):
-    # Every element width moves by its bits (tests/nd_tensor.rs:712-744).
-    shape = (5, 67, 70)
+@pytest.mark.parametrize("shape", [(5, 67, 70), (3, 68, 132), (2, 64, 256)])
+def test_permutes_of_every_width(axes, shape):
+    # Every element width moves by its bits (tests/nd_tensor.rs:712-744);
+    # extents that are multiples of four take the 16-byte tile path for
+    # 4-byte elements, with partial tiles at the edges.
     for kind, dtype in [("u8", np.uint8), ("u16", np.uint16), ("f32", np.float32), ("u64", np.uint64)]:
         x = (np.arange(np.prod(shape)) % 251).astype(dtype).reshape(shape)
         buffer = lib.Buffer.of(x)
