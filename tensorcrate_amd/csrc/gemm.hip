@@ -14,9 +14,12 @@
 // gfx950's transposing ds_read_tr16_b64, so `matmul`, `matmul_add` and both
 // `matmul_transposed_add` forms run the same kernel with no transpose pass.
 // Blocks own 256 x 256 tiles of C over eight waves (128 x 128 over four for
-// small products), walk K 64 at a time with double-buffered LDS, stage HBM
-// through buffer loads whose out-of-range reads return zeros, and weave each
-// step's loads, LDS traffic and matrix-core steps with scheduling groups.
+// small products) and walk K 64 at a time.  HBM reaches LDS through buffer
+// loads that write LDS directly (no staging registers), into XOR-swizzled,
+// double-buffered tiles; out-of-range reads return zeros.  Each step's loads,
+// LDS reads and matrix-core steps are woven with scheduling groups, and the
+// step's barrier sits before its last slice so the next step's first
+// fragments are read under that slice's matrix-core steps.
 //
 // f32 operands (v_mfma_f32_16x16x4_f32) and 16-bit operands whose rows are
 // not 16-byte aligned take the general kernels: both operands K-contiguous,
@@ -310,43 +313,31 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
     }
 }
 
-// ---- 16-bit operands in place: the tiled kernel ---------------------------------------
+// ---- 16-bit operands in place ---------------------------------------------------------
 //
 // C[M x N] (+)= A . B with each operand read in the layout it is stored in:
 // "K-contiguous" (A stored M x K, B stored N x K) or "row-contiguous" (A
 // stored K x M, B stored K x N — B's ordinary row-major form).  Each block
 // owns a BM x BN tile of C and walks K in 64-deep steps; the waves split the
 // tile WM x WN, each owning (BM/WM) x (BN/WN) as 32 x 32 matrix-core tiles.
-//
-// LDS holds each operand's tile in its HBM orientation, double-buffered:
-//  - K-contiguous: [rows][64 + 8] — a lane's 16-byte ds_read_b128 feeds one
-//    matrix-core step (row lane % 32, k (lane / 32) * 8 .. + 8); the 144-byte
-//    row stride puts each 16-lane phase on 16 distinct 4-bank groups.
-//  - row-contiguous: [64][rows + 32] — read with gfx950's transposing
-//    ds_read_tr16_b64, which hands each lane of a 16-lane group four
-//    k-consecutive values of one column: when lane j of the group addresses
-//    (k0 + j / 4, c0 + 4 (j % 4)), lane i receives rows k0 .. k0 + 3 of column
-//    c0 + i.  Two such reads give a lane the same (column, 8 k) fragment the
-//    K-contiguous read does, so no operand is ever transposed in HBM.  The
-//    (rows + 32)-element row stride keeps the four rows of a phase on
-//    distinct banks.
+// A lane's 8-element fragment of a 32 x 32 x 16 step is row lane % 32 (the
+// tile's M or N index) and k (lane / 32) * 8 .. + 8 of the slice:
+//  - from a K-contiguous tile with one ds_read_b128;
+//  - from a row-contiguous tile with gfx950's transposing ds_read_tr16_b64,
+//    which hands each lane of a 16-lane group four k-consecutive values of
+//    one column: when lane j of the group addresses (k0 + j / 4,
+//    c0 + 4 (j % 4)), lane i receives rows k0 .. k0 + 3 of column c0 + i.
+//    Two such reads give a lane the same fragment, so no operand is ever
+//    transposed in HBM.
 // Requirements (checked by the host): 16-byte aligned operands, K a multiple
-// of 8 for K-contiguous operands, and the contiguous extent a multiple of 8
-// for row-contiguous ones.  M and N edges clamp the rows a block loads (the
-// extra rows only feed results that are never stored), and the K tail loads
-// zeros, so any M, N and K with those alignments run here.
+// of 8 for K-contiguous operands, the contiguous extent a multiple of 8 for
+// row-contiguous ones, and operands under 2^31 bytes.  M and N edges and the
+// K tail load zeros (buffer reads past the operand) or values that only feed
+// results that are never stored.
 
 constexpr int kTileK = 64;
-constexpr int kPadK = 8;    // elements after each K-contiguous LDS row
-constexpr int kPadRow = 32;  // elements after each row-contiguous LDS row
 
 typedef short short4v __attribute__((ext_vector_type(4)));
-
-template <int ROWS, bool KC>
-struct LdsTile {
-    // Elements of one buffer of the operand's LDS tile.
-    static constexpr int kElems = KC ? ROWS * (kTileK + kPadK) : kTileK * (ROWS + kPadRow);
-};
 
 __device__ __forceinline__ short4v read_tr16(const void* lds_addr) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -356,100 +347,6 @@ __device__ __forceinline__ short4v read_tr16(const void* lds_addr) {
 // The descriptor word that makes a gfx9-family buffer resource a plain,
 // untyped byte range (32-bit data format, no swizzle, no stride).
 constexpr int kBufferFlags = 0x00020000;
-
-// One operand's global -> register -> LDS staging for a block: `ROWS` rows
-// (M for A, N for B) of the tile, 64 deep in K, `THREADS` threads.  Loads go
-// through a buffer resource over the operand, which answers zeros past its
-// end: rows past M or N at the bottom of a K-contiguous operand, and the K
-// tail of a row-contiguous one, load zeros with no test in the loop.  Every
-// chunk a thread stages sits a block-uniform distance from its first, so the
-// only per-thread state is one byte offset into HBM and one into LDS.
-template <typename S, int ROWS, bool KC, int THREADS>
-struct Stager {
-    static constexpr int kChunks = ROWS * kTileK / 8;  // 16-byte chunks per tile
-    static constexpr int kPer = kChunks / THREADS;
-    static_assert(kChunks % THREADS == 0, "tile chunks must divide among the threads");
-    // Threads per tile row and the tile rows one pass of them covers.
-    static constexpr int kRowThreads = KC ? kTileK / 8 : ROWS / 8;
-    static_assert(THREADS % kRowThreads == 0, "a pass of the threads must cover whole tile rows");
-    static constexpr int kPassRows = THREADS / kRowThreads;
-    static constexpr int kLdsRow = KC ? kTileK + kPadK : ROWS + kPadRow;
-
-    __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t offset;      // this thread's first chunk, in bytes from the resource's base
-    uint32_t pass_bytes;  // bytes between a thread's consecutive chunks
-    uint32_t k_bytes;     // bytes per step of k
-    uint32_t lds_at;      // this thread's first chunk in the LDS tile, in elements
-    uint32_t k_in;        // the k of a K-contiguous thread's chunks within a step
-
-    // `rows` and `ld` are the operand's extent along the tile's rows and its
-    // stored row length; `first` the tile's first row; `depth` is K.
-    __device__ void init(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int t) {
-        const uint32_t row = t / kRowThreads, part = (t % kRowThreads) * 8;
-        if (KC) {
-            // Based at the tile's first row: rows past the operand's last
-            // fall beyond the resource.
-            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + static_cast<uint64_t>(first) * ld), 0,
-                                                     (rows - first) * ld * sizeof(S), kBufferFlags);
-            offset = (row * ld + part) * sizeof(S);
-            pass_bytes = kPassRows * ld * sizeof(S);
-            k_bytes = sizeof(S);
-            k_in = part;
-        } else {
-            // Based at the tile's first column: k rows past K fall beyond
-            // the resource; columns past the last only feed results that
-            // are never stored.
-            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + first), 0,
-                                                     (depth * ld - first) * sizeof(S), kBufferFlags);
-            offset = (row * ld + part) * sizeof(S);
-            pass_bytes = kPassRows * ld * sizeof(S);
-            k_bytes = ld * sizeof(S);
-            k_in = 0;
-        }
-        lds_at = row * kLdsRow + part;
-    }
-    // The step at `k0`; `full` says all 64 k are inside K.  Past K a
-    // K-contiguous operand's chunks are the next row's, so they are pointed
-    // past the resource's end (2^31 and more; operands are smaller), where
-    // they load zeros.
-    __device__ __forceinline__ void fetch(uint4 (&stage)[kPer], uint32_t k0, uint32_t K, bool full) const {
-        const uint32_t at = (full || !KC || k0 + k_in < K) ? offset : 0x80000000u;
-#pragma unroll
-        for (int i = 0; i < kPer; i++) {
-            auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, at, i * pass_bytes + k0 * k_bytes, 0);
-            stage[i] = __builtin_bit_cast(uint4, v);
-        }
-    }
-    __device__ __forceinline__ void commit(const uint4 (&stage)[kPer], S* lds) const {
-        uint4* to = reinterpret_cast<uint4*>(lds);
-#pragma unroll
-        for (int i = 0; i < kPer; i++) to[(lds_at + i * kPassRows * kLdsRow) / 8] = stage[i];
-    }
-};
-
-// A lane's 8-element matrix-core fragment of tile row `row` (the tile's M or
-// N index) at k `k` (a multiple of 8) from an LDS tile.
-template <typename S, int ROWS, bool KC>
-__device__ __forceinline__ uint4 fragment(const S* lds, int row_base, int k_base, int lane) {
-    if (KC) {
-        // Indexed in 16-byte units, so the read is a single ds_read_b128.
-        constexpr int kRow16 = (kTileK + kPadK) / 8;
-        return reinterpret_cast<const uint4*>(lds)[(row_base + lane % 32) * kRow16 + k_base / 8 + lane / 32];
-    } else {
-        const int g = lane / 16, j = lane % 16;
-        const int k = k_base + (g / 2) * 8 + j / 4;
-        const int col = row_base + (g % 2) * 16 + 4 * (j % 4);
-        const S* at = lds + k * (ROWS + kPadRow) + col;
-        short4v lo = read_tr16(at);
-        short4v hi = read_tr16(at + 4 * (ROWS + kPadRow));
-        uint4 out;
-        out.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
-        out.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
-        out.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
-        out.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
-        return out;
-    }
-}
 
 // The order the scheduler is asked to keep within one step: F matrix-core
 // steps per slice, each followed by its share of the next step's HBM loads
@@ -472,32 +369,128 @@ __device__ __forceinline__ void weave() {
     }
 }
 
+// ---- staging straight into LDS ------------------------------------------------
+//
+// HBM -> LDS staging is done by gfx950's buffer loads that
+// write LDS directly (`buffer_load_dwordx4 ... lds`): no staging registers
+// and no ds_write instructions.  Such a load writes 64 lanes x 16 bytes to
+// consecutive LDS bytes, so tiles are unpadded and bank conflicts are avoided
+// by XOR-swizzling each row's 16-byte chunks instead: a lane loads the
+// global chunk that belongs at the LDS position it writes.
+//  - K-contiguous tile, 128-byte rows: logical chunk c of row r lives at
+//    chunk c ^ ((r >> 1) & 7), which spreads the 16 rows a ds_read_b128 phase
+//    touches over all 16 bank groups.
+//  - row-contiguous tile, ROWS x 2-byte rows: chunk c of k-row r lives at
+//    c ^ ((r & 3) << 2), which spreads the four rows of a transposing read
+//    over distinct bank groups.
+// A step's loads target the buffer the waves are not reading; a vmcnt(0)
+// wait and a barrier end each step.
+
+__device__ __forceinline__ int kc_swizzle(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int rc_swizzle(int row) { return (row & 3) << 2; }
+
+template <typename S, int ROWS, bool KC, int WAVES>
+struct DirectStager {
+    static constexpr int kTileBytes = ROWS * kTileK * 2;
+    static constexpr int kInstr = kTileBytes / 1024;  // one wave instruction moves 1 KiB
+    static constexpr int kPer = kInstr / WAVES;
+    static_assert(kInstr % WAVES == 0, "tile instructions must divide among the waves");
+    static constexpr int kRowsPer = KC ? 8 : 1024 / (ROWS * 2);  // tile rows one instruction fills
+    static constexpr int kChunksPerRow = KC ? 8 : ROWS / 8;
+
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t offset[kPer];  // this lane's chunk of each instruction, bytes at k0 = 0
+    uint32_t k_of[kPer];    // its k within a step (K-contiguous only)
+    uint32_t k_bytes;
+    int wave;
+
+    __device__ void init(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int w, int lane) {
+        wave = w;
+        if (KC) {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + static_cast<uint64_t>(first) * ld), 0,
+                                                     (rows - first) * ld * sizeof(S), kBufferFlags);
+            k_bytes = sizeof(S);
+        } else {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + first), 0, (depth * ld - first) * sizeof(S),
+                                                     kBufferFlags);
+            k_bytes = ld * sizeof(S);
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            const int first_row = kRowsPer * (w + WAVES * i);
+            const int row = first_row + lane / kChunksPerRow;
+            const int place = lane % kChunksPerRow;
+            const int chunk = place ^ (KC ? kc_swizzle(row) : rc_swizzle(row));
+            offset[i] = (static_cast<uint32_t>(row) * ld + chunk * 8) * sizeof(S);
+            k_of[i] = KC ? chunk * 8 : 0;
+        }
+    }
+    // Stage the step at `k0` into `tile` (the LDS buffer, bytes).  Past K a
+    // K-contiguous chunk is the next row's, so it is pointed past the
+    // resource (operands are under 2^31 bytes) and loads zeros.
+    __device__ __forceinline__ void fetch(S* tile, uint32_t k0, uint32_t K, bool full) const {
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            const uint32_t at = (full || !KC || k0 + k_of[i] < K) ? offset[i] : 0x80000000u;
+            uint8_t* dst = reinterpret_cast<uint8_t*>(tile) + 1024 * (wave + WAVES * i);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, at,
+                                                     k0 * k_bytes, 0, 0);
+        }
+    }
+};
+
+// A lane's fragment from a swizzled tile (see `fragment` for the lane map).
+template <typename S, int ROWS, bool KC>
+__device__ __forceinline__ uint4 swizzled_fragment(const S* lds, int row_base, int k_base, int lane) {
+    if (KC) {
+        const int row = row_base + lane % 32;
+        const int chunk = (k_base / 8 + lane / 32) ^ kc_swizzle(row);
+        return reinterpret_cast<const uint4*>(lds)[row * 8 + chunk];
+    } else {
+        const int g = lane / 16, j = lane % 16;
+        const int k = k_base + (g / 2) * 8 + j / 4;
+        const int col = row_base + (g % 2) * 16 + 4 * (j % 4);
+        const int chunk = (col / 8) ^ rc_swizzle(k);  // k + 4 swizzles the same way
+        const S* at = lds + k * ROWS + chunk * 8 + col % 8;
+        short4v lo = read_tr16(at);
+        short4v hi = read_tr16(at + 4 * ROWS);
+        uint4 out;
+        out.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
+        out.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
+        out.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
+        out.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
+        return out;
+    }
+}
+
 template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN>
-__global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(const S* __restrict__ A, const S* __restrict__ B,
-                                                               O* __restrict__ C, uint32_t M, uint32_t N,
-                                                               uint32_t K, bool accumulate) {
-    constexpr int kThreadsT = WM * WN * 64;
+__global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restrict__ A, const S* __restrict__ B,
+                                                                O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                                                                bool accumulate) {
+    constexpr int kWaves = WM * WN;
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-    constexpr int kA = LdsTile<BM, A_KC>::kElems, kB = LdsTile<BN, B_KC>::kElems;
-    __shared__ __attribute__((aligned(16))) S lds_a[2 * kA];
-    __shared__ __attribute__((aligned(16))) S lds_b[2 * kB];
+    constexpr int kA = BM * kTileK, kB = BN * kTileK;  // elements of one buffer
+    // One array per buffer, so every LDS read and every direct load has a
+    // distinct, statically known object: the compiler then waits for a
+    // step's loads only where that step's buffer is read.
+    __shared__ __attribute__((aligned(1024))) S a0[kA];
+    __shared__ __attribute__((aligned(1024))) S a1[kA];
+    __shared__ __attribute__((aligned(1024))) S b0[kB];
+    __shared__ __attribute__((aligned(1024))) S b1[kB];
 
     const uint32_t tiles_m = (M + BM - 1) / BM;
     const uint32_t tiles_n = (N + BN - 1) / BN;
     uint32_t tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const int t = threadIdx.x;
-    const int lane = t % 64;
-    const int wave = t / 64;
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int wm = wave / WN, wn = wave % WN;
 
-    Stager<S, BM, A_KC, kThreadsT> sa;
-    Stager<S, BN, B_KC, kThreadsT> sb;
-    sa.init(A, m0, M, A_KC ? K : M, K, t);
-    sb.init(B, n0, N, B_KC ? K : N, K, t);
-    uint4 stage_a[Stager<S, BM, A_KC, kThreadsT>::kPer];
-    uint4 stage_b[Stager<S, BN, B_KC, kThreadsT>::kPer];
+    DirectStager<S, BM, A_KC, kWaves> sa;
+    DirectStager<S, BN, B_KC, kWaves> sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
+    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -505,59 +498,59 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(const S* __restri
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
 
-    const uint32_t steps = (K + kTileK - 1) / kTileK;
-    if (steps > 0) {
-        const bool full = kTileK <= K;
-        sa.fetch(stage_a, 0, K, full);
-        sb.fetch(stage_b, 0, K, full);
-        sa.commit(stage_a, lds_a);
-        sb.commit(stage_b, lds_b);
-        __syncthreads();
-    }
-    // Fragments are double-buffered in registers: the reads for the next
-    // 16-deep slice are issued before the matrix-core steps of this one.
     uint4 fa[2][TM], fb[2][TN];
     auto read_fragments = [&](int slot, const S* la, const S* lb, int kk) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) fa[slot][i] = fragment<S, BM, A_KC>(la, wm * (BM / WM) + i * 32, kk, lane);
+        for (int i = 0; i < TM; i++) fa[slot][i] = swizzled_fragment<S, BM, A_KC>(la, wm * (BM / WM) + i * 32, kk, lane);
 #pragma unroll
-        for (int j = 0; j < TN; j++) fb[slot][j] = fragment<S, BN, B_KC>(lb, wn * (BN / WN) + j * 32, kk, lane);
+        for (int j = 0; j < TN; j++) fb[slot][j] = swizzled_fragment<S, BN, B_KC>(lb, wn * (BN / WN) + j * 32, kk, lane);
     };
-    if (steps > 0) read_fragments(0, lds_a, lds_b, 0);
-    // One step is one basic block, so the scheduler can weave it: the next
-    // step's HBM loads go out with the first slice's matrix-core steps, each
-    // slice's steps carry the next slice's LDS reads, and the last slice's
-    // carry the LDS writes of the staged step.  The last step re-loads
-    // itself rather than branch, and writes a buffer no one reads again.
+
     constexpr int kSlices = kTileK / 16;
-    constexpr int kSteps = TM * TN;  // matrix-core steps per slice
-    constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);  // LDS reads per slice
-    constexpr int kLoads = Stager<S, BM, A_KC, kThreadsT>::kPer + Stager<S, BN, B_KC, kThreadsT>::kPer;
-    for (uint32_t step = 0; step < steps; step++) {
-        const int buffer = step & 1;
-        const uint32_t k0 = (step + 1 < steps ? step + 1 : step) * kTileK;
-        const bool full = k0 + kTileK <= K;
-        sa.fetch(stage_a, k0, K, full);
-        sb.fetch(stage_b, k0, K, full);
-        const S* la = lds_a + buffer * kA;
-        const S* lb = lds_b + buffer * kB;
+    constexpr int kSteps = TM * TN;
+    constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
+    constexpr int kLoads = DirectStager<S, BM, A_KC, kWaves>::kPer + DirectStager<S, BN, B_KC, kWaves>::kPer;
+    const uint32_t steps = (K + kTileK - 1) / kTileK;
+    // One step: stage the next into (na, nb) while computing from (la, lb).
+    // The wait for the staged step and the barrier come before the last
+    // slice's matrix-core steps, so the next step's first fragments are read
+    // while they run; the last slice's own fragments were read earlier, and
+    // the next staging into (la, lb) starts only after that barrier.
+    auto step = [&](uint32_t s, const S* la, const S* lb, S* na, S* nb) {
+        const uint32_t k0 = (s + 1 < steps ? s + 1 : s) * kTileK;
+        sa.fetch(na, k0, K, k0 + kTileK <= K);
+        sb.fetch(nb, k0, K, k0 + kTileK <= K);
 #pragma unroll
-        for (int q = 0; q < kSlices; q++) {
-            if (q + 1 < kSlices) read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
+        for (int q = 0; q + 1 < kSlices; q++) {
+            read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[q & 1][i], fb[q & 1][j], acc[i][j]);
         }
-        sa.commit(stage_a, lds_a + (buffer ^ 1) * kA);
-        sb.commit(stage_b, lds_b + (buffer ^ 1) * kB);
-        weave<kSteps, kLoads, kReads, kSlices>();
+        weave<kSteps, kLoads, kReads, kSlices - 1>();
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the staged step is in LDS
         __syncthreads();
-        read_fragments(0, lds_a + (buffer ^ 1) * kA, lds_b + (buffer ^ 1) * kB, 0);
+        constexpr int last = (kSlices - 1) & 1;
+        read_fragments(last ^ 1, na, nb, 0);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[last][i], fb[last][j], acc[i][j]);
+        weave<kSteps, 0, kReads, 2>();
+    };
+    if (steps > 0) {
+        sa.fetch(a0, 0, K, kTileK <= K);
+        sb.fetch(b0, 0, K, kTileK <= K);
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();
+        read_fragments(0, a0, b0, 0);
+    }
+    for (uint32_t s = 0; s < steps; s += 2) {
+        step(s, a0, b0, a1, b1);
+        if (s + 1 < steps) step(s + 1, a1, b1, a0, b0);
     }
 
-    // A 32 x 32 result tile: lane holds column lane % 32, and rows
-    // 8 (e / 4) + 4 (lane / 32) + e % 4 for its 16 values e.
 #pragma unroll
     for (int i = 0; i < TM; i++) {
 #pragma unroll
@@ -581,10 +574,10 @@ void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32
                     hipStream_t s) {
     const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
     if (large >= static_cast<uint32_t>(compute_units())) {
-        tiled16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+        direct16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
     } else {
         const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);
-        tiled16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+        direct16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
     }
 }
 
@@ -632,8 +625,12 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
         // 16-bit operands read in place whenever their rows are 16-byte
         // aligned: A is K-contiguous unless LEFT, B only when RIGHT.
         const bool a_kc = transposed != TC_LEFT, b_kc = transposed == TC_RIGHT;
+        // The tiled kernel addresses each operand with 32-bit buffer offsets
+        // and points the K tail past 2^31 bytes, so operands stay below it.
+        const uint64_t limit = uint64_t{1} << 31;
         const bool in_place = aligned16(a) && aligned16(b) && (a_kc ? k % 8 == 0 : m % 8 == 0) &&
-                              (b_kc ? k % 8 == 0 : n % 8 == 0);
+                              (b_kc ? k % 8 == 0 : n % 8 == 0) && m * k * sizeof(S) < limit &&
+                              k * n * sizeof(S) < limit;
         if (in_place) {
             const uint32_t m32 = static_cast<uint32_t>(m), k32 = static_cast<uint32_t>(k),
                            n32 = static_cast<uint32_t>(n);
