@@ -138,20 +138,12 @@ def gemm(kind: str, m: int, k: int, n: int, seed: int, sigma, steps: int, warmup
     code = KIND[kind]
     op = lambda: lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
     ms = timed(op, steps, warmup)
-    # A 16-bit product is one kernel launch, so the call's event time is the
-    # kernel's; an f32 product first transposes B, so its kernel is timed on
-    # B^T directly (`matmul_transposed_add` Right, same kernel, same shapes).
+    # The product is one kernel launch, so the call's event time is the
+    # kernel's.
     kernel_ms = ms
-    extra = []
-    if kind == "f32":
-        bt = lib.Buffer(k * n * size)
-        lib.call("tc_transpose", size, k, n, b.ptr, bt.ptr)
-        kernel = lambda: lib.call("tc_matmul", code, code, lib.RIGHT, 0, m, k, n, a.ptr, bt.ptr, c.ptr)
-        kernel_ms = timed(kernel, steps, warmup)
-        extra.append(bt)
     flops = 2.0 * m * n * k
     achieved = flops / (kernel_ms * 1e-3) / 1e12
-    for buffer in (a, b, c, *extra):
+    for buffer in (a, b, c):
         buffer.free()
     return {
         "workload": f"{kind} GEMM {m}x{k}x{n}",

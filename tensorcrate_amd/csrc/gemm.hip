@@ -21,18 +21,23 @@
 // step's barrier sits before its last slice so the next step's first
 // fragments are read under that slice's matrix-core steps.
 //
-// f32 operands (v_mfma_f32_16x16x4_f32) and 16-bit operands whose rows are
-// not 16-byte aligned take the general kernels: both operands K-contiguous,
-// a product whose operand is stored the other way round first transposed
-// into a scratch block with the LDS tile transpose; 256 x 128 tiles, 64-deep
-// (16-bit) or 32-deep (f32) k steps, operands global -> registers -> LDS,
-// double-buffered, LDS rows padded by 16 bytes.  One 16-byte LDS read of f32
-// feeds four consecutive matrix-core steps, since the sum over k does not
-// care which lane holds which k as long as both operands agree.
+// f32 operands (v_mfma_f32_16x16x4_f32, the in-place f32 kernel) are read in
+// place the same way, a row-contiguous operand's four k per lane coming from
+// four LDS reads down its tile; 256 x 128 tiles, 32-deep steps.  One 16-byte
+// LDS read of a K-contiguous f32 tile feeds four consecutive matrix-core
+// steps, since the sum over k does not care which lane holds which k as long
+// as both operands agree.
+//
+// Operands whose rows are not 16-byte aligned, or past 2^31 bytes, take the
+// general kernels: both operands K-contiguous, one stored the other way round
+// first transposed into a scratch block, loads bounds-checked element by
+// element.
 //
 // Block tiles are ordered in groups of rows, and the linear block index is
 // first spread so that the blocks one XCD runs are neighbours, which keeps
 // each XCD's L2 working on a few A and B panels.
+
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -43,6 +48,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// The descriptor word that makes a gfx9-family buffer resource a plain,
+// untyped byte range (32-bit data format, no swizzle, no stride).
+constexpr int kBufferFlags = 0x00020000;
 
 constexpr int kBM = 256;
 constexpr int kBN = 128;
@@ -313,6 +322,154 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
     }
 }
 
+// ---- f32 operands in place ---------------------------------------------------------
+//
+// The f32 product with each operand read in its stored orientation, as the
+// 16-bit kernel does, so `matmul_transposed_add` (the tape's backward
+// products) and a plain `matmul` pay for no transpose pass.  A lane's four k
+// for one tile row come from one ds_read_b128 of a K-contiguous tile, or
+// four ds_read_b32 down a row-contiguous tile ([k][rows + 4]: the 4-float
+// pad puts the four k-rows a wave reads on distinct bank quarters).  HBM is
+// staged through buffer loads (zeros past the operand) into registers and
+// then LDS, double-buffered, 256 x 128 tiles, 32-deep steps, four waves of
+// 128 x 64.  Requirements as for the 16-bit kernel, with K (K-contiguous)
+// or the contiguous extent (row-contiguous) a multiple of 4.
+
+template <int ROWS, bool KC>
+struct Stager32 {
+    static constexpr int kRowChunks = KC ? kBK32 / 4 : ROWS / 4;  // 16-byte chunks per tile row
+    static constexpr int kPassRows = kThreads / kRowChunks;
+    static constexpr int kPasses = (KC ? ROWS : kBK32) / kPassRows;
+    static constexpr int kLdsRow = KC ? kLd32 : ROWS + 4;
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t offset, pass_bytes, k_bytes, lds_at, k_in;
+
+    __device__ void init(const float* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int t) {
+        const uint32_t row = t / kRowChunks, part = (t % kRowChunks) * 4;
+        if (KC) {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + static_cast<uint64_t>(first) * ld), 0,
+                                                     (rows - first) * ld * 4, kBufferFlags);
+            k_bytes = 4;
+            k_in = part;
+        } else {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + first), 0, (depth * ld - first) * 4,
+                                                     kBufferFlags);
+            k_bytes = ld * 4;
+            k_in = 0;
+        }
+        offset = (row * ld + part) * 4;
+        pass_bytes = kPassRows * ld * 4;
+        lds_at = row * kLdsRow + part;
+    }
+    __device__ __forceinline__ void fetch(uint4 (&stage)[kPasses], uint32_t k0, uint32_t K, bool full) const {
+        const uint32_t at = (full || !KC || k0 + k_in < K) ? offset : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < kPasses; i++) {
+            auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, at, i * pass_bytes + k0 * k_bytes, 0);
+            stage[i] = __builtin_bit_cast(uint4, v);
+        }
+    }
+    __device__ __forceinline__ void commit(const uint4 (&stage)[kPasses], float* lds) const {
+        uint4* to = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+        for (int i = 0; i < kPasses; i++) to[(lds_at + i * kPassRows * kLdsRow) / 4] = stage[i];
+    }
+    // Lane `lane`'s four k (4 (lane / 16) + 0..3 of the slice at `kk`) of
+    // tile row `row`.
+    __device__ __forceinline__ f32x4 fragment(const float* lds, int row, int kk, int lane) const {
+        const int k = kk + (lane / 16) * 4;
+        if (KC) return reinterpret_cast<const f32x4*>(lds)[(row * kLdsRow + k) / 4];
+        return f32x4{lds[k * kLdsRow + row], lds[(k + 1) * kLdsRow + row], lds[(k + 2) * kLdsRow + row],
+                     lds[(k + 3) * kLdsRow + row]};
+    }
+};
+
+template <typename O, bool A_KC, bool B_KC>
+__global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                             O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                                                             bool accumulate) {
+    using SA = Stager32<kBM, A_KC>;
+    using SB = Stager32<kBN, B_KC>;
+    constexpr int kA = A_KC ? kBM * kLd32 : kBK32 * (kBM + 4);
+    constexpr int kB = B_KC ? kBN * kLd32 : kBK32 * (kBN + 4);
+    __shared__ __attribute__((aligned(16))) float lds_a[2 * kA];
+    __shared__ __attribute__((aligned(16))) float lds_b[2 * kB];
+    const uint32_t tiles_m = (M + kBM - 1) / kBM;
+    const uint32_t tiles_n = (N + kBN - 1) / kBN;
+    uint32_t tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const uint32_t m0 = tm * kBM, n0 = tn * kBN;
+    const int t = threadIdx.x;
+    const int lane = t % 64;
+    const int wave = t / 64;
+    const int wm = wave / 2, wn = wave % 2;
+    SA sa;
+    SB sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, t);
+    sb.init(B, n0, N, B_KC ? K : N, K, t);
+    uint4 stage_a[SA::kPasses], stage_b[SB::kPasses];
+
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{};
+
+    const uint32_t steps = (K + kBK32 - 1) / kBK32;
+    if (steps > 0) {
+        sa.fetch(stage_a, 0, K, kBK32 <= K);
+        sb.fetch(stage_b, 0, K, kBK32 <= K);
+        sa.commit(stage_a, lds_a);
+        sb.commit(stage_b, lds_b);
+        __syncthreads();
+    }
+    const int row_in = lane % 16;
+    for (uint32_t step = 0; step < steps; step++) {
+        const int buffer = step & 1;
+        const bool more = step + 1 < steps;
+        if (more) {
+            const uint32_t k0 = (step + 1) * kBK32;
+            sa.fetch(stage_a, k0, K, k0 + kBK32 <= K);
+            sb.fetch(stage_b, k0, K, k0 + kBK32 <= K);
+        }
+        const float* la = lds_a + buffer * kA;
+        const float* lb = lds_b + buffer * kB;
+#pragma unroll
+        for (int kk = 0; kk < kBK32; kk += 16) {
+            f32x4 a[8], b[4];
+#pragma unroll
+            for (int i = 0; i < 8; i++) a[i] = sa.fragment(la, wm * 128 + i * 16 + row_in, kk, lane);
+#pragma unroll
+            for (int j = 0; j < 4; j++) b[j] = sb.fragment(lb, wn * 64 + j * 16 + row_in, kk, lane);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            sa.commit(stage_a, lds_a + (buffer ^ 1) * kA);
+            sb.commit(stage_b, lds_b + (buffer ^ 1) * kB);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t col = n0 + wn * 64 + j * 16 + lane % 16;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t row = m0 + wm * 128 + i * 16 + 4 * (lane / 16) + e;
+                if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
+            }
+        }
+    }
+}
+
 // ---- 16-bit operands in place ---------------------------------------------------------
 //
 // C[M x N] (+)= A . B with each operand read in the layout it is stored in:
@@ -344,10 +501,6 @@ __device__ __forceinline__ short4v read_tr16(const void* lds_addr) {
         (__attribute__((address_space(3))) short4v*)(const_cast<void*>(lds_addr)));
 }
 
-// The descriptor word that makes a gfx9-family buffer resource a plain,
-// untyped byte range (32-bit data format, no swizzle, no stride).
-constexpr int kBufferFlags = 0x00020000;
-
 // The order the scheduler is asked to keep within one step: F matrix-core
 // steps per slice, each followed by its share of the next step's HBM loads
 // (first slice), of the next slice's LDS reads (all but the last) or of the
@@ -371,32 +524,41 @@ __device__ __forceinline__ void weave() {
 
 // ---- staging straight into LDS ------------------------------------------------
 //
-// HBM -> LDS staging is done by gfx950's buffer loads that
-// write LDS directly (`buffer_load_dwordx4 ... lds`): no staging registers
-// and no ds_write instructions.  Such a load writes 64 lanes x 16 bytes to
-// consecutive LDS bytes, so tiles are unpadded and bank conflicts are avoided
-// by XOR-swizzling each row's 16-byte chunks instead: a lane loads the
-// global chunk that belongs at the LDS position it writes.
-//  - K-contiguous tile, 128-byte rows: logical chunk c of row r lives at
-//    chunk c ^ ((r >> 1) & 7), which spreads the 16 rows a ds_read_b128 phase
-//    touches over all 16 bank groups.
+// HBM -> LDS staging is done by gfx950's buffer loads that write LDS directly
+// (`buffer_load_dwordx4 ... lds`): no staging registers and no ds_write
+// instructions.  Such a load writes 64 lanes x 16 bytes to consecutive LDS
+// bytes, so tiles are unpadded and bank conflicts are avoided by
+// XOR-swizzling each row's 16-byte chunks instead: a lane loads the global
+// chunk that belongs at the LDS position it writes.
+//  - K-contiguous tile, BK x 2-byte rows (CPR = BK / 8 chunks a row, RPW =
+//    256 / (2 BK) rows per 256-byte bank window): logical chunk c of row r
+//    lives at chunk c ^ ((r / RPW) % CPR), which spreads the 16 rows a
+//    ds_read_b128 phase touches over all 16 bank groups.
 //  - row-contiguous tile, ROWS x 2-byte rows: chunk c of k-row r lives at
 //    c ^ ((r & 3) << 2), which spreads the four rows of a transposing read
 //    over distinct bank groups.
-// A step's loads target the buffer the waves are not reading; a vmcnt(0)
-// wait and a barrier end each step.
+// The K loop runs NS stages deep: each step issues the loads of the step
+// NS - 1 ahead into the stage the previous step freed, then waits only for
+// the next step's loads (vmcnt counts this wave's loads in issue order).
+// Two 64-deep stages measure faster on MI355X than three or four 32-deep
+// ones (1170 vs 950 TFLOP/s at 8192^3): the per-step barrier costs more
+// than the extra latency cover buys.
 
-__device__ __forceinline__ int kc_swizzle(int row) { return (row >> 1) & 7; }
+template <int BK>
+__device__ __forceinline__ int kc_swizzle(int row) {
+    constexpr int kCpr = BK / 8, kRpw = 256 / (2 * BK);
+    return (row / kRpw) % kCpr;
+}
 __device__ __forceinline__ int rc_swizzle(int row) { return (row & 3) << 2; }
 
-template <typename S, int ROWS, bool KC, int WAVES>
+template <typename S, int ROWS, bool KC, int WAVES, int BK>
 struct DirectStager {
-    static constexpr int kTileBytes = ROWS * kTileK * 2;
+    static constexpr int kTileBytes = ROWS * BK * 2;
     static constexpr int kInstr = kTileBytes / 1024;  // one wave instruction moves 1 KiB
     static constexpr int kPer = kInstr / WAVES;
     static_assert(kInstr % WAVES == 0, "tile instructions must divide among the waves");
-    static constexpr int kRowsPer = KC ? 8 : 1024 / (ROWS * 2);  // tile rows one instruction fills
-    static constexpr int kChunksPerRow = KC ? 8 : ROWS / 8;
+    static constexpr int kRowsPer = KC ? 1024 / (BK * 2) : 1024 / (ROWS * 2);  // tile rows one instruction fills
+    static constexpr int kChunksPerRow = KC ? BK / 8 : ROWS / 8;
 
     __amdgpu_buffer_rsrc_t rsrc;
     uint32_t offset[kPer];  // this lane's chunk of each instruction, bytes at k0 = 0
@@ -420,12 +582,12 @@ struct DirectStager {
             const int first_row = kRowsPer * (w + WAVES * i);
             const int row = first_row + lane / kChunksPerRow;
             const int place = lane % kChunksPerRow;
-            const int chunk = place ^ (KC ? kc_swizzle(row) : rc_swizzle(row));
+            const int chunk = place ^ (KC ? kc_swizzle<BK>(row) : rc_swizzle(row));
             offset[i] = (static_cast<uint32_t>(row) * ld + chunk * 8) * sizeof(S);
             k_of[i] = KC ? chunk * 8 : 0;
         }
     }
-    // Stage the step at `k0` into `tile` (the LDS buffer, bytes).  Past K a
+    // Stage the step at `k0` into `tile` (the LDS stage).  Past K a
     // K-contiguous chunk is the next row's, so it is pointed past the
     // resource (operands are under 2^31 bytes) and loads zeros.
     __device__ __forceinline__ void fetch(S* tile, uint32_t k0, uint32_t K, bool full) const {
@@ -439,13 +601,14 @@ struct DirectStager {
     }
 };
 
-// A lane's fragment from a swizzled tile (see `fragment` for the lane map).
-template <typename S, int ROWS, bool KC>
+// A lane's fragment of tile row `row_base + lane % 32` (the tile's M or N
+// index) for the 16-deep slice at `k_base`, from a swizzled tile.
+template <typename S, int ROWS, bool KC, int BK>
 __device__ __forceinline__ uint4 swizzled_fragment(const S* lds, int row_base, int k_base, int lane) {
     if (KC) {
         const int row = row_base + lane % 32;
-        const int chunk = (k_base / 8 + lane / 32) ^ kc_swizzle(row);
-        return reinterpret_cast<const uint4*>(lds)[row * 8 + chunk];
+        const int chunk = (k_base / 8 + lane / 32) ^ kc_swizzle<BK>(row);
+        return reinterpret_cast<const uint4*>(lds)[row * (BK / 8) + chunk];
     } else {
         const int g = lane / 16, j = lane % 16;
         const int k = k_base + (g / 2) * 8 + j / 4;
@@ -463,20 +626,27 @@ __device__ __forceinline__ uint4 swizzled_fragment(const S* lds, int row_base, i
     }
 }
 
-template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN>
+// s_waitcnt's immediate for vmcnt(n), other counters not waited on
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_wait(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+// One LDS stage of an operand.  A separate array per stage gives every LDS
+// read and every direct load a distinct, statically known object, so the
+// compiler waits for a stage's loads only where that stage is read.
+template <typename S, int ELEMS, int STAGE>
+__device__ __forceinline__ S* stage_tile() {
+    __shared__ __attribute__((aligned(1024))) S tile[ELEMS];
+    return tile;
+}
+
+template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN, int BK, int NS>
 __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restrict__ A, const S* __restrict__ B,
                                                                 O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
                                                                 bool accumulate) {
     constexpr int kWaves = WM * WN;
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-    constexpr int kA = BM * kTileK, kB = BN * kTileK;  // elements of one buffer
-    // One array per buffer, so every LDS read and every direct load has a
-    // distinct, statically known object: the compiler then waits for a
-    // step's loads only where that step's buffer is read.
-    __shared__ __attribute__((aligned(1024))) S a0[kA];
-    __shared__ __attribute__((aligned(1024))) S a1[kA];
-    __shared__ __attribute__((aligned(1024))) S b0[kB];
-    __shared__ __attribute__((aligned(1024))) S b1[kB];
+    constexpr int kA = BM * BK, kB = BN * BK;  // elements of one stage
+    static_assert(NS >= 2 && NS <= 4, "two to four stages");
 
     const uint32_t tiles_m = (M + BM - 1) / BM;
     const uint32_t tiles_n = (N + BN - 1) / BN;
@@ -487,8 +657,10 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restr
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int wm = wave / WN, wn = wave % WN;
 
-    DirectStager<S, BM, A_KC, kWaves> sa;
-    DirectStager<S, BN, B_KC, kWaves> sb;
+    using StagerA = DirectStager<S, BM, A_KC, kWaves, BK>;
+    using StagerB = DirectStager<S, BN, B_KC, kWaves, BK>;
+    StagerA sa;
+    StagerB sb;
     sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
     sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
 
@@ -501,25 +673,33 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restr
     uint4 fa[2][TM], fb[2][TN];
     auto read_fragments = [&](int slot, const S* la, const S* lb, int kk) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) fa[slot][i] = swizzled_fragment<S, BM, A_KC>(la, wm * (BM / WM) + i * 32, kk, lane);
+        for (int i = 0; i < TM; i++)
+            fa[slot][i] = swizzled_fragment<S, BM, A_KC, BK>(la, wm * (BM / WM) + i * 32, kk, lane);
 #pragma unroll
-        for (int j = 0; j < TN; j++) fb[slot][j] = swizzled_fragment<S, BN, B_KC>(lb, wn * (BN / WN) + j * 32, kk, lane);
+        for (int j = 0; j < TN; j++)
+            fb[slot][j] = swizzled_fragment<S, BN, B_KC, BK>(lb, wn * (BN / WN) + j * 32, kk, lane);
     };
 
-    constexpr int kSlices = kTileK / 16;
+    constexpr int kSlices = BK / 16;
     constexpr int kSteps = TM * TN;
     constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
-    constexpr int kLoads = DirectStager<S, BM, A_KC, kWaves>::kPer + DirectStager<S, BN, B_KC, kWaves>::kPer;
-    const uint32_t steps = (K + kTileK - 1) / kTileK;
-    // One step: stage the next into (na, nb) while computing from (la, lb).
-    // The wait for the staged step and the barrier come before the last
-    // slice's matrix-core steps, so the next step's first fragments are read
-    // while they run; the last slice's own fragments were read earlier, and
-    // the next staging into (la, lb) starts only after that barrier.
-    auto step = [&](uint32_t s, const S* la, const S* lb, S* na, S* nb) {
-        const uint32_t k0 = (s + 1 < steps ? s + 1 : s) * kTileK;
-        sa.fetch(na, k0, K, k0 + kTileK <= K);
-        sb.fetch(nb, k0, K, k0 + kTileK <= K);
+    constexpr int kLoads = StagerA::kPer + StagerB::kPer;  // this wave's loads per step
+    const uint32_t steps = (K + BK - 1) / BK;
+    auto stage_of = [&](auto t, uint32_t s) {
+        const uint32_t k0 = (s < steps ? s : steps - 1) * BK;  // past the end: a harmless reload
+        sa.fetch(stage_tile<S, kA, 2 * decltype(t)::value>(), k0, K, k0 + BK <= K);
+        sb.fetch(stage_tile<S, kB, 2 * decltype(t)::value + 1>(), k0, K, k0 + BK <= K);
+    };
+    // Step s computes from stage T = s % NS.  It first stages step s + NS - 1
+    // into stage (T + NS - 1) % NS, which every wave finished reading before
+    // the previous step's barrier; it waits for step s + 1 and meets the
+    // others at a barrier before its last slice, whose fragments it already
+    // holds, and reads step s + 1's first fragments under that slice.
+    auto step = [&](auto t, uint32_t s) {
+        constexpr int T = decltype(t)::value;
+        const S* la = stage_tile<S, kA, 2 * T>();
+        const S* lb = stage_tile<S, kB, 2 * T + 1>();
+        stage_of(std::integral_constant<int, (T + NS - 1) % NS>{}, s + NS - 1);
 #pragma unroll
         for (int q = 0; q + 1 < kSlices; q++) {
             read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
@@ -529,10 +709,11 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restr
                 for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[q & 1][i], fb[q & 1][j], acc[i][j]);
         }
         weave<kSteps, kLoads, kReads, kSlices - 1>();
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the staged step is in LDS
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(kLoads * (NS - 2)));  // step s + 1 is in LDS
         __syncthreads();
         constexpr int last = (kSlices - 1) & 1;
-        read_fragments(last ^ 1, na, nb, 0);
+        constexpr int U = (T + 1) % NS;
+        read_fragments(last ^ 1, stage_tile<S, kA, 2 * U>(), stage_tile<S, kB, 2 * U + 1>(), 0);
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -540,15 +721,22 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restr
         weave<kSteps, 0, kReads, 2>();
     };
     if (steps > 0) {
-        sa.fetch(a0, 0, K, kTileK <= K);
-        sb.fetch(b0, 0, K, kTileK <= K);
-        __builtin_amdgcn_s_waitcnt(0x0f70);
+        stage_of(std::integral_constant<int, 0>{}, 0);
+        if constexpr (NS > 2) stage_of(std::integral_constant<int, 1>{}, 1);
+        if constexpr (NS > 3) stage_of(std::integral_constant<int, 2>{}, 2);
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(kLoads * (NS - 2)));  // step 0 is in LDS
         __syncthreads();
-        read_fragments(0, a0, b0, 0);
+        read_fragments(0, stage_tile<S, kA, 0>(), stage_tile<S, kB, 1>(), 0);
     }
-    for (uint32_t s = 0; s < steps; s += 2) {
-        step(s, a0, b0, a1, b1);
-        if (s + 1 < steps) step(s + 1, a1, b1, a0, b0);
+    for (uint32_t s = 0; s < steps; s += NS) {
+        step(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < steps) step(std::integral_constant<int, 1 % NS>{}, s + 1);
+        if constexpr (NS > 2) {
+            if (s + 2 < steps) step(std::integral_constant<int, 2 % NS>{}, s + 2);
+        }
+        if constexpr (NS > 3) {
+            if (s + 3 < steps) step(std::integral_constant<int, 3 % NS>{}, s + 3);
+        }
     }
 
 #pragma unroll
@@ -574,10 +762,10 @@ void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32
                     hipStream_t s) {
     const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
     if (large >= static_cast<uint32_t>(compute_units())) {
-        direct16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+        direct16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64, 2><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
     } else {
         const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);
-        direct16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+        direct16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2, 64, 2><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
     }
 }
 
@@ -621,7 +809,28 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
     }
     const S* pa = static_cast<const S*>(a);
     const S* pb = static_cast<const S*>(b);
-    if constexpr (!std::is_same<S, float>::value) {
+    if constexpr (std::is_same<S, float>::value) {
+        // f32 operands read in place whenever their rows are 16-byte aligned
+        // and they stay under the buffer offsets' 2^31 bytes.
+        const bool a_kc = transposed != TC_LEFT, b_kc = transposed == TC_RIGHT;
+        const uint64_t limit = uint64_t{1} << 31;
+        const bool in_place = aligned16(a) && aligned16(b) && (a_kc ? k % 4 == 0 : m % 4 == 0) &&
+                              (b_kc ? k % 4 == 0 : n % 4 == 0) && m * k * 4 < limit && k * n * 4 < limit;
+        if (in_place) {
+            const uint32_t tiles = static_cast<uint32_t>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
+            const uint32_t m32 = static_cast<uint32_t>(m), k32 = static_cast<uint32_t>(k),
+                           n32 = static_cast<uint32_t>(n);
+            O* pc = static_cast<O*>(c);
+            if (a_kc && b_kc) {
+                inplace32_kernel<O, true, true><<<tiles, kThreads, 0, s>>>(pa, pb, pc, m32, n32, k32, accumulate);
+            } else if (a_kc) {
+                inplace32_kernel<O, true, false><<<tiles, kThreads, 0, s>>>(pa, pb, pc, m32, n32, k32, accumulate);
+            } else {
+                inplace32_kernel<O, false, false><<<tiles, kThreads, 0, s>>>(pa, pb, pc, m32, n32, k32, accumulate);
+            }
+            return check_launch("matmul");
+        }
+    } else {
         // 16-bit operands read in place whenever their rows are 16-byte
         // aligned: A is K-contiguous unless LEFT, B only when RIGHT.
         const bool a_kc = transposed != TC_LEFT, b_kc = transposed == TC_RIGHT;
