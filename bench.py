@@ -43,6 +43,11 @@ from tensorcrate_amd.optim import Adam  # noqa: E402
 from tensorcrate_amd.tensor import Tensor  # noqa: E402
 
 HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
+# HBM bytes per launch of the headline product, from `rocprofv3 --pmc
+# FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --traffic-probe`,
+# scaled by what the counters read for a plain 1 GiB copy (fetch x 2.0,
+# write x 1.0): 1.631 GB read + 0.148 GB written (profiles/gemm_bf16_8192_traffic.md).
+HEADLINE_TRAFFIC = 1.779e9
 MFMA_PEAK = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}  # dense TFLOP/s
 KIND = {"bf16": lib.BF16, "f16": lib.F16, "f32": lib.F32}
 METRIC = "GEMM TFLOP/s & %MFMA peak; reduce/elementwise/copy GB/s & %HBM peak"
@@ -355,7 +360,7 @@ def main() -> int:
         "data": "synthetic: A, B ~ N(0, 1/sqrt(K)) bf16, seed 3, numpy PCG64",
         "config": {"workload": "dense GEMM bf16 M=N=K=8192, f32 accumulate, bf16 out (configs[3])",
                    "m": m, "n": n, "k": k, "device": f"{name} {arch}"},
-        "roofline": head["roofline"],
+        "roofline": {**head["roofline"], "traffic": HEADLINE_TRAFFIC},
         "cpu_baseline": baseline,
         "workloads": workloads,
     }
