@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import itertools
 import json
 import os
 import sys
@@ -167,21 +168,38 @@ def hbm_line(workload: str, nbytes: float, ms: float) -> dict:
                          "traffic": None}}
 
 
+# Inputs smaller than the 256 MiB Infinity Cache would be read back from it
+# by back-to-back calls; rotating over copies that together pass 512 MiB keeps
+# every call's reads coming from HBM.
+COLD_BYTES = 512 << 20
+
+
+def rotation(make, nbytes: int) -> list:
+    return [make() for _ in range(max(1, -(-COLD_BYTES // nbytes)))]
+
+
+def rotating(inputs: list, call):
+    """A zero-argument function calling `call` on the next of `inputs`."""
+    turn = itertools.count()
+    return lambda: call(inputs[next(turn) % len(inputs)])
+
+
 def reductions(shape, seed: int, steps: int, warmup: int) -> list[dict]:
     rng = np.random.default_rng(seed)
-    x = Tensor.from_numpy(rng.standard_normal(shape, dtype=np.float32))
+    host = rng.standard_normal(shape, dtype=np.float32)
     n = int(np.prod(shape))
+    xs = rotation(lambda: Tensor.from_numpy(host), 4 * n)
     lines = []
     tag = "x".join(map(str, shape))
     for name, axes, results in [("sum", [2], n // shape[2]), ("max", [2], n // shape[2]),
                                 ("min", [2], n // shape[2]), ("mean", [2], n // shape[2]), ("var", [2], n // shape[2]),
                                 ("sum", [0, 1], shape[2]), ("max", [0, 1], shape[2]), ("var", [0, 1], shape[2])]:
-        fn = getattr(x, f"{name}_axes")
-        ms = timed_graph(lambda: fn(axes), steps, warmup)
+        fn = rotating(xs, lambda x: getattr(x, f"{name}_axes")(axes))
+        ms = timed_graph(fn, max(steps, 2 * len(xs)), warmup)
         lines.append(hbm_line(f"{name}_axes {axes} of f32 [{tag}]", 4 * (n + results), ms))
     for name in ("argmax", "argmin"):
-        fn = getattr(x, name)
-        ms = timed_graph(lambda: fn(1), steps, warmup)
+        fn = rotating(xs, lambda x: getattr(x, name)(1))
+        ms = timed_graph(fn, max(steps, 2 * len(xs)), warmup)
         lines.append(hbm_line(f"{name} axis 1 of f32 [{tag}]", 4 * n + 4 * (n // shape[1]), ms))
     return lines
 
@@ -204,8 +222,11 @@ def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
     ms = timed_graph(lambda: out.permute([0, 2, 1]).contiguous(), steps, warmup)
     lines.append(hbm_line("permute(0,2,1).contiguous, f32 [256,512,512]", 2 * mib, ms))
     p = out.permute([0, 2, 1]).contiguous()
-    ms = timed_graph(lambda: p.slice(1, 128, 384).contiguous(), steps, warmup)
+    # The slice reads 128 MiB, which the Infinity Cache could hold: rotate.
+    sources = rotation(lambda: out.permute([0, 2, 1]).contiguous(), mib // 2)
+    ms = timed_graph(rotating(sources, lambda q: q.slice(1, 128, 384).contiguous()), steps, warmup)
     lines.append(hbm_line("slice [:,128:384,:].contiguous, f32", mib, ms))
+    del sources
     halves = p.chunk(1, 2)
     ms = timed_graph(lambda: Tensor.concat(halves, 1), steps, warmup)
     lines.append(hbm_line("concat of two [256,256,512] halves on axis 1, f32", 2 * mib, ms))
@@ -301,6 +322,32 @@ def cpu_baseline(m: int, k: int, n: int) -> dict:
                       f"widen + single-thread AVX2 i-p-j FMA + round-once, {seconds:.1f} s, scaled linearly in M"}
 
 
+def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
+    """The other configurations' lines, each with its own roofline."""
+    workloads = []
+    if "gemm" in groups:
+        log("f32 GEMM 4096^3 ...")
+        workloads.append(gemm("f32", 4096, 4096, 4096, 3, None, steps, warmup))
+        log("f16 GEMM 16384x4096x1024 ...")
+        workloads.append(gemm("f16", 16384, 1024, 4096, 3, 1 / np.sqrt(1024), steps, warmup))
+    if "reductions" in groups:
+        log("reductions ...")
+        workloads += reductions((64, 128, 1024), 1, steps, warmup)
+        workloads += reductions((1024, 128, 1024), 1, max(steps // 2, 5), warmup)
+    if "copies" in groups:
+        log("broadcast chain and copies ...")
+        workloads += broadcast_and_copies(steps, warmup)
+    if "mlp" in groups:
+        log("MLP training step and Adam ...")
+        # Three untimed steps: Adam's programs compile on their second
+        # appearance, and the streaming one (the 4096 x 4096 weight) appears
+        # once a step from the second step on.
+        workloads += mlp_step(max(steps // 4, 3), 3)
+    for line in workloads:
+        log(f"  {line['workload']}: {line['value']:.1f} {line['unit']} ({line['roofline']['frac'] * 100:.1f}%)")
+    return workloads
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -310,6 +357,9 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--traffic-probe", action="store_true",
                         help="only the short copy + product run that HBM-traffic counters are read over")
+    parser.add_argument("--only", default="",
+                        help="comma-separated secondary groups to run alone (gemm, reductions, copies, mlp); "
+                             "prints their lines as a JSON list instead of the headline line")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path, so --gpus must be 1", file=sys.stderr)
@@ -321,25 +371,23 @@ def main() -> int:
         traffic_probe()
         return 0
 
+    if args.only:
+        groups = set(args.only.split(","))
+        unknown = groups - {"gemm", "reductions", "copies", "mlp"}
+        if unknown:
+            print(f"bench.py: no workload group {sorted(unknown)}", file=sys.stderr)
+            return 2
+        workloads = secondary(groups, args.steps, args.warmup)
+        print(json.dumps(workloads), flush=True)
+        return 0
+
     m = k = n = 8192
     log("bf16 GEMM 8192^3 ...")
     head = gemm("bf16", m, k, n, 3, 1 / np.sqrt(k), args.steps, args.warmup)
     log(f"  {head['value']:.1f} TFLOP/s ({head['ms']:.3f} ms/step), kernel {head['roofline']['achieved']:.1f}")
     workloads = []
     if not args.quick:
-        log("f32 GEMM 4096^3 ...")
-        workloads.append(gemm("f32", 4096, 4096, 4096, 3, None, args.steps, args.warmup))
-        log("f16 GEMM 16384x4096x1024 ...")
-        workloads.append(gemm("f16", 16384, 1024, 4096, 3, 1 / np.sqrt(1024), args.steps, args.warmup))
-        log("reductions ...")
-        workloads += reductions((64, 128, 1024), 1, args.steps, args.warmup)
-        workloads += reductions((1024, 128, 1024), 1, max(args.steps // 2, 5), args.warmup)
-        log("broadcast chain and copies ...")
-        workloads += broadcast_and_copies(args.steps, args.warmup)
-        log("MLP training step and Adam ...")
-        workloads += mlp_step(max(args.steps // 4, 3), 2)
-        for line in workloads:
-            log(f"  {line['workload']}: {line['value']:.1f} {line['unit']} ({line['roofline']['frac'] * 100:.1f}%)")
+        workloads = secondary({"gemm", "reductions", "copies", "mlp"}, args.steps, args.warmup)
     baseline = None
     if not args.quick and not args.no_cpu:
         log("CPU baseline ...")

@@ -61,37 +61,40 @@ struct ClampTo {
 
 // out[i] = f(a[i], b[i]) over n contiguous elements; `b` may be null when f
 // ignores it.  PACKED kernels move 16-byte packs (all pointers aligned), U
-// packs a thread in one pass with every load issued before any store, and
-// block 0 finishes the last partial pack element by element; NT marks a
-// streaming launch.
+// packs a thread a round with every load issued before any store, and block
+// 0 finishes the last partial pack element by element; NT marks a streaming
+// launch.  The grid normally covers the work in one round; the loop covers
+// tensors past the 2^32 work-items one dispatch can hold.
 template <typename S, typename F, bool PACKED, bool NT, int U>
 __global__ void __launch_bounds__(256) map_kernel(const S* __restrict__ a, const S* __restrict__ b,
                                                   S* __restrict__ out, uint64_t n, F f) {
     using E = Elem<S>;
     constexpr int N = Pack<S>::N;
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * 256 * U + threadIdx.x;
+    const uint64_t step = static_cast<uint64_t>(gridDim.x) * 256 * U;
     if (PACKED) {
         const uint64_t packs = n / N;
-        Pack<S> x[U], y[U];
+        for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * 256 * U + threadIdx.x; base < packs; base += step) {
+            Pack<S> x[U], y[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint64_t i = base + u * 256;
-            if (i < packs) {
-                x[u] = __builtin_bit_cast(Pack<S>, load_word<NT>(a + i * N));
-                if (b != nullptr) y[u] = __builtin_bit_cast(Pack<S>, load_word<NT>(b + i * N));
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint64_t i = base + u * 256;
-            if (i < packs) {
-                Pack<S> z;
-#pragma unroll
-                for (int k = 0; k < N; k++) {
-                    const float yv = b != nullptr ? E::widen(y[u].v[k]) : 0.0f;
-                    z.v[k] = E::narrow(f(E::widen(x[u].v[k]), yv));
+            for (int u = 0; u < U; u++) {
+                const uint64_t i = base + u * 256;
+                if (i < packs) {
+                    x[u] = __builtin_bit_cast(Pack<S>, load_word<NT>(a + i * N));
+                    if (b != nullptr) y[u] = __builtin_bit_cast(Pack<S>, load_word<NT>(b + i * N));
                 }
-                store_word<NT>(out + i * N, __builtin_bit_cast(uint4, z));
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const uint64_t i = base + u * 256;
+                if (i < packs) {
+                    Pack<S> z;
+#pragma unroll
+                    for (int k = 0; k < N; k++) {
+                        const float yv = b != nullptr ? E::widen(y[u].v[k]) : 0.0f;
+                        z.v[k] = E::narrow(f(E::widen(x[u].v[k]), yv));
+                    }
+                    store_word<NT>(out + i * N, __builtin_bit_cast(uint4, z));
+                }
             }
         }
         const uint64_t tail = n - packs * N;
@@ -101,12 +104,14 @@ __global__ void __launch_bounds__(256) map_kernel(const S* __restrict__ a, const
             out[i] = E::narrow(f(E::widen(a[i]), yv));
         }
     } else {
+        for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * 256 * U + threadIdx.x; base < n; base += step) {
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint64_t i = base + u * 256;
-            if (i < n) {
-                const float yv = b != nullptr ? E::widen(b[i]) : 0.0f;
-                out[i] = E::narrow(f(E::widen(a[i]), yv));
+            for (int u = 0; u < U; u++) {
+                const uint64_t i = base + u * 256;
+                if (i < n) {
+                    const float yv = b != nullptr ? E::widen(b[i]) : 0.0f;
+                    out[i] = E::narrow(f(E::widen(a[i]), yv));
+                }
             }
         }
     }
@@ -207,8 +212,12 @@ __global__ void __launch_bounds__(256) strided_binary_kernel(const S* __restrict
                                                              I groups, Div<I> per_run, I run_groups) {
     using E = Elem<S>;
     const int last = w.rank - 1;
-    const I g = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (g < groups) {
+    // One round normally; the loop (64-bit, so it cannot wrap) covers work
+    // past what one dispatch holds.
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t item = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; item < groups;
+         item += stride) {
+        const I g = static_cast<I>(item);
         const I row = per_run.div(g);
         const I col = (g - row * run_groups) * V;
         // The run's start in each operand, from the row's coordinates.

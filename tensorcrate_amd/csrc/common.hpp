@@ -45,6 +45,7 @@ int check_launch(const char* what);
 // Number of compute units, for sizing persistent and split grids.
 int compute_units();
 
+
 std::string shape_text(const uint64_t* values, uint32_t rank);
 
 // ---- element types ----------------------------------------------------------
@@ -204,12 +205,13 @@ __device__ __forceinline__ void store_word(void* p, uint4 v) {
 }
 
 // Blocks of 256 threads for a one-pass kernel over `work` items, `per_thread`
-// items a thread (never zero blocks).
+// items a thread (never zero blocks).  A dispatch holds fewer than 2^32
+// work-items, so past 2^24 - 1 blocks the kernels loop.
 inline uint32_t blocks_for(uint64_t work, uint32_t per_thread) {
     const uint64_t per_block = uint64_t{256} * per_thread;
     uint64_t blocks = (work + per_block - 1) / per_block;
     if (blocks == 0) blocks = 1;
-    if (blocks > 0x7fffffffu) blocks = 0x7fffffffu;
+    if (blocks > 0xffffffu) blocks = 0xffffffu;
     return static_cast<uint32_t>(blocks);
 }
 

@@ -89,14 +89,18 @@ __global__ void __launch_bounds__(256) gather_kernel(const T* __restrict__ src, 
 }
 
 // Rows of `run` words each, a word being one element or 16 bytes of them.
-// `rows_div` divides a flat (row, word) index by the words per row.  One
-// word a thread, over a grid that covers them; NT (16-byte words only) marks
-// a copy that streams past the Infinity Cache.
+// `run_div` divides a flat (row, word) index by the words per row.  One word
+// a thread, over a grid that covers them; NT (16-byte words only) marks a
+// copy that streams past the Infinity Cache.
 template <typename T, bool NT, typename I>
 __global__ void __launch_bounds__(256) rows_kernel(const T* __restrict__ src, T* __restrict__ dst,
                                                    Layout2<I> layout, Div<I> run_div, I run, I total) {
-    const I i = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < total) {
+    // One round normally; the loop (64-bit, so it cannot wrap) covers work
+    // past what one dispatch holds.
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t item = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; item < total;
+         item += stride) {
+        const I i = static_cast<I>(item);
         I row = run_div.div(i);
         I word = i - row * run;
         I from, to;
@@ -239,7 +243,7 @@ bool fits32(const Walk<2>& walk, uint64_t count) {
 }
 
 template <typename T, typename I>
-int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, hipStream_t s) {
+int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool stream, hipStream_t s) {
     const int rank = walk.rank;
     if (rank == 0) {
         Layout2<I> layout{};
@@ -270,7 +274,7 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, hipSt
             Div<I> run_div;
             run_div.set(run_words);
             const uint64_t total = rows * run_words;
-            if (2 * total * 16 > kStreamBytes) {
+            if (stream) {
                 rows_kernel<uint4, true, I><<<blocks_for(total, 1), 256, 0, s>>>(
                     reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), words, run_div,
                     static_cast<I>(run_words), static_cast<I>(total));
@@ -319,15 +323,16 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, hipSt
         }
         const uint64_t blocks = tiles_a * tiles_b * batches;
         // Four-byte elements whose rows start on 16-byte boundaries move 16
-        // bytes a lane.
-        bool wide = sizeof(T) == 4 && blocks <= 0x7fffffffu && walk.shape[axis_a] % 4 == 0 &&
+        // bytes a lane, one tile a block (so at most 2^24 - 1 tiles, the
+        // work-items one dispatch holds).
+        bool wide = sizeof(T) == 4 && blocks <= 0xffffffu && walk.shape[axis_a] % 4 == 0 &&
                     walk.shape[axis_b] % 4 == 0 && walk.strides[0][axis_b] % 4 == 0 &&
                     walk.strides[1][axis_a] % 4 == 0 && aligned16(src) && aligned16(dst);
         for (int k = 0; wide && k < t.batch_rank; k++) wide = t.batch_src[k] % 4 == 0 && t.batch_dst[k] % 4 == 0;
         if (wide) {
             const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
             uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-            if (2 * count * sizeof(T) > kStreamBytes) {
+            if (stream) {
                 tile4_kernel<I, true><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
             } else {
                 tile4_kernel<I, false><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
@@ -343,33 +348,37 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, hipSt
 }
 
 template <typename T>
-int copy_walk(const void* src, void* dst, const Walk<2>& walk, uint64_t count, hipStream_t s) {
+int copy_walk(const void* src, void* dst, const Walk<2>& walk, uint64_t count, bool stream, hipStream_t s) {
     if (count == 0) return TC_OK;
     const T* from = static_cast<const T*>(src) + walk.offsets[0];
     T* to = static_cast<T*>(dst) + walk.offsets[1];
-    if (fits32(walk, count)) return launch_copy<T, uint32_t>(from, to, walk, count, s);
-    return launch_copy<T, uint64_t>(from, to, walk, count, s);
+    if (fits32(walk, count)) return launch_copy<T, uint32_t>(from, to, walk, count, stream, s);
+    return launch_copy<T, uint64_t>(from, to, walk, count, stream, s);
 }
 
+// `traffic` is the bytes the whole operation moves: one larger than the
+// Infinity Cache streams past it, however it is split into launches.
 int copy_by_width(uint32_t width, const void* src, void* dst, const Walk<2>& walk, uint64_t count,
-                  const char* operation) {
+                  uint64_t traffic, const char* operation) {
     TC_STREAM(s);
+    const bool stream = traffic > kStreamBytes;
     switch (width) {
-        case 1: return copy_walk<Word<1>::type>(src, dst, walk, count, s);
-        case 2: return copy_walk<Word<2>::type>(src, dst, walk, count, s);
-        case 4: return copy_walk<Word<4>::type>(src, dst, walk, count, s);
-        case 8: return copy_walk<Word<8>::type>(src, dst, walk, count, s);
-        case 16: return copy_walk<Word<16>::type>(src, dst, walk, count, s);
+        case 1: return copy_walk<Word<1>::type>(src, dst, walk, count, stream, s);
+        case 2: return copy_walk<Word<2>::type>(src, dst, walk, count, stream, s);
+        case 4: return copy_walk<Word<4>::type>(src, dst, walk, count, stream, s);
+        case 8: return copy_walk<Word<8>::type>(src, dst, walk, count, stream, s);
+        case 16: return copy_walk<Word<16>::type>(src, dst, walk, count, stream, s);
         default:
             return fail(TC_UNSUPPORTED, std::string(operation) + ": no kernel for " +
                                             std::to_string(width) + "-byte elements");
     }
 }
 
-// One region: `shape` from `source` at `from` to `target` at `to`.
+// One region: `shape` from `source` at `from` to `target` at `to`, as part
+// of an operation moving `traffic` bytes (0: just this region).
 int write_region(uint32_t width, const void* source, uint64_t source_len, void* target,
                  uint64_t target_len, uint32_t rank, const uint64_t* shape, const tc_strided& from,
-                 const tc_strided& to, const char* operation) {
+                 const tc_strided& to, uint64_t traffic, const char* operation) {
     uint64_t count = 0;
     int status = check_strided(source_len, rank, shape, from.offset, from.strides,
                                (std::string(operation) + " source").c_str(), &count);
@@ -380,7 +389,8 @@ int write_region(uint32_t width, const void* source, uint64_t source_len, void* 
     const uint64_t* strides[2] = {from.strides, to.strides};
     const uint64_t offsets[2] = {from.offset, to.offset};
     Walk<2> walk = coalesce<2>(rank, shape, strides, offsets);
-    return copy_by_width(width, source, target, walk, count, operation);
+    if (traffic == 0) traffic = 2 * count * width;
+    return copy_by_width(width, source, target, walk, count, traffic, operation);
 }
 
 }  // namespace
@@ -409,12 +419,13 @@ int tc_strided_copy(uint32_t width, const void* src, uint64_t src_len, uint32_t 
     const uint64_t* strides[2] = {from->strides, to.strides};
     const uint64_t offsets[2] = {from->offset, 0};
     Walk<2> walk = coalesce<2>(rank, shape, strides, offsets);
-    return copy_by_width(width, src, dst, walk, count, "strided copy");
+    return copy_by_width(width, src, dst, walk, count, 2 * count * width, "strided copy");
 }
 
 int tc_assemble(uint32_t width, void* dst, uint64_t len, const tc_region* regions, uint32_t count) {
     // Every region is checked before anything is queued, so a bad one
     // leaves the target untouched.
+    uint64_t traffic = 0;
     for (uint32_t r = 0; r < count; r++) {
         const tc_region& region = regions[r];
         uint64_t elements = 0;
@@ -424,11 +435,12 @@ int tc_assemble(uint32_t width, void* dst, uint64_t len, const tc_region* region
         status = check_strided(len, region.rank, region.shape, region.to.offset, region.to.strides,
                                "assemble", &elements);
         if (status != TC_OK) return status;
+        traffic += 2 * elements * width;
     }
     for (uint32_t r = 0; r < count; r++) {
         const tc_region& region = regions[r];
         int status = write_region(width, region.source, region.source_len, dst, len, region.rank,
-                                  region.shape, region.from, region.to, "assemble");
+                                  region.shape, region.from, region.to, traffic, "assemble");
         if (status != TC_OK) return status;
     }
     return TC_OK;
@@ -436,7 +448,7 @@ int tc_assemble(uint32_t width, void* dst, uint64_t len, const tc_region* region
 
 int tc_strided_write(uint32_t width, void* target, uint64_t target_len, const tc_region* region) {
     return write_region(width, region->source, region->source_len, target, target_len, region->rank,
-                        region->shape, region->from, region->to, "strided write");
+                        region->shape, region->from, region->to, 0, "strided write");
 }
 
 int tc_transpose(uint32_t width, uint64_t rows, uint64_t cols, const void* src, void* dst) {

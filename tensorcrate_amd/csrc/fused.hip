@@ -360,14 +360,29 @@ struct CompiledArgs {
     uint64_t chunks;
 };
 
+// Bytes one chunk (four elements) of a dense program loads and stores.
+uint64_t dense_chunk_bytes(const tc_encoded* code, uint32_t count) {
+    uint64_t bytes = 0;
+    for (uint32_t pc = 0; pc < count; pc++) {
+        if (code[pc].kind == 0 || code[pc].kind == 5) bytes += code[pc].b == TC_F32 ? 16 : 8;
+    }
+    return bytes;
+}
+
 // The generated source of a dense program, and the order its constants
-// take in `CompiledArgs::constants`.
-std::string dense_source(const tc_encoded* code, uint32_t count, uint32_t dtype, std::vector<float>* constants) {
+// take in `CompiledArgs::constants`.  A streaming program (one whose traffic
+// exceeds the Infinity Cache) loads and stores with nontemporal hints.
+std::string dense_source(const tc_encoded* code, uint32_t count, uint32_t dtype, bool stream,
+                         std::vector<float>* constants) {
     static const char* const kRound[] = {"tc_round<0>", "tc_round<1>", "tc_round<2>"};
     static const char* const kBinary[] = {"+", "-", "*", "/"};
     const char* round = kRound[dtype];
     std::ostringstream src;
     src << "#include \"scalar_ops.h\"\n"
+        << "typedef float tc_f4 __attribute__((ext_vector_type(4)));\n"
+        << "typedef unsigned tc_u2 __attribute__((ext_vector_type(2)));\n"
+        << (stream ? "#define TC_LD(p) __builtin_nontemporal_load(p)\n#define TC_ST(v, p) __builtin_nontemporal_store(v, p)\n"
+                   : "#define TC_LD(p) (*(p))\n#define TC_ST(v, p) (*(p) = (v))\n")
         << "struct Args { const void* in[" << kDenseLoads << "]; void* out[" << TC_FUSED_MAX_OUTPUTS
         << "]; float constants[" << kCompiledConstants << "]; unsigned long long chunks; };\n"
         << "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_program(Args a) {\n"
@@ -384,13 +399,13 @@ std::string dense_source(const tc_encoded* code, uint32_t count, uint32_t dtype,
             const std::string value = reg[in.a].empty() ? "zero" : reg[in.a];
             if (reg[in.a].empty()) src << "    const float zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};\n";
             if (in.b == TC_F32) {
-                src << "    ((float4*)a.out[" << int(in.aux) << "])[chunk] = make_float4(" << value << "[0], " << value
-                    << "[1], " << value << "[2], " << value << "[3]);\n";
+                src << "    TC_ST(((tc_f4){" << value << "[0], " << value << "[1], " << value << "[2], " << value
+                    << "[3]}), (tc_f4*)a.out[" << int(in.aux) << "] + chunk);\n";
             } else {
                 const std::string narrow = in.b == TC_F16 ? "__builtin_bit_cast(unsigned short, (_Float16)(" : "tc_f32_to_bf16((";
                 src << "    { unsigned short h[4]; for (int e = 0; e < 4; e++) h[e] = " << narrow << value << "[e]));\n"
-                    << "      ((uint2*)a.out[" << int(in.aux) << "])[chunk] = make_uint2(h[0] | ((unsigned)h[1] << 16),"
-                    << " h[2] | ((unsigned)h[3] << 16)); }\n";
+                    << "      TC_ST(((tc_u2){h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16)}), (tc_u2*)a.out["
+                    << int(in.aux) << "] + chunk); }\n";
             }
             continue;
         }
@@ -399,12 +414,12 @@ std::string dense_source(const tc_encoded* code, uint32_t count, uint32_t dtype,
             case 0: {
                 const uint32_t j = loads++;
                 if (in.b == TC_F32) {
-                    src << "    { const float4 w = ((const float4*)a.in[" << j << "])[chunk]; " << v << "[0] = " << round
+                    src << "    { const tc_f4 w = TC_LD((const tc_f4*)a.in[" << j << "] + chunk); " << v << "[0] = " << round
                         << "(w.x); " << v << "[1] = " << round << "(w.y); " << v << "[2] = " << round << "(w.z); " << v
                         << "[3] = " << round << "(w.w); }\n";
                 } else {
                     const std::string widen = in.b == TC_F16 ? "(float)__builtin_bit_cast(_Float16, (unsigned short)(" : "tc_bf16_to_f32((unsigned short)(";
-                    src << "    { const uint2 w = ((const uint2*)a.in[" << j << "])[chunk];\n"
+                    src << "    { const tc_u2 w = TC_LD((const tc_u2*)a.in[" << j << "] + chunk);\n"
                         << "      const unsigned hw[4] = {w.x & 0xffffu, w.x >> 16, w.y & 0xffffu, w.y >> 16};\n"
                         << "      for (int e = 0; e < 4; e++) " << v << "[e] = " << round << "(" << widen << "hw[e]))); }\n";
                 }
@@ -492,7 +507,8 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
     std::vector<float> constants;
     int device = 0;
     (void)hipGetDevice(&device);
-    const std::string source = dense_source(code, count, dtype, &constants);
+    const bool stream = chunks * dense_chunk_bytes(code, count) > kStreamBytes;
+    const std::string source = dense_source(code, count, dtype, stream, &constants);
     if (constants.size() > static_cast<size_t>(kCompiledConstants)) return false;
     hipFunction_t function = nullptr;
     {
@@ -516,7 +532,7 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
     args.chunks = chunks;
     size_t size = sizeof(args);
     void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
-    const uint32_t blocks = grid_for(chunks, 256, 8);
+    const uint32_t blocks = blocks_for(chunks, 1);
     hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, nullptr, config);
     *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused program: ") + hipGetErrorString(error));
     return true;

@@ -51,6 +51,11 @@ struct Fold {
         for (int k = 0; k < N; k++) c = combine(c, x[k]);
         s = combine(s, c);
     }
+    // U packs of V elements, pack k starting at element first + k * step.
+    template <int U, int V>
+    __device__ static void add_packs(State& s, const float (&x)[U * V], uint32_t, uint32_t) {
+        add_chunk(s, x, 0);
+    }
     __device__ static State merge(State a, State b) { return combine(a, b); }
     __device__ static State shuffle(State s, int lane) { return __shfl(s, lane, 64); }
 };
@@ -88,6 +93,12 @@ struct Var {
         }
         s = merge_moments(s, Moments{static_cast<float>(N), mean, m2});
     }
+    // Every pack a lane holds is one chunk: the pairwise merge, with its
+    // division, runs once per U * V elements instead of once per pack.
+    template <int U, int V>
+    __device__ static void add_packs(State& s, const float (&x)[U * V], uint32_t, uint32_t) {
+        add_chunk(s, x, 0);
+    }
     __device__ static State merge(State a, State b) { return merge_moments(a, b); }
     __device__ static State shuffle(State s, int lane) {
         return Moments{__shfl(s.n, lane, 64), __shfl(s.mean, lane, 64), __shfl(s.m2, lane, 64)};
@@ -120,6 +131,14 @@ struct ArgFold {
     __device__ static void add_chunk(State& s, const float (&x)[N], uint32_t first) {
 #pragma unroll
         for (int k = 0; k < N; k++) add(s, x[k], first + k);
+    }
+    template <int U, int V>
+    __device__ static void add_packs(State& s, const float (&x)[U * V], uint32_t first, uint32_t step) {
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+#pragma unroll
+            for (int j = 0; j < V; j++) add(s, x[k * V + j], first + k * step + j);
+        }
     }
     __device__ static State merge(State a, State b) { return better(b, a) ? b : a; }
     __device__ static State shuffle(State s, int lane) {
@@ -178,6 +197,30 @@ __device__ inline typename P::State wave_reduce(typename P::State s) {
     return s;
 }
 
+// The wave's moments in closed form rather than by six pairwise merges:
+// with N = sum n_i and mean = sum n_i mean_i / N,
+//     M2 = sum (M2_i + n_i (mean_i - mean)^2),
+// the identity each of Chan's merges applies, taken over all 64 lanes at
+// once.  Two shuffle-sum trees and one division instead of six divisions
+// and eighteen shuffles; the fixed tree keeps the result deterministic.
+// A butterfly sum: every lane ends with the same total (each step adds one
+// pair, and addition is commutative).
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+template <>
+__device__ inline Moments wave_reduce<Var>(Moments s) {
+    const float n = wave_sum(s.n);
+    if (n == 0.0f) return Var::init();
+    const float mean = wave_sum(s.n * s.mean) / n;
+    const float d = s.mean - mean;
+    const float m2 = wave_sum(s.n == 0.0f ? 0.0f : s.m2 + s.n * d * d);
+    return Moments{n, mean, m2};
+}
+
 // ---- layouts ----------------------------------------------------------------
 
 template <typename I>
@@ -215,11 +258,30 @@ struct alignas(16) Pack {
 
 // ---- rows: one wave per contiguous slice ------------------------------------
 
-template <typename S, typename P, typename O, bool PACKED, typename I>
+// U packs of one lane, 64 packs apart, loaded together and widened.
+template <typename S, int U, bool NT>
+__device__ __forceinline__ void load_packs(const Pack<S>* packs, float (&x)[U * Pack<S>::N]) {
+    constexpr int V = Pack<S>::N;
+    uint4 w[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) w[k] = load_word<NT>(packs + k * 64);
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+        Pack<S> p;
+        __builtin_memcpy(&p, &w[k], 16);
+#pragma unroll
+        for (int j = 0; j < V; j++) x[k * V + j] = Elem<S>::widen(p.v[j]);
+    }
+}
+
+// With NT the input streams past the Infinity Cache (inputs larger than it).
+template <typename S, typename P, typename O, bool PACKED, bool NT, typename I>
 __global__ void __launch_bounds__(256) rows_kernel(const S* __restrict__ in, O* __restrict__ out,
                                                    Kept<I> kept, I results, I depth, Finish f) {
     using E = Elem<S>;
     constexpr int V = Pack<S>::N;
+    // Four 16-byte packs in flight per lane: a 4 KiB row per wave at once.
+    constexpr int U = 4;
     const int lane = threadIdx.x % 64;
     const I waves = static_cast<I>(gridDim.x) * (blockDim.x / 64);
     for (I r = static_cast<I>(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64; r < results; r += waves) {
@@ -229,24 +291,15 @@ __global__ void __launch_bounds__(256) rows_kernel(const S* __restrict__ in, O* 
             const Pack<S>* packs = reinterpret_cast<const Pack<S>*>(slice);
             const I count = depth / V;
             I p = lane;
-            // Two packs in flight per lane per step.
-            for (; p + 64 < count; p += 128) {
-                Pack<S> a = packs[p], b = packs[p + 64];
-                float x[V], y[V];
-#pragma unroll
-                for (int k = 0; k < V; k++) {
-                    x[k] = E::widen(a.v[k]);
-                    y[k] = E::widen(b.v[k]);
-                }
-                P::add_chunk(s, x, static_cast<uint32_t>(p * V));
-                P::add_chunk(s, y, static_cast<uint32_t>((p + 64) * V));
+            for (; p + 64 * (U - 1) < count; p += 64 * U) {
+                float x[U * V];
+                load_packs<S, U, NT>(packs + p, x);
+                P::template add_packs<U, V>(s, x, static_cast<uint32_t>(p * V), 64 * V);
             }
-            if (p < count) {
-                Pack<S> a = packs[p];
+            for (; p < count; p += 64) {
                 float x[V];
-#pragma unroll
-                for (int k = 0; k < V; k++) x[k] = E::widen(a.v[k]);
-                P::add_chunk(s, x, static_cast<uint32_t>(p * V));
+                load_packs<S, 1, NT>(packs + p, x);
+                P::template add_packs<1, V>(s, x, static_cast<uint32_t>(p * V), 0);
             }
         } else {
             for (I i = lane; i < depth; i += 64) P::add(s, E::widen(slice[i]), static_cast<uint32_t>(i));
@@ -274,19 +327,21 @@ struct ColumnWalk {
     I per_split;    // rows per split (the last may hold fewer)
 };
 
-// One block: kColumns columns x kGroups row groups over one split's rows.
+// One block: kColumns lanes, each on VC neighbouring columns (VC > 1 reads
+// them as one 16-byte word), times kGroups row groups over one split's rows.
 // With splits == 1 it finishes the results; otherwise it writes its states
-// to `partial[result][split]` for `combine_kernel`.
-template <typename S, typename P, typename O, typename I>
+// to `partial[result * splits + split]` for the combine kernels.
+template <typename S, typename P, typename O, int VC, bool NT, typename I>
 __global__ void __launch_bounds__(256) columns_kernel(const S* __restrict__ in, O* __restrict__ out,
                                                       typename P::State* __restrict__ partial,
                                                       ColumnWalk<I> w, I blocks, Finish f) {
     using E = Elem<S>;
     using State = typename P::State;
-    __shared__ State stage[kGroups][kColumns];
+    // Rows in flight per lane.
+    constexpr int U = 8;
+    __shared__ State stage[kGroups][VC][kColumns];
     const int lane = threadIdx.x % kColumns;
     const int group = threadIdx.x / kColumns;
-    const I results = w.columns;  // per outer index
     for (I block = blockIdx.x; block < blocks; block += gridDim.x) {
         // block -> (split, outer, tile), split outermost so neighbouring
         // blocks share rows.
@@ -295,7 +350,9 @@ __global__ void __launch_bounds__(256) columns_kernel(const S* __restrict__ in, 
         const I rest = block - split * per_split_blocks;
         const I outer = w.tiles_div.div(rest);
         const I tile = rest - outer * w.tiles;
-        const I column = tile * kColumns + lane;
+        // With VC > 1 the columns are a multiple of VC, so a lane's first
+        // column in range puts all VC in range.
+        const I column = (tile * kColumns + lane) * VC;
         const I row_begin = split * w.per_split;
         I row_end = row_begin + w.per_split;
         if (row_end > w.depth) row_end = w.depth;
@@ -306,29 +363,60 @@ __global__ void __launch_bounds__(256) columns_kernel(const S* __restrict__ in, 
         I last = first + per_group;
         if (last > row_end) last = row_end;
         if (first > row_end) first = row_end;
-        State s = P::init();
+        State s[VC];
+#pragma unroll
+        for (int c = 0; c < VC; c++) s[c] = P::init();
         if (column < w.columns) {
             const S* base = in + kept_offset(w.outer, outer) + column;
             I row = first;
-            constexpr int U = 8;
-            for (; row + U <= last; row += U) {
-                float x[U];
+            if (VC == 1) {
+                for (; row + U <= last; row += U) {
+                    float x[U];
 #pragma unroll
-                for (int k = 0; k < U; k++) x[k] = E::widen(base[(row + k) * w.step]);
-                P::add_chunk(s, x, static_cast<uint32_t>(row));
+                    for (int k = 0; k < U; k++) x[k] = E::widen(base[(row + k) * w.step]);
+                    P::add_chunk(s[0], x, static_cast<uint32_t>(row));
+                }
+                for (; row < last; row++) P::add(s[0], E::widen(base[row * w.step]), static_cast<uint32_t>(row));
+            } else {
+                for (; row + U <= last; row += U) {
+                    S v[U][VC];
+#pragma unroll
+                    for (int k = 0; k < U; k++) {
+                        const uint4 word = load_word<NT>(base + (row + k) * w.step);
+                        __builtin_memcpy(v[k], &word, 16);
+                    }
+#pragma unroll
+                    for (int c = 0; c < VC; c++) {
+                        float x[U];
+#pragma unroll
+                        for (int k = 0; k < U; k++) x[k] = E::widen(v[k][c]);
+                        P::add_chunk(s[c], x, static_cast<uint32_t>(row));
+                    }
+                }
+                for (; row < last; row++) {
+                    S v[VC];
+                    const uint4 word = load_word<NT>(base + row * w.step);
+                    __builtin_memcpy(v, &word, 16);
+#pragma unroll
+                    for (int c = 0; c < VC; c++) P::add(s[c], E::widen(v[c]), static_cast<uint32_t>(row));
+                }
             }
-            for (; row < last; row++) P::add(s, E::widen(base[row * w.step]), static_cast<uint32_t>(row));
         }
-        stage[group][lane] = s;
+#pragma unroll
+        for (int c = 0; c < VC; c++) stage[group][c][lane] = s[c];
         __syncthreads();
         if (group == 0 && column < w.columns) {
 #pragma unroll
-            for (int g = 1; g < kGroups; g++) s = P::merge(s, stage[g][lane]);
-            const I result = outer * results + column;
-            if (w.splits == 1) {
-                Finisher<P>::write(s, f, out, result);
-            } else {
-                partial[result * w.splits + split] = s;
+            for (int c = 0; c < VC; c++) {
+                State t = s[c];
+#pragma unroll
+                for (int g = 1; g < kGroups; g++) t = P::merge(t, stage[g][c][lane]);
+                const I result = outer * w.columns + column + c;
+                if (w.splits == 1) {
+                    Finisher<P>::write(t, f, out, result);
+                } else {
+                    partial[result * w.splits + split] = t;
+                }
             }
         }
         __syncthreads();
@@ -350,6 +438,19 @@ __global__ void __launch_bounds__(256) combine_kernel(const typename P::State* _
         for (I k = lane; k < splits; k += 64) s = P::merge(s, partial[r * splits + k]);
         s = wave_reduce<P>(s);
         if (lane == 0) Finisher<P>::write(s, f, out, r);
+    }
+}
+
+// The same merge for a few splits per result: one thread per result, folding
+// its splits left to right.
+template <typename P, typename O, typename I>
+__global__ void __launch_bounds__(256) combine_few_kernel(const typename P::State* __restrict__ partial,
+                                                          O* __restrict__ out, I results, I splits, Finish f) {
+    const I stride = static_cast<I>(gridDim.x) * blockDim.x;
+    for (I r = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; r < results; r += stride) {
+        typename P::State s = partial[r * splits];
+        for (I k = 1; k < splits; k++) s = P::merge(s, partial[r * splits + k]);
+        Finisher<P>::write(s, f, out, r);
     }
 }
 
@@ -424,6 +525,64 @@ struct Plan {
     uint64_t results, depth;
 };
 
+// The columns kernel over a plan whose innermost kept axis is contiguous and
+// whose one folded axis is strided; VC columns per lane.
+template <typename S, typename P, typename O, int VC, bool NT, typename I>
+int launch_columns(const S* in, O* out, const Plan& plan, const Finish& f, hipStream_t s, const char* what) {
+    const Axes& kept = plan.kept;
+    const uint64_t results = plan.results, depth = plan.depth;
+    ColumnWalk<I> w{};
+    w.outer = make_kept<I>(kept, kept.rank - 1);
+    const uint64_t columns = kept.shape[kept.rank - 1];
+    const uint64_t outer = results / columns;
+    const uint64_t tiles = (columns + kColumns * VC - 1) / (kColumns * VC);
+    w.columns = static_cast<I>(columns);
+    w.depth = static_cast<I>(depth);
+    w.step = static_cast<I>(plan.folded.strides[0]);
+    w.tiles = static_cast<I>(tiles);
+    w.tiles_div.set(tiles);
+    // Split the depth across blocks until there are four blocks for every
+    // CU, each row group keeping at least 32 rows (16 of 16-byte words); a
+    // split costs one partial state per result, written and read back once.
+    const uint64_t base_blocks = outer * tiles;
+    const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
+    uint64_t splits = 1;
+    if (base_blocks < want) {
+        splits = (want + base_blocks - 1) / base_blocks;
+        const uint64_t most = depth / (kGroups * (VC == 1 ? 32 : 16));
+        if (splits > most) splits = most;
+        if (splits < 1) splits = 1;
+    }
+    const uint64_t per_split = (depth + splits - 1) / splits;
+    splits = (depth + per_split - 1) / per_split;
+    w.splits = static_cast<I>(splits);
+    w.per_split = static_cast<I>(per_split);
+    const uint64_t blocks = base_blocks * splits;
+    typename P::State* partial = nullptr;
+    if (splits > 1) {
+        void* scratch = nullptr;
+        int status = tc_alloc(splits * results * sizeof(typename P::State), &scratch);
+        if (status != TC_OK) return status;
+        partial = static_cast<typename P::State*>(scratch);
+    }
+    columns_kernel<S, P, O, VC, NT, I><<<grid_for(blocks, 1, 64), 256, 0, s>>>(in, out, partial, w,
+                                                                                 static_cast<I>(blocks), f);
+    int status = check_launch(what);
+    if (status == TC_OK && splits > 1) {
+        if (splits <= 8) {
+            combine_few_kernel<P, O, I><<<grid_for(results, 256, 64), 256, 0, s>>>(
+                partial, out, static_cast<I>(results), static_cast<I>(splits), f);
+        } else {
+            combine_kernel<P, O, I><<<grid_for(results, 4, 64), 256, 0, s>>>(
+                partial, out, static_cast<I>(results), static_cast<I>(splits), f);
+        }
+        status = check_launch(what);
+    }
+    // Stream order keeps the block alive until both kernels have run.
+    if (partial != nullptr) tc_free(partial);
+    return status;
+}
+
 template <typename S, typename P, typename O, typename I>
 int launch_reduce(const S* in, O* out, const Plan& plan, const Finish& f, hipStream_t s, const char* what) {
     const Axes& kept = plan.kept;
@@ -436,62 +595,31 @@ int launch_reduce(const S* in, O* out, const Plan& plan, const Finish& f, hipStr
         for (int k = 0; packed && k < kept.rank; k++) packed = (kept.strides[k] * sizeof(S)) % 16 == 0;
         Kept<I> k = make_kept<I>(kept, kept.rank);
         const uint32_t blocks = grid_for(results, 4, 32);
-        if (packed) {
-            rows_kernel<S, P, O, true, I><<<blocks, 256, 0, s>>>(in, out, k, static_cast<I>(results),
-                                                                 static_cast<I>(depth), f);
+        const bool stream = results * depth * sizeof(S) > kStreamBytes;
+        if (packed && stream) {
+            rows_kernel<S, P, O, true, true, I><<<blocks, 256, 0, s>>>(in, out, k, static_cast<I>(results),
+                                                                       static_cast<I>(depth), f);
+        } else if (packed) {
+            rows_kernel<S, P, O, true, false, I><<<blocks, 256, 0, s>>>(in, out, k, static_cast<I>(results),
+                                                                        static_cast<I>(depth), f);
         } else {
-            rows_kernel<S, P, O, false, I><<<blocks, 256, 0, s>>>(in, out, k, static_cast<I>(results),
-                                                                  static_cast<I>(depth), f);
+            rows_kernel<S, P, O, false, false, I><<<blocks, 256, 0, s>>>(in, out, k, static_cast<I>(results),
+                                                                         static_cast<I>(depth), f);
         }
         return check_launch(what);
     }
     // Columns: contiguous neighbouring results, one strided folded axis.
     if (folded.rank == 1 && kept.rank >= 1 && kept.strides[kept.rank - 1] == 1 &&
         kept.shape[kept.rank - 1] >= 16) {
-        ColumnWalk<I> w{};
-        w.outer = make_kept<I>(kept, kept.rank - 1);
-        const uint64_t columns = kept.shape[kept.rank - 1];
-        const uint64_t outer = results / columns;
-        const uint64_t tiles = (columns + kColumns - 1) / kColumns;
-        w.columns = static_cast<I>(columns);
-        w.depth = static_cast<I>(depth);
-        w.step = static_cast<I>(folded.strides[0]);
-        w.tiles = static_cast<I>(tiles);
-        w.tiles_div.set(tiles);
-        // Enough blocks to put four on every CU, each split keeping at least
-        // 32 rows per row group.
-        const uint64_t base_blocks = outer * tiles;
-        const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
-        uint64_t splits = 1;
-        if (base_blocks < want) {
-            splits = (want + base_blocks - 1) / base_blocks;
-            const uint64_t most = depth / (kGroups * 32);
-            if (splits > most) splits = most;
-            if (splits < 1) splits = 1;
-        }
-        const uint64_t per_split = (depth + splits - 1) / splits;
-        splits = (depth + per_split - 1) / per_split;
-        w.splits = static_cast<I>(splits);
-        w.per_split = static_cast<I>(per_split);
-        const uint64_t blocks = base_blocks * splits;
-        typename P::State* partial = nullptr;
-        if (splits > 1) {
-            void* scratch = nullptr;
-            int status = tc_alloc(splits * results * sizeof(typename P::State), &scratch);
-            if (status != TC_OK) return status;
-            partial = static_cast<typename P::State*>(scratch);
-        }
-        columns_kernel<S, P, O, I><<<grid_for(blocks, 1, 64), 256, 0, s>>>(in, out, partial, w,
-                                                                             static_cast<I>(blocks), f);
-        int status = check_launch(what);
-        if (status == TC_OK && splits > 1) {
-            combine_kernel<P, O, I><<<grid_for(results, 4, 64), 256, 0, s>>>(partial, out, static_cast<I>(results),
-                                                                            static_cast<I>(splits), f);
-            status = check_launch(what);
-        }
-        // Stream order keeps the block alive until both kernels have run.
-        if (partial != nullptr) tc_free(partial);
-        return status;
+        // An input past the Infinity Cache streams with 16-byte words, VC
+        // columns a lane; a smaller one runs a column a lane, which spreads
+        // it over four times the blocks (measured faster below 256 MiB).
+        constexpr int VC = 16 / sizeof(S);
+        bool packed = results * depth * sizeof(S) > kStreamBytes && kept.shape[kept.rank - 1] % VC == 0 &&
+                      folded.strides[0] % VC == 0 && aligned16(in);
+        for (int k = 0; packed && k + 1 < kept.rank; k++) packed = kept.strides[k] % VC == 0;
+        if (packed) return launch_columns<S, P, O, VC, true, I>(in, out, plan, f, s, what);
+        return launch_columns<S, P, O, 1, false, I>(in, out, plan, f, s, what);
     }
     Kept<I> k = make_kept<I>(kept, kept.rank);
     Folded<I> fo{};

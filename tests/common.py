@@ -82,3 +82,38 @@ def same_bits(got: np.ndarray, want: np.ndarray, kind) -> bool:
     if not np.array_equal(gn, wn):
         return False
     return got[~gn].tobytes() == want[~wn].tobytes()
+
+
+class CapturedGraph:
+    """The calls `fn` makes on the library's stream, captured (relaxed mode)
+    into one HIP graph that `replay()` launches and waits for."""
+
+    def __init__(self, fn):
+        import ctypes
+
+        hip = ctypes.CDLL("libamdhip64.so")
+        vp = ctypes.c_void_p
+        hip.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        hip.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+        hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]
+        hip.hipGraphLaunch.argtypes = [vp, vp]
+        hip.hipGraphExecDestroy.argtypes = [vp]
+        hip.hipGraphDestroy.argtypes = [vp]
+        self._hip = hip
+        self._stream = vp()
+        lib.call("tc_stream", ctypes.byref(self._stream))
+        self._graph, self._exec = vp(), vp()
+        assert hip.hipStreamBeginCapture(self._stream, 2) == 0
+        try:
+            self.result = fn()
+        finally:
+            assert hip.hipStreamEndCapture(self._stream, ctypes.byref(self._graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(self._exec), self._graph, None, None, 0) == 0
+
+    def replay(self) -> None:
+        assert self._hip.hipGraphLaunch(self._exec, self._stream) == 0
+        lib.sync()
+
+    def close(self) -> None:
+        self._hip.hipGraphExecDestroy(self._exec)
+        self._hip.hipGraphDestroy(self._graph)

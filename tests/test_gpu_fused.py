@@ -142,3 +142,21 @@ def test_a_repeated_program_runs_compiled_and_stays_exact():
         expected = want.update(expected, g)
         assert np.array_equal(params.download(np.float32), expected)
     assert compiled() > before
+
+
+def test_a_compiled_program_past_the_infinity_cache_streams_and_stays_exact():
+    # 12 Mi parameters: the resumed Adam step moves 28 bytes a parameter,
+    # 336 MiB, past the 256 MiB Infinity Cache, so its compiled kernel takes
+    # the nontemporal loads and stores; its bits must not change.
+    rng = np.random.default_rng(13)
+    n = 12 << 20
+    p0 = rng.standard_normal(n, dtype=np.float32)
+    params = lib.Buffer.of(p0)
+    rule = Adam(1e-2)
+    want = mlp.Adam(1e-2)
+    expected = p0.copy()
+    for step in range(4):
+        g = rng.standard_normal(n, dtype=np.float32)
+        rule.update(params, lib.Buffer.of(g), 1, n)
+        expected = want.update(expected, g)
+    assert np.array_equal(params.download(np.float32), expected)

@@ -18,7 +18,7 @@ import pytest
 from oracle import binding as oracle
 from tensorcrate_amd import lib
 from tensorcrate_amd.tensor import Tensor
-from tests.common import KINDS, bits_equal, filler, same, to_kind, widen
+from tests.common import KINDS, CapturedGraph, bits_equal, filler, same, to_kind, widen
 
 pytestmark = pytest.mark.gpu
 
@@ -194,6 +194,29 @@ def test_config2_reductions():
         assert np.array_equal(getattr(t, name)(1).to_numpy(), want)
 
 
+def test_reductions_past_the_infinity_cache():
+    # 320 MiB, over the 256 MiB Infinity Cache: the row and column kernels
+    # stream with nontemporal loads.  Max and the arg indices stay bit-exact
+    # (numpy's max and first-index argmax are the Host rule on NaN-free
+    # data); sums and variances stay within the accumulated-rounding bound.
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((80, 1024, 1024), dtype=np.float32)
+    t = Tensor.from_numpy(x)
+    assert bits_equal(t.max_axes([2]).to_numpy(), x.max(2))
+    assert bits_equal(t.min_axes([0]).to_numpy(), x.min(0))
+    assert np.array_equal(t.argmax(2).to_numpy(), x.argmax(2))
+    assert np.array_equal(t.argmin(0).to_numpy(), x.argmin(0))
+    for axes in ([2], [0]):
+        s = slices(x, axes)
+        depth = s.shape[1]
+        check_sum_like(t.sum_axes(axes).to_numpy().reshape(-1), s.sum(1), np.abs(s).sum(1), depth, lib.F32, axes)
+        dev = s - s.mean(1, keepdims=True)
+        want = (dev ** 2).sum(1) / depth
+        check_sum_like(t.var_axes(axes).to_numpy().reshape(-1), want, want + np.abs(s).max(1) ** 2 / depth, depth,
+                       lib.F32, axes)
+        del s, dev
+
+
 def test_whole_vector_reduce_and_dot():
     rng = np.random.default_rng(12)
     for n in [1, 15, 16, 1000, 1 << 20]:
@@ -210,3 +233,41 @@ def test_whole_vector_reduce_and_dot():
         lib.call("tc_dot", lib.F32, da.ptr, db.ptr, n, result.ptr)
         want = np.dot(a.astype(np.float64), b)
         assert abs(result.download(np.float32)[0] - want) <= 2.0 ** -24 * 4 * np.sqrt(n) * np.abs(a * b).sum()
+
+
+def test_split_column_reductions_replay_from_a_graph_with_the_eager_bits():
+    # A column reduction split across blocks writes partial states to
+    # scratch and merges them in a second kernel, in a fixed order.  Captured
+    # into a HIP graph (on a thread of its own, so on a stream of its own) and
+    # replayed three times, with the program's own downloads between the
+    # replays, it gives the eager bits every time.
+    import threading
+
+    rng = np.random.default_rng(15)
+    x = rng.standard_normal((8192, 1024), dtype=np.float32)
+    eager = Tensor.from_numpy(x)
+    want = [eager.sum_axes([0]).to_numpy(), eager.var_axes([0]).to_numpy(), eager.max_axes([0]).to_numpy(),
+            eager.argmax(0).to_numpy()]
+    assert bits_equal(want[2], x.max(0))
+    assert np.array_equal(want[3], x.argmax(0))
+    failures = []
+
+    def captured():
+        try:
+            lib.call("tc_init", 0)
+            t = Tensor.from_numpy(x)
+            lib.sync()
+            graph = CapturedGraph(lambda: [t.sum_axes([0]), t.var_axes([0]), t.max_axes([0]), t.argmax(0)])
+            for replay in range(3):
+                graph.replay()
+                for k, (got, expected) in enumerate(zip(graph.result, want)):
+                    if not bits_equal(got.to_numpy(), expected):
+                        failures.append((replay, k))
+            graph.close()
+        except Exception as error:  # reported on the test's thread
+            failures.append(repr(error))
+
+    worker = threading.Thread(target=captured)
+    worker.start()
+    worker.join()
+    assert not failures, failures
