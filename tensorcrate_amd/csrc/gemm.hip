@@ -23,7 +23,8 @@
 //
 // f32 operands (v_mfma_f32_16x16x4_f32, the in-place f32 kernel) are read in
 // place the same way, a row-contiguous operand's four k per lane coming from
-// four LDS reads down its tile; 256 x 128 tiles, 32-deep steps.  One 16-byte
+// four LDS reads down its tile; 256 x 128 tiles (128 x 128 for products with
+// fewer such tiles than CUs), 32-deep steps.  One 16-byte
 // LDS read of a K-contiguous f32 tile feeds four consecutive matrix-core
 // steps, since the sum over k does not care which lane holds which k as long
 // as both operands agree.
@@ -331,8 +332,8 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
 // four ds_read_b32 down a row-contiguous tile ([k][rows + 4]: the 4-float
 // pad puts the four k-rows a wave reads on distinct bank quarters).  HBM is
 // staged through buffer loads (zeros past the operand) into registers and
-// then LDS, double-buffered, 256 x 128 tiles, 32-deep steps, four waves of
-// 128 x 64.  Requirements as for the 16-bit kernel, with K (K-contiguous)
+// then LDS, double-buffered, 256 x 128 or 128 x 128 tiles, 32-deep steps,
+// four waves of a quarter tile.  Requirements as for the 16-bit kernel, with K (K-contiguous)
 // or the contiguous extent (row-contiguous) a multiple of 4.
 
 template <int ROWS, bool KC>
@@ -384,21 +385,23 @@ struct Stager32 {
     }
 };
 
-template <typename O, bool A_KC, bool B_KC>
+// BM x BN tiles over four waves of (BM / 2) x (BN / 2).
+template <typename O, bool A_KC, bool B_KC, int BM, int BN>
 __global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                              O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
                                                              bool accumulate) {
-    using SA = Stager32<kBM, A_KC>;
-    using SB = Stager32<kBN, B_KC>;
-    constexpr int kA = A_KC ? kBM * kLd32 : kBK32 * (kBM + 4);
-    constexpr int kB = B_KC ? kBN * kLd32 : kBK32 * (kBN + 4);
+    using SA = Stager32<BM, A_KC>;
+    using SB = Stager32<BN, B_KC>;
+    constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wave
+    constexpr int kA = A_KC ? BM * kLd32 : kBK32 * (BM + 4);
+    constexpr int kB = B_KC ? BN * kLd32 : kBK32 * (BN + 4);
     __shared__ __attribute__((aligned(16))) float lds_a[2 * kA];
     __shared__ __attribute__((aligned(16))) float lds_b[2 * kB];
-    const uint32_t tiles_m = (M + kBM - 1) / kBM;
-    const uint32_t tiles_n = (N + kBN - 1) / kBN;
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
     uint32_t tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const uint32_t m0 = tm * kBM, n0 = tn * kBN;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
     const int t = threadIdx.x;
     const int lane = t % 64;
     const int wave = t / 64;
@@ -409,11 +412,11 @@ __global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __rest
     sb.init(B, n0, N, B_KC ? K : N, K, t);
     uint4 stage_a[SA::kPasses], stage_b[SB::kPasses];
 
-    f32x4 acc[8][4];
+    f32x4 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{};
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x4{};
 
     const uint32_t steps = (K + kBK32 - 1) / kBK32;
     if (steps > 0) {
@@ -436,17 +439,17 @@ __global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __rest
         const float* lb = lds_b + buffer * kB;
 #pragma unroll
         for (int kk = 0; kk < kBK32; kk += 16) {
-            f32x4 a[8], b[4];
+            f32x4 a[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < 8; i++) a[i] = sa.fragment(la, wm * 128 + i * 16 + row_in, kk, lane);
+            for (int i = 0; i < TM; i++) a[i] = sa.fragment(la, wm * (BM / 2) + i * 16 + row_in, kk, lane);
 #pragma unroll
-            for (int j = 0; j < 4; j++) b[j] = sb.fragment(lb, wn * 64 + j * 16 + row_in, kk, lane);
+            for (int j = 0; j < TN; j++) b[j] = sb.fragment(lb, wn * (BN / 2) + j * 16 + row_in, kk, lane);
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
-                for (int i = 0; i < 8; i++)
+                for (int i = 0; i < TM; i++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
+                    for (int j = 0; j < TN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
         }
         if (more) {
@@ -457,13 +460,13 @@ __global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __rest
     }
 
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < TM; i++) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t col = n0 + wn * 64 + j * 16 + lane % 16;
+        for (int j = 0; j < TN; j++) {
+            const uint32_t col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const uint32_t row = m0 + wm * 128 + i * 16 + 4 * (lane / 16) + e;
+                const uint32_t row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + e;
                 if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
             }
         }
@@ -769,6 +772,82 @@ void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32
     }
 }
 
+// The in-place f32 kernel's shapes: 256 x 128 tiles, or 128 x 128 when the
+// larger ones would leave CUs without a tile (a 4096 x 1024 product has 128
+// of them on 256 CUs).
+template <typename O, bool A_KC, bool B_KC>
+void launch_inplace32(const float* a, const float* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
+                      hipStream_t s) {
+    const uint32_t large = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
+    if (large >= static_cast<uint32_t>(compute_units())) {
+        inplace32_kernel<O, A_KC, B_KC, kBM, kBN><<<large, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate);
+    } else {
+        const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);
+        inplace32_kernel<O, A_KC, B_KC, 128, 128><<<small, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate);
+    }
+}
+
+// ---- products over a short K -----------------------------------------------------------
+//
+// A product with K below 8 (an outer product, K = 1, is how the tape
+// broadcasts a bias: `outer`, tape/mod.rs:1000-1006) does too little
+// arithmetic for the matrix cores and is bound by writing C.  Each thread
+// forms four neighbouring outputs of one row with an FMA chain over k, in
+// k order, and stores them as one 16-byte word where the row allows.  For
+// K = 1 the result is the single rounding of a·b, the host's own.
+template <typename S, typename O, bool A_KC, bool B_KC, bool VEC>
+__global__ void __launch_bounds__(256) short_k_kernel(const S* __restrict__ A, const S* __restrict__ B,
+                                                      O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                                                      bool accumulate) {
+    using EA = Elem<S>;
+    const uint32_t groups = (N + 3) / 4;
+    const uint64_t items = static_cast<uint64_t>(M) * groups;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t item = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; item < items;
+         item += stride) {
+        const uint32_t row = static_cast<uint32_t>(item / groups);
+        const uint32_t col = static_cast<uint32_t>(item - static_cast<uint64_t>(row) * groups) * 4;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t k = 0; k < K; k++) {
+            const float a = EA::widen(A_KC ? A[static_cast<uint64_t>(row) * K + k] : A[static_cast<uint64_t>(k) * M + row]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (VEC || col + e < N) {
+                    const uint32_t j = col + e;
+                    const float b = EA::widen(B_KC ? B[static_cast<uint64_t>(j) * K + k] : B[static_cast<uint64_t>(k) * N + j]);
+                    acc[e] = fmaf(a, b, acc[e]);
+                }
+            }
+        }
+        const uint64_t at = static_cast<uint64_t>(row) * N + col;
+        if constexpr (VEC) {
+            float4* to = reinterpret_cast<float4*>(C + at);
+            if (accumulate) {
+                const float4 c = *to;
+                acc[0] += c.x, acc[1] += c.y, acc[2] += c.z, acc[3] += c.w;
+            }
+            *to = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (col + e < N) store_out(C, at + e, acc[e], accumulate);
+            }
+        }
+    }
+}
+
+template <typename S, typename O, bool A_KC, bool B_KC>
+int launch_short_k(const S* a, const S* b, O* c, uint64_t m, uint64_t k, uint64_t n, bool accumulate, hipStream_t s) {
+    const uint32_t m32 = static_cast<uint32_t>(m), k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
+    const uint32_t blocks = blocks_for(m * ((n + 3) / 4), 1);
+    if (std::is_same<O, float>::value && n % 4 == 0 && aligned16(c)) {
+        short_k_kernel<S, O, A_KC, B_KC, true><<<blocks, 256, 0, s>>>(a, b, c, m32, n32, k32, accumulate);
+    } else {
+        short_k_kernel<S, O, A_KC, B_KC, false><<<blocks, 256, 0, s>>>(a, b, c, m32, n32, k32, accumulate);
+    }
+    return check_launch("matmul");
+}
+
 // ---- host side ---------------------------------------------------------------------
 
 // A K-contiguous copy of an operand stored the other way round, in a block
@@ -809,6 +888,12 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
     }
     const S* pa = static_cast<const S*>(a);
     const S* pb = static_cast<const S*>(b);
+    if (k < 8) {
+        O* pc = static_cast<O*>(c);
+        if (transposed == TC_PLAIN) return launch_short_k<S, O, true, false>(pa, pb, pc, m, k, n, accumulate, s);
+        if (transposed == TC_LEFT) return launch_short_k<S, O, false, false>(pa, pb, pc, m, k, n, accumulate, s);
+        return launch_short_k<S, O, true, true>(pa, pb, pc, m, k, n, accumulate, s);
+    }
     if constexpr (std::is_same<S, float>::value) {
         // f32 operands read in place whenever their rows are 16-byte aligned
         // and they stay under the buffer offsets' 2^31 bytes.
@@ -817,16 +902,15 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
         const bool in_place = aligned16(a) && aligned16(b) && (a_kc ? k % 4 == 0 : m % 4 == 0) &&
                               (b_kc ? k % 4 == 0 : n % 4 == 0) && m * k * 4 < limit && k * n * 4 < limit;
         if (in_place) {
-            const uint32_t tiles = static_cast<uint32_t>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
             const uint32_t m32 = static_cast<uint32_t>(m), k32 = static_cast<uint32_t>(k),
                            n32 = static_cast<uint32_t>(n);
             O* pc = static_cast<O*>(c);
             if (a_kc && b_kc) {
-                inplace32_kernel<O, true, true><<<tiles, kThreads, 0, s>>>(pa, pb, pc, m32, n32, k32, accumulate);
+                launch_inplace32<O, true, true>(pa, pb, pc, m32, k32, n32, accumulate, s);
             } else if (a_kc) {
-                inplace32_kernel<O, true, false><<<tiles, kThreads, 0, s>>>(pa, pb, pc, m32, n32, k32, accumulate);
+                launch_inplace32<O, true, false>(pa, pb, pc, m32, k32, n32, accumulate, s);
             } else {
-                inplace32_kernel<O, false, false><<<tiles, kThreads, 0, s>>>(pa, pb, pc, m32, n32, k32, accumulate);
+                launch_inplace32<O, false, false>(pa, pb, pc, m32, k32, n32, accumulate, s);
             }
             return check_launch("matmul");
         }

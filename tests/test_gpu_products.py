@@ -81,6 +81,33 @@ def test_transposed_products_accumulate(kind, m, k, n):
     assert error(got, widen(kind, a), widen(kind, b), widen(kind, want)) <= tol * 2
 
 
+@pytest.mark.parametrize("kind", [lib.F32, lib.BF16])
+@pytest.mark.parametrize("m,k,n", [(300, 1, 1024), (257, 1, 33), (64, 3, 130), (129, 7, 64)])
+def test_short_inner_dimensions(kind, m, k, n):
+    # K below 8 takes the write-bound kernel (K = 1 is the tape's bias
+    # broadcast, `outer`, tape/mod.rs:1000-1006), in every form and with an
+    # addend.  An outer product is each a_i b_j rounded once, as the host
+    # forms it: bit-exact.
+    rng = np.random.default_rng(m + k + n)
+    a = to_kind(rng.uniform(-1, 1, (m, k)), kind)
+    b = to_kind(rng.uniform(-1, 1, (k, n)), kind)
+    c = to_kind(rng.uniform(-1, 1, (m, n)), kind)
+    wa, wb = widen(kind, a), widen(kind, b)
+    tol = tolerance(kind, kind, k) + (2.0 ** -8 if kind == lib.BF16 else 0)
+    exact = wa.astype(np.float64) @ wb.astype(np.float64)
+    forms = [(lib.PLAIN, a, b), (lib.LEFT, np.ascontiguousarray(a.T), b), (lib.RIGHT, a, np.ascontiguousarray(b.T))]
+    for form, x, y in forms:
+        got = widen(kind, product(kind, kind, form, x, y, m, k, n))
+        if k == 1:
+            want = to_kind(wa.astype(np.float32) * wb.astype(np.float32), kind)
+            assert np.array_equal(got, widen(kind, want)), form
+        assert error(got, wa, wb, exact) <= tol, form
+        got = widen(kind, product(kind, kind, form, x, y, m, k, n, addend=c))
+        wc = widen(kind, c).astype(np.float64)
+        scale = np.abs(wa.astype(np.float64)) @ np.abs(wb.astype(np.float64)) + np.abs(wc)
+        assert np.max(np.abs(got - (exact + wc)) / scale) <= tol * 2, form
+
+
 def test_an_empty_inner_dimension_gives_zeros_or_the_addend():
     # ops.rs:163-168, tests/backend.rs:259-266.
     a = np.zeros((3, 0), np.float32)
