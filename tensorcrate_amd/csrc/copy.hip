@@ -9,9 +9,10 @@
 //    copied with 16-byte vector accesses when both runs are 16-byte aligned,
 //    which covers contiguous copies, slices and concatenation.
 //  - tile: one side is contiguous along an axis the other is not (a permute
-//    such as a transpose).  A 64 x 64 tile is read along the source's
-//    contiguous axis, held in LDS, and written along the target's, so both
-//    HBM streams are coalesced.
+//    such as a transpose).  A tile is read along the source's contiguous
+//    axis, held in LDS, and written along the target's, so both HBM streams
+//    are coalesced: 128 x 64 four-byte elements moved 16 bytes a lane, in
+//    diagonal block order, or 64 x 64 of any other width.
 //  - gather: anything else (broadcasts along inner axes, general strides),
 //    one element per thread with the coordinates recovered by multiply-shift
 //    division.
@@ -181,22 +182,30 @@ __global__ void __launch_bounds__(256) tile_kernel(const T* __restrict__ src, T*
 }
 
 // The same transpose for 4-byte elements moving 16 bytes a lane on both
-// sides: a lane reads four elements along `a` and, after the LDS exchange,
-// writes four along `b`.  The 65-word row pitch keeps both the row writes and
-// the column reads of a wave on 64 distinct banks.  Needs every extent,
-// offset and stride that steps along a vector to be a multiple of 4, which
-// the host checks; NT marks a transpose that streams past the Infinity Cache.
-template <typename I, bool NT>
+// sides, over TA x TB tiles (TA along `a`, TB along `b`): a lane reads four
+// elements along `a` and, after the LDS exchange, writes four along `b`.  The
+// odd row pitch (TA + 1 words) keeps the column reads of the write phase on
+// distinct banks.  Needs every extent, offset and stride that steps along a
+// vector to be a multiple of 4, which the host checks; NT marks a transpose
+// that streams past the Infinity Cache.
+template <typename I, bool NT, int TA, int TB>
 __global__ void __launch_bounds__(256) tile4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
                                                     TileLayout<I> t) {
-    __shared__ uint32_t tile[kTile][kTile + 1];
-    const int quad = threadIdx.x % 16;  // which four elements of a 64-element row
-    const int row = threadIdx.x / 16;   // 16 rows a pass, four passes
+    constexpr int kReadQuads = TA / 4, kReadRows = 256 / kReadQuads;
+    constexpr int kWriteQuads = TB / 4, kWriteRows = 256 / kWriteQuads;
+    __shared__ uint32_t tile[TB][TA + 1];
     I block = blockIdx.x;
     I rest = t.tiles_a_div.div(block);
     const I tile_a = block - rest * t.tiles_a;
     I batch = t.tiles_b_div.div(rest);
-    const I tile_b = rest - batch * t.tiles_b;
+    I tile_b = rest - batch * t.tiles_b;
+    // Diagonal order: the blocks running together (neighbouring tile_a)
+    // take different tile_b, so their writes land in different columns
+    // rather than all in the same few (long target rows would otherwise put
+    // them on the same HBM channels: an 8192 x 8192 transpose runs at 3.9
+    // TB/s without this, 5.8 with it).
+    tile_b += tile_a - t.tiles_b_div.div(tile_a) * t.tiles_b;
+    if (tile_b >= t.tiles_b) tile_b -= t.tiles_b;
     I from = 0, to = 0;
     for (int k = t.batch_rank - 1; k > 0; k--) {
         I q = t.batch_div[k].div(batch);
@@ -209,26 +218,34 @@ __global__ void __launch_bounds__(256) tile4_kernel(const uint32_t* __restrict__
         from += batch * t.batch_src[0];
         to += batch * t.batch_dst[0];
     }
-    const I a0 = tile_a * kTile, b0 = tile_b * kTile;
-    const I a = a0 + quad * 4;
+    const I a0 = tile_a * TA, b0 = tile_b * TB;
+    {
+        const int quad = threadIdx.x % kReadQuads, row = threadIdx.x / kReadQuads;
+        const I a = a0 + quad * 4;
+        uint4 v[TB / kReadRows];
 #pragma unroll
-    for (int pass = 0; pass < kTile / 16; pass++) {
-        const I b = b0 + row + pass * 16;
-        if (a < t.extent_a && b < t.extent_b) {
-            const uint4 v = load_word<NT>(src + from + a + b * t.src_b);
-            uint32_t* at = &tile[row + pass * 16][quad * 4];
-            at[0] = v.x, at[1] = v.y, at[2] = v.z, at[3] = v.w;
+        for (int pass = 0; pass < TB / kReadRows; pass++) {
+            const I b = b0 + row + pass * kReadRows;
+            if (a < t.extent_a && b < t.extent_b) v[pass] = load_word<NT>(src + from + a + b * t.src_b);
+        }
+#pragma unroll
+        for (int pass = 0; pass < TB / kReadRows; pass++) {
+            uint32_t* at = &tile[row + pass * kReadRows][quad * 4];
+            at[0] = v[pass].x, at[1] = v[pass].y, at[2] = v[pass].z, at[3] = v[pass].w;
         }
     }
     __syncthreads();
-    const I b = b0 + quad * 4;
+    {
+        const int quad = threadIdx.x % kWriteQuads, row = threadIdx.x / kWriteQuads;
+        const I b = b0 + quad * 4;
 #pragma unroll
-    for (int pass = 0; pass < kTile / 16; pass++) {
-        const I aa = a0 + row + pass * 16;
-        if (aa < t.extent_a && b < t.extent_b) {
-            const int c = row + pass * 16;
-            const uint4 v{tile[quad * 4][c], tile[quad * 4 + 1][c], tile[quad * 4 + 2][c], tile[quad * 4 + 3][c]};
-            store_word<NT>(dst + to + b + aa * t.dst_a, v);
+        for (int pass = 0; pass < TA / kWriteRows; pass++) {
+            const I aa = a0 + row + pass * kWriteRows;
+            if (aa < t.extent_a && b < t.extent_b) {
+                const int c = row + pass * kWriteRows;
+                const uint4 v{tile[quad * 4][c], tile[quad * 4 + 1][c], tile[quad * 4 + 2][c], tile[quad * 4 + 3][c]};
+                store_word<NT>(dst + to + b + aa * t.dst_a, v);
+            }
         }
     }
 }
@@ -305,12 +322,6 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
         t.extent_b = static_cast<I>(walk.shape[axis_b]);
         t.src_b = static_cast<I>(walk.strides[0][axis_b]);
         t.dst_a = static_cast<I>(walk.strides[1][axis_a]);
-        const uint64_t tiles_a = (walk.shape[axis_a] + kTile - 1) / kTile;
-        const uint64_t tiles_b = (walk.shape[axis_b] + kTile - 1) / kTile;
-        t.tiles_a = static_cast<I>(tiles_a);
-        t.tiles_b = static_cast<I>(tiles_b);
-        t.tiles_a_div.set(tiles_a);
-        t.tiles_b_div.set(tiles_b);
         uint64_t batches = 1;
         for (int k = 0; k < rank; k++) {
             if (k == axis_a || k == axis_b) continue;
@@ -321,10 +332,24 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
             t.batch_rank++;
             batches *= walk.shape[k];
         }
-        const uint64_t blocks = tiles_a * tiles_b * batches;
+        // Tiles of `ta` x `tb`; the number of blocks that covers them.
+        auto tiled = [&](uint64_t ta, uint64_t tb) {
+            const uint64_t tiles_a = (walk.shape[axis_a] + ta - 1) / ta;
+            const uint64_t tiles_b = (walk.shape[axis_b] + tb - 1) / tb;
+            t.tiles_a = static_cast<I>(tiles_a);
+            t.tiles_b = static_cast<I>(tiles_b);
+            t.tiles_a_div.set(tiles_a);
+            t.tiles_b_div.set(tiles_b);
+            return tiles_a * tiles_b * batches;
+        };
         // Four-byte elements whose rows start on 16-byte boundaries move 16
         // bytes a lane, one tile a block (so at most 2^24 - 1 tiles, the
         // work-items one dispatch holds).
+        // 128 x 64 tiles: 512-byte reads and 256-byte writes per row, the
+        // best of the shapes measured on the config-3 permute, an 8192^2
+        // transpose and a [64, 1024, 1024] batch.
+        constexpr int TA = 128, TB = 64;
+        uint64_t blocks = tiled(TA, TB);
         bool wide = sizeof(T) == 4 && blocks <= 0xffffffu && walk.shape[axis_a] % 4 == 0 &&
                     walk.shape[axis_b] % 4 == 0 && walk.strides[0][axis_b] % 4 == 0 &&
                     walk.strides[1][axis_a] % 4 == 0 && aligned16(src) && aligned16(dst);
@@ -333,12 +358,13 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
             const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
             uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
             if (stream) {
-                tile4_kernel<I, true><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
+                tile4_kernel<I, true, TA, TB><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
             } else {
-                tile4_kernel<I, false><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
+                tile4_kernel<I, false, TA, TB><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
             }
             return check_launch("strided copy");
         }
+        blocks = tiled(kTile, kTile);
         tile_kernel<T, I><<<grid_for(blocks, 1, 64), 256, 0, s>>>(src, dst, t, static_cast<I>(blocks));
         return check_launch("strided copy");
     }
