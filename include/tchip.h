@@ -75,6 +75,9 @@ typedef enum tc_pairwise { TC_PAIR_ARITHMETIC = 0, TC_PAIR_COMPARE = 1, TC_PAIR_
  * `Variance { divisor }`. */
 typedef enum tc_axis_reduction { TC_AXIS_FOLD = 0, TC_AXIS_MEAN = 1, TC_AXIS_VARIANCE = 2 } tc_axis_reduction;
 
+/* `Axis` (tensors/kernels.rs:482-487): fold each row, or each column. */
+typedef enum tc_axis { TC_AXIS_ROWS = 0, TC_AXIS_COLUMNS = 1 } tc_axis;
+
 /* `Transposed` (tensors/kernels.rs:462-467), with `TC_PLAIN` for neither. */
 typedef enum tc_transposed { TC_PLAIN = 0, TC_LEFT = 1, TC_RIGHT = 2 } tc_transposed;
 
@@ -300,6 +303,36 @@ int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_pl
              uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
              uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
              uint32_t output_count, uint64_t rows, uint64_t cols);
+
+/* `Kernels::row_moments` (kernels.rs:1090-1097; Host `host_row_moments`,
+ * fused/mod.rs:4030-4041, and `moments_of`, statistics/mod.rs:419-441): the
+ * rows x cols matrix `place` reads of `input` (stored as `input_dtype`,
+ * `input_len` elements), converted to `dtype`, and per row its mean into
+ * `means[rows]` and its sum of squared deviations from that mean into
+ * `deviations[rows]`, accumulated in f32 and rounded to `dtype` once.  A
+ * matrix with no columns gives NaNs. */
+int tc_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, uint64_t input_len,
+                   const tc_place* place, uint64_t rows, uint64_t cols, void* means, void* deviations);
+
+/* `Kernels::fused_sum` (kernels.rs:1120-1135; `Program::run_sum`,
+ * fused/mod.rs:1048-1082; `axis_sum`, :4045-4051): run a program whose one
+ * output is of type `dtype` (every store to output 0 as `dtype`) over a
+ * rows x cols space, as `tc_fused` does, and sum that output along `axis`
+ * (a `tc_axis`) into `out`: `rows` sums of rows, or `cols` sums of columns,
+ * accumulated in f32 and rounded once.  The output itself is not returned. */
+int tc_fused_sum(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                 uint32_t place_count, const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
+                 uint64_t rows, uint64_t cols, uint32_t axis, void* out);
+
+/* `Kernels::matmul_epilogue` (kernels.rs:1142-1149; Host `host_matmul`,
+ * fused/mod.rs:4754-4766; checks in `Program::run_matmul`, :1143-1200): the
+ * product A[m x k] . B[k x n] (row-major, `dtype`, as `tc_matmul` forms it)
+ * is the program's input 0, read unremapped over the m x n space, and
+ * `inputs` fill slots 1 on; outputs as `tc_fused`. */
+int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                       uint32_t place_count, uint64_t m, uint64_t k, uint64_t n, const void* a, const void* b,
+                       const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
+                       void* const* outputs, const uint64_t* output_lens, uint32_t output_count);
 
 /* How many fused programs this process has compiled into kernels of their
  * own.  A dense program (every load in element order, every load before any

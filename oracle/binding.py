@@ -56,6 +56,9 @@ _SIGNATURES = {
     "or_vecmat": ([u32, vp, vp, u64, u64, vp], None),
     "or_fold": ([u32, vp, u64, u32], f32),
     "or_fused": ([u32, vp, u32, vp, vp, vp, u64, u64], None),
+    "or_row_moments": ([u32, u32, vp, vp, u64, u64, vp, vp], None),
+    "or_fused_sum": ([u32, vp, u32, vp, vp, u64, u64, u32, vp], None),
+    "or_matmul_epilogue": ([u32, vp, u32, vp, vp, vp, u64, u64, u64, vp, u32, vp], None),
 }
 
 _lib = None
@@ -231,15 +234,49 @@ def fold(dtype, a, op) -> float:
     return load().or_fold(dtype, _p(a), a.size, op)
 
 
-def fused(dtype, code, places, inputs, outputs, rows, cols) -> None:
-    """Run an encoded program; ``code`` is a list of (kind, op, dst, a, b, aux,
-    value) and ``places`` of (offset, col_step, lead, dims, steps)."""
+def _program(code, places):
     enc = (Encoded * max(len(code), 1))(*[Encoded(*c) for c in code])
     pl = (Place * max(len(places), 1))()
     for k, (offset, col_step, lead, dims, steps) in enumerate(places):
         pl[k].offset, pl[k].col_step, pl[k].lead = offset, col_step, lead
         for d in range(len(dims)):
             pl[k].dims[d], pl[k].steps[d] = dims[d], steps[d]
+    return enc, pl
+
+
+def fused(dtype, code, places, inputs, outputs, rows, cols) -> None:
+    """Run an encoded program; ``code`` is a list of (kind, op, dst, a, b, aux,
+    value) and ``places`` of (offset, col_step, lead, dims, steps)."""
+    enc, pl = _program(code, places)
     ins = (vp * max(len(inputs), 1))(*[_p(x) for x in inputs])
     outs = (vp * max(len(outputs), 1))(*[_p(x) for x in outputs])
     load().or_fused(dtype, enc, len(code), pl, ins, outs, rows, cols)
+
+
+def row_moments(dtype, input_dtype, values, place, rows, cols):
+    """Each row's (mean, sum of squared deviations) of the matrix ``place``
+    reads, as arrays of ``dtype``'s storage type."""
+    values = np.ascontiguousarray(values)
+    _, pl = _program([], [place])
+    means = np.zeros(max(rows, 1), NUMPY[dtype])[:rows]
+    devs = np.zeros(max(rows, 1), NUMPY[dtype])[:rows]
+    load().or_row_moments(dtype, input_dtype, _p(values), pl, rows, cols, _p(means), _p(devs))
+    return means, devs
+
+
+def fused_sum(dtype, code, places, inputs, rows, cols, axis) -> np.ndarray:
+    """The program's one output summed along ``axis`` (0 rows, 1 columns)."""
+    enc, pl = _program(code, places)
+    ins = (vp * max(len(inputs), 1))(*[_p(x) for x in inputs])
+    out = np.zeros(max(rows if axis == 0 else cols, 1), NUMPY[dtype])[:rows if axis == 0 else cols]
+    load().or_fused_sum(dtype, enc, len(code), pl, ins, rows, cols, axis, _p(out))
+    return out
+
+
+def matmul_epilogue(dtype, code, places, a, b, m, k, n, inputs, outputs) -> None:
+    """The product ``a @ b`` as the program's input 0, ``inputs`` from slot 1."""
+    enc, pl = _program(code, places)
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    ins = (vp * max(len(inputs), 1))(*[_p(x) for x in inputs])
+    outs = (vp * max(len(outputs), 1))(*[_p(x) for x in outputs])
+    load().or_matmul_epilogue(dtype, enc, len(code), pl, _p(a), _p(b), m, k, n, ins, len(inputs), outs)

@@ -769,3 +769,62 @@ void or_fused(uint32_t dtype, const or_encoded* code, uint32_t count, const or_p
         }
     }
 }
+
+/* ---- the composed Kernels members (kernels.rs:1090-1149) ------------------- */
+
+static size_t elem_bytes(uint32_t dtype) { return dtype == F32 ? 4 : 2; }
+
+void or_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, const or_place* place, uint64_t rows,
+                    uint64_t cols, void* means, void* deviations) {
+    float* row = (float*)malloc((cols ? cols : 1) * sizeof(float));
+    for (uint64_t r = 0; r < rows; r++) {
+        if (cols == 0) {
+            narrow_one(dtype, means, r, NAN);
+            narrow_one(dtype, deviations, r, NAN);
+            continue;
+        }
+        for (uint64_t c = 0; c < cols; c++) row[c] = in_type(dtype, widen_one(input_dtype, input, place_at(place, r, c)));
+        float total = 0.0f;
+        for (uint64_t c = 0; c < cols; c++) total = total + row[c];
+        const float mean = total / (float)cols;
+        float squares = 0.0f;
+        for (uint64_t c = 0; c < cols; c++) {
+            const float d = row[c] - mean;
+            squares = squares + d * d;
+        }
+        narrow_one(dtype, means, r, mean);
+        narrow_one(dtype, deviations, r, squares);
+    }
+    free(row);
+}
+
+void or_fused_sum(uint32_t dtype, const or_encoded* code, uint32_t count, const or_place* places,
+                  const void* const* inputs, uint64_t rows, uint64_t cols, uint32_t axis, void* out) {
+    const uint64_t n = rows * cols;
+    void* data = malloc((n ? n : 1) * elem_bytes(dtype));
+    void* outputs[1] = {data};
+    or_fused(dtype, code, count, places, inputs, outputs, rows, cols);
+    const uint64_t len = axis == 0 ? cols : rows;
+    void* ones = malloc((len ? len : 1) * elem_bytes(dtype));
+    for (uint64_t i = 0; i < len; i++) narrow_one(dtype, ones, i, 1.0f);
+    if (axis == 0) {
+        or_matvec(dtype, data, ones, rows, cols, out, 0);
+    } else {
+        or_vecmat(dtype, ones, data, rows, cols, out);
+    }
+    free(ones);
+    free(data);
+}
+
+void or_matmul_epilogue(uint32_t dtype, const or_encoded* code, uint32_t count, const or_place* places,
+                        const void* a, const void* b, uint64_t m, uint64_t k, uint64_t n, const void* const* inputs,
+                        uint32_t input_count, void* const* outputs) {
+    void* product = malloc((m * n > 0 ? m * n : 1) * elem_bytes(dtype));
+    or_matmul(dtype, dtype, a, b, m, k, n, product, 0);
+    const void** all = (const void**)malloc((input_count + 1) * sizeof(void*));
+    all[0] = product;
+    for (uint32_t s = 0; s < input_count; s++) all[s + 1] = inputs[s];
+    or_fused(dtype, code, count, places, all, outputs, m, n);
+    free(all);
+    free(product);
+}

@@ -117,6 +117,27 @@ typedef struct or_place {
 void or_fused(uint32_t dtype, const or_encoded* code, uint32_t count, const or_place* places,
               const void* const* inputs, void* const* outputs, uint64_t rows, uint64_t cols);
 
+/* `Kernels::row_moments` on the Host (`host_row_moments`, fused/mod.rs:
+ * 4030-4041): the rows x cols matrix `place` reads of `input`, converted to
+ * dtype (`input_matrix`, :3984-3991), and per row `moments_of`
+ * (statistics/mod.rs:419-441): mean = sum / n, then the sum of squared
+ * deviations from it, both sequential f32 folds (the compact types widen to
+ * f32 and round the two results once); NaNs for an empty row. */
+void or_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, const or_place* place, uint64_t rows,
+                    uint64_t cols, void* means, void* deviations);
+
+/* `Kernels::fused_sum`'s default (kernels.rs:1120-1135): the program's one
+ * output, then `axis_sum` (fused/mod.rs:4045-4051), its products with ones:
+ * axis 0 (Rows) a matvec, axis 1 (Columns) a vecmat. */
+void or_fused_sum(uint32_t dtype, const or_encoded* code, uint32_t count, const or_place* places,
+                  const void* const* inputs, uint64_t rows, uint64_t cols, uint32_t axis, void* out);
+
+/* `host_matmul` (fused/mod.rs:4754-4766): the product, then the interpreter
+ * with it as input 0 and `inputs` (count `input_count`) from slot 1. */
+void or_matmul_epilogue(uint32_t dtype, const or_encoded* code, uint32_t count, const or_place* places,
+                        const void* a, const void* b, uint64_t m, uint64_t k, uint64_t n, const void* const* inputs,
+                        uint32_t input_count, void* const* outputs);
+
 #ifdef __cplusplus
 }
 #endif

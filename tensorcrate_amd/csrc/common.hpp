@@ -45,6 +45,12 @@ int check_launch(const char* what);
 // Number of compute units, for sizing persistent and split grids.
 int compute_units();
 
+// Each slice's mean into `means` and its sum of squared deviations into
+// `deviations`, both of `dtype`, in one pass (reduce.hip; the moments
+// `row_moments` returns).
+int reduce_moments(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split, void* means,
+                   void* deviations);
+
 
 std::string shape_text(const uint64_t* values, uint32_t rank);
 

@@ -505,9 +505,10 @@ __device__ __forceinline__ short4v read_tr16(const void* lds_addr) {
 }
 
 // The order the scheduler is asked to keep within one step: F matrix-core
-// steps per slice, each followed by its share of the next step's HBM loads
-// (first slice), of the next slice's LDS reads (all but the last) or of the
-// staged step's LDS writes (last slice).
+// steps per slice, each followed by its share of the step's HBM loads (first
+// slice) and of the next slice's LDS reads (every slice but the last, whose
+// reads the scheduler places itself; interleaving those too measured no
+// faster).
 template <int F, int LOADS, int READS, int SLICES, int Q = 0, int R = 0>
 __device__ __forceinline__ void weave() {
     if constexpr (Q < SLICES) {
@@ -516,7 +517,6 @@ __device__ __forceinline__ void weave() {
         constexpr int reads = READS * (R + 1) / F - READS * R / F;
         if constexpr (Q == 0 && loads > 0) __builtin_amdgcn_sched_group_barrier(0x020, loads, 0);  // HBM loads
         if constexpr (Q + 1 < SLICES && reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);  // LDS reads
-        if constexpr (Q + 1 == SLICES && loads > 0) __builtin_amdgcn_sched_group_barrier(0x200, loads, 0);  // LDS writes
         if constexpr (R + 1 < F) {
             weave<F, LOADS, READS, SLICES, Q, R + 1>();
         } else {

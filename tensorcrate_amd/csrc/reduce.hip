@@ -146,11 +146,17 @@ struct ArgFold {
     }
 };
 
+// Beside the public `tc_axis_reduction`s: a variance's two moments, the
+// mean to `out` and the sum of squared deviations to `Finish::second`
+// (`row_moments`, kernels.rs:1090).
+constexpr uint32_t kAxisMoments = 3;
+
 // What a finished slice writes.
 struct Finish {
-    uint32_t kind;     // tc_axis_reduction
+    uint32_t kind;     // tc_axis_reduction, or kAxisMoments
     float depth;       // the mean's count
     float divisor;     // the variance's divisor
+    void* second;      // kAxisMoments: where the deviation sums go
 };
 
 template <typename S>
@@ -174,7 +180,12 @@ template <>
 struct Finisher<Var> {
     template <typename S>
     __device__ static void write(const Moments& s, const Finish& f, S* out, uint64_t at) {
-        write_result(out, at, s.m2 / f.divisor);
+        if (f.kind == kAxisMoments) {
+            write_result(out, at, s.mean);
+            write_result(static_cast<S*>(f.second), at, s.m2);
+        } else {
+            write_result(out, at, s.m2 / f.divisor);
+        }
     }
 };
 template <uint32_t OP>
@@ -671,12 +682,21 @@ int check_split(const tc_split* split, uint64_t input_len, const char* what, Pla
 }
 
 template <typename S>
+int moments_typed(const void* input, uint64_t input_len, const tc_split* split, void* means, void* deviations) {
+    Plan plan;
+    int status = check_split(split, input_len, "row_moments", &plan);
+    if (status != TC_OK) return status;
+    Finish f{kAxisMoments, static_cast<float>(plan.depth), 1.0f, deviations};
+    return reduce_typed<S, Var, S>(input, means, split->offset, plan, f, input_len, "row_moments");
+}
+
+template <typename S>
 int reduce_axes_typed(const void* input, uint64_t input_len, const tc_split* split, uint32_t kind,
                       uint32_t op, uint64_t divisor, void* out) {
     Plan plan;
     int status = check_split(split, input_len, "reduce_axes", &plan);
     if (status != TC_OK) return status;
-    Finish f{kind, static_cast<float>(plan.depth), static_cast<float>(divisor)};
+    Finish f{kind, static_cast<float>(plan.depth), static_cast<float>(divisor), nullptr};
     const char* what = "reduce_axes";
     if (kind == TC_AXIS_VARIANCE) {
         return reduce_typed<S, Var, S>(input, out, split->offset, plan, f, input_len, what);
@@ -713,7 +733,7 @@ int arg_reduce_typed(const void* input, uint64_t input_len, const tc_split* spli
     Plan plan;
     int status = check_split(split, input_len, what, &plan);
     if (status != TC_OK) return status;
-    Finish f{TC_AXIS_FOLD, 0.0f, 0.0f};
+    Finish f{TC_AXIS_FOLD, 0.0f, 0.0f, nullptr};
     switch (op) {
         case TC_REDUCE_MIN:
             return reduce_typed<S, ArgFold<TC_REDUCE_MIN>, uint32_t>(input, out, split->offset, plan, f, input_len, what);
@@ -779,6 +799,14 @@ int total(const void* a, const void* b, uint64_t n, float* result, const char* w
 }
 
 }  // namespace
+}  // namespace tc
+
+namespace tc {
+int reduce_moments(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split, void* means,
+                   void* deviations) {
+    TC_DISPATCH_FLOAT(dtype, "row_moments", S, return moments_typed<S>(input, input_len, split, means, deviations));
+    return TC_OK;
+}
 }  // namespace tc
 
 using namespace tc;

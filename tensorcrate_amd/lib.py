@@ -139,6 +139,12 @@ SIGNATURES = {
     "tc_fused": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, ctypes.POINTER(vp),
                  ctypes.POINTER(u64), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32, u64, u64],
     "tc_fused_compiled": [ctypes.POINTER(u64)],
+    "tc_row_moments": [u32, u32, vp, u64, ctypes.POINTER(Place), u64, u64, vp, vp],
+    "tc_fused_sum": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, ctypes.POINTER(vp),
+                     ctypes.POINTER(u64), u32, u64, u64, u32, vp],
+    "tc_matmul_epilogue": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, u64, u64, u64, vp, vp,
+                           ctypes.POINTER(vp), ctypes.POINTER(u64), u32, ctypes.POINTER(vp), ctypes.POINTER(u64),
+                           u32],
 }
 
 
@@ -247,22 +253,79 @@ def split(offset: int, kept, kept_strides, folded, folded_strides) -> Split:
     return s
 
 
-def fused(dtype: int, code, places, inputs, outputs, rows: int, cols: int) -> None:
-    """``tc_fused`` over Python lists: ``code`` of (kind, op, dst, a, b, aux,
-    value) tuples, ``places`` of (offset, col_step, lead, dims, steps), and
-    ``inputs``/``outputs`` of (Buffer, element count) pairs."""
+def _program(code, places):
     enc = (Encoded * max(len(code), 1))(*[Encoded(*c) for c in code])
     pl = (Place * max(len(places), 1))()
     for k, (offset, col_step, lead, dims_, steps) in enumerate(places):
         pl[k].offset, pl[k].col_step, pl[k].lead = offset, col_step, lead
         for d in range(len(dims_)):
             pl[k].dims[d], pl[k].steps[d] = dims_[d], steps[d]
-    ins = (vp * max(len(inputs), 1))(*[b.ptr for b, _ in inputs])
-    in_lens = (u64 * max(len(inputs), 1))(*[n for _, n in inputs])
-    outs = (vp * max(len(outputs), 1))(*[b.ptr for b, _ in outputs])
-    out_lens = (u64 * max(len(outputs), 1))(*[n for _, n in outputs])
+    return enc, pl
+
+
+def _buffers(pairs):
+    ptrs = (vp * max(len(pairs), 1))(*[b.ptr for b, _ in pairs])
+    lens = (u64 * max(len(pairs), 1))(*[n for _, n in pairs])
+    return ptrs, lens
+
+
+def fused(dtype: int, code, places, inputs, outputs, rows: int, cols: int) -> None:
+    """``tc_fused`` over Python lists: ``code`` of (kind, op, dst, a, b, aux,
+    value) tuples, ``places`` of (offset, col_step, lead, dims, steps), and
+    ``inputs``/``outputs`` of (Buffer, element count) pairs."""
+    enc, pl = _program(code, places)
+    ins, in_lens = _buffers(inputs)
+    outs, out_lens = _buffers(outputs)
     call("tc_fused", dtype, enc, len(code), pl, len(places), ins, in_lens, len(inputs), outs, out_lens, len(outputs),
          rows, cols)
+
+
+def row_moments(dtype: int, input_dtype: int, source, source_len: int, place, rows: int, cols: int,
+                means, deviations) -> None:
+    """``tc_row_moments``: ``source``, ``means`` and ``deviations`` are
+    Buffers; ``place`` is (offset, col_step, lead, dims, steps)."""
+    _, pl = _program([], [place])
+    call("tc_row_moments", dtype, input_dtype, source.ptr, source_len, pl, rows, cols, means.ptr, deviations.ptr)
+
+
+def fused_sum(dtype: int, code, places, inputs, rows: int, cols: int, axis: int, out) -> None:
+    """``tc_fused_sum`` into the Buffer ``out``."""
+    enc, pl = _program(code, places)
+    ins, in_lens = _buffers(inputs)
+    call("tc_fused_sum", dtype, enc, len(code), pl, len(places), ins, in_lens, len(inputs), rows, cols, axis,
+         out.ptr)
+
+
+def fused_with_statistics(dtype: int, code, places, inputs, outputs, rows: int, cols: int, statistics) -> None:
+    """``Kernels::fused_with_statistics`` as the trait's default composes it
+    (kernels.rs:1103-1113; ``row_statistics``, fused/mod.rs:3995-4027): each
+    input's row moments computed once by ``tc_row_moments``, the statistics
+    the program reads appended after ``inputs``, then ``tc_fused``.
+
+    ``statistics`` lists, in slot order, (source Buffer, element count,
+    storage dtype, place, "mean" | "deviations"); a source read through the
+    same place shares one computation of its moments."""
+    moments = {}
+    extra = []
+    for source, source_len, source_dtype, place, which in statistics:
+        key = (source.ptr, source_dtype, repr(place))
+        if key not in moments:
+            size = 4 if dtype == F32 else 2
+            means, deviations = Buffer(max(rows, 1) * size), Buffer(max(rows, 1) * size)
+            row_moments(dtype, source_dtype, source, source_len, place, rows, cols, means, deviations)
+            moments[key] = {"mean": means, "deviations": deviations}
+        extra.append((moments[key][which], rows))
+    fused(dtype, code, places, list(inputs) + extra, outputs, rows, cols)
+
+
+def matmul_epilogue(dtype: int, code, places, a, b, m: int, k: int, n: int, inputs, outputs) -> None:
+    """``tc_matmul_epilogue``: ``a``, ``b`` Buffers; ``inputs`` (slots 1 on)
+    and ``outputs`` (Buffer, element count) pairs."""
+    enc, pl = _program(code, places)
+    ins, in_lens = _buffers(inputs)
+    outs, out_lens = _buffers(outputs)
+    call("tc_matmul_epilogue", dtype, enc, len(code), pl, len(places), m, k, n, a.ptr, b.ptr, ins, in_lens,
+         len(inputs), outs, out_lens, len(outputs))
 
 
 def region(source: Buffer | int, source_len: int, shape, src_offset, src_strides, dst_offset,

@@ -117,3 +117,66 @@ class CapturedGraph:
     def close(self) -> None:
         self._hip.hipGraphExecDestroy(self._exec)
         self._hip.hipGraphDestroy(self._graph)
+
+
+class Code:
+    """A fused program's encoded instructions, (kind, op, dst, a, b, aux,
+    value) tuples in order (`Encoded`, fused/mod.rs:1391-1410); each value
+    takes a fresh register unless `dst` names one to reuse."""
+
+    def __init__(self):
+        self.code = []
+        self._next = 0
+
+    def _dst(self, dst):
+        if dst is None:
+            dst = self._next
+            self._next += 1
+        assert dst < 16, "the kernels hold 16 registers"
+        return dst
+
+    def load(self, place, slot, dtype, dst=None):
+        d = self._dst(dst)
+        self.code.append((0, place, d, slot, dtype, 0, 0.0))
+        return d
+
+    def const(self, value, dst=None):
+        d = self._dst(dst)
+        self.code.append((1, 0, d, 0, 0, 0, float(value)))
+        return d
+
+    def binary(self, op, a, b, dst=None):
+        d = self._dst(dst)
+        self.code.append((2, op, d, a, b, 0, 0.0))
+        return d
+
+    def unary(self, op, a, dst=None):
+        d = self._dst(dst)
+        self.code.append((3, op, d, a, 0, 0, 0.0))
+        return d
+
+    def compare(self, op, a, b, dst=None):
+        d = self._dst(dst)
+        self.code.append((4, op, d, a, b, 0, 0.0))
+        return d
+
+    def store(self, a, dtype, slot):
+        self.code.append((5, 0, 0, a, dtype, slot, 0.0))
+
+
+def identity_place(rows, cols):
+    """Element (row, col) of a row-major rows x cols operand."""
+    return (0, 1, 1, [rows], [cols])
+
+
+def row_broadcast(cols):
+    """A length-`cols` vector read by every row."""
+    return (0, 1, 0, [], [])
+
+
+def column_broadcast(rows):
+    """A length-`rows` vector, one value per row."""
+    return (0, 0, 1, [rows], [1])
+
+
+EXP, SQRT = 8, 13  # `Analytic` (kernels.rs:334-354)

@@ -1,0 +1,155 @@
+"""The composed `Kernels` members on the GPU — `tc_row_moments`,
+`tc_fused_sum`, `tc_matmul_epilogue`, and `fused_with_statistics` as the
+trait's default composes it (kernels.rs:1090-1149) — against the oracle on
+the same inputs, and against the reference's known answers.
+
+Tolerances: moments and sums fold in a different order from the host's
+left-to-right loop, so they are held to the accumulated-rounding bound
+(2^-24 sqrt(n) of the magnitudes summed, plus the output's rounding); the
+epilogue's product to the f32 product tolerance 1e-5 sqrt(K) of sum|a||b|,
+the program after it then being the same arithmetic."""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import binding as oracle
+from tensorcrate_amd import lib
+from tests.common import Lcg, identity_place, row_broadcast, to_kind, widen
+from tests.test_oracle_composed import PLACES, exp_program, layer_norm, oracle_at, relu_layer, statistic_operands
+
+pytestmark = pytest.mark.gpu
+
+UNIT = {lib.F32: 2.0 ** -24, lib.F16: 2.0 ** -11, lib.BF16: 2.0 ** -8}
+HOST = {lib.F32: np.float32, lib.F16: np.float16, lib.BF16: np.uint16}
+
+
+def device_moments(dtype, input_dtype, source, place, rows, cols):
+    buf = lib.Buffer.of(source)
+    size = 4 if dtype == lib.F32 else 2
+    means, devs = lib.Buffer(max(rows, 1) * size), lib.Buffer(max(rows, 1) * size)
+    lib.row_moments(dtype, input_dtype, buf, source.size, place, rows, cols, means, devs)
+    return means.download(HOST[dtype], rows), devs.download(HOST[dtype], rows)
+
+
+@pytest.mark.parametrize("name,make", PLACES)
+@pytest.mark.parametrize("dtype,input_dtype", [(lib.F32, lib.F32), (lib.F32, lib.F16), (lib.BF16, lib.F32),
+                                               (lib.F16, lib.F16), (lib.BF16, lib.BF16)])
+@pytest.mark.parametrize("rows,cols", [(6, 37), (130, 1000), (3, 1)])
+def test_row_moments_against_the_oracle(name, make, dtype, input_dtype, rows, cols):
+    place, length = make(rows, cols)
+    rng = np.random.default_rng(rows * cols + dtype * 7 + input_dtype)
+    source = to_kind(rng.uniform(-3, 3, length), input_dtype)
+    got_mean, got_dev = device_moments(dtype, input_dtype, source, place, rows, cols)
+    want_mean, want_dev = oracle.row_moments(dtype, input_dtype, source, place, rows, cols)
+    values = widen(input_dtype, source).astype(np.float64)
+    scale = np.array([max(abs(values[oracle_at(place, r, c)]) for c in range(cols)) for r in range(rows)])
+    gm, wm = widen(dtype, got_mean), widen(dtype, want_mean)
+    gd, wd = widen(dtype, got_dev), widen(dtype, want_dev)
+    root = np.sqrt(cols)
+    assert np.all(np.abs(gm - wm) <= 4 * root * 2.0 ** -24 * scale + 2 * UNIT[dtype] * np.abs(wm) + 1e-30), name
+    assert np.all(np.abs(gd - wd) <= 8 * cols * root * 2.0 ** -24 * scale ** 2 + 2 * UNIT[dtype] * wd + 1e-30), name
+
+
+def test_row_moments_of_empty_rows_are_nans():
+    got_mean, got_dev = device_moments(lib.F32, lib.F32, np.zeros(4, np.float32), identity_place(4, 0), 4, 0)
+    assert np.all(np.isnan(got_mean)) and np.all(np.isnan(got_dev))
+
+
+def device_fused_sum(dtype, code, places, inputs, rows, cols, axis):
+    bufs = [(lib.Buffer.of(x), x.size) for x in inputs]
+    n = rows if axis == 0 else cols
+    out = lib.Buffer(max(n, 1) * (4 if dtype == lib.F32 else 2))
+    lib.fused_sum(dtype, code, places, bufs, rows, cols, axis, out)
+    return out.download(HOST[dtype], n)
+
+
+def test_fused_sum_known_answer():
+    x = np.array([0.0, 0.0, 1.0, 0.0], np.float32)
+    sums = device_fused_sum(lib.F32, exp_program(), [identity_place(2, 2)], [x], 2, 2, 0)
+    assert sums[0] == 2.0
+    assert abs(sums[1] - (math.e + 1.0)) <= 2 * 2.0 ** -24 * (math.e + 1.0)
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (33, 70), (1024, 512), (5, 100000)])
+def test_fused_sum_against_the_oracle(axis, rows, cols):
+    rng = np.random.default_rng(rows + cols + axis)
+    x = rng.uniform(-1, 1, rows * cols).astype(np.float32)
+    got = device_fused_sum(lib.F32, exp_program(), [identity_place(rows, cols)], [x], rows, cols, axis)
+    want = oracle.fused_sum(lib.F32, exp_program(), [identity_place(rows, cols)], [x], rows, cols, axis)
+    depth = cols if axis == 0 else rows
+    magnitude = np.exp(x.reshape(rows, cols).astype(np.float64)).sum(1 - axis)
+    assert np.all(np.abs(got - want) <= 4 * np.sqrt(depth) * 2.0 ** -24 * magnitude + 2.0 ** -24 * magnitude)
+
+
+def test_fused_sum_over_empty_rows_is_zero():
+    got = device_fused_sum(lib.F32, exp_program(), [identity_place(3, 0)], [np.zeros(1, np.float32)], 3, 0, 0)
+    assert got.tolist() == [0.0, 0.0, 0.0]
+
+
+def device_epilogue(code, places, a, b, m, k, n, inputs):
+    da, db = lib.Buffer.of(a), lib.Buffer.of(b)
+    bufs = [(lib.Buffer.of(x), x.size) for x in inputs]
+    out = lib.Buffer(m * n * 4)
+    lib.matmul_epilogue(lib.F32, code, places, da, db, m, k, n, bufs, [(out, m * n)])
+    return out.download(np.float32, m * n)
+
+
+def test_matmul_epilogue_known_answer():
+    x = np.array([[1.0, 2.0], [3.0, 4.0]], np.float32)
+    w = np.array([[1.0, -1.0], [0.0, 1.0]], np.float32)
+    bias = np.array([0.5, -2.5], np.float32)
+    y = device_epilogue(relu_layer(), [identity_place(2, 2), row_broadcast(2)], x, w, 2, 2, 2, [bias])
+    assert y.reshape(2, 2).tolist() == [[1.5, 0.0], [3.5, 0.0]]
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 2), (16, 16, 16), (17, 33, 15), (65, 130, 67), (128, 7, 200),
+                                   (1024, 512, 768)])
+def test_matmul_epilogue_against_the_oracle(m, k, n):
+    # The shapes of tests/fused.rs:1466-1475, and one past every tile edge.
+    rng = Lcg(31 + m)
+    a = rng.uniform(-1.0, 1.0, m * k).astype(np.float32)
+    b = rng.uniform(-1.0, 1.0, k * n).astype(np.float32)
+    bias = rng.uniform(-1.0, 1.0, n).astype(np.float32)
+    places = [identity_place(m, n), row_broadcast(n)]
+    got = device_epilogue(relu_layer(), places, a, b, m, k, n, [bias])
+    want = np.zeros(m * n, np.float32)
+    oracle.matmul_epilogue(lib.F32, relu_layer(), places, a, b, m, k, n, [bias], [want])
+    scale = (np.abs(a.reshape(m, k).astype(np.float64)) @ np.abs(b.reshape(k, n))).reshape(-1) + np.abs(np.tile(bias, m))
+    assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(k) * scale)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (9, 31), (17, 64), (40, 1000), (300, 7), (4096, 1024)])
+def test_fused_with_statistics_against_the_oracle(rows, cols):
+    # The layer norm of tests/fused.rs:1855-1879 with its statistics from
+    # tc_row_moments (one computation per input), then tc_fused.
+    rng = Lcg(5150 + rows)
+    if rows * cols > 100000:
+        np_rng = np.random.default_rng(rows)
+        x = np_rng.uniform(-3, 3, rows * cols).astype(np.float32)
+        gamma = np_rng.uniform(0.5, 1.5, cols).astype(np.float32)
+        h = np_rng.uniform(-1, 1, rows * cols).astype(np.float16)
+        start = np_rng.uniform(-1, 1, rows * cols).astype(np.float32)
+    else:
+        x, gamma, h, start = statistic_operands(rng, rows, cols)
+    code, places = layer_norm(rows, cols)
+    whole = identity_place(rows, cols)
+    dx, dg, dh, dacc = (lib.Buffer.of(v) for v in (x, gamma, h, start))
+    normalized = lib.Buffer(rows * cols * 4)
+    lib.fused_with_statistics(lib.F32, code, places, [(dx, x.size), (dg, cols), (dh, h.size), (dacc, start.size)],
+                              [(dacc, start.size), (normalized, rows * cols)], rows, cols,
+                              [(dx, x.size, lib.F32, whole, "mean"), (dx, x.size, lib.F32, whole, "deviations"),
+                               (dh, h.size, lib.F16, whole, "mean")])
+    mean, devs = oracle.row_moments(lib.F32, lib.F32, x, whole, rows, cols)
+    other, _ = oracle.row_moments(lib.F32, lib.F16, h, whole, rows, cols)
+    acc = start.copy()
+    want = np.zeros(rows * cols, np.float32)
+    oracle.fused(lib.F32, code, places, [x, gamma, h, acc, mean, devs, other], [acc, want], rows, cols)
+    got = normalized.download(np.float32, rows * cols)
+    # Normalized values are O(1); the statistics' rounding moves them by a
+    # few units of the mean's and the deviation's last places.
+    tol = 64 * np.sqrt(cols) * 2.0 ** -24 * 4.0
+    assert np.max(np.abs(got - want)) <= tol
+    assert np.max(np.abs(dacc.download(np.float32, rows * cols) - acc)) <= 2 * tol
