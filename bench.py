@@ -266,7 +266,10 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
     lib.call("tc_fill", grads.ptr, n, 4, ctypes.byref(ctypes.c_float(0.25)))
     rule = Adam(1e-3)
     rule.update(params, grads, 1, n)
-    ms = timed(lambda: rule.update(params, grads, 1, n), steps, warmup)
+    # Graph-captured like the other bandwidth lines: each captured update
+    # keeps its own step's constants, and the replay times the kernels back
+    # to back rather than this script's per-step host work.
+    ms = timed_graph(lambda: rule.update(params, grads, 1, n), steps, warmup)
     lines.append(hbm_line(f"Adam update, {n} f32 parameters (fused program)", 7 * 4 * n, ms))
     return lines
 
