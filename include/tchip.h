@@ -235,6 +235,33 @@ int tc_strided_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank,
                       const uint64_t* shape, const void* a, uint64_t a_len, const tc_strided* a_at,
                       const void* b, uint64_t b_len, const tc_strided* b_at, void* out);
 
+/* ---- analytic functions and powers (kernels.rs:876-895, :941-949) ------- */
+
+/* `Kernels::vector_unary` / `matrix_unary` (kernels.rs:876, :941): `op` (an
+ * `Analytic`, kernels.rs:293-308) of each element, in f32 and rounded to
+ * `dtype` once; for f16 and bf16, `Sec` and `Csc` are the reciprocal in
+ * `dtype` of the rounded cosine or sine (vmath.rs:483-507).  The device's
+ * own f32 functions stand in for the host's `vmath` ones: within a few ulp
+ * of each other, both within a few ulp of the exact value. */
+int tc_unary(uint32_t dtype, uint32_t op, const void* a, void* out, uint64_t n);
+
+/* `Kernels::vector_unary_dual` / `matrix_unary_dual` (kernels.rs:891, :949):
+ * `out_value = op(value)` and `out_tangent = op'(value) * tangent`, the
+ * derivative as `Analytic::derivative` composes it (kernels.rs:358-385),
+ * one rounding to `dtype` per operation. */
+int tc_unary_dual(uint32_t dtype, uint32_t op, const void* value, const void* tangent, void* out_value,
+                  void* out_tangent, uint64_t n);
+
+/* `Kernels::vector_power` / `matrix_power` (kernels.rs:884, :944): elementwise
+ * `a^b`, `powf` in f32 rounded once (primitive.rs:133-150). */
+int tc_power(uint32_t dtype, const void* a, const void* b, void* out, uint64_t n);
+
+/* `Kernels::vector_power_scalar` / `matrix_power_scalar` (kernels.rs:888,
+ * :947): `scalar^x` when `scalar_left`, else `x^scalar`, the latter with the
+ * host's exact fast exponents 0, 1, 2, 1/2 and -1 for f32
+ * (analytic.rs:415-476). */
+int tc_power_scalar(uint32_t dtype, const void* a, float scalar, int scalar_left, void* out, uint64_t n);
+
 /* ---- reductions (kernels.rs:867, :1175, :1187) -------------------------- */
 
 /* `Kernels::reduce_axes` (kernels.rs:1175-1179; Host strided.rs:105-162):

@@ -57,6 +57,10 @@ _SIGNATURES = {
     "or_fold": ([u32, vp, u64, u32], f32),
     "or_fused": ([u32, vp, u32, vp, vp, vp, u64, u64], None),
     "or_row_moments": ([u32, u32, vp, vp, u64, u64, vp, vp], None),
+    "or_unary": ([u32, u32, vp, vp, u64], None),
+    "or_unary_dual": ([u32, u32, vp, vp, vp, vp, u64], None),
+    "or_power": ([u32, vp, vp, vp, u64], None),
+    "or_power_scalar": ([u32, vp, f32, i32, vp, u64], None),
     "or_fused_sum": ([u32, vp, u32, vp, vp, u64, u64, u32, vp], None),
     "or_matmul_epilogue": ([u32, vp, u32, vp, vp, vp, u64, u64, u64, vp, u32, vp], None),
 }
@@ -280,3 +284,31 @@ def matmul_epilogue(dtype, code, places, a, b, m, k, n, inputs, outputs) -> None
     ins = (vp * max(len(inputs), 1))(*[_p(x) for x in inputs])
     outs = (vp * max(len(outputs), 1))(*[_p(x) for x in outputs])
     load().or_matmul_epilogue(dtype, enc, len(code), pl, _p(a), _p(b), m, k, n, ins, len(inputs), outs)
+
+
+def unary(dtype, op, a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.zeros_like(a)
+    load().or_unary(dtype, op, _p(a), _p(out), a.size)
+    return out
+
+
+def unary_dual(dtype, op, value, tangent):
+    value, tangent = np.ascontiguousarray(value), np.ascontiguousarray(tangent)
+    out_value, out_tangent = np.zeros_like(value), np.zeros_like(value)
+    load().or_unary_dual(dtype, op, _p(value), _p(tangent), _p(out_value), _p(out_tangent), value.size)
+    return out_value, out_tangent
+
+
+def power(dtype, a, b) -> np.ndarray:
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    out = np.zeros_like(a)
+    load().or_power(dtype, _p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def power_scalar(dtype, a, scalar, scalar_left) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.zeros_like(a)
+    load().or_power_scalar(dtype, _p(a), scalar, int(scalar_left), _p(out), a.size)
+    return out

@@ -828,3 +828,74 @@ void or_matmul_epilogue(uint32_t dtype, const or_encoded* code, uint32_t count, 
     free(all);
     free(product);
 }
+
+/* ---- analytic functions and powers (kernels.rs:293-385, analytic.rs:405-540) -- */
+
+static float analytic_in(uint32_t dtype, uint32_t op, float x) {
+    if (op == 3) return 1.0f / in_type(dtype, cosf(x));
+    if (op == 4) return 1.0f / in_type(dtype, sinf(x));
+    return analytic(op, x);
+}
+
+static float derivative_in(uint32_t dtype, uint32_t op, float x) {
+#define R(v) in_type(dtype, (v))
+#define VALUE(f) R(analytic_in(dtype, (f), x))
+    switch (op) {
+        case 0: return VALUE(1);
+        case 1: return -VALUE(0);
+        case 2: { float c = VALUE(1); return R(1.0f / R(c * c)); }
+        case 3: { float c = VALUE(1); return R(VALUE(0) / R(c * c)); }
+        case 4: { float s = VALUE(0); return R(-VALUE(1) / R(s * s)); }
+        case 5: return R(1.0f / R(sqrtf(R(1.0f - R(x * x)))));
+        case 6: return -R(1.0f / R(sqrtf(R(1.0f - R(x * x)))));
+        case 7: return R(1.0f / R(1.0f + R(x * x)));
+        case 8: return VALUE(8);
+        case 9: return R(1.0f / x);
+        case 10: return VALUE(11);
+        case 11: return VALUE(10);
+        case 12: { float t = VALUE(12); return R(1.0f - R(t * t)); }
+        default: return R(1.0f / R(2.0f * VALUE(13)));
+    }
+#undef VALUE
+#undef R
+}
+
+void or_unary(uint32_t dtype, uint32_t op, const void* a, void* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) narrow_one(dtype, out, i, analytic_in(dtype, op, widen_one(dtype, a, i)));
+}
+
+void or_unary_dual(uint32_t dtype, uint32_t op, const void* value, const void* tangent, void* out_value,
+                   void* out_tangent, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) {
+        const float x = widen_one(dtype, value, i);
+        narrow_one(dtype, out_value, i, analytic_in(dtype, op, x));
+        narrow_one(dtype, out_tangent, i, derivative_in(dtype, op, x) * widen_one(dtype, tangent, i));
+    }
+}
+
+void or_power(uint32_t dtype, const void* a, const void* b, void* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) narrow_one(dtype, out, i, powf(widen_one(dtype, a, i), widen_one(dtype, b, i)));
+}
+
+void or_power_scalar(uint32_t dtype, const void* a, float scalar, int scalar_left, void* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) {
+        const float x = widen_one(dtype, a, i);
+        float y;
+        if (scalar_left) {
+            y = powf(scalar, x);
+        } else if (dtype == F32 && scalar == 0.0f) {
+            y = 1.0f;
+        } else if (dtype == F32 && scalar == 1.0f) {
+            y = x;
+        } else if (dtype == F32 && scalar == 2.0f) {
+            y = x * x;
+        } else if (dtype == F32 && scalar == 0.5f) {
+            y = x == -INFINITY ? INFINITY : sqrtf(x) + 0.0f;
+        } else if (dtype == F32 && scalar == -1.0f) {
+            y = 1.0f / x;
+        } else {
+            y = powf(x, scalar);
+        }
+        narrow_one(dtype, out, i, y);
+    }
+}

@@ -117,6 +117,22 @@ typedef struct or_place {
 void or_fused(uint32_t dtype, const or_encoded* code, uint32_t count, const or_place* places,
               const void* const* inputs, void* const* outputs, uint64_t rows, uint64_t cols);
 
+/* `Analytic::value` applied to dtype elements as the host does
+ * (vmath.rs:483-507), in f32 libm: the value rounded once; f16/bf16 `Sec`
+ * and `Csc` the reciprocal in dtype of the rounded cosine or sine. */
+void or_unary(uint32_t dtype, uint32_t op, const void* a, void* out, uint64_t n);
+
+/* `(f(x), f'(x) * t)`, `Analytic::derivative` (kernels.rs:358-385) with one
+ * rounding to dtype per operation (`vector_unary_dual`, kernels.rs:1284-1300). */
+void or_unary_dual(uint32_t dtype, uint32_t op, const void* value, const void* tangent, void* out_value,
+                   void* out_tangent, uint64_t n);
+
+/* `powf` in f32 rounded once (primitive.rs:133-150), elementwise or with a
+ * scalar on either side; `x^s` takes the f32 fast exponents
+ * (analytic.rs:415-476). */
+void or_power(uint32_t dtype, const void* a, const void* b, void* out, uint64_t n);
+void or_power_scalar(uint32_t dtype, const void* a, float scalar, int scalar_left, void* out, uint64_t n);
+
 /* `Kernels::row_moments` on the Host (`host_row_moments`, fused/mod.rs:
  * 4030-4041): the rows x cols matrix `place` reads of `input`, converted to
  * dtype (`input_matrix`, :3984-3991), and per row `moments_of`

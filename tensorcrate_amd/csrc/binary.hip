@@ -188,6 +188,139 @@ int map_scalar(uint32_t kind, uint32_t op, const void* a, float scalar, bool lef
     return TC_OK;
 }
 
+// ---- analytic functions and powers (kernels.rs:876-895, :941-949) -----------
+
+// A value rounded to S and back: the host's arithmetic in S, one rounding per
+// operation, with f32 the identity.
+template <typename S>
+__device__ __forceinline__ float in_s(float v) {
+    return Elem<S>::widen(Elem<S>::narrow(v));
+}
+
+// `Analytic::value` as the host applies it to S (vmath.rs:483-507): in f32,
+// the caller rounding once; for f16 and bf16 `Sec` and `Csc` are the
+// reciprocal, in S, of the rounded cosine or sine.
+template <typename S>
+__device__ __forceinline__ float analytic_in(uint32_t op, float x) {
+    if (op == 3) return 1.0f / in_s<S>(cosf(x));
+    if (op == 4) return 1.0f / in_s<S>(sinf(x));
+    return tc_analytic(op, x);
+}
+
+// `Analytic::derivative` (kernels.rs:358-385), every operation rounded to S
+// as the host's arithmetic in S rounds it.
+template <typename S>
+__device__ float derivative_in(uint32_t op, float x) {
+    auto r = [](float v) { return in_s<S>(v); };
+    auto value = [&](uint32_t f) { return r(analytic_in<S>(f, x)); };
+    switch (op) {
+        case 0: return value(1);
+        case 1: return -value(0);
+        case 2: { const float c = value(1); return r(1.0f / r(c * c)); }
+        case 3: { const float c = value(1); return r(value(0) / r(c * c)); }
+        case 4: { const float sn = value(0); return r(-value(1) / r(sn * sn)); }
+        case 5: return r(1.0f / r(sqrtf(r(1.0f - r(x * x)))));
+        case 6: return -r(1.0f / r(sqrtf(r(1.0f - r(x * x)))));
+        case 7: return r(1.0f / r(1.0f + r(x * x)));
+        case 8: return value(8);
+        case 9: return r(1.0f / x);
+        case 10: return value(11);
+        case 11: return value(10);
+        case 12: { const float t = value(12); return r(1.0f - r(t * t)); }
+        default: return r(1.0f / r(2.0f * value(13)));
+    }
+}
+
+template <typename S>
+struct UnaryOf {
+    uint32_t op;
+    __device__ float operator()(float x, float) const { return analytic_in<S>(op, x); }
+};
+
+// `x^s` with the host's fast exponents for f32 (analytic.rs:415-476): 0, 1,
+// 2, 1/2 and -1 are single exact operations; anything else, and every f16 or
+// bf16 exponent, is `powf` rounded once.
+template <typename S>
+struct PowerRight {
+    float s;
+    int fast;  // 0 none, 1 zero, 2 one, 3 square, 4 root, 5 reciprocal
+    __device__ float operator()(float x, float) const {
+        switch (fast) {
+            case 1: return 1.0f;
+            case 2: return x;
+            case 3: return x * x;
+            case 4: return x == -INFINITY ? INFINITY : sqrtf(x) + 0.0f;
+            case 5: return 1.0f / x;
+            default: return powf(x, s);
+        }
+    }
+};
+
+// `(f(x), f'(x) t)` over n elements, 16 bytes of each operand a thread.
+template <typename S, bool PACKED>
+__global__ void __launch_bounds__(256) dual_kernel(const S* __restrict__ value, const S* __restrict__ tangent,
+                                                   S* __restrict__ out_value, S* __restrict__ out_tangent,
+                                                   uint64_t n, uint32_t op) {
+    using E = Elem<S>;
+    constexpr int N = PACKED ? Pack<S>::N : 1;
+    const uint64_t groups = PACKED ? n / N : n;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < groups; g += stride) {
+        S x[N], t[N], fx[N], ft[N];
+        if (PACKED) {
+            __builtin_memcpy(x, value + g * N, 16);
+            __builtin_memcpy(t, tangent + g * N, 16);
+        } else {
+            x[0] = value[g];
+            t[0] = tangent[g];
+        }
+#pragma unroll
+        for (int k = 0; k < N; k++) {
+            const float v = E::widen(x[k]);
+            fx[k] = E::narrow(analytic_in<S>(op, v));
+            ft[k] = E::narrow(derivative_in<S>(op, v) * E::widen(t[k]));
+        }
+        if (PACKED) {
+            __builtin_memcpy(out_value + g * N, fx, 16);
+            __builtin_memcpy(out_tangent + g * N, ft, 16);
+        } else {
+            out_value[g] = fx[0];
+            out_tangent[g] = ft[0];
+        }
+    }
+    if (PACKED && blockIdx.x == 0 && threadIdx.x < n - groups * N) {
+        const uint64_t i = groups * N + threadIdx.x;
+        const float v = E::widen(value[i]);
+        out_value[i] = E::narrow(analytic_in<S>(op, v));
+        out_tangent[i] = E::narrow(derivative_in<S>(op, v) * E::widen(tangent[i]));
+    }
+}
+
+template <typename S>
+int launch_dual(const void* value, const void* tangent, void* out_value, void* out_tangent, uint64_t n, uint32_t op) {
+    TC_STREAM(s);
+    if (n == 0) return TC_OK;
+    const S* v = static_cast<const S*>(value);
+    const S* t = static_cast<const S*>(tangent);
+    S* ov = static_cast<S*>(out_value);
+    S* ot = static_cast<S*>(out_tangent);
+    if (aligned16(v) && aligned16(t) && aligned16(ov) && aligned16(ot)) {
+        dual_kernel<S, true><<<blocks_for(n / Pack<S>::N + 1, 1), 256, 0, s>>>(v, t, ov, ot, n, op);
+    } else {
+        dual_kernel<S, false><<<blocks_for(n, 1), 256, 0, s>>>(v, t, ov, ot, n, op);
+    }
+    return check_launch("unary_dual");
+}
+
+int fast_exponent(float e) {
+    if (e == 0.0f) return 1;
+    if (e == 1.0f) return 2;
+    if (e == 2.0f) return 3;
+    if (e == 0.5f) return 4;
+    if (e == -1.0f) return 5;
+    return 0;
+}
+
 // ---- strided, broadcasting operands ----------------------------------------
 
 // How an operand steps along the innermost axis of a coalesced walk.
@@ -385,6 +518,38 @@ int tc_compare_scalar(uint32_t dtype, uint32_t op, const void* a, float scalar, 
     TC_DISPATCH_FLOAT(dtype, "compare_scalar", S,
                       return map_scalar<S>(TC_PAIR_COMPARE, op, a, scalar, scalar_left != 0, out, n,
                                            "compare_scalar"));
+    return TC_OK;
+}
+
+int tc_unary(uint32_t dtype, uint32_t op, const void* a, void* out, uint64_t n) {
+    if (op > 13) return fail(TC_INVALID, "no Analytic " + std::to_string(op));
+    TC_STREAM(s);
+    TC_DISPATCH_FLOAT(dtype, "unary", S, return launch_map<S>(a, nullptr, out, n, UnaryOf<S>{op}, s, "unary"));
+    return TC_OK;
+}
+
+int tc_unary_dual(uint32_t dtype, uint32_t op, const void* value, const void* tangent, void* out_value,
+                  void* out_tangent, uint64_t n) {
+    if (op > 13) return fail(TC_INVALID, "no Analytic " + std::to_string(op));
+    TC_DISPATCH_FLOAT(dtype, "unary_dual", S, return launch_dual<S>(value, tangent, out_value, out_tangent, n, op));
+    return TC_OK;
+}
+
+int tc_power(uint32_t dtype, const void* a, const void* b, void* out, uint64_t n) {
+    TC_DISPATCH_FLOAT(dtype, "power", S, return map_pair<S>(TC_PAIR_POWER, 0, a, b, out, n, "power"));
+    return TC_OK;
+}
+
+int tc_power_scalar(uint32_t dtype, const void* a, float scalar, int scalar_left, void* out, uint64_t n) {
+    if (scalar_left) {
+        TC_DISPATCH_FLOAT(dtype, "power", S,
+                          return map_scalar<S>(TC_PAIR_POWER, 0, a, scalar, true, out, n, "power"));
+        return TC_OK;
+    }
+    TC_STREAM(s);
+    const int fast = dtype == TC_F32 ? fast_exponent(scalar) : 0;
+    TC_DISPATCH_FLOAT(dtype, "power", S,
+                      return launch_map<S>(a, nullptr, out, n, PowerRight<S>{scalar, fast}, s, "power"));
     return TC_OK;
 }
 

@@ -126,6 +126,10 @@ SIGNATURES = {
     "tc_compare": [u32, u32, vp, vp, vp, u64],
     "tc_compare_scalar": [u32, u32, vp, f32, i32, vp, u64],
     "tc_clamp": [u32, vp, f32, f32, vp, u64],
+    "tc_unary": [u32, u32, vp, vp, u64],
+    "tc_unary_dual": [u32, u32, vp, vp, vp, vp, u64],
+    "tc_power": [u32, vp, vp, vp, u64],
+    "tc_power_scalar": [u32, vp, f32, i32, vp, u64],
     "tc_strided_binary": [u32, u32, u32, u32, ctypes.POINTER(u64), vp, u64, ctypes.POINTER(Strided), vp, u64,
                           ctypes.POINTER(Strided), vp],
     "tc_reduce_axes": [u32, vp, u64, ctypes.POINTER(Split), u32, u32, u64, vp],

@@ -180,3 +180,27 @@ def column_broadcast(rows):
 
 
 EXP, SQRT = 8, 13  # `Analytic` (kernels.rs:334-354)
+
+
+def ordered_bits(values: np.ndarray) -> np.ndarray:
+    """Float bit patterns mapped to integers in the same order as the values,
+    so that differences count ulps (f32, or raw 16-bit f16/bf16 patterns)."""
+    if values.dtype == np.float32:
+        bits = values.view(np.int32).astype(np.int64)
+        return np.where(bits < 0, -(bits & 0x7FFFFFFF), bits)
+    bits = values.view(np.uint16).astype(np.int64)
+    return np.where(bits & 0x8000, -(bits & 0x7FFF), bits)
+
+
+def ulps(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """Ulps between two arrays of one storage type; NaN against NaN is 0,
+    NaN against a number is huge."""
+    wide_got = got.astype(np.float32) if got.dtype != np.uint16 else None
+    gap = np.abs(ordered_bits(got) - ordered_bits(want))
+    if got.dtype == np.uint16:
+        nan_g = ((got & 0x7F80) == 0x7F80) & ((got & 0x7F) != 0)
+        nan_w = ((want & 0x7F80) == 0x7F80) & ((want & 0x7F) != 0)
+    else:
+        nan_g, nan_w = np.isnan(wide_got), np.isnan(want.astype(np.float32))
+    gap = np.where(nan_g & nan_w, 0, gap)
+    return np.where(nan_g != nan_w, 1 << 40, gap)
