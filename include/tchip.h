@@ -284,6 +284,21 @@ int tc_arg_reduce(uint32_t dtype, const void* input, uint64_t input_len, const t
  * Metal's `reduce` returns it (tensors/backend.rs:813-818). */
 int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result);
 
+/* `Kernels::vector_moments` / `matrix_moments` (kernels.rs:1035-1038; Host
+ * `moments_of`, statistics/mod.rs:419-441): the mean of all `n` elements into
+ * the device f32 `result[0]` and the sum of squared deviations from it into
+ * `result[1]`, unrounded (the caller rounds to the element type, as the
+ * compact types do); NaNs for no elements. */
+int tc_moments(uint32_t dtype, const void* a, uint64_t n, float* result);
+
+/* `Kernels::matrix_axis_moments` (kernels.rs:1042; Host
+ * statistics/mod.rs:451-520): per row (`axis` TC_AXIS_ROWS) or per column
+ * of the row-major rows x cols matrix `a`, the mean into `means` and the sum
+ * of squared deviations into `deviations`, accumulated in f32 and rounded to
+ * `dtype` once; NaNs along an empty axis. */
+int tc_axis_moments(uint32_t dtype, const void* a, uint64_t rows, uint64_t cols, uint32_t axis, void* means,
+                    void* deviations);
+
 /* `Kernels::dot` (kernels.rs:897): sum a[i]*b[i] into the device f32 scalar
  * `result`, unrounded. */
 int tc_dot(uint32_t dtype, const void* a, const void* b, uint64_t n, float* result);

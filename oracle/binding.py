@@ -58,6 +58,7 @@ _SIGNATURES = {
     "or_fused": ([u32, vp, u32, vp, vp, vp, u64, u64], None),
     "or_row_moments": ([u32, u32, vp, vp, u64, u64, vp, vp], None),
     "or_unary": ([u32, u32, vp, vp, u64], None),
+    "or_moments": ([u32, vp, u64, vp], None),
     "or_unary_dual": ([u32, u32, vp, vp, vp, vp, u64], None),
     "or_power": ([u32, vp, vp, vp, u64], None),
     "or_power_scalar": ([u32, vp, f32, i32, vp, u64], None),
@@ -312,3 +313,11 @@ def power_scalar(dtype, a, scalar, scalar_left) -> np.ndarray:
     out = np.zeros_like(a)
     load().or_power_scalar(dtype, _p(a), scalar, int(scalar_left), _p(out), a.size)
     return out
+
+
+def moments(dtype, a):
+    """(mean, sum of squared deviations) as f32, unrounded."""
+    a = np.ascontiguousarray(a)
+    out = np.zeros(2, np.float32)
+    load().or_moments(dtype, _p(a), a.size, _p(out))
+    return float(out[0]), float(out[1])

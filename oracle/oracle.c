@@ -899,3 +899,20 @@ void or_power_scalar(uint32_t dtype, const void* a, float scalar, int scalar_lef
         narrow_one(dtype, out, i, y);
     }
 }
+
+void or_moments(uint32_t dtype, const void* a, uint64_t n, float* out) {
+    if (n == 0) {
+        out[0] = out[1] = NAN;
+        return;
+    }
+    float total = 0.0f;
+    for (uint64_t i = 0; i < n; i++) total = total + widen_one(dtype, a, i);
+    const float mean = total / (float)n;
+    float squares = 0.0f;
+    for (uint64_t i = 0; i < n; i++) {
+        const float d = widen_one(dtype, a, i) - mean;
+        squares = squares + d * d;
+    }
+    out[0] = mean;
+    out[1] = squares;
+}

@@ -142,6 +142,11 @@ void or_power_scalar(uint32_t dtype, const void* a, float scalar, int scalar_lef
 void or_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, const or_place* place, uint64_t rows,
                     uint64_t cols, void* means, void* deviations);
 
+/* `vector_moments` / `matrix_moments` on the Host (`moments_of`,
+ * statistics/mod.rs:419-441): out[0] the mean, out[1] the sum of squared
+ * deviations, sequential f32 folds; NaNs for no elements. */
+void or_moments(uint32_t dtype, const void* a, uint64_t n, float* out);
+
 /* `Kernels::fused_sum`'s default (kernels.rs:1120-1135): the program's one
  * output, then `axis_sum` (fused/mod.rs:4045-4051), its products with ones:
  * axis 0 (Rows) a matvec, axis 1 (Columns) a vecmat. */

@@ -1,6 +1,7 @@
 // The `Kernels` members that compose a fused program with a product or a
 // reduction: `row_moments` (kernels.rs:1090), `fused_sum` (kernels.rs:1120)
-// and `matmul_epilogue` (kernels.rs:1142).  `fused_with_statistics`
+// and `matmul_epilogue` (kernels.rs:1142); and `matrix_axis_moments`
+// (kernels.rs:1042), the moments reduction along an axis.  `fused_with_statistics`
 // (kernels.rs:1103) is their composition on the host side: `row_moments`
 // for each statistic the program derives, then `tc_fused` with those as
 // extra inputs, as the trait's default does.
@@ -131,6 +132,28 @@ int tc_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, uint
     split.folded[0] = cols;
     split.folded_strides[0] = 1;
     return reduce_moments(dtype, matrix.ptr, n, &split, means, deviations);
+}
+
+int tc_axis_moments(uint32_t dtype, const void* a, uint64_t rows, uint64_t cols, uint32_t axis, void* means,
+                    void* deviations) {
+    if (axis > TC_AXIS_COLUMNS) return fail(TC_INVALID, "axis moments: no Axis " + std::to_string(axis));
+    if (!is_float(dtype)) return fail(TC_UNSUPPORTED, std::string("axis moments: no kernel for ") + dtype_name(dtype));
+    const uint64_t results = axis == TC_AXIS_ROWS ? rows : cols;
+    const uint64_t depth = axis == TC_AXIS_ROWS ? cols : rows;
+    if (results == 0) return TC_OK;
+    if (depth == 0) {  // moments of nothing (statistics/mod.rs:470-476)
+        int status = fill_nan(dtype, means, results);
+        return status == TC_OK ? fill_nan(dtype, deviations, results) : status;
+    }
+    tc_split split;
+    memset(&split, 0, sizeof(split));
+    split.kept_rank = 1;
+    split.folded_rank = 1;
+    split.kept[0] = results;
+    split.folded[0] = depth;
+    split.kept_strides[0] = axis == TC_AXIS_ROWS ? cols : 1;
+    split.folded_strides[0] = axis == TC_AXIS_ROWS ? 1 : cols;
+    return reduce_moments(dtype, a, rows * cols, &split, means, deviations);
 }
 
 int tc_fused_sum(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,

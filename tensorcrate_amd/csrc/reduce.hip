@@ -798,6 +798,76 @@ int total(const void* a, const void* b, uint64_t n, float* result, const char* w
     return status;
 }
 
+// The moments of a whole buffer, in the manner of `total`: each block folds
+// its grid-stride share (16-byte packs when aligned, each pack's exact
+// two-pass moments merged in), the waves' states merge in the closed form,
+// and one wave merges the blocks' states into `result[0]` (the mean) and
+// `result[1]` (the sum of squared deviations), unrounded f32; NaNs for an
+// empty buffer (statistics/mod.rs:428-434).
+template <typename S, bool PACKED>
+__global__ void __launch_bounds__(256) moments_total_kernel(const S* __restrict__ a, uint64_t n,
+                                                            Moments* __restrict__ partial) {
+    using E = Elem<S>;
+    constexpr int V = Pack<S>::N;
+    __shared__ Moments stage[4];
+    Moments s = Var::init();
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    const uint64_t first = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (PACKED) {
+        const uint64_t packs = n / V;
+        for (uint64_t p = first; p < packs; p += stride) {
+            float x[V];
+            load_packs<S, 1, false>(reinterpret_cast<const Pack<S>*>(a) + p, x);
+            Var::add_chunk(s, x, 0);
+        }
+        if (blockIdx.x == 0 && threadIdx.x < n - packs * V) Var::add(s, E::widen(a[packs * V + threadIdx.x]), 0);
+    } else {
+        for (uint64_t i = first; i < n; i += stride) Var::add(s, E::widen(a[i]), 0);
+    }
+    s = wave_reduce<Var>(s);
+    if (threadIdx.x % 64 == 0) stage[threadIdx.x / 64] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Moments t = stage[0];
+        for (int w = 1; w < 4; w++) t = merge_moments(t, stage[w]);
+        partial[blockIdx.x] = t;
+    }
+}
+
+__global__ void __launch_bounds__(64) finish_moments_kernel(const Moments* __restrict__ partial, uint32_t count,
+                                                            float* __restrict__ result) {
+    Moments s = Var::init();
+    for (uint32_t i = threadIdx.x; i < count; i += 64) s = merge_moments(s, partial[i]);
+    s = wave_reduce<Var>(s);
+    if (threadIdx.x == 0) {
+        result[0] = s.n == 0.0f ? NAN : s.mean;
+        result[1] = s.n == 0.0f ? NAN : s.m2;
+    }
+}
+
+template <typename S>
+int total_moments(const void* a, uint64_t n, float* result) {
+    TC_STREAM(s);
+    const uint32_t blocks = grid_for(n, 256 * 16, 4);
+    void* scratch = nullptr;
+    int status = tc_alloc(blocks * sizeof(Moments), &scratch);
+    if (status != TC_OK) return status;
+    Moments* partial = static_cast<Moments*>(scratch);
+    const S* in = static_cast<const S*>(a);
+    if (aligned16(in)) {
+        moments_total_kernel<S, true><<<blocks, 256, 0, s>>>(in, n, partial);
+    } else {
+        moments_total_kernel<S, false><<<blocks, 256, 0, s>>>(in, n, partial);
+    }
+    status = check_launch("moments");
+    if (status == TC_OK) {
+        finish_moments_kernel<<<1, 64, 0, s>>>(partial, blocks, result);
+        status = check_launch("moments");
+    }
+    tc_free(scratch);
+    return status;
+}
+
 }  // namespace
 }  // namespace tc
 
@@ -843,6 +913,11 @@ int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, flo
         default:
             return fail(TC_INVALID, "vector_reduce: no Reduce " + std::to_string(op));
     }
+    return TC_OK;
+}
+
+int tc_moments(uint32_t dtype, const void* a, uint64_t n, float* result) {
+    TC_DISPATCH_FLOAT(dtype, "moments", S, return total_moments<S>(a, n, result));
     return TC_OK;
 }
 

@@ -136,6 +136,8 @@ SIGNATURES = {
     "tc_arg_reduce": [u32, vp, u64, ctypes.POINTER(Split), u32, vp],
     "tc_vector_reduce": [u32, vp, u64, u32, vp],
     "tc_dot": [u32, vp, vp, u64, vp],
+    "tc_moments": [u32, vp, u64, vp],
+    "tc_axis_moments": [u32, vp, u64, u64, u32, vp, vp],
     "tc_matmul": [u32, u32, u32, i32, u64, u64, u64, vp, vp, vp],
     "tc_matvec": [u32, i32, u64, u64, vp, vp, vp],
     "tc_vecmat": [u32, u64, u64, vp, vp, vp],

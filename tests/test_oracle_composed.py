@@ -191,3 +191,16 @@ def test_row_statistics_feed_the_program_as_the_hand_formula_says():
                 assert normalized[i].view(np.uint32) == np.float32(want).view(np.uint32), (rows, cols, i)
                 updated = start[i] + (np.float32(want) * gamma[c] + other[r])
                 assert acc[i].view(np.uint32) == np.float32(updated).view(np.uint32), (rows, cols, i)
+
+
+def test_moments_known_answers_and_against_f64():
+    # statistics/mod.rs:419-441: mean = sum / n, then the deviations.
+    assert oracle.moments(lib.F32, np.array([1, 2, 3, 4], np.float32)) == (2.5, 5.0)
+    mean, devs = oracle.moments(lib.F32, np.zeros(0, np.float32))
+    assert math.isnan(mean) and math.isnan(devs)
+    rng = np.random.default_rng(21)
+    x = rng.uniform(-3, 3, 100000).astype(np.float32)
+    mean, devs = oracle.moments(lib.F32, x)
+    wide = x.astype(np.float64)
+    assert abs(mean - wide.mean()) <= 1e-4 * 3
+    assert abs(devs - ((wide - wide.mean()) ** 2).sum()) <= 1e-3 * devs
