@@ -330,6 +330,40 @@ int tc_vecmat(uint32_t dtype, uint64_t rows, uint64_t cols, const void* vector,
  * cols x rows transpose of a rows x cols matrix of `width`-byte elements. */
 int tc_transpose(uint32_t width, uint64_t rows, uint64_t cols, const void* src, void* dst);
 
+/* ---- correlation, padding, flipping (kernels.rs:990-1029) --------------- */
+
+/* `Kernels::correlate` (kernels.rs:998; Host `correlate_values`,
+ * kernels.rs:1720-1750): the valid correlation of the row-major rows x cols
+ * `input` with the window_rows x window_cols `window` into
+ * (rows - window_rows + 1) x (cols - window_cols + 1) `out`; `flip` reverses
+ * the window (convolution).  Each output sums its taps in row-major tap
+ * order, a separate multiply and add each, in f32, rounded to `dtype` once:
+ * the host's bits.  `correlate_window_gradient` is this with the adjoint as
+ * the window (kernels.rs:1544-1551).  A window larger than the input is
+ * refused with the reference's message. */
+int tc_correlate(uint32_t dtype, const void* input, uint64_t rows, uint64_t cols, const void* window,
+                 uint64_t window_rows, uint64_t window_cols, int flip, void* out);
+
+/* `Kernels::correlate_input_gradient` (kernels.rs:1017; Host
+ * kernels.rs:1754-1794): the full correlation of the adjoint_rows x
+ * adjoint_cols `adjoint` with the window, the taps applied the other way
+ * round from the forward pass's `forward_flip`, into the
+ * (adjoint_rows + window_rows - 1) x (adjoint_cols + window_cols - 1) `out`;
+ * the same order of operations as the host. */
+int tc_correlate_input_gradient(uint32_t dtype, const void* adjoint, uint64_t adjoint_rows, uint64_t adjoint_cols,
+                                const void* window, uint64_t window_rows, uint64_t window_cols, int forward_flip,
+                                void* out);
+
+/* `Kernels::pad` (kernels.rs:1025; Host kernels.rs:1575-1600): the rows x cols
+ * matrix of `width`-byte elements surrounded by `pad_rows` and `pad_cols`
+ * zeros on every side, into (rows + 2 pad_rows) x (cols + 2 pad_cols) `out`. */
+int tc_pad(uint32_t width, const void* input, uint64_t rows, uint64_t cols, uint64_t pad_rows, uint64_t pad_cols,
+           void* out);
+
+/* `Kernels::flip` (kernels.rs:1028; Host kernels.rs:1531-1542): both axes of a
+ * rows x cols matrix of `width`-byte elements reversed. */
+int tc_flip(uint32_t width, const void* input, uint64_t rows, uint64_t cols, void* out);
+
 /* ---- fused programs (kernels.rs:1077-1082; fused/mod.rs:959-1011) ------- */
 
 /* `Kernels::fused`: run `count` encoded instructions for every element of a

@@ -59,6 +59,10 @@ _SIGNATURES = {
     "or_row_moments": ([u32, u32, vp, vp, u64, u64, vp, vp], None),
     "or_unary": ([u32, u32, vp, vp, u64], None),
     "or_moments": ([u32, vp, u64, vp], None),
+    "or_correlate": ([u32, vp, u64, u64, vp, u64, u64, i32, vp], None),
+    "or_correlate_input_gradient": ([u32, vp, u64, u64, vp, u64, u64, i32, vp], None),
+    "or_pad": ([u32, vp, u64, u64, u64, u64, vp], None),
+    "or_flip": ([u32, vp, u64, u64, vp], None),
     "or_unary_dual": ([u32, u32, vp, vp, vp, vp, u64], None),
     "or_power": ([u32, vp, vp, vp, u64], None),
     "or_power_scalar": ([u32, vp, f32, i32, vp, u64], None),
@@ -321,3 +325,34 @@ def moments(dtype, a):
     out = np.zeros(2, np.float32)
     load().or_moments(dtype, _p(a), a.size, _p(out))
     return float(out[0]), float(out[1])
+
+
+def correlate(dtype, x, window, flip) -> np.ndarray:
+    x, window = np.ascontiguousarray(x), np.ascontiguousarray(window)
+    (rows, cols), (wr, wc) = x.shape, window.shape
+    out = np.zeros((rows - wr + 1, cols - wc + 1), x.dtype)
+    load().or_correlate(dtype, _p(x), rows, cols, _p(window), wr, wc, int(flip), _p(out))
+    return out
+
+
+def correlate_input_gradient(dtype, adjoint, window, forward_flip) -> np.ndarray:
+    adjoint, window = np.ascontiguousarray(adjoint), np.ascontiguousarray(window)
+    (ar, ac), (wr, wc) = adjoint.shape, window.shape
+    out = np.zeros((ar + wr - 1, ac + wc - 1), adjoint.dtype)
+    load().or_correlate_input_gradient(dtype, _p(adjoint), ar, ac, _p(window), wr, wc, int(forward_flip), _p(out))
+    return out
+
+
+def pad(x, pad_rows, pad_cols) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    out = np.ones((rows + 2 * pad_rows, cols + 2 * pad_cols), x.dtype)
+    load().or_pad(x.itemsize, _p(x), rows, cols, pad_rows, pad_cols, _p(out))
+    return out
+
+
+def flip(x) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    out = np.zeros_like(x)
+    load().or_flip(x.itemsize, _p(x), x.shape[0], x.shape[1], _p(out))
+    return out

@@ -916,3 +916,75 @@ void or_moments(uint32_t dtype, const void* a, uint64_t n, float* out) {
     out[0] = mean;
     out[1] = squares;
 }
+
+/* ---- correlation, padding, flipping (kernels.rs:1514-1600, :1720-1794) ------ */
+
+void or_correlate(uint32_t dtype, const void* input, uint64_t rows, uint64_t cols, const void* window,
+                  uint64_t window_rows, uint64_t window_cols, int flip, void* out) {
+    const uint64_t out_rows = rows - window_rows + 1, out_cols = cols - window_cols + 1;
+    for (uint64_t row = 0; row < out_rows; row++) {
+        for (uint64_t col = 0; col < out_cols; col++) {
+            float sum = 0.0f;
+            for (uint64_t i = 0; i < window_rows; i++) {
+                for (uint64_t j = 0; j < window_cols; j++) {
+                    const uint64_t tap_row = flip ? window_rows - 1 - i : i;
+                    const uint64_t tap_col = flip ? window_cols - 1 - j : j;
+                    sum = sum + widen_one(dtype, input, (row + i) * cols + col + j) *
+                                    widen_one(dtype, window, tap_row * window_cols + tap_col);
+                }
+            }
+            narrow_one(dtype, out, row * out_cols + col, sum);
+        }
+    }
+}
+
+void or_correlate_input_gradient(uint32_t dtype, const void* adjoint, uint64_t adjoint_rows, uint64_t adjoint_cols,
+                                 const void* window, uint64_t window_rows, uint64_t window_cols, int forward_flip,
+                                 void* out) {
+    const uint64_t rows = adjoint_rows + window_rows - 1, cols = adjoint_cols + window_cols - 1;
+    for (uint64_t row = 0; row < rows; row++) {
+        for (uint64_t col = 0; col < cols; col++) {
+            float sum = 0.0f;
+            for (uint64_t i = 0; i < window_rows; i++) {
+                for (uint64_t j = 0; j < window_cols; j++) {
+                    if (row < i || col < j) continue;
+                    const uint64_t source_row = row - i, source_col = col - j;
+                    if (source_row >= adjoint_rows || source_col >= adjoint_cols) continue;
+                    const uint64_t tap_row = forward_flip ? window_rows - 1 - i : i;
+                    const uint64_t tap_col = forward_flip ? window_cols - 1 - j : j;
+                    sum = sum + widen_one(dtype, adjoint, source_row * adjoint_cols + source_col) *
+                                    widen_one(dtype, window, tap_row * window_cols + tap_col);
+                }
+            }
+            narrow_one(dtype, out, row * cols + col, sum);
+        }
+    }
+}
+
+void or_pad(uint32_t width, const void* input, uint64_t rows, uint64_t cols, uint64_t pad_rows, uint64_t pad_cols,
+            void* out) {
+    const uint64_t padded_rows = rows + 2 * pad_rows, padded_cols = cols + 2 * pad_cols;
+    const uint8_t* in = (const uint8_t*)input;
+    uint8_t* o = (uint8_t*)out;
+    for (uint64_t row = 0; row < padded_rows; row++) {
+        for (uint64_t col = 0; col < padded_cols; col++) {
+            const int inside = row >= pad_rows && row < pad_rows + rows && col >= pad_cols && col < pad_cols + cols;
+            uint8_t* at = o + (row * padded_cols + col) * width;
+            if (inside) {
+                memcpy(at, in + ((row - pad_rows) * cols + col - pad_cols) * width, width);
+            } else {
+                memset(at, 0, width);
+            }
+        }
+    }
+}
+
+void or_flip(uint32_t width, const void* input, uint64_t rows, uint64_t cols, void* out) {
+    const uint8_t* in = (const uint8_t*)input;
+    uint8_t* o = (uint8_t*)out;
+    for (uint64_t row = 0; row < rows; row++) {
+        for (uint64_t col = 0; col < cols; col++) {
+            memcpy(o + (row * cols + col) * width, in + ((rows - 1 - row) * cols + cols - 1 - col) * width, width);
+        }
+    }
+}

@@ -147,6 +147,19 @@ void or_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, con
  * deviations, sequential f32 folds; NaNs for no elements. */
 void or_moments(uint32_t dtype, const void* a, uint64_t n, float* out);
 
+/* `correlate_values` (kernels.rs:1720-1750) and
+ * `correlate_input_gradient_values` (:1754-1794), f32 accumulation for the
+ * compact types rounded once (:1523-1527); `pad` (:1575-1600) and `flip`
+ * (:1531-1542) over `width`-byte elements. */
+void or_correlate(uint32_t dtype, const void* input, uint64_t rows, uint64_t cols, const void* window,
+                  uint64_t window_rows, uint64_t window_cols, int flip, void* out);
+void or_correlate_input_gradient(uint32_t dtype, const void* adjoint, uint64_t adjoint_rows, uint64_t adjoint_cols,
+                                 const void* window, uint64_t window_rows, uint64_t window_cols, int forward_flip,
+                                 void* out);
+void or_pad(uint32_t width, const void* input, uint64_t rows, uint64_t cols, uint64_t pad_rows, uint64_t pad_cols,
+            void* out);
+void or_flip(uint32_t width, const void* input, uint64_t rows, uint64_t cols, void* out);
+
 /* `Kernels::fused_sum`'s default (kernels.rs:1120-1135): the program's one
  * output, then `axis_sum` (fused/mod.rs:4045-4051), its products with ones:
  * axis 0 (Rows) a matvec, axis 1 (Columns) a vecmat. */

@@ -137,6 +137,10 @@ SIGNATURES = {
     "tc_vector_reduce": [u32, vp, u64, u32, vp],
     "tc_dot": [u32, vp, vp, u64, vp],
     "tc_moments": [u32, vp, u64, vp],
+    "tc_correlate": [u32, vp, u64, u64, vp, u64, u64, i32, vp],
+    "tc_correlate_input_gradient": [u32, vp, u64, u64, vp, u64, u64, i32, vp],
+    "tc_pad": [u32, vp, u64, u64, u64, u64, vp],
+    "tc_flip": [u32, vp, u64, u64, vp],
     "tc_axis_moments": [u32, vp, u64, u64, u32, vp, vp],
     "tc_matmul": [u32, u32, u32, i32, u64, u64, u64, vp, vp, vp],
     "tc_matvec": [u32, i32, u64, u64, vp, vp, vp],
