@@ -235,6 +235,20 @@ int tc_strided_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank,
                       const uint64_t* shape, const void* a, uint64_t a_len, const tc_strided* a_at,
                       const void* b, uint64_t b_len, const tc_strided* b_at, void* out);
 
+/* ---- scans and sorts (kernels.rs:870-873) -------------------------------- */
+
+/* `Kernels::vector_prefix_sum` (kernels.rs:870; Host vector.rs:578-589,
+ * compact.rs:209-221): the inclusive running sum of `n` elements,
+ * accumulated in f32 and rounded to `dtype` per output.  A deterministic
+ * tree order (the same bits every run); within the rounding of a sum of
+ * that many terms of the host's left-to-right order. */
+int tc_prefix_sum(uint32_t dtype, const void* a, void* out, uint64_t n);
+
+/* `Kernels::vector_sort` (kernels.rs:873; Host `Vector::sorted`): the `n`
+ * elements in `order` (a `SortOrder`, kernels.rs:252-255: 0 ascending, 1
+ * descending) of IEEE totalOrder (`total_cmp`), exactly. */
+int tc_sort(uint32_t dtype, const void* a, void* out, uint64_t n, uint32_t order);
+
 /* ---- analytic functions and powers (kernels.rs:876-895, :941-949) ------- */
 
 /* `Kernels::vector_unary` / `matrix_unary` (kernels.rs:876, :941): `op` (an

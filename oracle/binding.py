@@ -63,6 +63,8 @@ _SIGNATURES = {
     "or_correlate_input_gradient": ([u32, vp, u64, u64, vp, u64, u64, i32, vp], None),
     "or_pad": ([u32, vp, u64, u64, u64, u64, vp], None),
     "or_flip": ([u32, vp, u64, u64, vp], None),
+    "or_prefix_sum": ([u32, vp, u64, vp], None),
+    "or_sort": ([u32, vp, u64, u32, vp], None),
     "or_unary_dual": ([u32, u32, vp, vp, vp, vp, u64], None),
     "or_power": ([u32, vp, vp, vp, u64], None),
     "or_power_scalar": ([u32, vp, f32, i32, vp, u64], None),
@@ -355,4 +357,20 @@ def flip(x) -> np.ndarray:
     x = np.ascontiguousarray(x)
     out = np.zeros_like(x)
     load().or_flip(x.itemsize, _p(x), x.shape[0], x.shape[1], _p(out))
+    return out
+
+
+def prefix_sum(dtype, a) -> np.ndarray:
+    """Inclusive running total in f32, each output rounded to the type."""
+    a = np.ascontiguousarray(a)
+    out = np.zeros_like(a)
+    load().or_prefix_sum(dtype, _p(a), a.size, _p(out))
+    return out
+
+
+def sort(dtype, a, order) -> np.ndarray:
+    """`a` in IEEE totalOrder, `order` 0 ascending or 1 descending."""
+    a = np.ascontiguousarray(a)
+    out = np.zeros_like(a)
+    load().or_sort(dtype, _p(a), a.size, order, _p(out))
     return out

@@ -988,3 +988,57 @@ void or_flip(uint32_t width, const void* input, uint64_t rows, uint64_t cols, vo
         }
     }
 }
+
+/* ---- scans and sorts ----------------------------------------------------- */
+
+/* compact.rs:209-221 (the Host `Vector::prefix_sum`, vector.rs:578-589, for
+ * the three element types here): an inclusive running total kept in f32,
+ * left to right, each output rounded to the element type once. */
+void or_prefix_sum(uint32_t dtype, const void* a, uint64_t n, void* out) {
+    float running = 0.0f;
+    for (uint64_t i = 0; i < n; i++) {
+        running += widen_one(dtype, a, i);
+        narrow_one(dtype, out, i, running);
+    }
+}
+
+/* IEEE totalOrder on raw bit patterns of `bits` width (`total_cmp`,
+ * numbers/primitive.rs:70-72 via SortOrder::comparator, kernels.rs:259-266),
+ * from its definition: a set sign bit orders first; among two non-negative
+ * patterns the larger magnitude is larger; among two negative ones the larger
+ * magnitude is smaller.  NaNs sit beyond the infinities by sign and payload. */
+static int total_order(uint32_t x, uint32_t y, uint32_t bits) {
+    const uint32_t sign = 1u << (bits - 1);
+    const int nx = (x & sign) != 0, ny = (y & sign) != 0;
+    if (nx != ny) return nx ? -1 : 1;
+    const uint32_t mx = x & (sign - 1), my = y & (sign - 1);
+    if (mx == my) return 0;
+    if (nx) return mx > my ? -1 : 1;
+    return mx < my ? -1 : 1;
+}
+
+static int ascending32(const void* l, const void* r) {
+    return total_order(*(const uint32_t*)l, *(const uint32_t*)r, 32);
+}
+static int ascending16(const void* l, const void* r) {
+    return total_order(*(const uint16_t*)l, *(const uint16_t*)r, 16);
+}
+
+/* vector.rs:874-884 (`sort` / `sorted`): sort_unstable_by the order's
+ * comparator.  Elements equal under totalOrder are the same bit pattern, so
+ * an unstable sort fixes the output; descending is the ascending output
+ * reversed. */
+void or_sort(uint32_t dtype, const void* a, uint64_t n, uint32_t order, void* out) {
+    const size_t width = dtype == F32 ? 4 : 2;
+    memcpy(out, a, n * width);
+    qsort(out, n, width, width == 4 ? ascending32 : ascending16);
+    if (order == 1) {
+        uint8_t* o = (uint8_t*)out;
+        uint8_t tmp[4];
+        for (uint64_t i = 0, j = n ? n - 1 : 0; i < j; i++, j--) {
+            memcpy(tmp, o + i * width, width);
+            memcpy(o + i * width, o + j * width, width);
+            memcpy(o + j * width, tmp, width);
+        }
+    }
+}

@@ -160,6 +160,12 @@ void or_pad(uint32_t width, const void* input, uint64_t rows, uint64_t cols, uin
             void* out);
 void or_flip(uint32_t width, const void* input, uint64_t rows, uint64_t cols, void* out);
 
+/* The inclusive prefix sum, f32 running total rounded per output
+ * (compact.rs:209-221), and the sort in IEEE totalOrder, `order` 0
+ * ascending or 1 descending (vector.rs:874-884, kernels.rs:252-267). */
+void or_prefix_sum(uint32_t dtype, const void* a, uint64_t n, void* out);
+void or_sort(uint32_t dtype, const void* a, uint64_t n, uint32_t order, void* out);
+
 /* `Kernels::fused_sum`'s default (kernels.rs:1120-1135): the program's one
  * output, then `axis_sum` (fused/mod.rs:4045-4051), its products with ones:
  * axis 0 (Rows) a matvec, axis 1 (Columns) a vecmat. */

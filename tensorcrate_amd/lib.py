@@ -137,6 +137,8 @@ SIGNATURES = {
     "tc_vector_reduce": [u32, vp, u64, u32, vp],
     "tc_dot": [u32, vp, vp, u64, vp],
     "tc_moments": [u32, vp, u64, vp],
+    "tc_prefix_sum": [u32, vp, vp, u64],
+    "tc_sort": [u32, vp, vp, u64, u32],
     "tc_correlate": [u32, vp, u64, u64, vp, u64, u64, i32, vp],
     "tc_correlate_input_gradient": [u32, vp, u64, u64, vp, u64, u64, i32, vp],
     "tc_pad": [u32, vp, u64, u64, u64, u64, vp],
