@@ -313,6 +313,28 @@ int tc_moments(uint32_t dtype, const void* a, uint64_t n, float* result);
 int tc_axis_moments(uint32_t dtype, const void* a, uint64_t rows, uint64_t cols, uint32_t axis, void* means,
                     void* deviations);
 
+/* `Family` and `Statistic` (kernels.rs:536-590), the reference's u16 codes. */
+typedef enum tc_family { TC_NORMAL = 0, TC_INVERSE_GAUSSIAN = 1 } tc_family;
+typedef enum tc_statistic { TC_PDF = 0, TC_CDF = 1, TC_PPF = 2 } tc_statistic;
+
+/* `Kernels::vector_distribution` / `matrix_distribution` (kernels.rs:
+ * 1046-1059; Host statistics/mod.rs:649-651, :733-735): `statistic` of the
+ * `family` distribution with parameters (first, second) -- (mean, stddev)
+ * for the normal, (mean, shape) for the inverse Gaussian, each a `dtype`
+ * value widened exactly to f32 -- at each of the `n` elements, evaluated in
+ * f64 by the Host's methods (statistics/special.rs) and rounded once to f32,
+ * then to `dtype`.  Parameters that are not positive give NaNs. */
+int tc_distribution(uint32_t dtype, uint32_t family, uint32_t statistic, const void* a, void* out, uint64_t n,
+                    float first, float second);
+
+/* `Kernels::matrix_axis_distribution` (kernels.rs:1063-1070; Host
+ * `distribution_axis`, statistics/mod.rs:785-801, :582-600): as
+ * tc_distribution over the row-major rows x cols `a`, with the parameter
+ * pair of each element's row (`axis` TC_AXIS_ROWS: `first`/`second` hold
+ * `rows` device values of `dtype`) or column (TC_AXIS_COLUMNS: `cols`). */
+int tc_axis_distribution(uint32_t dtype, uint32_t family, uint32_t statistic, const void* a, uint64_t rows,
+                         uint64_t cols, uint32_t axis, const void* first, const void* second, void* out);
+
 /* `Kernels::dot` (kernels.rs:897): sum a[i]*b[i] into the device f32 scalar
  * `result`, unrounded. */
 int tc_dot(uint32_t dtype, const void* a, const void* b, uint64_t n, float* result);

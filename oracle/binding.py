@@ -23,6 +23,7 @@ NUMPY = {F32: np.float32, F16: np.float16, BF16: np.uint16}
 MAX_RANK = 6
 
 u32, u64, vp, f32, i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
+f64 = ctypes.c_double
 
 
 class Encoded(ctypes.Structure):
@@ -65,6 +66,12 @@ _SIGNATURES = {
     "or_flip": ([u32, vp, u64, u64, vp], None),
     "or_prefix_sum": ([u32, vp, u64, vp], None),
     "or_sort": ([u32, vp, u64, u32, vp], None),
+    "or_erf": ([f64], f64),
+    "or_erfc": ([f64], f64),
+    "or_normal_quantile": ([f64], f64),
+    "or_evaluate": ([u32, u32, f64, f64, f64], f64),
+    "or_distribution": ([u32, u32, u32, vp, vp, u64, f32, f32], None),
+    "or_axis_distribution": ([u32, u32, u32, vp, u64, u64, u32, vp, vp, vp], None),
     "or_unary_dual": ([u32, u32, vp, vp, vp, vp, u64], None),
     "or_power": ([u32, vp, vp, vp, u64], None),
     "or_power_scalar": ([u32, vp, f32, i32, vp, u64], None),
@@ -373,4 +380,28 @@ def sort(dtype, a, order) -> np.ndarray:
     a = np.ascontiguousarray(a)
     out = np.zeros_like(a)
     load().or_sort(dtype, _p(a), a.size, order, _p(out))
+    return out
+
+
+NORMAL, INVERSE_GAUSSIAN = 0, 1
+PDF, CDF, PPF = 0, 1, 2
+
+
+def evaluate(family, statistic, x, first, second) -> float:
+    """One distribution function in f64, unrounded."""
+    return load().or_evaluate(family, statistic, x, first, second)
+
+
+def distribution(dtype, family, statistic, a, first, second) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.zeros_like(a)
+    load().or_distribution(dtype, family, statistic, _p(a), _p(out), a.size, first, second)
+    return out
+
+
+def axis_distribution(dtype, family, statistic, a, axis, first, second) -> np.ndarray:
+    a, first, second = (np.ascontiguousarray(v) for v in (a, first, second))
+    rows, cols = a.shape
+    out = np.zeros_like(a)
+    load().or_axis_distribution(dtype, family, statistic, _p(a), rows, cols, axis, _p(first), _p(second), _p(out))
     return out

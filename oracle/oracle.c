@@ -1042,3 +1042,221 @@ void or_sort(uint32_t dtype, const void* a, uint64_t n, uint32_t order, void* ou
         }
     }
 }
+
+/* ---- distributions ------------------------------------------------------- */
+
+/* statistics/special.rs: every function in f64.  Cody's error function
+ * (special.rs:48-200, coefficient tables :101-113, :145-180) and Wichura's
+ * AS 241 quantile (:242-330), restated from the publications in the order the
+ * reference evaluates them. */
+
+static const double CODY_A[5] = {3.16112374387056560e00, 1.13864154151050156e02, 3.77485237685302021e02,
+                                 3.20937758913846947e03, 1.85777706184603153e-1};
+static const double CODY_B[4] = {2.36012909523441209e01, 2.44024637934444173e02, 1.28261652607737228e03,
+                                 2.84423683343917062e03};
+static const double CODY_C[9] = {5.64188496988670089e-1, 8.88314979438837594e00, 6.61191906371416295e01,
+                                 2.98635138197400131e02, 8.81952221241769090e02, 1.71204761263407058e03,
+                                 2.05107837782607147e03, 1.23033935479799725e03, 2.15311535474403846e-8};
+static const double CODY_D[8] = {1.57449261107098347e01, 1.17693950891312499e02, 5.37181101862009858e02,
+                                 1.62138957456669019e03, 3.29079923573345963e03, 4.36261909014324716e03,
+                                 3.43936767414372164e03, 1.23033935480374942e03};
+static const double CODY_P[6] = {3.05326634961232344e-1, 3.60344899949804439e-1, 1.25781726111229246e-1,
+                                 1.60837851487422766e-2, 6.58749161529837803e-4, 1.63153871373020978e-2};
+static const double CODY_Q[5] = {2.56852019228982242e00, 1.87295284992346047e00, 5.27905102951428412e-1,
+                                 6.05183413124413191e-2, 2.33520497626869185e-3};
+static const double PPND_A[8] = {3.3871328727963666080e0, 1.3314166789178437745e2, 1.9715909503065514427e3,
+                                 1.3731693765509461125e4, 4.5921953931549871457e4, 6.7265770927008700853e4,
+                                 3.3430575583588128105e4, 2.5090809287301226727e3};
+static const double PPND_B[7] = {4.2313330701600911252e1, 6.8718700749205790830e2, 5.3941960214247511077e3,
+                                 2.1213794301586595867e4, 3.9307895800092710610e4, 2.8729085735721942674e4,
+                                 5.2264952788528545610e3};
+static const double PPND_C[8] = {1.42343711074968357734e0, 4.63033784615654529590e0, 5.76949722146069140550e0,
+                                 3.64784832476320460504e0, 1.27045825245236838258e0, 2.41780725177450611770e-1,
+                                 2.27238449892691845833e-2, 7.74545014278341407640e-4};
+static const double PPND_D[7] = {2.05319162663775882187e0, 1.67638483018380384940e0, 6.89767334985100004550e-1,
+                                 1.48103976427480074590e-1, 1.51986665636164571966e-2, 5.47593808499534494600e-4,
+                                 1.05075007164441684324e-9};
+static const double PPND_E[8] = {6.65790464350110377720e0, 5.46378491116411436990e0, 1.78482653991729133580e0,
+                                 2.96560571828504891230e-1, 2.65321895265761230930e-2, 1.24266094738807843860e-3,
+                                 2.71155556874348757815e-5, 2.01033439929228813265e-7};
+static const double PPND_F[7] = {5.99832206555887937690e-1, 1.36929880922735805310e-1, 1.48753612908506148525e-2,
+                                 7.86869131145613259100e-4, 1.84631831751005468180e-5, 1.42151175831644588870e-7,
+                                 2.04426310338993978564e-15};
+
+/* special.rs:339-345: Horner from the constant term's end, starting at 0. */
+static double poly(const double* c, int n, double x) {
+    double total = 0.0;
+    for (int i = n - 1; i >= 0; i--) total = total * x + c[i];
+    return total;
+}
+
+/* special.rs:100-122 */
+static double erf_central(double x) {
+    double z = x * x, top = CODY_A[4] * z, bottom = z;
+    for (int i = 0; i < 3; i++) {
+        top = (top + CODY_A[i]) * z;
+        bottom = (bottom + CODY_B[i]) * z;
+    }
+    return x * (top + CODY_A[3]) / (bottom + CODY_B[3]);
+}
+
+/* special.rs:144-200 */
+static double erfc_scaled(double x) {
+    if (x <= 4.0) {
+        double top = CODY_C[8] * x, bottom = x;
+        for (int i = 0; i < 7; i++) {
+            top = (top + CODY_C[i]) * x;
+            bottom = (bottom + CODY_D[i]) * x;
+        }
+        return (top + CODY_C[7]) / (bottom + CODY_D[7]);
+    }
+    double z = 1.0 / (x * x), top = CODY_P[5] * z, bottom = z;
+    for (int i = 0; i < 4; i++) {
+        top = (top + CODY_P[i]) * z;
+        bottom = (bottom + CODY_Q[i]) * z;
+    }
+    double correction = z * (top + CODY_P[4]) / (bottom + CODY_Q[4]);
+    return (0.5641895835477563 - correction) / x;
+}
+
+/* special.rs:133-140 */
+static double erfc_positive(double x) {
+    if (x > 27.25) return 0.0;
+    double leading = trunc(x * 16.0) / 16.0;
+    double correction = (x - leading) * (x + leading);
+    return exp(-leading * leading) * exp(-correction) * erfc_scaled(x);
+}
+
+/* special.rs:48-60 */
+double or_erf(double x) {
+    if (isnan(x)) return x;
+    if (fabs(x) <= 0.46875) return erf_central(x);
+    double complement = 1.0 - erfc_positive(fabs(x));
+    return x < 0.0 ? -complement : complement;
+}
+
+/* special.rs:64-79 */
+double or_erfc(double x) {
+    if (isnan(x)) return x;
+    if (x < -0.46875) return 2.0 - erfc_positive(-x);
+    if (x <= 0.46875) return 1.0 - erf_central(x);
+    return erfc_positive(x);
+}
+
+/* special.rs:88-96 */
+static double ln_erfc(double x) {
+    if (isnan(x)) return x;
+    if (x <= 0.46875) return log(or_erfc(x));
+    return log(erfc_scaled(x)) - x * x;
+}
+
+/* special.rs:216-236 */
+static double std_pdf(double z) { return exp(-0.5 * z * z) / 2.5066282746310002; }
+static double std_cdf(double z) { return 0.5 * or_erfc(-z * 0.7071067811865476); }
+static double std_ln_cdf(double z) { return ln_erfc(-z * 0.7071067811865476) - 0.6931471805599453; }
+
+/* special.rs:242-331 */
+double or_normal_quantile(double p) {
+    if (isnan(p) || p < 0.0 || p > 1.0) return NAN;
+    if (p == 0.0) return -INFINITY;
+    if (p == 1.0) return INFINITY;
+    double q = p - 0.5;
+    if (fabs(q) <= 0.425) {
+        double r = 0.180625 - q * q;
+        return q * poly(PPND_A, 8, r) / (poly(PPND_B, 7, r) * r + 1.0);
+    }
+    double r = sqrt(-log(q < 0.0 ? p : 1.0 - p)), value;
+    if (r <= 5.0) {
+        r = r - 1.6;
+        value = poly(PPND_C, 8, r) / (poly(PPND_D, 7, r) * r + 1.0);
+    } else {
+        r = r - 5.0;
+        value = poly(PPND_E, 8, r) / (poly(PPND_F, 7, r) * r + 1.0);
+    }
+    return q < 0.0 ? -value : value;
+}
+
+/* special.rs:378-390 */
+static double wald_pdf(double x, double mean, double shape) {
+    if (x <= 0.0) return 0.0;
+    double deviation = x - mean;
+    double exponent = -shape * deviation * deviation / (2.0 * mean * mean * x);
+    return sqrt(shape / (2.0 * 3.141592653589793 * x * x * x)) * exp(exponent);
+}
+
+/* special.rs:397-410: Rust's f64::min returns the number when the sum is NaN,
+ * as fmin does. */
+static double wald_cdf(double x, double mean, double shape) {
+    if (x <= 0.0) return 0.0;
+    double scale = sqrt(shape / x), ratio = x / mean;
+    double lower = scale * (ratio - 1.0), upper = scale * (ratio + 1.0);
+    double tail = 2.0 * shape / mean + std_ln_cdf(-upper);
+    return fmin(std_cdf(lower) + exp(tail), 1.0);
+}
+
+/* special.rs:420-476 */
+static double wald_ppf(double p, double mean, double shape) {
+    if (isnan(p) || p < 0.0 || p > 1.0) return NAN;
+    if (p == 0.0) return 0.0;
+    if (p == 1.0) return INFINITY;
+    double low = 0.0, high = mean;
+    while (wald_cdf(high, mean, shape) < p) {
+        low = high;
+        high *= 2.0;
+        if (isinf(high)) return INFINITY;
+    }
+    double guess = 0.5 * (low + high);
+    for (int pass = 0; pass < 60; pass++) {
+        double error = wald_cdf(guess, mean, shape) - p;
+        if (error > 0.0) high = guess; else low = guess;
+        double density = wald_pdf(guess, mean, shape);
+        double step = density > 0.0 ? guess - error / density : NAN;
+        double next = (isfinite(step) && step > low && step < high) ? step : 0.5 * (low + high);
+        if (next == guess) break;
+        guess = next;
+    }
+    return guess;
+}
+
+/* `Distribution::evaluate` (statistics/mod.rs:273-297) with the family and
+ * statistic as codes: special.rs:348-370 for the normal, :378-476 for the
+ * inverse Gaussian, each guarded by its parameter checks (:334-336). */
+double or_evaluate(uint32_t family, uint32_t statistic, double x, double first, double second) {
+    if (family == 0) {
+        if (isnan(second) || second <= 0.0) return NAN;
+        if (statistic == 0) return std_pdf((x - first) / second) / second;
+        if (statistic == 1) return std_cdf((x - first) / second);
+        return first + second * or_normal_quantile(x);
+    }
+    if (!(first > 0.0) || !(second > 0.0)) return NAN;
+    if (statistic == 0) return wald_pdf(x, first, second);
+    if (statistic == 1) return wald_cdf(x, first, second);
+    return wald_ppf(x, first, second);
+}
+
+/* statistics/mod.rs:274-297's `cast` (`T::from`, half 2.7.1's `NumCast`
+ * for f16/bf16 converts through f32): f64 to f32 by round-to-nearest-even,
+ * then to the type. */
+static void store_double(uint32_t dtype, void* out, uint64_t i, double v) {
+    narrow_one(dtype, out, i, (float)v);
+}
+
+/* statistics/mod.rs:649-651 (`map` of `evaluate`). */
+void or_distribution(uint32_t dtype, uint32_t family, uint32_t statistic, const void* a, void* out, uint64_t n,
+                     float first, float second) {
+    for (uint64_t i = 0; i < n; i++) {
+        store_double(dtype, out, i, or_evaluate(family, statistic, widen_one(dtype, a, i), first, second));
+    }
+}
+
+/* statistics/mod.rs:582-600: element i takes the pair of its row
+ * (i / cols, `axis` 0) or column (i % cols, `axis` 1). */
+void or_axis_distribution(uint32_t dtype, uint32_t family, uint32_t statistic, const void* a, uint64_t rows,
+                          uint64_t cols, uint32_t axis, const void* first, const void* second, void* out) {
+    for (uint64_t i = 0; i < rows * cols; i++) {
+        uint64_t along = axis == 0 ? i / cols : i % cols;
+        double x = widen_one(dtype, a, i);
+        store_double(dtype, out, i,
+                     or_evaluate(family, statistic, x, widen_one(dtype, first, along), widen_one(dtype, second, along)));
+    }
+}

@@ -166,6 +166,20 @@ void or_flip(uint32_t width, const void* input, uint64_t rows, uint64_t cols, vo
 void or_prefix_sum(uint32_t dtype, const void* a, uint64_t n, void* out);
 void or_sort(uint32_t dtype, const void* a, uint64_t n, uint32_t order, void* out);
 
+/* The Host's special functions in f64 (statistics/special.rs) and the
+ * distribution members over them (statistics/mod.rs:273-297, :582-600,
+ * :649-651): `family` 0 normal (mean, stddev), 1 inverse Gaussian (mean,
+ * shape); `statistic` 0 pdf, 1 cdf, 2 ppf; results rounded to f32, then to
+ * `dtype`. */
+double or_erf(double x);
+double or_erfc(double x);
+double or_normal_quantile(double p);
+double or_evaluate(uint32_t family, uint32_t statistic, double x, double first, double second);
+void or_distribution(uint32_t dtype, uint32_t family, uint32_t statistic, const void* a, void* out, uint64_t n,
+                     float first, float second);
+void or_axis_distribution(uint32_t dtype, uint32_t family, uint32_t statistic, const void* a, uint64_t rows,
+                          uint64_t cols, uint32_t axis, const void* first, const void* second, void* out);
+
 /* `Kernels::fused_sum`'s default (kernels.rs:1120-1135): the program's one
  * output, then `axis_sum` (fused/mod.rs:4045-4051), its products with ones:
  * axis 0 (Rows) a matvec, axis 1 (Columns) a vecmat. */

@@ -138,6 +138,8 @@ SIGNATURES = {
     "tc_dot": [u32, vp, vp, u64, vp],
     "tc_moments": [u32, vp, u64, vp],
     "tc_prefix_sum": [u32, vp, vp, u64],
+    "tc_distribution": [u32, u32, u32, vp, vp, u64, f32, f32],
+    "tc_axis_distribution": [u32, u32, u32, vp, u64, u64, u32, vp, vp, vp],
     "tc_sort": [u32, vp, vp, u64, u32],
     "tc_correlate": [u32, vp, u64, u64, vp, u64, u64, i32, vp],
     "tc_correlate_input_gradient": [u32, vp, u64, u64, vp, u64, u64, i32, vp],
