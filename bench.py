@@ -161,6 +161,51 @@ def gemm(kind: str, m: int, k: int, n: int, seed: int, sigma, steps: int, warmup
     }
 
 
+def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> list[dict]:
+    """relu(x . w + bias) two ways: the program in the product kernel's
+    epilogue (`tc_matmul_epilogue`, one kernel, the product never in HBM)
+    and unfused (`tc_matmul`, then `tc_fused` over the stored product).
+    Both lines count the product's 2 m n k FLOP only."""
+    rng = np.random.default_rng(11)
+    code = KIND[kind]
+    size = 4 if kind == "f32" else 2
+    x = lib.Buffer.of(host_matrix(kind, m, k, rng, 1 / np.sqrt(k)))
+    w = lib.Buffer.of(host_matrix(kind, k, n, rng, 1 / np.sqrt(k)))
+    bias = lib.Buffer.of(host_matrix(kind, 1, n, rng).reshape(n))
+    out, product = lib.Buffer(m * n * size), lib.Buffer(m * n * size)
+    program = [(0, 0, 0, 0, code, 0, 0.0), (0, 1, 1, 1, code, 0, 0.0), (2, lib.ADD, 2, 0, 1, 0, 0.0),
+               (1, 0, 3, 0, 0, 0, 0.0), (4, lib.MAX, 4, 2, 3, 0, 0.0), (5, 0, 0, 4, code, 0, 0.0)]
+    enc, places = lib._program(program, [(0, 1, 1, [m], [n]), (0, 1, 0, [], [])])
+    bias_in, bias_len = lib._buffers([(bias, n)])
+    both_in, both_len = lib._buffers([(product, m * n), (bias, n)])
+    outs, out_lens = lib._buffers([(out, m * n)])
+
+    def fused():
+        lib.call("tc_matmul_epilogue", code, enc, len(program), places, 2, m, k, n, x.ptr, w.ptr, bias_in, bias_len,
+                 1, outs, out_lens, 1)
+
+    def unfused():
+        lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, x.ptr, w.ptr, product.ptr)
+        lib.call("tc_fused", code, enc, len(program), places, 2, both_in, both_len, 2, outs, out_lens, 1, m, n)
+
+    def product_only():
+        lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, x.ptr, w.ptr, product.ptr)
+
+    flops = 2.0 * m * n * k
+    lines = []
+    for name, fn in (("in the product's epilogue", fused), ("unfused: product, then program", unfused),
+                     ("the product alone", product_only)):
+        ms = timed(fn, steps, warmup)
+        achieved = flops / (ms * 1e-3) / 1e12
+        lines.append({"workload": f"{kind} dense layer relu(x w + b) {m}x{k}x{n}, {name}",
+                      "value": achieved, "unit": "TFLOP/s", "ms": ms,
+                      "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind],
+                                   "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK[kind], "traffic": None}})
+    for buffer in (x, w, bias, out, product):
+        buffer.free()
+    return lines
+
+
 def hbm_line(workload: str, nbytes: float, ms: float) -> dict:
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"workload": workload, "value": gbs, "unit": "GB/s", "ms": ms,
@@ -340,6 +385,10 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
     if "copies" in groups:
         log("broadcast chain and copies ...")
         workloads += broadcast_and_copies(steps, warmup)
+    if "fusion" in groups:
+        log("dense layers, fused and unfused ...")
+        workloads += dense_layer("bf16", 8192, 8192, 8192, steps, warmup)
+        workloads += dense_layer("f32", 4096, 1024, 4096, steps, warmup)
     if "mlp" in groups:
         log("MLP training step and Adam ...")
         # Three untimed steps: Adam's programs compile on their second
@@ -361,7 +410,7 @@ def main() -> int:
     parser.add_argument("--traffic-probe", action="store_true",
                         help="only the short copy + product run that HBM-traffic counters are read over")
     parser.add_argument("--only", default="",
-                        help="comma-separated secondary groups to run alone (gemm, reductions, copies, mlp); "
+                        help="comma-separated secondary groups to run alone (gemm, reductions, copies, fusion, mlp); "
                              "prints their lines as a JSON list instead of the headline line")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -376,7 +425,7 @@ def main() -> int:
 
     if args.only:
         groups = set(args.only.split(","))
-        unknown = groups - {"gemm", "reductions", "copies", "mlp"}
+        unknown = groups - {"gemm", "reductions", "copies", "fusion", "mlp"}
         if unknown:
             print(f"bench.py: no workload group {sorted(unknown)}", file=sys.stderr)
             return 2
@@ -390,7 +439,7 @@ def main() -> int:
     log(f"  {head['value']:.1f} TFLOP/s ({head['ms']:.3f} ms/step), kernel {head['roofline']['achieved']:.1f}")
     workloads = []
     if not args.quick:
-        workloads = secondary({"gemm", "reductions", "copies", "mlp"}, args.steps, args.warmup)
+        workloads = secondary({"gemm", "reductions", "copies", "fusion", "mlp"}, args.steps, args.warmup)
     baseline = None
     if not args.quick and not args.no_cpu:
         log("CPU baseline ...")

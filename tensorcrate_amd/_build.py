@@ -65,14 +65,24 @@ def _compile(source: Path, flags: list[str]) -> Path:
     return target
 
 
+# The headers the runtime compiler reads, each embedded as a C string: the
+# scalar operations every generated kernel calls, the element types and
+# operand addressing, and the product kernels a compiled epilogue is built
+# into.
+EMBEDDED = {"scalar_ops.h": "tc_scalar_ops_source", "device.hpp": "tc_device_source",
+            "gemm_kernels.hpp": "tc_gemm_kernels_source"}
+
+
 def _embedded_sources() -> Path:
-    """``scalar_ops.h`` as the C string ``tc_scalar_ops_source``: the header
-    the fused-program compiler hands hiprtc with every generated kernel."""
+    """The headers of ``EMBEDDED`` as C strings, for hiprtc at run time."""
     OBJECTS.mkdir(exist_ok=True)
-    text = (CSRC / "scalar_ops.h").read_text()
-    target = OBJECTS / "scalar_ops_source.cpp"
-    body = "".join(f"    {json.dumps(line + chr(10))}\n" for line in text.splitlines())
-    target.write_text('extern "C" const char tc_scalar_ops_source[] =\n' + body + "    ;\n")
+    target = OBJECTS / "embedded_sources.cpp"
+    parts = []
+    for header, symbol in EMBEDDED.items():
+        text = (CSRC / header).read_text()
+        body = "".join(f"    {json.dumps(line + chr(10))}\n" for line in text.splitlines())
+        parts.append(f'extern "C" const char {symbol}[] =\n' + body + "    ;\n")
+    target.write_text("".join(parts))
     return target
 
 
@@ -83,7 +93,7 @@ def build_library(jobs: int | None = None) -> Path:
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
         objects = list(pool.map(lambda s: _compile(s, HIP_FLAGS), sources))
-    embedded = OBJECTS / "scalar_ops_source.o"
+    embedded = OBJECTS / "embedded_sources.o"
     _run(["g++", "-O2", "-fPIC", "-c", str(_embedded_sources()), "-o", str(embedded)])
     staged = LIBRARY.with_suffix(".so.tmp")
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), str(embedded), "-lhiprtc",

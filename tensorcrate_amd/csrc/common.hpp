@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "../../include/tchip.h"
+#include "device.hpp"
 #include "scalar_ops.h"
 
 // The codes scalar_ops.h (which the runtime compiler also reads) uses are
@@ -23,6 +24,7 @@ static_assert(tc_ops::MIN == TC_MIN && tc_ops::MAX == TC_MAX && tc_ops::MAX_SHAR
                   tc_ops::GREATER_EQUAL == TC_GREATER_EQUAL,
               "Compare codes");
 static_assert(tc_ops::F32 == TC_F32 && tc_ops::F16 == TC_F16 && tc_ops::BF16 == TC_BF16, "DType codes");
+static_assert(tc::kPlaceLead == TC_FUSED_LEAD, "a place's folded axes");
 
 namespace tc {
 
@@ -51,44 +53,38 @@ int compute_units();
 int reduce_moments(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split, void* means,
                    void* deviations);
 
+// Everything `tc_fused` checks before a launch: the program's registers,
+// kinds and codes, and every load and store inside its buffer over a rows x
+// cols space (fused.hip).
+int check_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                uint32_t place_count, const uint64_t* input_lens, uint32_t input_count, const uint64_t* output_lens,
+                uint32_t output_count, uint64_t rows, uint64_t cols);
+
+// The product a . b (m x k by k x n, row-major, `dtype` operands) with the
+// checked program run over it in the product kernel's epilogue, input 0 the
+// product rounded to `dtype` (gemm.hip).  Sets `*fused` false, launching
+// nothing, when the product does not take the matrix-core kernels or the
+// program does not fit in kernel arguments.
+int matmul_program(uint32_t dtype, uint64_t m, uint64_t k, uint64_t n, const void* a, const void* b,
+                   const tc_encoded* code, uint32_t count, const tc_place* places, uint32_t place_count,
+                   const void* const* inputs, uint32_t input_count, void* const* outputs, uint32_t output_count,
+                   bool* fused);
+
+// Runtime compilation (fused.hip).  The straight-line body of an
+// epilogue's `group(live, row, col, N, product)` over `elems` elements, for
+// `code` computing in `dtype` with loads through `places` (their folded axes
+// are written into the source), its constants appended to `*constants`
+// (input 0 the product when `product_input`); and the kernels `kernels` of
+// `source`, compiled by hiprtc with the embedded headers on the source's
+// second request and cached for the process (false until then, or if it
+// does not compile).
+std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
+                           const tc_place* places, std::vector<float>* constants);
+bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out);
 
 std::string shape_text(const uint64_t* values, uint32_t rank);
 
-// ---- element types ----------------------------------------------------------
-
-__host__ __device__ inline float bf16_bits_to_f32(uint16_t bits) { return tc_bf16_to_f32(bits); }
-__host__ __device__ inline uint16_t f32_to_bf16_bits(float value) { return tc_f32_to_bf16(value); }
-
-struct bf16_t {
-    uint16_t bits;
-};
-
-// How a storage type widens to the f32 the kernels compute in, and rounds
-// back once.  f32 is the identity; f16 uses the hardware conversion, which
-// rounds to nearest even.
-template <typename S>
-struct Elem;
-
-template <>
-struct Elem<float> {
-    static constexpr int dtype = TC_F32;
-    __device__ static float widen(float v) { return v; }
-    __device__ static float narrow(float v) { return v; }
-};
-
-template <>
-struct Elem<_Float16> {
-    static constexpr int dtype = TC_F16;
-    __device__ static float widen(_Float16 v) { return static_cast<float>(v); }
-    __device__ static _Float16 narrow(float v) { return static_cast<_Float16>(v); }
-};
-
-template <>
-struct Elem<bf16_t> {
-    static constexpr int dtype = TC_BF16;
-    __device__ static float widen(bf16_t v) { return bf16_bits_to_f32(v.bits); }
-    __device__ static bf16_t narrow(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
-};
+// ---- element types (device.hpp) ---------------------------------------------
 
 inline size_t dtype_size(uint32_t dtype) {
     switch (dtype) {

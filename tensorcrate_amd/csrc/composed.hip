@@ -193,6 +193,26 @@ int tc_fused_sum(uint32_t dtype, const tc_encoded* code, uint32_t count, const t
     return tc_reduce_axes(dtype, data.ptr, n, &split, TC_AXIS_FOLD, TC_REDUCE_SUM, 0, out);
 }
 
+}  // extern "C"
+
+// Whether `p` reads element (row, col) of a row-major rows x cols matrix at
+// row * cols + col: no offset, unit column step, and lead axes that fold
+// the row index contiguously.
+static bool reads_in_order(const tc_place& p, uint64_t rows, uint64_t cols) {
+    if (p.offset != 0 || (p.col_step != 1 && cols > 1)) return false;
+    if (p.lead == 0) return rows <= 1;
+    if (p.lead > TC_FUSED_LEAD) return false;
+    uint64_t step = cols, folded = 1;
+    for (int d = static_cast<int>(p.lead) - 1; d >= 0; d--) {
+        if (p.dims[d] > 1 && p.steps[d] != step) return false;
+        step *= p.dims[d];
+        folded *= p.dims[d];
+    }
+    return folded == rows;
+}
+
+extern "C" {
+
 int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
                        uint32_t place_count, uint64_t m, uint64_t k, uint64_t n, const void* a, const void* b,
                        const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
@@ -201,8 +221,33 @@ int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, c
     if (input_count + 1 > TC_FUSED_MAX_INPUTS) {
         return fail(TC_INVALID, "fused program: " + std::to_string(input_count + 1) + " inputs, over the 16 limit");
     }
+    // fused/mod.rs:1185-1196: the product is input 0, read without a remap.
+    for (uint32_t pc = 0; pc < count; pc++) {
+        if (code[pc].kind == 0 && code[pc].a == 0) {
+            if (code[pc].op >= place_count || !reads_in_order(places[code[pc].op], m, n)) {
+                return fail(TC_INVALID, "fused matmul: the product is read through a remap");
+            }
+            if (code[pc].b != dtype) return fail(TC_INVALID, "fused matmul: the product is stored as the program's type");
+        }
+    }
     if (m == 0 || n == 0) return TC_OK;
     const uint64_t cells = m * n;
+    {
+        const void* all[TC_FUSED_MAX_INPUTS] = {};
+        uint64_t lens[TC_FUSED_MAX_INPUTS] = {};
+        lens[0] = cells;
+        for (uint32_t s = 0; s < input_count; s++) {
+            all[s + 1] = inputs[s];
+            lens[s + 1] = input_lens[s];
+        }
+        int status = check_fused(dtype, code, count, places, place_count, lens, input_count + 1, output_lens,
+                                 output_count, m, n);
+        if (status != TC_OK) return status;
+        bool fused = false;
+        status = matmul_program(dtype, m, k, n, a, b, code, count, places, place_count, all, input_count + 1, outputs,
+                                output_count, &fused);
+        if (status != TC_OK || fused) return status;
+    }
     Scratch product(cells * dtype_size(dtype));
     if (product.status != TC_OK) return product.status;
     int status = tc_matmul(dtype, dtype, TC_PLAIN, 0, m, k, n, a, b, product.ptr);

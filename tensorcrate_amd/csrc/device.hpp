@@ -1,0 +1,102 @@
+// The device-side element types and operand addressing shared by the
+// library's kernels and the kernels the runtime compiler builds from
+// generated source (fused programs, product epilogues).  It includes only
+// scalar_ops.h, so hiprtc can read it as it is.
+#pragma once
+
+#if defined(__HIPCC_RTC__)
+using __hip_internal::uint16_t;
+using __hip_internal::uint32_t;
+using __hip_internal::uint64_t;
+using __hip_internal::uint8_t;
+#else
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#endif
+
+#include "scalar_ops.h"
+
+namespace tc {
+
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t bits) { return tc_bf16_to_f32(bits); }
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float value) { return tc_f32_to_bf16(value); }
+
+struct bf16_t {
+    uint16_t bits;
+};
+
+// How a storage type widens to the f32 the kernels compute in, and rounds
+// back once.  f32 is the identity; f16 uses the hardware conversion, which
+// rounds to nearest even.
+template <typename S>
+struct Elem;
+
+template <>
+struct Elem<float> {
+    static constexpr int dtype = tc_ops::F32;
+    __device__ static float widen(float v) { return v; }
+    __device__ static float narrow(float v) { return v; }
+};
+
+template <>
+struct Elem<_Float16> {
+    static constexpr int dtype = tc_ops::F16;
+    __device__ static float widen(_Float16 v) { return static_cast<float>(v); }
+    __device__ static _Float16 narrow(float v) { return static_cast<_Float16>(v); }
+};
+
+template <>
+struct Elem<bf16_t> {
+    static constexpr int dtype = tc_ops::BF16;
+    __device__ static float widen(bf16_t v) { return bf16_bits_to_f32(v.bits); }
+    __device__ static bf16_t narrow(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+};
+
+// ---- fused-program operands ---------------------------------------------------
+
+constexpr int kPlaceLead = 5;  // a place's folded row axes (TC_FUSED_LEAD)
+
+// A load's place in device form (`Place`, fused/mod.rs:3230-3268): element
+// (row, col) reads offset + col * col_step plus the row index spread over
+// up to five folded axes.
+struct DevicePlace {
+    uint64_t offset;
+    uint64_t col_step;
+    uint32_t lead;
+    uint32_t pad;
+    uint64_t dims[kPlaceLead];
+    uint64_t steps[kPlaceLead];
+};
+
+// The storage element element (row, col) reads through `place`
+// (fused/mod.rs:3254-3268).
+__device__ __forceinline__ uint64_t place_at(const DevicePlace& p, uint64_t row, uint64_t col) {
+    uint64_t at = p.offset + col * p.col_step;
+    if (p.lead == 1) return at + row * p.steps[0];
+    if (p.lead > 1) {
+        for (int k = static_cast<int>(p.lead) - 1; k > 0; k--) {
+            at += (row % p.dims[k]) * p.steps[k];
+            row /= p.dims[k];
+        }
+        at += row * p.steps[0];
+    }
+    return at;
+}
+
+__device__ __forceinline__ float load_as(const void* base, uint32_t dtype, uint64_t index) {
+    switch (dtype) {
+        case tc_ops::F16: return static_cast<float>(static_cast<const _Float16*>(base)[index]);
+        case tc_ops::BF16: return bf16_bits_to_f32(static_cast<const uint16_t*>(base)[index]);
+        default: return static_cast<const float*>(base)[index];
+    }
+}
+
+__device__ __forceinline__ void store_as(void* base, uint32_t dtype, uint64_t index, float v) {
+    switch (dtype) {
+        case tc_ops::F16: static_cast<_Float16*>(base)[index] = static_cast<_Float16>(v); break;
+        case tc_ops::BF16: static_cast<uint16_t*>(base)[index] = f32_to_bf16_bits(v); break;
+        default: static_cast<float*>(base)[index] = v; break;
+    }
+}
+
+}  // namespace tc

@@ -28,162 +28,10 @@
 #include <unordered_map>
 
 #include "common.hpp"
+#include "program.hpp"
 
 namespace tc {
 namespace {
-
-constexpr int kLanesPerThread = 4;
-
-struct DevicePlace {
-    uint64_t offset;
-    uint64_t col_step;
-    uint32_t lead;
-    uint32_t pad;
-    uint64_t dims[TC_FUSED_LEAD];
-    uint64_t steps[TC_FUSED_LEAD];
-};
-
-template <int T>
-__device__ __forceinline__ float round_to(float v) {
-    return tc_round<T>(v);
-}
-
-__device__ __forceinline__ float load_as(const void* base, uint32_t dtype, uint64_t index) {
-    switch (dtype) {
-        case TC_F16: return static_cast<float>(static_cast<const _Float16*>(base)[index]);
-        case TC_BF16: return bf16_bits_to_f32(static_cast<const uint16_t*>(base)[index]);
-        default: return static_cast<const float*>(base)[index];
-    }
-}
-
-__device__ __forceinline__ void store_as(void* base, uint32_t dtype, uint64_t index, float v) {
-    switch (dtype) {
-        case TC_F16: static_cast<_Float16*>(base)[index] = static_cast<_Float16>(v); break;
-        case TC_BF16: static_cast<uint16_t*>(base)[index] = f32_to_bf16_bits(v); break;
-        default: static_cast<float*>(base)[index] = v; break;
-    }
-}
-
-__device__ __forceinline__ float analytic_value(uint32_t op, float x) { return tc_analytic(op, x); }
-
-// The storage element element (row, col) reads through `place`
-// (fused/mod.rs:3254-3268).
-__device__ __forceinline__ uint64_t place_at(const DevicePlace& p, uint64_t row, uint64_t col) {
-    uint64_t at = p.offset + col * p.col_step;
-    if (p.lead == 1) return at + row * p.steps[0];
-    if (p.lead > 1) {
-        for (int k = static_cast<int>(p.lead) - 1; k > 0; k--) {
-            at += (row % p.dims[k]) * p.steps[k];
-            row /= p.dims[k];
-        }
-        at += row * p.steps[0];
-    }
-    return at;
-}
-
-struct Buffers {
-    const void* inputs[TC_FUSED_MAX_INPUTS];
-    void* outputs[TC_FUSED_MAX_OUTPUTS];
-};
-
-// A program small enough to travel in the kernel's argument segment, where
-// the scalar unit reads it directly; larger ones are read from a device
-// block.  Either way every instruction and place is fetched by scalar loads
-// at a wave-uniform index, so the opcode, the register numbers and the
-// place are SGPR values and every lane runs the same instruction.
-constexpr int kInlineCode = 48;
-constexpr int kInlinePlaces = 8;
-
-struct Inline {
-    tc_encoded code[kInlineCode];
-    DevicePlace places[kInlinePlaces];
-};
-
-// The interpreter's register file: one 16-wide vector register per element
-// a thread runs, indexed only by uniform register numbers, so each stays in
-// VGPRs (indexed moves) rather than going to scratch memory.
-typedef float Regs16 __attribute__((ext_vector_type(TC_FUSED_REGISTERS)));
-
-struct Registers {
-    Regs16 r[kLanesPerThread];
-    template <int V>
-    __device__ __forceinline__ float get(uint32_t i) const {
-        return r[V][i];
-    }
-    template <int V>
-    __device__ __forceinline__ void set(uint32_t i, float v) {
-        r[V][i] = v;
-    }
-};
-
-// The rare analytic functions, kept out of line so the interpreter's hot
-// path stays small; `Sqrt`, the one Adam runs, is inline.
-__device__ __noinline__ float analytic_slow(uint32_t op, float x) { return analytic_value(op, x); }
-
-// Every element of one instruction, dispatched once on the (uniform) kind and
-// operation, then applied to each of a thread's elements.
-#define TC_EACH(body)                        \
-    {                                        \
-        constexpr int V = 0;                 \
-        body;                                \
-    }                                        \
-    {                                        \
-        constexpr int V = 1;                 \
-        body;                                \
-    }                                        \
-    {                                        \
-        constexpr int V = 2;                 \
-        body;                                \
-    }                                        \
-    {                                        \
-        constexpr int V = 3;                 \
-        body;                                \
-    }
-
-template <int T>
-__device__ __forceinline__ void run(Registers& regs, const tc_encoded& in, const DevicePlace* place,
-                                    const Buffers& buffers, const bool (&live)[kLanesPerThread],
-                                    const uint64_t (&row)[kLanesPerThread], const uint64_t (&col)[kLanesPerThread],
-                                    const uint64_t (&element)[kLanesPerThread]) {
-    static_assert(kLanesPerThread == 4, "TC_EACH covers four elements");
-    switch (in.kind) {
-        case 0: {  // load
-            const void* src = buffers.inputs[in.a];
-            TC_EACH(regs.set<V>(in.dst, live[V] ? round_to<T>(load_as(src, in.b, place_at(*place, row[V], col[V])))
-                                                : 0.0f));
-            break;
-        }
-        case 1:  // const: a T value, which f32 holds exactly
-            TC_EACH(regs.set<V>(in.dst, in.value));
-            break;
-        case 2:
-            switch (in.op) {
-                case TC_ADD: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) + regs.get<V>(in.b)))); break;
-                case TC_SUB: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) - regs.get<V>(in.b)))); break;
-                case TC_MUL: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) * regs.get<V>(in.b)))); break;
-                case TC_DIV: TC_EACH(regs.set<V>(in.dst, round_to<T>(regs.get<V>(in.a) / regs.get<V>(in.b)))); break;
-                default: TC_EACH(regs.set<V>(in.dst, round_to<T>(fmodf(regs.get<V>(in.a), regs.get<V>(in.b))))); break;
-            }
-            break;
-        case 3:
-            if (in.op == 13) {
-                TC_EACH(regs.set<V>(in.dst, round_to<T>(sqrtf(regs.get<V>(in.a)))));
-            } else {
-                TC_EACH(regs.set<V>(in.dst, round_to<T>(analytic_slow(in.op, regs.get<V>(in.a)))));
-            }
-            break;
-        case 4:
-            TC_EACH(regs.set<V>(in.dst, round_to<T>(compare_value(in.op, regs.get<V>(in.a), regs.get<V>(in.b)))));
-            break;
-        default: {  // store
-            void* dst = buffers.outputs[in.aux];
-            TC_EACH(if (live[V]) store_as(dst, in.b, element[V], regs.get<V>(in.a)));
-            break;
-        }
-    }
-}
-
-#undef TC_EACH
 
 template <int T, bool INLINE>
 __global__ void __launch_bounds__(256) fused_kernel(Inline small_program, const tc_encoded* __restrict__ code,
@@ -349,7 +197,10 @@ bool dense_plan(const tc_encoded* code, uint32_t count, const tc_place* places, 
 // kernels are cached by their source for the life of the process.  The
 // runtime compiler is hiprtc, with this library's own code-generation flags.
 
-extern "C" const char tc_scalar_ops_source[];  // scalar_ops.h, embedded by the build
+// The headers hiprtc reads, embedded by the build.
+extern "C" const char tc_scalar_ops_source[];
+extern "C" const char tc_device_source[];
+extern "C" const char tc_gemm_kernels_source[];
 
 constexpr int kCompiledConstants = kInlineCode;
 
@@ -458,7 +309,7 @@ struct Compiled {
     uint32_t seen = 0;
     bool failed = false;
     hipModule_t module = nullptr;
-    hipFunction_t function = nullptr;
+    std::vector<hipFunction_t> functions;
 };
 
 std::mutex compiled_mutex;
@@ -469,22 +320,35 @@ uint64_t compiled_count = 0;
 const char* const kCompileFlags[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
                                      "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
 
-bool compile_program(const std::string& source, Compiled* out) {
+// Compile `source` with the embedded headers and look up `kernels`, each an
+// extern "C" name or a template-id whose lowered name hiprtc reports.
+bool compile_program(const std::string& source, const std::vector<std::string>& kernels, Compiled* out) {
     hiprtcProgram program;
-    const char* headers[] = {tc_scalar_ops_source};
-    const char* names[] = {"scalar_ops.h"};
-    if (hiprtcCreateProgram(&program, source.c_str(), "tc_fused_program.hip", 1, headers, names) != HIPRTC_SUCCESS) {
+    const char* headers[] = {tc_scalar_ops_source, tc_device_source, tc_gemm_kernels_source};
+    const char* names[] = {"scalar_ops.h", "device.hpp", "gemm_kernels.hpp"};
+    if (hiprtcCreateProgram(&program, source.c_str(), "tc_fused_program.hip", 3, headers, names) != HIPRTC_SUCCESS) {
         return false;
+    }
+    for (const std::string& kernel : kernels) {
+        if (kernel.find('<') != std::string::npos) (void)hiprtcAddNameExpression(program, kernel.c_str());
     }
     bool ok = hiprtcCompileProgram(program, sizeof(kCompileFlags) / sizeof(kCompileFlags[0]), kCompileFlags) ==
               HIPRTC_SUCCESS;
     std::vector<char> binary;
+    std::vector<std::string> lowered;
     if (ok) {
         size_t size = 0;
         ok = hiprtcGetCodeSize(program, &size) == HIPRTC_SUCCESS && size > 0;
         if (ok) {
             binary.resize(size);
             ok = hiprtcGetCode(program, binary.data()) == HIPRTC_SUCCESS;
+        }
+        for (const std::string& kernel : kernels) {
+            const char* name = kernel.c_str();
+            if (ok && kernel.find('<') != std::string::npos) {
+                ok = hiprtcGetLoweredName(program, kernel.c_str(), &name) == HIPRTC_SUCCESS;
+            }
+            lowered.push_back(ok ? std::string(name) : std::string());
         }
     }
     hiprtcDestroyProgram(&program);
@@ -493,11 +357,101 @@ bool compile_program(const std::string& source, Compiled* out) {
         (void)hipGetLastError();
         return false;
     }
-    if (hipModuleGetFunction(&out->function, out->module, "tc_fused_program") != hipSuccess) {
-        (void)hipGetLastError();
-        return false;
+    for (const std::string& name : lowered) {
+        hipFunction_t function = nullptr;
+        if (hipModuleGetFunction(&function, out->module, name.c_str()) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        out->functions.push_back(function);
     }
     return true;
+}
+
+// The cached kernels of `source` for this device, compiled on the source's
+// second request; false (run something else) before that or if it does not
+// compile.
+bool cached_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out) {
+    int device = 0;
+    (void)hipGetDevice(&device);
+    std::lock_guard<std::mutex> lock(compiled_mutex);
+    Compiled& entry = compiled_programs["device " + std::to_string(device) + "\n" + source];
+    if (entry.failed) return false;
+    if (entry.functions.empty()) {
+        if (++entry.seen < 2) return false;
+        if (!compile_program(source, kernels, &entry)) {
+            entry.failed = true;
+            return false;
+        }
+        compiled_count++;
+    }
+    for (size_t k = 0; k < entry.functions.size(); k++) out[k] = entry.functions[k];
+    return true;
+}
+
+// The straight-line form of a program over `elems` of a thread's elements:
+// the body of an epilogue's `group(live, row, col, N, product)`, each
+// value a local, each load through `places[j]` of the epilogue's arguments,
+// each constant from `constants[]` (appended to `*constants`).  With
+// `product_input`, input 0 is the product rather than a load.
+std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
+                       const tc_place* places, std::vector<float>* constants) {
+    static const char* const kBinary[] = {"+", "-", "*", "/"};
+    const std::string round = "tc_round<" + std::to_string(dtype) + ">";
+    std::ostringstream src;
+    std::string reg[TC_FUSED_REGISTERS];
+    auto at = [&](uint8_t r) { return reg[r].empty() ? std::string("0.0f") : reg[r] + "[e]"; };
+    const std::string each = "    for (int e = 0; e < " + std::to_string(elems) + "; e++) ";
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind == 5) {
+            src << each << "if (live[e]) tc::store_as(out[" << int(in.aux) << "], " << int(in.b)
+                << "u, (uint64_t)row[e] * N + col[e], " << at(in.a) << ");\n";
+            continue;
+        }
+        const std::string v = "v" + std::to_string(pc);
+        src << "    float " << v << "[" << elems << "];\n" << each << v << "[e] = ";
+        switch (in.kind) {
+            case 0:
+                if (product_input && in.a == 0) {
+                    src << "live[e] ? " << round << "(product[e]) : 0.0f;\n";
+                } else {
+                    // Every lane loads, an element outside C at (0, 0), so
+                    // no load waits on a branch; the place's row walk is
+                    // written out for the usual one or no folded axes.
+                    const std::string p = "places[" + std::to_string(in.op) + "]";
+                    const std::string r = "(live[e] ? row[e] : 0u)", c = "(live[e] ? col[e] : 0u)";
+                    std::string index = p + ".offset + (uint64_t)" + c + " * " + p + ".col_step";
+                    if (places[in.op].lead == 1) {
+                        index += " + (uint64_t)" + r + " * " + p + ".steps[0]";
+                    } else if (places[in.op].lead > 1) {
+                        index = "tc::place_at(" + p + ", " + r + ", " + c + ")";
+                    }
+                    src << "live[e] ? " << round << "(tc::load_as(in[" << int(in.a) << "], " << int(in.b) << "u, "
+                        << index << ")) : 0.0f;\n";
+                }
+                break;
+            case 1:
+                src << "constants[" << constants->size() << "];\n";
+                constants->push_back(in.value);
+                break;
+            case 2:
+                if (in.op == TC_REM) {
+                    src << round << "(fmodf(" << at(in.a) << ", " << at(in.b) << "));\n";
+                } else {
+                    src << round << "(" << at(in.a) << " " << kBinary[in.op] << " " << at(in.b) << ");\n";
+                }
+                break;
+            case 3:
+                src << round << "(tc_analytic(" << int(in.op) << "u, " << at(in.a) << "));\n";
+                break;
+            default:
+                src << round << "(tc_compare(" << int(in.op) << "u, " << at(in.a) << ", " << at(in.b) << "));\n";
+                break;
+        }
+        reg[in.dst] = v;
+    }
+    return src.str();
 }
 
 // Run `code` compiled when it has been seen before and compiles; false when
@@ -505,26 +459,11 @@ bool compile_program(const std::string& source, Compiled* out) {
 bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const DenseLoads& loads,
                   uint32_t load_count, const Buffers& buffers, uint64_t chunks, hipStream_t s, int* status) {
     std::vector<float> constants;
-    int device = 0;
-    (void)hipGetDevice(&device);
     const bool stream = chunks * dense_chunk_bytes(code, count) > kStreamBytes;
     const std::string source = dense_source(code, count, dtype, stream, &constants);
     if (constants.size() > static_cast<size_t>(kCompiledConstants)) return false;
     hipFunction_t function = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(compiled_mutex);
-        Compiled& entry = compiled_programs["device " + std::to_string(device) + "\n" + source];
-        if (entry.failed) return false;
-        if (entry.function == nullptr) {
-            if (++entry.seen < 2) return false;
-            if (!compile_program(source, &entry)) {
-                entry.failed = true;
-                return false;
-            }
-            compiled_count++;
-        }
-        function = entry.function;
-    }
+    if (!cached_kernels(source, {"tc_fused_program"}, &function)) return false;
     CompiledArgs args{};
     for (uint32_t j = 0; j < load_count; j++) args.in[j] = loads.base[j];
     for (int k = 0; k < TC_FUSED_MAX_OUTPUTS; k++) args.out[k] = buffers.outputs[k];
@@ -571,6 +510,16 @@ int check_program(const tc_encoded* code, uint32_t count, uint32_t place_count, 
 }
 
 }  // namespace
+
+std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
+                           const tc_place* places, std::vector<float>* constants) {
+    return group_body(code, count, dtype, product_input, elems, places, constants);
+}
+
+bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out) {
+    return cached_kernels(source, kernels, out);
+}
+
 }  // namespace tc
 
 using namespace tc;
@@ -594,15 +543,13 @@ static bool place_end(const tc_place& p, uint64_t rows, uint64_t cols, uint64_t*
     return reach(rank, shape, p.offset, strides, end);
 }
 
-extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
-                        uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
-                        uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
-                        uint32_t output_count, uint64_t rows, uint64_t cols) {
+int tc::check_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                    uint32_t place_count, const uint64_t* input_lens, uint32_t input_count,
+                    const uint64_t* output_lens, uint32_t output_count, uint64_t rows, uint64_t cols) {
     int status = check_program(code, count, place_count, input_count, output_count);
     if (status != TC_OK) return status;
     if (dtype > TC_BF16) return fail(TC_UNSUPPORTED, std::string("fused program: no kernel computes in ") + dtype_name(dtype));
-    TC_STREAM(s);
-    if (rows == 0 || cols == 0 || count == 0) return TC_OK;
+    if (rows == 0 || cols == 0) return TC_OK;
     // Every load stays inside its input and every store inside its output.
     for (uint32_t pc = 0; pc < count; pc++) {
         const tc_encoded& in = code[pc];
@@ -620,6 +567,18 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
                                         std::to_string(rows * cols));
         }
     }
+    return TC_OK;
+}
+
+extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                        uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                        uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
+                        uint32_t output_count, uint64_t rows, uint64_t cols) {
+    int status = check_fused(dtype, code, count, places, place_count, input_lens, input_count, output_lens,
+                             output_count, rows, cols);
+    if (status != TC_OK) return status;
+    TC_STREAM(s);
+    if (rows == 0 || cols == 0 || count == 0) return TC_OK;
     Buffers buffers{};
     for (uint32_t k = 0; k < input_count; k++) buffers.inputs[k] = inputs[k];
     for (uint32_t k = 0; k < output_count; k++) buffers.outputs[k] = outputs[k];
@@ -639,21 +598,8 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
         return check_launch("fused program");
     }
     std::vector<DevicePlace> device_places(place_count);
-    for (uint32_t k = 0; k < place_count; k++) {
-        DevicePlace& p = device_places[k];
-        p = DevicePlace{};
-        p.offset = places[k].offset;
-        p.col_step = places[k].col_step;
-        p.lead = places[k].lead;
-        if (p.lead > TC_FUSED_LEAD) return fail(TC_INVALID, "fused program: a place folds more than 5 axes");
-        for (int d = 0; d < TC_FUSED_LEAD; d++) {
-            p.dims[d] = places[k].dims[d];
-            p.steps[d] = places[k].steps[d];
-            if (d < static_cast<int>(p.lead) && p.dims[d] == 0) {
-                return fail(TC_INVALID, "fused program: a place has an empty axis");
-            }
-        }
-    }
+    status = to_device_places(places, place_count, device_places.data());
+    if (status != TC_OK) return status;
     const uint64_t total = rows * cols;
     const bool small = total <= UINT32_MAX && cols <= UINT32_MAX;
     DivMod cols_div(small ? static_cast<uint32_t>(cols) : 1u);

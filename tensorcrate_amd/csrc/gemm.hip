@@ -38,93 +38,52 @@
 // first spread so that the blocks one XCD runs are neighbours, which keeps
 // each XCD's L2 working on a few A and B panels.
 
+#include <string.h>
+
 #include <type_traits>
 
 #include "common.hpp"
+#include "gemm_kernels.hpp"
+#include "program.hpp"
 
 namespace tc {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+// The program epilogue interpreted: the fused programs' interpreter over the
+// tile's staged products, instruction by instruction.
+template <int T>
+struct ProgramStore {
+    static constexpr bool kProgram = true;
+    static constexpr int kElems = kLanesPerThread;
+    Inline program;
+    Buffers buffers;
+    uint32_t count;
 
-// The descriptor word that makes a gfx9-family buffer resource a plain,
-// untyped byte range (32-bit data format, no swizzle, no stride).
-constexpr int kBufferFlags = 0x00020000;
-
-constexpr int kBM = 256;
-constexpr int kBN = 128;
-constexpr int kThreads = 256;
-constexpr int kGroupM = 8;  // block-tile rows per ordering group
-
-template <typename S>
-struct Mfma16;
-template <>
-struct Mfma16<bf16_t> {
-    __device__ static f32x16 step(uint4 a, uint4 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    }
-};
-template <>
-struct Mfma16<_Float16> {
-    __device__ static f32x16 step(uint4 a, uint4 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-    }
-};
-
-// The block tile a block computes, from its linear index: spread across the
-// XCDs first (hardware hands consecutive blocks to consecutive XCDs), then
-// grouped so that neighbouring blocks share rows of A.
-__device__ __forceinline__ void tile_of(uint32_t block, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm,
-                                        uint32_t& tn) {
-    const uint32_t total = tiles_m * tiles_n;
-    constexpr uint32_t kXcds = 8;
-    if (total % kXcds == 0) {
-        block = (block % kXcds) * (total / kXcds) + block / kXcds;
-    }
-    const uint32_t per_group = kGroupM * tiles_n;
-    const uint32_t group = block / per_group;
-    const uint32_t first_m = group * kGroupM;
-    const uint32_t rows = min(tiles_m - first_m, static_cast<uint32_t>(kGroupM));
-    const uint32_t in_group = block - group * per_group;
-    tm = first_m + in_group % rows;
-    tn = in_group / rows;
-}
-
-// 16 bytes of row `row`, from column `k`, of a K-contiguous operand with
-// `rows` rows of `K` elements of `E` bytes; zeros outside it.  `fast` says the
-// whole operand is 16-byte aligned row by row.
-template <int E>
-__device__ __forceinline__ uint4 load16(const uint8_t* base, uint32_t row, uint32_t k, uint32_t rows,
-                                        uint32_t K, bool fast) {
-    constexpr uint32_t per = 16 / E;
-    if (row < rows && fast && k + per <= K) {
-        return *reinterpret_cast<const uint4*>(base + (static_cast<uint64_t>(row) * K + k) * E);
-    }
-    uint8_t bytes[16] = {};
-    if (row < rows) {
-        for (uint32_t e = 0; e < per; e++) {
-            if (k + e < K) {
-                const uint8_t* at = base + (static_cast<uint64_t>(row) * K + k + e) * E;
-                for (int b = 0; b < E; b++) bytes[e * E + b] = at[b];
+    __device__ __forceinline__ void group(const bool (&live)[4], const uint32_t (&rows)[4], const uint32_t (&cols)[4],
+                                          uint32_t N, const float (&product)[4]) const {
+        uint64_t row[4], col[4], element[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            row[v] = rows[v];
+            col[v] = cols[v];
+            element[v] = row[v] * N + col[v];
+        }
+        Registers regs;
+        for (uint32_t pc = 0; pc < count; pc++) {
+            const tc_encoded in = program.code[pc];
+            float value[4];
+            bool writes = true;
+            if (in.kind == 0 && in.a == 0) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) value[v] = live[v] ? round_to<T>(product[v]) : 0.0f;
+            } else {
+                writes = evaluate<T>(regs, in, in.kind == 0 ? &program.places[in.op] : nullptr, buffers, live, row,
+                                     col, element, value);
             }
+            if (writes) write(regs, in.dst, value);
         }
     }
-    uint4 out;
-    __builtin_memcpy(&out, bytes, 16);
-    return out;
-}
-
-template <typename O>
-__device__ __forceinline__ void store_out(O* c, uint64_t at, float v, bool accumulate) {
-    using E = Elem<O>;
-    if (accumulate) v += E::widen(c[at]);
-    c[at] = E::narrow(v);
-}
+};
 
 // ---- 16-bit operands ------------------------------------------------------------
 
@@ -226,8 +185,6 @@ __global__ void __launch_bounds__(kThreads) gemm16_kernel(const S* __restrict__ 
 
 // ---- f32 operands ------------------------------------------------------------------
 
-constexpr int kBK32 = 32;
-constexpr int kLd32 = kBK32 + 4;
 
 template <typename O>
 __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restrict__ A, const float* __restrict__ Bt,
@@ -323,467 +280,36 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
     }
 }
 
-// ---- f32 operands in place ---------------------------------------------------------
-//
-// The f32 product with each operand read in its stored orientation, as the
-// 16-bit kernel does, so `matmul_transposed_add` (the tape's backward
-// products) and a plain `matmul` pay for no transpose pass.  A lane's four k
-// for one tile row come from one ds_read_b128 of a K-contiguous tile, or
-// four ds_read_b32 down a row-contiguous tile ([k][rows + 4]: the 4-float
-// pad puts the four k-rows a wave reads on distinct bank quarters).  HBM is
-// staged through buffer loads (zeros past the operand) into registers and
-// then LDS, double-buffered, 256 x 128 or 128 x 128 tiles, 32-deep steps,
-// four waves of a quarter tile.  Requirements as for the 16-bit kernel, with K (K-contiguous)
-// or the contiguous extent (row-contiguous) a multiple of 4.
-
-template <int ROWS, bool KC>
-struct Stager32 {
-    static constexpr int kRowChunks = KC ? kBK32 / 4 : ROWS / 4;  // 16-byte chunks per tile row
-    static constexpr int kPassRows = kThreads / kRowChunks;
-    static constexpr int kPasses = (KC ? ROWS : kBK32) / kPassRows;
-    static constexpr int kLdsRow = KC ? kLd32 : ROWS + 4;
-    __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t offset, pass_bytes, k_bytes, lds_at, k_in;
-
-    __device__ void init(const float* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int t) {
-        const uint32_t row = t / kRowChunks, part = (t % kRowChunks) * 4;
-        if (KC) {
-            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + static_cast<uint64_t>(first) * ld), 0,
-                                                     (rows - first) * ld * 4, kBufferFlags);
-            k_bytes = 4;
-            k_in = part;
-        } else {
-            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + first), 0, (depth * ld - first) * 4,
-                                                     kBufferFlags);
-            k_bytes = ld * 4;
-            k_in = 0;
-        }
-        offset = (row * ld + part) * 4;
-        pass_bytes = kPassRows * ld * 4;
-        lds_at = row * kLdsRow + part;
-    }
-    __device__ __forceinline__ void fetch(uint4 (&stage)[kPasses], uint32_t k0, uint32_t K, bool full) const {
-        const uint32_t at = (full || !KC || k0 + k_in < K) ? offset : 0x80000000u;
-#pragma unroll
-        for (int i = 0; i < kPasses; i++) {
-            auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, at, i * pass_bytes + k0 * k_bytes, 0);
-            stage[i] = __builtin_bit_cast(uint4, v);
-        }
-    }
-    __device__ __forceinline__ void commit(const uint4 (&stage)[kPasses], float* lds) const {
-        uint4* to = reinterpret_cast<uint4*>(lds);
-#pragma unroll
-        for (int i = 0; i < kPasses; i++) to[(lds_at + i * kPassRows * kLdsRow) / 4] = stage[i];
-    }
-    // Lane `lane`'s four k (4 (lane / 16) + 0..3 of the slice at `kk`) of
-    // tile row `row`.
-    __device__ __forceinline__ f32x4 fragment(const float* lds, int row, int kk, int lane) const {
-        const int k = kk + (lane / 16) * 4;
-        if (KC) return reinterpret_cast<const f32x4*>(lds)[(row * kLdsRow + k) / 4];
-        return f32x4{lds[k * kLdsRow + row], lds[(k + 1) * kLdsRow + row], lds[(k + 2) * kLdsRow + row],
-                     lds[(k + 3) * kLdsRow + row]};
-    }
-};
-
-// BM x BN tiles over four waves of (BM / 2) x (BN / 2).
-template <typename O, bool A_KC, bool B_KC, int BM, int BN>
-__global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                             O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
-                                                             bool accumulate) {
-    using SA = Stager32<BM, A_KC>;
-    using SB = Stager32<BN, B_KC>;
-    constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wave
-    constexpr int kA = A_KC ? BM * kLd32 : kBK32 * (BM + 4);
-    constexpr int kB = B_KC ? BN * kLd32 : kBK32 * (BN + 4);
-    __shared__ __attribute__((aligned(16))) float lds_a[2 * kA];
-    __shared__ __attribute__((aligned(16))) float lds_b[2 * kB];
-    const uint32_t tiles_m = (M + BM - 1) / BM;
-    const uint32_t tiles_n = (N + BN - 1) / BN;
-    uint32_t tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const int t = threadIdx.x;
-    const int lane = t % 64;
-    const int wave = t / 64;
-    const int wm = wave / 2, wn = wave % 2;
-    SA sa;
-    SB sb;
-    sa.init(A, m0, M, A_KC ? K : M, K, t);
-    sb.init(B, n0, N, B_KC ? K : N, K, t);
-    uint4 stage_a[SA::kPasses], stage_b[SB::kPasses];
-
-    f32x4 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = f32x4{};
-
-    const uint32_t steps = (K + kBK32 - 1) / kBK32;
-    if (steps > 0) {
-        sa.fetch(stage_a, 0, K, kBK32 <= K);
-        sb.fetch(stage_b, 0, K, kBK32 <= K);
-        sa.commit(stage_a, lds_a);
-        sb.commit(stage_b, lds_b);
-        __syncthreads();
-    }
-    const int row_in = lane % 16;
-    for (uint32_t step = 0; step < steps; step++) {
-        const int buffer = step & 1;
-        const bool more = step + 1 < steps;
-        if (more) {
-            const uint32_t k0 = (step + 1) * kBK32;
-            sa.fetch(stage_a, k0, K, k0 + kBK32 <= K);
-            sb.fetch(stage_b, k0, K, k0 + kBK32 <= K);
-        }
-        const float* la = lds_a + buffer * kA;
-        const float* lb = lds_b + buffer * kB;
-#pragma unroll
-        for (int kk = 0; kk < kBK32; kk += 16) {
-            f32x4 a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++) a[i] = sa.fragment(la, wm * (BM / 2) + i * 16 + row_in, kk, lane);
-#pragma unroll
-            for (int j = 0; j < TN; j++) b[j] = sb.fragment(lb, wn * (BN / 2) + j * 16 + row_in, kk, lane);
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            sa.commit(stage_a, lds_a + (buffer ^ 1) * kA);
-            sb.commit(stage_b, lds_b + (buffer ^ 1) * kB);
-        }
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int i = 0; i < TM; i++) {
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const uint32_t col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + e;
-                if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
-            }
-        }
-    }
-}
-
-// ---- 16-bit operands in place ---------------------------------------------------------
-//
-// C[M x N] (+)= A . B with each operand read in the layout it is stored in:
-// "K-contiguous" (A stored M x K, B stored N x K) or "row-contiguous" (A
-// stored K x M, B stored K x N — B's ordinary row-major form).  Each block
-// owns a BM x BN tile of C and walks K in 64-deep steps; the waves split the
-// tile WM x WN, each owning (BM/WM) x (BN/WN) as 32 x 32 matrix-core tiles.
-// A lane's 8-element fragment of a 32 x 32 x 16 step is row lane % 32 (the
-// tile's M or N index) and k (lane / 32) * 8 .. + 8 of the slice:
-//  - from a K-contiguous tile with one ds_read_b128;
-//  - from a row-contiguous tile with gfx950's transposing ds_read_tr16_b64,
-//    which hands each lane of a 16-lane group four k-consecutive values of
-//    one column: when lane j of the group addresses (k0 + j / 4,
-//    c0 + 4 (j % 4)), lane i receives rows k0 .. k0 + 3 of column c0 + i.
-//    Two such reads give a lane the same fragment, so no operand is ever
-//    transposed in HBM.
-// Requirements (checked by the host): 16-byte aligned operands, K a multiple
-// of 8 for K-contiguous operands, the contiguous extent a multiple of 8 for
-// row-contiguous ones, and operands under 2^31 bytes.  M and N edges and the
-// K tail load zeros (buffer reads past the operand) or values that only feed
-// results that are never stored.
-
-constexpr int kTileK = 64;
-
-typedef short short4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ short4v read_tr16(const void* lds_addr) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) short4v*)(const_cast<void*>(lds_addr)));
-}
-
-// The order the scheduler is asked to keep within one step: F matrix-core
-// steps per slice, each followed by its share of the step's HBM loads (first
-// slice) and of the next slice's LDS reads (every slice but the last, whose
-// reads the scheduler places itself; interleaving those too measured no
-// faster).
-template <int F, int LOADS, int READS, int SLICES, int Q = 0, int R = 0>
-__device__ __forceinline__ void weave() {
-    if constexpr (Q < SLICES) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // a matrix-core step
-        constexpr int loads = LOADS * (R + 1) / F - LOADS * R / F;
-        constexpr int reads = READS * (R + 1) / F - READS * R / F;
-        if constexpr (Q == 0 && loads > 0) __builtin_amdgcn_sched_group_barrier(0x020, loads, 0);  // HBM loads
-        if constexpr (Q + 1 < SLICES && reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);  // LDS reads
-        if constexpr (R + 1 < F) {
-            weave<F, LOADS, READS, SLICES, Q, R + 1>();
-        } else {
-            weave<F, LOADS, READS, SLICES, Q + 1, 0>();
-        }
-    }
-}
-
-// ---- staging straight into LDS ------------------------------------------------
-//
-// HBM -> LDS staging is done by gfx950's buffer loads that write LDS directly
-// (`buffer_load_dwordx4 ... lds`): no staging registers and no ds_write
-// instructions.  Such a load writes 64 lanes x 16 bytes to consecutive LDS
-// bytes, so tiles are unpadded and bank conflicts are avoided by
-// XOR-swizzling each row's 16-byte chunks instead: a lane loads the global
-// chunk that belongs at the LDS position it writes.
-//  - K-contiguous tile, BK x 2-byte rows (CPR = BK / 8 chunks a row, RPW =
-//    256 / (2 BK) rows per 256-byte bank window): logical chunk c of row r
-//    lives at chunk c ^ ((r / RPW) % CPR), which spreads the 16 rows a
-//    ds_read_b128 phase touches over all 16 bank groups.
-//  - row-contiguous tile, ROWS x 2-byte rows: chunk c of k-row r lives at
-//    c ^ ((r & 3) << 2), which spreads the four rows of a transposing read
-//    over distinct bank groups.
-// The K loop runs NS stages deep: each step issues the loads of the step
-// NS - 1 ahead into the stage the previous step freed, then waits only for
-// the next step's loads (vmcnt counts this wave's loads in issue order).
-// Two 64-deep stages measure faster on MI355X than three or four 32-deep
-// ones (1170 vs 950 TFLOP/s at 8192^3): the per-step barrier costs more
-// than the extra latency cover buys.
-
-template <int BK>
-__device__ __forceinline__ int kc_swizzle(int row) {
-    constexpr int kCpr = BK / 8, kRpw = 256 / (2 * BK);
-    return (row / kRpw) % kCpr;
-}
-__device__ __forceinline__ int rc_swizzle(int row) { return (row & 3) << 2; }
-
-template <typename S, int ROWS, bool KC, int WAVES, int BK>
-struct DirectStager {
-    static constexpr int kTileBytes = ROWS * BK * 2;
-    static constexpr int kInstr = kTileBytes / 1024;  // one wave instruction moves 1 KiB
-    static constexpr int kPer = kInstr / WAVES;
-    static_assert(kInstr % WAVES == 0, "tile instructions must divide among the waves");
-    static constexpr int kRowsPer = KC ? 1024 / (BK * 2) : 1024 / (ROWS * 2);  // tile rows one instruction fills
-    static constexpr int kChunksPerRow = KC ? BK / 8 : ROWS / 8;
-
-    __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t offset[kPer];  // this lane's chunk of each instruction, bytes at k0 = 0
-    uint32_t k_of[kPer];    // its k within a step (K-contiguous only)
-    uint32_t k_bytes;
-    int wave;
-
-    __device__ void init(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int w, int lane) {
-        wave = w;
-        if (KC) {
-            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + static_cast<uint64_t>(first) * ld), 0,
-                                                     (rows - first) * ld * sizeof(S), kBufferFlags);
-            k_bytes = sizeof(S);
-        } else {
-            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + first), 0, (depth * ld - first) * sizeof(S),
-                                                     kBufferFlags);
-            k_bytes = ld * sizeof(S);
-        }
-#pragma unroll
-        for (int i = 0; i < kPer; i++) {
-            const int first_row = kRowsPer * (w + WAVES * i);
-            const int row = first_row + lane / kChunksPerRow;
-            const int place = lane % kChunksPerRow;
-            const int chunk = place ^ (KC ? kc_swizzle<BK>(row) : rc_swizzle(row));
-            offset[i] = (static_cast<uint32_t>(row) * ld + chunk * 8) * sizeof(S);
-            k_of[i] = KC ? chunk * 8 : 0;
-        }
-    }
-    // Stage the step at `k0` into `tile` (the LDS stage).  Past K a
-    // K-contiguous chunk is the next row's, so it is pointed past the
-    // resource (operands are under 2^31 bytes) and loads zeros.
-    __device__ __forceinline__ void fetch(S* tile, uint32_t k0, uint32_t K, bool full) const {
-#pragma unroll
-        for (int i = 0; i < kPer; i++) {
-            const uint32_t at = (full || !KC || k0 + k_of[i] < K) ? offset[i] : 0x80000000u;
-            uint8_t* dst = reinterpret_cast<uint8_t*>(tile) + 1024 * (wave + WAVES * i);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, at,
-                                                     k0 * k_bytes, 0, 0);
-        }
-    }
-};
-
-// A lane's fragment of tile row `row_base + lane % 32` (the tile's M or N
-// index) for the 16-deep slice at `k_base`, from a swizzled tile.
-template <typename S, int ROWS, bool KC, int BK>
-__device__ __forceinline__ uint4 swizzled_fragment(const S* lds, int row_base, int k_base, int lane) {
-    if (KC) {
-        const int row = row_base + lane % 32;
-        const int chunk = (k_base / 8 + lane / 32) ^ kc_swizzle<BK>(row);
-        return reinterpret_cast<const uint4*>(lds)[row * (BK / 8) + chunk];
-    } else {
-        const int g = lane / 16, j = lane % 16;
-        const int k = k_base + (g / 2) * 8 + j / 4;
-        const int col = row_base + (g % 2) * 16 + 4 * (j % 4);
-        const int chunk = (col / 8) ^ rc_swizzle(k);  // k + 4 swizzles the same way
-        const S* at = lds + k * ROWS + chunk * 8 + col % 8;
-        short4v lo = read_tr16(at);
-        short4v hi = read_tr16(at + 4 * ROWS);
-        uint4 out;
-        out.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
-        out.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
-        out.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
-        out.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
-        return out;
-    }
-}
-
-// s_waitcnt's immediate for vmcnt(n), other counters not waited on
-// (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-constexpr int vmcnt_wait(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
-
-// One LDS stage of an operand.  A separate array per stage gives every LDS
-// read and every direct load a distinct, statically known object, so the
-// compiler waits for a stage's loads only where that stage is read.
-template <typename S, int ELEMS, int STAGE>
-__device__ __forceinline__ S* stage_tile() {
-    __shared__ __attribute__((aligned(1024))) S tile[ELEMS];
-    return tile;
-}
-
-template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN, int BK, int NS>
-__global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restrict__ A, const S* __restrict__ B,
-                                                                O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
-                                                                bool accumulate) {
-    constexpr int kWaves = WM * WN;
-    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-    constexpr int kA = BM * BK, kB = BN * BK;  // elements of one stage
-    static_assert(NS >= 2 && NS <= 4, "two to four stages");
-
-    const uint32_t tiles_m = (M + BM - 1) / BM;
-    const uint32_t tiles_n = (N + BN - 1) / BN;
-    uint32_t tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const int lane = threadIdx.x % 64;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    const int wm = wave / WN, wn = wave % WN;
-
-    using StagerA = DirectStager<S, BM, A_KC, kWaves, BK>;
-    using StagerB = DirectStager<S, BN, B_KC, kWaves, BK>;
-    StagerA sa;
-    StagerB sb;
-    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
-    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
-
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
-
-    uint4 fa[2][TM], fb[2][TN];
-    auto read_fragments = [&](int slot, const S* la, const S* lb, int kk) {
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-            fa[slot][i] = swizzled_fragment<S, BM, A_KC, BK>(la, wm * (BM / WM) + i * 32, kk, lane);
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-            fb[slot][j] = swizzled_fragment<S, BN, B_KC, BK>(lb, wn * (BN / WN) + j * 32, kk, lane);
-    };
-
-    constexpr int kSlices = BK / 16;
-    constexpr int kSteps = TM * TN;
-    constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
-    constexpr int kLoads = StagerA::kPer + StagerB::kPer;  // this wave's loads per step
-    const uint32_t steps = (K + BK - 1) / BK;
-    auto stage_of = [&](auto t, uint32_t s) {
-        const uint32_t k0 = (s < steps ? s : steps - 1) * BK;  // past the end: a harmless reload
-        sa.fetch(stage_tile<S, kA, 2 * decltype(t)::value>(), k0, K, k0 + BK <= K);
-        sb.fetch(stage_tile<S, kB, 2 * decltype(t)::value + 1>(), k0, K, k0 + BK <= K);
-    };
-    // Step s computes from stage T = s % NS.  It first stages step s + NS - 1
-    // into stage (T + NS - 1) % NS, which every wave finished reading before
-    // the previous step's barrier; it waits for step s + 1 and meets the
-    // others at a barrier before its last slice, whose fragments it already
-    // holds, and reads step s + 1's first fragments under that slice.
-    auto step = [&](auto t, uint32_t s) {
-        constexpr int T = decltype(t)::value;
-        const S* la = stage_tile<S, kA, 2 * T>();
-        const S* lb = stage_tile<S, kB, 2 * T + 1>();
-        stage_of(std::integral_constant<int, (T + NS - 1) % NS>{}, s + NS - 1);
-#pragma unroll
-        for (int q = 0; q + 1 < kSlices; q++) {
-            read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[q & 1][i], fb[q & 1][j], acc[i][j]);
-        }
-        weave<kSteps, kLoads, kReads, kSlices - 1>();
-        __builtin_amdgcn_s_waitcnt(vmcnt_wait(kLoads * (NS - 2)));  // step s + 1 is in LDS
-        __syncthreads();
-        constexpr int last = (kSlices - 1) & 1;
-        constexpr int U = (T + 1) % NS;
-        read_fragments(last ^ 1, stage_tile<S, kA, 2 * U>(), stage_tile<S, kB, 2 * U + 1>(), 0);
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[last][i], fb[last][j], acc[i][j]);
-        weave<kSteps, 0, kReads, 2>();
-    };
-    if (steps > 0) {
-        stage_of(std::integral_constant<int, 0>{}, 0);
-        if constexpr (NS > 2) stage_of(std::integral_constant<int, 1>{}, 1);
-        if constexpr (NS > 3) stage_of(std::integral_constant<int, 2>{}, 2);
-        __builtin_amdgcn_s_waitcnt(vmcnt_wait(kLoads * (NS - 2)));  // step 0 is in LDS
-        __syncthreads();
-        read_fragments(0, stage_tile<S, kA, 0>(), stage_tile<S, kB, 1>(), 0);
-    }
-    for (uint32_t s = 0; s < steps; s += NS) {
-        step(std::integral_constant<int, 0>{}, s);
-        if (s + 1 < steps) step(std::integral_constant<int, 1 % NS>{}, s + 1);
-        if constexpr (NS > 2) {
-            if (s + 2 < steps) step(std::integral_constant<int, 2 % NS>{}, s + 2);
-        }
-        if constexpr (NS > 3) {
-            if (s + 3 < steps) step(std::integral_constant<int, 3 % NS>{}, s + 3);
-        }
-    }
-
-#pragma unroll
-    for (int i = 0; i < TM; i++) {
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const uint32_t col = n0 + wn * (BN / WN) + j * 32 + lane % 32;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const uint32_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
-                if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
-            }
-        }
-    }
-}
-
 // The tiled kernel's shapes: a 256 x 256 tile over eight waves of 128 x 64
 // (two waves per SIMD, so one's waits overlap the other's matrix-core
 // steps), and a 128 x 128 tile over four waves of 64 x 64 for products too
 // small to give every CU a few large tiles.
-template <typename S, typename O, bool A_KC, bool B_KC>
+template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
-                    hipStream_t s) {
+                    hipStream_t s, const EPI& epi = EPI{}) {
     const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
     if (large >= static_cast<uint32_t>(compute_units())) {
-        direct16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64, 2><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+        direct16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64, 2, EPI><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k,
+                                                                                                 accumulate, epi);
     } else {
         const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);
-        direct16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2, 64, 2><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k, accumulate);
+        direct16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2, 64, 2, EPI><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k,
+                                                                                                 accumulate, epi);
     }
 }
 
 // The in-place f32 kernel's shapes: 256 x 128 tiles, or 128 x 128 when the
 // larger ones would leave CUs without a tile (a 4096 x 1024 product has 128
 // of them on 256 CUs).
-template <typename O, bool A_KC, bool B_KC>
+template <typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 void launch_inplace32(const float* a, const float* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
-                      hipStream_t s) {
+                      hipStream_t s, const EPI& epi = EPI{}) {
     const uint32_t large = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
     if (large >= static_cast<uint32_t>(compute_units())) {
-        inplace32_kernel<O, A_KC, B_KC, kBM, kBN><<<large, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate);
+        inplace32_kernel<O, A_KC, B_KC, kBM, kBN, EPI><<<large, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate, epi);
     } else {
         const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);
-        inplace32_kernel<O, A_KC, B_KC, 128, 128><<<small, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate);
+        inplace32_kernel<O, A_KC, B_KC, 128, 128, EPI><<<small, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate, epi);
     }
 }
 
@@ -961,7 +487,140 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
     return status;
 }
 
+// Elements a thread takes through a compiled epilogue at once: all their
+// loads are in flight together.
+constexpr int kCompiledElems = 16;
+
+// A compiled epilogue's arguments, laid out as the generated
+// `CompiledStore` declares its members.
+struct CompiledStoreArgs {
+    const void* in[TC_FUSED_MAX_INPUTS];
+    void* out[TC_FUSED_MAX_OUTPUTS];
+    DevicePlace places[kInlinePlaces];
+    float constants[kInlineCode];
+};
+
+// The product kernels with `code` compiled into their epilogue, once the
+// program has been seen before: true when they were launched.
+bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, const void* a, const void* b,
+                           const tc_encoded* code, uint32_t count, const tc_place* host_places,
+                           const DevicePlace* places, uint32_t place_count,
+                           const void* const* inputs, uint32_t input_count, void* const* outputs,
+                           uint32_t output_count, hipStream_t s, int* status) {
+    std::vector<float> constants;
+    const std::string body = epilogue_group(code, count, dtype, true, kCompiledElems, host_places, &constants);
+    if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
+    std::string source = "#include \"gemm_kernels.hpp\"\n"
+                         "struct CompiledStore {\n"
+                         "  static constexpr bool kProgram = true;\n"
+                         "  static constexpr int kElems = " + std::to_string(kCompiledElems) + ";\n"
+                         "  const void* in[" + std::to_string(TC_FUSED_MAX_INPUTS) + "];\n"
+                         "  void* out[" + std::to_string(TC_FUSED_MAX_OUTPUTS) + "];\n"
+                         "  tc::DevicePlace places[" + std::to_string(kInlinePlaces) + "];\n"
+                         "  float constants[" + std::to_string(kInlineCode) + "];\n"
+                         "  __device__ __forceinline__ void group(const bool (&live)[kElems], const uint32_t (&row)[kElems],\n"
+                         "      const uint32_t (&col)[kElems], uint32_t N, const float (&product)[kElems]) const {\n" +
+                         body + "  }\n};\n";
+    std::vector<std::string> kernels;
+    uint32_t large = 0, small = 0, large_threads = 0, small_threads = 0;
+    if (dtype == TC_F32) {
+        kernels = {"tc::inplace32_kernel<float, true, false, 256, 128, CompiledStore>",
+                   "tc::inplace32_kernel<float, true, false, 128, 128, CompiledStore>"};
+        large = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
+        large_threads = small_threads = kThreads;
+    } else {
+        const std::string type = dtype == TC_F16 ? "_Float16" : "tc::bf16_t";
+        kernels = {"tc::direct16_kernel<" + type + ", " + type + ", true, false, 256, 256, 2, 4, 64, 2, CompiledStore>",
+                   "tc::direct16_kernel<" + type + ", " + type + ", true, false, 128, 128, 2, 2, 64, 2, CompiledStore>"};
+        large = ((m + 255) / 256) * ((n + 255) / 256);
+        large_threads = 2 * 4 * 64;
+        small_threads = 2 * 2 * 64;
+    }
+    small = ((m + 127) / 128) * ((n + 127) / 128);
+    hipFunction_t functions[2] = {};
+    if (!compiled_kernels(source, kernels, functions)) return false;
+    CompiledStoreArgs args{};
+    for (uint32_t slot = 1; slot < input_count; slot++) args.in[slot] = inputs[slot];
+    for (uint32_t slot = 0; slot < output_count; slot++) args.out[slot] = outputs[slot];
+    for (uint32_t p = 0; p < place_count; p++) args.places[p] = places[p];
+    for (size_t c = 0; c < constants.size(); c++) args.constants[c] = constants[c];
+    void* none = nullptr;
+    bool accumulate = false;
+    void* params[] = {const_cast<void**>(&a), const_cast<void**>(&b), &none, &m, &n, &k, &accumulate, &args};
+    const bool use_large = large >= static_cast<uint32_t>(compute_units());
+    const hipError_t error = hipModuleLaunchKernel(use_large ? functions[0] : functions[1], use_large ? large : small,
+                                                   1, 1, use_large ? large_threads : small_threads, 1, 1, 0, s, params,
+                                                   nullptr);
+    *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused matmul: ") + hipGetErrorString(error));
+    return true;
+}
+
 }  // namespace
+
+int matmul_program(uint32_t dtype, uint64_t m, uint64_t k, uint64_t n, const void* a, const void* b,
+                   const tc_encoded* code, uint32_t count, const tc_place* places, uint32_t place_count,
+                   const void* const* inputs, uint32_t input_count, void* const* outputs, uint32_t output_count,
+                   bool* fused) {
+    *fused = false;
+    if (count > static_cast<uint32_t>(kInlineCode) || place_count > static_cast<uint32_t>(kInlinePlaces)) return TC_OK;
+    if (k < 8 || m == 0 || n == 0 || m > UINT32_MAX / 2 || n > UINT32_MAX / 2 || k > UINT32_MAX / 2) return TC_OK;
+    const size_t width = dtype == TC_F32 ? 4 : 2;
+    const uint64_t limit = uint64_t{1} << 31;
+    const uint64_t align = 16 / width;  // a row-major row of A (k) and of B (n) in whole 16-byte words
+    if (!aligned16(a) || !aligned16(b) || k % align != 0 || n % align != 0 || m * k * width >= limit ||
+        k * n * width >= limit) {
+        return TC_OK;
+    }
+    TC_STREAM(s);
+    const uint32_t m32 = static_cast<uint32_t>(m), k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
+    int status = TC_OK;
+    {
+        DevicePlace device_places[kInlinePlaces] = {};
+        status = to_device_places(places, place_count, device_places);
+        if (status != TC_OK) return status;
+        if (run_compiled_epilogue(dtype, m32, k32, n32, a, b, code, count, places, device_places, place_count, inputs,
+                                  input_count, outputs, output_count, s, &status)) {
+            *fused = true;
+            return status;
+        }
+    }
+    auto interpreted = [&](auto& epi) {
+        memcpy(epi.program.code, code, count * sizeof(tc_encoded));
+        status = to_device_places(places, place_count, epi.program.places);
+        for (uint32_t slot = 1; slot < input_count; slot++) epi.buffers.inputs[slot] = inputs[slot];
+        for (uint32_t slot = 0; slot < output_count; slot++) epi.buffers.outputs[slot] = outputs[slot];
+        epi.count = count;
+        return status == TC_OK;
+    };
+    switch (dtype) {
+        case TC_F32: {
+            ProgramStore<TC_F32> epi{};
+            if (!interpreted(epi)) return status;
+            launch_inplace32<float, true, false>(static_cast<const float*>(a), static_cast<const float*>(b), nullptr,
+                                                 m32, k32, n32, false, s, epi);
+            break;
+        }
+        case TC_F16: {
+            ProgramStore<TC_F16> epi{};
+            if (!interpreted(epi)) return status;
+            launch_tiled16<_Float16, _Float16, true, false>(static_cast<const _Float16*>(a),
+                                                            static_cast<const _Float16*>(b), nullptr, m32, k32, n32,
+                                                            false, s, epi);
+            break;
+        }
+        case TC_BF16: {
+            ProgramStore<TC_BF16> epi{};
+            if (!interpreted(epi)) return status;
+            launch_tiled16<bf16_t, bf16_t, true, false>(static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(b),
+                                                        nullptr, m32, k32, n32, false, s, epi);
+            break;
+        }
+        default: return TC_OK;
+    }
+    *fused = true;
+    return check_launch("fused matmul");
+}
+
 }  // namespace tc
 
 using namespace tc;

@@ -1,0 +1,675 @@
+// The matrix-core product kernels, shared by the library (gemm.hip) and the
+// product kernels the runtime compiler builds with a program's epilogue
+// compiled in: the tiled 16-bit kernel (`direct16_kernel`) and the in-place
+// f32 kernel (`inplace32_kernel`), templated on how a tile is finished.  It
+// includes only device.hpp and <type_traits>, which hiprtc provides.
+#pragma once
+
+#include <type_traits>
+
+#include "device.hpp"
+
+namespace tc {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// The descriptor word that makes a gfx9-family buffer resource a plain,
+// untyped byte range (32-bit data format, no swizzle, no stride).
+constexpr int kBufferFlags = 0x00020000;
+
+constexpr int kBM = 256;
+constexpr int kBN = 128;
+constexpr int kThreads = 256;
+constexpr int kGroupM = 8;  // block-tile rows per ordering group
+
+template <typename S>
+struct Mfma16;
+template <>
+struct Mfma16<bf16_t> {
+    __device__ static f32x16 step(uint4 a, uint4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+};
+template <>
+struct Mfma16<_Float16> {
+    __device__ static f32x16 step(uint4 a, uint4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+};
+
+// The block tile a block computes, from its linear index: spread across the
+// XCDs first (hardware hands consecutive blocks to consecutive XCDs), then
+// grouped so that neighbouring blocks share rows of A.
+__device__ __forceinline__ void tile_of(uint32_t block, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm,
+                                        uint32_t& tn) {
+    const uint32_t total = tiles_m * tiles_n;
+    constexpr uint32_t kXcds = 8;
+    if (total % kXcds == 0) {
+        block = (block % kXcds) * (total / kXcds) + block / kXcds;
+    }
+    const uint32_t per_group = kGroupM * tiles_n;
+    const uint32_t group = block / per_group;
+    const uint32_t first_m = group * kGroupM;
+    const uint32_t rows = min(tiles_m - first_m, static_cast<uint32_t>(kGroupM));
+    const uint32_t in_group = block - group * per_group;
+    tm = first_m + in_group % rows;
+    tn = in_group / rows;
+}
+
+// 16 bytes of row `row`, from column `k`, of a K-contiguous operand with
+// `rows` rows of `K` elements of `E` bytes; zeros outside it.  `fast` says the
+// whole operand is 16-byte aligned row by row.
+template <int E>
+__device__ __forceinline__ uint4 load16(const uint8_t* base, uint32_t row, uint32_t k, uint32_t rows,
+                                        uint32_t K, bool fast) {
+    constexpr uint32_t per = 16 / E;
+    if (row < rows && fast && k + per <= K) {
+        return *reinterpret_cast<const uint4*>(base + (static_cast<uint64_t>(row) * K + k) * E);
+    }
+    uint8_t bytes[16] = {};
+    if (row < rows) {
+        for (uint32_t e = 0; e < per; e++) {
+            if (k + e < K) {
+                const uint8_t* at = base + (static_cast<uint64_t>(row) * K + k + e) * E;
+                for (int b = 0; b < E; b++) bytes[e * E + b] = at[b];
+            }
+        }
+    }
+    uint4 out;
+    __builtin_memcpy(&out, bytes, 16);
+    return out;
+}
+
+template <typename O>
+__device__ __forceinline__ void store_out(O* c, uint64_t at, float v, bool accumulate) {
+    using E = Elem<O>;
+    if (accumulate) v += E::widen(c[at]);
+    c[at] = E::narrow(v);
+}
+
+// ---- how a tile is finished ---------------------------------------------------------
+//
+// A product kernel ends either with plain stores, C (+)= A . B, or with a
+// fused program run over its tile (`Kernels::matmul_epilogue`,
+// kernels.rs:1142; `Program::run_matmul`, fused/mod.rs:1143-1215): the
+// product is never written to memory unless the program stores it.  The
+// tile's accumulators are staged through the LDS the main loop used, a pass
+// of rows at a time, and the program then runs over the pass in row-major
+// order, four elements a thread 64 apart as the fused kernel runs them, so
+// its loads and stores are coalesced.  Input 0 is the product rounded to the
+// program's type, as the host's product is before its program reads it.
+//
+// An epilogue type with kProgram set provides kElems and
+//   group(live, row, col, N, product)
+// for kElems elements of C: whether each is inside C, its row and column
+// (its row-major index is row * N + col), and its f32 product.  The
+// library's interprets the program; a compiled one is the program as
+// straight-line code.
+
+struct PlainStore {
+    static constexpr bool kProgram = false;
+};
+
+// A workgroup barrier ordering LDS alone: fences scoped to the workgroup and
+// to LDS ("local") around the barrier, so LDS accesses stay on their side
+// and only LDS traffic is waited for.  Unlike __syncthreads it does not wait
+// for the epilogue's global stores, which only have to land by the end of
+// the kernel.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Where tile column `col` of staged row `row` sits: groups of G lanes that
+// store one row of a matrix-core tile, 4 rows apart, land on distinct banks.
+template <int G>
+__device__ __forceinline__ uint32_t staged_col(uint32_t row, uint32_t col) {
+    return col ^ (((row >> 2) & (64 / G - 1)) * G);
+}
+
+// The staged rows live in up to four LDS regions of REGION_ROWS rows each.
+template <int BN, int G, int REGION_ROWS>
+__device__ __forceinline__ float* staged_at(float* r0, float* r1, float* r2, float* r3, uint32_t row, uint32_t col) {
+    const uint32_t region = row / REGION_ROWS;
+    float* base = region == 0 ? r0 : region == 1 ? r1 : region == 2 ? r2 : r3;
+    return base + (row % REGION_ROWS) * BN + staged_col<G>(row, col);
+}
+
+// The epilogue over `rows` x BN staged products, EPI::kElems elements a
+// thread 64 apart in row-major order (each load and store instruction of a
+// wave then touches one contiguous run), handed to `epi.group`.  A pass holds
+// H rows of each wave row (WAVE_ROWS rows apart), its `pass`-th H: staged row
+// rr is tile row (rr / H) * WAVE_ROWS + pass * H + rr % H, so every wave
+// stages, and then stops holding, the same share of its accumulators in
+// every pass.
+template <int BN, int G, int REGION_ROWS, int H, int WAVE_ROWS, class EPI>
+__device__ __forceinline__ void program_pass(const EPI& epi, float* r0, float* r1, float* r2, float* r3,
+                                             uint32_t rows, uint32_t pass, uint32_t row_base, uint32_t col_base,
+                                             uint32_t M, uint32_t N) {
+    constexpr int E = EPI::kElems;
+    const uint32_t total = rows * BN;
+    const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const uint32_t per_round = blockDim.x * E;
+    for (uint32_t base = 0; base < total; base += per_round) {
+        uint32_t row[E], col[E];
+        bool live[E];
+        float product[E];
+#pragma unroll
+        for (int v = 0; v < E; v++) {
+            const uint32_t at = base + wave * (64 * E) + v * 64 + lane;
+            const uint32_t rr = at / BN, cc = at % BN;
+            const bool inside = at < total;
+            product[v] = inside ? *staged_at<BN, G, REGION_ROWS>(r0, r1, r2, r3, rr, cc) : 0.0f;
+            row[v] = row_base + (rr / H) * WAVE_ROWS + pass * H + rr % H;
+            col[v] = col_base + cc;
+            live[v] = inside && row[v] < M && col[v] < N;
+        }
+        epi.group(live, row, col, N, product);
+    }
+}
+
+constexpr int kBK32 = 32;
+constexpr int kLd32 = kBK32 + 4;
+
+// ---- f32 operands in place ---------------------------------------------------------
+//
+// The f32 product with each operand read in its stored orientation, as the
+// 16-bit kernel does, so `matmul_transposed_add` (the tape's backward
+// products) and a plain `matmul` pay for no transpose pass.  A lane's four k
+// for one tile row come from one ds_read_b128 of a K-contiguous tile, or
+// four ds_read_b32 down a row-contiguous tile ([k][rows + 4]: the 4-float
+// pad puts the four k-rows a wave reads on distinct bank quarters).  HBM is
+// staged through buffer loads (zeros past the operand) into registers and
+// then LDS, double-buffered, 256 x 128 or 128 x 128 tiles, 32-deep steps,
+// four waves of a quarter tile.  Requirements as for the 16-bit kernel, with K (K-contiguous)
+// or the contiguous extent (row-contiguous) a multiple of 4.
+
+template <int ROWS, bool KC>
+struct Stager32 {
+    static constexpr int kRowChunks = KC ? kBK32 / 4 : ROWS / 4;  // 16-byte chunks per tile row
+    static constexpr int kPassRows = kThreads / kRowChunks;
+    static constexpr int kPasses = (KC ? ROWS : kBK32) / kPassRows;
+    static constexpr int kLdsRow = KC ? kLd32 : ROWS + 4;
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t offset, pass_bytes, k_bytes, lds_at, k_in;
+
+    __device__ void init(const float* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int t) {
+        const uint32_t row = t / kRowChunks, part = (t % kRowChunks) * 4;
+        if (KC) {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + static_cast<uint64_t>(first) * ld), 0,
+                                                     (rows - first) * ld * 4, kBufferFlags);
+            k_bytes = 4;
+            k_in = part;
+        } else {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + first), 0, (depth * ld - first) * 4,
+                                                     kBufferFlags);
+            k_bytes = ld * 4;
+            k_in = 0;
+        }
+        offset = (row * ld + part) * 4;
+        pass_bytes = kPassRows * ld * 4;
+        lds_at = row * kLdsRow + part;
+    }
+    __device__ __forceinline__ void fetch(uint4 (&stage)[kPasses], uint32_t k0, uint32_t K, bool full) const {
+        const uint32_t at = (full || !KC || k0 + k_in < K) ? offset : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < kPasses; i++) {
+            auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, at, i * pass_bytes + k0 * k_bytes, 0);
+            stage[i] = __builtin_bit_cast(uint4, v);
+        }
+    }
+    __device__ __forceinline__ void commit(const uint4 (&stage)[kPasses], float* lds) const {
+        uint4* to = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+        for (int i = 0; i < kPasses; i++) to[(lds_at + i * kPassRows * kLdsRow) / 4] = stage[i];
+    }
+    // Lane `lane`'s four k (4 (lane / 16) + 0..3 of the slice at `kk`) of
+    // tile row `row`.
+    __device__ __forceinline__ f32x4 fragment(const float* lds, int row, int kk, int lane) const {
+        const int k = kk + (lane / 16) * 4;
+        if (KC) return reinterpret_cast<const f32x4*>(lds)[(row * kLdsRow + k) / 4];
+        return f32x4{lds[k * kLdsRow + row], lds[(k + 1) * kLdsRow + row], lds[(k + 2) * kLdsRow + row],
+                     lds[(k + 3) * kLdsRow + row]};
+    }
+};
+
+// BM x BN tiles over four waves of (BM / 2) x (BN / 2).
+template <typename O, bool A_KC, bool B_KC, int BM, int BN, class EPI = PlainStore>
+__global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                             O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                                                             bool accumulate, EPI epi) {
+    using SA = Stager32<BM, A_KC>;
+    using SB = Stager32<BN, B_KC>;
+    constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wave
+    constexpr int kA = A_KC ? BM * kLd32 : kBK32 * (BM + 4);
+    constexpr int kB = B_KC ? BN * kLd32 : kBK32 * (BN + 4);
+    __shared__ __attribute__((aligned(16))) float lds_a[2 * kA];
+    __shared__ __attribute__((aligned(16))) float lds_b[2 * kB];
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    uint32_t tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x;
+    const int lane = t % 64;
+    const int wave = t / 64;
+    const int wm = wave / 2, wn = wave % 2;
+    SA sa;
+    SB sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, t);
+    sb.init(B, n0, N, B_KC ? K : N, K, t);
+    uint4 stage_a[SA::kPasses], stage_b[SB::kPasses];
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x4{};
+
+    const uint32_t steps = (K + kBK32 - 1) / kBK32;
+    if (steps > 0) {
+        sa.fetch(stage_a, 0, K, kBK32 <= K);
+        sb.fetch(stage_b, 0, K, kBK32 <= K);
+        sa.commit(stage_a, lds_a);
+        sb.commit(stage_b, lds_b);
+        __syncthreads();
+    }
+    const int row_in = lane % 16;
+    for (uint32_t step = 0; step < steps; step++) {
+        const int buffer = step & 1;
+        const bool more = step + 1 < steps;
+        if (more) {
+            const uint32_t k0 = (step + 1) * kBK32;
+            sa.fetch(stage_a, k0, K, k0 + kBK32 <= K);
+            sb.fetch(stage_b, k0, K, k0 + kBK32 <= K);
+        }
+        const float* la = lds_a + buffer * kA;
+        const float* lb = lds_b + buffer * kB;
+#pragma unroll
+        for (int kk = 0; kk < kBK32; kk += 16) {
+            f32x4 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a[i] = sa.fragment(la, wm * (BM / 2) + i * 16 + row_in, kk, lane);
+#pragma unroll
+            for (int j = 0; j < TN; j++) b[j] = sb.fragment(lb, wn * (BN / 2) + j * 16 + row_in, kk, lane);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            sa.commit(stage_a, lds_a + (buffer ^ 1) * kA);
+            sb.commit(stage_b, lds_b + (buffer ^ 1) * kB);
+        }
+        __syncthreads();
+    }
+
+    if constexpr (EPI::kProgram) {
+        // Passes of a power-of-two number of rows that fit in both A stages,
+        // each taking the same share of both wave rows.
+        constexpr int kFit = 2 * kA / BN;
+        constexpr int kPass = kFit >= 128 ? 128 : 64;
+        constexpr int kPasses = BM / kPass, H = BM / 2 / kPasses;
+        static_assert(kFit >= kPass && BM % kPass == 0 && H % 16 == 0, "a pass fits in LDS");
+#pragma unroll
+        for (int pass = 0; pass < kPasses; pass++) {
+            lds_barrier();  // every wave is done with LDS
+#pragma unroll
+            for (int i = pass * H / 16; i < (pass + 1) * H / 16; i++) {
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const uint32_t col = wn * (BN / 2) + j * 16 + lane % 16;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t rr = wm * H + i * 16 - pass * H + 4 * (lane / 16) + e;
+                        *staged_at<BN, 16, kPass>(lds_a, lds_a, lds_a, lds_a, rr, col) = acc[i][j][e];
+                    }
+                }
+            }
+            lds_barrier();
+            program_pass<BN, 16, kPass, H, BM / 2>(epi, lds_a, lds_a, lds_a, lds_a, kPass, pass, m0, n0, M, N);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint32_t col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + e;
+                    if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
+                }
+            }
+        }
+    }
+}
+
+// ---- 16-bit operands in place ---------------------------------------------------------
+//
+// C[M x N] (+)= A . B with each operand read in the layout it is stored in:
+// "K-contiguous" (A stored M x K, B stored N x K) or "row-contiguous" (A
+// stored K x M, B stored K x N — B's ordinary row-major form).  Each block
+// owns a BM x BN tile of C and walks K in 64-deep steps; the waves split the
+// tile WM x WN, each owning (BM/WM) x (BN/WN) as 32 x 32 matrix-core tiles.
+// A lane's 8-element fragment of a 32 x 32 x 16 step is row lane % 32 (the
+// tile's M or N index) and k (lane / 32) * 8 .. + 8 of the slice:
+//  - from a K-contiguous tile with one ds_read_b128;
+//  - from a row-contiguous tile with gfx950's transposing ds_read_tr16_b64,
+//    which hands each lane of a 16-lane group four k-consecutive values of
+//    one column: when lane j of the group addresses (k0 + j / 4,
+//    c0 + 4 (j % 4)), lane i receives rows k0 .. k0 + 3 of column c0 + i.
+//    Two such reads give a lane the same fragment, so no operand is ever
+//    transposed in HBM.
+// Requirements (checked by the host): 16-byte aligned operands, K a multiple
+// of 8 for K-contiguous operands, the contiguous extent a multiple of 8 for
+// row-contiguous ones, and operands under 2^31 bytes.  M and N edges and the
+// K tail load zeros (buffer reads past the operand) or values that only feed
+// results that are never stored.
+
+constexpr int kTileK = 64;
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ short4v read_tr16(const void* lds_addr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) short4v*)(const_cast<void*>(lds_addr)));
+}
+
+// The order the scheduler is asked to keep within one step: F matrix-core
+// steps per slice, each followed by its share of the step's HBM loads (first
+// slice) and of the next slice's LDS reads (every slice but the last, whose
+// reads the scheduler places itself; interleaving those too measured no
+// faster).
+template <int F, int LOADS, int READS, int SLICES, int Q = 0, int R = 0>
+__device__ __forceinline__ void weave() {
+    if constexpr (Q < SLICES) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // a matrix-core step
+        constexpr int loads = LOADS * (R + 1) / F - LOADS * R / F;
+        constexpr int reads = READS * (R + 1) / F - READS * R / F;
+        if constexpr (Q == 0 && loads > 0) __builtin_amdgcn_sched_group_barrier(0x020, loads, 0);  // HBM loads
+        if constexpr (Q + 1 < SLICES && reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);  // LDS reads
+        if constexpr (R + 1 < F) {
+            weave<F, LOADS, READS, SLICES, Q, R + 1>();
+        } else {
+            weave<F, LOADS, READS, SLICES, Q + 1, 0>();
+        }
+    }
+}
+
+// ---- staging straight into LDS ------------------------------------------------
+//
+// HBM -> LDS staging is done by gfx950's buffer loads that write LDS directly
+// (`buffer_load_dwordx4 ... lds`): no staging registers and no ds_write
+// instructions.  Such a load writes 64 lanes x 16 bytes to consecutive LDS
+// bytes, so tiles are unpadded and bank conflicts are avoided by
+// XOR-swizzling each row's 16-byte chunks instead: a lane loads the global
+// chunk that belongs at the LDS position it writes.
+//  - K-contiguous tile, BK x 2-byte rows (CPR = BK / 8 chunks a row, RPW =
+//    256 / (2 BK) rows per 256-byte bank window): logical chunk c of row r
+//    lives at chunk c ^ ((r / RPW) % CPR), which spreads the 16 rows a
+//    ds_read_b128 phase touches over all 16 bank groups.
+//  - row-contiguous tile, ROWS x 2-byte rows: chunk c of k-row r lives at
+//    c ^ ((r & 3) << 2), which spreads the four rows of a transposing read
+//    over distinct bank groups.
+// The K loop runs NS stages deep: each step issues the loads of the step
+// NS - 1 ahead into the stage the previous step freed, then waits only for
+// the next step's loads (vmcnt counts this wave's loads in issue order).
+// Two 64-deep stages measure faster on MI355X than three or four 32-deep
+// ones (1170 vs 950 TFLOP/s at 8192^3): the per-step barrier costs more
+// than the extra latency cover buys.
+
+template <int BK>
+__device__ __forceinline__ int kc_swizzle(int row) {
+    constexpr int kCpr = BK / 8, kRpw = 256 / (2 * BK);
+    return (row / kRpw) % kCpr;
+}
+__device__ __forceinline__ int rc_swizzle(int row) { return (row & 3) << 2; }
+
+template <typename S, int ROWS, bool KC, int WAVES, int BK>
+struct DirectStager {
+    static constexpr int kTileBytes = ROWS * BK * 2;
+    static constexpr int kInstr = kTileBytes / 1024;  // one wave instruction moves 1 KiB
+    static constexpr int kPer = kInstr / WAVES;
+    static_assert(kInstr % WAVES == 0, "tile instructions must divide among the waves");
+    static constexpr int kRowsPer = KC ? 1024 / (BK * 2) : 1024 / (ROWS * 2);  // tile rows one instruction fills
+    static constexpr int kChunksPerRow = KC ? BK / 8 : ROWS / 8;
+
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t offset[kPer];  // this lane's chunk of each instruction, bytes at k0 = 0
+    uint32_t k_of[kPer];    // its k within a step (K-contiguous only)
+    uint32_t k_bytes;
+    int wave;
+
+    __device__ void init(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int w, int lane) {
+        wave = w;
+        if (KC) {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + static_cast<uint64_t>(first) * ld), 0,
+                                                     (rows - first) * ld * sizeof(S), kBufferFlags);
+            k_bytes = sizeof(S);
+        } else {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + first), 0, (depth * ld - first) * sizeof(S),
+                                                     kBufferFlags);
+            k_bytes = ld * sizeof(S);
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            const int first_row = kRowsPer * (w + WAVES * i);
+            const int row = first_row + lane / kChunksPerRow;
+            const int place = lane % kChunksPerRow;
+            const int chunk = place ^ (KC ? kc_swizzle<BK>(row) : rc_swizzle(row));
+            offset[i] = (static_cast<uint32_t>(row) * ld + chunk * 8) * sizeof(S);
+            k_of[i] = KC ? chunk * 8 : 0;
+        }
+    }
+    // Stage the step at `k0` into `tile` (the LDS stage).  Past K a
+    // K-contiguous chunk is the next row's, so it is pointed past the
+    // resource (operands are under 2^31 bytes) and loads zeros.
+    __device__ __forceinline__ void fetch(S* tile, uint32_t k0, uint32_t K, bool full) const {
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            const uint32_t at = (full || !KC || k0 + k_of[i] < K) ? offset[i] : 0x80000000u;
+            uint8_t* dst = reinterpret_cast<uint8_t*>(tile) + 1024 * (wave + WAVES * i);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, at,
+                                                     k0 * k_bytes, 0, 0);
+        }
+    }
+};
+
+// A lane's fragment of tile row `row_base + lane % 32` (the tile's M or N
+// index) for the 16-deep slice at `k_base`, from a swizzled tile.
+template <typename S, int ROWS, bool KC, int BK>
+__device__ __forceinline__ uint4 swizzled_fragment(const S* lds, int row_base, int k_base, int lane) {
+    if (KC) {
+        const int row = row_base + lane % 32;
+        const int chunk = (k_base / 8 + lane / 32) ^ kc_swizzle<BK>(row);
+        return reinterpret_cast<const uint4*>(lds)[row * (BK / 8) + chunk];
+    } else {
+        const int g = lane / 16, j = lane % 16;
+        const int k = k_base + (g / 2) * 8 + j / 4;
+        const int col = row_base + (g % 2) * 16 + 4 * (j % 4);
+        const int chunk = (col / 8) ^ rc_swizzle(k);  // k + 4 swizzles the same way
+        const S* at = lds + k * ROWS + chunk * 8 + col % 8;
+        short4v lo = read_tr16(at);
+        short4v hi = read_tr16(at + 4 * ROWS);
+        uint4 out;
+        out.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
+        out.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
+        out.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
+        out.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
+        return out;
+    }
+}
+
+// s_waitcnt's immediate for vmcnt(n), other counters not waited on
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_wait(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+// One LDS stage of an operand.  A separate array per stage gives every LDS
+// read and every direct load a distinct, statically known object, so the
+// compiler waits for a stage's loads only where that stage is read.
+template <typename S, int ELEMS, int STAGE>
+__device__ __forceinline__ S* stage_tile() {
+    __shared__ __attribute__((aligned(1024))) S tile[ELEMS];
+    return tile;
+}
+
+template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN, int BK, int NS,
+          class EPI = PlainStore>
+__global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restrict__ A, const S* __restrict__ B,
+                                                                O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                                                                bool accumulate, EPI epi) {
+    constexpr int kWaves = WM * WN;
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+    constexpr int kA = BM * BK, kB = BN * BK;  // elements of one stage
+    static_assert(NS >= 2 && NS <= 4, "two to four stages");
+
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    uint32_t tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int wm = wave / WN, wn = wave % WN;
+
+    using StagerA = DirectStager<S, BM, A_KC, kWaves, BK>;
+    using StagerB = DirectStager<S, BN, B_KC, kWaves, BK>;
+    StagerA sa;
+    StagerB sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
+    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
+
+    uint4 fa[2][TM], fb[2][TN];
+    auto read_fragments = [&](int slot, const S* la, const S* lb, int kk) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            fa[slot][i] = swizzled_fragment<S, BM, A_KC, BK>(la, wm * (BM / WM) + i * 32, kk, lane);
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            fb[slot][j] = swizzled_fragment<S, BN, B_KC, BK>(lb, wn * (BN / WN) + j * 32, kk, lane);
+    };
+
+    constexpr int kSlices = BK / 16;
+    constexpr int kSteps = TM * TN;
+    constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
+    constexpr int kLoads = StagerA::kPer + StagerB::kPer;  // this wave's loads per step
+    const uint32_t steps = (K + BK - 1) / BK;
+    auto stage_of = [&](auto t, uint32_t s) {
+        const uint32_t k0 = (s < steps ? s : steps - 1) * BK;  // past the end: a harmless reload
+        sa.fetch(stage_tile<S, kA, 2 * decltype(t)::value>(), k0, K, k0 + BK <= K);
+        sb.fetch(stage_tile<S, kB, 2 * decltype(t)::value + 1>(), k0, K, k0 + BK <= K);
+    };
+    // Step s computes from stage T = s % NS.  It first stages step s + NS - 1
+    // into stage (T + NS - 1) % NS, which every wave finished reading before
+    // the previous step's barrier; it waits for step s + 1 and meets the
+    // others at a barrier before its last slice, whose fragments it already
+    // holds, and reads step s + 1's first fragments under that slice.
+    auto step = [&](auto t, uint32_t s) {
+        constexpr int T = decltype(t)::value;
+        const S* la = stage_tile<S, kA, 2 * T>();
+        const S* lb = stage_tile<S, kB, 2 * T + 1>();
+        stage_of(std::integral_constant<int, (T + NS - 1) % NS>{}, s + NS - 1);
+#pragma unroll
+        for (int q = 0; q + 1 < kSlices; q++) {
+            read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[q & 1][i], fb[q & 1][j], acc[i][j]);
+        }
+        weave<kSteps, kLoads, kReads, kSlices - 1>();
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(kLoads * (NS - 2)));  // step s + 1 is in LDS
+        __syncthreads();
+        constexpr int last = (kSlices - 1) & 1;
+        constexpr int U = (T + 1) % NS;
+        read_fragments(last ^ 1, stage_tile<S, kA, 2 * U>(), stage_tile<S, kB, 2 * U + 1>(), 0);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[last][i], fb[last][j], acc[i][j]);
+        weave<kSteps, 0, kReads, 2>();
+    };
+    if (steps > 0) {
+        stage_of(std::integral_constant<int, 0>{}, 0);
+        if constexpr (NS > 2) stage_of(std::integral_constant<int, 1>{}, 1);
+        if constexpr (NS > 3) stage_of(std::integral_constant<int, 2>{}, 2);
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(kLoads * (NS - 2)));  // step 0 is in LDS
+        __syncthreads();
+        read_fragments(0, stage_tile<S, kA, 0>(), stage_tile<S, kB, 1>(), 0);
+    }
+    for (uint32_t s = 0; s < steps; s += NS) {
+        step(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < steps) step(std::integral_constant<int, 1 % NS>{}, s + 1);
+        if constexpr (NS > 2) {
+            if (s + 2 < steps) step(std::integral_constant<int, 2 % NS>{}, s + 2);
+        }
+        if constexpr (NS > 3) {
+            if (s + 3 < steps) step(std::integral_constant<int, 3 % NS>{}, s + 3);
+        }
+    }
+
+    if constexpr (EPI::kProgram) {
+        // The four stage arrays, BK / 2 rows of BN floats each, hold a pass
+        // of 2 BK rows.
+        static_assert(NS == 2 && BM == BN && kA == kB, "square tiles over two stages");
+        constexpr int kRegionRows = kA * static_cast<int>(sizeof(S)) / 4 / BN;
+        constexpr int kPass = 4 * kRegionRows;
+        constexpr int kPasses = BM / kPass, H = BM / WM / kPasses;
+        static_assert(BM % kPass == 0 && H % 32 == 0, "whole passes of whole matrix-core tiles");
+        float* r0 = reinterpret_cast<float*>(stage_tile<S, kA, 0>());
+        float* r1 = reinterpret_cast<float*>(stage_tile<S, kB, 1>());
+        float* r2 = reinterpret_cast<float*>(stage_tile<S, kA, 2>());
+        float* r3 = reinterpret_cast<float*>(stage_tile<S, kB, 3>());
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // the last step's reload has landed
+#pragma unroll
+        for (int pass = 0; pass < kPasses; pass++) {
+            lds_barrier();  // every wave is done with LDS
+#pragma unroll
+            for (int i = pass * H / 32; i < (pass + 1) * H / 32; i++) {
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const uint32_t col = wn * (BN / WN) + j * 32 + lane % 32;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const uint32_t rr = wm * H + i * 32 - pass * H + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                        *staged_at<BN, 32, kRegionRows>(r0, r1, r2, r3, rr, col) = acc[i][j][e];
+                    }
+                }
+            }
+            lds_barrier();
+            program_pass<BN, 32, kRegionRows, H, BM / WM>(epi, r0, r1, r2, r3, kPass, pass, m0, n0, M,
+                                                                           N);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint32_t col = n0 + wn * (BN / WN) + j * 32 + lane % 32;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                    if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
+                }
+            }
+        }
+    }
+}
+
+}  // namespace tc
