@@ -477,6 +477,63 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
     return true;
 }
 
+// A program whose loads do not all walk in element order (a broadcast
+// operand, a transposed view) runs compiled too, from its second
+// appearance: a kernel over the rows x cols space, 16 elements a thread 64
+// apart (each load and store instruction of a wave one contiguous run), each
+// element's row and column by one 32-bit division, the program as the same
+// straight-line code a product epilogue runs.
+constexpr int kGeneralElems = 16;
+
+bool run_general_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                          uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, hipStream_t s,
+                          int* status) {
+    const uint64_t total = rows * cols;
+    // 32-bit element indices: below 2^31, so no index of the last pass wraps.
+    if (place_count > static_cast<uint32_t>(kInlinePlaces) || total > (uint64_t{1} << 31)) return false;
+    std::vector<float> constants;
+    const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, &constants);
+    if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
+    const std::string E = std::to_string(kGeneralElems);
+    const std::string source =
+        "#include \"device.hpp\"\n"
+        "struct Program {\n" + std::string(compiled_members()) +
+        "  __device__ __forceinline__ void group(const bool (&live)[" + E + "], const uint32_t (&row)[" + E + "],\n"
+        "      const uint32_t (&col)[" + E + "], uint32_t N) const {\n" + body + "  }\n};\n"
+        "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_general(Program p, uint32_t cols, uint32_t total) {\n"
+        "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
+        "  const uint32_t per_block = 256u * " + E + ";\n"
+        "  for (uint32_t base = blockIdx.x * per_block; base < total; base += gridDim.x * per_block) {\n"
+        "    uint32_t row[" + E + "], col[" + E + "];\n"
+        "    bool live[" + E + "];\n"
+        "    for (int v = 0; v < " + E + "; v++) {\n"
+        "      const uint32_t at = base + wave * (64u * " + E + ") + v * 64u + lane;\n"
+        "      live[v] = at < total;\n"
+        "      row[v] = at / cols;\n"
+        "      col[v] = at - row[v] * cols;\n"
+        "    }\n"
+        "    p.group(live, row, col, cols);\n"
+        "  }\n"
+        "}\n";
+    hipFunction_t function = nullptr;
+    if (!cached_kernels(source, {"tc_fused_general"}, &function)) return false;
+    CompiledArgsOf args{};
+    for (int k = 0; k < TC_FUSED_MAX_INPUTS; k++) args.in[k] = buffers.inputs[k];
+    for (int k = 0; k < TC_FUSED_MAX_OUTPUTS; k++) args.out[k] = buffers.outputs[k];
+    int place_status = to_device_places(places, place_count, args.places);
+    if (place_status != TC_OK) {
+        *status = place_status;
+        return true;
+    }
+    for (size_t c = 0; c < constants.size(); c++) args.constants[c] = constants[c];
+    uint32_t cols32 = static_cast<uint32_t>(cols), total32 = static_cast<uint32_t>(total);
+    void* params[] = {&args, &cols32, &total32};
+    const uint32_t blocks = grid_for(total, 256 * kGeneralElems, 8);
+    const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);
+    *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused program: ") + hipGetErrorString(error));
+    return true;
+}
+
 // Host-side validation of what the kernel would otherwise trust.
 int check_program(const tc_encoded* code, uint32_t count, uint32_t place_count, uint32_t input_count,
                   uint32_t output_count) {
@@ -597,6 +654,7 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
         }
         return check_launch("fused program");
     }
+    if (run_general_compiled(code, count, dtype, places, place_count, buffers, rows, cols, s, &status)) return status;
     std::vector<DevicePlace> device_places(place_count);
     status = to_device_places(places, place_count, device_places.data());
     if (status != TC_OK) return status;

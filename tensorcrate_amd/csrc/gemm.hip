@@ -491,15 +491,6 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
 // loads are in flight together.
 constexpr int kCompiledElems = 16;
 
-// A compiled epilogue's arguments, laid out as the generated
-// `CompiledStore` declares its members.
-struct CompiledStoreArgs {
-    const void* in[TC_FUSED_MAX_INPUTS];
-    void* out[TC_FUSED_MAX_OUTPUTS];
-    DevicePlace places[kInlinePlaces];
-    float constants[kInlineCode];
-};
-
 // The product kernels with `code` compiled into their epilogue, once the
 // program has been seen before: true when they were launched.
 bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, const void* a, const void* b,
@@ -513,11 +504,8 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     std::string source = "#include \"gemm_kernels.hpp\"\n"
                          "struct CompiledStore {\n"
                          "  static constexpr bool kProgram = true;\n"
-                         "  static constexpr int kElems = " + std::to_string(kCompiledElems) + ";\n"
-                         "  const void* in[" + std::to_string(TC_FUSED_MAX_INPUTS) + "];\n"
-                         "  void* out[" + std::to_string(TC_FUSED_MAX_OUTPUTS) + "];\n"
-                         "  tc::DevicePlace places[" + std::to_string(kInlinePlaces) + "];\n"
-                         "  float constants[" + std::to_string(kInlineCode) + "];\n"
+                         "  static constexpr int kElems = " + std::to_string(kCompiledElems) + ";\n" +
+                         compiled_members() +
                          "  __device__ __forceinline__ void group(const bool (&live)[kElems], const uint32_t (&row)[kElems],\n"
                          "      const uint32_t (&col)[kElems], uint32_t N, const float (&product)[kElems]) const {\n" +
                          body + "  }\n};\n";
@@ -539,7 +527,7 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     small = ((m + 127) / 128) * ((n + 127) / 128);
     hipFunction_t functions[2] = {};
     if (!compiled_kernels(source, kernels, functions)) return false;
-    CompiledStoreArgs args{};
+    CompiledArgsOf args{};
     for (uint32_t slot = 1; slot < input_count; slot++) args.in[slot] = inputs[slot];
     for (uint32_t slot = 0; slot < output_count; slot++) args.out[slot] = outputs[slot];
     for (uint32_t p = 0; p < place_count; p++) args.places[p] = places[p];

@@ -39,6 +39,24 @@ struct Buffers {
 constexpr int kInlineCode = 48;
 constexpr int kInlinePlaces = 8;
 
+// The arguments of a compiled program (an epilogue's `CompiledStore` or a
+// general program's `Program`), laid out as the generated source declares
+// its members.
+struct CompiledArgsOf {
+    const void* in[TC_FUSED_MAX_INPUTS];
+    void* out[TC_FUSED_MAX_OUTPUTS];
+    DevicePlace places[8];
+    float constants[48];
+};
+
+static_assert(TC_FUSED_MAX_INPUTS == 16 && TC_FUSED_MAX_OUTPUTS == 8 && kInlinePlaces == 8 && kInlineCode == 48,
+              "the generated members' extents");
+
+// The generated declaration of those members.
+inline const char* compiled_members() {
+    return "  const void* in[16];\n  void* out[8];\n  tc::DevicePlace places[8];\n  float constants[48];\n";
+}
+
 struct Inline {
     tc_encoded code[kInlineCode];
     DevicePlace places[kInlinePlaces];

@@ -160,3 +160,42 @@ def test_a_compiled_program_past_the_infinity_cache_streams_and_stays_exact():
         rule.update(params, lib.Buffer.of(g), 1, n)
         expected = want.update(expected, g)
     assert np.array_equal(params.download(np.float32), expected)
+
+
+@pytest.mark.parametrize("rows,cols", [(37, 70), (1, 1), (4099, 1000), (1000, 3)])
+def test_a_repeated_broadcast_program_runs_compiled_and_stays_exact(rows, cols):
+    # A program with a broadcast row vector and a transposed matrix is not
+    # dense; from its second appearance it runs compiled (straight-line, 16
+    # elements a thread).  Every run, in every type, gives the oracle's bits
+    # (a square root: correctly rounded on both sides).
+    import ctypes
+
+    def compiled():
+        count = ctypes.c_uint64()
+        lib.call("tc_fused_compiled", ctypes.byref(count))
+        return count.value
+
+    rng = np.random.default_rng(rows + cols)
+    bias = to_kind(rng.standard_normal(cols), lib.F16)
+    tm = to_kind(rng.standard_normal((cols, rows)), lib.BF16)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    code = [(0, 0, 0, 0, lib.F16, 0, 0.0), (0, 1, 1, 1, lib.BF16, 0, 0.0), (0, 2, 2, 2, lib.F32, 0, 0.0),
+            (2, lib.MUL, 3, 1, 2, 0, 0.0), (2, lib.ADD, 3, 3, 0, 0, 0.0), (3, 13, 7, 3, 0, 0, 0.0),
+            (1, 0, 8, 0, 0, 0, 0.75), (2, lib.SUB, 7, 7, 8, 0, 0.0), (4, lib.GREATER, 5, 3, 0, 0, 0.0),
+            (5, 0, 0, 7, lib.BF16, 0, 0.0), (5, 0, 0, 5, lib.F32, 1, 0.0)]
+    places = [(0, 1, 1, [rows], [0]), (0, rows, 1, [rows], [1]), identity_place(rows, cols)]
+    d = [lib.Buffer.of(bias), lib.Buffer.of(tm), lib.Buffer.of(x)]
+    for dtype in KINDS:
+        out0 = np.zeros(rows * cols, np.uint16)
+        out1 = np.zeros(rows * cols, np.float32)
+        oracle.fused(dtype, code, places, [bias.view(np.uint16), tm, x], [out0, out1], rows, cols)
+        before = compiled()
+        for _ in range(3):
+            g0, g1 = lib.Buffer(out0.nbytes), lib.Buffer(out1.nbytes)
+            lib.fused(dtype, code, places, [(d[0], cols), (d[1], rows * cols), (d[2], rows * cols)],
+                      [(g0, rows * cols), (g1, rows * cols)], rows, cols)
+            assert same_bits(g0.download(np.uint16), out0, lib.BF16), dtype
+            assert bits_equal(g1.download(np.float32), out1), dtype
+        # Compiled once per type, on the first shape's second run (the source
+        # does not depend on the shape).
+        assert compiled() == before + (1 if (rows, cols) == (37, 70) else 0)
