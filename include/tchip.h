@@ -440,7 +440,10 @@ int tc_fused_sum(uint32_t dtype, const tc_encoded* code, uint32_t count, const t
  * fused/mod.rs:4754-4766; checks in `Program::run_matmul`, :1143-1200): the
  * product A[m x k] . B[k x n] (row-major, `dtype`, as `tc_matmul` forms it)
  * is the program's input 0, read unremapped over the m x n space, and
- * `inputs` fill slots 1 on; outputs as `tc_fused`. */
+ * `inputs` fill slots 1 on; outputs as `tc_fused`.  The program runs in the
+ * product kernel's epilogue, so the product is not written to memory; the
+ * results are the bits of `tc_matmul` then `tc_fused`.  A load of input 0
+ * through any other place, or as another type, is refused. */
 int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
                        uint32_t place_count, uint64_t m, uint64_t k, uint64_t n, const void* a, const void* b,
                        const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
