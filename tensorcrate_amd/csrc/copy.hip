@@ -93,23 +93,43 @@ __global__ void __launch_bounds__(256) gather_kernel(const T* __restrict__ src, 
 // `run_div` divides a flat (row, word) index by the words per row.  One word
 // a thread, over a grid that covers them; NT (16-byte words only) marks a
 // copy that streams past the Infinity Cache.
-template <typename T, bool NT, typename I>
+template <typename T, bool NT, typename I, int U = 1>
 __global__ void __launch_bounds__(256) rows_kernel(const T* __restrict__ src, T* __restrict__ dst,
                                                    Layout2<I> layout, Div<I> run_div, I run, I total) {
-    // One round normally; the loop (64-bit, so it cannot wrap) covers work
-    // past what one dispatch holds.
+    // U words a thread, a grid apart, all loads issued before any store; one
+    // round normally, the loop (64-bit, so it cannot wrap) covering work past
+    // what one dispatch holds.
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t item = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; item < total;
-         item += stride) {
-        const I i = static_cast<I>(item);
-        I row = run_div.div(i);
-        I word = i - row * run;
-        I from, to;
-        locate(layout, layout.rank - 1, row, from, to);
-        if constexpr (NT) {
-            store_word<true>(dst + to + word, load_word<true>(src + from + word));
-        } else {
-            dst[to + word] = src[from + word];
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; base < total;
+         base += stride * U) {
+        T value[U];
+        I to[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            const uint64_t item = base + k * stride;
+            if (item < total) {
+                const I i = static_cast<I>(item);
+                I row = run_div.div(i);
+                I word = i - row * run;
+                I from;
+                locate(layout, layout.rank - 1, row, from, to[k]);
+                to[k] += word;
+                if constexpr (NT) {
+                    value[k] = load_word<true>(src + from + word);
+                } else {
+                    value[k] = src[from + word];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            if (base + k * stride < total) {
+                if constexpr (NT) {
+                    store_word<true>(dst + to[k], value[k]);
+                } else {
+                    dst[to[k]] = value[k];
+                }
+            }
         }
     }
 }
@@ -382,12 +402,12 @@ int copy_walk(const void* src, void* dst, const Walk<2>& walk, uint64_t count, b
     return launch_copy<T, uint64_t>(from, to, walk, count, stream, s);
 }
 
-// `traffic` is the bytes the whole operation moves: one larger than the
+// `traffic` is the bytes the whole operation moves: one as large as the
 // Infinity Cache streams past it, however it is split into launches.
 int copy_by_width(uint32_t width, const void* src, void* dst, const Walk<2>& walk, uint64_t count,
                   uint64_t traffic, const char* operation) {
     TC_STREAM(s);
-    const bool stream = traffic > kStreamBytes;
+    const bool stream = traffic >= kStreamBytes;
     switch (width) {
         case 1: return copy_walk<Word<1>::type>(src, dst, walk, count, stream, s);
         case 2: return copy_walk<Word<2>::type>(src, dst, walk, count, stream, s);
