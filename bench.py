@@ -206,6 +206,63 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
     return lines
 
 
+PCIE_PEAK = 64.0  # GB/s, PCIe 5.0 x16, one direction
+
+
+def transfers() -> list[dict]:
+    """Host to HBM and back, 1 GiB of pageable memory each way: the plain
+    runtime copy (`tc_upload`) against the pinned double-buffered staging
+    (`tc_upload_staged`), and a TCR1 record of 1 GiB loaded from a file in
+    the page cache straight into HBM.  Wall time of each call, which returns
+    only when its host side is free."""
+    import tempfile
+
+    from oracle import tcr1  # writes the record the loader reads
+
+    nbytes = 1 << 30
+    host = np.random.default_rng(5).integers(0, 256, nbytes, dtype=np.uint8)
+    back = np.empty_like(host)
+    dev = lib.Buffer(nbytes)
+
+    def wall(fn, repeats=3):
+        fn()
+        lib.sync()
+        best = float("inf")
+        for _ in range(repeats):
+            start = time.perf_counter()
+            fn()
+            lib.sync()
+            best = min(best, time.perf_counter() - start)
+        return best * 1e3
+
+    def line(workload, ms):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"workload": workload, "value": gbs, "unit": "GB/s", "ms": ms,
+                "roofline": {"bound": "pcie", "achieved": gbs, "peak": PCIE_PEAK, "unit": "GB/s",
+                             "frac": gbs / PCIE_PEAK, "traffic": None}}
+
+    lines = [
+        line("upload 1 GiB pageable, runtime copy", wall(lambda: lib.call("tc_upload", dev.ptr, host.ctypes.data, nbytes))),
+        line("upload 1 GiB pageable, pinned staging",
+             wall(lambda: lib.call("tc_upload_staged", dev.ptr, host.ctypes.data, nbytes))),
+        line("download 1 GiB pageable, runtime copy",
+             wall(lambda: lib.call("tc_download", back.ctypes.data, dev.ptr, nbytes))),
+        line("download 1 GiB pageable, pinned staging",
+             wall(lambda: lib.call("tc_download_staged", back.ctypes.data, dev.ptr, nbytes))),
+    ]
+    with tempfile.TemporaryDirectory() as folder:
+        path = os.path.join(folder, "x.tcr")
+        tag = tcr1.tag("u8")
+        with open(path, "wb") as f:
+            f.write(tcr1.record(tcr1.VECTOR, [nbytes], tag, host.tobytes()))
+        h = lib.Tcr1()
+        lib.call("tc_tcr1_read_header", path.encode(), 0, tag, len(tag), tcr1.VECTOR, ctypes.byref(h))
+        lines.append(line("TCR1 record of 1 GiB, page-cached file to HBM",
+                          wall(lambda: lib.call("tc_tcr1_load", path.encode(), ctypes.byref(h), dev.ptr))))
+    dev.free()
+    return lines
+
+
 def hbm_line(workload: str, nbytes: float, ms: float) -> dict:
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"workload": workload, "value": gbs, "unit": "GB/s", "ms": ms,
@@ -389,6 +446,9 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
         log("dense layers, fused and unfused ...")
         workloads += dense_layer("bf16", 8192, 8192, 8192, steps, warmup)
         workloads += dense_layer("f32", 4096, 1024, 4096, steps, warmup)
+    if "transfer" in groups:
+        log("host transfers and TCR1 loads ...")
+        workloads += transfers()
     if "mlp" in groups:
         log("MLP training step and Adam ...")
         # Three untimed steps: Adam's programs compile on their second
@@ -410,7 +470,7 @@ def main() -> int:
     parser.add_argument("--traffic-probe", action="store_true",
                         help="only the short copy + product run that HBM-traffic counters are read over")
     parser.add_argument("--only", default="",
-                        help="comma-separated secondary groups to run alone (gemm, reductions, copies, fusion, mlp); "
+                        help="comma-separated secondary groups to run alone (gemm, reductions, copies, fusion, transfer, mlp); "
                              "prints their lines as a JSON list instead of the headline line")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -425,7 +485,7 @@ def main() -> int:
 
     if args.only:
         groups = set(args.only.split(","))
-        unknown = groups - {"gemm", "reductions", "copies", "fusion", "mlp"}
+        unknown = groups - {"gemm", "reductions", "copies", "fusion", "transfer", "mlp"}
         if unknown:
             print(f"bench.py: no workload group {sorted(unknown)}", file=sys.stderr)
             return 2

@@ -49,7 +49,9 @@ typedef enum tc_status {
     TC_INVALID = 1,     /* a shape, layout or argument the reference would panic on */
     TC_UNSUPPORTED = 2, /* a type or operation with no kernel: never a silent fallback */
     TC_DEVICE = 3,      /* a HIP runtime error */
-    TC_OUT_OF_MEMORY = 4
+    TC_OUT_OF_MEMORY = 4,
+    TC_FORMAT = 5, /* a stored tensor this build does not read: the reference's `Error::Format` */
+    TC_IO = 6      /* a file that cannot be opened, read or written, or ends early: `Error::Io` */
 } tc_status;
 
 /* Storage and arithmetic types: `fused::DType` (fused/mod.rs:145-150). */
@@ -180,7 +182,8 @@ int tc_free(void* pointer);
 /* Give every cached, unused block back to the device. */
 int tc_empty_cache(void);
 /* Host to device, device to host (`as_slice`, backend.rs:99; the download
- * waits for queued work), and device to device (`duplicate`, backend.rs:111). */
+ * waits for queued work), and device to device (`duplicate`, backend.rs:111).
+ * From 8 MiB up the first two take the pinned staging of tc_upload_staged. */
 int tc_upload(void* device_dst, const void* host_src, size_t bytes);
 int tc_download(void* host_dst, const void* device_src, size_t bytes);
 int tc_copy(void* device_dst, const void* device_src, size_t bytes);
@@ -234,6 +237,53 @@ int tc_clamp(uint32_t dtype, const void* a, float low, float high, void* out, ui
 int tc_strided_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank,
                       const uint64_t* shape, const void* a, uint64_t a_len, const tc_strided* a_at,
                       const void* b, uint64_t b_len, const tc_strided* b_at, void* out);
+
+/* ---- transfers and the TCR1 format (persist.rs:44-93) -------------------- */
+
+/* Host memory to and from HBM through the thread's two pinned staging
+ * buffers (16 MiB each, allocated on first use and held until the process
+ * ends), the CPU copying one chunk while the DMA engine moves the other.
+ * For pageable memory (`to_backend`, `as_slice`, tensors/backend.rs); the
+ * host buffer is free again when the call returns. */
+int tc_upload_staged(void* device_dst, const void* host_src, size_t bytes);
+int tc_download_staged(void* host_dst, const void* device_src, size_t bytes);
+
+/* A TCR1 record's header (persist.rs:44-93): `kind` 0 vector, 1 matrix, 2
+ * tensor; `rank` extents in `shape` (a vector's length, a matrix's rows and
+ * columns); `count` elements of `element_bytes` each, the payload at byte
+ * `data_offset` of the file and the record ending at `end_offset` (where a
+ * next record may begin). */
+typedef struct tc_tcr1 {
+    uint32_t kind;
+    uint32_t rank;
+    uint64_t shape[TC_MAX_RANK];
+    uint64_t count;
+    uint64_t element_bytes;
+    uint64_t data_offset;
+    uint64_t end_offset;
+} tc_tcr1;
+
+/* `read_from`'s header checks (persist.rs:266-330, :330-333, :453-480) for
+ * the record at byte `offset` of `path`, read into a target whose element
+ * tag is `tag` (persist.rs:105-189: f32 0x10, f16 0x12, bf16 0x13, ...) and
+ * whose kind is `kind` (a tensor target, 2, also reads vector and matrix
+ * records): TC_FORMAT with the reference's message for a wrong magic,
+ * version, kind, element type or too many axes; TC_IO for a file that ends
+ * before the record does. */
+int tc_tcr1_read_header(const char* path, uint64_t offset, const uint8_t* tag, uint32_t tag_length,
+                        uint32_t kind, tc_tcr1* out);
+
+/* The record's payload, as stored, into `device_dst` (`count *
+ * element_bytes` bytes): read from the file into pinned staging and copied
+ * to HBM, the two overlapped. */
+int tc_tcr1_load(const char* path, const tc_tcr1* header, void* device_dst);
+
+/* `write_to` (persist.rs:350-430) from the device: the header for `kind`,
+ * `rank` extents and element `tag`, then the `count * element size` bytes
+ * at `device_src`, copied to pinned staging and written to `path`
+ * (truncated, or appended to when `append` is nonzero). */
+int tc_tcr1_save(const char* path, int append, uint32_t kind, uint32_t rank, const uint64_t* shape,
+                 const uint8_t* tag, uint32_t tag_length, const void* device_src);
 
 /* ---- scans and sorts (kernels.rs:870-873) -------------------------------- */
 

@@ -311,9 +311,15 @@ int tc_empty_cache(void) {
     return TC_OK;
 }
 
+// Transfers this large go through the thread's pinned staging
+// (tc_upload_staged, persist.hip), at about twice the runtime's pageable
+// rate up and three times down; smaller ones cost less as one runtime copy.
+constexpr size_t kStagedBytes = size_t{8} << 20;
+
 int tc_upload(void* dst, const void* src, size_t bytes) {
     TC_STREAM(s);
     if (bytes == 0) return TC_OK;
+    if (bytes >= kStagedBytes) return tc_upload_staged(dst, src, bytes);
     // A pageable source: the runtime stages it before the call returns, so
     // the caller's buffer is free to reuse at once.
     hipError_t error = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
@@ -326,6 +332,7 @@ int tc_upload(void* dst, const void* src, size_t bytes) {
 int tc_download(void* dst, const void* src, size_t bytes) {
     TC_STREAM(s);
     if (bytes == 0) return TC_OK;
+    if (bytes >= kStagedBytes) return tc_download_staged(dst, src, bytes);
     hipError_t error = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
     if (error != hipSuccess) return hip_fail(error, "download");
     error = hipStreamSynchronize(s);

@@ -20,7 +20,7 @@ MAX_RANK = 6
 FUSED_LEAD = 5
 
 # Status codes (tc_status).
-OK, INVALID, UNSUPPORTED, DEVICE, OUT_OF_MEMORY = range(5)
+OK, INVALID, UNSUPPORTED, DEVICE, OUT_OF_MEMORY, FORMAT, IO = range(7)
 # Element types (fused::DType, fused/mod.rs:145-150).
 F32, F16, BF16, F64 = range(4)
 # BinaryOp (kernels.rs:32-38).
@@ -102,6 +102,13 @@ _lib: ctypes.CDLL | None = None
 
 u32, u64, vp, i32, f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int, ctypes.c_float
 
+
+class Tcr1(ctypes.Structure):
+    """`tc_tcr1`: a TCR1 record's header as the loader parsed it."""
+    _fields_ = [("kind", u32), ("rank", u32), ("shape", u64 * MAX_RANK), ("count", u64), ("element_bytes", u64),
+                ("data_offset", u64), ("end_offset", u64)]
+
+
 # Every entry point of include/tchip.h with its argument types.
 SIGNATURES = {
     "tc_init": [i32],
@@ -138,6 +145,11 @@ SIGNATURES = {
     "tc_dot": [u32, vp, vp, u64, vp],
     "tc_moments": [u32, vp, u64, vp],
     "tc_prefix_sum": [u32, vp, vp, u64],
+    "tc_upload_staged": [vp, vp, ctypes.c_size_t],
+    "tc_download_staged": [vp, vp, ctypes.c_size_t],
+    "tc_tcr1_read_header": [ctypes.c_char_p, u64, ctypes.c_char_p, u32, u32, vp],
+    "tc_tcr1_load": [ctypes.c_char_p, vp, vp],
+    "tc_tcr1_save": [ctypes.c_char_p, i32, u32, u32, vp, ctypes.c_char_p, u32, vp],
     "tc_distribution": [u32, u32, u32, vp, vp, u64, f32, f32],
     "tc_axis_distribution": [u32, u32, u32, vp, u64, u64, u32, vp, vp, vp],
     "tc_sort": [u32, vp, vp, u64, u32],
