@@ -248,6 +248,15 @@ int tc_strided_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank,
 int tc_upload_staged(void* device_dst, const void* host_src, size_t bytes);
 int tc_download_staged(void* host_dst, const void* device_src, size_t bytes);
 
+/* A small read (at most 64 bytes, such as a reduction's scalar) queued
+ * behind the thread's work into one of its 1024 pinned slots, returning at
+ * once with a `ticket` (the tape's unread loss, `Lazy`, tape/mod.rs:253-295:
+ * the value is only waited for when something reads it). */
+int tc_read_async(const void* device_src, size_t bytes, uint64_t* ticket);
+/* Wait for that read alone and copy its bytes to `host_dst`; TC_INVALID for
+ * a ticket this thread never issued or whose slot 1024 later reads reused. */
+int tc_read_wait(uint64_t ticket, void* host_dst, size_t bytes);
+
 /* A TCR1 record's header (persist.rs:44-93): `kind` 0 vector, 1 matrix, 2
  * tensor; `rank` extents in `shape` (a vector's length, a matrix's rows and
  * columns); `count` elements of `element_bytes` each, the payload at byte

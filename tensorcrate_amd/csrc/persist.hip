@@ -153,6 +153,23 @@ int staged_download(const void* device_src, size_t bytes, Drain drain) {
     return TC_OK;
 }
 
+// ---- small reads, queued --------------------------------------------------------
+
+// A reduction's result read back without a wait at the time it is asked for
+// (the tape's unread loss, tape/mod.rs:253-295): the copy is queued behind the
+// thread's work into one of its pinned slots, and only reading the ticket
+// waits, for that copy alone.
+constexpr uint64_t kSlots = 1024;
+constexpr size_t kSlotBytes = 64;
+
+struct Slots {
+    uint8_t* pinned = nullptr;
+    hipEvent_t done[kSlots] = {};
+    uint64_t issued = 0;  // tickets handed out; ticket t lives in slot t % kSlots
+};
+
+thread_local Slots slots;
+
 // ---- TCR1 -------------------------------------------------------------------
 
 constexpr uint8_t kMagic[4] = {'T', 'C', 'R', '1'};
@@ -280,6 +297,48 @@ int tc_download_staged(void* host_dst, const void* device_src, size_t bytes) {
             return TC_OK;
         });
     });
+}
+
+int tc_read_async(const void* device_src, size_t bytes, uint64_t* ticket) {
+    TC_STREAM(s);
+    if (bytes > kSlotBytes) return fail(TC_INVALID, "read_async: " + std::to_string(bytes) + " bytes, over 64");
+    if (slots.pinned == nullptr) {
+        void* block = nullptr;
+        hipError_t error = hipHostMalloc(&block, kSlots * kSlotBytes, hipHostMallocDefault);
+        if (error != hipSuccess) return fail(TC_OUT_OF_MEMORY, std::string("read slots: ") + hipGetErrorString(error));
+        slots.pinned = static_cast<uint8_t*>(block);
+    }
+    const uint64_t t = slots.issued;
+    const uint64_t slot = t % kSlots;
+    if (slots.done[slot] == nullptr) {
+        hipError_t error = hipEventCreateWithFlags(&slots.done[slot], hipEventDisableTiming);
+        if (error != hipSuccess) return fail(TC_DEVICE, std::string("read slot event: ") + hipGetErrorString(error));
+    } else {
+        // The slot's previous read must land before this one overwrites it.
+        hipError_t error = hipEventSynchronize(slots.done[slot]);
+        if (error != hipSuccess) return fail(TC_DEVICE, std::string("read slot: ") + hipGetErrorString(error));
+    }
+    hipError_t error = hipMemcpyAsync(slots.pinned + slot * kSlotBytes, device_src, bytes, hipMemcpyDeviceToHost, s);
+    if (error == hipSuccess) error = hipEventRecord(slots.done[slot], s);
+    if (error != hipSuccess) return fail(TC_DEVICE, std::string("read_async: ") + hipGetErrorString(error));
+    slots.issued = t + 1;
+    *ticket = t;
+    return TC_OK;
+}
+
+int tc_read_wait(uint64_t ticket, void* host_dst, size_t bytes) {
+    if (bytes > kSlotBytes) return fail(TC_INVALID, "read_wait: " + std::to_string(bytes) + " bytes, over 64");
+    if (ticket >= slots.issued || slots.issued - ticket > kSlots) {
+        return fail(TC_INVALID, "read_wait: ticket " + std::to_string(ticket) +
+                                    (ticket >= slots.issued ? " was never issued on this thread"
+                                                            : " was reused by 1024 later reads"));
+    }
+    const uint64_t slot = ticket % kSlots;
+    hipError_t error = hipEventSynchronize(slots.done[slot]);
+    if (error != hipSuccess) return fail(TC_DEVICE, std::string("the GPU failed; its output is invalid: ") +
+                                                        hipGetErrorString(error));
+    memcpy(host_dst, slots.pinned + slot * kSlotBytes, bytes);
+    return TC_OK;
 }
 
 int tc_tcr1_read_header(const char* path, uint64_t offset, const uint8_t* tag, uint32_t tag_length,

@@ -288,6 +288,23 @@ struct Kernels {
         check(tc_transpose(sizeof(T), m.rows(), m.cols(), m.storage().ptr(), out.ptr()));
         return Matrix<T>(m.cols(), m.rows(), std::move(out));
     }
+    // `vector_reduce` (kernels.rs:867) queued, its result read back behind
+    // it: the ticket's value is waited for only when it is read.
+    static uint64_t reduce_async(const Storage<T>& values, Reduce op) {
+        float* result = nullptr;
+        check(tc_alloc(sizeof(float), reinterpret_cast<void**>(&result)));
+        int status = tc_vector_reduce(dtype, values.ptr(), values.len(), static_cast<uint32_t>(op), result);
+        uint64_t ticket = 0;
+        if (status == TC_OK) status = tc_read_async(result, sizeof(float), &ticket);
+        tc_free(result);  // reused only by work queued after the read
+        check(status);
+        return ticket;
+    }
+    static T read(uint64_t ticket) {
+        float host = 0.0f;
+        check(tc_read_wait(ticket, &host, sizeof(float)));
+        return static_cast<T>(host);
+    }
     // `vector_reduce` (kernels.rs:867): the whole buffer folded; reading the
     // value waits for the device.
     static T reduce(const Storage<T>& values, Reduce op) {

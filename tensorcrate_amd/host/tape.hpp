@@ -404,11 +404,14 @@ class MatrixVar : public Var<Matrix<T>> {
                                         [parent](const M& adjoint) { parent->accumulate(K<T>::transpose(adjoint)); });
     }
 
-    // `MatrixVar::sum` (tape/mod.rs:1286-1297): recorded unread; the adjoint
-    // is a device fill of the scalar adjoint.
+    // `MatrixVar::sum` (tape/mod.rs:1286-1297): recorded unread -- the
+    // reduction and the read of its result are queued now, and only reading
+    // the value waits, for that read; the adjoint is a device fill of the
+    // scalar adjoint.
     ScalarVar sum() const {
         auto parent = this->node_;
-        Lazy<float> total = Lazy<float>::deferred([parent] { return K<T>::reduce(parent->get().storage(), Reduce::Sum); });
+        const uint64_t ticket = K<T>::reduce_async(parent->get().storage(), Reduce::Sum);
+        Lazy<float> total = Lazy<float>::deferred([ticket] { return static_cast<float>(K<T>::read(ticket)); });
         return ScalarVar(this->template record_lazy<float>(std::move(total), [parent](const float& adjoint) {
             const M& value = parent->get();
             parent->accumulate(M::filled(value.rows(), value.cols(), adjoint));

@@ -146,6 +146,8 @@ SIGNATURES = {
     "tc_moments": [u32, vp, u64, vp],
     "tc_prefix_sum": [u32, vp, vp, u64],
     "tc_upload_staged": [vp, vp, ctypes.c_size_t],
+    "tc_read_async": [vp, ctypes.c_size_t, ctypes.POINTER(u64)],
+    "tc_read_wait": [u64, vp, ctypes.c_size_t],
     "tc_download_staged": [vp, vp, ctypes.c_size_t],
     "tc_tcr1_read_header": [ctypes.c_char_p, u64, ctypes.c_char_p, u32, u32, vp],
     "tc_tcr1_load": [ctypes.c_char_p, vp, vp],

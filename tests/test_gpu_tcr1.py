@@ -101,3 +101,29 @@ def test_staged_transfers_round_trip(nbytes):
     lib.call("tc_download_staged", back.ctypes.data, dev.ptr, nbytes)
     assert np.array_equal(back, host)
     assert np.array_equal(dev.download(np.uint8, nbytes), host)
+
+
+def test_queued_small_reads_wait_for_themselves_only():
+    # The tape's unread loss (tape/mod.rs:253-295): a read queued behind the
+    # work that produces it, waited for when the value is wanted, in any order.
+    values = np.arange(10, dtype=np.float32) * 1.5 - 3
+    dev = lib.Buffer.of(values)
+    tickets = []
+    for k in range(10):
+        t = ctypes.c_uint64()
+        lib.call("tc_read_async", dev.ptr + 4 * k, 4, ctypes.byref(t))
+        tickets.append(t.value)
+    for k in reversed(range(10)):
+        got = ctypes.c_float()
+        lib.call("tc_read_wait", tickets[k], ctypes.byref(got), 4)
+        assert got.value == values[k]
+    # A ticket whose slot 1024 later reads reused, and one never issued.
+    for _ in range(1024):
+        t = ctypes.c_uint64()
+        lib.call("tc_read_async", dev.ptr, 4, ctypes.byref(t))
+    with pytest.raises(lib.HipError, match="reused by 1024 later reads"):
+        lib.call("tc_read_wait", tickets[0], ctypes.byref(ctypes.c_float()), 4)
+    with pytest.raises(lib.HipError, match="never issued"):
+        lib.call("tc_read_wait", t.value + 5, ctypes.byref(ctypes.c_float()), 4)
+    with pytest.raises(lib.HipError, match="over 64"):
+        lib.call("tc_read_async", dev.ptr, 65, ctypes.byref(t))
