@@ -82,6 +82,14 @@ std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtyp
                            const tc_place* places, std::vector<float>* constants);
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out);
 
+// `fused_sum` over rows as one compiled kernel (fused.hip): the checked
+// program's one output summed per row into `out`, rounded once to `dtype`.
+// Sets `*done` false, launching nothing, until the program has been seen
+// before (or when it does not fit the compiled form).
+int fused_row_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                   uint32_t place_count, const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
+                   uint64_t rows, uint64_t cols, void* out, bool* done);
+
 std::string shape_text(const uint64_t* values, uint32_t rank);
 
 // ---- element types (device.hpp) ---------------------------------------------

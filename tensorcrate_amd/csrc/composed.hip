@@ -14,12 +14,16 @@
 //    type and read through a place the reduction walk can take is read in
 //    place; any other is first converted into a scratch matrix by a two-
 //    instruction fused program.
-//  - fused_sum: the program's one output, written to scratch, summed along
-//    the axis (`axis_sum`, fused/mod.rs:4045-4051, defines the sums as
-//    products with ones; this sums with the reduction kernels, f32
-//    accumulation rounded once).
-//  - matmul_epilogue: the product into scratch, then the program with the
-//    product as input 0 (`host_matmul`, fused/mod.rs:4754-4766).
+//  - fused_sum: the program's one output summed along the axis
+//    (`axis_sum`, fused/mod.rs:4045-4051, defines the sums as products with
+//    ones; here f32 accumulation rounded once).  Row sums of a program seen
+//    before run as one compiled kernel (fused.hip) and never store the
+//    output; otherwise the output goes to scratch and the reduction kernels
+//    sum it.
+//  - matmul_epilogue: the program in the product kernel's epilogue
+//    (gemm.hip); only a product that takes neither matrix-core kernel is
+//    formed into scratch first, then the program runs with it as input 0
+//    (`host_matmul`, fused/mod.rs:4754-4766).
 // Scratch blocks come from the thread's stream-ordered cache and are
 // returned to it once the work that reads them is queued.
 
@@ -173,6 +177,12 @@ int tc_fused_sum(uint32_t dtype, const tc_encoded* code, uint32_t count, const t
     if (depth == 0) {  // sums of nothing
         const uint32_t zero = 0;
         return tc_fill(out, results, static_cast<uint32_t>(dtype_size(dtype)), &zero);
+    }
+    if (axis == TC_AXIS_ROWS) {
+        bool done = false;
+        int status = fused_row_sums(dtype, code, count, places, place_count, inputs, input_lens, input_count, rows,
+                                    cols, out, &done);
+        if (status != TC_OK || done) return status;
     }
     const uint64_t n = rows * cols;
     Scratch data(n * dtype_size(dtype));

@@ -395,7 +395,7 @@ bool cached_kernels(const std::string& source, const std::vector<std::string>& k
 // each constant from `constants[]` (appended to `*constants`).  With
 // `product_input`, input 0 is the product rather than a load.
 std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
-                       const tc_place* places, std::vector<float>* constants) {
+                       const tc_place* places, std::vector<float>* constants, bool sum_store = false) {
     static const char* const kBinary[] = {"+", "-", "*", "/"};
     const std::string round = "tc_round<" + std::to_string(dtype) + ">";
     std::ostringstream src;
@@ -405,8 +405,12 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
     for (uint32_t pc = 0; pc < count; pc++) {
         const tc_encoded& in = code[pc];
         if (in.kind == 5) {
-            src << each << "if (live[e]) tc::store_as(out[" << int(in.aux) << "], " << int(in.b)
-                << "u, (uint64_t)row[e] * N + col[e], " << at(in.a) << ");\n";
+            if (sum_store) {  // the one output, already in its type, summed in f32 in element order
+                src << each << "sum += live[e] ? " << at(in.a) << " : 0.0f;\n";
+            } else {
+                src << each << "if (live[e]) tc::store_as(out[" << int(in.aux) << "], " << int(in.b)
+                    << "u, (uint64_t)row[e] * N + col[e], " << at(in.a) << ");\n";
+            }
             continue;
         }
         const std::string v = "v" + std::to_string(pc);
@@ -534,6 +538,62 @@ bool run_general_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype
     return true;
 }
 
+// A program's one output summed along its rows (`fused_sum` over
+// `Axis::Rows`, kernels.rs:1120-1135) in one kernel, from the program's second
+// appearance: a wave a row, 16 elements a lane 64 apart, each lane summing in
+// element order and the wave in a fixed shuffle tree, so the output itself is
+// never stored.
+bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                           uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, void* out,
+                           hipStream_t s, int* status) {
+    if (place_count > static_cast<uint32_t>(kInlinePlaces) || rows * cols > (uint64_t{1} << 31)) return false;
+    std::vector<float> constants;
+    const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, &constants, true);
+    if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
+    const std::string E = std::to_string(kGeneralElems);
+    const std::string source =
+        "#include \"device.hpp\"\n"
+        "struct Program {\n" + std::string(compiled_members()) +
+        "  __device__ __forceinline__ void group(const bool (&live)[" + E + "], const uint32_t (&row)[" + E + "],\n"
+        "      const uint32_t (&col)[" + E + "], uint32_t N, float& sum) const {\n" + body + "  }\n};\n"
+        "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_row_sums(Program p, uint32_t rows,\n"
+        "    uint32_t cols, void* sums) {\n"
+        "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
+        "  for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {\n"
+        "    float sum = 0.0f;\n"
+        "    for (uint32_t c0 = 0; c0 < cols; c0 += 64u * " + E + ") {\n"
+        "      uint32_t row[" + E + "], col[" + E + "];\n"
+        "      bool live[" + E + "];\n"
+        "      for (int v = 0; v < " + E + "; v++) {\n"
+        "        col[v] = c0 + v * 64u + lane;\n"
+        "        row[v] = r;\n"
+        "        live[v] = col[v] < cols;\n"
+        "      }\n"
+        "      p.group(live, row, col, cols, sum);\n"
+        "    }\n"
+        "    for (int offset = 32; offset > 0; offset >>= 1) sum += __shfl_xor(sum, offset);\n"
+        "    if (lane == 0) tc::store_as(sums, " + std::to_string(dtype) + "u, r, sum);\n"
+        "  }\n"
+        "}\n";
+    hipFunction_t function = nullptr;
+    if (!cached_kernels(source, {"tc_fused_row_sums"}, &function)) return false;
+    CompiledArgsOf args{};
+    for (int k = 0; k < TC_FUSED_MAX_INPUTS; k++) args.in[k] = buffers.inputs[k];
+    int place_status = to_device_places(places, place_count, args.places);
+    if (place_status != TC_OK) {
+        *status = place_status;
+        return true;
+    }
+    for (size_t c = 0; c < constants.size(); c++) args.constants[c] = constants[c];
+    uint32_t rows32 = static_cast<uint32_t>(rows), cols32 = static_cast<uint32_t>(cols);
+    void* params[] = {&args, &rows32, &cols32, &out};
+    const uint64_t wanted = (rows + 3) / 4;
+    const uint32_t blocks = static_cast<uint32_t>(wanted < 0xffffffu ? wanted : 0xffffffu);
+    const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);
+    *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused sum: ") + hipGetErrorString(error));
+    return true;
+}
+
 // Host-side validation of what the kernel would otherwise trust.
 int check_program(const tc_encoded* code, uint32_t count, uint32_t place_count, uint32_t input_count,
                   uint32_t output_count) {
@@ -575,6 +635,20 @@ std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtyp
 
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out) {
     return cached_kernels(source, kernels, out);
+}
+
+int fused_row_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                   uint32_t place_count, const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
+                   uint64_t rows, uint64_t cols, void* out, bool* done) {
+    *done = false;
+    const uint64_t lens[1] = {rows * cols};
+    int status = check_fused(dtype, code, count, places, place_count, input_lens, input_count, lens, 1, rows, cols);
+    if (status != TC_OK) return status;
+    TC_STREAM(s);
+    Buffers buffers{};
+    for (uint32_t k = 0; k < input_count; k++) buffers.inputs[k] = inputs[k];
+    *done = run_compiled_row_sums(code, count, dtype, places, place_count, buffers, rows, cols, out, s, &status);
+    return status;
 }
 
 }  // namespace tc

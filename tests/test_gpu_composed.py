@@ -16,7 +16,7 @@ import pytest
 
 from oracle import binding as oracle
 from tensorcrate_amd import lib
-from tests.common import Lcg, identity_place, row_broadcast, to_kind, widen
+from tests.common import EXP, Code, Lcg, identity_place, row_broadcast, to_kind, widen
 from tests.test_oracle_composed import PLACES, exp_program, layer_norm, oracle_at, relu_layer, statistic_operands
 
 pytestmark = pytest.mark.gpu
@@ -153,3 +153,36 @@ def test_fused_with_statistics_against_the_oracle(rows, cols):
     tol = 64 * np.sqrt(cols) * 2.0 ** -24 * 4.0
     assert np.max(np.abs(got - want)) <= tol
     assert np.max(np.abs(dacc.download(np.float32, rows * cols) - acc)) <= 2 * tol
+
+
+@pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
+def test_row_sums_of_a_repeated_program_run_as_one_compiled_kernel(dtype):
+    # From the program's second appearance its row sums are one kernel that
+    # never stores the output; every run agrees with the oracle to the
+    # summation bound.  exp(x) * 0.5 + 0.25 is this test's own program.
+    import ctypes
+
+    code = Code()
+    x = code.load(0, 0, dtype)
+    y = code.binary(lib.ADD, code.binary(lib.MUL, code.unary(EXP, x), code.const(0.5)), code.const(0.25))
+    code.store(y, dtype, 0)
+    rows, cols = 300, 5000
+    rng = np.random.default_rng(dtype)
+    values = to_kind(rng.uniform(-1, 1, rows * cols).astype(np.float32), dtype)
+    want = widen(dtype, oracle.fused_sum(dtype, code.code, [identity_place(rows, cols)], [values], rows, cols, 0))
+    exact = (np.exp(widen(dtype, values).astype(np.float64)) * 0.5 + 0.25).reshape(rows, cols).sum(1)
+    unit = 2.0 ** -24 if dtype == lib.F32 else 2.0 ** -8
+    counts = []
+    for _ in range(3):
+        got = widen(dtype, device_fused_sum(dtype, code.code, [identity_place(rows, cols)], [values], rows, cols, 0))
+        # Per element: three operations rounded to the type (and exp's own
+        # error); per sum: a lane's run of cols / 64 additions and a 64-lane
+        # tree in f32, then the result rounded to the type.  The oracle sums
+        # left to right, within cols 2^-24 of the exact sum.
+        bound = (4 * unit + 2 * (cols / 64 + 8) * 2.0 ** -24) * exact + unit * exact
+        assert np.all(np.abs(got - exact) <= bound)
+        assert np.all(np.abs(got - want) <= bound + (4 * unit + cols * 2.0 ** -24) * exact)
+        count = ctypes.c_uint64()
+        lib.call("tc_fused_compiled", ctypes.byref(count))
+        counts.append(count.value)
+    assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
