@@ -288,7 +288,17 @@ template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
                     hipStream_t s, const EPI& epi = EPI{}) {
     const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
-    if (large >= static_cast<uint32_t>(compute_units())) {
+    const uint32_t cus = static_cast<uint32_t>(compute_units());
+    if constexpr (!EPI::kProgram) {
+        // Several tiles a CU and whole pairs of steps: the persistent form,
+        // one block a CU, each tile's first loads under the last one's steps.
+        if (large > cus && ((k + 63) / 64) % 2 == 0) {
+            direct16_persistent_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64><<<cus, 2 * 4 * 64, 0, s>>>(
+                a, b, c, m, n, k, accumulate);
+            return;
+        }
+    }
+    if (large >= cus) {
         direct16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64, 2, EPI><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k,
                                                                                                  accumulate, epi);
     } else {

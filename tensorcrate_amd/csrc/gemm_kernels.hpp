@@ -471,6 +471,18 @@ struct DirectStager {
             k_of[i] = KC ? chunk * 8 : 0;
         }
     }
+    // The same lanes' chunks of another block tile: only the resource
+    // (its base and range) depends on the tile.
+    __device__ __forceinline__ void retarget(const S* p, uint32_t first, uint32_t rows, uint32_t ld,
+                                             uint32_t depth) {
+        if (KC) {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + static_cast<uint64_t>(first) * ld), 0,
+                                                     (rows - first) * ld * sizeof(S), kBufferFlags);
+        } else {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + first), 0, (depth * ld - first) * sizeof(S),
+                                                     kBufferFlags);
+        }
+    }
     // Stage the step at `k0` into `tile` (the LDS stage).  Past K a
     // K-contiguous chunk is the next row's, so it is pointed past the
     // resource (operands are under 2^31 bytes) and loads zeros.
@@ -671,5 +683,134 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restr
         }
     }
 }
+// The tiled kernel made persistent, for products whose K is short: a block
+// owns every gridDim.x-th block tile in turn, and the last step of one tile
+// stages the first step of the next, so neither the next tile's first HBM
+// loads nor this tile's stores sit between two tiles' matrix-core steps.
+// The step loop, stages and weave are the tiled kernel's; a tile's steps
+// must come in whole pairs (an even step count) so that every tile starts on
+// stage 0.  Plain stores only: a program epilogue needs the LDS the next
+// tile's first step already occupies.
+template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN, int BK>
+__global__ void __launch_bounds__(WM * WN * 64) direct16_persistent_kernel(const S* __restrict__ A,
+                                                                           const S* __restrict__ B,
+                                                                           O* __restrict__ C, uint32_t M, uint32_t N,
+                                                                           uint32_t K, bool accumulate) {
+    constexpr int NS = 2;
+    constexpr int kWaves = WM * WN;
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+    constexpr int kA = BM * BK, kB = BN * BK;
+
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    const uint32_t tiles = tiles_m * tiles_n;
+    uint32_t tile = blockIdx.x;
+    if (tile >= tiles) return;
+    uint32_t tm, tn;
+    tile_of(tile, tiles_m, tiles_n, tm, tn);
+    uint32_t m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int wm = wave / WN, wn = wave % WN;
+
+    using StagerA = DirectStager<S, BM, A_KC, kWaves, BK>;
+    using StagerB = DirectStager<S, BN, B_KC, kWaves, BK>;
+    StagerA sa;
+    StagerB sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
+    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
+
+    f32x16 acc[TM][TN];
+    uint4 fa[2][TM], fb[2][TN];
+    auto read_fragments = [&](int slot, const S* la, const S* lb, int kk) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            fa[slot][i] = swizzled_fragment<S, BM, A_KC, BK>(la, wm * (BM / WM) + i * 32, kk, lane);
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            fb[slot][j] = swizzled_fragment<S, BN, B_KC, BK>(lb, wn * (BN / WN) + j * 32, kk, lane);
+    };
+
+    constexpr int kSlices = BK / 16;
+    constexpr int kSteps = TM * TN;
+    constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
+    constexpr int kLoads = StagerA::kPer + StagerB::kPer;
+    const uint32_t steps = (K + BK - 1) / BK;
+    // Step s of this tile; s == steps is the next tile's first step, or,
+    // after the last tile, a harmless reload of this tile's last.
+    auto stage_of = [&](auto t, uint32_t s) {
+        uint32_t k0;
+        if (s < steps) {
+            k0 = s * BK;
+        } else if (tile + gridDim.x < tiles) {
+            uint32_t next_m, next_n;
+            tile_of(tile + gridDim.x, tiles_m, tiles_n, next_m, next_n);
+            sa.retarget(A, next_m * BM, M, A_KC ? K : M, K);
+            sb.retarget(B, next_n * BN, N, B_KC ? K : N, K);
+            k0 = 0;
+        } else {
+            k0 = (steps - 1) * BK;
+        }
+        sa.fetch(stage_tile<S, kA, 2 * decltype(t)::value>(), k0, K, k0 + BK <= K);
+        sb.fetch(stage_tile<S, kB, 2 * decltype(t)::value + 1>(), k0, K, k0 + BK <= K);
+    };
+    auto step = [&](auto t, uint32_t s) {
+        constexpr int T = decltype(t)::value;
+        const S* la = stage_tile<S, kA, 2 * T>();
+        const S* lb = stage_tile<S, kB, 2 * T + 1>();
+        stage_of(std::integral_constant<int, (T + NS - 1) % NS>{}, s + NS - 1);
+#pragma unroll
+        for (int q = 0; q + 1 < kSlices; q++) {
+            read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[q & 1][i], fb[q & 1][j], acc[i][j]);
+        }
+        weave<kSteps, kLoads, kReads, kSlices - 1>();
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // step s + 1 is in LDS
+        __syncthreads();
+        constexpr int last = (kSlices - 1) & 1;
+        constexpr int U = (T + 1) % NS;
+        read_fragments(last ^ 1, stage_tile<S, kA, 2 * U>(), stage_tile<S, kB, 2 * U + 1>(), 0);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[last][i], fb[last][j], acc[i][j]);
+        weave<kSteps, 0, kReads, 2>();
+    };
+    stage_of(std::integral_constant<int, 0>{}, 0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // the first tile's first step is in LDS
+    __syncthreads();
+    read_fragments(0, stage_tile<S, kA, 0>(), stage_tile<S, kB, 1>(), 0);
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
+        for (uint32_t s = 0; s < steps; s += NS) {
+            step(std::integral_constant<int, 0>{}, s);
+            step(std::integral_constant<int, 1>{}, s + 1);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint32_t col = n0 + wn * (BN / WN) + j * 32 + lane % 32;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                    if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
+                }
+            }
+        }
+        tile += gridDim.x;
+        if (tile >= tiles) break;
+        tile_of(tile, tiles_m, tiles_n, tm, tn);
+        m0 = tm * BM;
+        n0 = tn * BN;
+    }
+}
+
 
 }  // namespace tc
