@@ -55,6 +55,66 @@ int tch_mlp_gradients(tch_mlp* mlp, uint32_t layer, float* weights, float* bias)
 
 void tch_mlp_destroy(tch_mlp* mlp);
 
+/* ---- a tape of tensor variables (src/tensors/tape/tensor.rs) ------------
+ *
+ * Each call records one `TensorVar` operation and answers its handle; the
+ * handles number the variables in recording order.  A handle names a tensor,
+ * or a scalar for `TCH_SUM` / `TCH_MEAN` and `tch_tape_add_scalars`.  Values
+ * are f32, row-major; shapes have at most TC_MAX_RANK axes. */
+
+typedef struct tch_tape tch_tape;
+
+/* Binary operations, broadcasting (tape/tensor.rs:126-250);  TCH_MATMUL is
+ * the last axis of `a` times the k x n tensor `b`, through `to_matrix`,
+ * `MatrixVar::matmul` and `to_tensor` (tape/tensor.rs:703-761). */
+typedef enum tch_binary {
+    TCH_ADD = 0, TCH_SUB = 1, TCH_MUL = 2, TCH_DIV = 3,
+    TCH_MAXIMUM = 4, TCH_MINIMUM = 5, TCH_POWER = 6, TCH_MATMUL = 7
+} tch_binary;
+
+/* Unary operations (tape/tensor.rs:187-333); `first` and `second` are the
+ * scalar, factor, offset or bounds; TCH_ANALYTIC + k is `analytic` of the
+ * k-th `Analytic` (kernels.rs:293-308). */
+typedef enum tch_unary {
+    TCH_CLAMP_MIN = 0, TCH_CLAMP_MAX = 1, TCH_CLAMP = 2, TCH_RELU = 3, TCH_ABS = 4, TCH_NEG = 5,
+    TCH_SCALE = 6, TCH_SHIFT = 7, TCH_POWER_SCALAR = 8, TCH_POWER_SCALAR_LEFT = 9, TCH_CONTIGUOUS = 10,
+    TCH_ANALYTIC = 32
+} tch_unary;
+
+/* Layout operations (tape/tensor.rs:335-420, :555-570): `values` is the new
+ * shape, the permutation, the two axes to swap (negative from the end), or
+ * the shape to broadcast to. */
+typedef enum tch_layout { TCH_RESHAPE = 0, TCH_PERMUTE = 1, TCH_TRANSPOSE = 2, TCH_BROADCAST_TO = 3 } tch_layout;
+
+/* Reductions (tape/tensor.rs:572-701): over `axes` (negative from the end),
+ * or, for TCH_SUM and TCH_MEAN, over everything to a scalar. */
+typedef enum tch_reduction {
+    TCH_SUM_AXES = 0, TCH_MEAN_AXES = 1, TCH_VAR_AXES = 2, TCH_VAR_AXES_SAMPLE = 3,
+    TCH_MAX_AXES = 4, TCH_MIN_AXES = 5, TCH_SUM = 6, TCH_MEAN = 7
+} tch_reduction;
+
+int tch_tape_create(tch_tape** out);
+void tch_tape_destroy(tch_tape* tape);
+/* A leaf: `values` holds the product of `shape` floats, copied to the device. */
+int tch_tape_tensor(tch_tape* tape, uint32_t rank, const uint64_t* shape, const float* values, uint32_t* out);
+int tch_tape_binary(tch_tape* tape, uint32_t op, uint32_t a, uint32_t b, uint32_t* out);
+int tch_tape_unary(tch_tape* tape, uint32_t op, uint32_t a, float first, float second, uint32_t* out);
+int tch_tape_layout(tch_tape* tape, uint32_t op, uint32_t a, uint32_t count, const int64_t* values, uint32_t* out);
+int tch_tape_reduce(tch_tape* tape, uint32_t op, uint32_t a, uint32_t count, const int64_t* axes, int keep_dims,
+                    uint32_t* out);
+/* The sum of two scalars (`ScalarVar::add`). */
+int tch_tape_add_scalars(tch_tape* tape, uint32_t a, uint32_t b, uint32_t* out);
+/* `backward_with` (tape/mod.rs:507-529) from `output`, seeded with `seed`
+ * (one float per element of a tensor output; for a scalar, NULL seeds 1). */
+int tch_tape_backward(tch_tape* tape, uint32_t output, const float* seed);
+/* A variable's shape (rank 0 for a scalar). */
+int tch_tape_shape(tch_tape* tape, uint32_t handle, uint32_t* rank, uint64_t* shape);
+/* A variable's value, or (`gradient` non-zero) its accumulated adjoint, a
+ * zero where the last backward pass did not reach it; waits for the device. */
+int tch_tape_read(tch_tape* tape, uint32_t handle, int gradient, float* out);
+/* `Tape::zero_grad` (tape/mod.rs:416-420). */
+int tch_tape_zero_grad(tch_tape* tape);
+
 #ifdef __cplusplus
 }
 #endif

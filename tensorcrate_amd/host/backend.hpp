@@ -16,6 +16,7 @@
 
 #include <stdint.h>
 
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -155,6 +156,71 @@ class Matrix {
 
    private:
     size_t rows_, cols_;
+    Storage<T> storage_;
+};
+
+// `Analytic` (kernels.rs:293-308), numbered as the kernels read it.
+enum class Analytic : uint32_t {
+    Sin = 0, Cos, Tan, Sec, Csc, Arcsin, Arccos, Arctan, Exp, Ln, Sinh, Cosh, Tanh, Sqrt
+};
+
+using Shape = std::vector<size_t>;
+
+inline size_t element_count(const Shape& shape) {
+    size_t n = 1;
+    for (size_t extent : shape) n *= extent;
+    return n;
+}
+
+inline std::string shape_text(const Shape& shape) {
+    std::string text = "[";
+    for (size_t k = 0; k < shape.size(); k++) text += (k ? ", " : "") + std::to_string(shape[k]);
+    return text + "]";
+}
+
+// `Tensor<T, Hip>` (tensors/tensor.rs:50): a shape over one row-major
+// storage.  The reference's views (offset + strides) are not kept: every
+// layout operation here makes its contiguous copy at once, one strided-copy
+// kernel, which is what a view's `contiguous()` costs when a kernel reads it.
+template <typename T>
+class Tensor {
+   public:
+    Tensor(Shape shape, Storage<T> s) : shape_(std::move(shape)), storage_(std::move(s)) {
+        if (shape_.size() > TC_MAX_RANK) {
+            throw std::invalid_argument("tensor: shape " + shape_text(shape_) + " has more than " +
+                                        std::to_string(TC_MAX_RANK) + " axes");
+        }
+        if (storage_.len() != element_count(shape_)) {
+            throw std::invalid_argument("from_storage: " + std::to_string(storage_.len()) +
+                                        " elements for shape " + shape_text(shape_));
+        }
+    }
+    static Tensor filled(Shape shape, T value) {
+        const size_t n = element_count(shape);
+        return Tensor(std::move(shape), n ? Storage<T>::filled(n, value) : Storage<T>(0));
+    }
+    static Tensor from_host(Shape shape, const std::vector<T>& values) {
+        return Tensor(std::move(shape), Storage<T>::store(values.data(), values.size()));
+    }
+    Tensor duplicate() const { return Tensor(shape_, len() ? storage_.duplicate() : Storage<T>(0)); }
+    std::vector<T> to_host() const { return len() ? storage_.to_host() : std::vector<T>(); }
+    // `Tensor::reshape` (tensor.rs): the same storage under `shape`.
+    Tensor reshape(Shape shape) && {
+        if (element_count(shape) != len()) {
+            throw std::invalid_argument("reshape: shape " + shape_text(shape_) + " holds " + std::to_string(len()) +
+                                        " elements, which " + shape_text(shape) + " cannot");
+        }
+        return Tensor(std::move(shape), std::move(storage_));
+    }
+    const Shape& shape() const { return shape_; }
+    size_t rank() const { return shape_.size(); }
+    size_t len() const { return storage_.len(); }
+    Storage<T>& storage() { return storage_; }
+    const Storage<T>& storage() const { return storage_; }
+    Storage<T> into_storage() && { return std::move(storage_); }
+
+   private:
+    Shape shape_;
     Storage<T> storage_;
 };
 
@@ -316,6 +382,254 @@ struct Kernels {
         tc_free(result);
         check(status);
         return static_cast<T>(host);
+    }
+
+    // ---- tensors: the trait's strided and axis operations -----------------
+
+    // `Pairwise::name` (kernels.rs:419-426) for a shape error.
+    static const char* pairwise_name(uint32_t kind, uint32_t op) {
+        if (kind == TC_PAIR_POWER) return "power";
+        if (kind == TC_PAIR_COMPARE) return op == TC_MIN ? "min" : op == TC_MAX ? "max" : "compare";
+        static const char* const names[] = {"add", "subtract", "multiply", "divide", "remainder"};
+        return op < 5 ? names[op] : "elementwise";
+    }
+
+    // `broadcast_shape` (layout.rs:316-340): numpy's rule from the last axis;
+    // false when the shapes do not broadcast.
+    static bool broadcast_shape(const Shape& left, const Shape& right, Shape& out) {
+        const size_t rank = std::max(left.size(), right.size());
+        out.assign(rank, 1);
+        for (size_t axis = 0; axis < rank; axis++) {
+            const size_t from_end = rank - axis;
+            const size_t l = left.size() >= from_end ? left[left.size() - from_end] : 1;
+            const size_t r = right.size() >= from_end ? right[right.size() - from_end] : 1;
+            if (l == r || r == 1) {
+                out[axis] = l;
+            } else if (l == 1) {
+                out[axis] = r;
+            } else {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    // The layout that reads a row-major `from` as `to` (`broadcast_strides`,
+    // layout.rs:347-363): an axis of extent 1 stretched to more repeats its
+    // element with stride 0.
+    static tc_strided broadcast_layout(const Shape& from, const Shape& to) {
+        tc_strided at{};
+        if (to.size() > TC_MAX_RANK) {
+            throw std::invalid_argument("broadcast_to: shape " + shape_text(to) + " has more than " +
+                                        std::to_string(TC_MAX_RANK) + " axes");
+        }
+        const size_t added = to.size() - from.size();
+        size_t step = 1;
+        for (size_t axis = from.size(); axis-- > 0;) {
+            const size_t wanted = to[added + axis];
+            if (from[axis] == wanted) {
+                at.strides[added + axis] = step;
+            } else if (from[axis] != 1) {
+                throw std::invalid_argument("broadcast_to: shape " + shape_text(from) + " does not broadcast to " +
+                                            shape_text(to));
+            }
+            step *= from[axis];
+        }
+        return at;
+    }
+
+    // `TensorView::zip` (tensor_ops.rs:71-91): two tensors of one shape take
+    // the vector kernel, anything else one strided kernel over both operands
+    // broadcast to their common shape and read in place.
+    static Tensor<T> zip(const Tensor<T>& a, const Tensor<T>& b, uint32_t kind, uint32_t op) {
+        Shape shape;
+        if (!broadcast_shape(a.shape(), b.shape(), shape)) {
+            throw std::invalid_argument(std::string(pairwise_name(kind, op)) + ": tensor shapes differ, " +
+                                        shape_text(a.shape()) + " and " + shape_text(b.shape()) +
+                                        ", and do not broadcast");
+        }
+        Storage<T> out(element_count(shape));
+        if (out.len() == 0) return Tensor<T>(std::move(shape), std::move(out));
+        if (a.shape() == b.shape() && kind != TC_PAIR_POWER) {
+            if (kind == TC_PAIR_ARITHMETIC) {
+                check(tc_elementwise(dtype, op, a.storage().ptr(), b.storage().ptr(), out.ptr(), out.len()));
+            } else {
+                check(tc_compare(dtype, op, a.storage().ptr(), b.storage().ptr(), out.ptr(), out.len()));
+            }
+            return Tensor<T>(std::move(shape), std::move(out));
+        }
+        if (a.shape() == b.shape() && kind == TC_PAIR_POWER) {
+            check(tc_power(dtype, a.storage().ptr(), b.storage().ptr(), out.ptr(), out.len()));
+            return Tensor<T>(std::move(shape), std::move(out));
+        }
+        const tc_strided a_at = broadcast_layout(a.shape(), shape);
+        const tc_strided b_at = broadcast_layout(b.shape(), shape);
+        const std::vector<uint64_t> dims(shape.begin(), shape.end());
+        check(tc_strided_binary(dtype, kind, op, static_cast<uint32_t>(shape.size()), dims.data(),
+                                a.storage().ptr(), a.len(), &a_at, b.storage().ptr(), b.len(), &b_at, out.ptr()));
+        return Tensor<T>(std::move(shape), std::move(out));
+    }
+    static Tensor<T> elementwise(const Tensor<T>& a, const Tensor<T>& b, BinaryOp op) {
+        return zip(a, b, TC_PAIR_ARITHMETIC, static_cast<uint32_t>(op));
+    }
+    static Tensor<T> compare(const Tensor<T>& a, const Tensor<T>& b, Compare op) {
+        return zip(a, b, TC_PAIR_COMPARE, static_cast<uint32_t>(op));
+    }
+    static Tensor<T> power(const Tensor<T>& a, const Tensor<T>& b) { return zip(a, b, TC_PAIR_POWER, 0); }
+
+    // `with_scalar`, `compare_scalar`, `power_scalar`, `unary`,
+    // `unary_dual` over the flat storage (tensor_ops.rs:93-199).
+    static Tensor<T> with_scalar(const Tensor<T>& a, T scalar, BinaryOp op, bool scalar_left) {
+        Storage<T> out(a.len());
+        if (a.len()) {
+            check(tc_broadcast(dtype, static_cast<uint32_t>(op), a.storage().ptr(), scalar, scalar_left, out.ptr(),
+                               a.len()));
+        }
+        return Tensor<T>(a.shape(), std::move(out));
+    }
+    static Tensor<T> scale(const Tensor<T>& a, T factor) { return with_scalar(a, factor, BinaryOp::Mul, false); }
+    static Tensor<T> compare_scalar(const Tensor<T>& a, T scalar, Compare op, bool scalar_left) {
+        Storage<T> out(a.len());
+        if (a.len()) {
+            check(tc_compare_scalar(dtype, static_cast<uint32_t>(op), a.storage().ptr(), scalar, scalar_left,
+                                    out.ptr(), a.len()));
+        }
+        return Tensor<T>(a.shape(), std::move(out));
+    }
+    static Tensor<T> power_scalar(const Tensor<T>& a, T scalar, bool scalar_left) {
+        Storage<T> out(a.len());
+        if (a.len()) check(tc_power_scalar(dtype, a.storage().ptr(), scalar, scalar_left, out.ptr(), a.len()));
+        return Tensor<T>(a.shape(), std::move(out));
+    }
+    static Tensor<T> unary(const Tensor<T>& a, Analytic f) {
+        Storage<T> out(a.len());
+        if (a.len()) check(tc_unary(dtype, static_cast<uint32_t>(f), a.storage().ptr(), out.ptr(), a.len()));
+        return Tensor<T>(a.shape(), std::move(out));
+    }
+    // f(x) and f'(x)·tangent in one dispatch (kernels.rs:891).
+    static std::pair<Tensor<T>, Tensor<T>> unary_dual(const Tensor<T>& x, const Tensor<T>& tangent, Analytic f) {
+        if (x.shape() != tangent.shape()) {
+            throw std::invalid_argument("unary_dual: tensor shapes differ, " + shape_text(x.shape()) + " and " +
+                                        shape_text(tangent.shape()));
+        }
+        Storage<T> value(x.len()), product(x.len());
+        if (x.len()) {
+            check(tc_unary_dual(dtype, static_cast<uint32_t>(f), x.storage().ptr(), tangent.storage().ptr(),
+                                value.ptr(), product.ptr(), x.len()));
+        }
+        return {Tensor<T>(x.shape(), std::move(value)), Tensor<T>(x.shape(), std::move(product))};
+    }
+
+    // `TensorView::broadcast_to(..).contiguous()` (view.rs:370, :407): one
+    // strided copy with the stretched axes at stride 0.
+    static Tensor<T> broadcast_to(const Tensor<T>& a, const Shape& shape) {
+        if (shape.size() < a.rank()) {
+            throw std::invalid_argument("broadcast_to: shape " + shape_text(a.shape()) + " does not broadcast to " +
+                                        shape_text(shape));
+        }
+        const tc_strided from = broadcast_layout(a.shape(), shape);
+        return copy_through(a, shape, from);
+    }
+    // `permute(..).contiguous()` (view.rs:133-160): axis k of the result is
+    // axis `axes[k]` of `a`.
+    static Tensor<T> permute(const Tensor<T>& a, const std::vector<size_t>& axes) {
+        std::vector<bool> seen(a.rank(), false);
+        bool valid = axes.size() == a.rank();
+        for (size_t axis : axes) {
+            if (!valid || axis >= a.rank() || seen[axis]) {
+                valid = false;
+                break;
+            }
+            seen[axis] = true;
+        }
+        if (!valid) throw std::invalid_argument("permute: the axes are not a permutation of " + shape_text(a.shape()));
+        std::vector<size_t> strides(a.rank());
+        size_t step = 1;
+        for (size_t axis = a.rank(); axis-- > 0;) {
+            strides[axis] = step;
+            step *= a.shape()[axis];
+        }
+        Shape shape(a.rank());
+        tc_strided from{};
+        for (size_t k = 0; k < axes.size(); k++) {
+            shape[k] = a.shape()[axes[k]];
+            from.strides[k] = strides[axes[k]];
+        }
+        return copy_through(a, shape, from);
+    }
+
+    // The axes of a reduction resolved against `rank`, negative ones from the
+    // end, sorted; out-of-range and repeated axes are refused with the
+    // reference's wording (layout.rs:205-238).
+    static std::vector<size_t> resolve_axes(const std::vector<long>& axes, const Shape& shape, const char* operation) {
+        std::vector<size_t> resolved;
+        const long rank = static_cast<long>(shape.size());
+        for (long axis : axes) {
+            const long k = axis < 0 ? axis + rank : axis;
+            if (k < 0 || k >= rank) {
+                throw std::invalid_argument(std::string(operation) + ": axis " + std::to_string(axis) +
+                                            " is out of range for shape " + shape_text(shape) + " (" +
+                                            std::to_string(rank) + " axes)");
+            }
+            resolved.push_back(static_cast<size_t>(k));
+        }
+        std::sort(resolved.begin(), resolved.end());
+        if (std::adjacent_find(resolved.begin(), resolved.end()) != resolved.end()) {
+            std::string named = "[";
+            for (size_t k = 0; k < axes.size(); k++) named += (k ? ", " : "") + std::to_string(axes[k]);
+            throw std::invalid_argument(std::string(operation) + ": axes " + named + "] are not distinct axes of shape " +
+                                        shape_text(shape));
+        }
+        return resolved;
+    }
+
+    // `reduce_axes` (kernels.rs:1175-1179) over a row-major tensor: the kept
+    // axes index the result, the folded ones (`axes`, resolved and sorted)
+    // are summed, averaged, or folded to their extreme; `divisor` is the
+    // variance's.  A slice with no elements gives `empty` (0 for a sum, the
+    // fold's identity, NaN for a mean or a variance), as the reference's host
+    // kernels do, without a launch.
+    static Tensor<T> reduce_axes(const Tensor<T>& a, const std::vector<size_t>& axes, bool keep_dims, uint32_t kind,
+                                 Reduce op, size_t divisor, bool divisor_defined, T empty) {
+        std::vector<size_t> strides(a.rank());
+        size_t step = 1;
+        for (size_t axis = a.rank(); axis-- > 0;) {
+            strides[axis] = step;
+            step *= a.shape()[axis];
+        }
+        tc_split split{};
+        Shape shape;
+        size_t depth = 1;
+        for (size_t axis = 0; axis < a.rank(); axis++) {
+            const bool folded = std::find(axes.begin(), axes.end(), axis) != axes.end();
+            if (folded) {
+                split.folded[split.folded_rank] = a.shape()[axis];
+                split.folded_strides[split.folded_rank++] = strides[axis];
+                depth *= a.shape()[axis];
+                if (keep_dims) shape.push_back(1);
+            } else {
+                split.kept[split.kept_rank] = a.shape()[axis];
+                split.kept_strides[split.kept_rank++] = strides[axis];
+                shape.push_back(a.shape()[axis]);
+            }
+        }
+        const size_t results = element_count(shape);
+        if (!divisor_defined || depth == 0 || results == 0) return Tensor<T>::filled(std::move(shape), empty);
+        Storage<T> out(results);
+        check(tc_reduce_axes(dtype, a.storage().ptr(), a.len(), &split, kind, static_cast<uint32_t>(op), divisor,
+                             out.ptr()));
+        return Tensor<T>(std::move(shape), std::move(out));
+    }
+
+   private:
+    static Tensor<T> copy_through(const Tensor<T>& a, const Shape& shape, const tc_strided& from) {
+        Storage<T> out(element_count(shape));
+        if (out.len()) {
+            const std::vector<uint64_t> dims(shape.begin(), shape.end());
+            check(tc_strided_copy(sizeof(T), a.storage().ptr(), a.len(), static_cast<uint32_t>(shape.size()),
+                                  dims.data(), &from, out.ptr()));
+        }
+        return Tensor<T>(shape, std::move(out));
     }
 };
 

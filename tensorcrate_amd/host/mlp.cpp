@@ -14,7 +14,7 @@
 // `residual.frobenius_dot(residual).scale(1 / (outputs · batch))`.
 //
 // The C entry points (include/tchip_host.h) drive this from Python and
-// return a status; the message of a failure is `tch_last_error()`.
+// return a status; the message of a failure is `tch_last_error()` (entry.hpp).
 
 #include "tchip_host.h"
 
@@ -23,33 +23,12 @@
 #include <vector>
 
 #include "backend.hpp"
+#include "entry.hpp"
 #include "optim.hpp"
 #include "tape.hpp"
 
 using namespace tensorcrate::hip;
 
-namespace {
-
-thread_local std::string last_error;
-
-template <typename F>
-int guarded(F&& body) {
-    try {
-        body();
-        return TC_OK;
-    } catch (const Error& e) {
-        last_error = e.what();
-        return e.status;
-    } catch (const std::invalid_argument& e) {
-        last_error = e.what();
-        return TC_INVALID;
-    } catch (const std::exception& e) {
-        last_error = e.what();
-        return TC_DEVICE;
-    }
-}
-
-}  // namespace
 
 struct tch_mlp {
     std::vector<size_t> widths;
@@ -117,7 +96,7 @@ struct tch_mlp {
 
 extern "C" {
 
-const char* tch_last_error(void) { return last_error.c_str(); }
+const char* tch_last_error(void) { return host_error.c_str(); }
 
 int tch_mlp_create(uint32_t layers, const uint64_t* widths, uint64_t batch, const float* const* weights,
                    const float* const* biases, const float* inputs, const float* targets, float rate,

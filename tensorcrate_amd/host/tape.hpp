@@ -1,6 +1,7 @@
 // Reverse-mode differentiation over Hip storage: tensorcrate's `Tape`, its
-// nodes and the scalar, vector and matrix variables with their backward
-// rules (src/tensors/tape/mod.rs), restated in C++ over backend.hpp.
+// nodes and the scalar, vector, matrix and tensor variables with their
+// backward rules (src/tensors/tape/mod.rs, tape/tensor.rs), restated in C++
+// over backend.hpp.
 //
 // The structure is the reference's: every operation computes its value now,
 // through `Kernels`, and records a rule that pushes the node's adjoint into
@@ -16,7 +17,9 @@
 // host uploads.
 #pragma once
 
+#include <cmath>
 #include <functional>
+#include <limits>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -45,6 +48,15 @@ struct TapeValue<Vector<T>> {
     static Vector<T> duplicate(const Vector<T>& v) { return v.duplicate(); }
     static Vector<T> add(const Vector<T>& a, const Vector<T>& b) {
         return Kernels<T>::vector_elementwise(a, b, BinaryOp::Add);
+    }
+};
+
+template <typename T>
+struct TapeValue<Tensor<T>> {
+    static Tensor<T> zeros_like(const Tensor<T>& t) { return Tensor<T>::filled(t.shape(), T(0)); }
+    static Tensor<T> duplicate(const Tensor<T>& t) { return t.duplicate(); }
+    static Tensor<T> add(const Tensor<T>& a, const Tensor<T>& b) {
+        return Kernels<T>::elementwise(a, b, BinaryOp::Add);
     }
 };
 
@@ -178,6 +190,10 @@ class Tape {
     Var<Matrix<T>> matrix(Matrix<T> value) {
         return push<Matrix<T>>(Lazy<Matrix<T>>::ready(std::move(value)), nullptr);
     }
+    template <typename T>
+    Var<Tensor<T>> tensor(Tensor<T> value) {
+        return push<Tensor<T>>(Lazy<Tensor<T>>::ready(std::move(value)), nullptr);
+    }
     size_t len() const { return nodes_.size(); }
     // `Tape::zero_grad` (tape/mod.rs:416-420).
     void zero_grad() {
@@ -236,6 +252,8 @@ Matrix<T> negated_matrix(const Matrix<T>& m) {
 
 template <typename T>
 class MatrixVar;
+template <typename T>
+class TensorVar;
 
 // `ScalarVar` (tape/mod.rs:600-760): the scalar operations a loss needs.
 class ScalarVar : public Var<float> {
@@ -250,6 +268,20 @@ class ScalarVar : public Var<float> {
                                 : Lazy<float>::deferred([parent, factor] { return parent->get() * factor; });
         return record_lazy<float>(std::move(value), [parent, factor](const float& adjoint) {
             parent->accumulate(adjoint * factor);
+        });
+    }
+    // `ScalarVar::add`, the `Add` arm of `ScalarVar::binary` (tape/mod.rs:611-640,
+    // :1385-1392): lazy when either operand is.
+    ScalarVar add(const ScalarVar& other) const {
+        assert_same_tape(other.tape());
+        auto left = node_;
+        auto right = other.node_;
+        Lazy<float> value = left->value.is_ready() && right->value.is_ready()
+                                ? Lazy<float>::ready(left->get() + right->get())
+                                : Lazy<float>::deferred([left, right] { return left->get() + right->get(); });
+        return record_lazy<float>(std::move(value), [left, right](const float& adjoint) {
+            left->accumulate(adjoint);
+            right->accumulate(adjoint);
         });
     }
     // `ScalarVar::backward` (tape/mod.rs:547-551): seed 1.
@@ -418,6 +450,10 @@ class MatrixVar : public Var<Matrix<T>> {
         }));
     }
 
+    // `MatrixVar::to_tensor` (tape/tensor.rs:744-761): the elements, row
+    // major, as a tensor of `shape`; the adjoint takes the matrix shape back.
+    TensorVar<T> to_tensor(const Shape& shape) const;
+
     // `MatrixVar::frobenius_dot` (tape/mod.rs:1299-1302).
     ScalarVar frobenius_dot(const MatrixVar& other) const { return binary(other, BinaryOp::Mul).sum(); }
 
@@ -451,6 +487,355 @@ class MatrixVar : public Var<Matrix<T>> {
 
     friend class VectorVar<T>;
 };
+
+// `sum_to_shape` (tape/tensor.rs:18-37): the adjoint of a broadcast, summed
+// down to the operand's `shape` in one reduction over the leading axes the
+// operand lacks and every axis where it has 1 and the gradient more.
+template <typename T>
+Tensor<T> sum_to_shape(const Tensor<T>& gradient, const Shape& shape) {
+    if (gradient.shape() == shape) return gradient.duplicate();
+    const size_t added = gradient.rank() - shape.size();
+    std::vector<size_t> axes;
+    for (size_t axis = 0; axis < gradient.rank(); axis++) {
+        if (axis < added || (shape[axis - added] == 1 && gradient.shape()[axis] != 1)) axes.push_back(axis);
+    }
+    Tensor<T> summed = axes.empty() ? gradient.duplicate()
+                                    : K<T>::reduce_axes(gradient, axes, true, TC_AXIS_FOLD, Reduce::Sum, 0, true, T(0));
+    return std::move(summed).reshape(shape);
+}
+
+// `Correction` (statistics/mod.rs:80-101): the variance's divisor n, or
+// n − 1 for a sample; too few elements leave it undefined.
+enum class Correction { Population, Sample };
+
+// `TensorVar` (tape/tensor.rs): an N-dimensional tensor on the tape.  Every
+// rule is written with the tensor kernels of backend.hpp, so a backward pass
+// stays on the device; an operand that was broadcast receives its adjoint
+// summed back to its own shape.
+template <typename T>
+class TensorVar : public Var<Tensor<T>> {
+    using Base = Var<Tensor<T>>;
+    using X = Tensor<T>;
+
+   public:
+    TensorVar(Var<Tensor<T>> v) : Base(std::move(v)) {}  // NOLINT
+
+    const Shape& shape() const { return this->value().shape(); }
+    size_t rank() const { return this->value().rank(); }
+    size_t len() const { return this->value().len(); }
+
+    TensorVar operator+(const TensorVar& rhs) const { return binary(rhs, BinaryOp::Add); }
+    TensorVar operator-(const TensorVar& rhs) const { return binary(rhs, BinaryOp::Sub); }
+    TensorVar operator*(const TensorVar& rhs) const { return binary(rhs, BinaryOp::Mul); }
+    TensorVar operator/(const TensorVar& rhs) const { return binary(rhs, BinaryOp::Div); }
+
+    // `TensorVar::binary` (tape/tensor.rs:126-160): c = a op b broadcast;
+    // ā, b̄ each summed to its operand's shape.  No tensor remainder is
+    // recorded, as in the reference.
+    TensorVar binary(const TensorVar& rhs, BinaryOp op) const {
+        this->assert_same_tape(rhs.tape());
+        if (op == BinaryOp::Rem) throw std::invalid_argument("no tensor remainder is recorded");
+        auto left = this->node_;
+        auto right = rhs.node_;
+        return this->template record<X>(K<T>::elementwise(this->value(), rhs.value(), op), [left, right, op](const X& adjoint) {
+            const X& a = left->get();
+            const X& b = right->get();
+            switch (op) {
+                case BinaryOp::Add:
+                    left->accumulate(sum_to_shape(adjoint, a.shape()));
+                    right->accumulate(sum_to_shape(adjoint, b.shape()));
+                    break;
+                case BinaryOp::Sub:
+                    left->accumulate(sum_to_shape(adjoint, a.shape()));
+                    right->accumulate(K<T>::scale(sum_to_shape(adjoint, b.shape()), T(-1)));
+                    break;
+                case BinaryOp::Mul:
+                    left->accumulate(sum_to_shape(K<T>::elementwise(adjoint, b, op), a.shape()));
+                    right->accumulate(sum_to_shape(K<T>::elementwise(adjoint, a, op), b.shape()));
+                    break;
+                case BinaryOp::Div: {
+                    // ā += c̄/b, b̄ −= (c̄/b)·a/b
+                    X over = K<T>::elementwise(adjoint, b, BinaryOp::Div);
+                    X scaled = K<T>::elementwise(K<T>::elementwise(over, a, BinaryOp::Mul), b, BinaryOp::Div);
+                    left->accumulate(sum_to_shape(over, a.shape()));
+                    right->accumulate(K<T>::scale(sum_to_shape(scaled, b.shape()), T(-1)));
+                    break;
+                }
+                default:
+                    break;
+            }
+        });
+    }
+
+    // `TensorVar::power` (tape/tensor.rs:162-185): ā += c̄·b·a^(b−1),
+    // b̄ += c̄·a^b·ln a, each summed to its operand's shape.
+    TensorVar power(const TensorVar& exponent) const {
+        this->assert_same_tape(exponent.tape());
+        auto base = this->node_;
+        auto power = exponent.node_;
+        return this->template record<X>(K<T>::power(this->value(), exponent.value()), [base, power](const X& adjoint) {
+            const X& a = base->get();
+            const X& b = power->get();
+            X lowered = K<T>::with_scalar(b, T(1), BinaryOp::Sub, false);
+            X slope = K<T>::elementwise(K<T>::power(a, lowered), b, BinaryOp::Mul);
+            base->accumulate(sum_to_shape(K<T>::elementwise(adjoint, slope, BinaryOp::Mul), a.shape()));
+            X growth = K<T>::elementwise(K<T>::power(a, b), K<T>::unary(a, Analytic::Ln), BinaryOp::Mul);
+            power->accumulate(sum_to_shape(K<T>::elementwise(adjoint, growth, BinaryOp::Mul), b.shape()));
+        });
+    }
+
+    // `TensorVar::power_scalar` (tape/tensor.rs:187-208): x^s, or s^x when
+    // `scalar_left`.
+    TensorVar power_scalar(T scalar, bool scalar_left) const {
+        auto parent = this->node_;
+        return this->template record<X>(
+            K<T>::power_scalar(this->value(), scalar, scalar_left), [parent, scalar, scalar_left](const X& adjoint) {
+                const X& x = parent->get();
+                X slope = scalar_left ? K<T>::scale(K<T>::power_scalar(x, scalar, true), T(std::log(scalar)))
+                                      : K<T>::scale(K<T>::power_scalar(x, scalar - T(1), false), scalar);
+                parent->accumulate(K<T>::elementwise(adjoint, slope, BinaryOp::Mul));
+            });
+    }
+
+    // `maximum` / `minimum` (tape/tensor.rs:210-250): the adjoint goes to
+    // whichever operand supplied the value, split evenly at ties.
+    TensorVar maximum(const TensorVar& other) const { return select_pair(other, true); }
+    TensorVar minimum(const TensorVar& other) const { return select_pair(other, false); }
+
+    // `clamp_min`, `clamp_max`, `clamp`, `relu`, `abs` (tape/tensor.rs:252-281).
+    TensorVar clamp_min(T floor) const { return select_scalar(floor, true); }
+    TensorVar clamp_max(T ceiling) const { return select_scalar(ceiling, false); }
+    TensorVar clamp(T floor, T ceiling) const {
+        if (floor > ceiling) throw std::invalid_argument("clamp: the lower bound exceeds the upper one");
+        return clamp_min(floor).clamp_max(ceiling);
+    }
+    TensorVar relu() const { return clamp_min(T(0)); }
+    TensorVar abs() const { return maximum(scale(T(-1))); }
+
+    // `TensorVar::analytic` (tape/tensor.rs:299-310): x̄ += f'(x)·ȳ in one
+    // dual dispatch.
+    TensorVar analytic(Analytic f) const {
+        auto parent = this->node_;
+        return this->template record<X>(K<T>::unary(this->value(), f), [parent, f](const X& adjoint) {
+            parent->accumulate(std::move(K<T>::unary_dual(parent->get(), adjoint, f).second));
+        });
+    }
+
+    // `neg`, `scale`, `shift` (tape/tensor.rs:311-333).
+    TensorVar neg() const { return scale(T(-1)); }
+    TensorVar scale(T factor) const {
+        auto parent = this->node_;
+        return this->template record<X>(K<T>::scale(this->value(), factor), [parent, factor](const X& adjoint) {
+            parent->accumulate(K<T>::scale(adjoint, factor));
+        });
+    }
+    TensorVar shift(T offset) const {
+        auto parent = this->node_;
+        return this->template record<X>(K<T>::with_scalar(this->value(), offset, BinaryOp::Add, false),
+                                        [parent](const X& adjoint) { parent->accumulate(adjoint.duplicate()); });
+    }
+
+    // ---- layout (tape/tensor.rs:335-420, :555-570) ----
+
+    // `reshape` (:335-350): the adjoint takes the old shape back.
+    TensorVar reshape(const Shape& shape) const {
+        auto parent = this->node_;
+        return this->template record<X>(this->value().duplicate().reshape(shape), [parent](const X& adjoint) {
+            parent->accumulate(adjoint.duplicate().reshape(parent->get().shape()));
+        });
+    }
+    // `contiguous` (:371-377): a copy; the adjoint passes through.
+    TensorVar contiguous() const {
+        auto parent = this->node_;
+        return this->template record<X>(this->value().duplicate(),
+                                        [parent](const X& adjoint) { parent->accumulate(adjoint.duplicate()); });
+    }
+    // `permute` (:379-400): the adjoint permuted back by the inverse.
+    TensorVar permute(const std::vector<size_t>& axes) const {
+        X value = K<T>::permute(this->value(), axes);
+        std::vector<size_t> inverse(axes.size());
+        for (size_t k = 0; k < axes.size(); k++) inverse[axes[k]] = k;
+        auto parent = this->node_;
+        return this->template record<X>(std::move(value), [parent, inverse](const X& adjoint) {
+            parent->accumulate(K<T>::permute(adjoint, inverse));
+        });
+    }
+    // `transpose` (:402-420): two axes swapped, negative ones from the end.
+    TensorVar transpose(long a, long b) const {
+        const std::vector<size_t> ab = K<T>::resolve_axes({a}, shape(), "transpose");
+        const std::vector<size_t> bb = K<T>::resolve_axes({b}, shape(), "transpose");
+        std::vector<size_t> axes(rank());
+        for (size_t k = 0; k < axes.size(); k++) axes[k] = k;
+        std::swap(axes[ab[0]], axes[bb[0]]);
+        return permute(axes);
+    }
+    // `broadcast_to` (:555-570): the adjoint summed back to this shape.
+    TensorVar broadcast_to(const Shape& shape) const {
+        auto parent = this->node_;
+        return this->template record<X>(K<T>::broadcast_to(this->value(), shape), [parent](const X& adjoint) {
+            parent->accumulate(sum_to_shape(adjoint, parent->get().shape()));
+        });
+    }
+
+    // ---- reductions (tape/tensor.rs:572-684) ----
+
+    // `sum_axes`: every element of a slice receives the slice's adjoint.
+    TensorVar sum_axes(const std::vector<long>& axes, bool keep_dims) const {
+        const Folding f = folding(axes, "sum_axes");
+        auto parent = this->node_;
+        X value = K<T>::reduce_axes(this->value(), f.folded, keep_dims, TC_AXIS_FOLD, Reduce::Sum, 0, true, T(0));
+        return this->template record<X>(std::move(value), [parent, f](const X& adjoint) {
+            parent->accumulate(K<T>::broadcast_to(adjoint.duplicate().reshape(f.kept), parent->get().shape()));
+        });
+    }
+    // `mean_axes`: the slice's adjoint over its length.
+    TensorVar mean_axes(const std::vector<long>& axes, bool keep_dims) const {
+        const Folding f = folding(axes, "mean_axes");
+        auto parent = this->node_;
+        X value = K<T>::reduce_axes(this->value(), f.folded, keep_dims, TC_AXIS_MEAN, Reduce::Sum, 0, true,
+                                    std::numeric_limits<T>::quiet_NaN());
+        const T share = T(1.0 / static_cast<double>(f.count));
+        return this->template record<X>(std::move(value), [parent, f, share](const X& adjoint) {
+            X scaled = K<T>::scale(adjoint, share);
+            parent->accumulate(K<T>::broadcast_to(std::move(scaled).reshape(f.kept), parent->get().shape()));
+        });
+    }
+    // `var_axes`: x̄ += ȳ·2(x − mean)/d, d the correction's divisor; a slice
+    // too short for the correction has a NaN variance and a NaN gradient.
+    TensorVar var_axes(const std::vector<long>& axes, Correction correction, bool keep_dims) const {
+        const Folding f = folding(axes, "var_axes");
+        const bool sample = correction == Correction::Sample;
+        const bool defined = sample ? f.count >= 2 : f.count >= 1;
+        const size_t divisor = defined ? (sample ? f.count - 1 : f.count) : 0;
+        const T nan = std::numeric_limits<T>::quiet_NaN();
+        X value = K<T>::reduce_axes(this->value(), f.folded, keep_dims, TC_AXIS_VARIANCE, Reduce::Sum, divisor,
+                                    defined, nan);
+        const T factor = defined ? T(2.0 / static_cast<double>(divisor)) : nan;
+        auto parent = this->node_;
+        return this->template record<X>(std::move(value), [parent, f, factor](const X& adjoint) {
+            const X& x = parent->get();
+            X mean = K<T>::reduce_axes(x, f.folded, true, TC_AXIS_MEAN, Reduce::Sum, 0, true,
+                                       std::numeric_limits<T>::quiet_NaN());
+            X deviation = K<T>::elementwise(x, mean, BinaryOp::Sub);
+            X weight = K<T>::scale(adjoint, factor);
+            parent->accumulate(K<T>::elementwise(deviation, std::move(weight).reshape(f.kept), BinaryOp::Mul));
+        });
+    }
+    // `max_axes` / `min_axes` through `extreme_axes`: the adjoint goes to
+    // the elements equal to their slice's extreme, shared evenly among ties;
+    // NaNs, which the fold passes over, receive none.
+    TensorVar max_axes(const std::vector<long>& axes, bool keep_dims) const {
+        return extreme_axes(axes, keep_dims, Reduce::Max, "max_axes");
+    }
+    TensorVar min_axes(const std::vector<long>& axes, bool keep_dims) const {
+        return extreme_axes(axes, keep_dims, Reduce::Min, "min_axes");
+    }
+
+    // `TensorVar::sum` (tape/tensor.rs:686-697): recorded unread, as
+    // `MatrixVar::sum` is; each element's adjoint is the scalar's, a fill.
+    ScalarVar sum() const {
+        auto parent = this->node_;
+        Lazy<float> total = Lazy<float>::ready(0.0f);
+        if (parent->get().len()) {
+            const uint64_t ticket = K<T>::reduce_async(parent->get().storage(), Reduce::Sum);
+            total = Lazy<float>::deferred([ticket] { return static_cast<float>(K<T>::read(ticket)); });
+        }
+        return ScalarVar(this->template record_lazy<float>(std::move(total), [parent](const float& adjoint) {
+            parent->accumulate(X::filled(parent->get().shape(), T(adjoint)));
+        }));
+    }
+    // `TensorVar::mean` (:699-701).
+    ScalarVar mean() const { return sum().scale(static_cast<float>(1.0 / static_cast<double>(len()))); }
+
+    // `TensorVar::to_matrix` (tape/tensor.rs:703-731): the elements, row
+    // major, as a rows × cols matrix; the adjoint takes this shape back.
+    MatrixVar<T> to_matrix(size_t rows, size_t cols) const {
+        if (rows * cols != len()) {
+            throw std::invalid_argument("to_matrix: shape " + shape_text(shape()) + " holds " + std::to_string(len()) +
+                                        " elements, which " + std::to_string(rows) + "×" + std::to_string(cols) +
+                                        " cannot");
+        }
+        auto parent = this->node_;
+        Matrix<T> value(rows, cols, this->value().duplicate().into_storage());
+        return MatrixVar<T>(this->template record<Matrix<T>>(std::move(value), [parent](const Matrix<T>& adjoint) {
+            parent->accumulate(X(parent->get().shape(), adjoint.duplicate().into_storage()));
+        }));
+    }
+
+   private:
+    // `folding` (tape/tensor.rs:39-53): the folded axes, the shape with them
+    // kept at extent 1, and the elements of a slice.
+    struct Folding {
+        std::vector<size_t> folded;
+        Shape kept;
+        size_t count;
+    };
+    Folding folding(const std::vector<long>& axes, const char* operation) const {
+        Folding f{K<T>::resolve_axes(axes, shape(), operation), shape(), 1};
+        for (size_t axis : f.folded) {
+            f.count *= f.kept[axis];
+            f.kept[axis] = 1;
+        }
+        return f;
+    }
+
+    TensorVar extreme_axes(const std::vector<long>& axes, bool keep_dims, Reduce op, const char* operation) const {
+        const Folding f = folding(axes, operation);
+        const T identity = op == Reduce::Max ? -std::numeric_limits<T>::infinity() : std::numeric_limits<T>::infinity();
+        X value = K<T>::reduce_axes(this->value(), f.folded, keep_dims, TC_AXIS_FOLD, op, 0, true, identity);
+        const Compare attains = op == Reduce::Max ? Compare::GreaterEqual : Compare::LessEqual;
+        auto parent = this->node_;
+        return this->template record<X>(std::move(value), [parent, f, op, attains, identity](const X& adjoint) {
+            const X& x = parent->get();
+            X extreme = K<T>::reduce_axes(x, f.folded, true, TC_AXIS_FOLD, op, 0, true, identity);
+            X mask = K<T>::compare(x, extreme, attains);
+            X ties = K<T>::compare_scalar(
+                K<T>::reduce_axes(mask, f.folded, true, TC_AXIS_FOLD, Reduce::Sum, 0, true, T(0)), T(1),
+                Compare::Max, false);
+            X share = K<T>::elementwise(adjoint.duplicate().reshape(f.kept), ties, BinaryOp::Div);
+            parent->accumulate(K<T>::elementwise(mask, share, BinaryOp::Mul));
+        });
+    }
+
+    TensorVar select_pair(const TensorVar& other, bool largest) const {
+        this->assert_same_tape(other.tape());
+        auto left = this->node_;
+        auto right = other.node_;
+        const Compare op = largest ? Compare::Max : Compare::Min;
+        return this->template record<X>(
+            K<T>::compare(this->value(), other.value(), op), [left, right, largest](const X& adjoint) {
+                const X& a = left->get();
+                const X& b = right->get();
+                X share = K<T>::compare(a, b, Compare::MaxShare);
+                X complement = K<T>::with_scalar(share, T(1), BinaryOp::Sub, true);
+                const X& mine = largest ? share : complement;
+                const X& theirs = largest ? complement : share;
+                left->accumulate(sum_to_shape(K<T>::elementwise(adjoint, mine, BinaryOp::Mul), a.shape()));
+                right->accumulate(sum_to_shape(K<T>::elementwise(adjoint, theirs, BinaryOp::Mul), b.shape()));
+            });
+    }
+
+    TensorVar select_scalar(T scalar, bool largest) const {
+        auto parent = this->node_;
+        const Compare op = largest ? Compare::Max : Compare::Min;
+        return this->template record<X>(
+            K<T>::compare_scalar(this->value(), scalar, op, false), [parent, scalar, largest](const X& adjoint) {
+                X share = K<T>::compare_scalar(parent->get(), scalar, Compare::MaxShare, false);
+                X weight = largest ? std::move(share) : K<T>::with_scalar(share, T(1), BinaryOp::Sub, true);
+                parent->accumulate(K<T>::elementwise(adjoint, weight, BinaryOp::Mul));
+            });
+    }
+};
+
+template <typename T>
+TensorVar<T> MatrixVar<T>::to_tensor(const Shape& shape) const {
+    auto parent = this->node_;
+    Tensor<T> value = Tensor<T>(Shape{this->rows(), this->cols()}, this->value().duplicate().into_storage()).reshape(shape);
+    return TensorVar<T>(this->template record<Tensor<T>>(std::move(value), [parent](const Tensor<T>& adjoint) {
+        const Matrix<T>& m = parent->get();
+        parent->accumulate(Matrix<T>(m.rows(), m.cols(), adjoint.duplicate().into_storage()));
+    }));
+}
 
 template <typename T>
 MatrixVar<T> VectorVar<T>::outer(const VectorVar& other) const {

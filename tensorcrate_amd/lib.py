@@ -382,7 +382,21 @@ HOST_SIGNATURES = {
     "tch_mlp_parameters": [vp, u32, vp, vp],
     "tch_mlp_gradients": [vp, u32, vp, vp],
     "tch_mlp_destroy": [vp],
+    "tch_tape_create": [ctypes.POINTER(vp)],
+    "tch_tape_destroy": [vp],
+    "tch_tape_tensor": [vp, u32, ctypes.POINTER(u64), vp, ctypes.POINTER(u32)],
+    "tch_tape_binary": [vp, u32, u32, u32, ctypes.POINTER(u32)],
+    "tch_tape_unary": [vp, u32, u32, f32, f32, ctypes.POINTER(u32)],
+    "tch_tape_layout": [vp, u32, u32, u32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(u32)],
+    "tch_tape_reduce": [vp, u32, u32, u32, ctypes.POINTER(ctypes.c_int64), i32, ctypes.POINTER(u32)],
+    "tch_tape_add_scalars": [vp, u32, u32, ctypes.POINTER(u32)],
+    "tch_tape_backward": [vp, u32, vp],
+    "tch_tape_shape": [vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u64)],
+    "tch_tape_read": [vp, u32, i32, vp],
+    "tch_tape_zero_grad": [vp],
 }
+
+HOST_VOID = {"tch_mlp_destroy", "tch_tape_destroy"}
 
 _host: ctypes.CDLL | None = None
 
@@ -400,7 +414,7 @@ def load_host() -> ctypes.CDLL:
     for name, argtypes in HOST_SIGNATURES.items():
         fn = getattr(host, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_char_p if name == "tch_last_error" else (None if name == "tch_mlp_destroy" else ctypes.c_int)
+        fn.restype = ctypes.c_char_p if name == "tch_last_error" else (None if name in HOST_VOID else ctypes.c_int)
     _host = host
     return host
 
@@ -458,3 +472,111 @@ class Mlp:
             self.close()
         except Exception:
             pass
+
+
+# ``tch_binary``, ``tch_unary``, ``tch_layout``, ``tch_reduction`` (include/tchip_host.h).
+TAPE_BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3, "maximum": 4, "minimum": 5, "power": 6, "matmul": 7}
+TAPE_UNARY = {"clamp_min": 0, "clamp_max": 1, "clamp": 2, "relu": 3, "abs": 4, "neg": 5, "scale": 6, "shift": 7,
+              "power_scalar": 8, "power_scalar_left": 9, "contiguous": 10}
+TAPE_ANALYTIC = 32
+TAPE_LAYOUT = {"reshape": 0, "permute": 1, "transpose": 2, "broadcast_to": 3}
+TAPE_REDUCE = {"sum_axes": 0, "mean_axes": 1, "var_axes": 2, "var_axes_sample": 3, "max_axes": 4, "min_axes": 5,
+               "sum": 6, "mean": 7}
+
+
+class Tape:
+    """A tape of tensor variables on the C++ mirror of tape/tensor.rs,
+    through ``tch_tape_*``: ``tensor`` records a leaf, the methods of
+    ``TapeVar`` record operations, ``backward`` runs the rules."""
+
+    def __init__(self):
+        handle = vp()
+        host_call("tch_tape_create", ctypes.byref(handle))
+        self.handle = handle.value
+
+    def _out(self, name, *args) -> "TapeVar":
+        out = u32()
+        host_call(name, self.handle, *args, ctypes.byref(out))
+        return TapeVar(self, out.value)
+
+    def tensor(self, values) -> "TapeVar":
+        values = np.array(values, np.float32, order="C")  # keeps a 0-d shape, which ascontiguousarray does not
+        dims = (u64 * max(values.ndim, 1))(*values.shape)
+        return self._out("tch_tape_tensor", values.ndim, dims, values.ctypes.data)
+
+    def zero_grad(self) -> None:
+        host_call("tch_tape_zero_grad", self.handle)
+
+    def close(self) -> None:
+        if self.handle is not None:
+            load_host().tch_tape_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _axes(axes):
+    axes = [axes] if isinstance(axes, int) else list(axes)
+    return len(axes), (ctypes.c_int64 * max(len(axes), 1))(*axes)
+
+
+class TapeVar:
+    """One variable of a ``Tape``: a tensor, or a scalar from ``sum``/``mean``."""
+
+    def __init__(self, tape: Tape, handle: int):
+        self.tape, self.handle = tape, handle
+
+    @property
+    def shape(self) -> tuple[int, ...]:
+        rank, dims = u32(), (u64 * 8)()
+        host_call("tch_tape_shape", self.tape.handle, self.handle, ctypes.byref(rank), dims)
+        return tuple(dims[k] for k in range(rank.value))
+
+    def _read(self, gradient: int):
+        shape = self.shape
+        out = np.empty(shape, np.float32)
+        host_call("tch_tape_read", self.tape.handle, self.handle, gradient, out.ctypes.data)
+        return out if shape else float(out)
+
+    def value(self):
+        return self._read(0)
+
+    def grad(self):
+        return self._read(1)
+
+    def binary(self, other: "TapeVar", op: str) -> "TapeVar":
+        return self.tape._out("tch_tape_binary", TAPE_BINARY[op], self.handle, other.handle)
+
+    __add__ = lambda self, o: self.binary(o, "add")
+    __sub__ = lambda self, o: self.binary(o, "sub")
+    __mul__ = lambda self, o: self.binary(o, "mul")
+    __truediv__ = lambda self, o: self.binary(o, "div")
+
+    def unary(self, op, first: float = 0.0, second: float = 0.0) -> "TapeVar":
+        code = op if isinstance(op, int) else TAPE_UNARY[op]
+        return self.tape._out("tch_tape_unary", code, self.handle, first, second)
+
+    def analytic(self, f: int) -> "TapeVar":
+        return self.unary(TAPE_ANALYTIC + f)
+
+    def layout(self, op: str, values) -> "TapeVar":
+        count, array = _axes(values)
+        return self.tape._out("tch_tape_layout", TAPE_LAYOUT[op], self.handle, count, array)
+
+    def reduce(self, op: str, axes=(), keep_dims: bool = False) -> "TapeVar":
+        count, array = _axes(axes)
+        return self.tape._out("tch_tape_reduce", TAPE_REDUCE[op], self.handle, count, array, int(keep_dims))
+
+    def add_scalar(self, other: "TapeVar") -> "TapeVar":
+        return self.tape._out("tch_tape_add_scalars", self.handle, other.handle)
+
+    def backward(self, seed=None) -> None:
+        if seed is None:
+            host_call("tch_tape_backward", self.tape.handle, self.handle, None)
+            return
+        seed = np.array(seed, np.float32, order="C")
+        host_call("tch_tape_backward", self.tape.handle, self.handle, seed.ctypes.data)

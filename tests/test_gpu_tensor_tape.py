@@ -1,0 +1,292 @@
+"""Tensor variables on the tape (host/tape.hpp's `TensorVar`, the C++ mirror
+of src/tensors/tape/tensor.rs) on the GPU, operation by operation, as
+tests/tensor_autodiff.rs:50-400 checks them in the reference.
+
+Each operation is written once against a small facade and run twice: on the
+device tape (`lib.Tape`), which differentiates it with one backward pass from
+a fixed seed, and in numpy f64, whose central differences of
+``<op(inputs), seed>`` are the expected gradients.  The f32 gradients must
+agree within 2e-4 of the largest expected magnitude, the reference's bound
+for f32 against f64 (tensor_autodiff.rs:388-391).  The inputs are rounded to
+f32 first, so both sides see the same values.  The harness itself is pinned
+on the CPU against closed forms (`test_the_difference_harness_...`).
+
+Not covered: narrow, slice, select, split, chunk, concat, stack and the
+vector round trip — operations this tape does not record.
+"""
+
+import numpy as np
+import pytest
+
+from tensorcrate_amd import lib
+from tests.test_oracle_analytic import NUMPY_F64
+
+X = (2, 3, 4, 5)
+
+
+def filled(shape, seed, low, high):
+    return np.random.default_rng(seed).uniform(low, high, shape).astype(np.float32).astype(np.float64)
+
+
+class Np:
+    """The facade in numpy f64: what each recorded operation computes."""
+
+    def __init__(self, value):
+        self.v = np.asarray(value, np.float64)
+
+    def binary(self, other, op):
+        a, b = self.v, other.v
+        return Np({"add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide,
+                   "maximum": np.maximum, "minimum": np.minimum, "power": np.power,
+                   "matmul": np.matmul}[op](a, b))
+
+    __add__ = lambda self, o: self.binary(o, "add")
+    __sub__ = lambda self, o: self.binary(o, "sub")
+    __mul__ = lambda self, o: self.binary(o, "mul")
+    __truediv__ = lambda self, o: self.binary(o, "div")
+
+    def unary(self, op, first=0.0, second=0.0):
+        x = self.v
+        table = {"clamp_min": lambda: np.maximum(x, first), "clamp_max": lambda: np.minimum(x, first),
+                 "clamp": lambda: np.clip(x, first, second), "relu": lambda: np.maximum(x, 0.0),
+                 "abs": lambda: np.abs(x), "neg": lambda: -x, "scale": lambda: x * first,
+                 "shift": lambda: x + first, "power_scalar": lambda: x ** first,
+                 "power_scalar_left": lambda: first ** x, "contiguous": lambda: x.copy()}
+        return Np(table[op]())
+
+    def analytic(self, f):
+        return Np(NUMPY_F64[f](self.v))
+
+    def layout(self, op, values):
+        x = self.v
+        if op == "reshape":
+            return Np(x.reshape(values))
+        if op == "permute":
+            return Np(np.transpose(x, values))
+        if op == "transpose":
+            return Np(np.swapaxes(x, *values))
+        return Np(np.broadcast_to(x, values).copy())
+
+    def reduce(self, op, axes=(), keep_dims=False):
+        x = self.v
+        axes = (axes,) if isinstance(axes, int) else tuple(axes)
+        if op == "sum":
+            return Np(x.sum())
+        if op == "mean":
+            return Np(x.mean())
+        fold = {"sum_axes": lambda: x.sum(axis=axes, keepdims=keep_dims),
+                "mean_axes": lambda: x.mean(axis=axes, keepdims=keep_dims),
+                "var_axes": lambda: x.var(axis=axes, keepdims=keep_dims),
+                "var_axes_sample": lambda: x.var(axis=axes, ddof=1, keepdims=keep_dims),
+                "max_axes": lambda: x.max(axis=axes, keepdims=keep_dims),
+                "min_axes": lambda: x.min(axis=axes, keepdims=keep_dims)}
+        return Np(fold[op]())
+
+
+def positive(shape, seed):
+    return filled(shape, seed, 0.5, 1.5)
+
+
+def x():
+    return filled(X, 1, -1.0, 1.0)
+
+
+# The operations of tensor_autodiff.rs:52-270 this tape records: name,
+# inputs, and the computation on recorded inputs `v`.
+OPS = [
+    ("add_same", lambda: [x(), filled(X, 2, -1, 1)], lambda v: v[0] + v[1]),
+    ("add_broadcast", lambda: [x(), filled((4, 1), 2, -1, 1)], lambda v: v[0] + v[1]),
+    ("sub_broadcast", lambda: [filled((3, 1, 5), 2, -1, 1), x()], lambda v: v[0] - v[1]),
+    ("mul_broadcast", lambda: [filled((2, 1, 4, 1), 1, -1, 1), filled((1, 3, 1, 5), 2, -1, 1)],
+     lambda v: v[0] * v[1]),
+    ("div_broadcast", lambda: [x(), positive((5,), 2)], lambda v: v[0] / v[1]),
+    ("div_left_broadcast", lambda: [filled((3, 1, 1), 2, -1, 1), positive(X, 3)], lambda v: v[0] / v[1]),
+    ("scalar_operand", lambda: [x(), filled((), 2, 0.5, 1.5)], lambda v: (v[0] * v[1]) + v[1]),
+    ("permuted_operand", lambda: [x(), filled((3, 1), 2, -1, 1)],
+     lambda v: v[0].layout("permute", [0, 2, 1, 3]) * v[1]),
+    ("maximum", lambda: [x(), filled((4, 5), 2, -1, 1)], lambda v: v[0].binary(v[1], "maximum")),
+    ("minimum", lambda: [filled((3, 1, 5), 2, -1, 1), x()], lambda v: v[0].binary(v[1], "minimum")),
+    ("power", lambda: [positive((2, 3, 4), 1), filled((4,), 2, -1, 2)], lambda v: v[0].binary(v[1], "power")),
+    ("power_scalar", lambda: [positive(X, 1)], lambda v: v[0].unary("power_scalar", 2.5)),
+    ("power_scalar_left", lambda: [x()], lambda v: v[0].unary("power_scalar_left", 1.7)),
+    ("scale_shift_neg", lambda: [x()], lambda v: v[0].unary("scale", -1.5).unary("shift", 0.25).unary("neg")),
+    ("abs", lambda: [x()], lambda v: v[0].unary("abs")),
+    ("relu", lambda: [x()], lambda v: v[0].unary("relu")),
+    ("clamp", lambda: [x()], lambda v: v[0].unary("clamp", -0.5, 0.4)),
+    *[(f"analytic_{f}", lambda: [filled((2, 3, 4), 1, 0.15, 0.85)], (lambda f: lambda v: v[0].analytic(f))(f))
+      for f in range(14)],
+    ("reshape", lambda: [x()], lambda v: v[0].layout("reshape", [6, 20])),
+    ("permute", lambda: [x()], lambda v: v[0].layout("permute", [0, 2, 3, 1])),
+    ("transpose", lambda: [x()], lambda v: v[0].layout("transpose", [-1, 1])),
+    ("squeeze_unsqueeze", lambda: [filled((2, 1, 4), 1, -1, 1)], lambda v: v[0].layout("reshape", [1, 2, 4, 1])),
+    ("broadcast_to", lambda: [filled((3, 1, 5), 1, -1, 1)], lambda v: v[0].layout("broadcast_to", list(X))),
+    ("contiguous", lambda: [x()], lambda v: v[0].unary("contiguous")),
+    ("sum_axes", lambda: [x()], lambda v: v[0].reduce("sum_axes", [1, 3])),
+    ("sum_axes_keep", lambda: [x()], lambda v: v[0].reduce("sum_axes", -2, True)),
+    ("sum_all", lambda: [x()], lambda v: v[0].reduce("sum_axes", [0, 1, 2, 3])),
+    ("mean_axes", lambda: [x()], lambda v: v[0].reduce("mean_axes", [0, 2], True)),
+    ("var_axes_population", lambda: [x()], lambda v: v[0].reduce("var_axes", [1, 2])),
+    ("var_axes_sample", lambda: [x()], lambda v: v[0].reduce("var_axes_sample", -1, True)),
+    ("max_axes", lambda: [x()], lambda v: v[0].reduce("max_axes", [1, 3])),
+    ("min_axes", lambda: [x()], lambda v: v[0].reduce("min_axes", -1, True)),
+    ("matrix_round_trip", lambda: [filled((2, 3, 4), 1, -1, 1), filled((4, 5), 2, -1, 1)],
+     lambda v: v[0].binary(v[1], "matmul").analytic(12)),
+    # A tensor used twice: the second rule adds into an adjoint already there.
+    ("reused_operand", lambda: [x()], lambda v: v[0].reduce("sum_axes", 1, True) + (v[0] * v[0])),
+]
+
+
+def seed_for(shape):
+    return filled(shape, 7, -1.0, 1.0)
+
+
+def projected(apply, inputs, seed):
+    return float(np.sum(apply([Np(a) for a in inputs]).v * seed))
+
+
+def differences(apply, inputs):
+    """Central differences of <apply(inputs), seed> in f64, step
+    1e-6·max(|x|, 1), as tensor_autodiff.rs:327-359 takes them."""
+    seed = seed_for(apply([Np(a) for a in inputs]).v.shape)
+    grads = []
+    for which, a in enumerate(inputs):
+        g = np.empty(a.size)
+        for k in range(a.size):
+            h = 1e-6 * max(abs(a.flat[k]), 1.0)
+            moved = [b.copy() for b in inputs]
+            moved[which].flat[k] = a.flat[k] + h
+            up = projected(apply, moved, seed)
+            moved[which].flat[k] = a.flat[k] - h
+            g[k] = (up - projected(apply, moved, seed)) / (2 * h)
+        grads.append(g.reshape(a.shape))
+    return grads, seed
+
+
+def assert_close(got, want, tolerance, what):
+    scale = max(1.0, float(np.max(np.abs(want))) if want.size else 0.0)
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - want))) if want.size else 0.0
+    assert err <= tolerance * scale, f"{what}: error {err} against scale {scale}"
+
+
+def test_the_difference_harness_reproduces_closed_forms():
+    """Pins the harness: d<a·b, s>/da = b·s summed over the broadcast,
+    d<Σ_axis x, s>/dx = s spread, d<max(x,0), s>/dx = s·[x>0]."""
+    a, b = filled((3, 1), 1, -1, 1), filled((3, 4), 2, -1, 1)
+    (ga, gb), s = differences(lambda v: v[0] * v[1], [a, b])
+    assert np.allclose(ga, (b * s).sum(axis=1, keepdims=True), atol=1e-8)
+    assert np.allclose(gb, a * s, atol=1e-8)
+    (gx,), s = differences(lambda v: v[0].reduce("sum_axes", 0), [b])
+    assert np.allclose(gx, np.broadcast_to(s, b.shape), atol=1e-8)
+    (gx,), s = differences(lambda v: v[0].unary("relu"), [b])
+    assert np.allclose(gx, s * (b > 0), atol=1e-8)
+    # A planted mistake (the wrong operand's value) is caught.
+    assert not np.allclose(ga, (a * s).sum(axis=1, keepdims=True), atol=1e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,inputs,apply", OPS, ids=[op[0] for op in OPS])
+def test_every_operation_matches_finite_differences(name, inputs, apply):
+    values = inputs()
+    want, seed = differences(apply, values)
+    tape = lib.Tape()
+    leaves = [tape.tensor(a) for a in values]
+    out = apply(leaves)
+    expected = apply([Np(a) for a in values]).v
+    assert out.shape == expected.shape, name
+    assert_close(out.value(), expected, 1e-5, f"{name} value")
+    out.backward(seed)
+    for which, (leaf, g) in enumerate(zip(leaves, want)):
+        got = leaf.grad()
+        assert np.shape(got) == g.shape, f"{name}: gradient shape"
+        assert_close(got, g, 2e-4, f"{name} d/d input{which}")
+    tape.close()
+
+
+@pytest.mark.gpu
+def test_axis_extremes_share_the_adjoint_among_ties_and_skip_nans():
+    # tensor_autodiff.rs:401-423
+    tape = lib.Tape()
+    x = tape.tensor(np.array([[1.0, 3.0, 3.0, 2.0], [np.nan, -1.0, 5.0, 5.0]]))
+    top = x.reduce("max_axes", -1)
+    assert np.array_equal(top.value(), [3.0, 5.0])
+    top.reduce("sum").backward()
+    assert np.array_equal(x.grad(), [[0, 0.5, 0.5, 0], [0, 0, 0.5, 0.5]])
+    bottom = x.reduce("min_axes", [0, 1], True)
+    assert np.array_equal(bottom.value(), [[-1.0]])
+    bottom.reduce("sum").backward()
+    assert np.array_equal(x.grad(), [[0, 0, 0, 0], [0, 1, 0, 0]])
+    nans = tape.tensor(np.array([[np.nan, np.nan]]))
+    nans.reduce("max_axes", 1).reduce("sum").backward()
+    assert np.array_equal(nans.grad(), [[0.0, 0.0]])
+    tape.close()
+
+
+@pytest.mark.gpu
+def test_elementwise_extremes_split_ties_and_sum_over_the_broadcast():
+    # tensor_autodiff.rs:425-434
+    tape = lib.Tape()
+    x = tape.tensor(np.array([[1.0, 2.0], [3.0, 0.0]]))
+    floor = tape.tensor(np.array([1.0, 1.0]))
+    x.binary(floor, "maximum").reduce("sum").backward()
+    assert np.array_equal(x.grad(), [[0.5, 1.0], [1.0, 0.0]])
+    assert np.array_equal(floor.grad(), [0.5, 1.0])
+    tape.close()
+
+
+@pytest.mark.gpu
+def test_whole_tensor_sums_and_means_are_lazy_scalars():
+    # tensor_autodiff.rs:436-450
+    tape = lib.Tape()
+    values = filled((2, 3, 4), 1, -1, 1)
+    x = tape.tensor(values)
+    total, mean = x.reduce("sum"), x.reduce("mean")
+    total.add_scalar(mean).backward()
+    assert np.allclose(x.grad(), 1.0 + 1.0 / 24.0, rtol=0, atol=1e-7)
+    assert abs(total.value() - values.sum()) <= 1e-5
+    assert abs(mean.value() - values.sum() / 24) <= 1e-6
+    tape.close()
+
+
+@pytest.mark.gpu
+def test_empty_and_unit_extents_differentiate():
+    # After tensor_autodiff.rs:452-477: a [0, 3] tensor folds to zeros and
+    # receives a [0, 3] gradient; the unit tensor's gradient is its partner.
+    tape = lib.Tape()
+    empty = tape.tensor(np.zeros((0, 3)))
+    unit = tape.tensor(np.array([[[1.0], [2.0], [3.0]]]))
+    folded = empty.reduce("sum_axes", 0)
+    assert np.array_equal(folded.value(), [0.0, 0.0, 0.0])
+    row = unit.layout("reshape", [3])
+    ((folded + row) * row).reduce("sum").backward()
+    assert empty.grad().shape == (0, 3)
+    assert np.array_equal(unit.grad(), [[[2.0], [4.0], [6.0]]])
+    tape.close()
+
+
+@pytest.mark.gpu
+def test_a_second_backward_pass_gives_the_same_tensor_gradients():
+    # tensor_autodiff.rs:484-496
+    tape = lib.Tape()
+    x = tape.tensor(filled((2, 3, 4), 1, -1, 1))
+    loss = ((x * x.analytic(8)) + x.reduce("max_axes", 1, True)).reduce("sum")
+    loss.backward()
+    first = x.grad()
+    loss.backward()
+    assert np.array_equal(x.grad(), first)
+    tape.zero_grad()
+    assert not np.any(x.grad())
+    tape.close()
+
+
+@pytest.mark.gpu
+def test_shapes_that_do_not_broadcast_are_rejected():
+    # tensor_autodiff.rs:498-514
+    tape = lib.Tape()
+    a, b = tape.tensor(np.zeros((2, 3))), tape.tensor(np.zeros(4))
+    with pytest.raises(lib.HipError, match=r"add: tensor shapes differ, \[2, 3\] and \[4\]"):
+        a + b
+    with pytest.raises(lib.HipError, match=r"sum_axes: axes \[1, -1\] are not distinct axes of shape \[2, 3\]"):
+        a.reduce("sum_axes", [1, -1])
+    with pytest.raises(lib.HipError, match=r"reshape: shape \[2, 3\] holds 6 elements"):
+        a.layout("reshape", [4])
+    tape.close()
