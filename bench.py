@@ -339,6 +339,41 @@ def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
     return lines
 
 
+def vector_products(steps: int, warmup: int) -> list[dict]:
+    """GEMV, vecmat and dot at the bandwidth sizes of configs a11, and the
+    4096 x 4096 transpose of a12; inputs rotate past the Infinity Cache."""
+    rng = np.random.default_rng(5)
+    rows = cols = 8192
+    mbytes = 4 * rows * cols
+    host = rng.standard_normal((rows, cols), dtype=np.float32)
+    mats = rotation(lambda: lib.Buffer.of(host), mbytes)
+    v = lib.Buffer.of(rng.standard_normal(cols, dtype=np.float32))
+    y = lib.Buffer(4 * rows)
+    lines = []
+    ms = timed_graph(rotating(mats, lambda m: lib.call("tc_matvec", lib.F32, 0, rows, cols, m.ptr, v.ptr, y.ptr)),
+                     max(steps, 2 * len(mats)), warmup)
+    lines.append(hbm_line(f"matvec, f32 [{rows}x{cols}] . [{cols}]", mbytes + 4 * (rows + cols), ms))
+    ms = timed_graph(rotating(mats, lambda m: lib.call("tc_vecmat", lib.F32, rows, cols, v.ptr, m.ptr, y.ptr)),
+                     max(steps, 2 * len(mats)), warmup)
+    lines.append(hbm_line(f"vecmat, f32 [{rows}] . [{rows}x{cols}]", mbytes + 4 * (rows + cols), ms))
+    del mats
+    n = 64 << 20
+    a = lib.Buffer.of(rng.standard_normal(n, dtype=np.float32))
+    b = lib.Buffer.of(rng.standard_normal(n, dtype=np.float32))
+    result = lib.Buffer(4)
+    ms = timed_graph(lambda: lib.call("tc_dot", lib.F32, a.ptr, b.ptr, n, result.ptr), steps, warmup)
+    lines.append(hbm_line("dot, f32 64 Mi elements", 8 * n, ms))
+    del a, b
+    side = 4096
+    tbytes = 4 * side * side
+    srcs = rotation(lambda: lib.Buffer.of(rng.standard_normal((side, side), dtype=np.float32)), tbytes)
+    dst = lib.Buffer(tbytes)
+    ms = timed_graph(rotating(srcs, lambda m: lib.call("tc_transpose", 4, side, side, m.ptr, dst.ptr)),
+                     max(steps, 2 * len(srcs)), warmup)
+    lines.append(hbm_line(f"transpose, f32 [{side}x{side}]", 2 * tbytes, ms))
+    return lines
+
+
 def mlp_step(steps: int, warmup: int) -> list[dict]:
     """Configuration 5: the training step of the reference's harness
     (``mlp_step``, benches/nn_ops.rs:875-921) at 1024 -> 4096 -> 4096 -> 1024,
@@ -442,6 +477,9 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
     if "copies" in groups:
         log("broadcast chain and copies ...")
         workloads += broadcast_and_copies(steps, warmup)
+    if "vectors" in groups:
+        log("matvec, vecmat, dot, transpose ...")
+        workloads += vector_products(steps, warmup)
     if "fusion" in groups:
         log("dense layers, fused and unfused ...")
         workloads += dense_layer("bf16", 8192, 8192, 8192, steps, warmup)
@@ -473,7 +511,7 @@ def main() -> int:
     parser.add_argument("--traffic-probe", action="store_true",
                         help="only the short copy + product run that HBM-traffic counters are read over")
     parser.add_argument("--only", default="",
-                        help="comma-separated secondary groups to run alone (gemm, reductions, copies, fusion, transfer, mlp); "
+                        help="comma-separated secondary groups to run alone (gemm, reductions, copies, vectors, fusion, transfer, mlp); "
                              "prints their lines as a JSON list instead of the headline line")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -488,7 +526,7 @@ def main() -> int:
 
     if args.only:
         groups = set(args.only.split(","))
-        unknown = groups - {"gemm", "reductions", "copies", "fusion", "transfer", "mlp"}
+        unknown = groups - {"gemm", "reductions", "copies", "vectors", "fusion", "transfer", "mlp"}
         if unknown:
             print(f"bench.py: no workload group {sorted(unknown)}", file=sys.stderr)
             return 2
@@ -502,7 +540,7 @@ def main() -> int:
     log(f"  {head['value']:.1f} TFLOP/s ({head['ms']:.3f} ms/step), kernel {head['roofline']['achieved']:.1f}")
     workloads = []
     if not args.quick:
-        workloads = secondary({"gemm", "reductions", "copies", "fusion", "mlp"}, args.steps, args.warmup)
+        workloads = secondary({"gemm", "reductions", "copies", "vectors", "fusion", "mlp"}, args.steps, args.warmup)
     baseline = None
     if not args.quick and not args.no_cpu:
         log("CPU baseline ...")

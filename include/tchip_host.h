@@ -81,10 +81,18 @@ typedef enum tch_unary {
     TCH_ANALYTIC = 32
 } tch_unary;
 
-/* Layout operations (tape/tensor.rs:335-420, :555-570): `values` is the new
- * shape, the permutation, the two axes to swap (negative from the end), or
- * the shape to broadcast to. */
-typedef enum tch_layout { TCH_RESHAPE = 0, TCH_PERMUTE = 1, TCH_TRANSPOSE = 2, TCH_BROADCAST_TO = 3 } tch_layout;
+/* Layout operations (tape/tensor.rs:335-462, :555-570): `values` is the new
+ * shape, the permutation, the two axes to swap, the shape to broadcast to,
+ * (axis, start, len) of a narrow, (axis, index) of a select, (axis, start,
+ * end) of a slice, or the one axis to squeeze or unsqueeze.  Axes may be
+ * negative, counted from the end. */
+typedef enum tch_layout {
+    TCH_RESHAPE = 0, TCH_PERMUTE = 1, TCH_TRANSPOSE = 2, TCH_BROADCAST_TO = 3,
+    TCH_NARROW = 4, TCH_SELECT = 5, TCH_SLICE = 6, TCH_SQUEEZE = 7, TCH_UNSQUEEZE = 8
+} tch_layout;
+
+/* Joins (tape/tensor.rs:502-553): along an existing axis, or a new one. */
+typedef enum tch_join { TCH_CONCAT = 0, TCH_STACK = 1 } tch_join;
 
 /* Reductions (tape/tensor.rs:572-701): over `axes` (negative from the end),
  * or, for TCH_SUM and TCH_MEAN, over everything to a scalar. */
@@ -102,6 +110,12 @@ int tch_tape_unary(tch_tape* tape, uint32_t op, uint32_t a, float first, float s
 int tch_tape_layout(tch_tape* tape, uint32_t op, uint32_t a, uint32_t count, const int64_t* values, uint32_t* out);
 int tch_tape_reduce(tch_tape* tape, uint32_t op, uint32_t a, uint32_t count, const int64_t* axes, int keep_dims,
                     uint32_t* out);
+/* `split` into pieces of `sizes` along `axis`, or with `sizes` NULL
+ * `chunk` into `count` equal pieces (tape/tensor.rs:464-500); `out` receives
+ * `count` handles. */
+int tch_tape_split(tch_tape* tape, uint32_t a, int64_t axis, uint32_t count, const uint64_t* sizes, uint32_t* out);
+/* `concat` or `stack` of `count` tensors along `axis`. */
+int tch_tape_join(tch_tape* tape, uint32_t op, uint32_t count, const uint32_t* handles, int64_t axis, uint32_t* out);
 /* The sum of two scalars (`ScalarVar::add`). */
 int tch_tape_add_scalars(tch_tape* tape, uint32_t a, uint32_t b, uint32_t* out);
 /* `backward_with` (tape/mod.rs:507-529) from `output`, seeded with `seed`

@@ -40,9 +40,25 @@ __global__ void __launch_bounds__(256) matvec_kernel(const S* __restrict__ m, co
         const S* row = m + r * cols;
         float total = 0.0f;
         if (PACKED) {
+            // Four 16-byte packs of the row in flight per lane.
             const Pack<S>* pr = reinterpret_cast<const Pack<S>*>(row);
             const Pack<S>* pv = reinterpret_cast<const Pack<S>*>(v);
-            for (uint64_t p = lane; p < cols / N; p += 64) {
+            const uint64_t packs = cols / N;
+            uint64_t p = lane;
+            for (; p + 3 * 64 < packs; p += 4 * 64) {
+                Pack<S> a[4], b[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    a[u] = pr[p + u * 64];
+                    b[u] = pv[p + u * 64];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+#pragma unroll
+                    for (int k = 0; k < N; k++) total += E::widen(a[u].v[k]) * E::widen(b[u].v[k]);
+                }
+            }
+            for (; p < packs; p += 64) {
                 Pack<S> a = pr[p], b = pv[p];
 #pragma unroll
                 for (int k = 0; k < N; k++) total += E::widen(a.v[k]) * E::widen(b.v[k]);
@@ -85,7 +101,25 @@ __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, co
 #pragma unroll
     for (int k = 0; k < V; k++) acc[k] = 0.0f;
     if (col0 < cols) {
-        for (uint64_t r = first; r < last; r++) {
+        uint64_t r = first;
+        if (V > 1) {
+            // Eight rows' packs in flight per lane before any is used.
+            for (; r + 8 <= last; r += 8) {
+                Pack<S> p[8];
+                float w[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    p[u] = *reinterpret_cast<const Pack<S>*>(m + (r + u) * cols + col0);
+                    w[u] = E::widen(v[r + u]);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+#pragma unroll
+                    for (int k = 0; k < V; k++) acc[k] += w[u] * E::widen(p[u].v[k]);
+                }
+            }
+        }
+        for (; r < last; r++) {
             const float w = E::widen(v[r]);
             if (V > 1) {
                 Pack<S> p = *reinterpret_cast<const Pack<S>*>(m + r * cols + col0);

@@ -748,17 +748,61 @@ int arg_reduce_typed(const void* input, uint64_t input_len, const tc_split* spli
 
 // Stage one: each block folds a strided share into `partial[block]`; stage
 // two: one block folds the partials in order into `result`.
-template <typename S, uint32_t OP, bool DOT>
+// PACKED reads 16-byte packs, four per operand in flight per lane; NT
+// streams inputs larger than the Infinity Cache past it.
+template <typename S, uint32_t OP, bool DOT, bool PACKED, bool NT>
 __global__ void __launch_bounds__(256) total_kernel(const S* __restrict__ a, const S* __restrict__ b,
                                                     uint64_t n, float* __restrict__ partial) {
     using E = Elem<S>;
     using P = Fold<OP>;
+    constexpr int V = Pack<S>::N;
+    constexpr int U = 4;
     __shared__ float stage[4];
     float s = P::init();
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
-        const float x = E::widen(a[i]);
-        P::add(s, DOT ? x * E::widen(b[i]) : x, 0);
+    const uint64_t first = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (PACKED) {
+        const Pack<S>* pa = reinterpret_cast<const Pack<S>*>(a);
+        const Pack<S>* pb = reinterpret_cast<const Pack<S>*>(b);
+        const uint64_t packs = n / V;
+        uint64_t p = first;
+        for (; p + (U - 1) * stride < packs; p += U * stride) {
+            uint4 wa[U], wb[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                wa[u] = load_word<NT>(pa + p + u * stride);
+                if (DOT) wb[u] = load_word<NT>(pb + p + u * stride);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                Pack<S> x, y;
+                __builtin_memcpy(&x, &wa[u], 16);
+                if (DOT) __builtin_memcpy(&y, &wb[u], 16);
+#pragma unroll
+                for (int j = 0; j < V; j++) {
+                    const float e = E::widen(x.v[j]);
+                    P::add(s, DOT ? e * E::widen(y.v[j]) : e, 0);
+                }
+            }
+        }
+        for (; p < packs; p += stride) {
+            Pack<S> x = pa[p];
+#pragma unroll
+            for (int j = 0; j < V; j++) {
+                const float e = E::widen(x.v[j]);
+                P::add(s, DOT ? e * E::widen(pb[p].v[j]) : e, 0);
+            }
+        }
+        const uint64_t i = packs * V + first;
+        if (i < n) {
+            const float x = E::widen(a[i]);
+            P::add(s, DOT ? x * E::widen(b[i]) : x, 0);
+        }
+    } else {
+        for (uint64_t i = first; i < n; i += stride) {
+            const float x = E::widen(a[i]);
+            P::add(s, DOT ? x * E::widen(b[i]) : x, 0);
+        }
     }
     s = wave_reduce<P>(s);
     if (threadIdx.x % 64 == 0) stage[threadIdx.x / 64] = s;
@@ -788,7 +832,17 @@ int total(const void* a, const void* b, uint64_t n, float* result, const char* w
     int status = tc_alloc(blocks * sizeof(float), &scratch);
     if (status != TC_OK) return status;
     float* partial = static_cast<float*>(scratch);
-    total_kernel<S, OP, DOT><<<blocks, 256, 0, s>>>(static_cast<const S*>(a), static_cast<const S*>(b), n, partial);
+    const S* pa = static_cast<const S*>(a);
+    const S* pb = static_cast<const S*>(b);
+    const bool packed = aligned16(a) && (!DOT || aligned16(b));
+    const bool stream = n * sizeof(S) * (DOT ? 2 : 1) >= kStreamBytes;
+    if (packed && stream) {
+        total_kernel<S, OP, DOT, true, true><<<blocks, 256, 0, s>>>(pa, pb, n, partial);
+    } else if (packed) {
+        total_kernel<S, OP, DOT, true, false><<<blocks, 256, 0, s>>>(pa, pb, n, partial);
+    } else {
+        total_kernel<S, OP, DOT, false, false><<<blocks, 256, 0, s>>>(pa, pb, n, partial);
+    }
     status = check_launch(what);
     if (status == TC_OK) {
         finish_total_kernel<OP><<<1, 64, 0, s>>>(partial, blocks, result);

@@ -621,7 +621,119 @@ struct Kernels {
         return Tensor<T>(std::move(shape), std::move(out));
     }
 
+    // ---- slices: `narrow`, `write_slice`, `concat` (view.rs, tensor.rs:504,
+    // backend.rs:157-173) ----
+
+    static std::vector<size_t> strides_of(const Shape& shape) {
+        std::vector<size_t> strides(shape.size());
+        size_t step = 1;
+        for (size_t axis = shape.size(); axis-- > 0;) {
+            strides[axis] = step;
+            step *= shape[axis];
+        }
+        return strides;
+    }
+    static void check_range(const Shape& shape, size_t axis, size_t start, size_t len, const char* operation) {
+        if (axis >= shape.size() || start > shape[axis] || len > shape[axis] - start) {
+            throw std::invalid_argument(std::string(operation) + ": " + std::to_string(start) + ".." +
+                                        std::to_string(start + len) + " is out of range for axis " +
+                                        std::to_string(axis) + " of shape " + shape_text(shape));
+        }
+    }
+    // Elements `start..start + len` of `axis`, copied out.
+    static Tensor<T> narrow(const Tensor<T>& a, size_t axis, size_t start, size_t len) {
+        check_range(a.shape(), axis, start, len, "narrow");
+        const std::vector<size_t> strides = strides_of(a.shape());
+        Shape shape = a.shape();
+        shape[axis] = len;
+        tc_strided from{};
+        from.offset = start * strides[axis];
+        for (size_t k = 0; k < strides.size(); k++) from.strides[k] = strides[k];
+        return copy_through(a, shape, from);
+    }
+    // `Tensor::write_slice` (tensor.rs:504): `delta` written over elements
+    // `start..` of `axis` of `target`, in place (`Backend::strided_write`).
+    static void write_slice(Tensor<T>& target, size_t axis, size_t start, const Tensor<T>& delta) {
+        if (delta.rank() != target.rank()) {
+            throw std::invalid_argument("write_slice: shape " + shape_text(delta.shape()) + " into " +
+                                        shape_text(target.shape()));
+        }
+        check_range(target.shape(), axis, start, delta.shape()[axis], "write_slice");
+        if (delta.len() == 0) return;
+        const tc_region place = slice_region(delta, target.shape(), axis, start);
+        check(tc_strided_write(sizeof(T), target.storage().ptr(), target.len(), &place));
+    }
+    // The elements `start..` of `axis` of `current` plus `delta`, reading
+    // `current` in place: one strided kernel, no copy of the slice.
+    static Tensor<T> narrow_add(const Tensor<T>& current, size_t axis, size_t start, const Tensor<T>& delta) {
+        if (delta.rank() != current.rank()) {
+            throw std::invalid_argument("narrow: shape " + shape_text(delta.shape()) + " against " +
+                                        shape_text(current.shape()));
+        }
+        check_range(current.shape(), axis, start, delta.shape()[axis], "narrow");
+        Storage<T> out(delta.len());
+        if (out.len()) {
+            const tc_region place = slice_region(delta, current.shape(), axis, start);
+            const std::vector<uint64_t> dims(delta.shape().begin(), delta.shape().end());
+            check(tc_strided_binary(dtype, TC_PAIR_ARITHMETIC, TC_ADD, static_cast<uint32_t>(delta.rank()),
+                                    dims.data(), current.storage().ptr(), current.len(), &place.to,
+                                    delta.storage().ptr(), delta.len(), &place.from, out.ptr()));
+        }
+        return Tensor<T>(delta.shape(), std::move(out));
+    }
+    // `Tensor::concat` (tensor.rs): the pieces joined along `axis`, one
+    // assemble of every piece's region.
+    static Tensor<T> concat(const std::vector<const Tensor<T>*>& pieces, size_t axis) {
+        if (pieces.empty()) throw std::invalid_argument("concat: there are no tensors to join");
+        Shape shape = pieces[0]->shape();
+        if (axis >= shape.size()) throw std::invalid_argument("concat: axis out of range for " + shape_text(shape));
+        shape[axis] = 0;
+        const Shape off_axis = shape;
+        for (const Tensor<T>* piece : pieces) {
+            Shape other = piece->shape();
+            if (other.size() != shape.size()) {
+                throw std::invalid_argument("concat: shapes " + shape_text(pieces[0]->shape()) + " and " +
+                                            shape_text(other) + " differ off axis " + std::to_string(axis));
+            }
+            const size_t extent = other[axis];
+            other[axis] = 0;
+            if (other != off_axis) {
+                throw std::invalid_argument("concat: shapes " + shape_text(pieces[0]->shape()) + " and " +
+                                            shape_text(piece->shape()) + " differ off axis " + std::to_string(axis));
+            }
+            shape[axis] += extent;
+        }
+        Storage<T> out(element_count(shape));
+        std::vector<tc_region> regions;
+        size_t start = 0;
+        for (const Tensor<T>* piece : pieces) {
+            if (piece->len()) regions.push_back(slice_region(*piece, shape, axis, start));
+            start += piece->shape()[axis];
+        }
+        if (out.len() && !regions.empty()) {
+            check(tc_assemble(sizeof(T), out.ptr(), out.len(), regions.data(), static_cast<uint32_t>(regions.size())));
+        }
+        return Tensor<T>(std::move(shape), std::move(out));
+    }
+
    private:
+    // `delta` (row-major) as the block at `start` of `axis` in a row-major
+    // tensor of `shape`: `from` reads `delta`, `to` addresses the block.
+    static tc_region slice_region(const Tensor<T>& delta, const Shape& shape, size_t axis, size_t start) {
+        tc_region region{};
+        region.source = delta.storage().ptr();
+        region.source_len = delta.len();
+        region.rank = static_cast<uint32_t>(delta.rank());
+        const std::vector<size_t> from = strides_of(delta.shape());
+        const std::vector<size_t> to = strides_of(shape);
+        for (size_t k = 0; k < delta.rank(); k++) {
+            region.shape[k] = delta.shape()[k];
+            region.from.strides[k] = from[k];
+            region.to.strides[k] = to[k];
+        }
+        region.to.offset = start * to[axis];
+        return region;
+    }
     static Tensor<T> copy_through(const Tensor<T>& a, const Shape& shape, const tc_strided& from) {
         Storage<T> out(element_count(shape));
         if (out.len()) {

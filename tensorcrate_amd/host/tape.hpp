@@ -504,6 +504,22 @@ Tensor<T> sum_to_shape(const Tensor<T>& gradient, const Shape& shape) {
     return std::move(summed).reshape(shape);
 }
 
+// `Node::accumulate_slice` (tape/tensor.rs:55-82): `delta` added into the
+// elements `start..` of `axis` of the node's adjoint.  With no adjoint yet
+// the slice is written into zeros; otherwise the slice of the adjoint plus
+// `delta` is written back in place, so the rest of it is never touched.
+template <typename T>
+void accumulate_slice(Node<Tensor<T>>& node, size_t axis, size_t start, const Tensor<T>& delta) {
+    if (node.adjoint) {
+        Tensor<T> sum = K<T>::narrow_add(*node.adjoint, axis, start, delta);
+        K<T>::write_slice(*node.adjoint, axis, start, sum);
+    } else {
+        Tensor<T> zeros = Tensor<T>::filled(node.get().shape(), T(0));
+        K<T>::write_slice(zeros, axis, start, delta);
+        node.adjoint.emplace(std::move(zeros));
+    }
+}
+
 // `Correction` (statistics/mod.rs:80-101): the variance's divisor n, or
 // n − 1 for a sample; too few elements leave it undefined.
 enum class Correction { Population, Sample };
@@ -669,6 +685,126 @@ class TensorVar : public Var<Tensor<T>> {
         std::swap(axes[ab[0]], axes[bb[0]]);
         return permute(axes);
     }
+    // `squeeze` / `unsqueeze` (:351-370): reshapes that drop or add an
+    // axis of extent 1.
+    TensorVar squeeze(long axis) const {
+        const size_t k = K<T>::resolve_axes({axis}, shape(), "squeeze")[0];
+        if (shape()[k] != 1) {
+            throw std::invalid_argument("squeeze: axis " + std::to_string(axis) + " of shape " + shape_text(shape()) +
+                                        " is not of extent 1");
+        }
+        Shape s = shape();
+        s.erase(s.begin() + static_cast<long>(k));
+        return reshape(s);
+    }
+    TensorVar unsqueeze(long axis) const {
+        const long rank = static_cast<long>(this->rank()) + 1;
+        const long k = axis < 0 ? axis + rank : axis;
+        if (k < 0 || k >= rank) {
+            throw std::invalid_argument("unsqueeze: axis " + std::to_string(axis) + " is out of range for shape " +
+                                        shape_text(shape()) + " (" + std::to_string(rank) + " axes)");
+        }
+        Shape s = shape();
+        s.insert(s.begin() + k, 1);
+        return reshape(s);
+    }
+
+    // `narrow` (:422-435): the adjoint written back where the slice came
+    // from (`accumulate_slice`); `slice` takes a range of the same axis.
+    TensorVar narrow(long axis, size_t start, size_t len) const {
+        const size_t k = K<T>::resolve_axes({axis}, shape(), "narrow")[0];
+        auto parent = this->node_;
+        return this->template record<X>(K<T>::narrow(this->value(), k, start, len), [parent, k, start](const X& adjoint) {
+            accumulate_slice(*parent, k, start, adjoint);
+        });
+    }
+    TensorVar slice(long axis, size_t start, size_t end) const {
+        if (end < start) throw std::invalid_argument("slice: the range " + std::to_string(start) + ".." +
+                                                     std::to_string(end) + " runs backwards");
+        return narrow(axis, start, end - start);
+    }
+    // `select` (:448-462): index `index` of `axis`, the axis dropped.
+    TensorVar select(long axis, size_t index) const {
+        const size_t k = K<T>::resolve_axes({axis}, shape(), "select")[0];
+        if (index >= shape()[k]) {
+            throw std::invalid_argument("select: index " + std::to_string(index) + " is out of range for axis " +
+                                        std::to_string(k) + " of shape " + shape_text(shape()));
+        }
+        Shape dropped = shape();
+        dropped.erase(dropped.begin() + static_cast<long>(k));
+        auto parent = this->node_;
+        X value = K<T>::narrow(this->value(), k, index, 1).reshape(dropped);
+        return this->template record<X>(std::move(value), [parent, k, index](const X& adjoint) {
+            Shape kept = adjoint.shape();
+            kept.insert(kept.begin() + static_cast<long>(k), 1);
+            accumulate_slice(*parent, k, index, adjoint.duplicate().reshape(kept));
+        });
+    }
+    // `split` (:464-487): consecutive narrows of `sizes`, which must cover
+    // the axis; `chunk` (:489-500): `parts` equal pieces.
+    std::vector<TensorVar> split(long axis, const std::vector<size_t>& sizes) const {
+        const size_t k = K<T>::resolve_axes({axis}, shape(), "split")[0];
+        size_t total = 0;
+        for (size_t size : sizes) total += size;
+        if (total != shape()[k]) {
+            throw std::invalid_argument("split: sizes adding to " + std::to_string(total) + " for axis " +
+                                        std::to_string(k) + " of shape " + shape_text(shape()));
+        }
+        std::vector<TensorVar> pieces;
+        size_t start = 0;
+        for (size_t size : sizes) {
+            pieces.push_back(narrow(static_cast<long>(k), start, size));
+            start += size;
+        }
+        return pieces;
+    }
+    std::vector<TensorVar> chunk(long axis, size_t parts) const {
+        const size_t k = K<T>::resolve_axes({axis}, shape(), "chunk")[0];
+        if (parts == 0 || shape()[k] % parts != 0) {
+            throw std::invalid_argument("chunk: axis " + std::to_string(k) + " of shape " + shape_text(shape()) +
+                                        " does not split into " + std::to_string(parts) + " equal parts");
+        }
+        return split(static_cast<long>(k), std::vector<size_t>(parts, shape()[k] / parts));
+    }
+    // `concat` (:502-533): each piece's adjoint is its block of the joined
+    // adjoint.
+    static TensorVar concat(const std::vector<TensorVar>& pieces, long axis) {
+        if (pieces.empty()) throw std::invalid_argument("concat: there are no tensors to join");
+        const TensorVar& first = pieces[0];
+        std::vector<const X*> values;
+        std::vector<std::shared_ptr<Node<X>>> nodes;
+        for (const TensorVar& piece : pieces) {
+            first.assert_same_tape(piece.tape());
+            values.push_back(&piece.value());
+            nodes.push_back(piece.node_);
+        }
+        const size_t k = K<T>::resolve_axes({axis}, first.shape(), "concat")[0];
+        return first.template record<X>(K<T>::concat(values, k), [nodes, k](const X& adjoint) {
+            size_t start = 0;
+            for (const auto& node : nodes) {
+                const size_t len = node->get().shape()[k];
+                node->accumulate(K<T>::narrow(adjoint, k, start, len));
+                start += len;
+            }
+        });
+    }
+    // `stack` (:535-553): the pieces joined along a new axis, each lifted
+    // by `unsqueeze` and then one `concat`; the adjoints are the same blocks
+    // the reference's `select`s give.
+    static TensorVar stack(const std::vector<TensorVar>& pieces, long axis) {
+        if (pieces.empty()) throw std::invalid_argument("stack: there are no tensors to stack");
+        std::vector<TensorVar> lifted;
+        for (const TensorVar& piece : pieces) {
+            if (piece.shape() != pieces[0].shape()) {
+                throw std::invalid_argument("stack: shapes " + shape_text(pieces[0].shape()) + " and " +
+                                            shape_text(piece.shape()) + " differ");
+            }
+            lifted.push_back(piece.unsqueeze(axis));
+        }
+        const long rank = static_cast<long>(pieces[0].rank()) + 1;
+        return concat(lifted, axis < 0 ? axis + rank : axis);
+    }
+
     // `broadcast_to` (:555-570): the adjoint summed back to this shape.
     TensorVar broadcast_to(const Shape& shape) const {
         auto parent = this->node_;

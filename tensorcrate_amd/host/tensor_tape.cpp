@@ -136,9 +136,16 @@ int tch_tape_unary(tch_tape* t, uint32_t op, uint32_t a, float first, float seco
 int tch_tape_layout(tch_tape* t, uint32_t op, uint32_t a, uint32_t count, const int64_t* values, uint32_t* out) {
     return guarded([&] {
         const TensorVar<float>& x = t->tensor(a);
+        const bool axis_first = op == TCH_NARROW || op == TCH_SELECT || op == TCH_SLICE || op == TCH_SQUEEZE ||
+                                op == TCH_UNSQUEEZE;
+        const uint32_t fixed[] = {0, 0, 2, 0, 3, 2, 3, 1, 1};
+        if (op < sizeof(fixed) / sizeof(fixed[0]) && fixed[op] && count != fixed[op]) {
+            throw std::invalid_argument("tape: layout operation " + std::to_string(op) + " takes " +
+                                        std::to_string(fixed[op]) + " values, not " + std::to_string(count));
+        }
         Shape dims;
         for (uint32_t k = 0; k < count; k++) {
-            if (values[k] < 0 && op != TCH_TRANSPOSE) {
+            if (values[k] < 0 && op != TCH_TRANSPOSE && !(axis_first && k == 0)) {
                 throw std::invalid_argument("tape: a negative extent or axis " + std::to_string(values[k]));
             }
             dims.push_back(static_cast<size_t>(values[k]));
@@ -147,10 +154,12 @@ int tch_tape_layout(tch_tape* t, uint32_t op, uint32_t a, uint32_t count, const 
             case TCH_RESHAPE: *out = t->add(x.reshape(dims)); break;
             case TCH_PERMUTE: *out = t->add(x.permute(dims)); break;
             case TCH_BROADCAST_TO: *out = t->add(x.broadcast_to(dims)); break;
-            case TCH_TRANSPOSE:
-                if (count != 2) throw std::invalid_argument("transpose: two axes, not " + std::to_string(count));
-                *out = t->add(x.transpose(values[0], values[1]));
-                break;
+            case TCH_TRANSPOSE: *out = t->add(x.transpose(values[0], values[1])); break;
+            case TCH_NARROW: *out = t->add(x.narrow(values[0], dims[1], dims[2])); break;
+            case TCH_SELECT: *out = t->add(x.select(values[0], dims[1])); break;
+            case TCH_SLICE: *out = t->add(x.slice(values[0], dims[1], dims[2])); break;
+            case TCH_SQUEEZE: *out = t->add(x.squeeze(values[0])); break;
+            case TCH_UNSQUEEZE: *out = t->add(x.unsqueeze(values[0])); break;
             default: throw std::invalid_argument("tape: no layout operation " + std::to_string(op));
         }
     });
@@ -172,6 +181,29 @@ int tch_tape_reduce(tch_tape* t, uint32_t op, uint32_t a, uint32_t count, const 
             case TCH_SUM: *out = t->add(x.sum()); break;
             case TCH_MEAN: *out = t->add(x.mean()); break;
             default: throw std::invalid_argument("tape: no reduction " + std::to_string(op));
+        }
+    });
+}
+
+int tch_tape_split(tch_tape* t, uint32_t a, int64_t axis, uint32_t count, const uint64_t* sizes, uint32_t* out) {
+    return guarded([&] {
+        const TensorVar<float>& x = t->tensor(a);
+        std::vector<TensorVar<float>> pieces =
+            sizes ? x.split(axis, std::vector<size_t>(sizes, sizes + count)) : x.chunk(axis, count);
+        for (size_t k = 0; k < pieces.size(); k++) out[k] = t->add(std::move(pieces[k]));
+    });
+}
+
+int tch_tape_join(tch_tape* t, uint32_t op, uint32_t count, const uint32_t* handles, int64_t axis, uint32_t* out) {
+    return guarded([&] {
+        std::vector<TensorVar<float>> pieces;
+        for (uint32_t k = 0; k < count; k++) pieces.push_back(t->tensor(handles[k]));
+        if (op == TCH_CONCAT) {
+            *out = t->add(TensorVar<float>::concat(pieces, axis));
+        } else if (op == TCH_STACK) {
+            *out = t->add(TensorVar<float>::stack(pieces, axis));
+        } else {
+            throw std::invalid_argument("tape: no join " + std::to_string(op));
         }
     });
 }

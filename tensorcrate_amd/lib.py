@@ -389,6 +389,8 @@ HOST_SIGNATURES = {
     "tch_tape_unary": [vp, u32, u32, f32, f32, ctypes.POINTER(u32)],
     "tch_tape_layout": [vp, u32, u32, u32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(u32)],
     "tch_tape_reduce": [vp, u32, u32, u32, ctypes.POINTER(ctypes.c_int64), i32, ctypes.POINTER(u32)],
+    "tch_tape_split": [vp, u32, ctypes.c_int64, u32, ctypes.POINTER(u64), ctypes.POINTER(u32)],
+    "tch_tape_join": [vp, u32, u32, ctypes.POINTER(u32), ctypes.c_int64, ctypes.POINTER(u32)],
     "tch_tape_add_scalars": [vp, u32, u32, ctypes.POINTER(u32)],
     "tch_tape_backward": [vp, u32, vp],
     "tch_tape_shape": [vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u64)],
@@ -479,7 +481,9 @@ TAPE_BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3, "maximum": 4, "minimum": 
 TAPE_UNARY = {"clamp_min": 0, "clamp_max": 1, "clamp": 2, "relu": 3, "abs": 4, "neg": 5, "scale": 6, "shift": 7,
               "power_scalar": 8, "power_scalar_left": 9, "contiguous": 10}
 TAPE_ANALYTIC = 32
-TAPE_LAYOUT = {"reshape": 0, "permute": 1, "transpose": 2, "broadcast_to": 3}
+TAPE_LAYOUT = {"reshape": 0, "permute": 1, "transpose": 2, "broadcast_to": 3, "narrow": 4, "select": 5, "slice": 6,
+               "squeeze": 7, "unsqueeze": 8}
+TAPE_JOIN = {"concat": 0, "stack": 1}
 TAPE_REDUCE = {"sum_axes": 0, "mean_axes": 1, "var_axes": 2, "var_axes_sample": 3, "max_axes": 4, "min_axes": 5,
                "sum": 6, "mean": 7}
 
@@ -503,6 +507,10 @@ class Tape:
         values = np.array(values, np.float32, order="C")  # keeps a 0-d shape, which ascontiguousarray does not
         dims = (u64 * max(values.ndim, 1))(*values.shape)
         return self._out("tch_tape_tensor", values.ndim, dims, values.ctypes.data)
+
+    def join(self, op: str, pieces, axis: int) -> "TapeVar":
+        handles = (u32 * max(len(pieces), 1))(*[p.handle for p in pieces])
+        return self._out("tch_tape_join", TAPE_JOIN[op], len(pieces), handles, axis)
 
     def zero_grad(self) -> None:
         host_call("tch_tape_zero_grad", self.handle)
@@ -570,6 +578,14 @@ class TapeVar:
     def reduce(self, op: str, axes=(), keep_dims: bool = False) -> "TapeVar":
         count, array = _axes(axes)
         return self.tape._out("tch_tape_reduce", TAPE_REDUCE[op], self.handle, count, array, int(keep_dims))
+
+    def split(self, axis: int, sizes=None, parts: int = 0) -> list["TapeVar"]:
+        """Pieces of ``sizes`` along ``axis``, or ``parts`` equal ones."""
+        count = len(sizes) if sizes is not None else parts
+        out = (u32 * max(count, 1))()
+        array = (u64 * max(count, 1))(*sizes) if sizes is not None else None
+        host_call("tch_tape_split", self.tape.handle, self.handle, axis, count, array, out)
+        return [TapeVar(self.tape, out[k]) for k in range(count)]
 
     def add_scalar(self, other: "TapeVar") -> "TapeVar":
         return self.tape._out("tch_tape_add_scalars", self.handle, other.handle)

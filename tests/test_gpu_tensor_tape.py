@@ -11,8 +11,8 @@ for f32 against f64 (tensor_autodiff.rs:388-391).  The inputs are rounded to
 f32 first, so both sides see the same values.  The harness itself is pinned
 on the CPU against closed forms (`test_the_difference_harness_...`).
 
-Not covered: narrow, slice, select, split, chunk, concat, stack and the
-vector round trip — operations this tape does not record.
+Not covered: the vector round trip (`to_vector`), which this tape does
+not record.
 """
 
 import numpy as np
@@ -65,7 +65,23 @@ class Np:
             return Np(np.transpose(x, values))
         if op == "transpose":
             return Np(np.swapaxes(x, *values))
+        if op == "narrow":
+            axis, start, length = values
+            return Np(np.take(x, range(start, start + length), axis=axis))
+        if op == "select":
+            return Np(np.take(x, values[1], axis=values[0]))
+        if op == "slice":
+            axis, start, end = values
+            return Np(np.take(x, range(start, end), axis=axis))
+        if op == "squeeze":
+            return Np(np.squeeze(x, axis=values[0]))
+        if op == "unsqueeze":
+            return Np(np.expand_dims(x, values[0]))
         return Np(np.broadcast_to(x, values).copy())
+
+    def split(self, axis, sizes=None, parts=0):
+        bounds = np.cumsum(sizes)[:-1] if sizes is not None else parts
+        return [Np(p) for p in np.split(self.v, bounds, axis=axis)]
 
     def reduce(self, op, axes=(), keep_dims=False):
         x = self.v
@@ -81,6 +97,14 @@ class Np:
                 "max_axes": lambda: x.max(axis=axes, keepdims=keep_dims),
                 "min_axes": lambda: x.min(axis=axes, keepdims=keep_dims)}
         return Np(fold[op]())
+
+
+def join(op, pieces, axis):
+    """`concat`/`stack` on either side of the facade."""
+    if isinstance(pieces[0], Np):
+        f = np.concatenate if op == "concat" else np.stack
+        return Np(f([p.v for p in pieces], axis=axis))
+    return pieces[0].tape.join(op, pieces, axis)
 
 
 def positive(shape, seed):
@@ -131,8 +155,32 @@ OPS = [
     ("min_axes", lambda: [x()], lambda v: v[0].reduce("min_axes", -1, True)),
     ("matrix_round_trip", lambda: [filled((2, 3, 4), 1, -1, 1), filled((4, 5), 2, -1, 1)],
      lambda v: v[0].binary(v[1], "matmul").analytic(12)),
+    ("narrowed_operand", lambda: [x(), filled((2, 1, 4, 5), 2, -1, 1)],
+     lambda v: v[0].layout("narrow", [1, 1, 1]) * v[1]),
+    ("narrow", lambda: [x()], lambda v: v[0].layout("narrow", [2, 1, 2])),
+    ("slice", lambda: [x()], lambda v: v[0].layout("slice", [-1, 1, 4])),
+    ("select", lambda: [x()], lambda v: v[0].layout("select", [1, 2])),
+    ("split", lambda: [filled((2, 3, 4, 6), 1, -1, 1)],
+     lambda v: (lambda p: p[0].reduce("sum_axes", -1, True) * p[1].analytic(12))(v[0].split(-1, sizes=[2, 4]))),
+    ("chunk", lambda: [filled((2, 3, 4, 6), 1, -1, 1)],
+     lambda v: (lambda p: (p[0] * p[1]) + p[2].analytic(0))(v[0].split(-1, parts=3))),
+    ("concat", lambda: [filled((2, 3, 4, 2), 1, -1, 1), filled((2, 3, 4, 3), 2, -1, 1)],
+     lambda v: join("concat", [v[1], v[0], v[1].unary("scale", 2.0)], -1)),
+    ("stack", lambda: [filled((2, 3, 4), 1, -1, 1), filled((2, 3, 4), 2, -1, 1)],
+     lambda v: join("stack", [v[0], v[1], v[0]], 1)),
+    ("squeeze_unsqueeze_axes", lambda: [filled((2, 1, 4), 1, -1, 1)],
+     lambda v: v[0].layout("squeeze", [1]).layout("unsqueeze", [0]).layout("unsqueeze", [-1])),
     # A tensor used twice: the second rule adds into an adjoint already there.
     ("reused_operand", lambda: [x()], lambda v: v[0].reduce("sum_axes", 1, True) + (v[0] * v[0])),
+    # The narrow's rule runs after the product's, so it adds into an adjoint
+    # that is already there (tensor_autodiff.rs:254-258).
+    ("slice_into_existing_adjoint", lambda: [x()],
+     lambda v: v[0].layout("narrow", [1, 0, 2]).reduce("sum_axes", 1, True) + (v[0] * v[0])),
+    # The product is recorded first, so the narrow's rule writes into zeros
+    # and the product's adds to that (tensor_autodiff.rs:259-264).
+    ("slice_before_other_use", lambda: [x()],
+     lambda v: (lambda square: v[0].layout("narrow", [-1, 2, 3]).analytic(8).reduce("sum_axes", -1, True) + square)(
+         v[0] * v[0])),
 ]
 
 
@@ -260,6 +308,15 @@ def test_empty_and_unit_extents_differentiate():
     ((folded + row) * row).reduce("sum").backward()
     assert empty.grad().shape == (0, 3)
     assert np.array_equal(unit.grad(), [[[2.0], [4.0], [6.0]]])
+    # Narrowing to nothing sends nothing back, into an adjoint or not.
+    x = tape.tensor(np.array([[1.0, 2.0], [3.0, 4.0]]))
+    none = x.layout("narrow", [1, 1, 0])
+    assert none.shape == (2, 0)
+    (none.reduce("sum_axes", 1, True) + x).reduce("sum").backward()
+    assert np.array_equal(x.grad(), np.ones((2, 2)))
+    after = x.unary("scale", 2.0)
+    (x.layout("narrow", [0, 2, 0]).reduce("sum_axes", 0) + after.reduce("sum_axes", 0)).reduce("sum").backward()
+    assert np.array_equal(x.grad(), np.full((2, 2), 2.0))
     tape.close()
 
 
@@ -289,4 +346,10 @@ def test_shapes_that_do_not_broadcast_are_rejected():
         a.reduce("sum_axes", [1, -1])
     with pytest.raises(lib.HipError, match=r"reshape: shape \[2, 3\] holds 6 elements"):
         a.layout("reshape", [4])
+    with pytest.raises(lib.HipError, match=r"narrow: 2\.\.4 is out of range for axis 1 of shape \[2, 3\]"):
+        a.layout("narrow", [1, 2, 2])
+    with pytest.raises(lib.HipError, match=r"chunk: axis 1 of shape \[2, 3\] does not split into 2 equal parts"):
+        a.split(1, parts=2)
+    with pytest.raises(lib.HipError, match=r"concat: shapes \[2, 3\] and \[4\] differ off axis 0"):
+        tape.join("concat", [a, b], 0)
     tape.close()
