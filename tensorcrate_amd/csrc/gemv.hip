@@ -4,8 +4,9 @@
 // Both stream the matrix once from HBM, so both are bandwidth kernels:
 //  - matvec: one wave per row, lanes reading 16 bytes of the row at a time,
 //    a 64-lane shuffle tree for the dot product.  The vector stays hot in L2.
-//  - vecmat: lanes on neighbouring columns, 16 bytes of a row each, so every
-//    row read is one coalesced run; four row groups split the rows inside a
+//  - vecmat: lanes on neighbouring columns, 16 bytes of a row at a time, so
+//    every row read is one coalesced run (up to 4 KiB per wave when the
+//    rows are wide); four row groups split the rows inside a
 //    block, and tall matrices split their rows across blocks, combined in
 //    order by a second pass, so the result does not depend on timing.
 // Accumulation is f32, rounded once to the element type (compact.rs:223-231).
@@ -76,86 +77,141 @@ __global__ void __launch_bounds__(256) matvec_kernel(const S* __restrict__ m, co
 
 constexpr int kGroups = 4;
 
-// Block: 64 lanes x kGroups row groups over `V`-column packs; `split` picks
-// the rows.  With one split the block finishes its columns; otherwise it
-// writes f32 partial sums to `partial[split][col]`.
-template <typename S, int V>
+// Block: 64 lanes x kGroups row groups.  A lane owns W packs of V columns,
+// 64 packs apart, so one wave reads 64·V·W contiguous columns of a row (4 KiB
+// for f32 at V = W = 4); `split` picks the rows.  With one split the block
+// finishes its columns; otherwise it writes f32 partial sums to
+// `partial[split][col]`.
+template <typename S, int V, int W>
 __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, const S* __restrict__ m,
                                                      S* __restrict__ y, float* __restrict__ partial,
                                                      uint64_t rows, uint64_t cols, uint64_t tiles,
                                                      uint64_t splits, uint64_t per_split) {
     using E = Elem<S>;
-    __shared__ float stage[kGroups][64 * V];
+    constexpr int kTile = 64 * V * W;
+    __shared__ float stage[kGroups][kTile];
     const int lane = threadIdx.x % 64;
     const int group = threadIdx.x / 64;
     const uint64_t tile = blockIdx.x % tiles;
     const uint64_t split = blockIdx.x / tiles;
-    const uint64_t col0 = (tile * 64 + lane) * V;
+    const uint64_t base = tile * kTile + lane * V;
     const uint64_t begin = split * per_split;
     const uint64_t end = min(begin + per_split, rows);
     const uint64_t span = end > begin ? end - begin : 0;
     const uint64_t per_group = (span + kGroups - 1) / kGroups;
     const uint64_t first = min(begin + group * per_group, end);
     const uint64_t last = min(first + per_group, end);
-    float acc[V];
+    float acc[W][V];
 #pragma unroll
-    for (int k = 0; k < V; k++) acc[k] = 0.0f;
-    if (col0 < cols) {
-        uint64_t r = first;
-        if (V > 1) {
-            // Eight rows' packs in flight per lane before any is used.
-            for (; r + 8 <= last; r += 8) {
-                Pack<S> p[8];
-                float w[8];
+    for (int u = 0; u < W; u++) {
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    p[u] = *reinterpret_cast<const Pack<S>*>(m + (r + u) * cols + col0);
-                    w[u] = E::widen(v[r + u]);
+        for (int k = 0; k < V; k++) acc[u][k] = 0.0f;
+    }
+    // Columns are whole packs (cols % V == 0 when V > 1), so a pack is either
+    // inside the matrix or wholly past its last column.
+    bool live[W];
+#pragma unroll
+    for (int u = 0; u < W; u++) live[u] = base + u * 64 * V < cols;
+    uint64_t r = first;
+    if (V > 1) {
+        // Two rows' packs in flight per lane before any is used: measured at
+        // 8192 x 8192 f32, four or eight rows in flight were slower (66% and
+        // 61% of HBM against 70%).
+        constexpr int R = 2;
+        for (; r + R <= last; r += R) {
+            Pack<S> p[R][W];
+            float w[R];
+#pragma unroll
+            for (int q = 0; q < R; q++) {
+                w[q] = E::widen(v[r + q]);
+#pragma unroll
+                for (int u = 0; u < W; u++) {
+                    if (live[u]) p[q][u] = *reinterpret_cast<const Pack<S>*>(m + (r + q) * cols + base + u * 64 * V);
                 }
+            }
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
+            for (int q = 0; q < R; q++) {
 #pragma unroll
-                    for (int k = 0; k < V; k++) acc[k] += w[u] * E::widen(p[u].v[k]);
+                for (int u = 0; u < W; u++) {
+                    if (!live[u]) continue;
+#pragma unroll
+                    for (int k = 0; k < V; k++) acc[u][k] += w[q] * E::widen(p[q][u].v[k]);
                 }
             }
         }
-        for (; r < last; r++) {
-            const float w = E::widen(v[r]);
-            if (V > 1) {
-                Pack<S> p = *reinterpret_cast<const Pack<S>*>(m + r * cols + col0);
+    }
+    for (; r < last; r++) {
+        const float w = E::widen(v[r]);
 #pragma unroll
-                for (int k = 0; k < V; k++) acc[k] += w * E::widen(p.v[k]);
+        for (int u = 0; u < W; u++) {
+            if (!live[u]) continue;
+            if (V > 1) {
+                Pack<S> p = *reinterpret_cast<const Pack<S>*>(m + r * cols + base + u * 64 * V);
+#pragma unroll
+                for (int k = 0; k < V; k++) acc[u][k] += w * E::widen(p.v[k]);
             } else {
-                acc[0] += w * E::widen(m[r * cols + col0]);
+                acc[u][0] += w * E::widen(m[r * cols + base + u * 64]);
             }
         }
     }
 #pragma unroll
-    for (int k = 0; k < V; k++) stage[group][lane * V + k] = acc[k];
+    for (int u = 0; u < W; u++) {
+#pragma unroll
+        for (int k = 0; k < V; k++) stage[group][u * 64 * V + lane * V + k] = acc[u][k];
+    }
     __syncthreads();
-    if (group == 0 && col0 < cols) {
+    if (group == 0) {
 #pragma unroll
-        for (int k = 0; k < V; k++) {
-            float total = stage[0][lane * V + k];
+        for (int u = 0; u < W; u++) {
+            if (!live[u]) continue;
+            const uint64_t col = base + u * 64 * V;
 #pragma unroll
-            for (int g = 1; g < kGroups; g++) total += stage[g][lane * V + k];
-            if (splits == 1) {
-                y[col0 + k] = E::narrow(total);
-            } else {
-                partial[split * cols + col0 + k] = total;
+            for (int k = 0; k < V; k++) {
+                float total = stage[0][u * 64 * V + lane * V + k];
+#pragma unroll
+                for (int g = 1; g < kGroups; g++) total += stage[g][u * 64 * V + lane * V + k];
+                if (splits == 1) {
+                    y[col + k] = E::narrow(total);
+                } else {
+                    partial[split * cols + col + k] = total;
+                }
             }
         }
     }
 }
 
+// The splits' partial sums of 64 columns a block: lane = column, each of
+// the four waves folding a quarter of the splits in order (eight loads in
+// flight), then the quarters in order, so the sum does not depend on timing.
 template <typename S>
 __global__ void __launch_bounds__(256) vecmat_combine_kernel(const float* __restrict__ partial, S* __restrict__ y,
                                                              uint64_t cols, uint64_t splits) {
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t c = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < cols; c += stride) {
-        float total = partial[c];
-        for (uint64_t k = 1; k < splits; k++) total += partial[k * cols + c];
-        y[c] = Elem<S>::narrow(total);
+    __shared__ float quarter[kGroups][64];
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * 64 + lane;
+    const uint64_t per_wave = (splits + kGroups - 1) / kGroups;
+    const uint64_t k0 = min(wave * per_wave, splits);
+    const uint64_t k1 = min(k0 + per_wave, splits);
+    float total = 0.0f;
+    if (c < cols) {
+        uint64_t k = k0;
+        for (; k + 8 <= k1; k += 8) {
+            float x[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) x[u] = partial[(k + u) * cols + c];
+#pragma unroll
+            for (int u = 0; u < 8; u++) total += x[u];
+        }
+        for (; k < k1; k++) total += partial[k * cols + c];
+    }
+    quarter[wave][lane] = total;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        float sum = quarter[0][lane];
+#pragma unroll
+        for (int g = 1; g < kGroups; g++) sum += quarter[g][lane];
+        y[c] = Elem<S>::narrow(sum);
     }
 }
 
@@ -176,9 +232,9 @@ int matvec_typed(bool accumulate, uint64_t rows, uint64_t cols, const void* m, c
     return check_launch("matvec");
 }
 
-template <typename S, int V>
+template <typename S, int V, int W>
 int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, hipStream_t s) {
-    const uint64_t tiles = (cols + 64 * V - 1) / (64 * V);
+    const uint64_t tiles = (cols + 64 * V * W - 1) / (64 * V * W);
     const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
     uint64_t splits = 1;
     if (tiles < want) {
@@ -196,11 +252,11 @@ int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, hi
         if (status != TC_OK) return status;
         partial = static_cast<float*>(scratch);
     }
-    vecmat_kernel<S, V><<<static_cast<uint32_t>(tiles * splits), 256, 0, s>>>(v, m, y, partial, rows, cols, tiles,
-                                                                              splits, per_split);
+    vecmat_kernel<S, V, W><<<static_cast<uint32_t>(tiles * splits), 256, 0, s>>>(v, m, y, partial, rows, cols,
+                                                                                 tiles, splits, per_split);
     int status = check_launch("vecmat");
     if (status == TC_OK && splits > 1) {
-        vecmat_combine_kernel<S><<<grid_for(cols, 256), 256, 0, s>>>(partial, y, cols, splits);
+        vecmat_combine_kernel<S><<<static_cast<uint32_t>((cols + 63) / 64), 256, 0, s>>>(partial, y, cols, splits);
         status = check_launch("vecmat");
     }
     if (partial != nullptr) tc_free(partial);
@@ -215,8 +271,12 @@ int vecmat_typed(uint64_t rows, uint64_t cols, const void* v, const void* m, voi
     const S* pm = static_cast<const S*>(m);
     S* py = static_cast<S*>(y);
     constexpr int V = Pack<S>::N;
-    if (cols % V == 0 && aligned16(m)) return launch_vecmat<S, V>(pv, pm, py, rows, cols, s);
-    return launch_vecmat<S, 1>(pv, pm, py, rows, cols, s);
+    // One pack a lane: measured at 8192 x 8192 f32, two or four packs a lane
+    // (2 or 4 KiB runs of a row per wave) were slower, 68% and 66% of HBM
+    // against 70%, their extra row splits costing more than the longer runs
+    // gain.
+    if (cols % V == 0 && aligned16(m)) return launch_vecmat<S, V, 1>(pv, pm, py, rows, cols, s);
+    return launch_vecmat<S, 1, 1>(pv, pm, py, rows, cols, s);
 }
 
 }  // namespace

@@ -120,7 +120,7 @@ def test_an_empty_inner_dimension_gives_zeros_or_the_addend():
 def test_matvec_vecmat():
     rng = np.random.default_rng(13)
     for kind in [lib.F32, lib.BF16, lib.F16]:
-        for rows, cols in [(1, 1), (37, 53), (1000, 64), (8, 8192), (513, 1031)]:
+        for rows, cols in [(1, 1), (37, 53), (1000, 64), (8, 8192), (513, 1031), (300, 5000), (64, 8200), (2000, 4096)]:
             m = to_kind(rng.uniform(-1, 1, (rows, cols)), kind)
             v = to_kind(rng.uniform(-1, 1, cols), kind)
             w = to_kind(rng.uniform(-1, 1, rows), kind)
