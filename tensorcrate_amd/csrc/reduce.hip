@@ -814,14 +814,32 @@ __global__ void __launch_bounds__(256) total_kernel(const S* __restrict__ a, con
     }
 }
 
+// 256 threads, each folding every 256th partial with four loads in flight,
+// then the waves in order: a fixed order, so the result does not depend on
+// timing, and a few load round trips rather than count / 64.
 template <uint32_t OP>
-__global__ void __launch_bounds__(64) finish_total_kernel(const float* __restrict__ partial, uint32_t count,
-                                                          float* __restrict__ result) {
+__global__ void __launch_bounds__(256) finish_total_kernel(const float* __restrict__ partial, uint32_t count,
+                                                           float* __restrict__ result) {
     using P = Fold<OP>;
+    __shared__ float stage[4];
     float s = P::init();
-    for (uint32_t i = threadIdx.x; i < count; i += 64) P::add(s, partial[i], 0);
+    uint32_t i = threadIdx.x;
+    for (; i + 3 * 256 < count; i += 4 * 256) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) x[u] = partial[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < 4; u++) P::add(s, x[u], 0);
+    }
+    for (; i < count; i += 256) P::add(s, partial[i], 0);
     s = wave_reduce<P>(s);
-    if (threadIdx.x == 0) *result = s;
+    if (threadIdx.x % 64 == 0) stage[threadIdx.x / 64] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = stage[0];
+        for (int w = 1; w < 4; w++) t = P::merge(t, stage[w]);
+        *result = t;
+    }
 }
 
 template <typename S, uint32_t OP, bool DOT>
@@ -845,7 +863,7 @@ int total(const void* a, const void* b, uint64_t n, float* result, const char* w
     }
     status = check_launch(what);
     if (status == TC_OK) {
-        finish_total_kernel<OP><<<1, 64, 0, s>>>(partial, blocks, result);
+        finish_total_kernel<OP><<<1, 256, 0, s>>>(partial, blocks, result);
         status = check_launch(what);
     }
     tc_free(scratch);
