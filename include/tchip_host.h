@@ -66,10 +66,13 @@ typedef struct tch_tape tch_tape;
 
 /* Binary operations, broadcasting (tape/tensor.rs:126-250);  TCH_MATMUL is
  * the last axis of `a` times the k x n tensor `b`, through `to_matrix`,
- * `MatrixVar::matmul` and `to_tensor` (tape/tensor.rs:703-761). */
+ * `MatrixVar::matmul` and `to_tensor` (tape/tensor.rs:703-761);
+ * TCH_VECTOR_MUL the elementwise product of two tensors of one length
+ * through `to_vector`, `VectorVar`'s product and `to_tensor` back to `a`'s
+ * shape (tape/tensor.rs:733-778). */
 typedef enum tch_binary {
     TCH_ADD = 0, TCH_SUB = 1, TCH_MUL = 2, TCH_DIV = 3,
-    TCH_MAXIMUM = 4, TCH_MINIMUM = 5, TCH_POWER = 6, TCH_MATMUL = 7
+    TCH_MAXIMUM = 4, TCH_MINIMUM = 5, TCH_POWER = 6, TCH_MATMUL = 7, TCH_VECTOR_MUL = 8
 } tch_binary;
 
 /* Unary operations (tape/tensor.rs:187-333); `first` and `second` are the
@@ -121,10 +124,12 @@ int tch_tape_add_scalars(tch_tape* tape, uint32_t a, uint32_t b, uint32_t* out);
 /* `backward_with` (tape/mod.rs:507-529) from `output`, seeded with `seed`
  * (one float per element of a tensor output; for a scalar, NULL seeds 1). */
 int tch_tape_backward(tch_tape* tape, uint32_t output, const float* seed);
-/* A variable's shape (rank 0 for a scalar). */
+/* A variable's shape (rank 0 for a scalar) into `shape`, which holds
+ * TC_MAX_RANK entries. */
 int tch_tape_shape(tch_tape* tape, uint32_t handle, uint32_t* rank, uint64_t* shape);
 /* A variable's value, or (`gradient` non-zero) its accumulated adjoint, a
- * zero where the last backward pass did not reach it; waits for the device. */
+ * zero where the last backward pass did not reach it, into `out`, which
+ * holds one float per element; waits for the device. */
 int tch_tape_read(tch_tape* tape, uint32_t handle, int gradient, float* out);
 /* `Tape::zero_grad` (tape/mod.rs:416-420). */
 int tch_tape_zero_grad(tch_tape* tape);

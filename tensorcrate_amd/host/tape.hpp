@@ -301,6 +301,53 @@ class VectorVar : public Var<Vector<T>> {
     // `VectorVar::outer` (tape/mod.rs:979-987): ū += Ȳ·v, v̄ += uᵀ·Ȳ.
     MatrixVar<T> outer(const VectorVar& other) const;
 
+    VectorVar operator+(const VectorVar& rhs) const { return binary(rhs, BinaryOp::Add); }
+    VectorVar operator-(const VectorVar& rhs) const { return binary(rhs, BinaryOp::Sub); }
+    VectorVar operator*(const VectorVar& rhs) const { return binary(rhs, BinaryOp::Mul); }
+    VectorVar operator/(const VectorVar& rhs) const { return binary(rhs, BinaryOp::Div); }
+
+    // `VectorVar::binary` (tape/mod.rs:764-810): the matrix rules over
+    // vectors; `Rem` is refused on the device as `MatrixVar`'s is.
+    VectorVar binary(const VectorVar& rhs, BinaryOp op) const {
+        this->assert_same_tape(rhs.tape());
+        if (op == BinaryOp::Rem) {
+            throw Error(TC_UNSUPPORTED, "Hip % could not execute on the GPU; Host fallback is disabled");
+        }
+        using V = Vector<T>;
+        auto left = this->node_;
+        auto right = rhs.node_;
+        auto apply = [](const V& a, const V& b, BinaryOp o) { return K<T>::vector_elementwise(a, b, o); };
+        return this->template record<V>(apply(this->value(), rhs.value(), op), [left, right, op, apply](const V& adjoint) {
+            switch (op) {
+                case BinaryOp::Add:
+                    left->accumulate(adjoint.duplicate());
+                    right->accumulate(adjoint.duplicate());
+                    break;
+                case BinaryOp::Sub:
+                    left->accumulate(adjoint.duplicate());
+                    right->accumulate(K<T>::vector_broadcast(adjoint, T(-1), BinaryOp::Mul, false));
+                    break;
+                case BinaryOp::Mul:
+                    left->accumulate(apply(adjoint, right->get(), BinaryOp::Mul));
+                    right->accumulate(apply(adjoint, left->get(), BinaryOp::Mul));
+                    break;
+                case BinaryOp::Div: {
+                    left->accumulate(apply(adjoint, right->get(), BinaryOp::Div));
+                    V squared = apply(right->get(), right->get(), BinaryOp::Mul);
+                    V scaled = apply(apply(adjoint, left->get(), BinaryOp::Mul), squared, BinaryOp::Div);
+                    right->accumulate(K<T>::vector_broadcast(scaled, T(-1), BinaryOp::Mul, false));
+                    break;
+                }
+                default:
+                    break;
+            }
+        });
+    }
+
+    // `VectorVar::to_tensor` (tape/tensor.rs:764-778): the elements as a
+    // tensor of `shape`; the adjoint is flattened back.
+    TensorVar<T> to_tensor(const Shape& shape) const;
+
     // `VectorVar::scale`.
     VectorVar scale(T factor) const {
         auto parent = this->node_;
@@ -883,6 +930,16 @@ class TensorVar : public Var<Tensor<T>> {
     // `TensorVar::mean` (:699-701).
     ScalarVar mean() const { return sum().scale(static_cast<float>(1.0 / static_cast<double>(len()))); }
 
+    // `TensorVar::to_vector` (tape/tensor.rs:733-742): the elements, row
+    // major, as a vector; the adjoint takes this shape back.
+    VectorVar<T> to_vector() const {
+        auto parent = this->node_;
+        Vector<T> value(this->value().duplicate().into_storage());
+        return VectorVar<T>(this->template record<Vector<T>>(std::move(value), [parent](const Vector<T>& adjoint) {
+            parent->accumulate(X(parent->get().shape(), adjoint.duplicate().into_storage()));
+        }));
+    }
+
     // `TensorVar::to_matrix` (tape/tensor.rs:703-731): the elements, row
     // major, as a rows × cols matrix; the adjoint takes this shape back.
     MatrixVar<T> to_matrix(size_t rows, size_t cols) const {
@@ -962,6 +1019,15 @@ class TensorVar : public Var<Tensor<T>> {
             });
     }
 };
+
+template <typename T>
+TensorVar<T> VectorVar<T>::to_tensor(const Shape& shape) const {
+    auto parent = this->node_;
+    Tensor<T> value = Tensor<T>(Shape{this->len()}, this->value().duplicate().into_storage()).reshape(shape);
+    return TensorVar<T>(this->template record<Tensor<T>>(std::move(value), [parent](const Tensor<T>& adjoint) {
+        parent->accumulate(Vector<T>(adjoint.duplicate().into_storage()));
+    }));
+}
 
 template <typename T>
 TensorVar<T> MatrixVar<T>::to_tensor(const Shape& shape) const {

@@ -104,6 +104,19 @@ int tch_tape_binary(tch_tape* t, uint32_t op, uint32_t a, uint32_t b, uint32_t* 
             case TCH_MINIMUM: *out = t->add(x.minimum(y)); break;
             case TCH_POWER: *out = t->add(x.power(y)); break;
             case TCH_MATMUL: *out = t->add(product(x, y)); break;
+            case TCH_VECTOR_MUL: {
+                // `to_vector`, `VectorVar`'s product, `to_tensor`: one flat
+                // variable when both operands are the same tensor, as in
+                // tests/tensor_autodiff.rs:251-254.
+                if (x.len() != y.len()) {
+                    throw std::invalid_argument("elementwise: vector lengths differ, " + std::to_string(x.len()) +
+                                                " and " + std::to_string(y.len()));
+                }
+                VectorVar<float> fa = x.to_vector();
+                VectorVar<float> fb = a == b ? fa : y.to_vector();
+                *out = t->add((fa * fb).to_tensor(x.shape()));
+                break;
+            }
             default: throw std::invalid_argument("tape: no binary operation " + std::to_string(op));
         }
     });

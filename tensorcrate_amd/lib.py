@@ -477,7 +477,8 @@ class Mlp:
 
 
 # ``tch_binary``, ``tch_unary``, ``tch_layout``, ``tch_reduction`` (include/tchip_host.h).
-TAPE_BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3, "maximum": 4, "minimum": 5, "power": 6, "matmul": 7}
+TAPE_BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3, "maximum": 4, "minimum": 5, "power": 6, "matmul": 7,
+               "vector_mul": 8}
 TAPE_UNARY = {"clamp_min": 0, "clamp_max": 1, "clamp": 2, "relu": 3, "abs": 4, "neg": 5, "scale": 6, "shift": 7,
               "power_scalar": 8, "power_scalar_left": 9, "contiguous": 10}
 TAPE_ANALYTIC = 32

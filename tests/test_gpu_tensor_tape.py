@@ -11,8 +11,7 @@ for f32 against f64 (tensor_autodiff.rs:388-391).  The inputs are rounded to
 f32 first, so both sides see the same values.  The harness itself is pinned
 on the CPU against closed forms (`test_the_difference_harness_...`).
 
-Not covered: the vector round trip (`to_vector`), which this tape does
-not record.
+Every operation of the reference's table is covered.
 """
 
 import numpy as np
@@ -38,7 +37,8 @@ class Np:
         a, b = self.v, other.v
         return Np({"add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide,
                    "maximum": np.maximum, "minimum": np.minimum, "power": np.power,
-                   "matmul": np.matmul}[op](a, b))
+                   "matmul": np.matmul,
+                   "vector_mul": lambda a, b: (a.ravel() * b.ravel()).reshape(a.shape)}[op](a, b))
 
     __add__ = lambda self, o: self.binary(o, "add")
     __sub__ = lambda self, o: self.binary(o, "sub")
@@ -170,6 +170,11 @@ OPS = [
      lambda v: join("stack", [v[0], v[1], v[0]], 1)),
     ("squeeze_unsqueeze_axes", lambda: [filled((2, 1, 4), 1, -1, 1)],
      lambda v: v[0].layout("squeeze", [1]).layout("unsqueeze", [0]).layout("unsqueeze", [-1])),
+    # tensor_autodiff.rs:251-254: flat = x.to_vector(); (flat * flat).to_tensor([4, 6]).
+    ("vector_round_trip", lambda: [filled((2, 3, 4), 1, -1, 1)],
+     lambda v: v[0].binary(v[0], "vector_mul").layout("reshape", [4, 6])),
+    ("vector_product", lambda: [filled((2, 3, 4), 1, -1, 1), positive((6, 4), 2)],
+     lambda v: v[0].binary(v[1], "vector_mul")),
     # A tensor used twice: the second rule adds into an adjoint already there.
     ("reused_operand", lambda: [x()], lambda v: v[0].reduce("sum_axes", 1, True) + (v[0] * v[0])),
     # The narrow's rule runs after the product's, so it adds into an adjoint
