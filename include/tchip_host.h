@@ -69,10 +69,11 @@ typedef struct tch_tape tch_tape;
  * `MatrixVar::matmul` and `to_tensor` (tape/tensor.rs:703-761);
  * TCH_VECTOR_MUL the elementwise product of two tensors of one length
  * through `to_vector`, `VectorVar`'s product and `to_tensor` back to `a`'s
- * shape (tape/tensor.rs:733-778). */
+ * shape (tape/tensor.rs:733-778); TCH_MATVEC the r x c tensor `a` times
+ * the length-c tensor `b` through `MatrixVar::matvec` (tape/mod.rs:1249-1257). */
 typedef enum tch_binary {
     TCH_ADD = 0, TCH_SUB = 1, TCH_MUL = 2, TCH_DIV = 3,
-    TCH_MAXIMUM = 4, TCH_MINIMUM = 5, TCH_POWER = 6, TCH_MATMUL = 7, TCH_VECTOR_MUL = 8
+    TCH_MAXIMUM = 4, TCH_MINIMUM = 5, TCH_POWER = 6, TCH_MATMUL = 7, TCH_VECTOR_MUL = 8, TCH_MATVEC = 9
 } tch_binary;
 
 /* Unary operations (tape/tensor.rs:187-333); `first` and `second` are the
@@ -109,6 +110,9 @@ void tch_tape_destroy(tch_tape* tape);
 /* A leaf: `values` holds the product of `shape` floats, copied to the device. */
 int tch_tape_tensor(tch_tape* tape, uint32_t rank, const uint64_t* shape, const float* values, uint32_t* out);
 int tch_tape_binary(tch_tape* tape, uint32_t op, uint32_t a, uint32_t b, uint32_t* out);
+/* `MatrixVar::matvec_add` (tape/mod.rs:1259-1274): the r x c tensor `m`
+ * times the length-c tensor `v` plus the length-r tensor `addend`. */
+int tch_tape_matvec_add(tch_tape* tape, uint32_t m, uint32_t v, uint32_t addend, uint32_t* out);
 int tch_tape_unary(tch_tape* tape, uint32_t op, uint32_t a, float first, float second, uint32_t* out);
 int tch_tape_layout(tch_tape* tape, uint32_t op, uint32_t a, uint32_t count, const int64_t* values, uint32_t* out);
 int tch_tape_reduce(tch_tape* tape, uint32_t op, uint32_t a, uint32_t count, const int64_t* axes, int keep_dims,

@@ -338,6 +338,17 @@ struct Kernels {
         check(tc_matvec(dtype, 0, m.rows(), m.cols(), m.storage().ptr(), v.storage().ptr(), out.ptr()));
         return Vector<T>(std::move(out));
     }
+    // `matvec_add` (kernels.rs:908): M·v + addend, the addend consumed as
+    // the accumulator.
+    static Vector<T> matvec_add(const Matrix<T>& m, const Vector<T>& v, Vector<T> addend) {
+        if (m.cols() != v.len() || m.rows() != addend.len()) {
+            throw std::invalid_argument("matvec_add: a " + dims(m.shape()) + " matrix times a length-" +
+                                        std::to_string(v.len()) + " vector plus a length-" +
+                                        std::to_string(addend.len()) + " vector");
+        }
+        check(tc_matvec(dtype, 1, m.rows(), m.cols(), m.storage().ptr(), v.storage().ptr(), addend.storage().ptr()));
+        return addend;
+    }
     // `vecmat` (kernels.rs:899): vᵀ·M.
     static Vector<T> vecmat(const Vector<T>& v, const Matrix<T>& m) {
         if (m.rows() != v.len()) {

@@ -476,6 +476,33 @@ class MatrixVar : public Var<Matrix<T>> {
             });
     }
 
+    // `MatrixVar::matvec` / `matvec_add` (tape/mod.rs:1249-1274):
+    // M̄ += ȳ ⊗ v, v̄ += ȳᵀ·M, and the addend's adjoint is ȳ.
+    VectorVar<T> matvec(const VectorVar<T>& v) const {
+        this->assert_same_tape(v.tape());
+        auto matrix = this->node_;
+        auto vector = v.node();
+        return VectorVar<T>(this->template record<Vector<T>>(
+            K<T>::matvec(this->value(), v.value()), [matrix, vector](const Vector<T>& adjoint) {
+                matrix->accumulate(hip::outer(adjoint, vector->get()));
+                vector->accumulate(K<T>::vecmat(adjoint, matrix->get()));
+            }));
+    }
+    VectorVar<T> matvec_add(const VectorVar<T>& v, const VectorVar<T>& addend) const {
+        this->assert_same_tape(v.tape());
+        this->assert_same_tape(addend.tape());
+        auto matrix = this->node_;
+        auto vector = v.node();
+        auto bias = addend.node();
+        return VectorVar<T>(this->template record<Vector<T>>(
+            K<T>::matvec_add(this->value(), v.value(), addend.value().duplicate()),
+            [matrix, vector, bias](const Vector<T>& adjoint) {
+                matrix->accumulate(hip::outer(adjoint, vector->get()));
+                vector->accumulate(K<T>::vecmat(adjoint, matrix->get()));
+                bias->accumulate(adjoint.duplicate());
+            }));
+    }
+
     // `MatrixVar::transpose` (tape/mod.rs:1272-1279).
     MatrixVar transpose() const {
         auto parent = this->node_;

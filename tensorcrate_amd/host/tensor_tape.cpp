@@ -104,6 +104,15 @@ int tch_tape_binary(tch_tape* t, uint32_t op, uint32_t a, uint32_t b, uint32_t* 
             case TCH_MINIMUM: *out = t->add(x.minimum(y)); break;
             case TCH_POWER: *out = t->add(x.power(y)); break;
             case TCH_MATMUL: *out = t->add(product(x, y)); break;
+            case TCH_MATVEC: {
+                if (x.rank() != 2 || y.rank() != 1) {
+                    throw std::invalid_argument("matvec: shapes " + shape_text(x.shape()) + " and " +
+                                                shape_text(y.shape()) + " are not a matrix and a vector");
+                }
+                MatrixVar<float> m = x.to_matrix(x.shape()[0], x.shape()[1]);
+                *out = t->add(m.matvec(y.to_vector()).to_tensor({x.shape()[0]}));
+                break;
+            }
             case TCH_VECTOR_MUL: {
                 // `to_vector`, `VectorVar`'s product, `to_tensor`: one flat
                 // variable when both operands are the same tensor, as in
@@ -119,6 +128,20 @@ int tch_tape_binary(tch_tape* t, uint32_t op, uint32_t a, uint32_t b, uint32_t* 
             }
             default: throw std::invalid_argument("tape: no binary operation " + std::to_string(op));
         }
+    });
+}
+
+int tch_tape_matvec_add(tch_tape* t, uint32_t m, uint32_t v, uint32_t addend, uint32_t* out) {
+    return guarded([&] {
+        const TensorVar<float>& x = t->tensor(m);
+        const TensorVar<float>& y = t->tensor(v);
+        const TensorVar<float>& z = t->tensor(addend);
+        if (x.rank() != 2 || y.rank() != 1 || z.rank() != 1) {
+            throw std::invalid_argument("matvec_add: shapes " + shape_text(x.shape()) + ", " + shape_text(y.shape()) +
+                                        " and " + shape_text(z.shape()) + " are not a matrix and two vectors");
+        }
+        MatrixVar<float> matrix = x.to_matrix(x.shape()[0], x.shape()[1]);
+        *out = t->add(matrix.matvec_add(y.to_vector(), z.to_vector()).to_tensor({x.shape()[0]}));
     });
 }
 

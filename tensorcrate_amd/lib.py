@@ -386,6 +386,7 @@ HOST_SIGNATURES = {
     "tch_tape_destroy": [vp],
     "tch_tape_tensor": [vp, u32, ctypes.POINTER(u64), vp, ctypes.POINTER(u32)],
     "tch_tape_binary": [vp, u32, u32, u32, ctypes.POINTER(u32)],
+    "tch_tape_matvec_add": [vp, u32, u32, u32, ctypes.POINTER(u32)],
     "tch_tape_unary": [vp, u32, u32, f32, f32, ctypes.POINTER(u32)],
     "tch_tape_layout": [vp, u32, u32, u32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(u32)],
     "tch_tape_reduce": [vp, u32, u32, u32, ctypes.POINTER(ctypes.c_int64), i32, ctypes.POINTER(u32)],
@@ -478,7 +479,7 @@ class Mlp:
 
 # ``tch_binary``, ``tch_unary``, ``tch_layout``, ``tch_reduction`` (include/tchip_host.h).
 TAPE_BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3, "maximum": 4, "minimum": 5, "power": 6, "matmul": 7,
-               "vector_mul": 8}
+               "vector_mul": 8, "matvec": 9}
 TAPE_UNARY = {"clamp_min": 0, "clamp_max": 1, "clamp": 2, "relu": 3, "abs": 4, "neg": 5, "scale": 6, "shift": 7,
               "power_scalar": 8, "power_scalar_left": 9, "contiguous": 10}
 TAPE_ANALYTIC = 32
@@ -587,6 +588,9 @@ class TapeVar:
         array = (u64 * max(count, 1))(*sizes) if sizes is not None else None
         host_call("tch_tape_split", self.tape.handle, self.handle, axis, count, array, out)
         return [TapeVar(self.tape, out[k]) for k in range(count)]
+
+    def matvec_add(self, v: "TapeVar", addend: "TapeVar") -> "TapeVar":
+        return self.tape._out("tch_tape_matvec_add", self.handle, v.handle, addend.handle)
 
     def add_scalar(self, other: "TapeVar") -> "TapeVar":
         return self.tape._out("tch_tape_add_scalars", self.handle, other.handle)

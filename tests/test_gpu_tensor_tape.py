@@ -1,6 +1,8 @@
 """Tensor variables on the tape (host/tape.hpp's `TensorVar`, the C++ mirror
 of src/tensors/tape/tensor.rs) on the GPU, operation by operation, as
-tests/tensor_autodiff.rs:50-400 checks them in the reference.
+tests/tensor_autodiff.rs:50-400 checks them in the reference; the matrix
+and vector rules they pass through (`MatrixVar::matmul`, `matvec`,
+`matvec_add`, `VectorVar`'s products) are checked the same way.
 
 Each operation is written once against a small facade and run twice: on the
 device tape (`lib.Tape`), which differentiates it with one backward pass from
@@ -38,7 +40,11 @@ class Np:
         return Np({"add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide,
                    "maximum": np.maximum, "minimum": np.minimum, "power": np.power,
                    "matmul": np.matmul,
-                   "vector_mul": lambda a, b: (a.ravel() * b.ravel()).reshape(a.shape)}[op](a, b))
+                   "vector_mul": lambda a, b: (a.ravel() * b.ravel()).reshape(a.shape),
+                   "matvec": np.matmul}[op](a, b))
+
+    def matvec_add(self, v, addend):
+        return Np(self.v @ v.v + addend.v)
 
     __add__ = lambda self, o: self.binary(o, "add")
     __sub__ = lambda self, o: self.binary(o, "sub")
@@ -175,6 +181,9 @@ OPS = [
      lambda v: v[0].binary(v[0], "vector_mul").layout("reshape", [4, 6])),
     ("vector_product", lambda: [filled((2, 3, 4), 1, -1, 1), positive((6, 4), 2)],
      lambda v: v[0].binary(v[1], "vector_mul")),
+    ("matvec", lambda: [filled((5, 7), 1, -1, 1), filled((7,), 2, -1, 1)], lambda v: v[0].binary(v[1], "matvec")),
+    ("matvec_add", lambda: [filled((5, 7), 1, -1, 1), filled((7,), 2, -1, 1), filled((5,), 3, -1, 1)],
+     lambda v: v[0].matvec_add(v[1], v[2])),
     # A tensor used twice: the second rule adds into an adjoint already there.
     ("reused_operand", lambda: [x()], lambda v: v[0].reduce("sum_axes", 1, True) + (v[0] * v[0])),
     # The narrow's rule runs after the product's, so it adds into an adjoint
