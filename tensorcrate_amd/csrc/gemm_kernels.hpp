@@ -668,6 +668,22 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restr
             program_pass<BN, 32, kRegionRows, H, BM / WM>(epi, r0, r1, r2, r3, kPass, pass, m0, n0, M,
                                                                            N);
         }
+    } else if (m0 + BM <= M && n0 + BN <= N) {
+        // A whole tile: no bounds to check, and each lane's column walks down
+        // from one base pointer in steps of N.
+        O* base = C + static_cast<uint64_t>(m0 + wm * (BM / WM) + 4 * (lane / 32)) * N + n0 + wn * (BN / WN) +
+                  lane % 32;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t r = i * 32 + 8 * (e / 4) + e % 4;
+                    store_out(base, static_cast<uint64_t>(r) * N + j * 32, acc[i][j][e], accumulate);
+                }
+            }
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
@@ -792,15 +808,35 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_persistent_kernel(const
             step(std::integral_constant<int, 0>{}, s);
             step(std::integral_constant<int, 1>{}, s + 1);
         }
+        if (m0 + BM <= M && n0 + BN <= N) {
+            // A whole tile: no bounds to check, and each lane's column walks
+            // down from one base pointer in steps of N.
+            O* base = C + static_cast<uint64_t>(m0 + wm * (BM / WM) + 4 * (lane / 32)) * N + n0 + wn * (BN / WN) +
+                      lane % 32;
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
+            for (int i = 0; i < TM; i++) {
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const uint32_t col = n0 + wn * (BN / WN) + j * 32 + lane % 32;
+                for (int j = 0; j < TN; j++) {
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const uint32_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
-                    if (row < M && col < N) store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
+                    for (int e = 0; e < 16; e++) {
+                        const uint32_t r = i * 32 + 8 * (e / 4) + e % 4;
+                        store_out(base, static_cast<uint64_t>(r) * N + j * 32, acc[i][j][e], accumulate);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const uint32_t col = n0 + wn * (BN / WN) + j * 32 + lane % 32;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const uint32_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                        if (row < M && col < N) {
+                            store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
+                        }
+                    }
                 }
             }
         }
