@@ -118,6 +118,9 @@ def timed_graph(fn, steps: int, warmup: int) -> float:
     lib.sync()
     hip.hipGraphExecDestroy(graph_exec)
     hip.hipGraphDestroy(graph)
+    # The graph is gone: the storage its captured calls used may serve
+    # eager work again.
+    lib.call("tc_release_graph_memory")
     return ms.value / steps
 
 

@@ -177,10 +177,27 @@ int tc_timer_end(float* milliseconds);
  * `Backend::store` / `from_vec` allocate with this and then upload. */
 int tc_alloc(size_t bytes, void** out);
 /* Return storage to the calling thread's cache; work already queued that
- * reads it still completes first (the pool fence of metal/pool.rs:34-48). */
+ * reads it still completes first (the pool fence of metal/pool.rs:34-48).
+ * Storage allocated or freed while the thread's stream is being captured
+ * into a HIP graph stays with the graphs, which touch it again on every
+ * replay: it is reused only within the capture that freed it, and after
+ * that capture ends it is retired, handed to no other allocation. */
 int tc_free(void* pointer);
-/* Give every cached, unused block back to the device. */
+/* Give every cached, unused block back to the device (retired graph
+ * storage excepted).  Refused while the stream is capturing. */
 int tc_empty_cache(void);
+/* The caller's promise that no graph captured on this thread will run
+ * again: retired graph storage returns to the cache and live graph storage
+ * becomes ordinary.  No reference counterpart (Metal has no graphs); the
+ * fence of metal/pool.rs:34-48 applied to replays. */
+int tc_release_graph_memory(void);
+/* Bytes of live and of retired (or capture-free) graph storage. */
+int tc_graph_memory(uint64_t* live_bytes, uint64_t* retired_bytes);
+/* This thread's operations queued on its stream (kernel launches and device
+ * copies) and the times the host waited for the stream, since the thread
+ * began: the `dispatches` and `syncs` of counters::Counts
+ * (src/counters.rs:33-57, recorded at :100-135). */
+int tc_activity(uint64_t* dispatches, uint64_t* waits);
 /* Host to device, device to host (`as_slice`, backend.rs:99; the download
  * waits for queued work), and device to device (`duplicate`, backend.rs:111).
  * From 8 MiB up the first two take the pinned staging of tc_upload_staged. */

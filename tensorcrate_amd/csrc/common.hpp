@@ -37,8 +37,14 @@ int fail(int status, const std::string& message);
 // The calling thread's stream, initialising device 0 on first use; nullptr
 // (with the error recorded) if the device cannot be set up.
 hipStream_t stream();
-// TC_OK, or the HIP error from the launch just made, recorded under `what`.
+// TC_OK, or the HIP error from the launch just made, recorded under `what`;
+// counts the launch as one operation queued on the thread's stream.
 int check_launch(const char* what);
+// Count an operation queued without check_launch (a module launch, a copy).
+void count_dispatch();
+// Wait for the stream or an event on the host, counted as a host wait.
+hipError_t host_wait(hipStream_t s);
+hipError_t host_wait(hipEvent_t e);
 // Shorthand: set up the thread's stream or return its failure.
 #define TC_STREAM(var)                                \
     hipStream_t var = ::tc::stream();                 \

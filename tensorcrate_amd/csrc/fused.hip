@@ -312,6 +312,51 @@ struct Compiled {
     std::vector<hipFunction_t> functions;
 };
 
+// Programs too large for kernel arguments, resident on the device for the
+// process by their bytes (the host copy is kept beside each, the source of
+// its one upload).  A program first seen while the stream is being captured
+// is refused: its upload would be a node of the graph reading host memory.
+struct ResidentProgram {
+    std::string host;
+    void* device = nullptr;
+};
+std::mutex resident_mutex;
+std::unordered_map<std::string, ResidentProgram> resident_programs;
+constexpr size_t kResidentPrograms = 4096;
+
+int resident_program(const std::string& key, hipStream_t s, void** device) {
+    std::lock_guard<std::mutex> lock(resident_mutex);
+    auto found = resident_programs.find(key);
+    if (found != resident_programs.end()) {
+        *device = found->second.device;
+        return TC_OK;
+    }
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &capture) != hipSuccess) (void)hipGetLastError();
+    if (capture != hipStreamCaptureStatusNone) {
+        return fail(TC_UNSUPPORTED, "fused program: a program of more than " + std::to_string(kInlineCode) +
+                                        " instructions or " + std::to_string(kInlinePlaces) +
+                                        " places must run once before it is captured");
+    }
+    if (resident_programs.size() >= kResidentPrograms) {
+        return fail(TC_UNSUPPORTED, "fused program: more than " + std::to_string(kResidentPrograms) +
+                                        " distinct large programs");
+    }
+    ResidentProgram entry;
+    entry.host = key;
+    hipError_t error = hipMalloc(&entry.device, key.size());
+    if (error != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(TC_OUT_OF_MEMORY, std::string("fused program upload: ") + hipGetErrorString(error));
+    }
+    count_dispatch();
+    auto placed = resident_programs.emplace(key, std::move(entry)).first;
+    error = hipMemcpyAsync(placed->second.device, placed->second.host.data(), key.size(), hipMemcpyHostToDevice, s);
+    if (error != hipSuccess) return fail(TC_DEVICE, std::string("fused program upload: ") + hipGetErrorString(error));
+    *device = placed->second.device;
+    return TC_OK;
+}
+
 std::mutex compiled_mutex;
 std::unordered_map<std::string, Compiled> compiled_programs;
 uint64_t compiled_count = 0;
@@ -476,6 +521,7 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
     size_t size = sizeof(args);
     void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
     const uint32_t blocks = blocks_for(chunks, 1);
+    count_dispatch();
     hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, nullptr, config);
     *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused program: ") + hipGetErrorString(error));
     return true;
@@ -533,6 +579,7 @@ bool run_general_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype
     uint32_t cols32 = static_cast<uint32_t>(cols), total32 = static_cast<uint32_t>(total);
     void* params[] = {&args, &cols32, &total32};
     const uint32_t blocks = grid_for(total, 256 * kGeneralElems, 8);
+    count_dispatch();
     const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);
     *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused program: ") + hipGetErrorString(error));
     return true;
@@ -589,6 +636,7 @@ bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtyp
     void* params[] = {&args, &rows32, &cols32, &out};
     const uint64_t wanted = (rows + 3) / 4;
     const uint32_t blocks = static_cast<uint32_t>(wanted < 0xffffffu ? wanted : 0xffffffu);
+    count_dispatch();
     const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);
     *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused sum: ") + hipGetErrorString(error));
     return true;
@@ -747,19 +795,15 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
         if (place_count) memcpy(program.places, device_places.data(), place_count * sizeof(DevicePlace));
     } else {
         // A larger program and its places travel in one block of device
-        // memory, freed once the kernel has been queued (stream order keeps
-        // it alive until the kernel has run).
+        // memory, uploaded on the program's first sight and kept for the
+        // process, keyed by its bytes: a later run, captured into a graph or
+        // not, reads it in place, and no copy or block belongs to one call.
         const size_t code_bytes = (count * sizeof(tc_encoded) + 15) / 16 * 16;
-        std::vector<uint8_t> host(code_bytes + place_count * sizeof(DevicePlace));
-        memcpy(host.data(), code, count * sizeof(tc_encoded));
-        if (place_count) memcpy(host.data() + code_bytes, device_places.data(), place_count * sizeof(DevicePlace));
-        status = tc_alloc(host.size(), &device);
+        std::string key(code_bytes + place_count * sizeof(DevicePlace), '\0');
+        memcpy(&key[0], code, count * sizeof(tc_encoded));
+        if (place_count) memcpy(&key[code_bytes], device_places.data(), place_count * sizeof(DevicePlace));
+        status = resident_program(key, s, &device);
         if (status != TC_OK) return status;
-        hipError_t error = hipMemcpyAsync(device, host.data(), host.size(), hipMemcpyHostToDevice, s);
-        if (error != hipSuccess) {
-            tc_free(device);
-            return fail(TC_DEVICE, std::string("fused program upload: ") + hipGetErrorString(error));
-        }
         dcode = static_cast<const tc_encoded*>(device);
         dplaces = reinterpret_cast<const DevicePlace*>(static_cast<uint8_t*>(device) + code_bytes);
     }
@@ -780,9 +824,7 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
         }
     }
 #undef TC_FUSED_LAUNCH
-    status = check_launch("fused program");
-    if (device != nullptr) tc_free(device);
-    return status;
+    return check_launch("fused program");
 }
 
 extern "C" int tc_fused_compiled(uint64_t* count) {

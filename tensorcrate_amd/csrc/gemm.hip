@@ -546,6 +546,7 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     bool accumulate = false;
     void* params[] = {const_cast<void**>(&a), const_cast<void**>(&b), &none, &m, &n, &k, &accumulate, &args};
     const bool use_large = large >= static_cast<uint32_t>(compute_units());
+    count_dispatch();
     const hipError_t error = hipModuleLaunchKernel(use_large ? functions[0] : functions[1], use_large ? large : small,
                                                    1, 1, use_large ? large_threads : small_threads, 1, 1, 0, s, params,
                                                    nullptr);

@@ -95,7 +95,7 @@ int in_parallel(size_t bytes, const std::function<int(size_t, size_t)>& work) {
 // Wait until the DMA last queued on buffer `k` is done with it.
 int wait_buffer(int k) {
     if (!staging.pending[k]) return TC_OK;
-    hipError_t error = hipEventSynchronize(staging.done[k]);
+    hipError_t error = host_wait(staging.done[k]);
     staging.pending[k] = false;
     return error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("staging: ") + hipGetErrorString(error));
 }
@@ -111,6 +111,7 @@ int staged_upload(void* device_dst, size_t bytes, Fill fill) {
         const size_t n = bytes - done < kStageBytes ? bytes - done : kStageBytes;
         if ((status = wait_buffer(k)) != TC_OK) return status;
         if ((status = fill(staging.buffer[k], done, n)) != TC_OK) return status;
+        count_dispatch();
         hipError_t error = hipMemcpyAsync(static_cast<char*>(device_dst) + done, staging.buffer[k], n,
                                           hipMemcpyHostToDevice, s);
         if (error == hipSuccess) error = hipEventRecord(staging.done[k], s);
@@ -131,6 +132,7 @@ int staged_download(const void* device_src, size_t bytes, Drain drain) {
     if (status != TC_OK) return status;
     auto issue = [&](size_t at, int k) -> int {
         const size_t n = bytes - at < kStageBytes ? bytes - at : kStageBytes;
+        count_dispatch();
         hipError_t error = hipMemcpyAsync(staging.buffer[k], static_cast<const char*>(device_src) + at, n,
                                           hipMemcpyDeviceToHost, s);
         if (error == hipSuccess) error = hipEventRecord(staging.done[k], s);
@@ -315,9 +317,10 @@ int tc_read_async(const void* device_src, size_t bytes, uint64_t* ticket) {
         if (error != hipSuccess) return fail(TC_DEVICE, std::string("read slot event: ") + hipGetErrorString(error));
     } else {
         // The slot's previous read must land before this one overwrites it.
-        hipError_t error = hipEventSynchronize(slots.done[slot]);
+        hipError_t error = host_wait(slots.done[slot]);
         if (error != hipSuccess) return fail(TC_DEVICE, std::string("read slot: ") + hipGetErrorString(error));
     }
+    count_dispatch();
     hipError_t error = hipMemcpyAsync(slots.pinned + slot * kSlotBytes, device_src, bytes, hipMemcpyDeviceToHost, s);
     if (error == hipSuccess) error = hipEventRecord(slots.done[slot], s);
     if (error != hipSuccess) return fail(TC_DEVICE, std::string("read_async: ") + hipGetErrorString(error));
@@ -334,7 +337,7 @@ int tc_read_wait(uint64_t ticket, void* host_dst, size_t bytes) {
                                                             : " was reused by 1024 later reads"));
     }
     const uint64_t slot = ticket % kSlots;
-    hipError_t error = hipEventSynchronize(slots.done[slot]);
+    hipError_t error = host_wait(slots.done[slot]);
     if (error != hipSuccess) return fail(TC_DEVICE, std::string("the GPU failed; its output is invalid: ") +
                                                         hipGetErrorString(error));
     memcpy(host_dst, slots.pinned + slot * kSlotBytes, bytes);

@@ -4,10 +4,19 @@
 // It takes the roles the reference's Metal runtime splits across
 // metal/device.rs (the thread-local device and queue), metal/pool.rs (buffer
 // reuse fenced against queued work), metal/buffer.rs (reads that wait for
-// the GPU) and metal/sync.rs (failure reported at the next wait), re-cut for
-// HIP: one in-order stream per host thread makes reuse of a freed block safe
-// without fences, because any later use of it is queued behind every earlier
-// one.
+// the GPU), metal/sync.rs (failure reported at the next wait) and
+// counters.rs (operations queued and host waits), re-cut for HIP: one
+// in-order stream per host thread makes reuse of a freed block safe without
+// fences, because any later use of it is queued behind every earlier one.
+//
+// Stream capture breaks that premise: work captured into a HIP graph runs
+// again at every replay, after anything queued eagerly in between.  So a
+// block allocated or freed while the thread's stream is capturing belongs
+// to the graphs: freed during the capture that made it, it is reused only
+// by later allocations of that same capture (whose graph replays in the
+// order it was captured); freed after, or left over when the capture ends,
+// it is retired, handed to nothing, until tc_release_graph_memory says the
+// graphs are gone.
 
 #include <stdio.h>
 #include <string.h>
@@ -34,6 +43,16 @@ struct ThreadState {
     std::multimap<size_t, void*> cached;
     std::unordered_map<void*, size_t> live;
     size_t cached_bytes = 0;
+    // Blocks that captured graphs may touch on replay (allocated or freed
+    // while capturing): live ones, those free for reuse within the capture
+    // `capture_id` (0: none), and retired ones, reused by nothing.
+    std::unordered_map<void*, size_t> graph_live;
+    std::multimap<size_t, void*> capture_free;
+    std::vector<std::pair<void*, size_t>> retired;
+    unsigned long long capture_id = 0;
+    // Operations queued on the stream and times the host waited for it.
+    uint64_t dispatches = 0;
+    uint64_t waits = 0;
     // Nothing is released at thread exit: the HIP runtime may already be
     // gone by then, and the device reclaims everything with the process.
 };
@@ -94,10 +113,45 @@ hipStream_t stream() {
 }
 
 int check_launch(const char* what) {
+    state.dispatches++;
     hipError_t error = hipGetLastError();
     if (error != hipSuccess) return hip_fail(error, what);
     return TC_OK;
 }
+
+void count_dispatch() { state.dispatches++; }
+
+hipError_t host_wait(hipStream_t s) {
+    state.waits++;
+    return hipStreamSynchronize(s);
+}
+
+hipError_t host_wait(hipEvent_t e) {
+    state.waits++;
+    return hipEventSynchronize(e);
+}
+
+namespace {
+
+// The capture the thread's stream is in (0: none), ending the previous one
+// first if it is over: its free blocks are retired.
+unsigned long long current_capture(hipStream_t s) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    if (hipStreamGetCaptureInfo(s, &status, &id) != hipSuccess) {
+        (void)hipGetLastError();
+        status = hipStreamCaptureStatusNone;
+    }
+    if (status != hipStreamCaptureStatusActive) id = 0;
+    if (id != state.capture_id) {
+        for (auto& entry : state.capture_free) state.retired.emplace_back(entry.second, entry.first);
+        state.capture_free.clear();
+        state.capture_id = id;
+    }
+    return id;
+}
+
+}  // namespace
 
 int compute_units() {
     std::call_once(cus_once, [] {
@@ -212,7 +266,7 @@ const char* tc_last_error(void) { return last_error.c_str(); }
 
 int tc_sync(void) {
     TC_STREAM(s);
-    hipError_t error = hipStreamSynchronize(s);
+    hipError_t error = host_wait(s);
     if (error != hipSuccess) return hip_fail(error, "the GPU failed; its output is invalid");
     return TC_OK;
 }
@@ -250,7 +304,7 @@ int tc_timer_end(float* milliseconds) {
     if (state.timer_start == nullptr) return fail(TC_INVALID, "tc_timer_end without tc_timer_begin");
     hipError_t error;
     if ((error = hipEventRecord(state.timer_stop, s)) != hipSuccess) return hip_fail(error, "hipEventRecord");
-    if ((error = hipEventSynchronize(state.timer_stop)) != hipSuccess) return hip_fail(error, "the GPU failed; its output is invalid");
+    if ((error = host_wait(state.timer_stop)) != hipSuccess) return hip_fail(error, "the GPU failed; its output is invalid");
     if ((error = hipEventElapsedTime(milliseconds, state.timer_start, state.timer_stop)) != hipSuccess) {
         return hip_fail(error, "hipEventElapsedTime");
     }
@@ -259,22 +313,31 @@ int tc_timer_end(float* milliseconds) {
 
 int tc_alloc(size_t bytes, void** out) {
     TC_STREAM(s);
-    (void)s;
     size_t size = rounded(bytes);
+    const bool capturing = current_capture(s) != 0;
+    if (capturing) {
+        auto hit = state.capture_free.find(size);
+        if (hit != state.capture_free.end()) {
+            *out = hit->second;
+            state.capture_free.erase(hit);
+            state.graph_live[*out] = size;
+            return TC_OK;
+        }
+    }
     auto hit = state.cached.find(size);
     if (hit != state.cached.end()) {
         *out = hit->second;
         state.cached.erase(hit);
         state.cached_bytes -= size;
-        state.live[*out] = size;
+        (capturing ? state.graph_live : state.live)[*out] = size;
         return TC_OK;
     }
     void* pointer = nullptr;
     hipError_t error = hipMalloc(&pointer, size);
-    if (error == hipErrorOutOfMemory && !state.cached.empty()) {
+    if (error == hipErrorOutOfMemory && !state.cached.empty() && !capturing) {
         // Give the cache back and try once more before reporting.
         (void)hipGetLastError();
-        (void)hipStreamSynchronize(s);
+        (void)host_wait(s);
         for (auto& entry : state.cached) (void)hipFree(entry.second);
         state.cached.clear();
         state.cached_bytes = 0;
@@ -284,30 +347,82 @@ int tc_alloc(size_t bytes, void** out) {
         (void)hipGetLastError();
         return hip_fail(error, ("allocating " + std::to_string(bytes) + " bytes").c_str());
     }
-    state.live[pointer] = size;
+    (capturing ? state.graph_live : state.live)[pointer] = size;
     *out = pointer;
     return TC_OK;
 }
 
 int tc_free(void* pointer) {
     if (pointer == nullptr) return TC_OK;
+    TC_STREAM(s);
+    const bool capturing = current_capture(s) != 0;
     auto found = state.live.find(pointer);
-    if (found == state.live.end()) {
-        return fail(TC_INVALID, "tc_free: the pointer was not allocated by tc_alloc on this thread");
+    size_t size = 0;
+    bool graphs = capturing;
+    if (found != state.live.end()) {
+        size = found->second;
+        state.live.erase(found);
+    } else {
+        auto owned = state.graph_live.find(pointer);
+        if (owned == state.graph_live.end()) {
+            return fail(TC_INVALID, "tc_free: the pointer was not allocated by tc_alloc on this thread");
+        }
+        size = owned->second;
+        state.graph_live.erase(owned);
+        graphs = true;
     }
-    state.cached.emplace(found->second, pointer);
-    state.cached_bytes += found->second;
-    state.live.erase(found);
+    if (!graphs) {
+        state.cached.emplace(size, pointer);
+        state.cached_bytes += size;
+    } else if (capturing) {
+        state.capture_free.emplace(size, pointer);
+    } else {
+        state.retired.emplace_back(pointer, size);
+    }
+    return TC_OK;
+}
+
+int tc_release_graph_memory(void) {
+    TC_STREAM(s);
+    if (current_capture(s) != 0) {
+        return fail(TC_INVALID, "tc_release_graph_memory: the stream is capturing");
+    }
+    for (auto& entry : state.retired) {
+        state.cached.emplace(entry.second, entry.first);
+        state.cached_bytes += entry.second;
+    }
+    state.retired.clear();
+    for (auto& entry : state.graph_live) state.live.emplace(entry.first, entry.second);
+    state.graph_live.clear();
+    return TC_OK;
+}
+
+int tc_graph_memory(uint64_t* live_bytes, uint64_t* retired_bytes) {
+    TC_STREAM(s);
+    (void)current_capture(s);
+    uint64_t live = 0, retired = 0;
+    for (auto& entry : state.graph_live) live += entry.second;
+    for (auto& entry : state.capture_free) retired += entry.first;
+    for (auto& entry : state.retired) retired += entry.second;
+    *live_bytes = live;
+    *retired_bytes = retired;
     return TC_OK;
 }
 
 int tc_empty_cache(void) {
     TC_STREAM(s);
-    hipError_t error = hipStreamSynchronize(s);
+    if (current_capture(s) != 0) return fail(TC_INVALID, "tc_empty_cache: the stream is capturing");
+    hipError_t error = host_wait(s);
     if (error != hipSuccess) return hip_fail(error, "the GPU failed; its output is invalid");
     for (auto& entry : state.cached) (void)hipFree(entry.second);
     state.cached.clear();
     state.cached_bytes = 0;
+    return TC_OK;
+}
+
+int tc_activity(uint64_t* dispatches, uint64_t* waits) {
+    *dispatches = state.dispatches;
+    *waits = state.waits;
     return TC_OK;
 }
 
@@ -324,7 +439,7 @@ int tc_upload(void* dst, const void* src, size_t bytes) {
     // the caller's buffer is free to reuse at once.
     hipError_t error = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
     if (error != hipSuccess) return hip_fail(error, "upload");
-    error = hipStreamSynchronize(s);
+    error = host_wait(s);
     if (error != hipSuccess) return hip_fail(error, "upload");
     return TC_OK;
 }
@@ -335,7 +450,7 @@ int tc_download(void* dst, const void* src, size_t bytes) {
     if (bytes >= kStagedBytes) return tc_download_staged(dst, src, bytes);
     hipError_t error = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
     if (error != hipSuccess) return hip_fail(error, "download");
-    error = hipStreamSynchronize(s);
+    error = host_wait(s);
     if (error != hipSuccess) return hip_fail(error, "the GPU failed; its output is invalid");
     return TC_OK;
 }
@@ -354,6 +469,7 @@ int tc_copy(void* dst, const void* src, size_t bytes) {
         from.strides[0] = 1;
         return tc_strided_copy(4, src, words, 1, shape, &from, dst);
     }
+    count_dispatch();
     hipError_t error = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
     if (error != hipSuccess) return hip_fail(error, "duplicate");
     return TC_OK;

@@ -28,9 +28,13 @@ constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;
 
-// An inclusive scan of one value a thread across the block (Hillis-Steele in
-// LDS: a fixed order); `total` receives the block's sum.
-__device__ float block_inclusive_scan(float v, float* lds, float* total) {
+// A scan of one value a thread across the block (Hillis-Steele in LDS: a
+// fixed order).  Returns the inclusive sum; `exclusive` receives the sum of
+// the threads before this one, read from the scan itself (thread t - 1's
+// inclusive sum, zero for thread 0), never as the inclusive sum minus the
+// value: a later infinity, NaN or very large element then cannot reach the
+// sums before it.  `total` receives the block's sum.
+__device__ float block_scan(float v, float* lds, float* exclusive, float* total) {
     const int t = threadIdx.x;
     lds[t] = v;
     __syncthreads();
@@ -41,6 +45,7 @@ __device__ float block_inclusive_scan(float v, float* lds, float* total) {
         __syncthreads();
     }
     const float out = lds[t];
+    *exclusive = t > 0 ? lds[t - 1] : 0.0f;
     *total = lds[kScanThreads - 1];
     __syncthreads();
     return out;
@@ -57,8 +62,8 @@ __global__ void __launch_bounds__(kScanThreads) tile_sums_kernel(const S* __rest
         const uint64_t i = base + k * kScanThreads + threadIdx.x;
         if (i < n) s = s + Elem<S>::widen(a[i]);
     }
-    float total;
-    block_inclusive_scan(s, lds, &total);
+    float before, total;
+    block_scan(s, lds, &before, &total);
     if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
@@ -69,9 +74,9 @@ __global__ void __launch_bounds__(kScanThreads) scan_sums_kernel(float* __restri
     for (uint32_t first = 0; first < count; first += kScanThreads) {
         const uint32_t i = first + threadIdx.x;
         const float v = i < count ? sums[i] : 0.0f;
-        float total;
-        const float inclusive = block_inclusive_scan(v, lds, &total);
-        if (i < count) sums[i] = carry + (inclusive - v);
+        float before, total;
+        block_scan(v, lds, &before, &total);
+        if (i < count) sums[i] = carry + before;
         carry = carry + total;
     }
 }
@@ -97,8 +102,8 @@ __global__ void __launch_bounds__(kScanThreads) tile_scan_kernel(const S* __rest
         s = s + tile[slot(threadIdx.x * kScanItems + k)];
         run[k] = s;
     }
-    float total;
-    const float before = block_inclusive_scan(s, lds, &total) - s;
+    float before, total;
+    block_scan(s, lds, &before, &total);
     const float offset = offsets[blockIdx.x] + before;
 #pragma unroll
     for (int k = 0; k < kScanItems; k++) tile[slot(threadIdx.x * kScanItems + k)] = offset + run[k];

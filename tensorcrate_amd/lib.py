@@ -121,6 +121,9 @@ SIGNATURES = {
     "tc_alloc": [ctypes.c_size_t, ctypes.POINTER(vp)],
     "tc_free": [vp],
     "tc_empty_cache": [],
+    "tc_release_graph_memory": [],
+    "tc_graph_memory": [ctypes.POINTER(u64), ctypes.POINTER(u64)],
+    "tc_activity": [ctypes.POINTER(u64), ctypes.POINTER(u64)],
     "tc_upload": [vp, vp, ctypes.c_size_t],
     "tc_download": [vp, vp, ctypes.c_size_t],
     "tc_copy": [vp, vp, ctypes.c_size_t],
@@ -208,6 +211,20 @@ def call(name: str, *args) -> None:
 
 def sync() -> None:
     call("tc_sync")
+
+
+def activity() -> tuple[int, int]:
+    """This thread's (operations queued, host waits) so far (`tc_activity`)."""
+    dispatches, waits = u64(), u64()
+    call("tc_activity", ctypes.byref(dispatches), ctypes.byref(waits))
+    return dispatches.value, waits.value
+
+
+def graph_memory() -> tuple[int, int]:
+    """Bytes of (live, retired) storage that captured graphs may touch."""
+    live, retired = u64(), u64()
+    call("tc_graph_memory", ctypes.byref(live), ctypes.byref(retired))
+    return live.value, retired.value
 
 
 def device_info() -> tuple[str, str]:

@@ -157,11 +157,13 @@ def test_config1_f32_512_cubed():
 
 
 @pytest.mark.parametrize("in_kind,m,k,n", [(lib.BF16, 8192, 8192, 8192), (lib.F32, 4096, 4096, 4096),
-                                           (lib.F16, 16384, 4096, 1024)])
+                                           (lib.F16, 16384, 4096, 1024), (lib.F16, 16384, 1024, 4096)])
 def test_config4_sweep_on_sampled_entries(in_kind, m, k, n):
     # The dense sweep at full size, seed 3: bf16 A, B ~ N(0, 1/sqrt(K)) (the
     # second parameter read as the standard deviation), f32 U(-1, 1), f16
-    # N(0, 1/sqrt(K)); 64 sampled rows against the f64 product.
+    # N(0, 1/sqrt(K)); 64 sampled rows against the f64 product.  The f16
+    # "skinny" product is checked both ways round: K = 4096 with N = 1024,
+    # and K = 1024 with N = 4096, the orientation bench.py times.
     rng = np.random.default_rng(3)
     if in_kind == lib.F32:
         a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
@@ -175,3 +177,40 @@ def test_config4_sweep_on_sampled_entries(in_kind, m, k, n):
     wa, wb = widen(in_kind, a[rows]), widen(in_kind, b)
     want = wa.astype(np.float64) @ wb.astype(np.float64)
     assert error(widen(in_kind, got[rows]), wa, wb, want) <= tolerance(in_kind, in_kind, k)
+
+
+def sampled_form(kind, form, m, k, n, rng, addend):
+    """A product in `form` on the GPU, and its f64 value on 48 sampled rows."""
+    a = to_kind(rng.standard_normal((m, k), dtype=np.float32) / np.float32(np.sqrt(k)), kind)
+    b = to_kind(rng.standard_normal((k, n), dtype=np.float32) / np.float32(np.sqrt(k)), kind)
+    c = to_kind(rng.uniform(-1, 1, (m, n)), kind) if addend else None
+    x = np.ascontiguousarray(a.T) if form == lib.LEFT else a
+    y = np.ascontiguousarray(b.T) if form == lib.RIGHT else b
+    got = product(kind, kind, form, x, y, m, k, n, addend=c)
+    rows = np.sort(rng.choice(m, 48, replace=False))
+    rows = np.unique(np.concatenate([rows, [0, m - 1]]))
+    wa, wb = widen(kind, a[rows]).astype(np.float64), widen(kind, b).astype(np.float64)
+    want = wa @ wb
+    scale = np.abs(wa) @ np.abs(wb)
+    if addend:
+        wc = widen(kind, c[rows]).astype(np.float64)
+        want, scale = want + wc, scale + np.abs(wc)
+    return widen(kind, got[rows]).astype(np.float64), want, scale
+
+
+@pytest.mark.parametrize("kind", [lib.BF16, lib.F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("form", [lib.PLAIN, lib.LEFT, lib.RIGHT], ids=["plain", "left", "right"])
+@pytest.mark.parametrize("addend", [False, True], ids=["product", "accumulate"])
+@pytest.mark.parametrize("m,k,n", [(4200, 128, 4200), (4200, 192, 4200), (4352, 1024, 4352), (4100, 1024, 4200)])
+def test_products_with_more_tiles_than_compute_units(kind, form, addend, m, k, n):
+    # More 256 x 256 tiles than the part's 256 CUs, so a block walks several
+    # tiles in turn: ragged edges in both dimensions (4200 = 16 x 256 + 104),
+    # whole tiles only (4352 = 17 x 256), and a ragged M with whole-tile
+    # columns; every form the tape's backward products take (LEFT is
+    # Aᵀ·B, RIGHT is A·Bᵀ, tape/mod.rs:1195-1246), with and without an
+    # addend.  The first and last rows are always sampled, so the edge tiles
+    # are checked.
+    rng = np.random.default_rng(m + 3 * k + 7 * n + 11 * form + int(addend))
+    got, want, scale = sampled_form(kind, form, m, k, n, rng, addend)
+    tol = tolerance(kind, kind, k) + (2.0 ** -8 if addend else 0.0)
+    assert np.max(np.abs(got - want) / scale) <= tol

@@ -55,6 +55,39 @@ def test_prefix_sum_of_half_integers_matches_the_host(n):
 
 
 @pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("special", ["inf", "-inf", "nan", "inf_then_minus_inf", "spike"])
+def test_prefix_sum_keeps_specials_out_of_earlier_outputs(kind, special):
+    # An infinity, a NaN or a very large element part-way into a tile (and in
+    # a later tile) must not reach the outputs before it: the host's running
+    # total is finite up to there (vector.rs:578-589).  Where the special
+    # sits and what follows it match the host's classes exactly; finite
+    # outputs stay within the f64 bound of the other prefix-sum tests.
+    n = 3 * 4096 + 123
+    x = np.full(n, 0.1, np.float32)
+    spots = [2050, 4096 + 3000]
+    if special == "spike":
+        x[spots[0]] = 1e9 if kind == lib.F32 else (60000.0 if kind == lib.F16 else 1e9)
+    elif special == "inf_then_minus_inf":
+        x[spots[0]], x[spots[1]] = np.inf, -np.inf
+    else:
+        x[spots[0]] = {"inf": np.inf, "-inf": -np.inf, "nan": np.nan}[special]
+    x = to_kind(x, kind)
+    got = widen(kind, device_prefix_sum(kind, x)).astype(np.float64)
+    host = widen(kind, oracle.prefix_sum(kind, x)).astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(host))
+    assert np.array_equal(np.isposinf(got), np.isposinf(host)) and np.array_equal(np.isneginf(got), np.isneginf(host))
+    assert np.all(np.isfinite(got[:spots[0]]))
+    finite = np.isfinite(host)
+    wide = widen(kind, x).astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        exact = np.cumsum(np.where(np.isfinite(wide), wide, 0.0))
+        scale = np.cumsum(np.abs(np.where(np.isfinite(wide), wide, 0.0)))
+    depth = 64 + n / 2 ** 20
+    bound = depth * 2.0 ** -24 * scale + UNIT[kind] * (np.abs(exact) + depth * 2.0 ** -24 * scale) + 2.0 ** -24
+    assert np.all(np.abs(got[finite] - exact[finite]) <= bound[finite])
+
+
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("n", [1, 300, 4097, 1 << 20, (1 << 22) + 17, (1 << 26) + 5])
 def test_prefix_sum_against_f64(kind, n):
     if kind != lib.F32 and n > (1 << 22) + 17:

@@ -9,6 +9,9 @@ training run within 1e-4 relative of the f32 restatement, which runs the
 same Adam program in f32.
 """
 
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -67,9 +70,28 @@ def test_ten_adam_steps_follow_the_restatement():
     net.close()
 
 
-def test_an_unreached_bias_gradient_is_a_zero_and_shapes_are_refused():
+def test_a_network_without_layers_is_refused():
     with pytest.raises(lib.HipError, match="no layers"):
         lib.Mlp([4], 3, [], [], np.zeros((4, 3)), np.zeros((4, 3)), 1e-3)
+
+
+def test_gradients_behind_a_dead_rectifier_are_zeros():
+    # A first layer whose pre-activations are all negative: the rectifier's
+    # share is 0 everywhere (MaxShare, kernels.rs:138-153), so no adjoint
+    # reaches that layer and its weight and bias gradients are exact zeros,
+    # while the last layer's are not.
+    widths, batch = (6, 5, 3), 4
+    weights, biases, x, y = network(widths, batch, 9)
+    biases[0] = np.full(widths[1], -100.0, np.float32)
+    net = lib.Mlp(widths, batch, weights, biases, x, y, 1e-3)
+    net.step(update=False)
+    w, b = net.gradients(0)
+    assert np.all(w == 0) and np.all(b == 0)
+    _, last_bias = net.gradients(1)
+    assert np.any(last_bias != 0)
+    _, _, gb = mlp.gradients([p.astype(np.float64) for p in weights], [p.astype(np.float64) for p in biases], x, y)
+    assert normwise(last_bias, gb[1]) <= 1e-4 and np.all(gb[0] == 0)
+    net.close()
 
 
 def test_config5_mlp_step_at_full_size():
@@ -90,3 +112,25 @@ def test_config5_mlp_step_at_full_size():
     net.step(update=False)
     assert net.loss() < first
     net.close()
+
+
+def test_config5_loss_curve_at_full_size():
+    # Configuration 5's ten training steps (the harness's `mlp_step`,
+    # benches/nn_ops.rs:875-921; Adam trajectories as in
+    # tests/tensor_autodiff.rs:596) against the f32 restatement's curve,
+    # kept as a fixture (tests/golden/make_mlp_curve.py writes it).  The
+    # GPU's products and sums add in another order than numpy's, nothing
+    # else differs; each loss must agree within 1e-4 relative.
+    curve = json.loads((Path(__file__).parent / "golden" / "mlp_config5_curve.json").read_text())
+    widths, batch = tuple(curve["widths"]), curve["batch"]
+    weights, biases = mlp.he_init(widths, curve["seed"])
+    x, y = mlp.batch_of(widths, batch, curve["seed"])
+    net = lib.Mlp(widths, batch, weights, biases, x, y, curve["rate"])
+    losses = []
+    for _ in range(curve["steps"]):
+        net.step()
+        losses.append(net.loss())
+    net.close()
+    want = np.array(curve["losses"])
+    print("losses", losses, "relative", (np.array(losses) - want) / want, flush=True)
+    assert np.allclose(losses, want, rtol=1e-4, atol=0), (losses, list(want))
