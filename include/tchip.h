@@ -374,6 +374,15 @@ int tc_arg_reduce(uint32_t dtype, const void* input, uint64_t input_len, const t
  * Metal's `reduce` returns it (tensors/backend.rs:813-818). */
 int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result);
 
+/* `tc_vector_reduce` that allocates nothing, with identical results: its
+ * block partials go to a 16 KiB array the library holds on each GPU (4096
+ * f32, enough for any length on parts of up to 1024 CUs; more partials are
+ * refused with TC_UNSUPPORTED).  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops).  Every call on one GPU shares that array, so calls that overlap in
+ * time on one GPU (other streams or threads) race. */
+int tc_vector_reduce_noalloc(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result);
+
 /* `Kernels::vector_moments` / `matrix_moments` (kernels.rs:1035-1038; Host
  * `moments_of`, statistics/mod.rs:419-441): the mean of all `n` elements into
  * the device f32 `result[0]` and the sum of squared deviations from it into

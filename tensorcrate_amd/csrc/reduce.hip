@@ -26,7 +26,17 @@
 
 #include <math.h>
 
+#include <mutex>
+#include <unordered_map>
+
 #include "common.hpp"
+
+// The whole-buffer fold's block partials for `tc_vector_reduce_noalloc`,
+// which allocates nothing: `total` launches at most four blocks a CU, so
+// 4096 floats (16 KiB a GPU, held until the process ends) cover parts of up
+// to 1024 CUs.
+constexpr uint32_t kStaticPartials = 4096;
+static __device__ __align__(256) float scratch[kStaticPartials];
 
 namespace tc {
 namespace {
@@ -842,14 +852,16 @@ __global__ void __launch_bounds__(256) finish_total_kernel(const float* __restri
     }
 }
 
+// Blocks of `total` for `n` elements: at most four a CU.
+inline uint32_t total_blocks(uint64_t n) { return grid_for(n, 256 * 8, 4); }
+
+// `total` with the blocks' partials in `partial` (total_blocks(n) floats),
+// which every block writes before the finishing wave reads it: nothing in it
+// has to start at zero.
 template <typename S, uint32_t OP, bool DOT>
-int total(const void* a, const void* b, uint64_t n, float* result, const char* what) {
-    TC_STREAM(s);
-    const uint32_t blocks = grid_for(n, 256 * 8, 4);
-    void* scratch = nullptr;
-    int status = tc_alloc(blocks * sizeof(float), &scratch);
-    if (status != TC_OK) return status;
-    float* partial = static_cast<float*>(scratch);
+int total_into(const void* a, const void* b, uint64_t n, float* result, float* partial, const char* what,
+               hipStream_t s) {
+    const uint32_t blocks = total_blocks(n);
     const S* pa = static_cast<const S*>(a);
     const S* pb = static_cast<const S*>(b);
     const bool packed = aligned16(a) && (!DOT || aligned16(b));
@@ -861,13 +873,70 @@ int total(const void* a, const void* b, uint64_t n, float* result, const char* w
     } else {
         total_kernel<S, OP, DOT, false, false><<<blocks, 256, 0, s>>>(pa, pb, n, partial);
     }
-    status = check_launch(what);
+    int status = check_launch(what);
     if (status == TC_OK) {
         finish_total_kernel<OP><<<1, 256, 0, s>>>(partial, blocks, result);
         status = check_launch(what);
     }
+    return status;
+}
+
+template <typename S, uint32_t OP, bool DOT>
+int total(const void* a, const void* b, uint64_t n, float* result, const char* what) {
+    TC_STREAM(s);
+    void* scratch = nullptr;
+    int status = tc_alloc(total_blocks(n) * sizeof(float), &scratch);
+    if (status != TC_OK) return status;
+    status = total_into<S, OP, DOT>(a, b, n, result, static_cast<float*>(scratch), what, s);
     tc_free(scratch);
     return status;
+}
+
+// ---- the whole-buffer fold without allocation ----------------------------
+//
+// Partials of `tc_vector_reduce_noalloc` live in the file-scope device array
+// `scratch` (top of this file), one copy per GPU.  Host code reaches a GPU's
+// copy only through the address hipGetSymbolAddress gives for it with that
+// device current, looked up on the entry point's first call on the device
+// and kept; the array's name in host code is a host-side stand-in, never
+// passed to a kernel.  Calls on one GPU share the array: calls that overlap
+// in time (on different streams or threads) race on it.
+
+std::mutex scratch_mutex;
+std::unordered_map<int, float*> scratch_by_device;
+
+int static_partials(float** out) {
+    int device = -1;
+    hipError_t error = hipGetDevice(&device);
+    if (error != hipSuccess) return fail(TC_DEVICE, std::string("vector_reduce_noalloc: ") + hipGetErrorString(error));
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    auto found = scratch_by_device.find(device);
+    if (found == scratch_by_device.end()) {
+        void* address = nullptr;
+        error = hipGetSymbolAddress(&address, HIP_SYMBOL(::scratch));
+        if (error != hipSuccess || address == nullptr) {
+            (void)hipGetLastError();
+            return fail(TC_DEVICE, std::string("vector_reduce_noalloc: the partials array of device ") +
+                                       std::to_string(device) + ": " + hipGetErrorString(error));
+        }
+        found = scratch_by_device.emplace(device, static_cast<float*>(address)).first;
+    }
+    *out = found->second;
+    return TC_OK;
+}
+
+template <typename S, uint32_t OP>
+int total_noalloc(const void* a, uint64_t n, float* result) {
+    TC_STREAM(s);
+    const uint32_t blocks = total_blocks(n);
+    if (blocks > kStaticPartials) {
+        return fail(TC_UNSUPPORTED, "vector_reduce_noalloc: " + std::to_string(blocks) + " partials, over the " +
+                                        std::to_string(kStaticPartials) + " the library holds");
+    }
+    float* partial = nullptr;
+    int status = static_partials(&partial);
+    if (status != TC_OK) return status;
+    return total_into<S, OP, false>(a, nullptr, n, result, partial, "vector_reduce_noalloc", s);
 }
 
 // The moments of a whole buffer, in the manner of `total`: each block folds
@@ -990,6 +1059,22 @@ int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, flo
 
 int tc_moments(uint32_t dtype, const void* a, uint64_t n, float* result) {
     TC_DISPATCH_FLOAT(dtype, "moments", S, return total_moments<S>(a, n, result));
+    return TC_OK;
+}
+
+int tc_vector_reduce_noalloc(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result) {
+    switch (op) {
+        case TC_REDUCE_SUM:
+            TC_DISPATCH_FLOAT(dtype, "vector_reduce_noalloc", S, return total_noalloc<S, TC_REDUCE_SUM>(a, n, result));
+            break;
+        case TC_REDUCE_MIN:
+            TC_DISPATCH_FLOAT(dtype, "vector_reduce_noalloc", S, return total_noalloc<S, TC_REDUCE_MIN>(a, n, result));
+            break;
+        case TC_REDUCE_MAX:
+            TC_DISPATCH_FLOAT(dtype, "vector_reduce_noalloc", S, return total_noalloc<S, TC_REDUCE_MAX>(a, n, result));
+            break;
+        default: return fail(TC_INVALID, "vector_reduce_noalloc: no Reduce " + std::to_string(op));
+    }
     return TC_OK;
 }
 

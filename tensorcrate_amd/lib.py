@@ -145,6 +145,7 @@ SIGNATURES = {
     "tc_reduce_axes": [u32, vp, u64, ctypes.POINTER(Split), u32, u32, u64, vp],
     "tc_arg_reduce": [u32, vp, u64, ctypes.POINTER(Split), u32, vp],
     "tc_vector_reduce": [u32, vp, u64, u32, vp],
+    "tc_vector_reduce_noalloc": [u32, vp, u64, u32, vp],
     "tc_dot": [u32, vp, vp, u64, vp],
     "tc_moments": [u32, vp, u64, vp],
     "tc_prefix_sum": [u32, vp, vp, u64],
