@@ -136,32 +136,52 @@ def host_matrix(kind: str, rows: int, cols: int, rng, sigma=None) -> np.ndarray:
     return values
 
 
-def gemm(kind: str, m: int, k: int, n: int, seed: int, sigma, steps: int, warmup: int) -> dict:
-    rng = np.random.default_rng(seed)
-    a = lib.Buffer.of(host_matrix(kind, m, k, rng, sigma))
-    b_host = host_matrix(kind, k, n, rng, sigma)
-    b = lib.Buffer.of(b_host)
-    del b_host
-    size = 4 if kind == "f32" else 2
-    c = lib.Buffer(m * n * size)
-    code = KIND[kind]
-    op = lambda: lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
-    ms = timed(op, steps, warmup)
-    # The product is one kernel launch, so the call's event time is the
-    # kernel's.
-    kernel_ms = ms
-    flops = 2.0 * m * n * k
-    achieved = flops / (kernel_ms * 1e-3) / 1e12
-    for buffer in (a, b, c):
-        buffer.free()
-    return {
-        "workload": f"{kind} GEMM {m}x{k}x{n}",
-        "value": flops / (ms * 1e-3) / 1e12,
-        "unit": "TFLOP/s",
-        "ms": ms,
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind], "unit": "TFLOP/s",
-                     "frac": achieved / MFMA_PEAK[kind], "traffic": None, "kernel_ms": kernel_ms},
-    }
+class Product:
+    """One product's operands, generated and uploaded to HBM, ready to time."""
+
+    def __init__(self, kind: str, m: int, k: int, n: int, seed: int, sigma):
+        rng = np.random.default_rng(seed)
+        self.kind, self.m, self.k, self.n = kind, m, k, n
+        self.a_host = host_matrix(kind, m, k, rng, sigma)
+        self.b_host = host_matrix(kind, k, n, rng, sigma)
+        self.a, self.b = lib.Buffer.of(self.a_host), lib.Buffer.of(self.b_host)
+        self.c = lib.Buffer(m * n * (4 if kind == "f32" else 2))
+
+    def time(self, steps: int, warmup: int, cpu: bool = False) -> dict:
+        kind, m, k, n = self.kind, self.m, self.k, self.n
+        a, b, c, code = self.a, self.b, self.c, KIND[kind]
+        op = lambda: lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
+        ms = timed(op, steps, warmup)
+        # The product is one kernel launch, so the call's event time is the
+        # kernel's.
+        kernel_ms = ms
+        flops = 2.0 * m * n * k
+        achieved = flops / (kernel_ms * 1e-3) / 1e12
+        for buffer in (a, b, c):
+            buffer.free()
+        baseline = None
+        if cpu:
+            from oracle import binding as oracle  # the CPU baseline's restatement
+            band = 64
+            band_a, b_host = np.ascontiguousarray(self.a_host[:band]), self.b_host
+            baseline = cpu_rate(lambda: oracle.matmul(code, band_a, b_host, band, k, n), 2.0 * band * k * n,
+                                "TFLOP/s", f"rows 0..{band} of A times all of B: the oracle's widen + single-thread "
+                                "AVX2 i-p-j FMA + round-once (compact.rs:232-262, simd_x86.rs:1302-1331), linear in M",
+                                1e12, min_seconds=1.0)
+        self.a_host = self.b_host = None
+        return {
+            "workload": f"{kind} GEMM {m}x{k}x{n}",
+            "cpu_baseline": baseline,
+            "value": flops / (ms * 1e-3) / 1e12,
+            "unit": "TFLOP/s",
+            "ms": ms,
+            "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind], "unit": "TFLOP/s",
+                         "frac": achieved / MFMA_PEAK[kind], "traffic": None, "kernel_ms": kernel_ms},
+        }
+
+
+def gemm(kind: str, m: int, k: int, n: int, seed: int, sigma, steps: int, warmup: int, cpu: bool = False) -> dict:
+    return Product(kind, m, k, n, seed, sigma).time(steps, warmup, cpu)
 
 
 def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> list[dict]:
@@ -169,12 +189,15 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
     epilogue (`tc_matmul_epilogue`, one kernel, the product never in HBM)
     and unfused (`tc_matmul`, then `tc_fused` over the stored product).
     Both lines count the product's 2 m n k FLOP only."""
+    from oracle import binding as oracle  # the CPU baseline's restatement
+
     rng = np.random.default_rng(11)
     code = KIND[kind]
     size = 4 if kind == "f32" else 2
-    x = lib.Buffer.of(host_matrix(kind, m, k, rng, 1 / np.sqrt(k)))
-    w = lib.Buffer.of(host_matrix(kind, k, n, rng, 1 / np.sqrt(k)))
-    bias = lib.Buffer.of(host_matrix(kind, 1, n, rng).reshape(n))
+    hx = host_matrix(kind, m, k, rng, 1 / np.sqrt(k))
+    hw = host_matrix(kind, k, n, rng, 1 / np.sqrt(k))
+    hbias = host_matrix(kind, 1, n, rng).reshape(n)
+    x, w, bias = lib.Buffer.of(hx), lib.Buffer.of(hw), lib.Buffer.of(hbias)
     out, product = lib.Buffer(m * n * size), lib.Buffer(m * n * size)
     program = [(0, 0, 0, 0, code, 0, 0.0), (0, 1, 1, 1, code, 0, 0.0), (2, lib.ADD, 2, 0, 1, 0, 0.0),
                (1, 0, 3, 0, 0, 0, 0.0), (4, lib.MAX, 4, 2, 3, 0, 0.0), (5, 0, 0, 4, code, 0, 0.0)]
@@ -195,6 +218,17 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
         lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, x.ptr, w.ptr, product.ptr)
 
     flops = 2.0 * m * n * k
+    # The CPU baseline: the oracle's product-then-program (the Host's
+    # run_matmul, fused/mod.rs:1143-1215) over a band of rows of x.
+    band = 32 if kind != "f32" else 128
+    band_x = np.ascontiguousarray(hx[:band])
+    band_places = [(0, 1, 1, [band], [n]), (0, 1, 0, [], [])]
+    band_out = np.empty(band * n, hx.dtype)
+    baseline = cpu_rate(lambda: oracle.matmul_epilogue(code, program, band_places, band_x, hw, band, k, n, [hbias],
+                                                       [band_out]),
+                        2.0 * band * k * n, "TFLOP/s",
+                        f"rows 0..{band} of x: the oracle's single-thread product, then the program, linear in M",
+                        1e12, min_seconds=1.0)
     lines = []
     for name, fn in (("in the product's epilogue", fused), ("unfused: product, then program", unfused),
                      ("the product alone", product_only)):
@@ -203,7 +237,8 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
         lines.append({"workload": f"{kind} dense layer relu(x w + b) {m}x{k}x{n}, {name}",
                       "value": achieved, "unit": "TFLOP/s", "ms": ms,
                       "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind],
-                                   "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK[kind], "traffic": None}})
+                                   "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK[kind], "traffic": None},
+                      "cpu_baseline": baseline})
     for buffer in (x, w, bias, out, product):
         buffer.free()
     return lines
@@ -273,6 +308,58 @@ def hbm_line(workload: str, nbytes: float, ms: float) -> dict:
                          "traffic": None}}
 
 
+def _host_cpu() -> tuple[str, int]:
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for text in f:
+                if text.startswith("model name"):
+                    model = text.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, len(os.sched_getaffinity(0))
+
+
+CPU_MODEL, NPROC = _host_cpu()
+
+
+# CPU baselines are measured after every GPU timing, so that the GPU runs
+# its workloads back to back: each line's record is filled in then.
+DEFERRED: list = []
+
+
+def cpu_rate(fn, work: float, unit: str, sample: str, scale: float, min_seconds: float = 0.4) -> dict:
+    """The oracle's C restatement of the Host (simd) algorithm (one thread)
+    run on this host: `fn` does `work` units of the line's metric per call;
+    called until `min_seconds` pass after one untimed call, the rate is
+    work x calls / seconds / `scale`.  Returns the line's record, filled in
+    by `run_cpu_baselines`."""
+    record = {"value": None, "unit": unit, "cores": 1, "kind": "port", "sample": sample, "cpu": CPU_MODEL,
+              "nproc": NPROC}
+    DEFERRED.append((record, fn, work, scale, min_seconds))
+    return record
+
+
+def run_cpu_baselines() -> None:
+    while DEFERRED:
+        record, fn, work, scale, min_seconds = DEFERRED.pop(0)
+        fn()
+        calls, start = 0, time.perf_counter()
+        while True:
+            fn()
+            calls += 1
+            elapsed = time.perf_counter() - start
+            if elapsed >= min_seconds:
+                break
+        record["value"] = work * calls / elapsed / scale
+
+
+def with_cpu(line: dict, baseline: dict) -> dict:
+    line["cpu_baseline"] = baseline
+    return line
+
+
 # Inputs smaller than the 256 MiB Infinity Cache would be read back from it
 # by back-to-back calls; rotating over copies that together pass 512 MiB keeps
 # every call's reads coming from HBM.
@@ -290,90 +377,164 @@ def rotating(inputs: list, call):
 
 
 def reductions(shape, seed: int, steps: int, warmup: int) -> list[dict]:
+    from oracle import binding as oracle  # the CPU baselines' restatement
+
     rng = np.random.default_rng(seed)
     host = rng.standard_normal(shape, dtype=np.float32)
     n = int(np.prod(shape))
     xs = rotation(lambda: Tensor.from_numpy(host), 4 * n)
     lines = []
     tag = "x".join(map(str, shape))
+    # The CPU baseline folds a leading slab of at most 8 Mi elements with the
+    # same axes: the Host walk costs the same per element at any size.
+    slab_rows = max(1, min(shape[0], (8 << 20) // (shape[1] * shape[2])))
+    slab = np.ascontiguousarray(host[:slab_rows])
+    slab_shape = [slab_rows, shape[1], shape[2]]
+    strides = [shape[1] * shape[2], shape[2], 1]
+    sample = f"the oracle's sequential Host walk over [{slab_rows},{shape[1]},{shape[2]}]" + \
+        ("" if slab_rows == shape[0] else f", the leading slab of [{tag}]")
+    fold_code = {"sum": (lib.FOLD, lib.SUM, 0), "max": (lib.FOLD, lib.RMAX, 0), "min": (lib.FOLD, lib.RMIN, 0)}
     for name, axes, results in [("sum", [2], n // shape[2]), ("max", [2], n // shape[2]),
                                 ("min", [2], n // shape[2]), ("mean", [2], n // shape[2]), ("var", [2], n // shape[2]),
                                 ("sum", [0, 1], shape[2]), ("max", [0, 1], shape[2]), ("var", [0, 1], shape[2])]:
         fn = rotating(xs, lambda x: getattr(x, f"{name}_axes")(axes))
         ms = timed_graph(fn, max(steps, 2 * len(xs)), warmup)
-        lines.append(hbm_line(f"{name}_axes {axes} of f32 [{tag}]", 4 * (n + results), ms))
-    for name in ("argmax", "argmin"):
+        line = hbm_line(f"{name}_axes {axes} of f32 [{tag}]", 4 * (n + results), ms)
+        depth = int(np.prod([slab_shape[a] for a in axes]))
+        kind, op, divisor = fold_code.get(name, (lib.MEAN if name == "mean" else lib.VARIANCE, 0,
+                                                 0 if name == "mean" else depth))
+        slab_results = int(np.prod(slab_shape)) // depth
+        work = 4.0 * (slab.size + slab_results)
+        lines.append(with_cpu(line, cpu_rate(
+            lambda: oracle.reduce(lib.F32, slab, slab_shape, 0, strides, axes, kind, op, divisor),
+            work, "GB/s", sample, 1e9)))
+    for name, op in (("argmax", lib.RMAX), ("argmin", lib.RMIN)):
         fn = rotating(xs, lambda x: getattr(x, name)(1))
         ms = timed_graph(fn, max(steps, 2 * len(xs)), warmup)
-        lines.append(hbm_line(f"{name} axis 1 of f32 [{tag}]", 4 * n + 4 * (n // shape[1]), ms))
+        line = hbm_line(f"{name} axis 1 of f32 [{tag}]", 4 * n + 4 * (n // shape[1]), ms)
+        work = 4.0 * slab.size + 4.0 * (slab.size // shape[1])
+        lines.append(with_cpu(line, cpu_rate(
+            lambda: oracle.arg_reduce(lib.F32, slab, slab_shape, 0, strides, 1, op), work, "GB/s", sample, 1e9)))
     return lines
 
 
 def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
+    from oracle import binding as oracle  # the CPU baselines' restatement
+
     rng = np.random.default_rng(2)
     shape = (256, 512, 512)
-    x = Tensor.from_numpy(rng.standard_normal(shape, dtype=np.float32))
-    y = Tensor.from_numpy(rng.uniform(-1, 1, (1, 512, 1)).astype(np.float32))
-    z = Tensor.from_numpy(rng.uniform(-1, 1, (256, 1, 512)).astype(np.float32))
+    hx = rng.standard_normal(shape, dtype=np.float32)
+    hy = rng.uniform(-1, 1, (1, 512, 1)).astype(np.float32)
+    hz = rng.uniform(-1, 1, (256, 1, 512)).astype(np.float32)
+    x, y, z = Tensor.from_numpy(hx), Tensor.from_numpy(hy), Tensor.from_numpy(hz)
     n = 256 * 512 * 512
     mib = 4 * n
+    # CPU baselines run the oracle's Host restatements over the leading
+    # [32,512,512] slab (an eighth; the walks cost the same per element).
+    rows = 32
+    sx, sz = np.ascontiguousarray(hx[:rows]), np.ascontiguousarray(hz[:rows])
+    sn = rows * 512 * 512
+    slab = f"the oracle's Host walk over the leading [{rows},512,512] slab"
     lines = []
     ms = timed_graph(lambda: x * y, steps, warmup)
-    lines.append(hbm_line("x*y, f32 [256,512,512] x [1,512,1]", 2 * mib + 4 * 512, ms))
+    lines.append(with_cpu(hbm_line("x*y, f32 [256,512,512] x [1,512,1]", 2 * mib + 4 * 512, ms), cpu_rate(
+        lambda: oracle.binary(lib.F32, lib.ARITHMETIC, lib.MUL, [rows, 512, 512], sx, 0, [262144, 512, 1], hy, 0,
+                              [0, 1, 0]), 8.0 * sn + 4 * 512, "GB/s", slab + " (strided.rs:29-78)", 1e9)))
     t = x * y
+    st = np.ascontiguousarray(t.to_numpy()[:rows])
     ms = timed_graph(lambda: t + z, steps, warmup)
-    lines.append(hbm_line("t+z, f32 [256,512,512] + [256,1,512]", 2 * mib + 4 * 256 * 512, ms))
+    lines.append(with_cpu(hbm_line("t+z, f32 [256,512,512] + [256,1,512]", 2 * mib + 4 * 256 * 512, ms), cpu_rate(
+        lambda: oracle.binary(lib.F32, lib.ARITHMETIC, lib.ADD, [rows, 512, 512], st, 0, [262144, 512, 1], sz, 0,
+                              [512, 0, 1]), 8.0 * sn + 4 * rows * 512, "GB/s", slab + " (strided.rs:29-78)", 1e9)))
     out = t + z
+    so = np.ascontiguousarray(out.to_numpy()[:rows])
     ms = timed_graph(lambda: out.permute([0, 2, 1]).contiguous(), steps, warmup)
-    lines.append(hbm_line("permute(0,2,1).contiguous, f32 [256,512,512]", 2 * mib, ms))
+    lines.append(with_cpu(hbm_line("permute(0,2,1).contiguous, f32 [256,512,512]", 2 * mib, ms), cpu_rate(
+        lambda: oracle.strided_copy(so, [rows, 512, 512], 0, [262144, 1, 512]), 8.0 * sn, "GB/s",
+        slab + " (backend.rs:255-274)", 1e9)))
     p = out.permute([0, 2, 1]).contiguous()
+    sp = np.ascontiguousarray(p.to_numpy()[:rows])
     # The slice reads 128 MiB, which the Infinity Cache could hold: rotate.
     sources = rotation(lambda: out.permute([0, 2, 1]).contiguous(), mib // 2)
     ms = timed_graph(rotating(sources, lambda q: q.slice(1, 128, 384).contiguous()), steps, warmup)
-    lines.append(hbm_line("slice [:,128:384,:].contiguous, f32", mib, ms))
+    lines.append(with_cpu(hbm_line("slice [:,128:384,:].contiguous, f32", mib, ms), cpu_rate(
+        lambda: oracle.strided_copy(sp, [rows, 256, 512], 128 * 512, [262144, 512, 1]), 4.0 * sn, "GB/s",
+        slab + " (backend.rs:255-274)", 1e9)))
     del sources
     halves = p.chunk(1, 2)
     ms = timed_graph(lambda: Tensor.concat(halves, 1), steps, warmup)
-    lines.append(hbm_line("concat of two [256,256,512] halves on axis 1, f32", 2 * mib, ms))
+
+    def assemble_slab():
+        # backend.rs:303-323: each half's region copied into its place.
+        target = np.empty((rows, 512, 512), np.float32)
+        for half in range(2):
+            oracle.strided_write(sp, target, [rows, 256, 512], half * 256 * 512, [262144, 512, 1], half * 256 * 512,
+                                 [262144, 512, 1])
+        return target
+    lines.append(with_cpu(hbm_line("concat of two [256,256,512] halves on axis 1, f32", 2 * mib, ms), cpu_rate(
+        assemble_slab, 8.0 * sn, "GB/s", slab + " (backend.rs:303-323)", 1e9)))
     a, b = x.storage, t.storage
     dst = lib.Buffer(mib)
     ms = timed_graph(lambda: lib.call("tc_elementwise", lib.F32, lib.ADD, a.ptr, b.ptr, dst.ptr, n), steps, warmup)
-    lines.append(hbm_line("same-shape add, f32 64 Mi elements", 3 * mib, ms))
+    ea, eb = sx.reshape(-1), st.reshape(-1)
+    lines.append(with_cpu(hbm_line("same-shape add, f32 64 Mi elements", 3 * mib, ms), cpu_rate(
+        lambda: oracle.elementwise(lib.F32, lib.ARITHMETIC, lib.ADD, ea, eb), 12.0 * sn, "GB/s",
+        f"the oracle's elementwise loop over {sn} elements, one thread (the Host splits this over all cores, "
+        "simd_dispatch.rs:54-75)", 1e9)))
     return lines
 
 
 def vector_products(steps: int, warmup: int) -> list[dict]:
     """GEMV, vecmat and dot at the bandwidth sizes of configs a11, and the
     4096 x 4096 transpose of a12; inputs rotate past the Infinity Cache."""
+    from oracle import binding as oracle  # the CPU baselines' restatement
+
     rng = np.random.default_rng(5)
     rows = cols = 8192
     mbytes = 4 * rows * cols
     host = rng.standard_normal((rows, cols), dtype=np.float32)
     mats = rotation(lambda: lib.Buffer.of(host), mbytes)
-    v = lib.Buffer.of(rng.standard_normal(cols, dtype=np.float32))
+    hv = rng.standard_normal(cols, dtype=np.float32)
+    v = lib.Buffer.of(hv)
     y = lib.Buffer(4 * rows)
+    band = 1024  # CPU baselines: a band of 1024 rows of the matrix
+    hb = np.ascontiguousarray(host[:band])
+    sample = f"the oracle's Host loop over rows 0..{band} of the [{rows}x{cols}] matrix"
     lines = []
     ms = timed_graph(rotating(mats, lambda m: lib.call("tc_matvec", lib.F32, 0, rows, cols, m.ptr, v.ptr, y.ptr)),
                      max(steps, 2 * len(mats)), warmup)
-    lines.append(hbm_line(f"matvec, f32 [{rows}x{cols}] . [{cols}]", mbytes + 4 * (rows + cols), ms))
+    lines.append(with_cpu(hbm_line(f"matvec, f32 [{rows}x{cols}] . [{cols}]", mbytes + 4 * (rows + cols), ms),
+                          cpu_rate(lambda: oracle.matvec(lib.F32, hb, hv), 4.0 * (band * cols + band + cols), "GB/s",
+                                   sample + " (simd_dispatch.rs:626-659)", 1e9)))
     ms = timed_graph(rotating(mats, lambda m: lib.call("tc_vecmat", lib.F32, rows, cols, v.ptr, m.ptr, y.ptr)),
                      max(steps, 2 * len(mats)), warmup)
-    lines.append(hbm_line(f"vecmat, f32 [{rows}] . [{rows}x{cols}]", mbytes + 4 * (rows + cols), ms))
+    hw = np.ascontiguousarray(hv[:band])
+    lines.append(with_cpu(hbm_line(f"vecmat, f32 [{rows}] . [{rows}x{cols}]", mbytes + 4 * (rows + cols), ms),
+                          cpu_rate(lambda: oracle.vecmat(lib.F32, hw, hb), 4.0 * (band * cols + band + cols), "GB/s",
+                                   sample + " (vector.rs:491)", 1e9)))
     del mats
     n = 64 << 20
-    a = lib.Buffer.of(rng.standard_normal(n, dtype=np.float32))
-    b = lib.Buffer.of(rng.standard_normal(n, dtype=np.float32))
+    ha, hb2 = rng.standard_normal(n, dtype=np.float32), rng.standard_normal(n, dtype=np.float32)
+    a, b = lib.Buffer.of(ha), lib.Buffer.of(hb2)
     result = lib.Buffer(4)
     ms = timed_graph(lambda: lib.call("tc_dot", lib.F32, a.ptr, b.ptr, n, result.ptr), steps, warmup)
-    lines.append(hbm_line("dot, f32 64 Mi elements", 8 * n, ms))
+    da, db = np.ascontiguousarray(ha[: 8 << 20]), np.ascontiguousarray(hb2[: 8 << 20])
+    lines.append(with_cpu(hbm_line("dot, f32 64 Mi elements", 8 * n, ms),
+                          cpu_rate(lambda: oracle.dot(lib.F32, da, db), 8.0 * da.size, "GB/s",
+                                   "the oracle's eight-lane AVX2 dot (simd_x86.rs:57-101) over the first 8 Mi pairs",
+                                   1e9)))
     del a, b
     side = 4096
     tbytes = 4 * side * side
-    srcs = rotation(lambda: lib.Buffer.of(rng.standard_normal((side, side), dtype=np.float32)), tbytes)
+    first = rng.standard_normal((side, side), dtype=np.float32)
+    srcs = rotation(lambda: lib.Buffer.of(first), tbytes)
     dst = lib.Buffer(tbytes)
     ms = timed_graph(rotating(srcs, lambda m: lib.call("tc_transpose", 4, side, side, m.ptr, dst.ptr)),
                      max(steps, 2 * len(srcs)), warmup)
-    lines.append(hbm_line(f"transpose, f32 [{side}x{side}]", 2 * tbytes, ms))
+    lines.append(with_cpu(hbm_line(f"transpose, f32 [{side}x{side}]", 2 * tbytes, ms),
+                          cpu_rate(lambda: oracle.transpose(first), 2.0 * tbytes, "GB/s",
+                                   f"the oracle's transpose of the whole [{side}x{side}] matrix, one thread "
+                                   "(the Host blocks 32 x 32 over all cores, matrix.rs:1173-1206)", 1e9)))
     return lines
 
 
@@ -385,19 +546,33 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
     its nine f32 products; the Adam step alone is timed as its own line."""
     from oracle import mlp  # the synthetic network's generator only
 
+    from oracle import binding as oracle  # the CPU baselines' restatement
+    from tensorcrate_amd.optim import adam_program, identity_place
+
     widths, batch = (1024, 4096, 4096, 1024), 4096
     weights, biases = mlp.he_init(widths, 4)
     x, y = mlp.batch_of(widths, batch, 4)
     net = lib.Mlp(widths, batch, weights, biases, x, y, 1e-3)
-    del weights, biases, x, y
     ms = timed(net.step, steps, warmup)
     flops = sum(2.0 * widths[l] * widths[l + 1] * batch for l in range(3)) * 3
     net.close()
     achieved = flops / (ms * 1e-3) / 1e12
+    # The CPU baseline: the step's first product (W0 . X) on a band of W0's
+    # rows through the oracle's single-thread f32 Host product, its rate
+    # scaled to the step's 618.5 GFLOP, which the nine products dominate.
+    band = 64
+    w_band = np.ascontiguousarray(weights[1][:band])
+    right = np.ascontiguousarray(weights[1])  # a 4096 x 4096 operand of the step's largest products
+    baseline = cpu_rate(lambda: oracle.matmul(lib.F32, w_band, right, band, widths[1], widths[2]),
+                        2.0 * band * widths[1] * widths[2], "steps/s",
+                        f"rows 0..{band} of W1 times a {widths[1]}x{widths[2]} operand: the oracle's single-thread "
+                        "AVX2 i-p-j f32 product, its rate divided by the step's 618.5 GFLOP", flops, min_seconds=1.0)
+    del weights, biases, x, y
     lines = [{"workload": "MLP training step 1024-4096-4096-1024, batch 4096, f32, tape + Adam (configs[4])",
               "value": 1e3 / ms, "unit": "steps/s", "ms": ms,
               "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK["f32"], "unit": "TFLOP/s",
-                           "frac": achieved / MFMA_PEAK["f32"], "traffic": None}}]
+                           "frac": achieved / MFMA_PEAK["f32"], "traffic": None},
+              "cpu_baseline": baseline}]
     # The Adam step over all 25,175,040 parameters as one tensor: reads the
     # gradient, parameters and both moments, writes the last three.
     n = sum(widths[l] * widths[l + 1] + widths[l + 1] for l in range(3))
@@ -410,7 +585,15 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
     # keeps its own step's constants, and the replay times the kernels back
     # to back rather than this script's per-step host work.
     ms = timed_graph(lambda: rule.update(params, grads, 1, n), steps, warmup)
-    lines.append(hbm_line(f"Adam update, {n} f32 parameters (fused program)", 7 * 4 * n, ms))
+    sample_n = 1 << 20
+    code, loads = adam_program(True, lib.F32, 1e-3, 0.9, 0.999, 1e-8, 2)
+    hp = np.full(sample_n, 0.5, np.float32)
+    hg, hm, hv = np.full(sample_n, 0.25, np.float32), np.zeros(sample_n, np.float32), np.zeros(sample_n, np.float32)
+    adam_places = [identity_place(1, sample_n)] * loads
+    lines.append(with_cpu(hbm_line(f"Adam update, {n} f32 parameters (fused program)", 7 * 4 * n, ms), cpu_rate(
+        lambda: oracle.fused(lib.F32, code, adam_places, [hg, hp, hm, hv], [hp, hm, hv], 1, sample_n),
+        7.0 * 4 * sample_n, "GB/s", f"the oracle's program interpreter over {sample_n} parameters, one thread "
+        "(the Host's tile interpreter splits over all cores, fused/mod.rs:4255-4290)", 1e9)))
     return lines
 
 
@@ -462,7 +645,8 @@ def cpu_baseline(m: int, k: int, n: int) -> dict:
     flops = 2.0 * rows * k * n
     return {"value": flops / seconds / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"rows 0..{rows} of A ({rows} of {m}) times all of B, bf16 {m}x{k}x{n}: the oracle's "
-                      f"widen + single-thread AVX2 i-p-j FMA + round-once, {seconds:.1f} s, scaled linearly in M"}
+                      f"widen + single-thread AVX2 i-p-j FMA + round-once, {seconds:.1f} s, scaled linearly in M",
+            "cpu": CPU_MODEL, "nproc": NPROC}
 
 
 def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
@@ -470,9 +654,9 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
     workloads = []
     if "gemm" in groups:
         log("f32 GEMM 4096^3 ...")
-        workloads.append(gemm("f32", 4096, 4096, 4096, 3, None, steps, warmup))
+        workloads.append(gemm("f32", 4096, 4096, 4096, 3, None, steps, warmup, cpu=True))
         log("f16 GEMM 16384x4096x1024 ...")
-        workloads.append(gemm("f16", 16384, 1024, 4096, 3, 1 / np.sqrt(1024), steps, warmup))
+        workloads.append(gemm("f16", 16384, 1024, 4096, 3, 1 / np.sqrt(1024), steps, warmup, cpu=True))
     if "reductions" in groups:
         log("reductions ...")
         workloads += reductions((64, 128, 1024), 1, steps, warmup)
@@ -483,10 +667,6 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
     if "vectors" in groups:
         log("matvec, vecmat, dot, transpose ...")
         workloads += vector_products(steps, warmup)
-    if "fusion" in groups:
-        log("dense layers, fused and unfused ...")
-        workloads += dense_layer("bf16", 8192, 8192, 8192, steps, warmup)
-        workloads += dense_layer("f32", 4096, 1024, 4096, steps, warmup)
     if "transfer" in groups:
         log("host transfers and TCR1 loads ...")
         workloads += transfers()
@@ -496,6 +676,12 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
         # appearance, and the streaming one (the 4096 x 4096 weight) appears
         # once a step from the second step on.
         workloads += mlp_step(max(steps // 4, 3), 3)
+    if "fusion" in groups:
+        # Last: the bf16 8192^3 products, so that a headline timed next runs
+        # in the power state of sustained matrix-core work.
+        log("dense layers, fused and unfused ...")
+        workloads += dense_layer("f32", 4096, 1024, 4096, steps, warmup)
+        workloads += dense_layer("bf16", 8192, 8192, 8192, steps, warmup)
     for line in workloads:
         log(f"  {line['workload']}: {line['value']:.1f} {line['unit']} ({line['roofline']['frac'] * 100:.1f}%)")
     return workloads
@@ -534,21 +720,33 @@ def main() -> int:
             print(f"bench.py: no workload group {sorted(unknown)}", file=sys.stderr)
             return 2
         workloads = secondary(groups, args.steps, args.warmup)
+        if not args.no_cpu:
+            run_cpu_baselines()
         print(json.dumps(workloads), flush=True)
         return 0
 
     m = k = n = 8192
-    log("bf16 GEMM 8192^3 ...")
-    head = gemm("bf16", m, k, n, 3, 1 / np.sqrt(k), args.steps, args.warmup)
-    log(f"  {head['value']:.1f} TFLOP/s ({head['ms']:.3f} ms/step), kernel {head['roofline']['achieved']:.1f}")
+    # The headline's operands are made and uploaded first; the other
+    # workloads then run, the bf16 8192^3 dense layers last, and the
+    # headline's W warmup and K timed steps follow them at once, so the timed
+    # steps see the part's sustained-load clock rather than the ramp a cold
+    # part goes through over its first few dozen dense products.
+    head_operands = Product("bf16", m, k, n, 3, 1 / np.sqrt(k))
     workloads = []
     if not args.quick:
         workloads = secondary({"gemm", "reductions", "copies", "vectors", "fusion", "mlp"}, args.steps, args.warmup)
+    log("bf16 GEMM 8192^3 ...")
+    head = head_operands.time(args.steps, args.warmup)
+    log(f"  {head['value']:.1f} TFLOP/s ({head['ms']:.3f} ms/step), kernel {head['roofline']['achieved']:.1f}")
     baseline = None
     if not args.quick and not args.no_cpu:
-        log("CPU baseline ...")
+        log("CPU baselines ...")
+        run_cpu_baselines()
         baseline = cpu_baseline(m, k, n)
         log(f"  {baseline['value'] * 1e3:.2f} GFLOP/s on one core")
+    for w in workloads:
+        if w.get("cpu_baseline") is not None and w["cpu_baseline"]["value"] is None:
+            w["cpu_baseline"] = None
     line = {
         "metric": METRIC,
         "value": head["value"],

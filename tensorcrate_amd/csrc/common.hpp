@@ -76,6 +76,12 @@ int matmul_program(uint32_t dtype, uint64_t m, uint64_t k, uint64_t n, const voi
                    const void* const* inputs, uint32_t input_count, void* const* outputs, uint32_t output_count,
                    bool* fused);
 
+// The matrix-vector kernels (gemv.hip): out[rows] (+)= matrix[rows x cols] .
+// vector[cols], or with `row_vector` out[cols] (+)= vector[rows] .
+// matrix[rows x cols]; `dtype` operands and output.
+int vector_product(uint32_t dtype, bool row_vector, bool accumulate, uint64_t rows, uint64_t cols, const void* matrix,
+                   const void* vector, void* out);
+
 // Runtime compilation (fused.hip).  The straight-line body of an
 // epilogue's `group(live, row, col, N, product)` over `elems` elements, for
 // `code` computing in `dtype` with loads through `places` (their folded axes

@@ -424,6 +424,22 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
     }
     const S* pa = static_cast<const S*>(a);
     const S* pb = static_cast<const S*>(b);
+    if constexpr (std::is_same<S, O>::value) {
+        // One output column or row: the matrix-vector kernels, which spread
+        // it over the whole part where a product's tiles would leave all but
+        // a few CUs idle (MetalBuffer::product_into, metal/ops.rs:176-200).
+        // Each form's vector is contiguous: B's one column (PLAIN, RIGHT),
+        // A's one row (PLAIN, LEFT).
+        if (k > 0 && (n == 1 || m == 1)) {
+            const uint32_t dtype = Elem<S>::dtype;
+            if (n == 1) {
+                if (transposed == TC_LEFT) return vector_product(dtype, true, accumulate, k, m, a, b, c);  // b . A
+                return vector_product(dtype, false, accumulate, m, k, a, b, c);                            // A . b
+            }
+            if (transposed == TC_RIGHT) return vector_product(dtype, false, accumulate, n, k, b, a, c);    // B . a
+            return vector_product(dtype, true, accumulate, k, n, b, a, c);                                 // a . B
+        }
+    }
     if (k < 8) {
         O* pc = static_cast<O*>(c);
         if (transposed == TC_PLAIN) return launch_short_k<S, O, true, false>(pa, pb, pc, m, k, n, accumulate, s);

@@ -88,7 +88,7 @@ template <typename S, int V, int W>
 __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, const S* __restrict__ m,
                                                      S* __restrict__ y, float* __restrict__ partial,
                                                      uint64_t rows, uint64_t cols, uint64_t tiles,
-                                                     uint64_t splits, uint64_t per_split) {
+                                                     uint64_t splits, uint64_t per_split, bool accumulate) {
     using E = Elem<S>;
     constexpr int kTile = 64 * V * W;
     __shared__ float stage[kGroups][kTile];
@@ -173,6 +173,7 @@ __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, co
 #pragma unroll
                 for (int g = 1; g < kGroups; g++) total += stage[g][u * 64 * V + lane * V + k];
                 if (splits == 1) {
+                    if (accumulate) total += E::widen(y[col + k]);
                     y[col + k] = E::narrow(total);
                 } else {
                     partial[split * cols + col + k] = total;
@@ -187,7 +188,7 @@ __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, co
 // flight), then the quarters in order, so the sum does not depend on timing.
 template <typename S>
 __global__ void __launch_bounds__(256) vecmat_combine_kernel(const float* __restrict__ partial, S* __restrict__ y,
-                                                             uint64_t cols, uint64_t splits) {
+                                                             uint64_t cols, uint64_t splits, bool accumulate) {
     __shared__ float quarter[kGroups][64];
     const int lane = threadIdx.x % 64;
     const int wave = threadIdx.x / 64;
@@ -213,6 +214,7 @@ __global__ void __launch_bounds__(256) vecmat_combine_kernel(const float* __rest
         float sum = quarter[0][lane];
 #pragma unroll
         for (int g = 1; g < kGroups; g++) sum += quarter[g][lane];
+        if (accumulate) sum += Elem<S>::widen(y[c]);
         y[c] = Elem<S>::narrow(sum);
     }
 }
@@ -235,7 +237,7 @@ int matvec_typed(bool accumulate, uint64_t rows, uint64_t cols, const void* m, c
 }
 
 template <typename S, int V, int W>
-int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, hipStream_t s) {
+int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, bool accumulate, hipStream_t s) {
     const uint64_t tiles = (cols + 64 * V * W - 1) / (64 * V * W);
     const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
     uint64_t splits = 1;
@@ -255,10 +257,10 @@ int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, hi
         partial = static_cast<float*>(scratch);
     }
     vecmat_kernel<S, V, W><<<static_cast<uint32_t>(tiles * splits), 256, 0, s>>>(v, m, y, partial, rows, cols,
-                                                                                 tiles, splits, per_split);
+                                                                                 tiles, splits, per_split, accumulate);
     int status = check_launch("vecmat");
     if (status == TC_OK && splits > 1) {
-        vecmat_combine_kernel<S><<<static_cast<uint32_t>((cols + 63) / 64), 256, 0, s>>>(partial, y, cols, splits);
+        vecmat_combine_kernel<S><<<static_cast<uint32_t>((cols + 63) / 64), 256, 0, s>>>(partial, y, cols, splits, accumulate);
         status = check_launch("vecmat");
     }
     if (partial != nullptr) tc_free(partial);
@@ -266,7 +268,7 @@ int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, hi
 }
 
 template <typename S>
-int vecmat_typed(uint64_t rows, uint64_t cols, const void* v, const void* m, void* y) {
+int vecmat_typed(bool accumulate, uint64_t rows, uint64_t cols, const void* v, const void* m, void* y) {
     TC_STREAM(s);
     if (cols == 0) return TC_OK;
     const S* pv = static_cast<const S*>(v);
@@ -277,11 +279,22 @@ int vecmat_typed(uint64_t rows, uint64_t cols, const void* v, const void* m, voi
     // (2 or 4 KiB runs of a row per wave) were slower, 68% and 66% of HBM
     // against 70%, their extra row splits costing more than the longer runs
     // gain.
-    if (cols % V == 0 && aligned16(m)) return launch_vecmat<S, V, 1>(pv, pm, py, rows, cols, s);
-    return launch_vecmat<S, 1, 1>(pv, pm, py, rows, cols, s);
+    if (cols % V == 0 && aligned16(m)) return launch_vecmat<S, V, 1>(pv, pm, py, rows, cols, accumulate, s);
+    return launch_vecmat<S, 1, 1>(pv, pm, py, rows, cols, accumulate, s);
 }
 
 }  // namespace
+
+int vector_product(uint32_t dtype, bool row_vector, bool accumulate, uint64_t rows, uint64_t cols, const void* matrix,
+                   const void* vector, void* out) {
+    if (row_vector) {
+        TC_DISPATCH_FLOAT(dtype, "vecmat", S, return vecmat_typed<S>(accumulate, rows, cols, vector, matrix, out));
+    } else {
+        TC_DISPATCH_FLOAT(dtype, "matvec", S, return matvec_typed<S>(accumulate, rows, cols, matrix, vector, out));
+    }
+    return TC_OK;
+}
+
 }  // namespace tc
 
 using namespace tc;
@@ -295,7 +308,7 @@ int tc_matvec(uint32_t dtype, int accumulate, uint64_t rows, uint64_t cols, cons
 }
 
 int tc_vecmat(uint32_t dtype, uint64_t rows, uint64_t cols, const void* vector, const void* matrix, void* out) {
-    TC_DISPATCH_FLOAT(dtype, "vecmat", S, return vecmat_typed<S>(rows, cols, vector, matrix, out));
+    TC_DISPATCH_FLOAT(dtype, "vecmat", S, return vecmat_typed<S>(false, rows, cols, vector, matrix, out));
     return TC_OK;
 }
 

@@ -214,3 +214,27 @@ def test_products_with_more_tiles_than_compute_units(kind, form, addend, m, k, n
     got, want, scale = sampled_form(kind, form, m, k, n, rng, addend)
     tol = tolerance(kind, kind, k) + (2.0 ** -8 if addend else 0.0)
     assert np.max(np.abs(got - want) / scale) <= tol
+
+
+@pytest.mark.parametrize("kind", [lib.F32, lib.BF16, lib.F16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("form", [lib.PLAIN, lib.LEFT, lib.RIGHT], ids=["plain", "left", "right"])
+@pytest.mark.parametrize("m,k,n", [(3000, 700, 1), (1, 700, 3000), (1, 4096, 1), (257, 8, 1), (1, 33, 129)])
+def test_one_row_or_one_column_products(kind, form, m, k, n):
+    # A product with one column or one row of output runs on the
+    # matrix-vector kernels (MetalBuffer::product_into, metal/ops.rs:176-200),
+    # in every form and with an addend, against f64.
+    rng = np.random.default_rng(m + 7 * k + 11 * n + form)
+    a = to_kind(rng.uniform(-1, 1, (m, k)), kind)
+    b = to_kind(rng.uniform(-1, 1, (k, n)), kind)
+    c = to_kind(rng.uniform(-1, 1, (m, n)), kind)
+    x = np.ascontiguousarray(a.T) if form == lib.LEFT else a
+    y = np.ascontiguousarray(b.T) if form == lib.RIGHT else b
+    wa, wb, wc = (widen(kind, v).astype(np.float64) for v in (a, b, c))
+    unit = {lib.F32: 2.0 ** -24, lib.F16: 2.0 ** -11, lib.BF16: 2.0 ** -8}[kind]
+    scale = np.abs(wa) @ np.abs(wb)
+    got = widen(kind, product(kind, kind, form, x, y, m, k, n)).astype(np.float64)
+    want = wa @ wb
+    assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(k) * scale + unit * np.abs(want) + 1e-30)
+    got = widen(kind, product(kind, kind, form, x, y, m, k, n, addend=c)).astype(np.float64)
+    want = want + wc
+    assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(k) * scale + unit * (np.abs(want) + np.abs(wc)) + 1e-30)
