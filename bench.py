@@ -598,10 +598,12 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
 
 
 def traffic_probe() -> None:
-    """A short run for ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``: three
-    plain contiguous copies of 1 GiB through ``tc_strided_copy`` (the rows
-    kernel; 1 GiB read and 1 GiB written each, the counters' calibration),
-    then three launches of the headline product."""
+    """A short run for ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``, each
+    kernel launched eagerly so every dispatch is one workload's: three plain
+    contiguous copies of 1 GiB through ``tc_strided_copy`` (the rows kernel;
+    1 GiB read and 1 GiB written each, the counters' calibration), three
+    launches of the headline product, then one call of every bandwidth
+    workload in the order ``TRAFFIC_PROBE`` lists them."""
     n = 1 << 28
     src, dst = lib.Buffer(4 * n), lib.Buffer(4 * n)
     lib.call("tc_fill", src.ptr, n, 4, ctypes.byref(ctypes.c_float(1.0)))
@@ -620,7 +622,66 @@ def traffic_probe() -> None:
     for _ in range(3):
         lib.call("tc_matmul", lib.BF16, lib.BF16, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
     lib.sync()
+    for buffer in (a, b, c):
+        buffer.free()
+    for workload, run in traffic_workloads():
+        log(f"probe: {workload}")
+        run()
+        lib.sync()
     log("traffic probe done")
+
+
+def traffic_workloads():
+    """(workload, call) for every bandwidth line, in a fixed order, each call
+    on inputs made beforehand (so the probe's dispatches are the calls')."""
+    rng = np.random.default_rng(2)
+    x = Tensor.from_numpy(rng.standard_normal((256, 512, 512), dtype=np.float32))
+    y = Tensor.from_numpy(rng.uniform(-1, 1, (1, 512, 1)).astype(np.float32))
+    z = Tensor.from_numpy(rng.uniform(-1, 1, (256, 1, 512)).astype(np.float32))
+    t = x * y
+    out = t + z
+    p = out.permute([0, 2, 1]).contiguous()
+    halves = p.chunk(1, 2)
+    n = 256 * 512 * 512
+    dst = lib.Buffer(4 * n)
+    small = Tensor.from_numpy(rng.standard_normal((64, 128, 1024), dtype=np.float32))
+    large = Tensor.from_numpy(rng.standard_normal((1024, 128, 1024), dtype=np.float32))
+    mat = lib.Buffer.of(rng.standard_normal((8192, 8192), dtype=np.float32))
+    vec = lib.Buffer.of(rng.standard_normal(8192, dtype=np.float32))
+    yv = lib.Buffer(4 * 8192)
+    da = lib.Buffer.of(rng.standard_normal(64 << 20, dtype=np.float32))
+    db = lib.Buffer.of(rng.standard_normal(64 << 20, dtype=np.float32))
+    dot_out = lib.Buffer(4)
+    sq = lib.Buffer.of(rng.standard_normal((4096, 4096), dtype=np.float32))
+    sq_t = lib.Buffer(4 * 4096 * 4096)
+    keep = (x, y, z, t, out, p, halves, dst, small, large, mat, vec, yv, da, db, dot_out, sq, sq_t)
+    calls = [
+        ("x*y, f32 [256,512,512] x [1,512,1]", lambda: x * y),
+        ("t+z, f32 [256,512,512] + [256,1,512]", lambda: t + z),
+        ("permute(0,2,1).contiguous, f32 [256,512,512]", lambda: out.permute([0, 2, 1]).contiguous()),
+        ("slice [:,128:384,:].contiguous, f32", lambda: p.slice(1, 128, 384).contiguous()),
+        ("concat of two [256,256,512] halves on axis 1, f32", lambda: Tensor.concat(halves, 1)),
+        ("same-shape add, f32 64 Mi elements",
+         lambda: lib.call("tc_elementwise", lib.F32, lib.ADD, x.storage.ptr, t.storage.ptr, dst.ptr, n)),
+    ]
+    for tag, tensor in (("64x128x1024", small), ("1024x128x1024", large)):
+        calls += [
+            (f"sum_axes [2] of f32 [{tag}]", lambda tensor=tensor: tensor.sum_axes([2])),
+            (f"var_axes [2] of f32 [{tag}]", lambda tensor=tensor: tensor.var_axes([2])),
+            (f"sum_axes [0, 1] of f32 [{tag}]", lambda tensor=tensor: tensor.sum_axes([0, 1])),
+            (f"var_axes [0, 1] of f32 [{tag}]", lambda tensor=tensor: tensor.var_axes([0, 1])),
+            (f"argmax axis 1 of f32 [{tag}]", lambda tensor=tensor: tensor.argmax(1)),
+        ]
+    calls += [
+        ("matvec, f32 [8192x8192] . [8192]",
+         lambda: lib.call("tc_matvec", lib.F32, 0, 8192, 8192, mat.ptr, vec.ptr, yv.ptr)),
+        ("vecmat, f32 [8192] . [8192x8192]",
+         lambda: lib.call("tc_vecmat", lib.F32, 8192, 8192, vec.ptr, mat.ptr, yv.ptr)),
+        ("dot, f32 64 Mi elements", lambda: lib.call("tc_dot", lib.F32, da.ptr, db.ptr, 64 << 20, dot_out.ptr)),
+        ("transpose, f32 [4096x4096]", lambda: lib.call("tc_transpose", 4, 4096, 4096, sq.ptr, sq_t.ptr)),
+    ]
+    traffic_workloads.keep = keep
+    return calls
 
 
 def cpu_baseline(m: int, k: int, n: int) -> dict:

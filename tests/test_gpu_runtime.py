@@ -152,3 +152,34 @@ def test_a_training_step_waits_only_when_its_loss_is_read():
     loss = net.loss()
     assert np.isfinite(loss) and lib.activity()[1] == waits + 1
     net.close()
+
+
+def test_a_split_reduction_replays_from_a_graph_like_its_eager_run():
+    # A reduction over [0, 1] of [64, 128, 1024] splits each column's 8192
+    # rows over blocks, the last block of a column tile finishing it through
+    # an arrival count that every launch leaves at zero; replays of a
+    # captured graph, with eager work between them, must each give the
+    # eager result, bit for bit.
+    rng = np.random.default_rng(21)
+    host = rng.standard_normal((64, 128, 1024), dtype=np.float32)
+    x = Tensor.from_numpy(host)
+    eager = {name: getattr(x, f"{name}_axes")([0, 1]).to_numpy() for name in ("sum", "max", "var")}
+    out = {}
+    lib.call("tc_release_graph_memory")
+    with Graph() as graph:
+        for name in ("sum", "max", "var"):
+            out[name] = getattr(x, f"{name}_axes")([0, 1])
+    for replay in range(3):
+        graph.replay()
+        lib.sync()
+        for name in ("sum", "max", "var"):
+            assert np.array_equal(out[name].to_numpy(), eager[name]), (name, replay)
+        # Eager work between the replays, through the same arrival counts.
+        again = x.sum_axes([0, 1]).to_numpy()
+        assert np.array_equal(again, eager["sum"])
+    wide = host.astype(np.float64)
+    assert np.allclose(eager["sum"], wide.sum((0, 1)), rtol=0, atol=1e-6 * np.sqrt(8192) * np.abs(wide).sum((0, 1)).max())
+    assert np.array_equal(eager["max"], host.max((0, 1)))
+    graph.destroy()
+    del out
+    lib.call("tc_release_graph_memory")
