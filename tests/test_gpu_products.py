@@ -59,7 +59,7 @@ def test_matmul_against_the_oracle(in_kind, out_kind, m, k, n):
 
 
 @pytest.mark.parametrize("kind", [lib.F32, lib.BF16])
-@pytest.mark.parametrize("m,k,n", [(64, 48, 80), (130, 257, 33), (4, 4, 4)])
+@pytest.mark.parametrize("m,k,n", [(64, 48, 80), (130, 257, 33), (4, 4, 4), (96, 64, 131), (300, 128, 258)])
 def test_transposed_products_accumulate(kind, m, k, n):
     # C + A^T B (A stored k x m) and C + A B^T (B stored n x k): the matmul
     # backward's two products (tape/mod.rs:1199-1214).
