@@ -47,8 +47,33 @@ HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
 # HBM bytes per launch of the headline product, from `rocprofv3 --pmc
 # FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --traffic-probe`,
 # scaled by what the counters read for a plain 1 GiB copy (fetch x 2.0,
-# write x 1.0): 1.631 GB read + 0.148 GB written (profiles/gemm_bf16_8192_traffic.md).
-HEADLINE_TRAFFIC = 1.779e9
+# write x 1.0): 1.660 GB read + 0.151 GB written (profiles/gemm_bf16_8192_traffic.md).
+HEADLINE_TRAFFIC = 1.811e9
+# HBM bytes per call of each bandwidth workload, from the same two counters
+# over `bench.py --traffic-probe` with the same calibration
+# (profiles/bandwidth_traffic.md): within 5% of the algorithmic bytes.
+MEASURED_TRAFFIC = {
+    "x*y, f32 [256,512,512] x [1,512,1]": 5.365e+08,
+    "t+z, f32 [256,512,512] + [256,1,512]": 5.407e+08,
+    "permute(0,2,1).contiguous, f32 [256,512,512]": 5.365e+08,
+    "slice [:,128:384,:].contiguous, f32": 2.683e+08,
+    "concat of two [256,256,512] halves on axis 1, f32": 5.366e+08,
+    "same-shape add, f32 64 Mi elements": 8.049e+08,
+    "sum_axes [2] of f32 [64x128x1024]": 3.367e+07,
+    "var_axes [2] of f32 [64x128x1024]": 3.366e+07,
+    "sum_axes [0, 1] of f32 [64x128x1024]": 3.416e+07,
+    "var_axes [0, 1] of f32 [64x128x1024]": 3.523e+07,
+    "argmax axis 1 of f32 [64x128x1024]": 3.387e+07,
+    "sum_axes [2] of f32 [1024x128x1024]": 5.38e+08,
+    "var_axes [2] of f32 [1024x128x1024]": 5.38e+08,
+    "sum_axes [0, 1] of f32 [1024x128x1024]": 5.401e+08,
+    "var_axes [0, 1] of f32 [1024x128x1024]": 5.465e+08,
+    "argmax axis 1 of f32 [1024x128x1024]": 5.412e+08,
+    "matvec, f32 [8192x8192] . [8192]": 2.688e+08,
+    "vecmat, f32 [8192] . [8192x8192]": 2.71e+08,
+    "dot, f32 64 Mi elements": 5.37e+08,
+    "transpose, f32 [4096x4096]": 1.342e+08,
+}
 MFMA_PEAK = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}  # dense TFLOP/s
 KIND = {"bf16": lib.BF16, "f16": lib.F16, "f32": lib.F32}
 METRIC = "GEMM TFLOP/s & %MFMA peak; reduce/elementwise/copy GB/s & %HBM peak"
@@ -305,7 +330,7 @@ def hbm_line(workload: str, nbytes: float, ms: float) -> dict:
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"workload": workload, "value": gbs, "unit": "GB/s", "ms": ms,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK, "unit": "GB/s", "frac": gbs / HBM_PEAK,
-                         "traffic": None}}
+                         "traffic": MEASURED_TRAFFIC.get(workload)}}
 
 
 def _host_cpu() -> tuple[str, int]:
@@ -672,6 +697,16 @@ def traffic_workloads():
             (f"var_axes [0, 1] of f32 [{tag}]", lambda tensor=tensor: tensor.var_axes([0, 1])),
             (f"argmax axis 1 of f32 [{tag}]", lambda tensor=tensor: tensor.argmax(1)),
         ]
+    # Plain 32 MiB streams beside the 32 MiB reductions: what one launch of
+    # that size reaches when it only reads, or only copies.
+    plain = lib.Buffer.of(rng.standard_normal(8 << 20, dtype=np.float32))
+    plain_out, plain_sum = lib.Buffer(32 << 20), lib.Buffer(4)
+    keep += (plain, plain_out, plain_sum)
+    calls += [
+        ("read of 32 MiB (vector_reduce sum), f32",
+         lambda: lib.call("tc_vector_reduce", lib.F32, plain.ptr, 8 << 20, lib.SUM, plain_sum.ptr)),
+        ("copy of 32 MiB, f32", lambda: lib.call("tc_copy", plain_out.ptr, plain.ptr, 32 << 20)),
+    ]
     calls += [
         ("matvec, f32 [8192x8192] . [8192]",
          lambda: lib.call("tc_matvec", lib.F32, 0, 8192, 8192, mat.ptr, vec.ptr, yv.ptr)),
