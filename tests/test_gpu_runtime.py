@@ -156,10 +156,9 @@ def test_a_training_step_waits_only_when_its_loss_is_read():
 
 def test_a_split_reduction_replays_from_a_graph_like_its_eager_run():
     # A reduction over [0, 1] of [64, 128, 1024] splits each column's 8192
-    # rows over blocks, the last block of a column tile finishing it through
-    # an arrival count that every launch leaves at zero; replays of a
-    # captured graph, with eager work between them, must each give the
-    # eager result, bit for bit.
+    # rows over blocks, whose partial states a second launch combines from
+    # memory the runtime allocates; replays of a captured graph, with eager
+    # work between them, must each give the eager result, bit for bit.
     rng = np.random.default_rng(21)
     host = rng.standard_normal((64, 128, 1024), dtype=np.float32)
     x = Tensor.from_numpy(host)
@@ -174,7 +173,7 @@ def test_a_split_reduction_replays_from_a_graph_like_its_eager_run():
         lib.sync()
         for name in ("sum", "max", "var"):
             assert np.array_equal(out[name].to_numpy(), eager[name]), (name, replay)
-        # Eager work between the replays, through the same arrival counts.
+        # Eager work between the replays, allocating partials of its own.
         again = x.sum_axes([0, 1]).to_numpy()
         assert np.array_equal(again, eager["sum"])
     wide = host.astype(np.float64)
