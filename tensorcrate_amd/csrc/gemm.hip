@@ -280,21 +280,32 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
     }
 }
 
-// The tiled kernel's shapes: a 256 x 256 tile over eight waves of 128 x 64
+// The tiled kernels' shapes: a 256 x 256 tile over eight waves of 128 x 64
 // (two waves per SIMD, so one's waits overlap the other's matrix-core
 // steps), and a 128 x 128 tile over four waves of 64 x 64 for products too
-// small to give every CU a few large tiles.
+// small to give every CU a few large tiles.  Plain products of at least a
+// tile a CU run the 16 x 16 x 32 kernel, a tile a block; those whose tiles
+// are short (K up to kShortK) and outnumber the CUs run the persistent 32 x
+// 32 x 16 kernel instead, which starts each tile's loads under the previous
+// tile's steps (on MI355X, f16 16384 x 4096 x 1024: 988 TFLOP/s against 822
+// a tile a block).  A program epilogue runs in the 32 x 32 x 16 kernel,
+// whose LDS staging of the tile it uses.
+constexpr uint32_t kShortK = 2048;
+
 template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
                     hipStream_t s, const EPI& epi = EPI{}) {
     const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
     const uint32_t cus = static_cast<uint32_t>(compute_units());
     if constexpr (!EPI::kProgram) {
-        // Several tiles a CU and whole pairs of steps: the persistent form,
-        // one block a CU, each tile's first loads under the last one's steps.
-        if (large > cus && ((k + 63) / 64) % 2 == 0) {
+        // Several short tiles a CU and whole pairs of steps: the persistent form.
+        if (large > cus && k <= kShortK && ((k + 63) / 64) % 2 == 0) {
             direct16_persistent_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64><<<cus, 2 * 4 * 64, 0, s>>>(
                 a, b, c, m, n, k, accumulate);
+            return;
+        }
+        if (large >= cus) {
+            gemm16x16_kernel<S, O, A_KC, B_KC><<<large, 512, 0, s>>>(a, b, c, m, n, k, accumulate);
             return;
         }
     }

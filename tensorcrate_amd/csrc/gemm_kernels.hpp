@@ -848,5 +848,330 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_persistent_kernel(const
     }
 }
 
+// ---- the 16 x 16 x 32 kernel ---------------------------------------------------
+//
+// The large-product kernel: 256 x 256 block tiles over eight waves of 128 x 64
+// (two waves a SIMD), 16 x 16 x 32 matrix-core steps, 64-deep K steps in two
+// LDS stages filled by direct loads.  Measured on MI355X against the 32 x 32
+// x 16 kernel above at 8192^3 bf16, it holds a higher clock under sustained
+// load (the smaller step moves fewer accumulator bytes through the register
+// file per product), and the order below keeps the matrix cores busier:
+//  - Operands are swapped into the matrix-core step (B's fragment first), so
+//    a lane's four accumulators are four consecutive columns of C, stored as
+//    one 8-byte write.
+//  - Step s runs its first 32-deep slice from registers while reading the
+//    second slice's fragments from stage s % 2; at the barrier that follows,
+//    stage s % 2 is free and step s + 1 is visible, so step s + 2's loads go
+//    into stage s % 2 at once: a load has a whole step to land.  The second
+//    slice then runs while step s + 1's first fragments are read.
+//  - A's fragments are read back into the same registers right after their
+//    last use; B's are double-buffered.  Each slice is ordered as groups of
+//    four matrix-core steps, each followed by its share of the LDS reads (all
+//    issued before the slice's last group, so the wait at the barrier is
+//    short) and of the direct loads.
+//  - Barriers are bare s_barrier with explicit waits: __syncthreads' fence
+//    would also wait for the loads of the step ahead.
+// Row-contiguous stage tiles are swizzled so that the eight k-rows a
+// half-wave's transposing read touches fall on distinct bank groups.
+
+template <typename S>
+struct Mfma16x16;
+template <>
+struct Mfma16x16<bf16_t> {
+    __device__ static f32x4 step(uint4 a, uint4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                       0, 0, 0);
+    }
+};
+template <>
+struct Mfma16x16<_Float16> {
+    __device__ static f32x4 step(uint4 a, uint4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                      0, 0);
+    }
+};
+
+// s_waitcnt immediates: vmcnt(n) and lgkmcnt(0); lgkmcnt(0) alone.
+constexpr int vmcnt_lgkm0(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4); }
+
+// A workgroup barrier that orders nothing by itself: callers wait for what
+// they need first.  The compiler keeps memory accesses on their side.
+__device__ __forceinline__ void bare_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Chunk swizzle of a row-contiguous tile for the 16 x 16 x 32 reads: k-rows 0-3
+// and 8-11 of a slice (one half-wave's transposing read) differ in the low
+// four chunk bits.
+__device__ __forceinline__ int rc16_swizzle(int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); }
+
+// Direct-load staging of one operand's stage tile with a single per-lane
+// offset: the swizzle of a lane's chunk repeats every instruction, so
+// instruction i only adds a uniform stride (kept in a scalar register).
+template <typename S, int ROWS, bool KC, int WAVES, int BK>
+struct StrideStager {
+    static constexpr int kInstr = ROWS * BK * 2 / 1024;  // one wave instruction moves 1 KiB
+    static constexpr int kPer = kInstr / WAVES;
+    static constexpr int kRowsPer = KC ? 1024 / (BK * 2) : 1024 / (ROWS * 2);
+    static constexpr int kChunksPerRow = KC ? BK / 8 : ROWS / 8;
+    static_assert(kInstr % WAVES == 0, "whole instructions per wave");
+    static_assert((kRowsPer * WAVES) % 16 == 0, "each instruction's rows repeat the swizzle (period 16 rows)");
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t offset;  // this lane's chunk of instruction 0, bytes at k0 = 0
+    uint32_t k_of;    // its k within a step (K-contiguous only)
+    uint32_t stride;  // bytes from one instruction's rows to the next's
+    uint32_t k_bytes;
+    int wave;
+
+    __device__ void init(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int w, int lane) {
+        wave = w;
+        const int row = kRowsPer * w + lane / kChunksPerRow;
+        const int chunk = (lane % kChunksPerRow) ^ (KC ? kc_swizzle<BK>(row) : rc16_swizzle(row));
+        offset = (static_cast<uint32_t>(row) * ld + chunk * 8) * sizeof(S);
+        k_of = KC ? chunk * 8 : 0;
+        stride = kRowsPer * WAVES * ld * sizeof(S);
+        k_bytes = KC ? sizeof(S) : ld * sizeof(S);
+        retarget(p, first, rows, ld, depth);
+    }
+    // Another block tile of the same operand: only the resource changes.
+    __device__ __forceinline__ void retarget(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth) {
+        if (KC) {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + static_cast<uint64_t>(first) * ld), 0,
+                                                     (rows - first) * ld * sizeof(S), kBufferFlags);
+        } else {
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(p + first), 0, (depth * ld - first) * sizeof(S),
+                                                     kBufferFlags);
+        }
+    }
+    // Stage the step at k0 into `tile`.  Past K a K-contiguous chunk is the
+    // next row's, so it is pointed past the resource (operands are under
+    // 2^31 bytes) and loads zeros.
+    __device__ __forceinline__ void fetch(S* tile, uint32_t k0, uint32_t K, bool full) const {
+        const uint32_t at = (full || !KC || k0 + k_of < K) ? offset : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < kPer; i++) {
+            uint8_t* dst = reinterpret_cast<uint8_t*>(tile) + 1024 * (wave + WAVES * i);
+            // The scalar offset is uniform; said so, the compiler keeps it in
+            // a scalar register rather than looping over lanes.
+            const uint32_t soffset = __builtin_amdgcn_readfirstlane(k0 * k_bytes + i * stride);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, at,
+                                                     soffset, 0, 0);
+        }
+    }
+};
+
+// Per-lane byte offsets of 16 x 16 x 32 operands in a 64-deep stage tile.  A
+// lane's operand is tile row (first + 16 blk + lane % 16) at k = 32 q + 8 (lane
+// / 16) .. + 8.  K-contiguous tile (rows of 128 bytes, chunk c of row r at
+// c ^ ((r / 2) % 8)): offset(q) + 2048 blk.
+__device__ __forceinline__ uint32_t kc16_offset(int lane, int first_row, int q) {
+    const int r = first_row + lane % 16, g = lane / 16;
+    return static_cast<uint32_t>(r * 128 + ((4 * q + g) ^ ((r / 2) % 8)) * 16);
+}
+// Row-contiguous tile (k-rows of ROWS elements): the transposing reads of
+// column block `blk` are at offset(blk) + 32 q * ROWS * 2 and four k-rows on.
+template <int ROWS>
+__device__ __forceinline__ uint32_t rc16_offset(int lane, int first_col, int blk) {
+    const int g = lane / 16, j = lane % 16;
+    const int k = 8 * g + j / 4;
+    const int col = first_col + 16 * blk + 4 * (j % 4);
+    const int chunk = (col / 8) ^ rc16_swizzle(k);
+    return static_cast<uint32_t>(k * ROWS * 2 + chunk * 16 + (col % 8) * 2);
+}
+
+template <typename S>
+__device__ __forceinline__ uint4 lds_b128(const S* tile, uint32_t offset) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(tile) + offset);
+}
+template <typename S, int ROWS>
+__device__ __forceinline__ uint4 lds_tr_pair(const S* tile, uint32_t offset) {
+    const uint8_t* at = reinterpret_cast<const uint8_t*>(tile) + offset;
+    short4v lo = read_tr16(at);
+    short4v hi = read_tr16(at + 4 * ROWS * 2);
+    uint4 out;
+    out.x = static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16);
+    out.y = static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16);
+    out.z = static_cast<uint16_t>(hi[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
+    out.w = static_cast<uint16_t>(hi[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[3])) << 16);
+    return out;
+}
+
+// One slice's order: G groups of PER matrix-core steps, each followed by its
+// share of READS LDS reads (spread over the first G - LAG groups) and of
+// LOADS direct loads.
+template <int G, int PER, int READS, int LOADS, int LAG, int g = 0>
+__device__ __forceinline__ void weave16() {
+    if constexpr (g < G) {
+        __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // matrix-core steps
+        constexpr int RG = G - LAG;
+        constexpr int r = g < RG ? READS * (g + 1) / RG - READS * g / RG : 0;
+        constexpr int l = LOADS * (g + 1) / G - LOADS * g / G;
+        if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);  // LDS reads
+        if constexpr (l > 0) __builtin_amdgcn_sched_group_barrier(0x020, l, 0);  // direct loads
+        weave16<G, PER, READS, LOADS, LAG, g + 1>();
+    }
+}
+
+// Four consecutive columns of C from a lane's accumulators, (+)=, rounded once
+// (`at` aligned to four elements).
+template <typename O>
+__device__ __forceinline__ void store_quad(O* at, f32x4 v, bool accumulate) {
+    using E = Elem<O>;
+    if constexpr (sizeof(O) == 4) {
+        if (accumulate) v += *reinterpret_cast<const f32x4*>(at);
+        *reinterpret_cast<f32x4*>(at) = v;
+    } else {
+        if (accumulate) {
+            const uint2 old = *reinterpret_cast<const uint2*>(at);
+            v[0] += E::widen(__builtin_bit_cast(O, static_cast<uint16_t>(old.x & 0xffff)));
+            v[1] += E::widen(__builtin_bit_cast(O, static_cast<uint16_t>(old.x >> 16)));
+            v[2] += E::widen(__builtin_bit_cast(O, static_cast<uint16_t>(old.y & 0xffff)));
+            v[3] += E::widen(__builtin_bit_cast(O, static_cast<uint16_t>(old.y >> 16)));
+        }
+        uint2 out;
+        out.x = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[0]))) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[1]))) << 16);
+        out.y = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[2]))) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[3]))) << 16);
+        *reinterpret_cast<uint2*>(at) = out;
+    }
+}
+
+// C (+)= A . B on 256 x 256 tiles, one tile a block.  Operands are 16-byte
+// aligned row by row and under 2^31 bytes.
+template <typename S, typename O, bool A_KC, bool B_KC>
+__global__ void __launch_bounds__(512) gemm16x16_kernel(const S* __restrict__ A, const S* __restrict__ B,
+                                                         O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                                                         bool accumulate) {
+    constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
+    constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16-wide blocks of a wave's 128 x 64
+    constexpr int kA = BM * BK, kB = BN * BK;
+    using StagerA = StrideStager<S, BM, A_KC, kWaves, BK>;
+    using StagerB = StrideStager<S, BN, B_KC, kWaves, BK>;
+    constexpr int kLoads = StagerA::kPer + StagerB::kPer;
+    constexpr int kReads = TM * (A_KC ? 1 : 2) + TN * (B_KC ? 1 : 2);
+
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    if (blockIdx.x >= tiles_m * tiles_n) return;
+    uint32_t tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int wm = wave / WN, wn = wave % WN;
+
+    StagerA sa;
+    StagerB sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
+    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
+
+    // Fragment offsets: K-contiguous operands one per slice, row-contiguous
+    // ones one per 16-wide block.
+    uint32_t a_off[A_KC ? 2 : TM], b_off[B_KC ? 2 : TN];
+    if constexpr (A_KC) {
+        a_off[0] = kc16_offset(lane, wm * (BM / WM), 0);
+        a_off[1] = kc16_offset(lane, wm * (BM / WM), 1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++) a_off[i] = rc16_offset<BM>(lane, wm * (BM / WM), i);
+    }
+    if constexpr (B_KC) {
+        b_off[0] = kc16_offset(lane, wn * (BN / WN), 0);
+        b_off[1] = kc16_offset(lane, wn * (BN / WN), 1);
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; j++) b_off[j] = rc16_offset<BN>(lane, wn * (BN / WN), j);
+    }
+    auto frag_a = [&](const S* t, int i, int q) __attribute__((always_inline)) {
+        return A_KC ? lds_b128(t, a_off[q] + 2048 * i) : lds_tr_pair<S, BM>(t, a_off[i] + q * 32 * BM * 2);
+    };
+    auto frag_b = [&](const S* t, int j, int q) __attribute__((always_inline)) {
+        return B_KC ? lds_b128(t, b_off[q] + 2048 * j) : lds_tr_pair<S, BN>(t, b_off[j] + q * 32 * BN * 2);
+    };
+
+    f32x4 acc[TM][TN];
+    uint4 fa[TM], fb[2][TN];
+    const uint32_t steps = (K + BK - 1) / BK;
+    // Step s; past the last step, a harmless reload of it.
+    auto stage_of = [&](auto t, uint32_t s) __attribute__((always_inline)) {
+        const uint32_t k0 = (s < steps ? s : steps - 1) * BK;
+        sa.fetch(stage_tile<S, kA, 2 * decltype(t)::value>(), k0, K, k0 + BK <= K);
+        sb.fetch(stage_tile<S, kB, 2 * decltype(t)::value + 1>(), k0, K, k0 + BK <= K);
+    };
+    auto read_b = [&](int slot, const S* lb, int q) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) fb[slot][j] = frag_b(lb, j, q);
+    };
+    // One slice's products; A's block i is re-read from (la, q) after its
+    // last product.
+    auto slice = [&](int slot, const S* la, int q) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = Mfma16x16<S>::step(fb[slot][j], fa[i], acc[i][j]);
+            fa[i] = frag_a(la, i, q);
+        }
+    };
+    auto step = [&](auto t, uint32_t s) __attribute__((always_inline)) {
+        constexpr int T = decltype(t)::value;
+        constexpr int U = T ^ 1;
+        read_b(1, stage_tile<S, kB, 2 * T + 1>(), 1);
+        slice(0, stage_tile<S, kA, 2 * T>(), 1);
+        weave16<TM, TN, kReads, 0, 1>();
+        __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));  // step s + 1 is in LDS; stage T is read
+        bare_barrier();
+        stage_of(t, s + 2);
+        read_b(0, stage_tile<S, kB, 2 * U + 1>(), 0);
+        slice(1, stage_tile<S, kA, 2 * U>(), 0);
+        weave16<TM, TN, kReads, kLoads, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    if (steps > 0) {
+        stage_of(std::integral_constant<int, 0>{}, 0);
+        stage_of(std::integral_constant<int, 1>{}, 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(kLoads));  // step 0 is in LDS
+        bare_barrier();
+        read_b(0, stage_tile<S, kB, 1>(), 0);
+#pragma unroll
+        for (int i = 0; i < TM; i++) fa[i] = frag_a(stage_tile<S, kA, 0>(), i, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x4{};
+    for (uint32_t s = 0; s < steps; s += 2) {
+        step(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < steps) step(std::integral_constant<int, 1>{}, s + 1);
+    }
+    // lane holds C[row][col .. col + 3] for row = m0 + wm*128 + 16 i + lane % 16,
+    // col = n0 + wn*64 + 16 j + 4 (lane / 16).
+    const bool quads = (N % 4) == 0 && (reinterpret_cast<uint64_t>(C) % (4 * sizeof(O))) == 0;
+    const uint32_t row0 = m0 + wm * (BM / WM) + lane % 16;
+    const uint32_t col0 = n0 + wn * (BN / WN) + 4 * (lane / 16);
+    O* base = C + static_cast<uint64_t>(row0) * N + col0;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const uint32_t row = row0 + 16 * i, col = col0 + 16 * j;
+            O* at = base + static_cast<uint64_t>(16 * i) * N + 16 * j;
+            if (quads && row < M && col + 4 <= N) {
+                store_quad(at, acc[i][j], accumulate);
+            } else if (row < M) {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (col + e < N) store_out(at, e, acc[i][j][e], accumulate);
+            }
+        }
+    }
+    // No direct load may still be writing LDS when the block ends.
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));
+}
 
 }  // namespace tc

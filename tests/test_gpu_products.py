@@ -201,15 +201,19 @@ def sampled_form(kind, form, m, k, n, rng, addend):
 @pytest.mark.parametrize("kind", [lib.BF16, lib.F16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("form", [lib.PLAIN, lib.LEFT, lib.RIGHT], ids=["plain", "left", "right"])
 @pytest.mark.parametrize("addend", [False, True], ids=["product", "accumulate"])
-@pytest.mark.parametrize("m,k,n", [(4200, 128, 4200), (4200, 192, 4200), (4352, 1024, 4352), (4100, 1024, 4200)])
+@pytest.mark.parametrize("m,k,n", [(4200, 128, 4200), (4200, 192, 4200), (4352, 1024, 4352), (4100, 1024, 4200),
+                                   (4104, 2120, 4200), (4200, 2176, 4104), (4352, 4096, 4352)])
 def test_products_with_more_tiles_than_compute_units(kind, form, addend, m, k, n):
-    # More 256 x 256 tiles than the part's 256 CUs, so a block walks several
-    # tiles in turn: ragged edges in both dimensions (4200 = 16 x 256 + 104),
-    # whole tiles only (4352 = 17 x 256), and a ragged M with whole-tile
-    # columns; every form the tape's backward products take (LEFT is
-    # Aᵀ·B, RIGHT is A·Bᵀ, tape/mod.rs:1195-1246), with and without an
-    # addend.  The first and last rows are always sampled, so the edge tiles
-    # are checked.
+    # More 256 x 256 tiles than the part's 256 CUs.  Short K with an even
+    # step count takes the persistent kernel, where a block walks several
+    # tiles in turn; an odd step count (192) and long K (from 2120 on) take
+    # the 16 x 16 x 32 kernel, a tile a block, including a K tail that is not
+    # a whole 64-deep step (2120 = 33 x 64 + 8).  Ragged edges in both
+    # dimensions (4200 = 16 x 256 + 104), whole tiles only (4352 = 17 x 256),
+    # and a ragged M with whole-tile columns; every form the tape's backward
+    # products take (LEFT is Aᵀ·B, RIGHT is A·Bᵀ, tape/mod.rs:1195-1246),
+    # with and without an addend.  The first and last rows are always
+    # sampled, so the edge tiles are checked.
     rng = np.random.default_rng(m + 3 * k + 7 * n + 11 * form + int(addend))
     got, want, scale = sampled_form(kind, form, m, k, n, rng, addend)
     tol = tolerance(kind, kind, k) + (2.0 ** -8 if addend else 0.0)
