@@ -47,8 +47,8 @@ HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
 # HBM bytes per launch of the headline product, from `rocprofv3 --pmc
 # FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --traffic-probe`,
 # scaled by what the counters read for a plain 1 GiB copy (fetch x 2.0,
-# write x 1.0): 1.660 GB read + 0.151 GB written (profiles/gemm_bf16_8192_traffic.md).
-HEADLINE_TRAFFIC = 1.811e9
+# write x 0.998): 1.625 GB read + 0.161 GB written (profiles/gemm_bf16_8192_traffic.md).
+HEADLINE_TRAFFIC = 1.786e9
 # HBM bytes per call of each bandwidth workload, from the same two counters
 # over `bench.py --traffic-probe` with the same calibration
 # (profiles/bandwidth_traffic.md): within 5% of the algorithmic bytes.
