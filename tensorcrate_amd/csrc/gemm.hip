@@ -283,13 +283,12 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
 // The tiled kernels' shapes: a 256 x 256 tile over eight waves of 128 x 64
 // (two waves per SIMD, so one's waits overlap the other's matrix-core
 // steps), and a 128 x 128 tile over four waves of 64 x 64 for products too
-// small to give every CU a few large tiles.  Plain products of at least a
-// tile a CU run the 16 x 16 x 32 kernel, a tile a block; those whose tiles
-// are short (K up to kShortK) and outnumber the CUs run the persistent 32 x
-// 32 x 16 kernel instead, which starts each tile's loads under the previous
+// small to give every CU a few large tiles.  Products of at least a tile a
+// CU run the 16 x 16 x 32 kernel, a tile a block; plain ones whose tiles are
+// short (K up to kShortK) and outnumber the CUs run the persistent 32 x 32 x
+// 16 kernel instead, which starts each tile's loads under the previous
 // tile's steps (on MI355X, f16 16384 x 4096 x 1024: 988 TFLOP/s against 822
-// a tile a block).  A program epilogue runs in the 32 x 32 x 16 kernel,
-// whose LDS staging of the tile it uses.
+// a tile a block).
 constexpr uint32_t kShortK = 2048;
 
 template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
@@ -304,14 +303,9 @@ void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32
                 a, b, c, m, n, k, accumulate);
             return;
         }
-        if (large >= cus) {
-            gemm16x16_kernel<S, O, A_KC, B_KC><<<large, 512, 0, s>>>(a, b, c, m, n, k, accumulate);
-            return;
-        }
     }
     if (large >= cus) {
-        direct16_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64, 2, EPI><<<large, 2 * 4 * 64, 0, s>>>(a, b, c, m, n, k,
-                                                                                                 accumulate, epi);
+        gemm16x16_kernel<S, O, A_KC, B_KC, EPI><<<large, 512, 0, s>>>(a, b, c, m, n, k, accumulate, epi);
     } else {
         const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);
         direct16_kernel<S, O, A_KC, B_KC, 128, 128, 2, 2, 64, 2, EPI><<<small, 2 * 2 * 64, 0, s>>>(a, b, c, m, n, k,
@@ -555,10 +549,10 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
         large_threads = small_threads = kThreads;
     } else {
         const std::string type = dtype == TC_F16 ? "_Float16" : "tc::bf16_t";
-        kernels = {"tc::direct16_kernel<" + type + ", " + type + ", true, false, 256, 256, 2, 4, 64, 2, CompiledStore>",
+        kernels = {"tc::gemm16x16_kernel<" + type + ", " + type + ", true, false, CompiledStore>",
                    "tc::direct16_kernel<" + type + ", " + type + ", true, false, 128, 128, 2, 2, 64, 2, CompiledStore>"};
         large = ((m + 255) / 256) * ((n + 255) / 256);
-        large_threads = 2 * 4 * 64;
+        large_threads = 512;
         small_threads = 2 * 2 * 64;
     }
     small = ((m + 127) / 128) * ((n + 127) / 128);

@@ -128,9 +128,17 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Where tile column `col` of staged row `row` sits: groups of G lanes that
 // store one row of a matrix-core tile, 4 rows apart, land on distinct banks.
+// G = 0 is the 16 x 16 x 32 kernel's layout, where a lane stores four
+// consecutive columns of one row as one 16-byte write and 16 lanes store 16
+// consecutive rows: the row's low four bits pick the quad's 16-byte place
+// within its 64 columns.
 template <int G>
 __device__ __forceinline__ uint32_t staged_col(uint32_t row, uint32_t col) {
-    return col ^ (((row >> 2) & (64 / G - 1)) * G);
+    if constexpr (G == 0) {
+        return col ^ ((row & 15) << 2);
+    } else {
+        return col ^ (((row >> 2) & (64 / G - 1)) * G);
+    }
 }
 
 // The staged rows live in up to four LDS regions of REGION_ROWS rows each.
@@ -1041,12 +1049,13 @@ __device__ __forceinline__ void store_quad(O* at, f32x4 v, bool accumulate) {
     }
 }
 
-// C (+)= A . B on 256 x 256 tiles, one tile a block.  Operands are 16-byte
-// aligned row by row and under 2^31 bytes.
-template <typename S, typename O, bool A_KC, bool B_KC>
+// C (+)= A . B on 256 x 256 tiles, one tile a block, finished by plain
+// stores or a program epilogue (how a tile is finished, above).  Operands are
+// 16-byte aligned row by row and under 2^31 bytes.
+template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 __global__ void __launch_bounds__(512) gemm16x16_kernel(const S* __restrict__ A, const S* __restrict__ B,
                                                          O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
-                                                         bool accumulate) {
+                                                         bool accumulate, EPI epi) {
     constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16-wide blocks of a wave's 128 x 64
     constexpr int kA = BM * BK, kB = BN * BK;
@@ -1151,6 +1160,36 @@ __global__ void __launch_bounds__(512) gemm16x16_kernel(const S* __restrict__ A,
     }
     // lane holds C[row][col .. col + 3] for row = m0 + wm*128 + 16 i + lane % 16,
     // col = n0 + wn*64 + 16 j + 4 (lane / 16).
+    if constexpr (EPI::kProgram) {
+        // The four stage arrays, BK / 2 rows of BN floats each, hold a pass of
+        // 128 rows: 64 of each wave row, so each wave stages the same share of
+        // its accumulators in every pass.
+        constexpr int kRegionRows = kA * static_cast<int>(sizeof(S)) / 4 / BN;
+        constexpr int kPass = 4 * kRegionRows;
+        constexpr int kPasses = BM / kPass, H = BM / WM / kPasses;
+        static_assert(BM == BN && kA == kB && BM % kPass == 0 && H % 16 == 0, "whole passes of whole 16-row blocks");
+        float* r0 = reinterpret_cast<float*>(stage_tile<S, kA, 0>());
+        float* r1 = reinterpret_cast<float*>(stage_tile<S, kB, 1>());
+        float* r2 = reinterpret_cast<float*>(stage_tile<S, kA, 2>());
+        float* r3 = reinterpret_cast<float*>(stage_tile<S, kB, 3>());
+        __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));  // the last step's reloads have landed
+#pragma unroll
+        for (int pass = 0; pass < kPasses; pass++) {
+            lds_barrier();  // every wave is done with LDS
+#pragma unroll
+            for (int i = pass * H / 16; i < (pass + 1) * H / 16; i++) {
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const uint32_t rr = wm * H + 16 * i + lane % 16 - pass * H;
+                    const uint32_t col = wn * (BN / WN) + 16 * j + 4 * (lane / 16);
+                    *reinterpret_cast<f32x4*>(staged_at<BN, 0, kRegionRows>(r0, r1, r2, r3, rr, col)) = acc[i][j];
+                }
+            }
+            lds_barrier();
+            program_pass<BN, 0, kRegionRows, H, BM / WM>(epi, r0, r1, r2, r3, kPass, pass, m0, n0, M, N);
+        }
+        return;
+    }
     const bool quads = (N % 4) == 0 && (reinterpret_cast<uint64_t>(C) % (4 * sizeof(O))) == 0;
     const uint32_t row0 = m0 + wm * (BM / WM) + lane % 16;
     const uint32_t col0 = n0 + wn * (BN / WN) + 4 * (lane / 16);

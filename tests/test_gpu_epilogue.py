@@ -111,19 +111,23 @@ def test_the_product_must_be_read_in_order():
                             [(lib.Buffer.of(np.ones(n, np.float32)), n)], [(out, m * n)])
 
 
-@pytest.mark.parametrize("kind", [lib.F32, lib.BF16])
-def test_a_repeated_program_runs_compiled_with_the_same_bits(kind):
+@pytest.mark.parametrize("kind", [lib.F32, lib.BF16, lib.F16])
+@pytest.mark.parametrize("m,k,n", [(520, 136, 1032), (4100, 136, 4104)], ids=["small-tiles", "large-tiles"])
+def test_a_repeated_program_runs_compiled_with_the_same_bits(kind, m, k, n):
     # The first appearance of a program runs the interpreter epilogue; from
     # the second the program is compiled into the product kernel (as the
     # reference's Metal backend specializes a program seen before).  Both
-    # give the unfused bits.  A constant no other test uses keeps this
-    # program's source new to the process.
+    # give the unfused bits, in the kernel for fewer 256 x 256 tiles than
+    # CUs and in the one for more (17 x 17 tiles, ragged).  Compiled
+    # kernels are cached by source, constants being arguments, so each case
+    # has a program of its own shape: the bias added for the small tiles,
+    # subtracted for the large.
     code = Code()
     p = code.load(0, 0, kind)
     b = code.load(1, 1, kind)
-    scaled = code.binary(lib.MUL, code.binary(lib.ADD, p, b), code.const(0.375 + kind))
+    shifted = code.binary(lib.SUB if m > 1000 else lib.ADD, p, b)
+    scaled = code.binary(lib.MUL, shifted, code.const(0.375 + kind))
     code.store(code.compare(lib.MAX, scaled, code.const(-0.25)), kind, 0)
-    m, k, n = 520, 136, 1032
     rng = np.random.default_rng(kind)
     a = to_kind(rng.uniform(-1, 1, (m, k)).astype(np.float32), kind)
     w = to_kind(rng.uniform(-1, 1, (k, n)).astype(np.float32), kind)
