@@ -102,9 +102,10 @@ typedef struct tc_region {
     tc_strided to;
 } tc_region;
 
-/* A layout split for a reduction (`Split`, tensors/layout.rs:370-376): result
- * [k..] folds storage elements `offset + sum(k_i kept_strides[i]) +
- * sum(f_j folded_strides[j])` over every index [f..] of `folded`. */
+/* How a reduction walks its input (`Split`, tensors/layout.rs:370-376): the
+ * output at kept index [k..] reduces the storage elements at
+ * offset + Σ k_i·kept_strides[i] + Σ f_j·folded_strides[j], for every folded
+ * index [f..] within `folded`. */
 typedef struct tc_split {
     uint64_t offset;
     uint32_t kept_rank;
@@ -248,9 +249,10 @@ int tc_compare_scalar(uint32_t dtype, uint32_t op, const void* a, float scalar, 
 int tc_clamp(uint32_t dtype, const void* a, float low, float high, void* out, uint64_t n);
 
 /* `Kernels::strided_binary` (kernels.rs:1162-1166; Host strided.rs:29-78):
- * op(a, b) over `shape`, each operand read in place through its own layout
- * (a zero stride repeats an element, as a broadcast does), into the
- * row-major `out`.  `kind` is a `tc_pairwise`; `op` its BinaryOp or Compare. */
+ * out = op(a, b) element by element over `shape`, written row-major; a and b
+ * are addressed through their own strided layouts, so a stride of 0 reuses
+ * one element along that axis (broadcasting) without copying.  `kind` is a
+ * `tc_pairwise`; `op` its BinaryOp or Compare. */
 int tc_strided_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank,
                       const uint64_t* shape, const void* a, uint64_t a_len, const tc_strided* a_at,
                       const void* b, uint64_t b_len, const tc_strided* b_at, void* out);

@@ -12,12 +12,12 @@
 // scratch memory.  Each thread runs four elements 64 apart, so every load
 // and store instruction of a wave touches one contiguous run.
 //
-// A program computes in its own type T (f32, f16 or bf16): loads convert
-// their storage type to T, every operation rounds to T, and stores convert T
-// to the output's storage type — the exact per-instruction arithmetic of the
-// host interpreter (fused/mod.rs:62-70), since each operation computed in
-// f32 and rounded once is T's own correctly rounded result.  No
-// multiply-add is ever contracted.
+// Arithmetic follows the host interpreter instruction by instruction
+// (fused/mod.rs:62-70): a program has one working type T (f32, f16 or bf16);
+// every load widens its storage element and rounds it to T, every operation
+// is done in f32 and rounded to T once — which is T's correctly rounded
+// result — and every store converts from T to the output's element type.
+// Multiply and add are never fused.
 
 #include <hip/hiprtc.h>
 #include <math.h>
@@ -185,17 +185,18 @@ bool dense_plan(const tc_encoded* code, uint32_t count, const tc_place* places, 
 
 // ---- compiled programs -----------------------------------------------------
 //
-// A dense program that runs more than once is compiled into a kernel of its
-// own, as the reference's Metal backend compiles its fused programs
-// (metal/codegen.rs:1-40): straight-line code, one local per value, every
-// opcode and storage type a constant the compiler folds away, calling the
-// same scalar functions the interpreter does (scalar_ops.h, embedded in the
-// generated source).  Constants travel in the kernel's arguments, so
-// programs that differ only in their constants — an optimizer's, rebuilt
-// every step — share one compiled kernel.  A program is compiled on its
-// second appearance, so one run once never waits for the compiler, and
-// kernels are cached by their source for the life of the process.  The
-// runtime compiler is hiprtc, with this library's own code-generation flags.
+// Specialisation (the reference's Metal backend does the same for its fused
+// programs, metal/codegen.rs:1-40): the second time a dense program is seen,
+// it is turned into HIP source with no interpreter loop left — each value a
+// local variable, each opcode and storage type a literal the compiler can
+// fold — built with hiprtc and this library's code-generation flags, and
+// launched instead of the interpreter from then on.  The generated code
+// calls scalar_ops.h, the functions the interpreter uses, so both give the
+// same bits.  Literal constants are passed as kernel arguments rather than
+// written into the source, which lets a program rebuilt each step with new
+// constants (an optimizer's) reuse its kernel; kernels are kept, keyed by
+// source, until the process ends.  A program seen only once is never
+// compiled, so a one-off never waits for the compiler.
 
 // The headers hiprtc reads, embedded by the build.
 extern "C" const char tc_scalar_ops_source[];

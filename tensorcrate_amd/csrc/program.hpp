@@ -3,10 +3,11 @@
 // tables, a program small enough to travel in kernel arguments, and `run`,
 // which applies one instruction to each of a thread's four elements.
 //
-// A program computes in its own type T (f32, f16 or bf16): loads convert
-// their storage type to T, every operation rounds to T, and stores convert T
-// to the output's storage type -- the per-instruction arithmetic of the host
-// interpreter (fused/mod.rs:62-70).  No multiply-add is ever contracted.
+// Arithmetic follows the host interpreter instruction by instruction
+// (fused/mod.rs:62-70): one working type T per program (f32, f16 or bf16),
+// loads rounded to T, each operation done in f32 and rounded to T, stores
+// converted from T to the output's element type; multiply and add are
+// never fused.
 
 #pragma once
 

@@ -69,8 +69,9 @@ struct TapeValue<Matrix<T>> {
     }
 };
 
-// A node's value, computed when recorded or — for a scalar reduced from
-// device storage — when first read (`Lazy`, tape/mod.rs:253-295).
+// Holds a node's value, either at once or as a thunk run the first time the
+// value is asked for: a loss reduced on the device stays queued until the
+// host reads it (`Lazy`, tape/mod.rs:253-295).
 template <typename V>
 class Lazy {
    public:
@@ -98,7 +99,8 @@ class Lazy {
     std::function<V()> pending_;
 };
 
-// The type-erased face of a node (`Backprop`, tape/mod.rs:333-346).
+// What the tape calls on every node without knowing its value type
+// (`Backprop`, tape/mod.rs:333-346).
 struct Backprop {
     virtual ~Backprop() = default;
     virtual void propagate() = 0;
@@ -231,7 +233,7 @@ Var<U> Var<V>::record_lazy(Lazy<U> value, std::function<void(const U&)> rule) co
 template <typename T>
 using K = Kernels<T>;
 
-// The outer product u ⊗ v as a (u.len × 1)·(1 × v.len) product
+// u ⊗ v, computed as the product of u as one column with v as one row
 // (`outer`, tape/mod.rs:1000-1006).
 template <typename T>
 Matrix<T> outer(const Vector<T>& u, const Vector<T>& v) {
@@ -344,8 +346,8 @@ class VectorVar : public Var<Vector<T>> {
         });
     }
 
-    // `VectorVar::to_tensor` (tape/tensor.rs:764-778): the elements as a
-    // tensor of `shape`; the adjoint is flattened back.
+    // `VectorVar::to_tensor` (tape/tensor.rs:764-778): the same storage
+    // viewed with `shape`; backward reads the gradient as a flat vector.
     TensorVar<T> to_tensor(const Shape& shape) const;
 
     // `VectorVar::scale`.
@@ -524,8 +526,8 @@ class MatrixVar : public Var<Matrix<T>> {
         }));
     }
 
-    // `MatrixVar::to_tensor` (tape/tensor.rs:744-761): the elements, row
-    // major, as a tensor of `shape`; the adjoint takes the matrix shape back.
+    // `MatrixVar::to_tensor` (tape/tensor.rs:744-761): the row-major storage
+    // viewed with `shape`; backward reads the gradient as rows × cols.
     TensorVar<T> to_tensor(const Shape& shape) const;
 
     // `MatrixVar::frobenius_dot` (tape/mod.rs:1299-1302).
@@ -563,8 +565,8 @@ class MatrixVar : public Var<Matrix<T>> {
 };
 
 // `sum_to_shape` (tape/tensor.rs:18-37): the adjoint of a broadcast, summed
-// down to the operand's `shape` in one reduction over the leading axes the
-// operand lacks and every axis where it has 1 and the gradient more.
+// down to the operand's `shape`: one reduction folds the gradient's extra
+// leading axes and each axis that broadcasting stretched from extent 1.
 template <typename T>
 Tensor<T> sum_to_shape(const Tensor<T>& gradient, const Shape& shape) {
     if (gradient.shape() == shape) return gradient.duplicate();
@@ -578,10 +580,10 @@ Tensor<T> sum_to_shape(const Tensor<T>& gradient, const Shape& shape) {
     return std::move(summed).reshape(shape);
 }
 
-// `Node::accumulate_slice` (tape/tensor.rs:55-82): `delta` added into the
-// elements `start..` of `axis` of the node's adjoint.  With no adjoint yet
-// the slice is written into zeros; otherwise the slice of the adjoint plus
-// `delta` is written back in place, so the rest of it is never touched.
+// `Node::accumulate_slice` (tape/tensor.rs:55-82): adds `delta` to one
+// window along `axis` (from index `start`) of the node's gradient.  A node
+// without a gradient yet gets a zero tensor with `delta` written into the
+// window; otherwise only the window is read, summed and written back.
 template <typename T>
 void accumulate_slice(Node<Tensor<T>>& node, size_t axis, size_t start, const Tensor<T>& delta) {
     if (node.adjoint) {
@@ -598,10 +600,10 @@ void accumulate_slice(Node<Tensor<T>>& node, size_t axis, size_t start, const Te
 // n − 1 for a sample; too few elements leave it undefined.
 enum class Correction { Population, Sample };
 
-// `TensorVar` (tape/tensor.rs): an N-dimensional tensor on the tape.  Every
-// rule is written with the tensor kernels of backend.hpp, so a backward pass
-// stays on the device; an operand that was broadcast receives its adjoint
-// summed back to its own shape.
+// `TensorVar` (tape/tensor.rs): an N-dimensional value recorded on the tape.
+// Its backward rules call only the device kernels of backend.hpp, so the
+// whole backward pass runs on the GPU; a gradient flowing to a broadcast
+// operand is reduced to that operand's shape first.
 template <typename T>
 class TensorVar : public Var<Tensor<T>> {
     using Base = Var<Tensor<T>>;
@@ -619,9 +621,9 @@ class TensorVar : public Var<Tensor<T>> {
     TensorVar operator*(const TensorVar& rhs) const { return binary(rhs, BinaryOp::Mul); }
     TensorVar operator/(const TensorVar& rhs) const { return binary(rhs, BinaryOp::Div); }
 
-    // `TensorVar::binary` (tape/tensor.rs:126-160): c = a op b broadcast;
-    // ā, b̄ each summed to its operand's shape.  No tensor remainder is
-    // recorded, as in the reference.
+    // `TensorVar::binary` (tape/tensor.rs:126-160): c = a op b with
+    // broadcasting; both gradients are reduced to their operands' shapes.
+    // Remainder has no rule here, as in the reference.
     TensorVar binary(const TensorVar& rhs, BinaryOp op) const {
         this->assert_same_tape(rhs.tape());
         if (op == BinaryOp::Rem) throw std::invalid_argument("no tensor remainder is recorded");
@@ -644,7 +646,7 @@ class TensorVar : public Var<Tensor<T>> {
                     right->accumulate(sum_to_shape(K<T>::elementwise(adjoint, a, op), b.shape()));
                     break;
                 case BinaryOp::Div: {
-                    // ā += c̄/b, b̄ −= (c̄/b)·a/b
+                    // d(a/b)/da = 1/b, d(a/b)/db = −a/b²
                     X over = K<T>::elementwise(adjoint, b, BinaryOp::Div);
                     X scaled = K<T>::elementwise(K<T>::elementwise(over, a, BinaryOp::Mul), b, BinaryOp::Div);
                     left->accumulate(sum_to_shape(over, a.shape()));
@@ -657,8 +659,8 @@ class TensorVar : public Var<Tensor<T>> {
         });
     }
 
-    // `TensorVar::power` (tape/tensor.rs:162-185): ā += c̄·b·a^(b−1),
-    // b̄ += c̄·a^b·ln a, each summed to its operand's shape.
+    // `TensorVar::power` (tape/tensor.rs:162-185): d(a^b)/da = b·a^(b−1)
+    // and d(a^b)/db = a^b·ln a, each gradient reduced to its operand's shape.
     TensorVar power(const TensorVar& exponent) const {
         this->assert_same_tape(exponent.tape());
         auto base = this->node_;
@@ -687,8 +689,8 @@ class TensorVar : public Var<Tensor<T>> {
             });
     }
 
-    // `maximum` / `minimum` (tape/tensor.rs:210-250): the adjoint goes to
-    // whichever operand supplied the value, split evenly at ties.
+    // `maximum` / `minimum` (tape/tensor.rs:210-250): the gradient follows
+    // the operand the result came from; equal operands share it in halves.
     TensorVar maximum(const TensorVar& other) const { return select_pair(other, true); }
     TensorVar minimum(const TensorVar& other) const { return select_pair(other, false); }
 
@@ -727,7 +729,7 @@ class TensorVar : public Var<Tensor<T>> {
 
     // ---- layout (tape/tensor.rs:335-420, :555-570) ----
 
-    // `reshape` (:335-350): the adjoint takes the old shape back.
+    // `reshape` (:335-350): backward views the gradient in the input's shape.
     TensorVar reshape(const Shape& shape) const {
         auto parent = this->node_;
         return this->template record<X>(this->value().duplicate().reshape(shape), [parent](const X& adjoint) {
@@ -840,8 +842,8 @@ class TensorVar : public Var<Tensor<T>> {
         }
         return split(static_cast<long>(k), std::vector<size_t>(parts, shape()[k] / parts));
     }
-    // `concat` (:502-533): each piece's adjoint is its block of the joined
-    // adjoint.
+    // `concat` (:502-533): backward hands each input the window of the
+    // gradient that its elements occupy.
     static TensorVar concat(const std::vector<TensorVar>& pieces, long axis) {
         if (pieces.empty()) throw std::invalid_argument("concat: there are no tensors to join");
         const TensorVar& first = pieces[0];
@@ -889,7 +891,8 @@ class TensorVar : public Var<Tensor<T>> {
 
     // ---- reductions (tape/tensor.rs:572-684) ----
 
-    // `sum_axes`: every element of a slice receives the slice's adjoint.
+    // `sum_axes`: backward broadcasts each output's gradient over the inputs
+    // it summed.
     TensorVar sum_axes(const std::vector<long>& axes, bool keep_dims) const {
         const Folding f = folding(axes, "sum_axes");
         auto parent = this->node_;
@@ -898,7 +901,7 @@ class TensorVar : public Var<Tensor<T>> {
             parent->accumulate(K<T>::broadcast_to(adjoint.duplicate().reshape(f.kept), parent->get().shape()));
         });
     }
-    // `mean_axes`: the slice's adjoint over its length.
+    // `mean_axes`: as the sum, divided by the number of elements averaged.
     TensorVar mean_axes(const std::vector<long>& axes, bool keep_dims) const {
         const Folding f = folding(axes, "mean_axes");
         auto parent = this->node_;
@@ -910,8 +913,9 @@ class TensorVar : public Var<Tensor<T>> {
             parent->accumulate(K<T>::broadcast_to(std::move(scaled).reshape(f.kept), parent->get().shape()));
         });
     }
-    // `var_axes`: x̄ += ȳ·2(x − mean)/d, d the correction's divisor; a slice
-    // too short for the correction has a NaN variance and a NaN gradient.
+    // `var_axes`: dvar/dx = 2(x − mean)/d with d the divisor the correction
+    // gives; where there are too few elements for it, value and gradient are
+    // both NaN.
     TensorVar var_axes(const std::vector<long>& axes, Correction correction, bool keep_dims) const {
         const Folding f = folding(axes, "var_axes");
         const bool sample = correction == Correction::Sample;
@@ -957,8 +961,8 @@ class TensorVar : public Var<Tensor<T>> {
     // `TensorVar::mean` (:699-701).
     ScalarVar mean() const { return sum().scale(static_cast<float>(1.0 / static_cast<double>(len()))); }
 
-    // `TensorVar::to_vector` (tape/tensor.rs:733-742): the elements, row
-    // major, as a vector; the adjoint takes this shape back.
+    // `TensorVar::to_vector` (tape/tensor.rs:733-742): the row-major storage
+    // as one vector; backward views the gradient in the tensor's shape.
     VectorVar<T> to_vector() const {
         auto parent = this->node_;
         Vector<T> value(this->value().duplicate().into_storage());
@@ -967,8 +971,8 @@ class TensorVar : public Var<Tensor<T>> {
         }));
     }
 
-    // `TensorVar::to_matrix` (tape/tensor.rs:703-731): the elements, row
-    // major, as a rows × cols matrix; the adjoint takes this shape back.
+    // `TensorVar::to_matrix` (tape/tensor.rs:703-731): the row-major storage
+    // as rows × cols; backward views the gradient in the tensor's shape.
     MatrixVar<T> to_matrix(size_t rows, size_t cols) const {
         if (rows * cols != len()) {
             throw std::invalid_argument("to_matrix: shape " + shape_text(shape()) + " holds " + std::to_string(len()) +
@@ -983,8 +987,9 @@ class TensorVar : public Var<Tensor<T>> {
     }
 
    private:
-    // `folding` (tape/tensor.rs:39-53): the folded axes, the shape with them
-    // kept at extent 1, and the elements of a slice.
+    // `folding` (tape/tensor.rs:39-53): which axes a reduction folds, the
+    // input shape with those axes set to 1, and how many inputs each output
+    // reduces.
     struct Folding {
         std::vector<size_t> folded;
         Shape kept;
