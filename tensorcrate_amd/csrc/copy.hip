@@ -202,71 +202,108 @@ __global__ void __launch_bounds__(256) tile_kernel(const T* __restrict__ src, T*
 }
 
 // The same transpose for 4-byte elements moving 16 bytes a lane on both
-// sides, over TA x TB tiles (TA along `a`, TB along `b`): a lane reads four
-// elements along `a` and, after the LDS exchange, writes four along `b`.  The
-// odd row pitch (TA + 1 words) keeps the column reads of the write phase on
-// distinct banks.  Needs every extent, offset and stride that steps along a
+// sides, over TA x TB tiles (TA along `a`, TB along `b`).  A lane reads four
+// elements along `a` and writes them to LDS as one 16-byte word; after the
+// barrier it reads a 4 x 4 block (four 16-byte words from four consecutive
+// `b` rows), transposes it in registers and writes four 16-byte words along
+// `b`.  So the LDS sees a quarter of the instructions a word-at-a-time
+// exchange would, and no padding: the 16-byte chunks of tile row r sit at
+// chunk ^ ((r / 4) % 16), which puts the 16 rows a quarter-wave reads on
+// distinct bank groups in the second phase and permutes a row's chunks in
+// the first.  Needs every extent, offset and stride that steps along a
 // vector to be a multiple of 4, which the host checks; NT marks a transpose
 // that streams past the Infinity Cache.
 template <typename I, bool NT, int TA, int TB>
 __global__ void __launch_bounds__(256) tile4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
-                                                    TileLayout<I> t) {
-    constexpr int kReadQuads = TA / 4, kReadRows = 256 / kReadQuads;
-    constexpr int kWriteQuads = TB / 4, kWriteRows = 256 / kWriteQuads;
-    __shared__ uint32_t tile[TB][TA + 1];
+                                                    TileLayout<I> t, I tiles) {
+    constexpr int kReadQuads = TA / 4, kReadRows = 256 / kReadQuads;  // first phase: lanes along `a`
+    constexpr int kBlocksB = TB / 4;                                   // second phase: 4 x 4 blocks along `b`
+    constexpr int kBlockRows = 256 / kBlocksB;                         // ... and along `a`, per pass
+    static_assert(TA / 4 >= TB / 4 && (TB & (TB - 1)) == 0, "the swizzle stays within a row");
+    __shared__ __attribute__((aligned(16))) uint32_t tile[TB][TA];
+    auto chunk_at = [](int r, int chunk) { return (chunk ^ ((r / 4) % (TB / 4))) * 4; };
+    // Where tile `block` starts in the source (`from`, plus a0 along `a` and
+    // b0 along `b`) and in the target (`to`).
+    struct Place {
+        I from, to, a0, b0;
+    };
+    auto place_of = [&](I block) {
+        I rest = t.tiles_a_div.div(block);
+        const I tile_a = block - rest * t.tiles_a;
+        I batch = t.tiles_b_div.div(rest);
+        I tile_b = rest - batch * t.tiles_b;
+        // Diagonal order: the blocks running together (neighbouring tile_a)
+        // take different tile_b, so their writes land in different columns
+        // rather than all in the same few (long target rows would otherwise
+        // put them on the same HBM channels: an 8192 x 8192 transpose runs at
+        // 3.9 TB/s without this, 5.8 with it).
+        tile_b += tile_a - t.tiles_b_div.div(tile_a) * t.tiles_b;
+        if (tile_b >= t.tiles_b) tile_b -= t.tiles_b;
+        Place p{0, 0, tile_a * TA, tile_b * TB};
+        for (int k = t.batch_rank - 1; k > 0; k--) {
+            I q = t.batch_div[k].div(batch);
+            I c = batch - q * t.batch_shape[k];
+            p.from += c * t.batch_src[k];
+            p.to += c * t.batch_dst[k];
+            batch = q;
+        }
+        if (t.batch_rank > 0) {
+            p.from += batch * t.batch_src[0];
+            p.to += batch * t.batch_dst[0];
+        }
+        return p;
+    };
+    const int quad = threadIdx.x % kReadQuads, row = threadIdx.x / kReadQuads;
+    uint4 v[TB / kReadRows];
+    auto load = [&](const Place& p) {
+        const I a = p.a0 + quad * 4;
+#pragma unroll
+        for (int pass = 0; pass < TB / kReadRows; pass++) {
+            const I b = p.b0 + row + pass * kReadRows;
+            if (a < t.extent_a && b < t.extent_b) v[pass] = load_word<NT>(src + p.from + a + b * t.src_b);
+        }
+    };
+    // Each block walks every gridDim.x-th tile; the next tile's loads are
+    // in flight while this one's stores go out.
     I block = blockIdx.x;
-    I rest = t.tiles_a_div.div(block);
-    const I tile_a = block - rest * t.tiles_a;
-    I batch = t.tiles_b_div.div(rest);
-    I tile_b = rest - batch * t.tiles_b;
-    // Diagonal order: the blocks running together (neighbouring tile_a)
-    // take different tile_b, so their writes land in different columns
-    // rather than all in the same few (long target rows would otherwise put
-    // them on the same HBM channels: an 8192 x 8192 transpose runs at 3.9
-    // TB/s without this, 5.8 with it).
-    tile_b += tile_a - t.tiles_b_div.div(tile_a) * t.tiles_b;
-    if (tile_b >= t.tiles_b) tile_b -= t.tiles_b;
-    I from = 0, to = 0;
-    for (int k = t.batch_rank - 1; k > 0; k--) {
-        I q = t.batch_div[k].div(batch);
-        I c = batch - q * t.batch_shape[k];
-        from += c * t.batch_src[k];
-        to += c * t.batch_dst[k];
-        batch = q;
-    }
-    if (t.batch_rank > 0) {
-        from += batch * t.batch_src[0];
-        to += batch * t.batch_dst[0];
-    }
-    const I a0 = tile_a * TA, b0 = tile_b * TB;
-    {
-        const int quad = threadIdx.x % kReadQuads, row = threadIdx.x / kReadQuads;
-        const I a = a0 + quad * 4;
-        uint4 v[TB / kReadRows];
+    Place here = place_of(block);
+    load(here);
+    for (;;) {
 #pragma unroll
         for (int pass = 0; pass < TB / kReadRows; pass++) {
-            const I b = b0 + row + pass * kReadRows;
-            if (a < t.extent_a && b < t.extent_b) v[pass] = load_word<NT>(src + from + a + b * t.src_b);
+            const int r = row + pass * kReadRows;
+            *reinterpret_cast<uint4*>(&tile[r][chunk_at(r, quad)]) = v[pass];
         }
-#pragma unroll
-        for (int pass = 0; pass < TB / kReadRows; pass++) {
-            uint32_t* at = &tile[row + pass * kReadRows][quad * 4];
-            at[0] = v[pass].x, at[1] = v[pass].y, at[2] = v[pass].z, at[3] = v[pass].w;
+        __syncthreads();
+        const I next = block + gridDim.x;
+        Place there{};
+        if (next < tiles) {
+            there = place_of(next);
+            load(there);
         }
-    }
-    __syncthreads();
-    {
-        const int quad = threadIdx.x % kWriteQuads, row = threadIdx.x / kWriteQuads;
-        const I b = b0 + quad * 4;
+        const int cb = threadIdx.x % kBlocksB;
+        const I b = here.b0 + cb * 4;
 #pragma unroll
-        for (int pass = 0; pass < TA / kWriteRows; pass++) {
-            const I aa = a0 + row + pass * kWriteRows;
-            if (aa < t.extent_a && b < t.extent_b) {
-                const int c = row + pass * kWriteRows;
-                const uint4 v{tile[quad * 4][c], tile[quad * 4 + 1][c], tile[quad * 4 + 2][c], tile[quad * 4 + 3][c]};
-                store_word<NT>(dst + to + b + aa * t.dst_a, v);
+        for (int pass = 0; pass < TA / 4 / kBlockRows; pass++) {
+            const int ca = threadIdx.x / kBlocksB + pass * kBlockRows;
+            uint4 q[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                q[r] = *reinterpret_cast<const uint4*>(&tile[cb * 4 + r][chunk_at(cb * 4 + r, ca)]);
+            }
+            const I aa = here.a0 + ca * 4;
+            uint32_t* out = dst + here.to + b + aa * t.dst_a;
+            if (b < t.extent_b) {
+                if (aa < t.extent_a) store_word<NT>(out, uint4{q[0].x, q[1].x, q[2].x, q[3].x});
+                if (aa + 1 < t.extent_a) store_word<NT>(out + t.dst_a, uint4{q[0].y, q[1].y, q[2].y, q[3].y});
+                if (aa + 2 < t.extent_a) store_word<NT>(out + 2 * t.dst_a, uint4{q[0].z, q[1].z, q[2].z, q[3].z});
+                if (aa + 3 < t.extent_a) store_word<NT>(out + 3 * t.dst_a, uint4{q[0].w, q[1].w, q[2].w, q[3].w});
             }
         }
+        if (next >= tiles) break;
+        __syncthreads();  // every wave has read the tile before the next is written
+        block = next;
+        here = there;
     }
 }
 
@@ -363,24 +400,26 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
             return tiles_a * tiles_b * batches;
         };
         // Four-byte elements whose rows start on 16-byte boundaries move 16
-        // bytes a lane, one tile a block (so at most 2^24 - 1 tiles, the
-        // work-items one dispatch holds).
+        // bytes a lane; a block walks several tiles, at most eight blocks a
+        // CU.
         // 128 x 64 tiles: 512-byte reads and 256-byte writes per row, the
         // best of the shapes measured on the config-3 permute, an 8192^2
-        // transpose and a [64, 1024, 1024] batch.
+        // transpose and a [64, 1024, 1024] batch (128 x 128 measured the
+        // same: 70% of HBM on the permute, 64% on a 4096^2 transpose).
         constexpr int TA = 128, TB = 64;
         uint64_t blocks = tiled(TA, TB);
-        bool wide = sizeof(T) == 4 && blocks <= 0xffffffu && walk.shape[axis_a] % 4 == 0 &&
+        bool wide = sizeof(T) == 4 && blocks <= UINT32_MAX && walk.shape[axis_a] % 4 == 0 &&
                     walk.shape[axis_b] % 4 == 0 && walk.strides[0][axis_b] % 4 == 0 &&
                     walk.strides[1][axis_a] % 4 == 0 && aligned16(src) && aligned16(dst);
         for (int k = 0; wide && k < t.batch_rank; k++) wide = t.batch_src[k] % 4 == 0 && t.batch_dst[k] % 4 == 0;
         if (wide) {
             const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
             uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+            const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>(blocks, 8 * compute_units()));
             if (stream) {
-                tile4_kernel<I, true, TA, TB><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
+                tile4_kernel<I, true, TA, TB><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
             } else {
-                tile4_kernel<I, false, TA, TB><<<static_cast<uint32_t>(blocks), 256, 0, s>>>(s32, d32, t);
+                tile4_kernel<I, false, TA, TB><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
             }
             return check_launch("strided copy");
         }
