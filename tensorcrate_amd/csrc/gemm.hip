@@ -283,28 +283,25 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
 // The tiled kernels' shapes: a 256 x 256 tile over eight waves of 128 x 64
 // (two waves per SIMD, so one's waits overlap the other's matrix-core
 // steps), and a 128 x 128 tile over four waves of 64 x 64 for products too
-// small to give every CU a few large tiles.  Products of at least a tile a
-// CU run the 16 x 16 x 32 kernel, a tile a block; plain ones whose tiles are
-// short (K up to kShortK) and outnumber the CUs run the persistent 32 x 32 x
-// 16 kernel instead, which starts each tile's loads under the previous
-// tile's steps (on MI355X, f16 16384 x 4096 x 1024: 988 TFLOP/s against 822
-// a tile a block).
-constexpr uint32_t kShortK = 2048;
-
+// small to give every CU a tile.  Products of at least a tile a CU run the
+// 16 x 16 x 32 kernels: the persistent one for plain stores and whole pairs
+// of steps (on MI355X, bf16 8192^3: 1443 against 1395 TFLOP/s a tile a
+// block; f16 16384 x 4096 x 1024: 1203 against 1065 for the persistent 32 x
+// 32 x 16 kernel it replaced), the one-tile kernel for program epilogues
+// and odd step counts.
 template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
                     hipStream_t s, const EPI& epi = EPI{}) {
     const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
     const uint32_t cus = static_cast<uint32_t>(compute_units());
-    if constexpr (!EPI::kProgram) {
-        // Several short tiles a CU and whole pairs of steps: the persistent form.
-        if (large > cus && k <= kShortK && ((k + 63) / 64) % 2 == 0) {
-            direct16_persistent_kernel<S, O, A_KC, B_KC, 256, 256, 2, 4, 64><<<cus, 2 * 4 * 64, 0, s>>>(
-                a, b, c, m, n, k, accumulate);
-            return;
-        }
-    }
     if (large >= cus) {
+        if constexpr (!EPI::kProgram) {
+            // k >= 8 here, so an even step count is at least two.
+            if (((k + 63) / 64) % 2 == 0) {
+                gemm16x16_persistent_kernel<S, O, A_KC, B_KC><<<cus, 512, 0, s>>>(a, b, c, m, n, k, accumulate);
+                return;
+            }
+        }
         gemm16x16_kernel<S, O, A_KC, B_KC, EPI><<<large, 512, 0, s>>>(a, b, c, m, n, k, accumulate, epi);
     } else {
         const uint32_t small = ((m + 127) / 128) * ((n + 127) / 128);

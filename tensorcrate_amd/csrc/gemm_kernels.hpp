@@ -15,6 +15,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // The descriptor word that makes a gfx9-family buffer resource a plain,
 // untyped byte range (32-bit data format, no swizzle, no stride).
@@ -707,155 +709,6 @@ __global__ void __launch_bounds__(WM * WN * 64) direct16_kernel(const S* __restr
         }
     }
 }
-// The tiled kernel made persistent, for products whose K is short: a block
-// owns every gridDim.x-th block tile in turn, and the last step of one tile
-// stages the first step of the next, so neither the next tile's first HBM
-// loads nor this tile's stores sit between two tiles' matrix-core steps.
-// The step loop, stages and weave are the tiled kernel's; a tile's steps
-// must come in whole pairs (an even step count) so that every tile starts on
-// stage 0.  Plain stores only: a program epilogue needs the LDS the next
-// tile's first step already occupies.
-template <typename S, typename O, bool A_KC, bool B_KC, int BM, int BN, int WM, int WN, int BK>
-__global__ void __launch_bounds__(WM * WN * 64) direct16_persistent_kernel(const S* __restrict__ A,
-                                                                           const S* __restrict__ B,
-                                                                           O* __restrict__ C, uint32_t M, uint32_t N,
-                                                                           uint32_t K, bool accumulate) {
-    constexpr int NS = 2;
-    constexpr int kWaves = WM * WN;
-    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-    constexpr int kA = BM * BK, kB = BN * BK;
-
-    const uint32_t tiles_m = (M + BM - 1) / BM;
-    const uint32_t tiles_n = (N + BN - 1) / BN;
-    const uint32_t tiles = tiles_m * tiles_n;
-    uint32_t tile = blockIdx.x;
-    if (tile >= tiles) return;
-    uint32_t tm, tn;
-    tile_of(tile, tiles_m, tiles_n, tm, tn);
-    uint32_t m0 = tm * BM, n0 = tn * BN;
-    const int lane = threadIdx.x % 64;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    const int wm = wave / WN, wn = wave % WN;
-
-    using StagerA = DirectStager<S, BM, A_KC, kWaves, BK>;
-    using StagerB = DirectStager<S, BN, B_KC, kWaves, BK>;
-    StagerA sa;
-    StagerB sb;
-    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
-    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
-
-    f32x16 acc[TM][TN];
-    uint4 fa[2][TM], fb[2][TN];
-    auto read_fragments = [&](int slot, const S* la, const S* lb, int kk) {
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-            fa[slot][i] = swizzled_fragment<S, BM, A_KC, BK>(la, wm * (BM / WM) + i * 32, kk, lane);
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-            fb[slot][j] = swizzled_fragment<S, BN, B_KC, BK>(lb, wn * (BN / WN) + j * 32, kk, lane);
-    };
-
-    constexpr int kSlices = BK / 16;
-    constexpr int kSteps = TM * TN;
-    constexpr int kReads = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
-    constexpr int kLoads = StagerA::kPer + StagerB::kPer;
-    const uint32_t steps = (K + BK - 1) / BK;
-    // Step s of this tile; s == steps is the next tile's first step, or,
-    // after the last tile, a harmless reload of this tile's last.
-    auto stage_of = [&](auto t, uint32_t s) {
-        uint32_t k0;
-        if (s < steps) {
-            k0 = s * BK;
-        } else if (tile + gridDim.x < tiles) {
-            uint32_t next_m, next_n;
-            tile_of(tile + gridDim.x, tiles_m, tiles_n, next_m, next_n);
-            sa.retarget(A, next_m * BM, M, A_KC ? K : M, K);
-            sb.retarget(B, next_n * BN, N, B_KC ? K : N, K);
-            k0 = 0;
-        } else {
-            k0 = (steps - 1) * BK;
-        }
-        sa.fetch(stage_tile<S, kA, 2 * decltype(t)::value>(), k0, K, k0 + BK <= K);
-        sb.fetch(stage_tile<S, kB, 2 * decltype(t)::value + 1>(), k0, K, k0 + BK <= K);
-    };
-    auto step = [&](auto t, uint32_t s) {
-        constexpr int T = decltype(t)::value;
-        const S* la = stage_tile<S, kA, 2 * T>();
-        const S* lb = stage_tile<S, kB, 2 * T + 1>();
-        stage_of(std::integral_constant<int, (T + NS - 1) % NS>{}, s + NS - 1);
-#pragma unroll
-        for (int q = 0; q + 1 < kSlices; q++) {
-            read_fragments((q + 1) & 1, la, lb, (q + 1) * 16);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[q & 1][i], fb[q & 1][j], acc[i][j]);
-        }
-        weave<kSteps, kLoads, kReads, kSlices - 1>();
-        __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // step s + 1 is in LDS
-        __syncthreads();
-        constexpr int last = (kSlices - 1) & 1;
-        constexpr int U = (T + 1) % NS;
-        read_fragments(last ^ 1, stage_tile<S, kA, 2 * U>(), stage_tile<S, kB, 2 * U + 1>(), 0);
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) acc[i][j] = Mfma16<S>::step(fa[last][i], fb[last][j], acc[i][j]);
-        weave<kSteps, 0, kReads, 2>();
-    };
-    stage_of(std::integral_constant<int, 0>{}, 0);
-    __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // the first tile's first step is in LDS
-    __syncthreads();
-    read_fragments(0, stage_tile<S, kA, 0>(), stage_tile<S, kB, 1>(), 0);
-    for (;;) {
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
-        for (uint32_t s = 0; s < steps; s += NS) {
-            step(std::integral_constant<int, 0>{}, s);
-            step(std::integral_constant<int, 1>{}, s + 1);
-        }
-        if (m0 + BM <= M && n0 + BN <= N) {
-            // A whole tile: no bounds to check, and each lane's column walks
-            // down from one base pointer in steps of N.
-            O* base = C + static_cast<uint64_t>(m0 + wm * (BM / WM) + 4 * (lane / 32)) * N + n0 + wn * (BN / WN) +
-                      lane % 32;
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const uint32_t r = i * 32 + 8 * (e / 4) + e % 4;
-                        store_out(base, static_cast<uint64_t>(r) * N + j * 32, acc[i][j][e], accumulate);
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const uint32_t col = n0 + wn * (BN / WN) + j * 32 + lane % 32;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const uint32_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
-                        if (row < M && col < N) {
-                            store_out(C, static_cast<uint64_t>(row) * N + col, acc[i][j][e], accumulate);
-                        }
-                    }
-                }
-            }
-        }
-        tile += gridDim.x;
-        if (tile >= tiles) break;
-        tile_of(tile, tiles_m, tiles_n, tm, tn);
-        m0 = tm * BM;
-        n0 = tn * BN;
-    }
-}
-
 // ---- the 16 x 16 x 32 kernel ---------------------------------------------------
 //
 // The large-product kernel: 256 x 256 block tiles over eight waves of 128 x 64
@@ -1208,6 +1061,232 @@ __global__ void __launch_bounds__(512) gemm16x16_kernel(const S* __restrict__ A,
                     if (col + e < N) store_out(at, e, acc[i][j][e], accumulate);
             }
         }
+    }
+    // No direct load may still be writing LDS when the block ends.
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));
+}
+
+// The 16 x 16 x 32 kernel made persistent: one block a CU walks every
+// gridDim.x-th tile, so a tile's first loads and the previous tile's stores
+// do not sit between two tiles' matrix-core steps.
+//  - The step loop is the one-tile kernel's, in pairs; the last pair of a
+//    tile fetches the next tile's first two steps (its operand resources are
+//    retargeted at the top of that pair), and the last step's trailing reads
+//    are the next tile's first fragments.  Steps must come in whole pairs
+//    (an even count) so that every tile starts on stage 0.
+//  - A whole tile of 16-bit C is stored as whole rows: each wave stages a
+//    quarter of its 128 x 64 results at a time in its own 4 KiB of a further
+//    32 KiB of LDS (16-byte chunk c of row r at c ^ (r % 8)) and writes them
+//    back 16 bytes a lane, eight lanes a 128-byte row.  Measured on MI355X at
+//    f16 16384 x 4096 x 1024, against 8-byte stores straight from the
+//    accumulators (16 rows of 32 bytes an instruction): 114 against 129 us.
+//    The staging's LDS accesses are written as inline assembly: the compiler
+//    cannot tell the staging array from the stages the direct loads are
+//    filling, and would otherwise wait for the next tile's loads before the
+//    first staging write.  Within a wave, LDS accesses complete in order.
+//  - Edge tiles, f32 C and accumulation store from the accumulators, as the
+//    one-tile kernel does.
+// Plain stores only: a program epilogue needs LDS that the next tile's
+// first steps already occupy.
+template <typename S, typename O, bool A_KC, bool B_KC>
+__global__ void __launch_bounds__(512) gemm16x16_persistent_kernel(const S* __restrict__ A, const S* __restrict__ B,
+                                                                    O* __restrict__ C, uint32_t M, uint32_t N,
+                                                                    uint32_t K, bool accumulate) {
+    constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
+    constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+    constexpr int kA = BM * BK, kB = BN * BK;
+    using StagerA = StrideStager<S, BM, A_KC, kWaves, BK>;
+    using StagerB = StrideStager<S, BN, B_KC, kWaves, BK>;
+    constexpr int kLoads = StagerA::kPer + StagerB::kPer;
+    constexpr int kReads = TM * (A_KC ? 1 : 2) + TN * (B_KC ? 1 : 2);
+    constexpr int kRegion = 4096;  // staging bytes a wave
+
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    const uint32_t tiles = tiles_m * tiles_n;
+    uint32_t tile = blockIdx.x;
+    if (tile >= tiles) return;
+    uint32_t tm, tn;
+    tile_of(tile, tiles_m, tiles_n, tm, tn);
+    uint32_t m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int wm = wave / WN, wn = wave % WN;
+
+    StagerA sa;
+    StagerB sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
+    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
+
+    uint32_t a_off[A_KC ? 2 : TM], b_off[B_KC ? 2 : TN];
+    if constexpr (A_KC) {
+        a_off[0] = kc16_offset(lane, wm * (BM / WM), 0);
+        a_off[1] = kc16_offset(lane, wm * (BM / WM), 1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++) a_off[i] = rc16_offset<BM>(lane, wm * (BM / WM), i);
+    }
+    if constexpr (B_KC) {
+        b_off[0] = kc16_offset(lane, wn * (BN / WN), 0);
+        b_off[1] = kc16_offset(lane, wn * (BN / WN), 1);
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; j++) b_off[j] = rc16_offset<BN>(lane, wn * (BN / WN), j);
+    }
+    auto frag_a = [&](const S* t, int i, int q) __attribute__((always_inline)) {
+        return A_KC ? lds_b128(t, a_off[q] + 2048 * i) : lds_tr_pair<S, BM>(t, a_off[i] + q * 32 * BM * 2);
+    };
+    auto frag_b = [&](const S* t, int j, int q) __attribute__((always_inline)) {
+        return B_KC ? lds_b128(t, b_off[q] + 2048 * j) : lds_tr_pair<S, BN>(t, b_off[j] + q * 32 * BN * 2);
+    };
+
+    f32x4 acc[TM][TN];
+    uint4 fa[TM], fb[2][TN];
+    const uint32_t steps = (K + BK - 1) / BK;
+    auto fetch = [&](auto t, uint32_t k0) __attribute__((always_inline)) {
+        sa.fetch(stage_tile<S, kA, 2 * decltype(t)::value>(), k0, K, k0 + BK <= K);
+        sb.fetch(stage_tile<S, kB, 2 * decltype(t)::value + 1>(), k0, K, k0 + BK <= K);
+    };
+    auto read_b = [&](int slot, const S* lb, int q) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) fb[slot][j] = frag_b(lb, j, q);
+    };
+    auto slice = [&](int slot, const S* la, int q) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = Mfma16x16<S>::step(fb[slot][j], fa[i], acc[i][j]);
+            fa[i] = frag_a(la, i, q);
+        }
+    };
+    // One step from stage T; after its barrier, stage T takes the step at
+    // `k_next` (of this tile or the next).
+    auto step = [&](auto t, uint32_t k_next) __attribute__((always_inline)) {
+        constexpr int T = decltype(t)::value;
+        constexpr int U = T ^ 1;
+        read_b(1, stage_tile<S, kB, 2 * T + 1>(), 1);
+        slice(0, stage_tile<S, kA, 2 * T>(), 1);
+        weave16<TM, TN, kReads, 0, 1>();
+        __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));  // the next step is in LDS; stage T is read
+        bare_barrier();
+        fetch(t, k_next);
+        read_b(0, stage_tile<S, kB, 2 * U + 1>(), 0);
+        slice(1, stage_tile<S, kA, 2 * U>(), 0);
+        weave16<TM, TN, kReads, kLoads, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Each lane's staging offsets: where it writes the quad of columns
+    // 16 j + 4 (lane / 16) of row r (16-byte chunk 2 j + lane / 32), and
+    // where it reads chunk lane % 8 of row lane / 8 (and 8, 16, 24 rows on,
+    // which share the row's swizzle).
+    __shared__ __attribute__((aligned(1024))) uint8_t rows_lds[kWaves * kRegion];
+    const uint32_t region = static_cast<uint32_t>(reinterpret_cast<uint64_t>(
+                                (__attribute__((address_space(3))) uint8_t*)(rows_lds))) +
+                            wave * kRegion;
+    const uint32_t read_at = region + (lane / 8) * 128 + (((lane % 8) ^ (lane / 8)) * 16);
+    const uint32_t row_off = ((lane / 8) * N + 8 * (lane % 8)) * sizeof(O);
+    const bool rows_ok = sizeof(O) == 2 && (N % 8) == 0 && (reinterpret_cast<uint64_t>(C) % 16) == 0 && !accumulate;
+
+    fetch(std::integral_constant<int, 0>{}, 0);
+    fetch(std::integral_constant<int, 1>{}, BK);
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(kLoads));  // the first step is in LDS
+    bare_barrier();
+    read_b(0, stage_tile<S, kB, 1>(), 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) fa[i] = frag_a(stage_tile<S, kA, 0>(), i, 0);
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = f32x4{};
+        for (uint32_t s = 0; s < steps; s += 2) {
+            uint32_t k_next = (s + 2) * BK;
+            if (s + 2 == steps) {
+                // After the last tile, its own first steps again: harmless
+                // loads into stages nobody reads.
+                const uint32_t next = tile + gridDim.x < tiles ? tile + gridDim.x : tile;
+                uint32_t nm, nn;
+                tile_of(next, tiles_m, tiles_n, nm, nn);
+                sa.retarget(A, nm * BM, M, A_KC ? K : M, K);
+                sb.retarget(B, nn * BN, N, B_KC ? K : N, K);
+                k_next = 0;
+            }
+            step(std::integral_constant<int, 0>{}, k_next);
+            step(std::integral_constant<int, 1>{}, k_next + BK);
+        }
+        // lane holds C[row][col .. col + 3] for row = m0 + wm*128 + 16 i + lane % 16,
+        // col = n0 + wn*64 + 16 j + 4 (lane / 16).
+        if (rows_ok && m0 + BM <= M && n0 + BN <= N) {
+          if constexpr (sizeof(O) == 2) {
+            using E = Elem<O>;
+            const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+                C + static_cast<uint64_t>(m0 + wm * (BM / WM)) * N + n0 + wn * (BN / WN), 0, 0x7fffffff,
+                kBufferFlags);
+            const int g = lane / 16;
+#pragma unroll
+            for (int p = 0; p < TM / 2; p++) {
+#pragma unroll
+                for (int ii = 0; ii < 2; ii++) {
+                    const int r = ii * 16 + lane % 16;
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const f32x4 v = acc[2 * p + ii][j];
+                        u32x2 out;
+                        out.x = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[0]))) |
+                                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[1]))) << 16);
+                        out.y = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[2]))) |
+                                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[3]))) << 16);
+                        const uint32_t at = region + r * 128 + (((2 * j + g / 2) ^ (r % 8)) * 16) + (g % 2) * 8;
+                        asm volatile("ds_write_b64 %0, %1" ::"v"(at), "v"(out) : "memory");
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                u32x4 v0, v1, v2, v3;
+                asm volatile(
+                    "ds_read_b128 %0, %4\n\t"
+                    "ds_read_b128 %1, %4 offset:1024\n\t"
+                    "ds_read_b128 %2, %4 offset:2048\n\t"
+                    "ds_read_b128 %3, %4 offset:3072\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+                    : "v"(read_at)
+                    : "memory");
+                const uint32_t first = __builtin_amdgcn_readfirstlane(32 * p * N * sizeof(O));
+                const uint32_t eight = __builtin_amdgcn_readfirstlane(8 * N * sizeof(O));
+                __builtin_amdgcn_raw_buffer_store_b128(v0, rc, row_off, first, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(v1, rc, row_off, first + eight, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(v2, rc, row_off, first + 2 * eight, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(v3, rc, row_off, first + 3 * eight, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        } else {
+            const bool quads = (N % 4) == 0 && (reinterpret_cast<uint64_t>(C) % (4 * sizeof(O))) == 0;
+            const uint32_t row0 = m0 + wm * (BM / WM) + lane % 16;
+            const uint32_t col0 = n0 + wn * (BN / WN) + 4 * (lane / 16);
+            O* base = C + static_cast<uint64_t>(row0) * N + col0;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const uint32_t row = row0 + 16 * i, col = col0 + 16 * j;
+                    O* at = base + static_cast<uint64_t>(16 * i) * N + 16 * j;
+                    if (quads && row < M && col + 4 <= N) {
+                        store_quad(at, acc[i][j], accumulate);
+                    } else if (row < M) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (col + e < N) store_out(at, e, acc[i][j][e], accumulate);
+                    }
+                }
+            }
+        }
+        tile += gridDim.x;
+        if (tile >= tiles) break;
+        tile_of(tile, tiles_m, tiles_n, tm, tn);
+        m0 = tm * BM;
+        n0 = tn * BN;
     }
     // No direct load may still be writing LDS when the block ends.
     __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));

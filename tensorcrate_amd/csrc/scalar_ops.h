@@ -24,10 +24,14 @@ __host__ __device__ inline float tc_bf16_to_f32(unsigned short bits) {
 // `half::bf16::from_f32` that the reference narrows with.  Adding 0x7fff plus
 // the kept half's lowest bit carries into the kept half exactly when the
 // dropped half is above one half, or exactly one half with an odd kept half.
+// Both results are formed and one selected, so a wave converts without
+// branching (a branch per element costs a kernel's epilogue a dozen
+// instructions each).
 __host__ __device__ inline unsigned short tc_f32_to_bf16(float value) {
     const unsigned x = __float_as_uint(value);
-    if ((x & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((x >> 16) | 0x0040u);
-    return static_cast<unsigned short>((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+    const unsigned rounded = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+    const unsigned quiet = (x >> 16) | 0x0040u;
+    return static_cast<unsigned short>((x & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 // `BinaryOp` in f32 (kernels.rs:431-437); the caller rounds once.  `Rem` is

@@ -204,11 +204,10 @@ def sampled_form(kind, form, m, k, n, rng, addend):
 @pytest.mark.parametrize("m,k,n", [(4200, 128, 4200), (4200, 192, 4200), (4352, 1024, 4352), (4100, 1024, 4200),
                                    (4104, 2120, 4200), (4200, 2176, 4104), (4352, 4096, 4352)])
 def test_products_with_more_tiles_than_compute_units(kind, form, addend, m, k, n):
-    # More 256 x 256 tiles than the part's 256 CUs.  Short K with an even
-    # step count takes the persistent kernel, where a block walks several
-    # tiles in turn; an odd step count (192) and long K (from 2120 on) take
-    # the 16 x 16 x 32 kernel, a tile a block, including a K tail that is not
-    # a whole 64-deep step (2120 = 33 x 64 + 8).  Ragged edges in both
+    # More 256 x 256 tiles than the part's 256 CUs.  An even step count
+    # takes the persistent kernel, where a block walks several tiles in turn,
+    # including a K tail that is not a whole 64-deep step (2120 = 33 x 64 +
+    # 8, 34 steps); an odd step count (192, 2176) takes the one-tile kernel.  Ragged edges in both
     # dimensions (4200 = 16 x 256 + 104), whole tiles only (4352 = 17 x 256),
     # and a ragged M with whole-tile columns; every form the tape's backward
     # products take (LEFT is Aᵀ·B, RIGHT is A·Bᵀ, tape/mod.rs:1195-1246),
@@ -218,6 +217,28 @@ def test_products_with_more_tiles_than_compute_units(kind, form, addend, m, k, n
     got, want, scale = sampled_form(kind, form, m, k, n, rng, addend)
     tol = tolerance(kind, kind, k) + (2.0 ** -8 if addend else 0.0)
     assert np.max(np.abs(got - want) / scale) <= tol
+
+
+@pytest.mark.parametrize("in_kind,out_kind", [(lib.BF16, lib.BF16), (lib.F16, lib.F16), (lib.BF16, lib.F32),
+                                              (lib.F16, lib.F32)])
+@pytest.mark.parametrize("form", [lib.PLAIN, lib.RIGHT], ids=["plain", "right"])
+def test_every_element_of_a_persistent_product(in_kind, out_kind, form):
+    # 4352 x 128 x 4352: 289 whole 256 x 256 tiles on 256 CUs, so some blocks
+    # walk two tiles, each of two steps.  A 16-bit C leaves through the
+    # staged whole-row stores, an f32 C through the accumulators' own; every
+    # element is checked against the oracle and f64, so a misplaced row or
+    # chunk of the staging cannot hide between sampled rows.
+    m, k, n = 4352, 128, 4352
+    rng = np.random.default_rng(4352 + out_kind + 5 * form)
+    a = to_kind(rng.uniform(-1, 1, (m, k)), in_kind)
+    b = to_kind(rng.uniform(-1, 1, (k, n)), in_kind)
+    y = np.ascontiguousarray(b.T) if form == lib.RIGHT else b
+    wa, wb = widen(in_kind, a), widen(in_kind, b)
+    got = widen(out_kind, product(in_kind, out_kind, form, a, y, m, k, n))
+    tol = tolerance(in_kind, out_kind, k)
+    assert error(got, wa, wb, wa.astype(np.float64) @ wb.astype(np.float64)) <= tol
+    want = widen(out_kind, oracle.matmul(in_kind, a, b, m, k, n, out_dtype=out_kind))
+    assert error(got, wa, wb, want) <= 2 * tol
 
 
 @pytest.mark.parametrize("kind", [lib.F32, lib.BF16, lib.F16], ids=["f32", "bf16", "f16"])
