@@ -17,6 +17,21 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two f32 values rounded once to the 16-bit O and packed, the first in the
+// low half: one gfx950 conversion instruction a pair, with the rounding of
+// Elem<O>::narrow (IEEE round to nearest even; tc_f32_to_bf16's rule for bf16).
+template <typename O>
+__device__ __forceinline__ uint32_t pack_pair(float lo, float hi) {
+    if constexpr (std::is_same<O, _Float16>::value) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+    }
+}
 
 // The descriptor word that makes a gfx9-family buffer resource a plain,
 // untyped byte range (32-bit data format, no swizzle, no stride).
@@ -894,10 +909,8 @@ __device__ __forceinline__ void store_quad(O* at, f32x4 v, bool accumulate) {
             v[3] += E::widen(__builtin_bit_cast(O, static_cast<uint16_t>(old.y >> 16)));
         }
         uint2 out;
-        out.x = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[0]))) |
-                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[1]))) << 16);
-        out.y = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[2]))) |
-                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[3]))) << 16);
+        out.x = pack_pair<O>(v[0], v[1]);
+        out.y = pack_pair<O>(v[2], v[3]);
         *reinterpret_cast<uint2*>(at) = out;
     }
 }
@@ -1219,7 +1232,6 @@ __global__ void __launch_bounds__(512) gemm16x16_persistent_kernel(const S* __re
         // col = n0 + wn*64 + 16 j + 4 (lane / 16).
         if (rows_ok && m0 + BM <= M && n0 + BN <= N) {
           if constexpr (sizeof(O) == 2) {
-            using E = Elem<O>;
             const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
                 C + static_cast<uint64_t>(m0 + wm * (BM / WM)) * N + n0 + wn * (BN / WN), 0, 0x7fffffff,
                 kBufferFlags);
@@ -1232,11 +1244,7 @@ __global__ void __launch_bounds__(512) gemm16x16_persistent_kernel(const S* __re
 #pragma unroll
                     for (int j = 0; j < TN; j++) {
                         const f32x4 v = acc[2 * p + ii][j];
-                        u32x2 out;
-                        out.x = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[0]))) |
-                                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[1]))) << 16);
-                        out.y = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[2]))) |
-                                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, E::narrow(v[3]))) << 16);
+                        const u32x2 out = {pack_pair<O>(v[0], v[1]), pack_pair<O>(v[2], v[3])};
                         const uint32_t at = region + r * 128 + (((2 * j + g / 2) ^ (r % 8)) * 16) + (g % 2) * 8;
                         asm volatile("ds_write_b64 %0, %1" ::"v"(at), "v"(out) : "memory");
                     }

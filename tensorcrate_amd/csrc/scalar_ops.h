@@ -24,14 +24,18 @@ __host__ __device__ inline float tc_bf16_to_f32(unsigned short bits) {
 // `half::bf16::from_f32` that the reference narrows with.  Adding 0x7fff plus
 // the kept half's lowest bit carries into the kept half exactly when the
 // dropped half is above one half, or exactly one half with an odd kept half.
-// Both results are formed and one selected, so a wave converts without
-// branching (a branch per element costs a kernel's epilogue a dozen
-// instructions each).
+// On the device, gfx950's conversion instruction (v_cvt_pk_bf16_f32) is this
+// rule exactly: run over every one of the 2^32 f32 bit patterns on MI355X it
+// gave the bits below for all of them, NaN payloads included.
 __host__ __device__ inline unsigned short tc_f32_to_bf16(float value) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_bit_cast(unsigned short, static_cast<__bf16>(value));
+#else
     const unsigned x = __float_as_uint(value);
     const unsigned rounded = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
     const unsigned quiet = (x >> 16) | 0x0040u;
     return static_cast<unsigned short>((x & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
+#endif
 }
 
 // `BinaryOp` in f32 (kernels.rs:431-437); the caller rounds once.  `Rem` is
