@@ -47,12 +47,13 @@ HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
 # HBM bytes per launch of the headline product, from `rocprofv3 --pmc
 # FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --traffic-probe`,
 # scaled by what the counters read for a plain 1 GiB copy (fetch x 2.0,
-# write x 0.998): 1.625 GB read + 0.161 GB written (profiles/gemm_bf16_8192_traffic.md).
-HEADLINE_TRAFFIC = 1.786e9
+# write x 0.9994): 1.801 GB read + 0.134 GB written (profiles/gemm_bf16_8192_traffic.md).
+HEADLINE_TRAFFIC = 1.935e9
 # HBM bytes per call of each bandwidth workload, from the same two counters
 # over `bench.py --traffic-probe` with the same calibration
 # (profiles/bandwidth_traffic.md): within 5% of the algorithmic bytes.
 MEASURED_TRAFFIC = {
+    "f16 GEMM 16384x1024x4096": 3.419e+08,
     "x*y, f32 [256,512,512] x [1,512,1]": 5.365e+08,
     "t+z, f32 [256,512,512] + [256,1,512]": 5.407e+08,
     "permute(0,2,1).contiguous, f32 [256,512,512]": 5.365e+08,
@@ -201,7 +202,8 @@ class Product:
             "unit": "TFLOP/s",
             "ms": ms,
             "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind], "unit": "TFLOP/s",
-                         "frac": achieved / MFMA_PEAK[kind], "traffic": None, "kernel_ms": kernel_ms},
+                         "frac": achieved / MFMA_PEAK[kind],
+                         "traffic": MEASURED_TRAFFIC.get(f"{kind} GEMM {m}x{k}x{n}"), "kernel_ms": kernel_ms},
         }
 
 
@@ -399,6 +401,27 @@ def rotating(inputs: list, call):
     """A zero-argument function calling `call` on the next of `inputs`."""
     turn = itertools.count()
     return lambda: call(inputs[next(turn) % len(inputs)])
+
+
+def launch_floor(steps: int, warmup: int) -> dict:
+    """What one graph-replayed launch costs with no work in it: a copy of one
+    f32 element through `tc_strided_copy`, timed as the bandwidth lines are.
+    A launch moving B bytes cannot take less than this plus B / 8 TB/s, so at
+    32 MiB no single launch reaches more than about 70% of HBM."""
+    src, dst = lib.Buffer(16), lib.Buffer(16)
+    shape = lib.dims([1])
+    at = lib.strided(0, [1])
+    ms = timed_graph(lambda: lib.call("tc_strided_copy", 4, src.ptr, 1, 1, shape, ctypes.byref(at), dst.ptr),
+                     steps, warmup)
+    src.free()
+    dst.free()
+    us = ms * 1e3
+    ceiling = (32 << 20) / ((32 << 20) / (HBM_PEAK * 1e9) + us * 1e-6) / 1e9
+    return {"workload": "launch floor: a one-element copy, graph-replayed", "value": us, "unit": "us/launch",
+            "higher_is_better": False, "ms": ms,
+            "roofline": {"bound": "launch", "achieved": None, "peak": None, "unit": "GB/s", "frac": None,
+                         "traffic": None, "ceiling_32MiB_GBps": ceiling},
+            "cpu_baseline": None}
 
 
 def reductions(shape, seed: int, steps: int, warmup: int) -> list[dict]:
@@ -627,8 +650,9 @@ def traffic_probe() -> None:
     kernel launched eagerly so every dispatch is one workload's: three plain
     contiguous copies of 1 GiB through ``tc_strided_copy`` (the rows kernel;
     1 GiB read and 1 GiB written each, the counters' calibration), three
-    launches of the headline product, then one call of every bandwidth
-    workload in the order ``TRAFFIC_PROBE`` lists them."""
+    launches of the headline product, three of the f16 16384 x 1024 x 4096
+    product, then one call of every bandwidth workload in the order
+    ``traffic_workloads`` lists them."""
     n = 1 << 28
     src, dst = lib.Buffer(4 * n), lib.Buffer(4 * n)
     lib.call("tc_fill", src.ptr, n, 4, ctypes.byref(ctypes.c_float(1.0)))
@@ -646,6 +670,16 @@ def traffic_probe() -> None:
     c = lib.Buffer(m * n * 2)
     for _ in range(3):
         lib.call("tc_matmul", lib.BF16, lib.BF16, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
+    lib.sync()
+    for buffer in (a, b, c):
+        buffer.free()
+    # The f16 skinny product of the sweep, as its workload line runs it.
+    m, k, n = 16384, 1024, 4096
+    a = lib.Buffer.of(host_matrix("f16", m, k, rng, 1 / np.sqrt(k)))
+    b = lib.Buffer.of(host_matrix("f16", k, n, rng, 1 / np.sqrt(k)))
+    c = lib.Buffer(m * n * 2)
+    for _ in range(3):
+        lib.call("tc_matmul", lib.F16, lib.F16, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
     lib.sync()
     for buffer in (a, b, c):
         buffer.free()
@@ -755,6 +789,7 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
         workloads.append(gemm("f16", 16384, 1024, 4096, 3, 1 / np.sqrt(1024), steps, warmup, cpu=True))
     if "reductions" in groups:
         log("reductions ...")
+        workloads.append(launch_floor(steps, warmup))
         workloads += reductions((64, 128, 1024), 1, steps, warmup)
         workloads += reductions((1024, 128, 1024), 1, max(steps // 2, 5), warmup)
     if "copies" in groups:
@@ -779,7 +814,8 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
         workloads += dense_layer("f32", 4096, 1024, 4096, steps, warmup)
         workloads += dense_layer("bf16", 8192, 8192, 8192, steps, warmup)
     for line in workloads:
-        log(f"  {line['workload']}: {line['value']:.1f} {line['unit']} ({line['roofline']['frac'] * 100:.1f}%)")
+        frac = line["roofline"]["frac"]
+        log(f"  {line['workload']}: {line['value']:.1f} {line['unit']}" + (f" ({frac * 100:.1f}%)" if frac else ""))
     return workloads
 
 
