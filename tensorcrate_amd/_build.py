@@ -91,13 +91,17 @@ def build_library(jobs: int | None = None) -> Path:
     (with hiprtc, which compiles fused programs at run time)."""
     sources = sorted(CSRC.glob("*.hip"))
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
+    # The ROCm whose code-object compiler the runtime compiler should find
+    # loaded: the one hipcc belongs to (csrc/fused.hip, runtime_compiler_is_ours).
+    rocm_lib = Path(hipcc()).resolve().parent.parent / "lib"
+    flags = HIP_FLAGS + [f'-DTC_ROCM_LIB="{rocm_lib}"']
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
-        objects = list(pool.map(lambda s: _compile(s, HIP_FLAGS), sources))
+        objects = list(pool.map(lambda s: _compile(s, flags), sources))
     embedded = OBJECTS / "embedded_sources.o"
     _run(["g++", "-O2", "-fPIC", "-c", str(_embedded_sources()), "-o", str(embedded)])
     staged = LIBRARY.with_suffix(".so.tmp")
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), str(embedded), "-lhiprtc",
-          "-o", str(staged)])
+          "-ldl", "-o", str(staged)])
     os.replace(staged, LIBRARY)
     return LIBRARY
 

@@ -93,6 +93,9 @@ int vector_product(uint32_t dtype, bool row_vector, bool accumulate, uint64_t ro
 std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                            const tc_place* places, std::vector<float>* constants);
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out);
+// Whether hiprtc in this process compiles with the code-object compiler of
+// the ROCm the library was built against (fused.hip).
+bool runtime_compiler_is_ours();
 
 // `fused_sum` over rows as one compiled kernel (fused.hip): the checked
 // program's one output summed per row into `out`, rounded once to `dtype`.

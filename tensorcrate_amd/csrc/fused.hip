@@ -19,8 +19,11 @@
 // result — and every store converts from T to the output's element type.
 // Multiply and add are never fused.
 
+#include <dlfcn.h>
 #include <hip/hiprtc.h>
+#include <limits.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -684,6 +687,31 @@ std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtyp
 
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out) {
     return cached_kernels(source, kernels, out);
+}
+
+// hiprtc hands the compile to the code-object compiler library (comgr) that
+// the process has loaded under its soname.  A PyTorch build bundles an older
+// one under the same soname, and in a process that imported it first hiprtc
+// compiles with that: it handles the one-tile product kernels with a program
+// epilogue but crashes on the persistent one (ROCm 7.0's, measured).  So that
+// kernel is compiled only when comgr is not loaded yet (the system's will be)
+// or the loaded one is the file of the ROCm this library was built with.
+bool runtime_compiler_is_ours() {
+    static const bool ours = [] {
+        void* handle = dlopen("libamd_comgr.so.3", RTLD_NOW | RTLD_NOLOAD);
+        if (handle == nullptr) return true;
+        bool same = false;
+        void* symbol = dlsym(handle, "amd_comgr_get_version");
+        Dl_info info{};
+        if (symbol != nullptr && dladdr(symbol, &info) != 0 && info.dli_fname != nullptr) {
+            char loaded[PATH_MAX], built[PATH_MAX];
+            same = realpath(info.dli_fname, loaded) != nullptr &&
+                   realpath(TC_ROCM_LIB "/libamd_comgr.so.3", built) != nullptr && strcmp(loaded, built) == 0;
+        }
+        dlclose(handle);
+        return same;
+    }();
+    return ours;
 }
 
 int fused_row_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,

@@ -298,7 +298,8 @@ void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32
         if constexpr (!EPI::kProgram) {
             // k >= 8 here, so an even step count is at least two.
             if (((k + 63) / 64) % 2 == 0) {
-                gemm16x16_persistent_kernel<S, O, A_KC, B_KC><<<cus, 512, 0, s>>>(a, b, c, m, n, k, accumulate);
+                gemm16x16_persistent_kernel<S, O, A_KC, B_KC><<<cus, 512, 0, s>>>(a, b, c, m, n, k, accumulate,
+                                                                                PlainStore{});
                 return;
             }
         }
@@ -548,12 +549,15 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
         const std::string type = dtype == TC_F16 ? "_Float16" : "tc::bf16_t";
         kernels = {"tc::gemm16x16_kernel<" + type + ", " + type + ", true, false, CompiledStore>",
                    "tc::direct16_kernel<" + type + ", " + type + ", true, false, 128, 128, 2, 2, 64, 2, CompiledStore>"};
+        if (runtime_compiler_is_ours()) {
+            kernels.push_back("tc::gemm16x16_persistent_kernel<" + type + ", " + type + ", true, false, CompiledStore>");
+        }
         large = ((m + 255) / 256) * ((n + 255) / 256);
         large_threads = 512;
         small_threads = 2 * 2 * 64;
     }
     small = ((m + 127) / 128) * ((n + 127) / 128);
-    hipFunction_t functions[2] = {};
+    hipFunction_t functions[3] = {};
     if (!compiled_kernels(source, kernels, functions)) return false;
     CompiledArgsOf args{};
     for (uint32_t slot = 1; slot < input_count; slot++) args.in[slot] = inputs[slot];
@@ -563,11 +567,16 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     void* none = nullptr;
     bool accumulate = false;
     void* params[] = {const_cast<void**>(&a), const_cast<void**>(&b), &none, &m, &n, &k, &accumulate, &args};
-    const bool use_large = large >= static_cast<uint32_t>(compute_units());
+    const uint32_t cus = static_cast<uint32_t>(compute_units());
+    const bool use_large = large >= cus;
+    // 16-bit products with whole pairs of steps take the persistent kernel,
+    // as plain ones do (launch_tiled16).
+    const bool persistent = kernels.size() == 3 && use_large && ((k + 63) / 64) % 2 == 0;
+    hipFunction_t function = persistent ? functions[2] : use_large ? functions[0] : functions[1];
+    const uint32_t grid = persistent ? cus : use_large ? large : small;
     count_dispatch();
-    const hipError_t error = hipModuleLaunchKernel(use_large ? functions[0] : functions[1], use_large ? large : small,
-                                                   1, 1, use_large ? large_threads : small_threads, 1, 1, 0, s, params,
-                                                   nullptr);
+    const hipError_t error = hipModuleLaunchKernel(function, grid, 1, 1, use_large ? large_threads : small_threads, 1,
+                                                   1, 0, s, params, nullptr);
     *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused matmul: ") + hipGetErrorString(error));
     return true;
 }

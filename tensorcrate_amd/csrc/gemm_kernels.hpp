@@ -1099,12 +1099,16 @@ __global__ void __launch_bounds__(512) gemm16x16_kernel(const S* __restrict__ A,
 //    first staging write.  Within a wave, LDS accesses complete in order.
 //  - Edge tiles, f32 C and accumulation store from the accumulators, as the
 //    one-tile kernel does.
-// Plain stores only: a program epilogue needs LDS that the next tile's
-// first steps already occupy.
-template <typename S, typename O, bool A_KC, bool B_KC>
+//  - A program epilogue runs wave by wave over the same 4 KiB: a wave
+//    stages one 16-row block of its f32 results at a time (16-byte chunk c
+//    of row r at c ^ r, conflict-free both ways) and hands the program
+//    EPI::kElems elements a lane, 64 lanes on 64 neighbouring columns, so
+//    its loads and stores are row runs.  No block barrier is needed: each
+//    wave reads back only what it wrote.
+template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 __global__ void __launch_bounds__(512) gemm16x16_persistent_kernel(const S* __restrict__ A, const S* __restrict__ B,
                                                                     O* __restrict__ C, uint32_t M, uint32_t N,
-                                                                    uint32_t K, bool accumulate) {
+                                                                    uint32_t K, bool accumulate, EPI epi) {
     constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
     constexpr int kA = BM * BK, kB = BN * BK;
@@ -1230,7 +1234,33 @@ __global__ void __launch_bounds__(512) gemm16x16_persistent_kernel(const S* __re
         }
         // lane holds C[row][col .. col + 3] for row = m0 + wm*128 + 16 i + lane % 16,
         // col = n0 + wn*64 + 16 j + 4 (lane / 16).
-        if (rows_ok && m0 + BM <= M && n0 + BN <= N) {
+        if constexpr (EPI::kProgram) {
+            constexpr int E = EPI::kElems;
+            static_assert(16 % E == 0, "whole groups of a staged block's 16 rows");
+            float* staged = reinterpret_cast<float*>(rows_lds + wave * kRegion);
+            const int r = lane % 16, g = lane / 16;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    *reinterpret_cast<f32x4*>(staged + r * 64 + (((4 * j + g) ^ r) * 4)) = acc[i][j];
+#pragma unroll
+                for (int v0 = 0; v0 < 16; v0 += E) {
+                    bool live[E];
+                    uint32_t row[E], col[E];
+                    float product[E];
+#pragma unroll
+                    for (int e = 0; e < E; e++) {
+                        const int v = v0 + e;
+                        product[e] = staged[v * 64 + (((lane / 4) ^ v) * 4) + lane % 4];
+                        row[e] = m0 + wm * (BM / WM) + 16 * i + v;
+                        col[e] = n0 + wn * (BN / WN) + lane;
+                        live[e] = row[e] < M && col[e] < N;
+                    }
+                    epi.group(live, row, col, N, product);
+                }
+            }
+        } else if (rows_ok && m0 + BM <= M && n0 + BN <= N) {
           if constexpr (sizeof(O) == 2) {
             const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
                 C + static_cast<uint64_t>(m0 + wm * (BM / WM)) * N + n0 + wn * (BN / WN), 0, 0x7fffffff,

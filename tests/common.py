@@ -8,6 +8,23 @@ import numpy as np
 from oracle import binding as oracle
 from tensorcrate_amd import lib
 
+class _Torch:
+    """torch, imported on first use.  Only CPU tests use it (as an independent
+    reference for rounding); importing it at collection would put its bundled
+    ROCm runtime and code-object compiler into every test process, GPU ones
+    included, where they share their sonames with the system ROCm the
+    library is built against and whichever loads first is the one used."""
+
+    def __getattr__(self, name):
+        if name.startswith("__"):  # collection probes objects for dunders
+            raise AttributeError(name)
+        import torch as module
+
+        return getattr(module, name)
+
+
+torch = _Torch()
+
 KINDS = [lib.F32, lib.F16, lib.BF16]
 KIND_NAMES = {lib.F32: "f32", lib.F16: "f16", lib.BF16: "bf16"}
 

@@ -112,22 +112,29 @@ def test_the_product_must_be_read_in_order():
 
 
 @pytest.mark.parametrize("kind", [lib.F32, lib.BF16, lib.F16])
-@pytest.mark.parametrize("m,k,n", [(520, 136, 1032), (4100, 136, 4104)], ids=["small-tiles", "large-tiles"])
+@pytest.mark.parametrize("m,k,n", [(520, 136, 1032), (4100, 136, 4104), (4100, 200, 4104)],
+                         ids=["small-tiles", "large-tiles", "persistent"])
 def test_a_repeated_program_runs_compiled_with_the_same_bits(kind, m, k, n):
     # The first appearance of a program runs the interpreter epilogue; from
     # the second the program is compiled into the product kernel (as the
-    # reference's Metal backend specializes a program seen before).  Both
-    # give the unfused bits, in the kernel for fewer 256 x 256 tiles than
-    # CUs and in the one for more (17 x 17 tiles, ragged).  Compiled
-    # kernels are cached by source, constants being arguments, so each case
-    # has a program of its own shape: the bias added for the small tiles,
-    # subtracted for the large.
+    # reference's Metal backend specializes a program seen before).  All
+    # give the unfused bits: in the kernel for fewer 256 x 256 tiles than
+    # CUs, in the one-tile kernel for more (17 x 17 tiles, ragged, three
+    # steps), and, for 16-bit types with a whole pair of steps, in the
+    # persistent kernel.  Compiled kernels are cached by source, constants
+    # being arguments, so each case has a program of its own shape: the bias
+    # added for the small tiles, subtracted for the large ones, and the
+    # scaled product's maximum with the bias for the persistent ones.
     code = Code()
     p = code.load(0, 0, kind)
     b = code.load(1, 1, kind)
-    shifted = code.binary(lib.SUB if m > 1000 else lib.ADD, p, b)
-    scaled = code.binary(lib.MUL, shifted, code.const(0.375 + kind))
-    code.store(code.compare(lib.MAX, scaled, code.const(-0.25)), kind, 0)
+    if k == 200:
+        scaled = code.binary(lib.MUL, p, code.const(0.375 + kind))
+        code.store(code.compare(lib.MAX, scaled, b), kind, 0)
+    else:
+        shifted = code.binary(lib.SUB if m > 1000 else lib.ADD, p, b)
+        scaled = code.binary(lib.MUL, shifted, code.const(0.375 + kind))
+        code.store(code.compare(lib.MAX, scaled, code.const(-0.25)), kind, 0)
     rng = np.random.default_rng(kind)
     a = to_kind(rng.uniform(-1, 1, (m, k)).astype(np.float32), kind)
     w = to_kind(rng.uniform(-1, 1, (k, n)).astype(np.float32), kind)

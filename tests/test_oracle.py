@@ -10,11 +10,10 @@ import itertools
 
 import numpy as np
 import pytest
-import torch
 
 from oracle import binding as oracle
 from tensorcrate_amd import lib
-from tests.common import Lcg, filler, same, to_kind, widen
+from tests.common import Lcg, filler, same, to_kind, torch, widen
 
 
 def walk(shape, offset, strides):

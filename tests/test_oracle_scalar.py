@@ -17,11 +17,10 @@ propagates a NaN bound fails one of them.
 
 import numpy as np
 import pytest
-import torch
 
 from oracle import binding as oracle
 from tensorcrate_amd import lib
-from tests.common import KINDS, KIND_NAMES, same, to_kind, widen
+from tests.common import KINDS, KIND_NAMES, same, to_kind, torch, widen
 
 ARITHMETIC_OPS = [lib.ADD, lib.SUB, lib.MUL, lib.DIV, lib.REM]
 COMPARE_OPS = [lib.MIN, lib.MAX, lib.MAX_SHARE, lib.LESS, lib.LESS_EQUAL, lib.GREATER, lib.GREATER_EQUAL]
