@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(256) tile_kernel(const T* __restrict__ src, T*
 // exchange would, and no padding: the 16-byte chunks of tile row r sit at
 // chunk ^ ((r / 4) % 16), which puts the 16 rows a quarter-wave reads on
 // distinct bank groups in the second phase and permutes a row's chunks in
-// the first.  Needs every extent, offset and stride that steps along a
+// the first (the period is the smaller of a row's chunks and TB / 4).  Needs every extent, offset and stride that steps along a
 // vector to be a multiple of 4, which the host checks; NT marks a transpose
 // that streams past the Infinity Cache.
 template <typename I, bool NT, int TA, int TB>
@@ -219,9 +219,11 @@ __global__ void __launch_bounds__(256) tile4_kernel(const uint32_t* __restrict__
     constexpr int kReadQuads = TA / 4, kReadRows = 256 / kReadQuads;  // first phase: lanes along `a`
     constexpr int kBlocksB = TB / 4;                                   // second phase: 4 x 4 blocks along `b`
     constexpr int kBlockRows = 256 / kBlocksB;                         // ... and along `a`, per pass
-    static_assert(TA / 4 >= TB / 4 && (TB & (TB - 1)) == 0, "the swizzle stays within a row");
+    // The swizzle's period: at most a row's chunks, so it stays within a row.
+    constexpr int kSwizzle = TA / 4 < TB / 4 ? TA / 4 : TB / 4;
+    static_assert((kSwizzle & (kSwizzle - 1)) == 0, "the swizzle stays within a row");
     __shared__ __attribute__((aligned(16))) uint32_t tile[TB][TA];
-    auto chunk_at = [](int r, int chunk) { return (chunk ^ ((r / 4) % (TB / 4))) * 4; };
+    auto chunk_at = [](int r, int chunk) { return (chunk ^ ((r / 4) % kSwizzle)) * 4; };
     // Where tile `block` starts in the source (`from`, plus a0 along `a` and
     // b0 along `b`) and in the target (`to`).
     struct Place {
@@ -401,12 +403,17 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
         };
         // Four-byte elements whose rows start on 16-byte boundaries move 16
         // bytes a lane; a block walks several tiles, at most eight blocks a
-        // CU.
-        // 128 x 64 tiles: 512-byte reads and 256-byte writes per row, the
-        // best of the shapes measured on the config-3 permute, an 8192^2
-        // transpose and a [64, 1024, 1024] batch (128 x 128 measured the
-        // same: 70% of HBM on the permute, 64% on a 4096^2 transpose).
-        constexpr int TA = 128, TB = 64;
+        // CU.  64 x 128 tiles (256-byte reads and 512-byte writes per row):
+        // measured on MI355X over ten shapes from 2048^2 to [1024, 256, 256],
+        // streaming, with inputs and outputs both cold, they averaged 5.55
+        // TB/s against 5.46 for 128 x 64 and 5.49 for 256 x 32 (the config-3
+        // permute 5.89 against 5.69).  Streaming beat plain accesses on every
+        // shape there, but writing into a target that is still in the
+        // Infinity Cache it loses (a 4096^2 transpose into one reused target:
+        // 4.86 against 5.18 TB/s), so, as for every copy, only traffic past
+        // that cache streams.
+        constexpr int TA = 64, TB = 128;
+        const bool stream_tiles = stream;
         uint64_t blocks = tiled(TA, TB);
         bool wide = sizeof(T) == 4 && blocks <= UINT32_MAX && walk.shape[axis_a] % 4 == 0 &&
                     walk.shape[axis_b] % 4 == 0 && walk.strides[0][axis_b] % 4 == 0 &&
@@ -416,7 +423,7 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
             const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
             uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
             const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>(blocks, 8 * compute_units()));
-            if (stream) {
+            if (stream_tiles) {
                 tile4_kernel<I, true, TA, TB><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
             } else {
                 tile4_kernel<I, false, TA, TB><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
