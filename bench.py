@@ -651,7 +651,8 @@ def traffic_probe() -> None:
     contiguous copies of 1 GiB through ``tc_strided_copy`` (the rows kernel;
     1 GiB read and 1 GiB written each, the counters' calibration), three
     launches of the headline product, three of the f16 16384 x 1024 x 4096
-    product, then one call of every bandwidth workload in the order
+    product, three each of the f32 4096^3 product in its PLAIN, LEFT and
+    RIGHT forms, then one call of every bandwidth workload in the order
     ``traffic_workloads`` lists them."""
     n = 1 << 28
     src, dst = lib.Buffer(4 * n), lib.Buffer(4 * n)
@@ -680,6 +681,18 @@ def traffic_probe() -> None:
     c = lib.Buffer(m * n * 2)
     for _ in range(3):
         lib.call("tc_matmul", lib.F16, lib.F16, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
+    lib.sync()
+    for buffer in (a, b, c):
+        buffer.free()
+    # The f32 4096^3 product in each form the MLP step's products take:
+    # PLAIN (A.B), LEFT (A^T.B, the weight gradients), RIGHT (A.B^T).
+    m = k = n = 4096
+    a = lib.Buffer.of(host_matrix("f32", m, k, rng, None))
+    b = lib.Buffer.of(host_matrix("f32", k, n, rng, None))
+    c = lib.Buffer(m * n * 4)
+    for form in (lib.PLAIN, lib.LEFT, lib.RIGHT):
+        for _ in range(3):
+            lib.call("tc_matmul", lib.F32, lib.F32, form, 0, m, k, n, a.ptr, b.ptr, c.ptr)
     lib.sync()
     for buffer in (a, b, c):
         buffer.free()

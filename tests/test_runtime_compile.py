@@ -30,7 +30,7 @@ KERNELS = [
     "tc::gemm16x16_persistent_kernel<tc::bf16_t, tc::bf16_t, true, false>",
     "tc::gemm16x16_persistent_kernel<_Float16, float, false, false>",
     "tc::direct16_kernel<tc::bf16_t, tc::bf16_t, true, false, 128, 128, 2, 2, 64, 2, tc::PlainStore>",
-    "tc::inplace32_kernel<float, true, false, 256, 128, tc::PlainStore>",
+    "tc::inplace32_kernel<float, true, false, 128, 128, tc::PlainStore>",
     "tc::gemm16x16_persistent_kernel<tc::bf16_t, tc::bf16_t, true, false, RowStore>",
     "tc::gemm16x16_kernel<_Float16, _Float16, true, false, RowStore>",
 ]
