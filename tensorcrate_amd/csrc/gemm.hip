@@ -280,21 +280,49 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
     }
 }
 
+// The four-wave kernel's instances, named here: launched from a template
+// alone, the host compiler emitted no launch stub for it (its step order is
+// built from nested generic lambdas) and the library failed to load.
+}  // namespace
+template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, true, true>(const bf16_t*, const bf16_t*, bf16_t*,
+                                                                           uint32_t, uint32_t, uint32_t);
+template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, true, false>(const bf16_t*, const bf16_t*, bf16_t*,
+                                                                            uint32_t, uint32_t, uint32_t);
+template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, false, false>(const bf16_t*, const bf16_t*, bf16_t*,
+                                                                             uint32_t, uint32_t, uint32_t);
+template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, true, true>(const _Float16*, const _Float16*,
+                                                                               _Float16*, uint32_t, uint32_t, uint32_t);
+template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, true, false>(const _Float16*, const _Float16*,
+                                                                                _Float16*, uint32_t, uint32_t, uint32_t);
+template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, false, false>(const _Float16*, const _Float16*,
+                                                                                 _Float16*, uint32_t, uint32_t,
+                                                                                 uint32_t);
+namespace {
+
 // The tiled kernels' shapes: a 256 x 256 tile over eight waves of 128 x 64
 // (two waves per SIMD, so one's waits overlap the other's matrix-core
 // steps), and a 128 x 128 tile over four waves of 64 x 64 for products too
 // small to give every CU a tile.  Products of at least a tile a CU run the
-// 16 x 16 x 32 kernels: the persistent one for plain stores and whole pairs
-// of steps (on MI355X, bf16 8192^3: 1443 against 1395 TFLOP/s a tile a
-// block; f16 16384 x 4096 x 1024: 1203 against 1065 for the persistent 32 x
-// 32 x 16 kernel it replaced), the one-tile kernel for program epilogues
-// and odd step counts.
+// 16 x 16 x 32 kernels: the four-wave one for a 16-bit C written whole over
+// whole pairs of steps, the eight-wave persistent one for other plain stores
+// and whole pairs of steps (on MI355X, bf16 8192^3: 1443 against 1395
+// TFLOP/s a tile a block; f16 16384 x 4096 x 1024: 1203 against 1065 for
+// the persistent 32 x 32 x 16 kernel it replaced), the one-tile kernel for
+// program epilogues and odd step counts.
 template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
                     hipStream_t s, const EPI& epi = EPI{}) {
     const uint32_t large = ((m + 255) / 256) * ((n + 255) / 256);
     const uint32_t cus = static_cast<uint32_t>(compute_units());
     if (large >= cus) {
+        if constexpr (!EPI::kProgram && sizeof(O) == 2) {
+            // A 16-bit C written whole, by rows of 16-byte pieces, over whole
+            // step pairs: the four-wave kernel.
+            if (!accumulate && n % 8 == 0 && reinterpret_cast<uintptr_t>(c) % 16 == 0 && k % 128 == 0) {
+                gemm16x16_wide_kernel<S, O, A_KC, B_KC><<<cus, 256, 0, s>>>(a, b, c, m, n, k);
+                return;
+            }
+        }
         if constexpr (!EPI::kProgram) {
             // k >= 8 here, so an even step count is at least two.
             if (((k + 63) / 64) % 2 == 0) {

@@ -785,31 +785,39 @@ __device__ __forceinline__ void bare_barrier() {
 // four chunk bits.
 __device__ __forceinline__ int rc16_swizzle(int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); }
 
-// Direct-load staging of one operand's stage tile with a single per-lane
-// offset: the swizzle of a lane's chunk repeats every instruction, so
-// instruction i only adds a uniform stride (kept in a scalar register).
+// Direct-load staging of one operand's stage tile with per-lane offsets that
+// repeat: the swizzle of a lane's chunk has a period of 16 rows, so when a
+// wave's consecutive instructions are 16 rows apart (or a multiple) one
+// offset serves them all, and when they are 8 rows apart (four waves over a
+// row-contiguous tile) two alternate.  Instruction i adds a uniform stride
+// (kept in a scalar register) to offset i % kPeriod.
 template <typename S, int ROWS, bool KC, int WAVES, int BK>
 struct StrideStager {
     static constexpr int kInstr = ROWS * BK * 2 / 1024;  // one wave instruction moves 1 KiB
     static constexpr int kPer = kInstr / WAVES;
     static constexpr int kRowsPer = KC ? 1024 / (BK * 2) : 1024 / (ROWS * 2);
     static constexpr int kChunksPerRow = KC ? BK / 8 : ROWS / 8;
+    static constexpr int kApart = kRowsPer * WAVES;  // rows from one of a wave's instructions to the next
+    static constexpr int kPeriod = kApart % 16 == 0 ? 1 : 16 / kApart;
     static_assert(kInstr % WAVES == 0, "whole instructions per wave");
-    static_assert((kRowsPer * WAVES) % 16 == 0, "each instruction's rows repeat the swizzle (period 16 rows)");
+    static_assert((kApart * kPeriod) % 16 == 0 && kPer % kPeriod == 0, "whole swizzle periods per wave");
     __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t offset;  // this lane's chunk of instruction 0, bytes at k0 = 0
-    uint32_t k_of;    // its k within a step (K-contiguous only)
-    uint32_t stride;  // bytes from one instruction's rows to the next's
+    uint32_t offset[kPeriod];  // this lane's chunk of instructions 0 .. kPeriod - 1, bytes at k0 = 0
+    uint32_t k_of[kPeriod];    // its k within a step (K-contiguous only)
+    uint32_t stride;           // bytes from one period's rows to the next's
     uint32_t k_bytes;
     int wave;
 
     __device__ void init(const S* p, uint32_t first, uint32_t rows, uint32_t ld, uint32_t depth, int w, int lane) {
         wave = w;
-        const int row = kRowsPer * w + lane / kChunksPerRow;
-        const int chunk = (lane % kChunksPerRow) ^ (KC ? kc_swizzle<BK>(row) : rc16_swizzle(row));
-        offset = (static_cast<uint32_t>(row) * ld + chunk * 8) * sizeof(S);
-        k_of = KC ? chunk * 8 : 0;
-        stride = kRowsPer * WAVES * ld * sizeof(S);
+#pragma unroll
+        for (int q = 0; q < kPeriod; q++) {
+            const int row = kRowsPer * w + kApart * q + lane / kChunksPerRow;
+            const int chunk = (lane % kChunksPerRow) ^ (KC ? kc_swizzle<BK>(row) : rc16_swizzle(row));
+            offset[q] = (static_cast<uint32_t>(row) * ld + chunk * 8) * sizeof(S);
+            k_of[q] = KC ? chunk * 8 : 0;
+        }
+        stride = kApart * kPeriod * ld * sizeof(S);
         k_bytes = KC ? sizeof(S) : ld * sizeof(S);
         retarget(p, first, rows, ld, depth);
     }
@@ -827,16 +835,25 @@ struct StrideStager {
     // next row's, so it is pointed past the resource (operands are under
     // 2^31 bytes) and loads zeros.
     __device__ __forceinline__ void fetch(S* tile, uint32_t k0, uint32_t K, bool full) const {
-        const uint32_t at = (full || !KC || k0 + k_of < K) ? offset : 0x80000000u;
 #pragma unroll
         for (int i = 0; i < kPer; i++) {
+            const int q = i % kPeriod;
+            const uint32_t at = (full || !KC || k0 + k_of[q] < K) ? offset[q] : 0x80000000u;
             uint8_t* dst = reinterpret_cast<uint8_t*>(tile) + 1024 * (wave + WAVES * i);
             // The scalar offset is uniform; said so, the compiler keeps it in
             // a scalar register rather than looping over lanes.
-            const uint32_t soffset = __builtin_amdgcn_readfirstlane(k0 * k_bytes + i * stride);
+            const uint32_t soffset = __builtin_amdgcn_readfirstlane(k0 * k_bytes + (i / kPeriod) * stride);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, at,
                                                      soffset, 0, 0);
         }
+    }
+    // Instruction i of this wave's share of a whole step (no K tail).
+    __device__ __forceinline__ void fetch_one(S* tile, uint32_t k0, int i) const {
+        const int q = i % kPeriod;
+        uint8_t* dst = reinterpret_cast<uint8_t*>(tile) + 1024 * (wave + WAVES * i);
+        const uint32_t soffset = __builtin_amdgcn_readfirstlane(k0 * k_bytes + (i / kPeriod) * stride);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)dst, 16, offset[q],
+                                                 soffset, 0, 0);
     }
 };
 
@@ -1318,6 +1335,275 @@ __global__ void __launch_bounds__(512) gemm16x16_persistent_kernel(const S* __re
                             if (col + e < N) store_out(at, e, acc[i][j][e], accumulate);
                     }
                 }
+            }
+        }
+        tile += gridDim.x;
+        if (tile >= tiles) break;
+        tile_of(tile, tiles_m, tiles_n, tm, tn);
+        m0 = tm * BM;
+        n0 = tn * BN;
+    }
+    // No direct load may still be writing LDS when the block ends.
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));
+}
+
+// ---- the wide-wave product kernel ------------------------------------------------------
+//
+// The same 256 x 256 tiles, 64-deep steps and persistent tile walk as above,
+// over four waves of 128 x 128 (one wave a SIMD) instead of eight of 128 x 64.
+// A wave reads 16 KiB of operand fragments from LDS per 64 matrix-core steps
+// rather than 24 KiB, and the whole loop is ordered by hand:
+//  - The 256 accumulators of a 128 x 128 wave tile fill the AGPRs.  The
+//    compiler's own allocation of that many MFMA accumulators copies them
+//    between register files and spills; each matrix-core step is therefore
+//    written as one in-place instruction on an AGPR operand, which pins them.
+//    The compiler cannot see these instructions' hazards, so the code around
+//    them supplies its own: fragments are read by LDS loads straight into
+//    the operand registers (a load's wait count covers it), zeroed
+//    accumulators stand five wait states before the first step reads them,
+//    and 42 wait states separate the last step from the reads of its results.
+//  - Every operand fragment is double-buffered: a step's 32-deep slice runs
+//    from one slot while the next slice's fragments load into the other.
+//  - Memory operations sit one at a time between matrix-core steps: with one
+//    wave a SIMD, a burst of them would leave the matrix core idle.  Slice 0
+//    reads slice 1's fragments after its odd steps 1-31; one block barrier
+//    follows (the next step has landed, this one is in registers); slice 1
+//    issues the 16 direct loads of the step after next after every fourth
+//    step and reads the next step's first fragments after odd steps 3-33.
+// Measured on MI355X against the eight-wave persistent kernel (stand-alone
+// harness, same bits): bf16 8192^3 1518-1523 against 1411-1437 TFLOP/s,
+// the matrix cores 82% busy at 1.81 GHz against 71-72% at 1.92; f16 16384 x
+// 1024 x 4096 within 1%.  Spreading the memory operations mattered: placed
+// in bursts after each group of eight steps the kernel ran no faster than
+// the eight-wave one, and with the loads all in the first half of the slice
+// 3% slower than evenly spread.
+//
+// For 16-bit C written whole (no accumulate, no program), N a multiple of 8,
+// C 16-byte aligned and K a multiple of 128: each tile leaves through the
+// staged whole-row stores, a lane's 16-byte piece stored only where it lies
+// inside C, so edge tiles need no other path.
+template <typename S>
+struct InPlaceMfma;
+template <>
+struct InPlaceMfma<bf16_t> {
+    __device__ static __forceinline__ void step(f32x4& c, const uint4& a, const uint4& b) {
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                     : "+a"(c)
+                     : "v"(__builtin_bit_cast(u32x4, a)), "v"(__builtin_bit_cast(u32x4, b)));
+    }
+};
+template <>
+struct InPlaceMfma<_Float16> {
+    __device__ static __forceinline__ void step(f32x4& c, const uint4& a, const uint4& b) {
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
+                     : "+a"(c)
+                     : "v"(__builtin_bit_cast(u32x4, a)), "v"(__builtin_bit_cast(u32x4, b)));
+    }
+};
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// What follows matrix-core step t (0-63) of a slice: fragment read r (even r
+// an A fragment, odd a B fragment, of block r / 2), direct load 100 + i, or
+// nothing.
+template <int SLICE>
+__device__ constexpr int wide_op_at(int t) {
+    if (SLICE == 0) return t % 2 == 1 && t < 32 ? t / 2 : -1;
+    if (t % 4 == 0) return 100 + t / 4;
+    return t % 2 == 1 && t >= 3 && t <= 33 ? (t - 3) / 2 : -1;
+}
+
+template <typename S, typename O, bool A_KC, bool B_KC>
+__global__ void __launch_bounds__(256) gemm16x16_wide_kernel(const S* __restrict__ A, const S* __restrict__ B,
+                                                             O* __restrict__ C, uint32_t M, uint32_t N,
+                                                             uint32_t K) {
+    static_assert(sizeof(O) == 2, "16-bit C");
+    constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 2, kWaves = WM * WN;
+    constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+    constexpr int kA = BM * BK, kB = BN * BK;
+    using StagerA = StrideStager<S, BM, A_KC, kWaves, BK>;
+    using StagerB = StrideStager<S, BN, B_KC, kWaves, BK>;
+    static_assert(StagerA::kPer == 8 && StagerB::kPer == 8, "sixteen direct loads a step");
+    static_assert(TM == 8 && TN == 8, "sixteen fragments a slice");
+    constexpr int kRegion = 4096;  // staging bytes a wave
+
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    const uint32_t tiles = tiles_m * tiles_n;
+    uint32_t tile = blockIdx.x;
+    if (tile >= tiles) return;
+    uint32_t tm, tn;
+    tile_of(tile, tiles_m, tiles_n, tm, tn);
+    uint32_t m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int wm = wave / WN, wn = wave % WN;
+
+    StagerA sa;
+    StagerB sb;
+    sa.init(A, m0, M, A_KC ? K : M, K, wave, lane);
+    sb.init(B, n0, N, B_KC ? K : N, K, wave, lane);
+
+    uint32_t a_off[A_KC ? 2 : TM], b_off[B_KC ? 2 : TN];
+    if constexpr (A_KC) {
+        a_off[0] = kc16_offset(lane, wm * (BM / WM), 0);
+        a_off[1] = kc16_offset(lane, wm * (BM / WM), 1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++) a_off[i] = rc16_offset<BM>(lane, wm * (BM / WM), i);
+    }
+    if constexpr (B_KC) {
+        b_off[0] = kc16_offset(lane, wn * (BN / WN), 0);
+        b_off[1] = kc16_offset(lane, wn * (BN / WN), 1);
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; j++) b_off[j] = rc16_offset<BN>(lane, wn * (BN / WN), j);
+    }
+    auto frag_a = [&](const S* t, int i, int q) __attribute__((always_inline)) {
+        return A_KC ? lds_b128(t, a_off[q] + 2048 * i) : lds_tr_pair<S, BM>(t, a_off[i] + q * 32 * BM * 2);
+    };
+    auto frag_b = [&](const S* t, int j, int q) __attribute__((always_inline)) {
+        return B_KC ? lds_b128(t, b_off[q] + 2048 * j) : lds_tr_pair<S, BN>(t, b_off[j] + q * 32 * BN * 2);
+    };
+
+    f32x4 acc[TM][TN];
+    uint4 fa[2][TM], fb[2][TN];
+    const uint32_t steps = K / BK;
+
+    // One step from stage T: slice 0 from slot 0 (read during the previous
+    // step), slice 1 from slot 1; stage T then takes the step at k_next.
+    auto step = [&](auto t, uint32_t k_next) __attribute__((always_inline)) {
+        constexpr int T = decltype(t)::value;
+        constexpr int U = T ^ 1;
+        const S* ca = stage_tile<S, kA, 2 * T>();
+        const S* cb = stage_tile<S, kB, 2 * T + 1>();
+        static_for<0, TM * TN>([&](auto x) __attribute__((always_inline)) {
+            constexpr int s = decltype(x)::value;
+            InPlaceMfma<S>::step(acc[s / TN][s % TN], fb[0][s % TN], fa[0][s / TN]);
+            constexpr int op = wide_op_at<0>(s);
+            if constexpr (op >= 0) {
+                if constexpr (op % 2 == 0) fa[1][op / 2] = frag_a(ca, op / 2, 1);
+                else fb[1][op / 2] = frag_b(cb, op / 2, 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));  // the next step is in LDS; this one is read
+        bare_barrier();
+        static_for<0, TM * TN>([&](auto x) __attribute__((always_inline)) {
+            constexpr int s = decltype(x)::value;
+            InPlaceMfma<S>::step(acc[s / TN][s % TN], fb[1][s % TN], fa[1][s / TN]);
+            constexpr int op = wide_op_at<1>(s);
+            if constexpr (op >= 100) {
+                if constexpr (op < 108) sa.fetch_one(stage_tile<S, kA, 2 * T>(), k_next, op - 100);
+                else sb.fetch_one(stage_tile<S, kB, 2 * T + 1>(), k_next, op - 108);
+            } else if constexpr (op >= 0) {
+                if constexpr (op % 2 == 0) fa[0][op / 2] = frag_a(stage_tile<S, kA, 2 * U>(), op / 2, 0);
+                else fb[0][op / 2] = frag_b(stage_tile<S, kB, 2 * U + 1>(), op / 2, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    // Staging as in the persistent kernel, per half of a wave's 128 columns.
+    __shared__ __attribute__((aligned(1024))) uint8_t rows_lds[kWaves * kRegion];
+    const uint32_t region = static_cast<uint32_t>(reinterpret_cast<uint64_t>(
+                                (__attribute__((address_space(3))) uint8_t*)(rows_lds))) +
+                            wave * kRegion;
+    const uint32_t read_at = region + (lane / 8) * 128 + (((lane % 8) ^ (lane / 8)) * 16);
+    const uint32_t row_off = ((lane / 8) * N + 8 * (lane % 8)) * sizeof(O);
+
+#pragma unroll
+    for (int i = 0; i < StagerA::kPer; i++) sa.fetch_one(stage_tile<S, kA, 0>(), 0, i);
+#pragma unroll
+    for (int i = 0; i < StagerB::kPer; i++) sb.fetch_one(stage_tile<S, kB, 1>(), 0, i);
+#pragma unroll
+    for (int i = 0; i < StagerA::kPer; i++) sa.fetch_one(stage_tile<S, kA, 2>(), BK, i);
+#pragma unroll
+    for (int i = 0; i < StagerB::kPer; i++) sb.fetch_one(stage_tile<S, kB, 3>(), BK, i);
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(StagerA::kPer + StagerB::kPer));  // the first step is in LDS
+    bare_barrier();
+#pragma unroll
+    for (int i = 0; i < TM; i++) fa[0][i] = frag_a(stage_tile<S, kA, 0>(), i, 0);
+#pragma unroll
+    for (int j = 0; j < TN; j++) fb[0][j] = frag_b(stage_tile<S, kB, 1>(), j, 0);
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = f32x4{};
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 4" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        for (uint32_t s = 0; s < steps; s += 2) {
+            uint32_t k_next = (s + 2) * BK;
+            if (s + 2 == steps) {
+                // After the last tile, its own first steps again: harmless
+                // loads into stages nobody reads.
+                const uint32_t next = tile + gridDim.x < tiles ? tile + gridDim.x : tile;
+                uint32_t nm, nn;
+                tile_of(next, tiles_m, tiles_n, nm, nn);
+                sa.retarget(A, nm * BM, M, A_KC ? K : M, K);
+                sb.retarget(B, nn * BN, N, B_KC ? K : N, K);
+                k_next = 0;
+            }
+            step(std::integral_constant<int, 0>{}, k_next);
+            step(std::integral_constant<int, 1>{}, k_next + BK);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // lane's accumulators of block (i, j): C[row][col .. col + 3] for row =
+        // m0 + wm*128 + 16 i + lane % 16, col = n0 + wn*128 + 16 j + 4 (lane / 16).
+        const bool whole = m0 + BM <= M && n0 + BN <= N;
+        const int g = lane / 16;
+#pragma unroll
+        for (int h = 0; h < TN / 4; h++) {
+            const uint32_t row0 = m0 + wm * (BM / WM), col0 = n0 + wn * (BN / WN) + 64 * h;
+            const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+                C + static_cast<uint64_t>(row0) * N + col0, 0, 0x7fffffff, kBufferFlags);
+            const bool col_ok = col0 + 8 * (lane % 8) < N;
+#pragma unroll
+            for (int p = 0; p < TM / 2; p++) {
+#pragma unroll
+                for (int ii = 0; ii < 2; ii++) {
+                    const int r = ii * 16 + lane % 16;
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        const f32x4 v = acc[2 * p + ii][4 * h + jj];
+                        const u32x2 out = {pack_pair<O>(v[0], v[1]), pack_pair<O>(v[2], v[3])};
+                        const uint32_t at = region + r * 128 + (((2 * jj + g / 2) ^ (r % 8)) * 16) + (g % 2) * 8;
+                        asm volatile("ds_write_b64 %0, %1" ::"v"(at), "v"(out) : "memory");
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                u32x4 v0, v1, v2, v3;
+                asm volatile(
+                    "ds_read_b128 %0, %4\n\t"
+                    "ds_read_b128 %1, %4 offset:1024\n\t"
+                    "ds_read_b128 %2, %4 offset:2048\n\t"
+                    "ds_read_b128 %3, %4 offset:3072\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+                    : "v"(read_at)
+                    : "memory");
+                const uint32_t first = __builtin_amdgcn_readfirstlane(32 * p * N * sizeof(O));
+                const uint32_t eight = __builtin_amdgcn_readfirstlane(8 * N * sizeof(O));
+                // Row 32 p + 8 e + lane / 8 of the wave's band.
+                const uint32_t row = row0 + 32 * p + lane / 8;
+                if (whole || (col_ok && row < M)) __builtin_amdgcn_raw_buffer_store_b128(v0, rc, row_off, first, 0);
+                if (whole || (col_ok && row + 8 < M))
+                    __builtin_amdgcn_raw_buffer_store_b128(v1, rc, row_off, first + eight, 0);
+                if (whole || (col_ok && row + 16 < M))
+                    __builtin_amdgcn_raw_buffer_store_b128(v2, rc, row_off, first + 2 * eight, 0);
+                if (whole || (col_ok && row + 24 < M))
+                    __builtin_amdgcn_raw_buffer_store_b128(v3, rc, row_off, first + 3 * eight, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         tile += gridDim.x;

@@ -221,20 +221,34 @@ def test_products_with_more_tiles_than_compute_units(kind, form, addend, m, k, n
 
 @pytest.mark.parametrize("in_kind,out_kind", [(lib.BF16, lib.BF16), (lib.F16, lib.F16), (lib.BF16, lib.F32),
                                               (lib.F16, lib.F32)])
-@pytest.mark.parametrize("form", [lib.PLAIN, lib.RIGHT], ids=["plain", "right"])
-def test_every_element_of_a_persistent_product(in_kind, out_kind, form):
+@pytest.mark.parametrize("form", [lib.PLAIN, lib.LEFT, lib.RIGHT], ids=["plain", "left", "right"])
+@pytest.mark.parametrize("m,k,n", [(4352, 128, 4352), (4100, 128, 4200)], ids=["whole", "ragged"])
+def test_every_element_of_a_persistent_product(in_kind, out_kind, form, m, k, n):
     # 4352 x 128 x 4352: 289 whole 256 x 256 tiles on 256 CUs, so some blocks
-    # walk two tiles, each of two steps.  A 16-bit C leaves through the
-    # staged whole-row stores, an f32 C through the accumulators' own; every
-    # element is checked against the oracle and f64, so a misplaced row or
-    # chunk of the staging cannot hide between sampled rows.
-    m, k, n = 4352, 128, 4352
-    rng = np.random.default_rng(4352 + out_kind + 5 * form)
+    # walk two tiles, each of two steps; 4100 x 128 x 4200 the same count
+    # with a ragged last tile row and column.  A 16-bit C runs the four-wave
+    # kernel, whose staged whole-row stores skip the 16-byte pieces outside
+    # C; an f32 C runs the eight-wave kernel and leaves through the
+    # accumulators' own stores.  Every element is checked against the oracle
+    # and f64, so a misplaced row or chunk of the staging, or a store past an
+    # edge, cannot hide between sampled rows.
+    rng = np.random.default_rng(m + n + out_kind + 5 * form)
     a = to_kind(rng.uniform(-1, 1, (m, k)), in_kind)
     b = to_kind(rng.uniform(-1, 1, (k, n)), in_kind)
+    x = np.ascontiguousarray(a.T) if form == lib.LEFT else a
     y = np.ascontiguousarray(b.T) if form == lib.RIGHT else b
     wa, wb = widen(in_kind, a), widen(in_kind, b)
-    got = widen(out_kind, product(in_kind, out_kind, form, a, y, m, k, n))
+    # C is followed by 256 rows of a sentinel that no store may touch.
+    guard = 256 * n
+    if out_kind == lib.F32:
+        sentinel = np.full(m * n + guard, 12345.5, dtype=np.float32)
+    else:
+        sentinel = np.full(m * n + guard, 0x7777, dtype=np.uint16).view(HOST[out_kind])
+    da, db, dc = lib.Buffer.of(x), lib.Buffer.of(y), lib.Buffer.of(sentinel)
+    lib.call("tc_matmul", in_kind, out_kind, form, 0, m, k, n, da.ptr, db.ptr, dc.ptr)
+    whole = dc.download(HOST[out_kind], m * n + guard)
+    assert np.array_equal(whole[m * n:].view(np.uint8), sentinel[m * n:].view(np.uint8))
+    got = widen(out_kind, whole[: m * n].reshape(m, n))
     tol = tolerance(in_kind, out_kind, k)
     assert error(got, wa, wb, wa.astype(np.float64) @ wb.astype(np.float64)) <= tol
     want = widen(out_kind, oracle.matmul(in_kind, a, b, m, k, n, out_dtype=out_kind))
