@@ -47,13 +47,15 @@ HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
 # HBM bytes per launch of the headline product, from `rocprofv3 --pmc
 # FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --traffic-probe`,
 # scaled by what the counters read for a plain 1 GiB copy (fetch x 2.0,
-# write x 0.9994): 1.801 GB read + 0.134 GB written (profiles/gemm_bf16_8192_traffic.md).
-HEADLINE_TRAFFIC = 1.935e9
-# HBM bytes per call of each bandwidth workload, from the same two counters
-# over `bench.py --traffic-probe` with the same calibration
-# (profiles/bandwidth_traffic.md): within 5% of the algorithmic bytes.
+# write x 0.998): 2.017 GB read + 0.134 GB written (profiles/gemm_bf16_8192_traffic.md).
+HEADLINE_TRAFFIC = 2.151e9
+# HBM bytes per call of each bandwidth workload and of the other products,
+# from the same two counters over `bench.py --traffic-probe` with the same
+# calibration (profiles/bandwidth_traffic.md, profiles/gemm_bf16_8192_traffic.md):
+# the bandwidth workloads within 5% of their algorithmic bytes.
 MEASURED_TRAFFIC = {
     "f16 GEMM 16384x1024x4096": 3.419e+08,
+    "f32 GEMM 4096x4096x4096": 8.246e+08,
     "x*y, f32 [256,512,512] x [1,512,1]": 5.365e+08,
     "t+z, f32 [256,512,512] + [256,1,512]": 5.407e+08,
     "permute(0,2,1).contiguous, f32 [256,512,512]": 5.365e+08,
