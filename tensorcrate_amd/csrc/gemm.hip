@@ -284,19 +284,18 @@ __global__ void __launch_bounds__(kThreads) gemm32_kernel(const float* __restric
 // alone, the host compiler emitted no launch stub for it (its step order is
 // built from nested generic lambdas) and the library failed to load.
 }  // namespace
-template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, true, true>(const bf16_t*, const bf16_t*, bf16_t*,
-                                                                           uint32_t, uint32_t, uint32_t);
-template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, true, false>(const bf16_t*, const bf16_t*, bf16_t*,
-                                                                            uint32_t, uint32_t, uint32_t);
-template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, false, false>(const bf16_t*, const bf16_t*, bf16_t*,
-                                                                             uint32_t, uint32_t, uint32_t);
-template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, true, true>(const _Float16*, const _Float16*,
-                                                                               _Float16*, uint32_t, uint32_t, uint32_t);
-template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, true, false>(const _Float16*, const _Float16*,
-                                                                                _Float16*, uint32_t, uint32_t, uint32_t);
-template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, false, false>(const _Float16*, const _Float16*,
-                                                                                 _Float16*, uint32_t, uint32_t,
-                                                                                 uint32_t);
+template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, true, true>(
+    const bf16_t*, const bf16_t*, bf16_t*, uint32_t, uint32_t, uint32_t, bool, PlainStore);
+template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, true, false>(
+    const bf16_t*, const bf16_t*, bf16_t*, uint32_t, uint32_t, uint32_t, bool, PlainStore);
+template __global__ void gemm16x16_wide_kernel<bf16_t, bf16_t, false, false>(
+    const bf16_t*, const bf16_t*, bf16_t*, uint32_t, uint32_t, uint32_t, bool, PlainStore);
+template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, true, true>(
+    const _Float16*, const _Float16*, _Float16*, uint32_t, uint32_t, uint32_t, bool, PlainStore);
+template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, true, false>(
+    const _Float16*, const _Float16*, _Float16*, uint32_t, uint32_t, uint32_t, bool, PlainStore);
+template __global__ void gemm16x16_wide_kernel<_Float16, _Float16, false, false>(
+    const _Float16*, const _Float16*, _Float16*, uint32_t, uint32_t, uint32_t, bool, PlainStore);
 namespace {
 
 // The tiled kernels' shapes: a 256 x 256 tile over eight waves of 128 x 64
@@ -319,7 +318,7 @@ void launch_tiled16(const S* a, const S* b, O* c, uint32_t m, uint32_t k, uint32
             // A 16-bit C written whole, by rows of 16-byte pieces, over whole
             // step pairs: the four-wave kernel.
             if (!accumulate && n % 8 == 0 && reinterpret_cast<uintptr_t>(c) % 16 == 0 && k % 128 == 0) {
-                gemm16x16_wide_kernel<S, O, A_KC, B_KC><<<cus, 256, 0, s>>>(a, b, c, m, n, k);
+                gemm16x16_wide_kernel<S, O, A_KC, B_KC><<<cus, 256, 0, s>>>(a, b, c, m, n, k, false, PlainStore{});
                 return;
             }
         }
@@ -577,13 +576,14 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
                    "tc::direct16_kernel<" + type + ", " + type + ", true, false, 128, 128, 2, 2, 64, 2, CompiledStore>"};
         if (runtime_compiler_is_ours()) {
             kernels.push_back("tc::gemm16x16_persistent_kernel<" + type + ", " + type + ", true, false, CompiledStore>");
+            kernels.push_back("tc::gemm16x16_wide_kernel<" + type + ", " + type + ", true, false, CompiledStore>");
         }
         large = ((m + 255) / 256) * ((n + 255) / 256);
         large_threads = 512;
         small_threads = 2 * 2 * 64;
     }
     small = ((m + 127) / 128) * ((n + 127) / 128);
-    hipFunction_t functions[3] = {};
+    hipFunction_t functions[4] = {};
     if (!compiled_kernels(source, kernels, functions)) return false;
     CompiledArgsOf args{};
     for (uint32_t slot = 1; slot < input_count; slot++) args.in[slot] = inputs[slot];
@@ -595,17 +595,20 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     void* params[] = {const_cast<void**>(&a), const_cast<void**>(&b), &none, &m, &n, &k, &accumulate, &args};
     const uint32_t cus = static_cast<uint32_t>(compute_units());
     const bool use_large = dtype != TC_F32 && large >= cus;
-    // 16-bit products with whole pairs of steps take the persistent kernel,
-    // as plain ones do (launch_tiled16).
-    const bool persistent = kernels.size() == 3 && use_large && ((k + 63) / 64) % 2 == 0;
+    // 16-bit products over whole step pairs take the persistent kernels, as
+    // plain ones do (launch_tiled16): the four-wave one when K is a multiple
+    // of 128, else the eight-wave one.
+    const bool wide = kernels.size() == 4 && use_large && k % 128 == 0;
+    const bool persistent = kernels.size() == 4 && use_large && ((k + 63) / 64) % 2 == 0;
     hipFunction_t function = dtype == TC_F32 ? functions[0]
+                             : wide          ? functions[3]
                              : persistent    ? functions[2]
                              : use_large     ? functions[0]
                                              : functions[1];
-    const uint32_t grid = persistent ? cus : use_large ? large : small;
+    const uint32_t grid = wide || persistent ? cus : use_large ? large : small;
+    const uint32_t threads = wide ? 256 : use_large ? large_threads : small_threads;
     count_dispatch();
-    const hipError_t error = hipModuleLaunchKernel(function, grid, 1, 1, use_large ? large_threads : small_threads, 1,
-                                                   1, 0, s, params, nullptr);
+    const hipError_t error = hipModuleLaunchKernel(function, grid, 1, 1, threads, 1, 1, 0, s, params, nullptr);
     *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused matmul: ") + hipGetErrorString(error));
     return true;
 }

@@ -1378,10 +1378,11 @@ __global__ void __launch_bounds__(512) gemm16x16_persistent_kernel(const S* __re
 // the eight-wave one, and with the loads all in the first half of the slice
 // 3% slower than evenly spread.
 //
-// For 16-bit C written whole (no accumulate, no program), N a multiple of 8,
-// C 16-byte aligned and K a multiple of 128: each tile leaves through the
-// staged whole-row stores, a lane's 16-byte piece stored only where it lies
-// inside C, so edge tiles need no other path.
+// For 16-bit C written whole (no accumulate), N a multiple of 8, C 16-byte
+// aligned and K a multiple of 128: each tile leaves through the staged
+// whole-row stores, a lane's 16-byte piece stored only where it lies inside
+// C, so edge tiles need no other path.  A program epilogue (compiled) runs
+// wave by wave over the same staging, as in the persistent kernel.
 template <typename S>
 struct InPlaceMfma;
 template <>
@@ -1419,11 +1420,12 @@ __device__ constexpr int wide_op_at(int t) {
     return t % 2 == 1 && t >= 3 && t <= 33 ? (t - 3) / 2 : -1;
 }
 
-template <typename S, typename O, bool A_KC, bool B_KC>
+template <typename S, typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 __global__ void __launch_bounds__(256) gemm16x16_wide_kernel(const S* __restrict__ A, const S* __restrict__ B,
-                                                             O* __restrict__ C, uint32_t M, uint32_t N,
-                                                             uint32_t K) {
+                                                             O* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                                                             bool accumulate, EPI epi) {
     static_assert(sizeof(O) == 2, "16-bit C");
+    (void)accumulate;  // C is written whole: launched with false
     constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 2, kWaves = WM * WN;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
     constexpr int kA = BM * BK, kB = BN * BK;
@@ -1560,6 +1562,39 @@ __global__ void __launch_bounds__(256) gemm16x16_wide_kernel(const S* __restrict
         __builtin_amdgcn_sched_barrier(0);
         // lane's accumulators of block (i, j): C[row][col .. col + 3] for row =
         // m0 + wm*128 + 16 i + lane % 16, col = n0 + wn*128 + 16 j + 4 (lane / 16).
+        if constexpr (EPI::kProgram) {
+            // As in the persistent kernel, per 64-column half of the wave's
+            // tile: one 16-row block of f32 results at a time in the wave's
+            // own 4 KiB, handed to the program EPI::kElems rows a lane.
+            constexpr int E = EPI::kElems;
+            static_assert(16 % E == 0, "whole groups of a staged block's 16 rows");
+            float* staged = reinterpret_cast<float*>(rows_lds + wave * kRegion);
+            const int r = lane % 16, g = lane / 16;
+#pragma unroll
+            for (int h = 0; h < TN / 4; h++) {
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++)
+                        *reinterpret_cast<f32x4*>(staged + r * 64 + (((4 * jj + g) ^ r) * 4)) = acc[i][4 * h + jj];
+#pragma unroll
+                    for (int v0 = 0; v0 < 16; v0 += E) {
+                        bool live[E];
+                        uint32_t row[E], col[E];
+                        float product[E];
+#pragma unroll
+                        for (int e = 0; e < E; e++) {
+                            const int v = v0 + e;
+                            product[e] = staged[v * 64 + (((lane / 4) ^ v) * 4) + lane % 4];
+                            row[e] = m0 + wm * (BM / WM) + 16 * i + v;
+                            col[e] = n0 + wn * (BN / WN) + 64 * h + lane;
+                            live[e] = row[e] < M && col[e] < N;
+                        }
+                        epi.group(live, row, col, N, product);
+                    }
+                }
+            }
+        } else {
         const bool whole = m0 + BM <= M && n0 + BN <= N;
         const int g = lane / 16;
 #pragma unroll
@@ -1605,6 +1640,7 @@ __global__ void __launch_bounds__(256) gemm16x16_wide_kernel(const S* __restrict
                     __builtin_amdgcn_raw_buffer_store_b128(v3, rc, row_off, first + 3 * eight, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
+        }
         }
         tile += gridDim.x;
         if (tile >= tiles) break;

@@ -112,8 +112,8 @@ def test_the_product_must_be_read_in_order():
 
 
 @pytest.mark.parametrize("kind", [lib.F32, lib.BF16, lib.F16])
-@pytest.mark.parametrize("m,k,n", [(520, 136, 1032), (4100, 136, 4104), (4100, 200, 4104)],
-                         ids=["small-tiles", "large-tiles", "persistent"])
+@pytest.mark.parametrize("m,k,n", [(520, 136, 1032), (4100, 136, 4104), (4100, 200, 4104), (4100, 256, 4104)],
+                         ids=["small-tiles", "large-tiles", "persistent", "four-wave"])
 def test_a_repeated_program_runs_compiled_with_the_same_bits(kind, m, k, n):
     # The first appearance of a program runs the interpreter epilogue; from
     # the second the program is compiled into the product kernel (as the
@@ -121,14 +121,19 @@ def test_a_repeated_program_runs_compiled_with_the_same_bits(kind, m, k, n):
     # give the unfused bits: in the kernel for fewer 256 x 256 tiles than
     # CUs, in the one-tile kernel for more (17 x 17 tiles, ragged, three
     # steps), and, for 16-bit types with a whole pair of steps, in the
-    # persistent kernel.  Compiled kernels are cached by source, constants
-    # being arguments, so each case has a program of its own shape: the bias
-    # added for the small tiles, subtracted for the large ones, and the
-    # scaled product's maximum with the bias for the persistent ones.
+    # eight-wave persistent kernel, or with K a multiple of 128 in the
+    # four-wave one.  Compiled kernels are cached by source, constants being
+    # arguments, so each case has a program of its own shape: the bias added
+    # for the small tiles, subtracted for the large ones, the scaled
+    # product's maximum with the bias for the persistent ones, and the
+    # minimum of product plus bias with a constant for the four-wave ones.
     code = Code()
     p = code.load(0, 0, kind)
     b = code.load(1, 1, kind)
-    if k == 200:
+    if k == 256:
+        summed = code.binary(lib.ADD, p, b)
+        code.store(code.compare(lib.MIN, summed, code.const(0.5 + kind)), kind, 0)
+    elif k == 200:
         scaled = code.binary(lib.MUL, p, code.const(0.375 + kind))
         code.store(code.compare(lib.MAX, scaled, b), kind, 0)
     else:

@@ -33,6 +33,8 @@ KERNELS = [
     "tc::inplace32_kernel<float, true, false, 128, 128, tc::PlainStore>",
     "tc::gemm16x16_persistent_kernel<tc::bf16_t, tc::bf16_t, true, false, RowStore>",
     "tc::gemm16x16_kernel<_Float16, _Float16, true, false, RowStore>",
+    "tc::gemm16x16_wide_kernel<tc::bf16_t, tc::bf16_t, true, false>",
+    "tc::gemm16x16_wide_kernel<_Float16, _Float16, false, false, RowStore>",
 ]
 # A program epilogue of the shape the library generates (csrc/gemm.hip,
 # run_compiled_epilogue): sixteen elements a thread, stored where live.
