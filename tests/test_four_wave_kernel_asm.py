@@ -1,0 +1,168 @@
+"""The four-wave product kernel's hazard cover, checked in its gfx950 assembly.
+
+`gemm16x16_wide_kernel` (csrc/gemm_kernels.hpp) writes each matrix-core step
+as one inline-assembly instruction on an in-place AGPR accumulator, so the
+compiler's hazard recognizer does not know those instructions are
+matrix-core steps and inserts no wait states around them.  The kernel relies
+on three facts instead:
+
+- a step's A and B operand registers are written by LDS loads only, whose
+  wait counts cover them, never by another vector instruction shortly
+  before the step reads them;
+- the zeroed accumulators stand several wait states before the first step
+  reads them;
+- 42 wait states separate the last step from the first read of its results.
+
+This compiles every instance the library launches, and one with a program
+epilogue, to assembly with the library's own flags, and checks those facts
+(and that nothing spills) by a straight-line scan of each kernel.  A compiler
+that moved a register copy next to a step would fail here, on the CPU,
+rather than give wrong products on the GPU.  Runs on the CPU: hipcc
+cross-compiles for gfx950.
+"""
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from tensorcrate_amd import _build
+
+CSRC = Path(__file__).resolve().parent.parent / "tensorcrate_amd" / "csrc"
+INSTANCES = [(t, f) for t in ("tc::bf16_t", "_Float16") for f in ("true, true", "true, false", "false, false")]
+SOURCE = """#include <hip/hip_runtime.h>
+#include "gemm_kernels.hpp"
+struct RowStore {
+  static constexpr bool kProgram = true;
+  static constexpr int kElems = 16;
+  float* out;
+  const float* bias;
+  __device__ __forceinline__ void group(const bool (&live)[16], const uint32_t (&row)[16], const uint32_t (&col)[16],
+                                        uint32_t N, const float (&product)[16]) const {
+    for (int e = 0; e < 16; e++)
+      if (live[e]) out[row[e] * N + col[e]] = fmaxf(product[e] + bias[col[e]], 0.0f);
+  }
+};
+namespace tc {
+%s
+}
+"""
+# Wait states a non-matrix-core vector write must stand before a step reads
+# the register, and a step's result before anything else reads it.
+BEFORE_STEP = 12
+AFTER_STEP = 18
+
+
+def instance(t, forms, epi="PlainStore"):
+    return (f"template __global__ void gemm16x16_wide_kernel<{t}, {t}, {forms}, {epi}>(const {t}*, const {t}*, "
+            f"{t}*, uint32_t, uint32_t, uint32_t, bool, {epi});")
+
+
+def registers(token, kind):
+    m = re.fullmatch(kind + r"\[(\d+):(\d+)\]", token)
+    if m:
+        return range(int(m.group(1)), int(m.group(2)) + 1)
+    m = re.fullmatch(kind + r"(\d+)", token)
+    return range(int(m.group(1)), int(m.group(1)) + 1) if m else range(0)
+
+
+def scan(body):
+    """Problems in one kernel's instructions, in program order."""
+    last = {}  # (file, register) -> (position, "step" | "vector" | "memory", text)
+    position, steps, problems = 0, 0, []
+    for raw in body.split("\n"):
+        line = raw.split(";")[0].strip()
+        if not line or line.startswith(".") or line.endswith(":"):
+            continue
+        parts = line.replace(",", " ").split()
+        op = parts[0]
+        if op == "s_nop":
+            position += int(parts[1], 0) + 1
+            continue
+        position += 1
+        if op.startswith("v_mfma"):
+            steps += 1
+            reads = [("v", r) for r in [*registers(parts[2], "v"), *registers(parts[3], "v")]]
+            reads += [("a", r) for r in registers(parts[4], "a")]
+            for reg in reads:
+                if reg in last and last[reg][1] == "vector" and position - last[reg][0] < BEFORE_STEP:
+                    problems.append(f"{last[reg][2]!r} then {line!r} {position - last[reg][0]} states later")
+            for kind in ("a", "v"):
+                for r in registers(parts[1], kind):
+                    last[(kind, r)] = (position, "step", line)
+            continue
+        if op.startswith("v_") or op.startswith(("ds_write", "buffer_store", "global_store")):
+            sources = parts[2:] if op.startswith("v_") else parts[1:]
+            for token in sources:
+                for kind in ("a", "v"):
+                    for r in registers(token, kind):
+                        reg = (kind, r)
+                        if reg in last and last[reg][1] == "step" and position - last[reg][0] < AFTER_STEP:
+                            problems.append(f"{last[reg][2]!r} then {line!r} {position - last[reg][0]} states later")
+        if op.startswith("v_") and len(parts) > 1:
+            for kind in ("a", "v"):
+                for r in registers(parts[1], kind):
+                    last[(kind, r)] = (position, "vector", line)
+        elif op.startswith(("ds_read", "buffer_load", "global_load", "scratch_load")) and len(parts) > 1:
+            if not line.endswith(" lds"):  # a load into LDS writes no register
+                for r in registers(parts[1], "v"):
+                    last[("v", r)] = (position, "memory", line)
+    return steps, problems
+
+
+@pytest.fixture(scope="module")
+def assembly(tmp_path_factory):
+    try:
+        compiler = _build.hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc is not installed")
+    work = tmp_path_factory.mktemp("asm")
+    source = work / "wide.hip"
+    lines = [instance(t, f) for t, f in INSTANCES] + [instance("tc::bf16_t", "true, false", "::RowStore")]
+    source.write_text(SOURCE % "\n".join(lines))
+    target = work / "wide.s"
+    flags = [f for f in _build.HIP_FLAGS if f != "-fPIC"]
+    result = subprocess.run([compiler, *flags, f"-I{CSRC}", "--cuda-device-only", "-S", str(source), "-o",
+                             str(target)], capture_output=True, text=True)
+    assert result.returncode == 0, result.stderr[-4000:]
+    return target.read_text()
+
+
+def kernels(text):
+    for chunk in re.split(r"\n(?=_Z\S*:)", text):
+        name = chunk.split(":", 1)[0]
+        if name.startswith("_Z") and "gemm16x16_wide_kernel" in name:
+            yield name, chunk
+
+
+def test_every_instance_is_there_and_nothing_spills(assembly):
+    names = [name for name, _ in kernels(assembly)]
+    assert len(names) == len(INSTANCES) + 1
+    spills = re.findall(r"\.name:\s+(\S*gemm16x16_wide_kernel\S*)\n(?:.*\n)*?\s+\.vgpr_spill_count:\s+(\d+)", assembly)
+    assert len(spills) == len(names)
+    assert all(count == "0" for _, count in spills), spills
+    agprs = re.findall(r"\.agpr_count:\s+(\d+)\n(?:.*\n)*?\s+\.name:\s+\S*gemm16x16_wide_kernel", assembly)
+    assert agprs and all(count == "256" for count in agprs), agprs
+
+
+def test_no_vector_write_stands_close_before_a_matrix_core_step(assembly):
+    for name, body in kernels(assembly):
+        steps, problems = scan(body)
+        assert steps == 256, (name, steps)  # two 64-deep steps of 2 x 64 matrix-core steps
+        assert not problems, (name, problems[:5])
+
+
+def test_the_scan_finds_a_planted_hazard():
+    # The same scan over a made-up sequence: a copy into an operand register
+    # one instruction before the step that reads it, and an accumulator read
+    # right after the step that writes it.
+    body = "\n".join([
+        "v_mov_b32_e32 v4, v9",
+        "v_mfma_f32_16x16x32_bf16 a[0:3], v[4:7], v[8:11], a[0:3]",
+        "v_accvgpr_read_b32 v20, a1",
+        "s_nop 7", "s_nop 7", "s_nop 7",
+        "v_mfma_f32_16x16x32_bf16 a[4:7], v[12:15], v[8:11], a[4:7]",
+    ])
+    steps, problems = scan(body)
+    assert steps == 2 and len(problems) == 2
