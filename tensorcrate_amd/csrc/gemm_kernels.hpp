@@ -209,7 +209,11 @@ constexpr int kLd32 = kBK32 + 4;
 // products) and a plain `matmul` pay for no transpose pass.  A lane's four k
 // for one tile row come from one ds_read_b128 of a K-contiguous tile, or
 // four ds_read_b32 down a row-contiguous tile ([k][rows + 4]: the 4-float
-// pad puts the four k-rows a wave reads on distinct bank quarters).  HBM is
+// pad puts the four k-rows a wave reads on distinct bank quarters).  A
+// K-contiguous tile's rows are 128 bytes, 16-byte chunk c of row r at
+// c ^ ((r / 2) % 8): conflict-free for the 16 rows a ds_read_b128 reads,
+// where rows padded to 144 bytes measured a 2-way conflict on every read
+// (16.8M conflict cycles a 4096^3 launch for each such operand).  HBM is
 // staged through buffer loads (zeros past the operand) into registers and
 // then LDS, double-buffered, 256 x 128 or 128 x 128 tiles, 32-deep steps,
 // four waves of a quarter tile.  Requirements as for the 16-bit kernel, with K (K-contiguous)
@@ -220,7 +224,10 @@ struct Stager32 {
     static constexpr int kRowChunks = KC ? kBK32 / 4 : ROWS / 4;  // 16-byte chunks per tile row
     static constexpr int kPassRows = kThreads / kRowChunks;
     static constexpr int kPasses = (KC ? ROWS : kBK32) / kPassRows;
-    static constexpr int kLdsRow = KC ? kLd32 : ROWS + 4;
+    static constexpr int kLdsRow = KC ? kBK32 : ROWS + 4;
+    static constexpr int kTile = KC ? ROWS * kLdsRow : kBK32 * kLdsRow;  // floats a stage
+    static_assert(!KC || kPassRows % 16 == 0, "a pass's rows repeat the swizzle");
+    __device__ static __forceinline__ int swizzle(int row) { return (row / 2) % 8; }
     __amdgpu_buffer_rsrc_t rsrc;
     uint32_t offset, pass_bytes, k_bytes, lds_at, k_in;
 
@@ -239,7 +246,7 @@ struct Stager32 {
         }
         offset = (row * ld + part) * 4;
         pass_bytes = kPassRows * ld * 4;
-        lds_at = row * kLdsRow + part;
+        lds_at = row * kLdsRow + (KC ? ((part / 4) ^ swizzle(row)) * 4 : part);
     }
     __device__ __forceinline__ void fetch(uint4 (&stage)[kPasses], uint32_t k0, uint32_t K, bool full) const {
         const uint32_t at = (full || !KC || k0 + k_in < K) ? offset : 0x80000000u;
@@ -258,7 +265,7 @@ struct Stager32 {
     // tile row `row`.
     __device__ __forceinline__ f32x4 fragment(const float* lds, int row, int kk, int lane) const {
         const int k = kk + (lane / 16) * 4;
-        if (KC) return reinterpret_cast<const f32x4*>(lds)[(row * kLdsRow + k) / 4];
+        if (KC) return reinterpret_cast<const f32x4*>(lds)[row * (kLdsRow / 4) + ((k / 4) ^ swizzle(row))];
         return f32x4{lds[k * kLdsRow + row], lds[(k + 1) * kLdsRow + row], lds[(k + 2) * kLdsRow + row],
                      lds[(k + 3) * kLdsRow + row]};
     }
@@ -272,8 +279,8 @@ __global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __rest
     using SA = Stager32<BM, A_KC>;
     using SB = Stager32<BN, B_KC>;
     constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wave
-    constexpr int kA = A_KC ? BM * kLd32 : kBK32 * (BM + 4);
-    constexpr int kB = B_KC ? BN * kLd32 : kBK32 * (BN + 4);
+    constexpr int kA = SA::kTile;
+    constexpr int kB = SB::kTile;
     __shared__ __attribute__((aligned(16))) float lds_a[2 * kA];
     __shared__ __attribute__((aligned(16))) float lds_b[2 * kB];
     const uint32_t tiles_m = (M + BM - 1) / BM;
