@@ -273,6 +273,73 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
     return lines
 
 
+def layer_norm(rows: int, cols: int, steps: int, warmup: int) -> list[dict]:
+    """(x - mean) / sqrt(deviations / cols + 1e-5) * gamma over the rows of an
+    f32 matrix, its row statistics read by the program (`fused_with_statistics`,
+    kernels.rs:1103): one kernel computing each row's statistics and running
+    the program over that row (`tc_fused_with_statistics`, compiled from the
+    program's second appearance), against the trait's default composition
+    (`tc_row_moments`, then `tc_fused`).  Both lines count x read once and
+    the result written once; inputs rotate past the Infinity Cache."""
+    from oracle import binding as oracle  # the CPU baseline's restatement
+
+    rng = np.random.default_rng(17)
+    nbytes = rows * cols * 4
+    xs = rotation(lambda: lib.Buffer.of(rng.uniform(-3, 3, rows * cols).astype(np.float32)), nbytes)
+    hgamma = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    gamma = lib.Buffer.of(hgamma)
+    out, means, devs = lib.Buffer(nbytes), lib.Buffer(rows * 4), lib.Buffer(rows * 4)
+    f32 = lib.F32
+    program = [(0, 0, 0, 0, f32, 0, 0.0), (0, 1, 1, 1, f32, 0, 0.0), (0, 2, 2, 2, f32, 0, 0.0),
+               (0, 2, 3, 3, f32, 0, 0.0), (1, 0, 4, 0, 0, 0, float(np.float32(1.0 / cols))),
+               (2, lib.MUL, 3, 3, 4, 0, 0.0), (1, 0, 4, 0, 0, 0, 1e-5), (2, lib.ADD, 3, 3, 4, 0, 0.0),
+               (3, 13, 3, 3, 0, 0, 0.0), (2, lib.SUB, 0, 0, 2, 0, 0.0), (2, lib.DIV, 0, 0, 3, 0, 0.0),
+               (2, lib.MUL, 0, 0, 1, 0, 0.0), (5, 0, 0, 0, f32, 0, 0.0)]
+    whole = (0, 1, 1, [rows], [cols])
+    place_list = [whole, (0, 1, 0, [], []), (0, 0, 1, [rows], [1])]
+    enc, places = lib._program(program, place_list)
+    _, whole_place = lib._program([], [whole])
+    outs, out_lens = lib._buffers([(out, rows * cols)])
+
+    def one_kernel(x):
+        ins, in_lens = lib._buffers([(x, rows * cols), (gamma, cols)])
+        stats = (lib.Statistic * 2)()
+        for i, which in enumerate((lib.STAT_MEAN, lib.STAT_DEVIATIONS)):
+            stats[i].source, stats[i].source_len, stats[i].source_dtype = x.ptr, rows * cols, f32
+            stats[i].which, stats[i].place = which, whole_place[0]
+        lib.call("tc_fused_with_statistics", f32, enc, len(program), places, 3, ins, in_lens, 2, outs, out_lens, 1,
+                 rows, cols, stats, 2)
+
+    def composed(x):
+        lib.call("tc_row_moments", f32, f32, x.ptr, rows * cols, whole_place, rows, cols, means.ptr, devs.ptr)
+        ins, in_lens = lib._buffers([(x, rows * cols), (gamma, cols), (means, rows), (devs, rows)])
+        lib.call("tc_fused", f32, enc, len(program), places, 3, ins, in_lens, 4, outs, out_lens, 1, rows, cols)
+
+    # The CPU baseline: the oracle's row moments, then its program, over a
+    # band of rows.
+    band = 64
+    hx = rng.uniform(-3, 3, band * cols).astype(np.float32)
+    band_whole = (0, 1, 1, [band], [cols])
+    band_places = [band_whole, (0, 1, 0, [], []), (0, 0, 1, [band], [1])]
+    band_out = np.empty(band * cols, np.float32)
+
+    def cpu():
+        m, d = oracle.row_moments(f32, f32, hx, band_whole, band, cols)
+        oracle.fused(f32, program, band_places, [hx, hgamma, m, d], [band_out], band, cols)
+
+    baseline = cpu_rate(cpu, 8.0 * band * cols, "GB/s",
+                        f"rows 0..{band}: the oracle's row moments, then its program, one thread", 1e9)
+    lines = []
+    for name, fn in (("statistics and program in one kernel", one_kernel),
+                     ("composed: row moments, then the program", composed)):
+        ms = timed_graph(rotating(xs, fn), steps, warmup)
+        lines.append(with_cpu(hbm_line(f"layer norm f32 [{rows}x{cols}] (fused_with_statistics), {name}",
+                                       2.0 * nbytes, ms), baseline))
+    for buffer in xs + [gamma, out, means, devs]:
+        buffer.free()
+    return lines
+
+
 PCIE_PEAK = 64.0  # GB/s, PCIe 5.0 x16, one direction
 
 
@@ -826,6 +893,7 @@ def secondary(groups: set, steps: int, warmup: int) -> list[dict]:
         # Last: the bf16 8192^3 products, so that a headline timed next runs
         # in the power state of sustained matrix-core work.
         log("dense layers, fused and unfused ...")
+        workloads += layer_norm(8192, 8192, steps, max(warmup, 3))
         workloads += dense_layer("f32", 4096, 1024, 4096, steps, warmup)
         workloads += dense_layer("bf16", 8192, 8192, 8192, steps, warmup)
     for line in workloads:

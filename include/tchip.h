@@ -513,6 +513,36 @@ int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_pl
 int tc_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, uint64_t input_len,
                    const tc_place* place, uint64_t rows, uint64_t cols, void* means, void* deviations);
 
+/* One row statistic a program reads (`RowStatistic`, fused/mod.rs:547-553):
+ * the mean, or the sum of squared deviations from it, of each row of the
+ * rows x cols matrix `place` reads of `source` (stored as `source_dtype`,
+ * `source_len` elements), as `tc_row_moments` gives them. */
+typedef enum tc_row_statistic { TC_STAT_MEAN = 0, TC_STAT_DEVIATIONS = 1 } tc_row_statistic;
+typedef struct tc_row_stat {
+    const void* source;
+    uint64_t source_len;
+    uint32_t source_dtype;
+    uint32_t which; /* a tc_row_statistic */
+    tc_place place;
+} tc_row_stat;
+
+/* `Kernels::fused_with_statistics` (kernels.rs:1103-1113; `row_statistics`,
+ * fused/mod.rs:3995-4027): run a program, as `tc_fused` does, whose inputs
+ * are `inputs` followed by `statistic_count` row statistics, statistic i
+ * being input slot `input_count + i`, a vector of `rows` values of `dtype`.
+ * By default each distinct (source, type, place) has its moments computed
+ * once by `tc_row_moments` and the program then runs with them; from the
+ * program's second appearance, when every statistic is read one value a row
+ * and at most four sources are involved, one compiled kernel computes each
+ * row's statistics and runs the program over that row, so the statistics
+ * are never stored.  Results then agree with the composition within the
+ * statistics' rounding (the moments fold in another order). */
+int tc_fused_with_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                             uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                             uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
+                             uint32_t output_count, uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
+                             uint32_t statistic_count);
+
 /* `Kernels::fused_sum` (kernels.rs:1120-1135; `Program::run_sum`,
  * fused/mod.rs:1048-1082; `axis_sum`, :4045-4051): run a program whose one
  * output is of type `dtype` (every store to output 0 as `dtype`) over a

@@ -105,6 +105,17 @@ int fused_row_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const
                    uint32_t place_count, const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
                    uint64_t rows, uint64_t cols, void* out, bool* done);
 
+// `fused_with_statistics` as one compiled kernel (fused.hip), for a checked
+// program: each row's statistics computed in registers and the program run
+// over that row.  Sets `*done` false, launching nothing, until the program
+// has been seen before or when it does not fit the compiled form (a
+// statistic read other than one value a row, more than four sources).
+int fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                         uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                         uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
+                         uint32_t output_count, uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
+                         uint32_t statistic_count, bool* done);
+
 std::string shape_text(const uint64_t* values, uint32_t rank);
 
 // ---- element types (device.hpp) ---------------------------------------------

@@ -1,10 +1,11 @@
 // The `Kernels` members that compose a fused program with a product or a
 // reduction: `row_moments` (kernels.rs:1090), `fused_sum` (kernels.rs:1120)
 // and `matmul_epilogue` (kernels.rs:1142); and `matrix_axis_moments`
-// (kernels.rs:1042), the moments reduction along an axis.  `fused_with_statistics`
-// (kernels.rs:1103) is their composition on the host side: `row_moments`
-// for each statistic the program derives, then `tc_fused` with those as
-// extra inputs, as the trait's default does.
+// (kernels.rs:1042), the moments reduction along an axis; and
+// `fused_with_statistics` (kernels.rs:1103): from a program's second
+// appearance one compiled kernel (fused.hip), otherwise `row_moments` for
+// each statistic the program derives, then `tc_fused` with those as extra
+// inputs, as the trait's default does.
 //
 // Each runs as the Host backend defines it, over device storage:
 //  - row_moments: the rows x cols matrix a place reads of an input, in the
@@ -136,6 +137,81 @@ int tc_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, uint
     split.folded[0] = cols;
     split.folded_strides[0] = 1;
     return reduce_moments(dtype, matrix.ptr, n, &split, means, deviations);
+}
+
+int tc_fused_with_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                             uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                             uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
+                             uint32_t output_count, uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
+                             uint32_t statistic_count) {
+    if (!is_float(dtype)) {
+        return fail(TC_UNSUPPORTED, std::string("fused with statistics: no kernel computes in ") + dtype_name(dtype));
+    }
+    if (input_count + statistic_count > TC_FUSED_MAX_INPUTS) {
+        return fail(TC_INVALID, "fused with statistics: " + std::to_string(input_count + statistic_count) +
+                                    " inputs with the statistics, over the " + std::to_string(TC_FUSED_MAX_INPUTS) +
+                                    " limit");
+    }
+    for (uint32_t i = 0; i < statistic_count; i++) {
+        const tc_row_stat& st = statistics[i];
+        if (st.which > TC_STAT_DEVIATIONS || !is_float(st.source_dtype) || st.place.lead > TC_FUSED_LEAD) {
+            return fail(TC_INVALID, "fused with statistics: statistic " + std::to_string(i) + " is malformed");
+        }
+    }
+    const void* all[TC_FUSED_MAX_INPUTS] = {};
+    uint64_t all_lens[TC_FUSED_MAX_INPUTS] = {};
+    for (uint32_t k = 0; k < input_count; k++) {
+        all[k] = inputs[k];
+        all_lens[k] = input_lens[k];
+    }
+    for (uint32_t i = 0; i < statistic_count; i++) all_lens[input_count + i] = rows;
+    const uint32_t total = input_count + statistic_count;
+    int status = check_fused(dtype, code, count, places, place_count, all_lens, total, output_lens, output_count,
+                             rows, cols);
+    if (status != TC_OK) return status;
+    if (rows == 0) return TC_OK;
+    if (statistic_count == 0) {
+        return tc_fused(dtype, code, count, places, place_count, all, all_lens, total, outputs, output_lens,
+                        output_count, rows, cols);
+    }
+    bool done = false;
+    status = fused_row_statistics(dtype, code, count, places, place_count, all, all_lens, input_count, outputs,
+                                  output_lens, output_count, rows, cols, statistics, statistic_count, &done);
+    if (status != TC_OK || done) return status;
+    // The trait's default: each distinct source's moments once, then the
+    // program with them as inputs.
+    const uint64_t width = dtype_size(dtype);
+    Scratch moments(2 * statistic_count * rows * width);
+    if (moments.status != TC_OK) return moments.status;
+    uint8_t* base = static_cast<uint8_t*>(moments.ptr);
+    uint32_t computed[8];
+    uint32_t distinct = 0;
+    for (uint32_t i = 0; i < statistic_count; i++) {
+        const tc_row_stat& st = statistics[i];
+        uint32_t j = 0;
+        for (; j < distinct; j++) {
+            const tc_row_stat& f = statistics[computed[j]];
+            bool same = f.source == st.source && f.source_dtype == st.source_dtype &&
+                        f.place.offset == st.place.offset && f.place.col_step == st.place.col_step &&
+                        f.place.lead == st.place.lead;
+            for (uint32_t d = 0; same && d < st.place.lead; d++) {
+                same = f.place.dims[d] == st.place.dims[d] && f.place.steps[d] == st.place.steps[d];
+            }
+            if (same) break;
+        }
+        void* means = base + 2 * j * rows * width;
+        void* deviations = base + (2 * j + 1) * rows * width;
+        if (j == distinct) {
+            if (distinct == 8) return fail(TC_INVALID, "fused with statistics: more than 8 statistics");
+            computed[distinct++] = i;
+            status = tc_row_moments(dtype, st.source_dtype, st.source, st.source_len, &st.place, rows, cols, means,
+                                    deviations);
+            if (status != TC_OK) return status;
+        }
+        all[input_count + i] = st.which == TC_STAT_MEAN ? means : deviations;
+    }
+    return tc_fused(dtype, code, count, places, place_count, all, all_lens, total, outputs, output_lens,
+                    output_count, rows, cols);
 }
 
 int tc_axis_moments(uint32_t dtype, const void* a, uint64_t rows, uint64_t cols, uint32_t axis, void* means,

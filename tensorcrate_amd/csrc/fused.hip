@@ -444,7 +444,8 @@ bool cached_kernels(const std::string& source, const std::vector<std::string>& k
 // each constant from `constants[]` (appended to `*constants`).  With
 // `product_input`, input 0 is the product rather than a load.
 std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
-                       const tc_place* places, std::vector<float>* constants, bool sum_store = false) {
+                       const tc_place* places, std::vector<float>* constants, bool sum_store = false,
+                       int stat_first = -1) {
     static const char* const kBinary[] = {"+", "-", "*", "/"};
     const std::string round = "tc_round<" + std::to_string(dtype) + ">";
     std::ostringstream src;
@@ -468,6 +469,9 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
             case 0:
                 if (product_input && in.a == 0) {
                     src << "live[e] ? " << round << "(product[e]) : 0.0f;\n";
+                } else if (stat_first >= 0 && in.a >= stat_first) {
+                    // A row statistic, one value a row, already in the type.
+                    src << "stat[" << (in.a - stat_first) << "];\n";
                 } else {
                     // Every lane loads, an element outside C at (0, 0), so
                     // no load waits on a branch; the place's row walk is
@@ -859,5 +863,154 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
 extern "C" int tc_fused_compiled(uint64_t* count) {
     std::lock_guard<std::mutex> lock(compiled_mutex);
     *count = compiled_count;
+    return TC_OK;
+}
+
+// `fused_with_statistics` (kernels.rs:1103-1113) as one compiled kernel, from
+// the program's second appearance: a wave a row.  For each distinct source it
+// sums the row's values (through the source's place, rounded to the
+// program's type) lane by lane in element order and the wave in a fixed
+// shuffle tree, takes the mean, then sums the squared deviations from it the
+// same way; mean and deviations are rounded to the program's type, as the
+// composed form stores them, and the program then runs over the row with
+// each statistic read from a register.  The row is read from HBM once; its
+// second and third reads hit the caches.
+int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                             uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                             uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
+                             uint32_t output_count, uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
+                             uint32_t statistic_count, bool* done) {
+    *done = false;
+    constexpr uint32_t kMaxSources = 4;
+    if (statistic_count == 0 || statistic_count > 8 || place_count > static_cast<uint32_t>(kInlinePlaces) ||
+        rows == 0 || cols == 0 || rows * cols > (uint64_t{1} << 31)) {
+        return TC_OK;
+    }
+    // Every load of a statistic reads one value a row, in the program's type.
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind != 0 || in.a < input_count) continue;
+        if (in.op >= place_count || in.b != dtype) return TC_OK;
+        const tc_place& p = places[in.op];
+        if (p.offset != 0 || p.col_step != 0 || p.lead != 1 || p.dims[0] != rows || p.steps[0] != 1) return TC_OK;
+    }
+    // The distinct sources, each with its place checked against its length.
+    uint32_t source_of[8];
+    uint32_t sources = 0;
+    const tc_row_stat* first[kMaxSources];
+    for (uint32_t i = 0; i < statistic_count; i++) {
+        const tc_row_stat& st = statistics[i];
+        uint32_t j = 0;
+        for (; j < sources; j++) {
+            const tc_row_stat& f = *first[j];
+            bool same = f.source == st.source && f.source_dtype == st.source_dtype && f.place.offset == st.place.offset &&
+                        f.place.col_step == st.place.col_step && f.place.lead == st.place.lead;
+            for (uint32_t d = 0; same && d < st.place.lead; d++) {
+                same = f.place.dims[d] == st.place.dims[d] && f.place.steps[d] == st.place.steps[d];
+            }
+            if (same) break;
+        }
+        if (j == sources) {
+            if (sources == kMaxSources) return TC_OK;
+            uint64_t end = 0;
+            if (!place_end(st.place, rows, cols, &end) || end > st.source_len) {
+                return fail(TC_INVALID, "fused with statistics: statistic " + std::to_string(i) +
+                                            " reads past its source's " + std::to_string(st.source_len) + " elements");
+            }
+            first[sources++] = &st;
+        }
+        source_of[i] = j;
+    }
+    std::vector<float> constants;
+    const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, &constants, false,
+                                        static_cast<int>(input_count));
+    if (constants.size() > static_cast<size_t>(kInlineCode)) return TC_OK;
+    const std::string E = std::to_string(kGeneralElems), S = std::to_string(statistic_count),
+                      T = std::to_string(dtype);
+    std::ostringstream src;
+    src << "#include \"device.hpp\"\n"
+           "struct Program {\n" << compiled_members()
+        << "  __device__ __forceinline__ void group(const bool (&live)[" << E << "], const uint32_t (&row)[" << E
+        << "],\n      const uint32_t (&col)[" << E << "], uint32_t N, const float (&stat)[" << S << "]) const {\n"
+        << body << "  }\n};\n"
+           "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
+           "__device__ __forceinline__ float wave_sum(float v) {\n"
+           "  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);\n"
+           "  return v;\n"
+           "}\n"
+           "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_row_statistics(Program p, Sources src,\n"
+           "    uint32_t rows, uint32_t cols) {\n"
+           "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
+           "  for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {\n"
+           "    float stat[" << S << "];\n";
+    for (uint32_t j = 0; j < sources; j++) {
+        const std::string J = std::to_string(j), D = std::to_string(first[j]->source_dtype);
+        // Sixteen loads in flight a lane; each lane still adds its
+        // elements in column order.
+        const std::string value = "tc_round<" + T + ">(tc::load_as(src.in[" + J + "], " + D +
+                                  "u, tc::place_at(src.places[" + J + "], r, c)))";
+        const std::string batch = "      for (uint32_t c0 = lane; c0 < cols; c0 += 64u * 16u) {\n"
+                                  "        float x[16];\n"
+                                  "        for (int u = 0; u < 16; u++) {\n"
+                                  "          const uint32_t c = c0 + 64u * u;\n"
+                                  "          x[u] = c < cols ? " + value + " : 0.0f;\n"
+                                  "        }\n";
+        src << "    {\n"
+               "      float sum = 0.0f;\n" << batch <<
+               "        for (int u = 0; u < 16; u++) if (c0 + 64u * u < cols) sum += x[u];\n"
+               "      }\n"
+               "      const float mean = wave_sum(sum) / (float)cols;\n"
+               "      float squares = 0.0f;\n" << batch <<
+               "        for (int u = 0; u < 16; u++) {\n"
+               "          const float d = x[u] - mean;\n"
+               "          if (c0 + 64u * u < cols) squares += d * d;\n"
+               "        }\n"
+               "      }\n"
+               "      const float deviations = wave_sum(squares);\n";
+        for (uint32_t i = 0; i < statistic_count; i++) {
+            if (source_of[i] != j) continue;
+            src << "      stat[" << i << "] = tc_round<" << T << ">("
+                << (statistics[i].which == TC_STAT_MEAN ? "mean" : "deviations") << ");\n";
+        }
+        src << "    }\n";
+    }
+    src << "    for (uint32_t c0 = 0; c0 < cols; c0 += 64u * " << E << ") {\n"
+           "      uint32_t row[" << E << "], col[" << E << "];\n"
+           "      bool live[" << E << "];\n"
+           "      for (int v = 0; v < " << E << "; v++) {\n"
+           "        col[v] = c0 + v * 64u + lane;\n"
+           "        row[v] = r;\n"
+           "        live[v] = col[v] < cols;\n"
+           "      }\n"
+           "      p.group(live, row, col, cols, stat);\n"
+           "    }\n"
+           "  }\n"
+           "}\n";
+    hipFunction_t function = nullptr;
+    if (!cached_kernels(src.str(), {"tc_fused_row_statistics"}, &function)) return TC_OK;
+    TC_STREAM(s);
+    CompiledArgsOf args{};
+    for (uint32_t k = 0; k < input_count; k++) args.in[k] = inputs[k];
+    for (uint32_t k = 0; k < output_count; k++) args.out[k] = outputs[k];
+    int status = to_device_places(places, place_count, args.places);
+    if (status != TC_OK) return status;
+    for (size_t c = 0; c < constants.size(); c++) args.constants[c] = constants[c];
+    struct {
+        const void* in[4];
+        DevicePlace places[4];
+    } where{};
+    for (uint32_t j = 0; j < sources; j++) {
+        where.in[j] = first[j]->source;
+        status = to_device_places(&first[j]->place, 1, &where.places[j]);
+        if (status != TC_OK) return status;
+    }
+    uint32_t rows32 = static_cast<uint32_t>(rows), cols32 = static_cast<uint32_t>(cols);
+    void* params[] = {&args, &where, &rows32, &cols32};
+    const uint64_t wanted = (rows + 3) / 4;
+    const uint32_t blocks = static_cast<uint32_t>(wanted < 0xffffffu ? wanted : 0xffffffu);
+    count_dispatch();
+    const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);
+    if (error != hipSuccess) return fail(TC_DEVICE, std::string("fused with statistics: ") + hipGetErrorString(error));
+    *done = true;
     return TC_OK;
 }

@@ -90,6 +90,20 @@ class Place(ctypes.Structure):
     ]
 
 
+class Statistic(ctypes.Structure):
+    """``tc_row_stat``: one row statistic a program reads."""
+    _fields_ = [
+        ("source", ctypes.c_void_p),
+        ("source_len", ctypes.c_uint64),
+        ("source_dtype", ctypes.c_uint32),
+        ("which", ctypes.c_uint32),
+        ("place", Place),
+    ]
+
+
+STAT_MEAN, STAT_DEVIATIONS = 0, 1
+
+
 class HipError(RuntimeError):
     """A failed call: the status code and the library's message."""
 
@@ -172,6 +186,9 @@ SIGNATURES = {
                  ctypes.POINTER(u64), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32, u64, u64],
     "tc_fused_compiled": [ctypes.POINTER(u64)],
     "tc_row_moments": [u32, u32, vp, u64, ctypes.POINTER(Place), u64, u64, vp, vp],
+    "tc_fused_with_statistics": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, ctypes.POINTER(vp),
+                                 ctypes.POINTER(u64), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32, u64, u64,
+                                 ctypes.POINTER(Statistic), u32],
     "tc_fused_sum": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, ctypes.POINTER(vp),
                      ctypes.POINTER(u64), u32, u64, u64, u32, vp],
     "tc_matmul_epilogue": [u32, ctypes.POINTER(Encoded), u32, ctypes.POINTER(Place), u32, u64, u64, u64, vp, vp,
@@ -343,25 +360,26 @@ def fused_sum(dtype: int, code, places, inputs, rows: int, cols: int, axis: int,
 
 
 def fused_with_statistics(dtype: int, code, places, inputs, outputs, rows: int, cols: int, statistics) -> None:
-    """``Kernels::fused_with_statistics`` as the trait's default composes it
-    (kernels.rs:1103-1113; ``row_statistics``, fused/mod.rs:3995-4027): each
-    input's row moments computed once by ``tc_row_moments``, the statistics
-    the program reads appended after ``inputs``, then ``tc_fused``.
+    """``tc_fused_with_statistics`` (``Kernels::fused_with_statistics``,
+    kernels.rs:1103-1113): the program runs over ``inputs`` followed by its
+    row statistics, statistic i being input slot ``len(inputs) + i``.
 
     ``statistics`` lists, in slot order, (source Buffer, element count,
-    storage dtype, place, "mean" | "deviations"); a source read through the
-    same place shares one computation of its moments."""
-    moments = {}
-    extra = []
-    for source, source_len, source_dtype, place, which in statistics:
-        key = (source.ptr, source_dtype, repr(place))
-        if key not in moments:
-            size = 4 if dtype == F32 else 2
-            means, deviations = Buffer(max(rows, 1) * size), Buffer(max(rows, 1) * size)
-            row_moments(dtype, source_dtype, source, source_len, place, rows, cols, means, deviations)
-            moments[key] = {"mean": means, "deviations": deviations}
-        extra.append((moments[key][which], rows))
-    fused(dtype, code, places, list(inputs) + extra, outputs, rows, cols)
+    storage dtype, place, "mean" | "deviations").  The library computes each
+    distinct source's moments once (``tc_row_moments``) and runs the program
+    with them, or, from the program's second appearance, runs one compiled
+    kernel that never stores them."""
+    enc, pl = _program(code, places)
+    ins, in_lens = _buffers(inputs)
+    outs, out_lens = _buffers(outputs)
+    stats = (Statistic * max(len(statistics), 1))()
+    for i, (source, source_len, source_dtype, place, which) in enumerate(statistics):
+        _, spl = _program([], [place])
+        stats[i].source, stats[i].source_len, stats[i].source_dtype = source.ptr, source_len, source_dtype
+        stats[i].which = {"mean": STAT_MEAN, "deviations": STAT_DEVIATIONS}[which]
+        stats[i].place = spl[0]
+    call("tc_fused_with_statistics", dtype, enc, len(code), pl, len(places), ins, in_lens, len(inputs), outs,
+         out_lens, len(outputs), rows, cols, stats, len(statistics))
 
 
 def matmul_epilogue(dtype: int, code, places, a, b, m: int, k: int, n: int, inputs, outputs) -> None:

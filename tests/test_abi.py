@@ -57,6 +57,7 @@ def test_struct_layouts_match_the_header():
     assert ctypes.sizeof(lib.Region) == 24 + 48 + 2 * 56
     assert lib.Split.kept.offset == 16
     assert ctypes.sizeof(lib.Place) == 8 + 8 + 8 + 40 + 40
+    assert ctypes.sizeof(lib.Statistic) == 8 + 8 + 4 + 4 + ctypes.sizeof(lib.Place)
 
 
 def test_errors_are_reported_not_raised_on_the_device():

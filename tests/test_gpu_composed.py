@@ -16,7 +16,7 @@ import pytest
 
 from oracle import binding as oracle
 from tensorcrate_amd import lib
-from tests.common import EXP, Code, Lcg, identity_place, row_broadcast, to_kind, widen
+from tests.common import EXP, Code, Lcg, column_broadcast, identity_place, row_broadcast, to_kind, widen
 from tests.test_oracle_composed import PLACES, exp_program, layer_norm, oracle_at, relu_layer, statistic_operands
 
 pytestmark = pytest.mark.gpu
@@ -186,3 +186,44 @@ def test_row_sums_of_a_repeated_program_run_as_one_compiled_kernel(dtype):
         lib.call("tc_fused_compiled", ctypes.byref(count))
         counts.append(count.value)
     assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
+
+
+@pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
+def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype):
+    # From the program's second appearance its statistics and the program run
+    # as one kernel (the statistics never stored): compiled once, and every
+    # run, composed or compiled, within the statistics' rounding of the
+    # oracle.  (x - mean) / (deviations / cols + 1) is this test's own
+    # program; the moments fold in another order than the oracle's, which
+    # moves the statistics by their last place at most.
+    import ctypes
+
+    rows, cols = 300, 777
+    code = Code()
+    x = code.load(0, 0, dtype)
+    mean = code.load(1, 1, dtype)
+    deviations = code.load(1, 2, dtype)
+    centered = code.binary(lib.SUB, x, mean)
+    scale = code.binary(lib.ADD, code.binary(lib.MUL, deviations, code.const(np.float32(1.0 / cols))),
+                        code.const(1.0))
+    code.store(code.binary(lib.DIV, centered, scale), dtype, 0)
+    places = [identity_place(rows, cols), column_broadcast(rows)]
+    whole = identity_place(rows, cols)
+    xs = to_kind(np.random.default_rng(dtype).uniform(-3, 3, rows * cols).astype(np.float32), dtype)
+    dx = lib.Buffer.of(xs)
+    means, devs = oracle.row_moments(dtype, dtype, xs, whole, rows, cols)
+    want = np.zeros(rows * cols, HOST[dtype])
+    oracle.fused(dtype, code.code, places, [xs, means, devs], [want], rows, cols)
+    want = widen(dtype, want).astype(np.float64)
+    tol = 4 * UNIT[dtype] * np.max(np.abs(want)) + 64 * np.sqrt(cols) * 2.0 ** -24 * 4
+    compiled = []
+    for _ in range(3):
+        out = lib.Buffer(rows * cols * np.dtype(HOST[dtype]).itemsize)
+        lib.fused_with_statistics(dtype, code.code, places, [(dx, xs.size)], [(out, rows * cols)], rows, cols,
+                                  [(dx, xs.size, dtype, whole, "mean"), (dx, xs.size, dtype, whole, "deviations")])
+        got = widen(dtype, out.download(HOST[dtype], rows * cols)).astype(np.float64)
+        assert np.max(np.abs(got - want)) <= tol
+        count = ctypes.c_uint64()
+        lib.call("tc_fused_compiled", ctypes.byref(count))
+        compiled.append(count.value)
+    assert compiled[1] == compiled[0] + 1 and compiled[2] == compiled[1]
