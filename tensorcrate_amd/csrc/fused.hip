@@ -538,8 +538,9 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
 // A program whose loads do not all walk in element order (a broadcast
 // operand, a transposed view) runs compiled too, from its second
 // appearance: a kernel over the rows x cols space, 16 elements a thread 64
-// apart (each load and store instruction of a wave one contiguous run), each
-// element's row and column by one 32-bit division, the program as the same
+// apart (each load and store instruction of a wave one contiguous run), a
+// thread's first element's row and column by one 32-bit division and the
+// rest by stepping 64 columns on, the program as the same
 // straight-line code a product epilogue runs.
 constexpr int kGeneralElems = 16;
 
@@ -564,11 +565,24 @@ bool run_general_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype
         "  for (uint32_t base = blockIdx.x * per_block; base < total; base += gridDim.x * per_block) {\n"
         "    uint32_t row[" + E + "], col[" + E + "];\n"
         "    bool live[" + E + "];\n"
+        "    const uint32_t first = base + wave * (64u * " + E + ") + lane;\n"
+        "    uint32_t r = first / cols, c = first - r * cols;\n"
         "    for (int v = 0; v < " + E + "; v++) {\n"
-        "      const uint32_t at = base + wave * (64u * " + E + ") + v * 64u + lane;\n"
+        "      const uint32_t at = first + v * 64u;\n"
         "      live[v] = at < total;\n"
-        "      row[v] = at / cols;\n"
-        "      col[v] = at - row[v] * cols;\n"
+        "      if (v > 0) {\n"
+        "        // 64 elements on: one step of the row walk when rows are at\n"
+        "        // least 64 long, a division otherwise.\n"
+        "        if (cols >= 64u) {\n"
+        "          c += 64u;\n"
+        "          if (c >= cols) { c -= cols; r++; }\n"
+        "        } else {\n"
+        "          r = at / cols;\n"
+        "          c = at - r * cols;\n"
+        "        }\n"
+        "      }\n"
+        "      row[v] = r;\n"
+        "      col[v] = c;\n"
         "    }\n"
         "    p.group(live, row, col, cols);\n"
         "  }\n"
