@@ -188,17 +188,20 @@ def test_row_sums_of_a_repeated_program_run_as_one_compiled_kernel(dtype):
     assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
 
 
+@pytest.mark.parametrize("shape", [(300, 777), (40, 8300)])
 @pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
-def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype):
+def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # From the program's second appearance its statistics and the program run
     # as one kernel (the statistics never stored): compiled once, and every
     # run, composed or compiled, within the statistics' rounding of the
     # oracle.  (x - mean) / (deviations / cols + 1) is this test's own
     # program; the moments fold in another order than the oracle's, which
-    # moves the statistics by their last place at most.
+    # moves the statistics by their last place at most.  Rows of 777 are
+    # ragged against a wave's 64 lanes and its 16-load batches; rows of 8300
+    # take more than eight batches a pass.
     import ctypes
 
-    rows, cols = 300, 777
+    rows, cols = shape
     code = Code()
     x = code.load(0, 0, dtype)
     mean = code.load(1, 1, dtype)
