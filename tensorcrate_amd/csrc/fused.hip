@@ -443,6 +443,22 @@ bool cached_kernels(const std::string& source, const std::vector<std::string>& k
 // value a local, each load through `places[j]` of the epilogue's arguments,
 // each constant from `constants[]` (appended to `*constants`).  With
 // `product_input`, input 0 is the product rather than a load.
+// The element index of `place` (the device copy named `p`) at row `r`,
+// column `c`: column steps of 0 and 1 and a row step of 0, the usual
+// broadcast and contiguous places, are written without their multiply, so
+// the kernel's source (and its cache key) carries them.
+std::string place_index(const tc_place& place, const std::string& p, const std::string& r, const std::string& c) {
+    if (place.lead > 1) return "tc::place_at(" + p + ", " + r + ", " + c + ")";
+    std::string index = p + ".offset";
+    if (place.col_step == 1) {
+        index += " + (uint64_t)" + c;
+    } else if (place.col_step != 0) {
+        index += " + (uint64_t)" + c + " * " + p + ".col_step";
+    }
+    if (place.lead == 1 && place.steps[0] != 0) index += " + (uint64_t)" + r + " * " + p + ".steps[0]";
+    return index;
+}
+
 std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                        const tc_place* places, std::vector<float>* constants, bool sum_store = false,
                        int stat_first = -1) {
@@ -478,12 +494,7 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                     // written out for the usual one or no folded axes.
                     const std::string p = "places[" + std::to_string(in.op) + "]";
                     const std::string r = "(live[e] ? row[e] : 0u)", c = "(live[e] ? col[e] : 0u)";
-                    std::string index = p + ".offset + (uint64_t)" + c + " * " + p + ".col_step";
-                    if (places[in.op].lead == 1) {
-                        index += " + (uint64_t)" + r + " * " + p + ".steps[0]";
-                    } else if (places[in.op].lead > 1) {
-                        index = "tc::place_at(" + p + ", " + r + ", " + c + ")";
-                    }
+                    std::string index = place_index(places[in.op], p, r, c);
                     src << "live[e] ? " << round << "(tc::load_as(in[" << int(in.a) << "], " << int(in.b) << "u, "
                         << index << ")) : 0.0f;\n";
                 }
@@ -961,8 +972,8 @@ int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
         const std::string J = std::to_string(j), D = std::to_string(first[j]->source_dtype);
         // Sixteen loads in flight a lane; each lane still adds its
         // elements in column order.
-        const std::string value = "tc_round<" + T + ">(tc::load_as(src.in[" + J + "], " + D +
-                                  "u, tc::place_at(src.places[" + J + "], r, c)))";
+        const std::string value = "tc_round<" + T + ">(tc::load_as(src.in[" + J + "], " + D + "u, " +
+                                  place_index(first[j]->place, "src.places[" + J + "]", "r", "c") + "))";
         const std::string batch = "      for (uint32_t c0 = lane; c0 < cols; c0 += 64u * 16u) {\n"
                                   "        float x[16];\n"
                                   "        for (int u = 0; u < 16; u++) {\n"

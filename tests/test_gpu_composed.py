@@ -198,7 +198,9 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # program; the moments fold in another order than the oracle's, which
     # moves the statistics by their last place at most.  Rows of 777 are
     # ragged against a wave's 64 lanes and its 16-load batches; rows of 8300
-    # take more than eight batches a pass.
+    # take more than eight batches a pass.  The kernel's source does not
+    # depend on the shape, so the second shape may find it compiled already;
+    # either way the last call is one launch.
     import ctypes
 
     rows, cols = shape
@@ -222,11 +224,14 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     compiled = []
     for _ in range(3):
         out = lib.Buffer(rows * cols * np.dtype(HOST[dtype]).itemsize)
+        before = lib.activity()[0]
         lib.fused_with_statistics(dtype, code.code, places, [(dx, xs.size)], [(out, rows * cols)], rows, cols,
                                   [(dx, xs.size, dtype, whole, "mean"), (dx, xs.size, dtype, whole, "deviations")])
+        launches = lib.activity()[0] - before
         got = widen(dtype, out.download(HOST[dtype], rows * cols)).astype(np.float64)
         assert np.max(np.abs(got - want)) <= tol
         count = ctypes.c_uint64()
         lib.call("tc_fused_compiled", ctypes.byref(count))
         compiled.append(count.value)
-    assert compiled[1] == compiled[0] + 1 and compiled[2] == compiled[1]
+    assert compiled[1] - compiled[0] in (0, 1) and compiled[2] == compiled[1]
+    assert launches == 1
