@@ -892,14 +892,15 @@ extern "C" int tc_fused_compiled(uint64_t* count) {
 }
 
 // `fused_with_statistics` (kernels.rs:1103-1113) as one compiled kernel, from
-// the program's second appearance: a wave a row.  For each distinct source it
-// sums the row's values (through the source's place, rounded to the
-// program's type) lane by lane in element order and the wave in a fixed
-// shuffle tree, takes the mean, then sums the squared deviations from it the
-// same way; mean and deviations are rounded to the program's type, as the
+// the program's second appearance: a wave a row.  For each distinct source
+// one pass over the row (through the source's place, rounded to the
+// program's type) takes each lane's batches of 16 elements, their mean and
+// squared deviations from it, and merges them into the lane's running
+// moments (Chan's pairwise update), then merges the wave's lanes in a fixed
+// tree; mean and deviations are rounded to the program's type, as the
 // composed form stores them, and the program then runs over the row with
-// each statistic read from a register.  The row is read from HBM once; its
-// second and third reads hit the caches.
+// each statistic read from a register.  The row's second read, for the
+// program, mostly hits the caches.
 int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
                              uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
                              uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
@@ -959,9 +960,22 @@ int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
         << "],\n      const uint32_t (&col)[" << E << "], uint32_t N, const float (&stat)[" << S << "]) const {\n"
         << body << "  }\n};\n"
            "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
-           "__device__ __forceinline__ float wave_sum(float v) {\n"
-           "  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);\n"
-           "  return v;\n"
+           "struct Moments { float n, mean, m2; };\n"
+           "// Chan's pairwise merge of two (count, mean, squared deviations).\n"
+           "__device__ __forceinline__ Moments merge(Moments a, Moments b) {\n"
+           "  if (b.n == 0.0f) return a;\n"
+           "  if (a.n == 0.0f) return b;\n"
+           "  const float n = a.n + b.n, delta = b.mean - a.mean, share = b.n / n;\n"
+           "  return Moments{n, a.mean + delta * share, a.m2 + b.m2 + delta * delta * (a.n * share)};\n"
+           "}\n"
+           "// Every lane ends with the same bits: each step merges the lower\n"
+           "// lane's moments with the higher lane's, on both lanes.\n"
+           "__device__ __forceinline__ Moments wave_merge(Moments m, uint32_t lane) {\n"
+           "  for (int offset = 1; offset < 64; offset <<= 1) {\n"
+           "    const Moments o{__shfl_xor(m.n, offset), __shfl_xor(m.mean, offset), __shfl_xor(m.m2, offset)};\n"
+           "    m = (lane & offset) == 0 ? merge(m, o) : merge(o, m);\n"
+           "  }\n"
+           "  return m;\n"
            "}\n"
            "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_row_statistics(Program p, Sources src,\n"
            "    uint32_t rows, uint32_t cols) {\n"
@@ -980,18 +994,22 @@ int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
                                   "          const uint32_t c = c0 + 64u * u;\n"
                                   "          x[u] = c < cols ? " + value + " : 0.0f;\n"
                                   "        }\n";
+        // One pass: each batch's own mean and squared deviations, merged
+        // into the lane's running moments, then the wave's lanes merged.
         src << "    {\n"
-               "      float sum = 0.0f;\n" << batch <<
-               "        for (int u = 0; u < 16; u++) if (c0 + 64u * u < cols) sum += x[u];\n"
-               "      }\n"
-               "      const float mean = wave_sum(sum) / (float)cols;\n"
-               "      float squares = 0.0f;\n" << batch <<
+               "      Moments m{0.0f, 0.0f, 0.0f};\n" << batch <<
+               "        float bs = 0.0f, bn = 0.0f;\n"
+               "        for (int u = 0; u < 16; u++) if (c0 + 64u * u < cols) { bs += x[u]; bn += 1.0f; }\n"
+               "        const float bm = bn > 0.0f ? bs / bn : 0.0f;\n"
+               "        float bq = 0.0f;\n"
                "        for (int u = 0; u < 16; u++) {\n"
-               "          const float d = x[u] - mean;\n"
-               "          if (c0 + 64u * u < cols) squares += d * d;\n"
+               "          const float d = x[u] - bm;\n"
+               "          if (c0 + 64u * u < cols) bq += d * d;\n"
                "        }\n"
+               "        m = merge(m, Moments{bn, bm, bq});\n"
                "      }\n"
-               "      const float deviations = wave_sum(squares);\n";
+               "      m = wave_merge(m, lane);\n"
+               "      const float mean = m.mean, deviations = m.m2;\n";
         for (uint32_t i = 0; i < statistic_count; i++) {
             if (source_of[i] != j) continue;
             src << "      stat[" << i << "] = tc_round<" << T << ">("
