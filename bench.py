@@ -86,19 +86,32 @@ def log(message: str) -> None:
     print(message, file=sys.stderr, flush=True)
 
 
-def timed(fn, steps: int, warmup: int) -> float:
-    """Milliseconds per call of `fn` over `steps` calls after `warmup`."""
-    for _ in range(warmup):
-        fn()
-    lib.sync()
-    lib.call("tc_timer_begin")
-    for _ in range(steps):
-        fn()
-    ms = ctypes.c_float()
-    lib.call("tc_timer_end", ctypes.byref(ms))
-    lib.sync()
-    return ms.value / steps
+class Timing(float):
+    """Mean milliseconds per call over every timed call, carrying the spread
+    the reference harness reports (benches/nn_ops.rs:185-252): the median
+    and minimum of the samples, and their median absolute deviation as a
+    fraction of the median."""
 
+    median: float
+    low: float
+    mad: float
+    samples: int
+
+    @staticmethod
+    def of(mean: float, samples: list[float]) -> "Timing":
+        t = Timing(mean)
+        ordered = sorted(samples)
+        t.median = ordered[len(ordered) // 2]
+        t.low = ordered[0]
+        deviations = sorted(abs(x - t.median) for x in ordered)
+        t.mad = deviations[len(deviations) // 2] / t.median if t.median > 0 else 0.0
+        t.samples = len(ordered)
+        return t
+
+
+# Samples a graph-replayed workload is timed over (the reference harness
+# takes 15, benches/nn_ops.rs).
+SAMPLES = 15
 
 _hip = None
 
@@ -114,21 +127,80 @@ def _hip_runtime() -> ctypes.CDLL:
         _hip.hipGraphLaunch.argtypes = [vp, vp]
         _hip.hipGraphExecDestroy.argtypes = [vp]
         _hip.hipGraphDestroy.argtypes = [vp]
+        _hip.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        _hip.hipEventRecord.argtypes = [vp, vp]
+        _hip.hipEventSynchronize.argtypes = [vp]
+        _hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        _hip.hipEventDestroy.argtypes = [vp]
     return _hip
 
 
-def timed_graph(fn, steps: int, warmup: int) -> float:
-    """Milliseconds per call of `fn`, with the `steps` calls captured into one
-    HIP graph on the library's stream and the graph's replay timed by HIP
-    events on that stream: the kernels run back to back, as they would from
-    a compiled caller, rather than paced by this script's per-call overhead.
-    Falls back to `timed` if the stream cannot be captured."""
+def _stream() -> ctypes.c_void_p:
+    stream = ctypes.c_void_p()
+    lib.call("tc_stream", ctypes.byref(stream))
+    return stream
+
+
+class _Marks:
+    """HIP events recorded on the library's stream (the stream every kernel
+    is launched on): mark i is recorded after the i-th timed unit."""
+
+    def __init__(self, count: int):
+        self.hip, self.stream = _hip_runtime(), _stream()
+        self.events = []
+        for _ in range(count):
+            event = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(event)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self.events.append(event)
+
+    def record(self, i: int) -> None:
+        if self.hip.hipEventRecord(self.events[i], self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def between(self, i: int, j: int) -> float:
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), self.events[i], self.events[j]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def finish(self) -> None:
+        self.hip.hipEventSynchronize(self.events[-1])
+        lib.sync()
+        for event in self.events:
+            self.hip.hipEventDestroy(event)
+
+
+def timed(fn, steps: int, warmup: int) -> Timing:
+    """`fn` called `warmup` times untimed, then exactly `steps` times between
+    HIP events on the library's stream, with the stream synchronised before
+    and after; an event after every call makes each call one sample."""
     for _ in range(warmup):
         fn()
     lib.sync()
-    hip = _hip_runtime()
-    stream = ctypes.c_void_p()
-    lib.call("tc_stream", ctypes.byref(stream))
+    marks = _Marks(steps + 1)
+    marks.record(0)
+    for i in range(steps):
+        fn()
+        marks.record(i + 1)
+    marks.hip.hipEventSynchronize(marks.events[-1])
+    samples = [marks.between(i, i + 1) for i in range(steps)]
+    total = marks.between(0, steps)
+    marks.finish()
+    return Timing.of(total / steps, samples)
+
+
+def timed_graph(fn, steps: int, warmup: int) -> Timing:
+    """Milliseconds per call of `fn`, with `steps` calls captured into one
+    HIP graph on the library's stream and the graph replayed SAMPLES times
+    between HIP events on that stream, each replay one sample: the kernels
+    run back to back, as they would from a compiled caller, rather than
+    paced by this script's per-call overhead.  Falls back to `timed` if the
+    stream cannot be captured."""
+    for _ in range(warmup):
+        fn()
+    lib.sync()
+    hip, stream = _hip_runtime(), _stream()
     graph, graph_exec = ctypes.c_void_p(), ctypes.c_void_p()
     if hip.hipStreamBeginCapture(stream, 2) != 0:  # hipStreamCaptureModeRelaxed
         return timed(fn, steps, 0)
@@ -139,17 +211,21 @@ def timed_graph(fn, steps: int, warmup: int) -> float:
         return timed(fn, steps, 0)
     hip.hipGraphLaunch(graph_exec, stream)  # one untimed replay
     lib.sync()
-    lib.call("tc_timer_begin")
-    hip.hipGraphLaunch(graph_exec, stream)
-    ms = ctypes.c_float()
-    lib.call("tc_timer_end", ctypes.byref(ms))
-    lib.sync()
+    marks = _Marks(SAMPLES + 1)
+    marks.record(0)
+    for i in range(SAMPLES):
+        hip.hipGraphLaunch(graph_exec, stream)
+        marks.record(i + 1)
+    hip.hipEventSynchronize(marks.events[-1])
+    samples = [marks.between(i, i + 1) / steps for i in range(SAMPLES)]
+    total = marks.between(0, SAMPLES)
+    marks.finish()
     hip.hipGraphExecDestroy(graph_exec)
     hip.hipGraphDestroy(graph)
     # The graph is gone: the storage its captured calls used may serve
     # eager work again.
     lib.call("tc_release_graph_memory")
-    return ms.value / steps
+    return Timing.of(total / (SAMPLES * steps), samples)
 
 
 def host_matrix(kind: str, rows: int, cols: int, rng, sigma=None) -> np.ndarray:
@@ -199,13 +275,16 @@ class Product:
         self.a_host = self.b_host = None
         return {
             "workload": f"{kind} GEMM {m}x{k}x{n}",
+            "key": f"gemm {kind} {m}x{k}x{n}",
+            "spread": spread(ms),
             "cpu_baseline": baseline,
             "value": flops / (ms * 1e-3) / 1e12,
             "unit": "TFLOP/s",
             "ms": ms,
             "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind], "unit": "TFLOP/s",
                          "frac": achieved / MFMA_PEAK[kind],
-                         "traffic": MEASURED_TRAFFIC.get(f"{kind} GEMM {m}x{k}x{n}"), "kernel_ms": kernel_ms},
+                         "traffic": MEASURED_TRAFFIC.get(f"{kind} GEMM {m}x{k}x{n}"), "kernel_ms": kernel_ms,
+                         "bytes": (m * k + k * n + m * n) * (4 if kind == "f32" else 2)},
         }
 
 
@@ -259,11 +338,13 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
                         f"rows 0..{band} of x: the oracle's single-thread product, then the program, linear in M",
                         1e12, min_seconds=1.0)
     lines = []
-    for name, fn in (("in the product's epilogue", fused), ("unfused: product, then program", unfused),
-                     ("the product alone", product_only)):
+    for name, short, fn in (("in the product's epilogue", "epilogue", fused),
+                            ("unfused: product, then program", "unfused", unfused),
+                            ("the product alone", "product", product_only)):
         ms = timed(fn, steps, warmup)
         achieved = flops / (ms * 1e-3) / 1e12
         lines.append({"workload": f"{kind} dense layer relu(x w + b) {m}x{k}x{n}, {name}",
+                      "key": f"dense {kind} {m}x{k}x{n} {short}", "spread": spread(ms),
                       "value": achieved, "unit": "TFLOP/s", "ms": ms,
                       "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind],
                                    "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK[kind], "traffic": None},
@@ -330,11 +411,11 @@ def layer_norm(rows: int, cols: int, steps: int, warmup: int) -> list[dict]:
     baseline = cpu_rate(cpu, 8.0 * band * cols, "GB/s",
                         f"rows 0..{band}: the oracle's row moments, then its program, one thread", 1e9)
     lines = []
-    for name, fn in (("statistics and program in one kernel", one_kernel),
-                     ("composed: row moments, then the program", composed)):
+    for name, short, fn in (("statistics and program in one kernel", "1 kernel", one_kernel),
+                            ("composed: row moments, then the program", "composed", composed)):
         ms = timed_graph(rotating(xs, fn), steps, warmup)
         lines.append(with_cpu(hbm_line(f"layer norm f32 [{rows}x{cols}] (fused_with_statistics), {name}",
-                                       2.0 * nbytes, ms), baseline))
+                                       2.0 * nbytes, ms, f"layernorm {short}"), baseline))
     for buffer in xs + [gamma, out, means, devs]:
         buffer.free()
     return lines
@@ -369,20 +450,21 @@ def transfers() -> list[dict]:
             best = min(best, time.perf_counter() - start)
         return best * 1e3
 
-    def line(workload, ms):
+    def line(workload, ms, key):
         gbs = nbytes / (ms * 1e-3) / 1e9
-        return {"workload": workload, "value": gbs, "unit": "GB/s", "ms": ms,
+        return {"workload": workload, "key": key, "value": gbs, "unit": "GB/s", "ms": ms,
                 "roofline": {"bound": "pcie", "achieved": gbs, "peak": PCIE_PEAK, "unit": "GB/s",
                              "frac": gbs / PCIE_PEAK, "traffic": None}}
 
     lines = [
-        line("upload 1 GiB pageable, runtime copy", wall(lambda: lib.call("tc_upload", dev.ptr, host.ctypes.data, nbytes))),
+        line("upload 1 GiB pageable, runtime copy", wall(lambda: lib.call("tc_upload", dev.ptr, host.ctypes.data, nbytes)),
+             "upload runtime"),
         line("upload 1 GiB pageable, pinned staging",
-             wall(lambda: lib.call("tc_upload_staged", dev.ptr, host.ctypes.data, nbytes))),
+             wall(lambda: lib.call("tc_upload_staged", dev.ptr, host.ctypes.data, nbytes)), "upload staged"),
         line("download 1 GiB pageable, runtime copy",
-             wall(lambda: lib.call("tc_download", back.ctypes.data, dev.ptr, nbytes))),
+             wall(lambda: lib.call("tc_download", back.ctypes.data, dev.ptr, nbytes)), "download runtime"),
         line("download 1 GiB pageable, pinned staging",
-             wall(lambda: lib.call("tc_download_staged", back.ctypes.data, dev.ptr, nbytes))),
+             wall(lambda: lib.call("tc_download_staged", back.ctypes.data, dev.ptr, nbytes)), "download staged"),
     ]
     with tempfile.TemporaryDirectory() as folder:
         path = os.path.join(folder, "x.tcr")
@@ -392,14 +474,22 @@ def transfers() -> list[dict]:
         h = lib.Tcr1()
         lib.call("tc_tcr1_read_header", path.encode(), 0, tag, len(tag), tcr1.VECTOR, ctypes.byref(h))
         lines.append(line("TCR1 record of 1 GiB, page-cached file to HBM",
-                          wall(lambda: lib.call("tc_tcr1_load", path.encode(), ctypes.byref(h), dev.ptr))))
+                          wall(lambda: lib.call("tc_tcr1_load", path.encode(), ctypes.byref(h), dev.ptr)), "tcr1 load"))
     dev.free()
     return lines
 
 
-def hbm_line(workload: str, nbytes: float, ms: float) -> dict:
+def spread(ms) -> dict | None:
+    """The samples' median, minimum and MAD (a fraction of the median) of a
+    `Timing`, as the reference harness reports them."""
+    if not isinstance(ms, Timing):
+        return None
+    return {"samples": ms.samples, "median_ms": ms.median, "min_ms": ms.low, "mad": ms.mad}
+
+
+def hbm_line(workload: str, nbytes: float, ms: float, key: str) -> dict:
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"workload": workload, "value": gbs, "unit": "GB/s", "ms": ms,
+    return {"workload": workload, "key": key, "value": gbs, "unit": "GB/s", "ms": ms, "spread": spread(ms),
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK, "unit": "GB/s", "frac": gbs / HBM_PEAK,
                          "traffic": MEASURED_TRAFFIC.get(workload)}}
 
@@ -425,30 +515,45 @@ CPU_MODEL, NPROC = _host_cpu()
 DEFERRED: list = []
 
 
-def cpu_rate(fn, work: float, unit: str, sample: str, scale: float, min_seconds: float = 0.4) -> dict:
-    """The oracle's C restatement of the Host (simd) algorithm (one thread)
-    run on this host: `fn` does `work` units of the line's metric per call;
-    called until `min_seconds` pass after one untimed call, the rate is
-    work x calls / seconds / `scale`.  Returns the line's record, filled in
-    by `run_cpu_baselines`."""
-    record = {"value": None, "unit": unit, "cores": 1, "kind": "port", "sample": sample, "cpu": CPU_MODEL,
+# Threads for the Host paths that split over every core: the host's CPUs,
+# at most the 16 a one-GPU box's share holds.
+HOST_THREADS = max(1, min(NPROC, 16))
+
+
+def cpu_rate(fn, work: float, unit: str, sample: str, scale: float, min_seconds: float = 0.4,
+             chunks: int = 0) -> dict:
+    """The oracle's C restatement of the Host (simd) algorithm run on this
+    host: `fn` does `work` units of the line's metric per call; called until
+    `min_seconds` pass after one untimed call, the rate is work x calls /
+    seconds / `scale`.  With `chunks`, a call is `fn(i)` for every chunk i,
+    spread over HOST_THREADS threads (the oracle's C calls release the
+    interpreter's lock), as the Host splits its elementwise kernels and its
+    fused interpreter over every core (parallel.rs:1-14, simd_dispatch.rs:54-75,
+    fused/mod.rs:4255-4290).  Returns the line's record, filled in by
+    `run_cpu_baselines`."""
+    threads = HOST_THREADS if chunks else 1
+    record = {"value": None, "unit": unit, "cores": threads, "kind": "port", "sample": sample, "cpu": CPU_MODEL,
               "nproc": NPROC}
-    DEFERRED.append((record, fn, work, scale, min_seconds))
+    DEFERRED.append((record, fn, work, scale, min_seconds, chunks))
     return record
 
 
 def run_cpu_baselines() -> None:
-    while DEFERRED:
-        record, fn, work, scale, min_seconds = DEFERRED.pop(0)
-        fn()
-        calls, start = 0, time.perf_counter()
-        while True:
-            fn()
-            calls += 1
-            elapsed = time.perf_counter() - start
-            if elapsed >= min_seconds:
-                break
-        record["value"] = work * calls / elapsed / scale
+    from concurrent.futures import ThreadPoolExecutor
+
+    with ThreadPoolExecutor(HOST_THREADS) as pool:
+        while DEFERRED:
+            record, fn, work, scale, min_seconds, chunks = DEFERRED.pop(0)
+            call = (lambda: list(pool.map(fn, range(chunks)))) if chunks else fn
+            call()
+            calls, start = 0, time.perf_counter()
+            while True:
+                call()
+                calls += 1
+                elapsed = time.perf_counter() - start
+                if elapsed >= min_seconds:
+                    break
+            record["value"] = work * calls / elapsed / scale
 
 
 def with_cpu(line: dict, baseline: dict) -> dict:
@@ -486,7 +591,8 @@ def launch_floor(steps: int, warmup: int) -> dict:
     dst.free()
     us = ms * 1e3
     ceiling = (32 << 20) / ((32 << 20) / (HBM_PEAK * 1e9) + us * 1e-6) / 1e9
-    return {"workload": "launch floor: a one-element copy, graph-replayed", "value": us, "unit": "us/launch",
+    return {"workload": "launch floor: a one-element copy, graph-replayed", "key": "launch floor", "value": us,
+            "unit": "us/launch", "spread": spread(ms),
             "higher_is_better": False, "ms": ms,
             "roofline": {"bound": "launch", "achieved": None, "peak": None, "unit": "GB/s", "frac": None,
                          "traffic": None, "ceiling_32MiB_GBps": ceiling},
@@ -502,6 +608,7 @@ def reductions(shape, seed: int, steps: int, warmup: int) -> list[dict]:
     xs = rotation(lambda: Tensor.from_numpy(host), 4 * n)
     lines = []
     tag = "x".join(map(str, shape))
+    size = f"{4 * n >> 20}M"
     # The CPU baseline folds a leading slab of at most 8 Mi elements with the
     # same axes: the Host walk costs the same per element at any size.
     slab_rows = max(1, min(shape[0], (8 << 20) // (shape[1] * shape[2])))
@@ -516,7 +623,8 @@ def reductions(shape, seed: int, steps: int, warmup: int) -> list[dict]:
                                 ("sum", [0, 1], shape[2]), ("max", [0, 1], shape[2]), ("var", [0, 1], shape[2])]:
         fn = rotating(xs, lambda x: getattr(x, f"{name}_axes")(axes))
         ms = timed_graph(fn, max(steps, 2 * len(xs)), warmup)
-        line = hbm_line(f"{name}_axes {axes} of f32 [{tag}]", 4 * (n + results), ms)
+        line = hbm_line(f"{name}_axes {axes} of f32 [{tag}]", 4 * (n + results), ms,
+                        f"{name}[{','.join(map(str, axes))}] {size}")
         depth = int(np.prod([slab_shape[a] for a in axes]))
         kind, op, divisor = fold_code.get(name, (lib.MEAN if name == "mean" else lib.VARIANCE, 0,
                                                  0 if name == "mean" else depth))
@@ -528,7 +636,7 @@ def reductions(shape, seed: int, steps: int, warmup: int) -> list[dict]:
     for name, op in (("argmax", lib.RMAX), ("argmin", lib.RMIN)):
         fn = rotating(xs, lambda x: getattr(x, name)(1))
         ms = timed_graph(fn, max(steps, 2 * len(xs)), warmup)
-        line = hbm_line(f"{name} axis 1 of f32 [{tag}]", 4 * n + 4 * (n // shape[1]), ms)
+        line = hbm_line(f"{name} axis 1 of f32 [{tag}]", 4 * n + 4 * (n // shape[1]), ms, f"{name}[1] {size}")
         work = 4.0 * slab.size + 4.0 * (slab.size // shape[1])
         lines.append(with_cpu(line, cpu_rate(
             lambda: oracle.arg_reduce(lib.F32, slab, slab_shape, 0, strides, 1, op), work, "GB/s", sample, 1e9)))
@@ -554,19 +662,19 @@ def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
     slab = f"the oracle's Host walk over the leading [{rows},512,512] slab"
     lines = []
     ms = timed_graph(lambda: x * y, steps, warmup)
-    lines.append(with_cpu(hbm_line("x*y, f32 [256,512,512] x [1,512,1]", 2 * mib + 4 * 512, ms), cpu_rate(
+    lines.append(with_cpu(hbm_line("x*y, f32 [256,512,512] x [1,512,1]", 2 * mib + 4 * 512, ms, "x*y"), cpu_rate(
         lambda: oracle.binary(lib.F32, lib.ARITHMETIC, lib.MUL, [rows, 512, 512], sx, 0, [262144, 512, 1], hy, 0,
                               [0, 1, 0]), 8.0 * sn + 4 * 512, "GB/s", slab + " (strided.rs:29-78)", 1e9)))
     t = x * y
     st = np.ascontiguousarray(t.to_numpy()[:rows])
     ms = timed_graph(lambda: t + z, steps, warmup)
-    lines.append(with_cpu(hbm_line("t+z, f32 [256,512,512] + [256,1,512]", 2 * mib + 4 * 256 * 512, ms), cpu_rate(
+    lines.append(with_cpu(hbm_line("t+z, f32 [256,512,512] + [256,1,512]", 2 * mib + 4 * 256 * 512, ms, "t+z"), cpu_rate(
         lambda: oracle.binary(lib.F32, lib.ARITHMETIC, lib.ADD, [rows, 512, 512], st, 0, [262144, 512, 1], sz, 0,
                               [512, 0, 1]), 8.0 * sn + 4 * rows * 512, "GB/s", slab + " (strided.rs:29-78)", 1e9)))
     out = t + z
     so = np.ascontiguousarray(out.to_numpy()[:rows])
     ms = timed_graph(lambda: out.permute([0, 2, 1]).contiguous(), steps, warmup)
-    lines.append(with_cpu(hbm_line("permute(0,2,1).contiguous, f32 [256,512,512]", 2 * mib, ms), cpu_rate(
+    lines.append(with_cpu(hbm_line("permute(0,2,1).contiguous, f32 [256,512,512]", 2 * mib, ms, "permute"), cpu_rate(
         lambda: oracle.strided_copy(so, [rows, 512, 512], 0, [262144, 1, 512]), 8.0 * sn, "GB/s",
         slab + " (backend.rs:255-274)", 1e9)))
     p = out.permute([0, 2, 1]).contiguous()
@@ -574,7 +682,7 @@ def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
     # The slice reads 128 MiB, which the Infinity Cache could hold: rotate.
     sources = rotation(lambda: out.permute([0, 2, 1]).contiguous(), mib // 2)
     ms = timed_graph(rotating(sources, lambda q: q.slice(1, 128, 384).contiguous()), steps, warmup)
-    lines.append(with_cpu(hbm_line("slice [:,128:384,:].contiguous, f32", mib, ms), cpu_rate(
+    lines.append(with_cpu(hbm_line("slice [:,128:384,:].contiguous, f32", mib, ms, "slice"), cpu_rate(
         lambda: oracle.strided_copy(sp, [rows, 256, 512], 128 * 512, [262144, 512, 1]), 4.0 * sn, "GB/s",
         slab + " (backend.rs:255-274)", 1e9)))
     del sources
@@ -588,16 +696,21 @@ def broadcast_and_copies(steps: int, warmup: int) -> list[dict]:
             oracle.strided_write(sp, target, [rows, 256, 512], half * 256 * 512, [262144, 512, 1], half * 256 * 512,
                                  [262144, 512, 1])
         return target
-    lines.append(with_cpu(hbm_line("concat of two [256,256,512] halves on axis 1, f32", 2 * mib, ms), cpu_rate(
+    lines.append(with_cpu(hbm_line("concat of two [256,256,512] halves on axis 1, f32", 2 * mib, ms, "concat"), cpu_rate(
         assemble_slab, 8.0 * sn, "GB/s", slab + " (backend.rs:303-323)", 1e9)))
     a, b = x.storage, t.storage
     dst = lib.Buffer(mib)
     ms = timed_graph(lambda: lib.call("tc_elementwise", lib.F32, lib.ADD, a.ptr, b.ptr, dst.ptr, n), steps, warmup)
     ea, eb = sx.reshape(-1), st.reshape(-1)
-    lines.append(with_cpu(hbm_line("same-shape add, f32 64 Mi elements", 3 * mib, ms), cpu_rate(
-        lambda: oracle.elementwise(lib.F32, lib.ARITHMETIC, lib.ADD, ea, eb), 12.0 * sn, "GB/s",
-        f"the oracle's elementwise loop over {sn} elements, one thread (the Host splits this over all cores, "
-        "simd_dispatch.rs:54-75)", 1e9)))
+    # The Host splits a same-shape kernel into windows over every core
+    # (simd_dispatch.rs:54-75; four chunks a thread, parallel.rs:28).
+    pieces = 4 * HOST_THREADS
+    bounds = [sn * i // pieces for i in range(pieces + 1)]
+    lines.append(with_cpu(hbm_line("same-shape add, f32 64 Mi elements", 3 * mib, ms, "add"), cpu_rate(
+        lambda i: oracle.elementwise(lib.F32, lib.ARITHMETIC, lib.ADD, ea[bounds[i]:bounds[i + 1]],
+                                     eb[bounds[i]:bounds[i + 1]]), 12.0 * sn, "GB/s",
+        f"the oracle's elementwise loop over {sn} elements in {pieces} windows on {HOST_THREADS} threads "
+        "(simd_dispatch.rs:54-75)", 1e9, chunks=pieces)))
     return lines
 
 
@@ -620,13 +733,13 @@ def vector_products(steps: int, warmup: int) -> list[dict]:
     lines = []
     ms = timed_graph(rotating(mats, lambda m: lib.call("tc_matvec", lib.F32, 0, rows, cols, m.ptr, v.ptr, y.ptr)),
                      max(steps, 2 * len(mats)), warmup)
-    lines.append(with_cpu(hbm_line(f"matvec, f32 [{rows}x{cols}] . [{cols}]", mbytes + 4 * (rows + cols), ms),
+    lines.append(with_cpu(hbm_line(f"matvec, f32 [{rows}x{cols}] . [{cols}]", mbytes + 4 * (rows + cols), ms, "matvec"),
                           cpu_rate(lambda: oracle.matvec(lib.F32, hb, hv), 4.0 * (band * cols + band + cols), "GB/s",
                                    sample + " (simd_dispatch.rs:626-659)", 1e9)))
     ms = timed_graph(rotating(mats, lambda m: lib.call("tc_vecmat", lib.F32, rows, cols, v.ptr, m.ptr, y.ptr)),
                      max(steps, 2 * len(mats)), warmup)
     hw = np.ascontiguousarray(hv[:band])
-    lines.append(with_cpu(hbm_line(f"vecmat, f32 [{rows}] . [{rows}x{cols}]", mbytes + 4 * (rows + cols), ms),
+    lines.append(with_cpu(hbm_line(f"vecmat, f32 [{rows}] . [{rows}x{cols}]", mbytes + 4 * (rows + cols), ms, "vecmat"),
                           cpu_rate(lambda: oracle.vecmat(lib.F32, hw, hb), 4.0 * (band * cols + band + cols), "GB/s",
                                    sample + " (vector.rs:491)", 1e9)))
     del mats
@@ -636,7 +749,7 @@ def vector_products(steps: int, warmup: int) -> list[dict]:
     result = lib.Buffer(4)
     ms = timed_graph(lambda: lib.call("tc_dot", lib.F32, a.ptr, b.ptr, n, result.ptr), steps, warmup)
     da, db = np.ascontiguousarray(ha[: 8 << 20]), np.ascontiguousarray(hb2[: 8 << 20])
-    lines.append(with_cpu(hbm_line("dot, f32 64 Mi elements", 8 * n, ms),
+    lines.append(with_cpu(hbm_line("dot, f32 64 Mi elements", 8 * n, ms, "dot"),
                           cpu_rate(lambda: oracle.dot(lib.F32, da, db), 8.0 * da.size, "GB/s",
                                    "the oracle's eight-lane AVX2 dot (simd_x86.rs:57-101) over the first 8 Mi pairs",
                                    1e9)))
@@ -648,7 +761,7 @@ def vector_products(steps: int, warmup: int) -> list[dict]:
     dst = lib.Buffer(tbytes)
     ms = timed_graph(rotating(srcs, lambda m: lib.call("tc_transpose", 4, side, side, m.ptr, dst.ptr)),
                      max(steps, 2 * len(srcs)), warmup)
-    lines.append(with_cpu(hbm_line(f"transpose, f32 [{side}x{side}]", 2 * tbytes, ms),
+    lines.append(with_cpu(hbm_line(f"transpose, f32 [{side}x{side}]", 2 * tbytes, ms, "transpose"),
                           cpu_rate(lambda: oracle.transpose(first), 2.0 * tbytes, "GB/s",
                                    f"the oracle's transpose of the whole [{side}x{side}] matrix, one thread "
                                    "(the Host blocks 32 x 32 over all cores, matrix.rs:1173-1206)", 1e9)))
@@ -686,6 +799,7 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
                         "AVX2 i-p-j f32 product, its rate divided by the step's 618.5 GFLOP", flops, min_seconds=1.0)
     del weights, biases, x, y
     lines = [{"workload": "MLP training step 1024-4096-4096-1024, batch 4096, f32, tape + Adam (configs[4])",
+              "key": "mlp step", "spread": spread(ms),
               "value": 1e3 / ms, "unit": "steps/s", "ms": ms,
               "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK["f32"], "unit": "TFLOP/s",
                            "frac": achieved / MFMA_PEAK["f32"], "traffic": None},
@@ -702,15 +816,26 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
     # keeps its own step's constants, and the replay times the kernels back
     # to back rather than this script's per-step host work.
     ms = timed_graph(lambda: rule.update(params, grads, 1, n), steps, warmup)
-    sample_n = 1 << 20
+    # The CPU baseline: the oracle's interpreter over 8 Mi parameters, split
+    # into windows over every core as the Host's tile interpreter splits a
+    # program (fused/mod.rs:4255-4290).
+    sample_n = 8 << 20
+    pieces = 4 * HOST_THREADS
+    window = -(-sample_n // pieces)
     code, loads = adam_program(True, lib.F32, 1e-3, 0.9, 0.999, 1e-8, 2)
     hp = np.full(sample_n, 0.5, np.float32)
     hg, hm, hv = np.full(sample_n, 0.25, np.float32), np.zeros(sample_n, np.float32), np.zeros(sample_n, np.float32)
-    adam_places = [identity_place(1, sample_n)] * loads
-    lines.append(with_cpu(hbm_line(f"Adam update, {n} f32 parameters (fused program)", 7 * 4 * n, ms), cpu_rate(
-        lambda: oracle.fused(lib.F32, code, adam_places, [hg, hp, hm, hv], [hp, hm, hv], 1, sample_n),
-        7.0 * 4 * sample_n, "GB/s", f"the oracle's program interpreter over {sample_n} parameters, one thread "
-        "(the Host's tile interpreter splits over all cores, fused/mod.rs:4255-4290)", 1e9)))
+
+    def adam_window(i):
+        at = slice(i * window, min(sample_n, (i + 1) * window))
+        count = at.stop - at.start
+        if count > 0:
+            views = [a[at] for a in (hg, hp, hm, hv)]
+            oracle.fused(lib.F32, code, [identity_place(1, count)] * loads, views, views[1:], 1, count)
+    lines.append(with_cpu(hbm_line(f"Adam update, {n} f32 parameters (fused program)", 7 * 4 * n, ms, "adam"), cpu_rate(
+        adam_window, 7.0 * 4 * sample_n, "GB/s",
+        f"the oracle's program interpreter over {sample_n} parameters in {pieces} windows on {HOST_THREADS} threads "
+        "(fused/mod.rs:4255-4290)", 1e9, chunks=pieces)))
     return lines
 
 
@@ -962,27 +1087,69 @@ def main() -> int:
     for w in workloads:
         if w.get("cpu_baseline") is not None and w["cpu_baseline"]["value"] is None:
             w["cpu_baseline"] = None
-    line = {
+    # Every workload's full record goes to stderr as one JSON object; the
+    # last stdout line is the compact headline.
+    log("workloads: " + json.dumps(workloads))
+    line = headline_line(head, baseline, workloads, args.steps, args.warmup, f"{name} {arch}")
+    print(json.dumps(line, separators=(",", ":")), flush=True)
+    return 0
+
+
+# The fields of each entry of the headline line's "workloads" table.
+WORKLOAD_FIELDS = ["value", "unit", "frac", "traffic_ratio", "mad", "cpu"]
+
+
+def _round(value, digits=5):
+    return None if value is None else float(f"{value:.{digits}g}")
+
+
+def compact(line: dict) -> list:
+    """A workload as one row of the headline's table: value, unit, fraction
+    of its roofline, HBM traffic over algorithmic bytes, the samples' MAD as
+    a fraction of their median, and the CPU baseline's value."""
+    roof = line.get("roofline") or {}
+    ratio = None
+    if roof.get("traffic") and line.get("ms"):
+        if roof.get("unit") == "GB/s" and roof.get("achieved"):
+            ratio = roof["traffic"] / (roof["achieved"] * 1e9 * line["ms"] * 1e-3)
+        elif roof.get("bytes"):
+            ratio = roof["traffic"] / roof["bytes"]
+    cpu = line.get("cpu_baseline") or {}
+    return [_round(line["value"]), line["unit"], _round(roof.get("frac"), 3), _round(ratio, 3),
+            _round((line.get("spread") or {}).get("mad"), 2), _round(cpu.get("value"), 3)]
+
+
+def headline_line(head: dict, baseline: dict | None, workloads: list[dict], steps: int, warmup: int,
+                  device: str) -> dict:
+    """The one JSON line the driver reads: BASELINE.json's metric on the bf16
+    8192^3 product, its roofline and CPU baseline, and every other workload
+    as a compact row keyed by a short name (full records go to stderr)."""
+    roof = {k: (_round(v) if isinstance(v, float) else v) for k, v in head["roofline"].items()}
+    roof["traffic"] = HEADLINE_TRAFFIC
+    cpu = None
+    if baseline is not None:
+        cpu = {k: (_round(v) if isinstance(v, float) else v) for k, v in baseline.items()}
+    return {
         "metric": METRIC,
-        "value": head["value"],
+        "value": _round(head["value"], 5),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": head["ms"],
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": _round(head["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: A, B ~ N(0, 1/sqrt(K)) bf16, seed 3, numpy PCG64",
         "config": {"workload": "dense GEMM bf16 M=N=K=8192, f32 accumulate, bf16 out (configs[3])",
-                   "m": m, "n": n, "k": k, "device": f"{name} {arch}"},
-        "roofline": {**head["roofline"], "traffic": HEADLINE_TRAFFIC},
-        "cpu_baseline": baseline,
-        "workloads": workloads,
+                   "m": 8192, "n": 8192, "k": 8192, "device": device},
+        "spread": {k: (_round(v) if isinstance(v, float) else v) for k, v in (head.get("spread") or {}).items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "workload_fields": WORKLOAD_FIELDS,
+        "workloads": {w["key"]: compact(w) for w in workloads},
     }
-    print(json.dumps(line), flush=True)
-    return 0
 
 
 if __name__ == "__main__":

@@ -381,8 +381,11 @@ int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, flo
  * f32, enough for any length on parts of up to 1024 CUs; more partials are
  * refused with TC_UNSUPPORTED).  No counterpart in the reference: it is for
  * callers that cannot allocate (code under HIP graph capture, tight serving
- * loops).  Every call on one GPU shares that array, so calls that overlap in
- * time on one GPU (other streams or threads) race. */
+ * loops).  Every call on one GPU shares that array, which belongs to the
+ * stream of the last call that used it: a call from another stream while
+ * that call is still queued is refused with TC_UNSUPPORTED instead of
+ * racing.  Replays of a captured call are not tracked, so a graph holding
+ * one must not replay beside other users of the array on that GPU. */
 int tc_vector_reduce_noalloc(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result);
 
 /* `Kernels::vector_moments` / `matrix_moments` (kernels.rs:1035-1038; Host
@@ -574,6 +577,16 @@ int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, c
  * reference's interface: a diagnostic in the manner of its `counters`
  * feature (counters.rs:1-110), for tests and profiling. */
 int tc_fused_compiled(uint64_t* count);
+
+/* Programs beyond what kernel arguments carry (more than 48 instructions or
+ * 8 places) run from a device copy kept for the process, keyed by their
+ * bytes, up to a limit (4096 by default); past it an uncaptured run uploads
+ * its program into a block of its own, freed once its kernel is queued, and
+ * a captured run of a program not yet resident is refused.  Reports how many
+ * are resident and the limit in force, after setting it to `limit` if that
+ * is not 0 (lowering it keeps what is resident).  No counterpart in the
+ * reference's interface: a diagnostic and tuning hook, for tests. */
+int tc_fused_resident(uint64_t limit, uint64_t* resident, uint64_t* current_limit);
 
 #ifdef __cplusplus
 }

@@ -55,7 +55,6 @@ _SIGNATURES = {
     "or_dot": ([u32, vp, vp, u64], f32),
     "or_matvec": ([u32, vp, vp, u64, u64, vp, i32], None),
     "or_vecmat": ([u32, vp, vp, u64, u64, vp], None),
-    "or_fold": ([u32, vp, u64, u32], f32),
     "or_fused": ([u32, vp, u32, vp, vp, vp, u64, u64], None),
     "or_row_moments": ([u32, u32, vp, vp, u64, u64, vp, vp], None),
     "or_unary": ([u32, u32, vp, vp, u64], None),
@@ -245,11 +244,6 @@ def vecmat(dtype, v, m) -> np.ndarray:
     out = np.empty(cols, NUMPY[dtype])
     load().or_vecmat(dtype, _p(v), _p(m), rows, cols, _p(out))
     return out
-
-
-def fold(dtype, a, op) -> float:
-    a = np.ascontiguousarray(a)
-    return load().or_fold(dtype, _p(a), a.size, op)
 
 
 def _program(code, places):

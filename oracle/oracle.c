@@ -702,15 +702,6 @@ void or_vecmat(uint32_t dtype, const void* v, const void* m, uint64_t rows, uint
     }
 }
 
-float or_fold(uint32_t dtype, const void* a, uint64_t n, uint32_t op) {
-    float t = op == 0 ? 0.0f : (op == 1 ? INFINITY : -INFINITY);
-    for (uint64_t i = 0; i < n; i++) {
-        float x = widen_one(dtype, a, i);
-        t = op == 0 ? t + x : (op == 1 ? fminf(t, x) : fmaxf(t, x));
-    }
-    return t;
-}
-
 /* ---- fused programs (fused/mod.rs:62-70, :3254-3268) ------------------------ */
 
 static uint64_t place_at(const or_place* p, uint64_t row, uint64_t col) {

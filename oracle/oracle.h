@@ -88,10 +88,6 @@ void or_matvec(uint32_t dtype, const void* m, const void* v, uint64_t rows, uint
                int accumulate);
 void or_vecmat(uint32_t dtype, const void* v, const void* m, uint64_t rows, uint64_t cols, void* out);
 
-/* `Reduce::fold` over a whole vector: sequential f32 fold (kernels.rs:219-226,
- * compact.rs:202-206). */
-float or_fold(uint32_t dtype, const void* a, uint64_t n, uint32_t op);
-
 /* One instruction of a fused program (`Encoded`, fused/mod.rs:1402-1410). */
 typedef struct or_encoded {
     uint16_t kind;

@@ -318,18 +318,81 @@ struct Compiled {
 
 // Programs too large for kernel arguments, resident on the device for the
 // process by their bytes (the host copy is kept beside each, the source of
-// its one upload).  A program first seen while the stream is being captured
-// is refused: its upload would be a node of the graph reading host memory.
+// its one upload), up to `resident_limit` of them.  A program first seen
+// while the stream is being captured is refused: its upload would be a node
+// of the graph reading host memory.  Past the limit, an uncaptured run
+// uploads its program into a stream-ordered block of its own, freed once the
+// kernel is queued (`transient_program`), so a stream of distinct programs
+// (new shapes, offsets or constants each call) keeps running and holds no
+// device memory beyond the limit's.
 struct ResidentProgram {
     std::string host;
     void* device = nullptr;
 };
 std::mutex resident_mutex;
 std::unordered_map<std::string, ResidentProgram> resident_programs;
-constexpr size_t kResidentPrograms = 4096;
+size_t resident_limit = 4096;
 
-int resident_program(const std::string& key, hipStream_t s, void** device) {
+// Host copies of transient uploads, each kept until the event recorded
+// after its copy has passed: the copy reads host memory when the stream
+// reaches it, not when it is queued.  Never destroyed (the process's end
+// releases it), so no thread's exit races another's upload.
+struct PendingUpload {
+    hipEvent_t done;
+    std::string host;
+};
+std::vector<PendingUpload>* pending_uploads = new std::vector<PendingUpload>();
+
+void release_finished_uploads() {
+    auto& pending = *pending_uploads;
+    size_t kept = 0;
+    for (size_t i = 0; i < pending.size(); i++) {
+        const hipError_t state = hipEventQuery(pending[i].done);
+        if (state == hipSuccess) {
+            (void)hipEventDestroy(pending[i].done);
+            continue;
+        }
+        if (state != hipErrorNotReady) (void)hipGetLastError();
+        if (kept != i) pending[kept] = std::move(pending[i]);
+        kept++;
+    }
+    pending.resize(kept);
+}
+
+// `key` uploaded into a block from the thread's stream-ordered cache, which
+// the caller frees with `tc_free` once its kernel is queued.
+int transient_program(const std::string& key, hipStream_t s, void** device) {
+    release_finished_uploads();
+    int status = tc_alloc(key.size(), device);
+    if (status != TC_OK) return status;
+    PendingUpload upload{nullptr, key};
+    hipError_t error = hipEventCreateWithFlags(&upload.done, hipEventDisableTiming);
+    if (error == hipSuccess) {
+        count_dispatch();
+        error = hipMemcpyAsync(*device, upload.host.data(), key.size(), hipMemcpyHostToDevice, s);
+        if (error == hipSuccess) error = hipEventRecord(upload.done, s);
+    }
+    if (error != hipSuccess) {
+        (void)hipGetLastError();
+        if (upload.done != nullptr) {
+            // The copy may have been queued before the record failed: wait
+            // for the stream before the host copy goes.
+            (void)hipStreamSynchronize(s);
+            (void)hipEventDestroy(upload.done);
+        }
+        tc_free(*device);
+        *device = nullptr;
+        return fail(TC_DEVICE, std::string("fused program upload: ") + hipGetErrorString(error));
+    }
+    pending_uploads->push_back(std::move(upload));
+    return TC_OK;
+}
+
+// The device copy of a large program: resident (`*transient` false) or, past
+// the limit, a transient block the caller frees after its launch.
+int resident_program(const std::string& key, hipStream_t s, void** device, bool* transient) {
     std::lock_guard<std::mutex> lock(resident_mutex);
+    *transient = false;
     auto found = resident_programs.find(key);
     if (found != resident_programs.end()) {
         *device = found->second.device;
@@ -342,9 +405,9 @@ int resident_program(const std::string& key, hipStream_t s, void** device) {
                                         " instructions or " + std::to_string(kInlinePlaces) +
                                         " places must run once before it is captured");
     }
-    if (resident_programs.size() >= kResidentPrograms) {
-        return fail(TC_UNSUPPORTED, "fused program: more than " + std::to_string(kResidentPrograms) +
-                                        " distinct large programs");
+    if (resident_programs.size() >= resident_limit) {
+        *transient = true;
+        return transient_program(key, s, device);
     }
     ResidentProgram entry;
     entry.host = key;
@@ -356,7 +419,15 @@ int resident_program(const std::string& key, hipStream_t s, void** device) {
     count_dispatch();
     auto placed = resident_programs.emplace(key, std::move(entry)).first;
     error = hipMemcpyAsync(placed->second.device, placed->second.host.data(), key.size(), hipMemcpyHostToDevice, s);
-    if (error != hipSuccess) return fail(TC_DEVICE, std::string("fused program upload: ") + hipGetErrorString(error));
+    if (error != hipSuccess) {
+        (void)hipGetLastError();
+        // The entry never held the program: drop it, so a later run of the
+        // same program uploads again rather than reading unwritten memory.
+        // The copy failed to queue, so nothing on the device reads the block.
+        (void)hipFree(placed->second.device);
+        resident_programs.erase(placed);
+        return fail(TC_DEVICE, std::string("fused program upload: ") + hipGetErrorString(error));
+    }
     *device = placed->second.device;
     return TC_OK;
 }
@@ -846,6 +917,7 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
     const bool inline_program = count <= static_cast<uint32_t>(kInlineCode) &&
                                 place_count <= static_cast<uint32_t>(kInlinePlaces);
     void* device = nullptr;
+    bool transient = false;
     const tc_encoded* dcode = nullptr;
     const DevicePlace* dplaces = nullptr;
     if (inline_program) {
@@ -855,12 +927,13 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
         // A larger program and its places travel in one block of device
         // memory, uploaded on the program's first sight and kept for the
         // process, keyed by its bytes: a later run, captured into a graph or
-        // not, reads it in place, and no copy or block belongs to one call.
+        // not, reads it in place.  Past the resident limit the block is this
+        // call's own, freed below once the kernel is queued.
         const size_t code_bytes = (count * sizeof(tc_encoded) + 15) / 16 * 16;
         std::string key(code_bytes + place_count * sizeof(DevicePlace), '\0');
         memcpy(&key[0], code, count * sizeof(tc_encoded));
         if (place_count) memcpy(&key[code_bytes], device_places.data(), place_count * sizeof(DevicePlace));
-        status = resident_program(key, s, &device);
+        status = resident_program(key, s, &device, &transient);
         if (status != TC_OK) return status;
         dcode = static_cast<const tc_encoded*>(device);
         dplaces = reinterpret_cast<const DevicePlace*>(static_cast<uint8_t*>(device) + code_bytes);
@@ -882,12 +955,23 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
         }
     }
 #undef TC_FUSED_LAUNCH
-    return check_launch("fused program");
+    status = check_launch("fused program");
+    // Stream order keeps a transient block alive until the kernel has run.
+    if (transient) tc_free(device);
+    return status;
 }
 
 extern "C" int tc_fused_compiled(uint64_t* count) {
     std::lock_guard<std::mutex> lock(compiled_mutex);
     *count = compiled_count;
+    return TC_OK;
+}
+
+extern "C" int tc_fused_resident(uint64_t limit, uint64_t* resident, uint64_t* current_limit) {
+    std::lock_guard<std::mutex> lock(resident_mutex);
+    if (limit != 0) resident_limit = static_cast<size_t>(limit);
+    if (resident != nullptr) *resident = resident_programs.size();
+    if (current_limit != nullptr) *current_limit = resident_limit;
     return TC_OK;
 }
 

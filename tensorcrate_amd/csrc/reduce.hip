@@ -899,19 +899,34 @@ int total(const void* a, const void* b, uint64_t n, float* result, const char* w
 // copy only through the address hipGetSymbolAddress gives for it with that
 // device current, looked up on the entry point's first call on the device
 // and kept; the array's name in host code is a host-side stand-in, never
-// passed to a kernel.  Calls on one GPU share the array: calls that overlap
-// in time (on different streams or threads) race on it.
+// passed to a kernel.
+//
+// Calls on one GPU share the array, so each GPU's copy has an owner: the
+// stream of the last call that used it, with an event recorded after that
+// call's kernels.  A call from another stream takes the array over only once
+// that event has passed; while the owner's last use is still queued the call
+// is refused (TC_UNSUPPORTED) rather than racing on the array.  The check,
+// the launch and the event's record are one step under a lock, so two
+// threads cannot both take the array over.  Replays of a captured call are
+// not tracked: a graph holding one must not replay beside eager calls or
+// other graphs holding one on that GPU.
+struct StaticPartials {
+    float* address = nullptr;
+    hipEvent_t last_use = nullptr;
+    hipStream_t owner = nullptr;
+};
 
 std::mutex scratch_mutex;
-std::unordered_map<int, float*> scratch_by_device;
+std::unordered_map<int, StaticPartials> scratch_by_device;
 
-int static_partials(float** out) {
+// The device's array, set up on its first call there; `scratch_mutex` held.
+int static_partials(StaticPartials** out) {
     int device = -1;
     hipError_t error = hipGetDevice(&device);
     if (error != hipSuccess) return fail(TC_DEVICE, std::string("vector_reduce_noalloc: ") + hipGetErrorString(error));
-    std::lock_guard<std::mutex> lock(scratch_mutex);
     auto found = scratch_by_device.find(device);
     if (found == scratch_by_device.end()) {
+        StaticPartials entry;
         void* address = nullptr;
         error = hipGetSymbolAddress(&address, HIP_SYMBOL(::scratch));
         if (error != hipSuccess || address == nullptr) {
@@ -919,9 +934,15 @@ int static_partials(float** out) {
             return fail(TC_DEVICE, std::string("vector_reduce_noalloc: the partials array of device ") +
                                        std::to_string(device) + ": " + hipGetErrorString(error));
         }
-        found = scratch_by_device.emplace(device, static_cast<float*>(address)).first;
+        entry.address = static_cast<float*>(address);
+        error = hipEventCreateWithFlags(&entry.last_use, hipEventDisableTiming);
+        if (error != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(TC_DEVICE, std::string("vector_reduce_noalloc: ") + hipGetErrorString(error));
+        }
+        found = scratch_by_device.emplace(device, entry).first;
     }
-    *out = found->second;
+    *out = &found->second;
     return TC_OK;
 }
 
@@ -933,10 +954,33 @@ int total_noalloc(const void* a, uint64_t n, float* result) {
         return fail(TC_UNSUPPORTED, "vector_reduce_noalloc: " + std::to_string(blocks) + " partials, over the " +
                                         std::to_string(kStaticPartials) + " the library holds");
     }
-    float* partial = nullptr;
-    int status = static_partials(&partial);
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    StaticPartials* partials = nullptr;
+    int status = static_partials(&partials);
     if (status != TC_OK) return status;
-    return total_into<S, OP, false>(a, nullptr, n, result, partial, "vector_reduce_noalloc", s);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &capture) != hipSuccess) (void)hipGetLastError();
+    if (partials->owner != nullptr && partials->owner != s) {
+        const hipError_t state = hipEventQuery(partials->last_use);
+        if (state != hipSuccess) {
+            if (state != hipErrorNotReady) (void)hipGetLastError();
+            return fail(TC_UNSUPPORTED, "vector_reduce_noalloc: the device's partials array is in use by another "
+                                        "stream's call that has not finished");
+        }
+    }
+    status = total_into<S, OP, false>(a, nullptr, n, result, partials->address, "vector_reduce_noalloc", s);
+    if (status != TC_OK || capture != hipStreamCaptureStatusNone) return status;
+    const hipError_t error = hipEventRecord(partials->last_use, s);
+    if (error != hipSuccess) {
+        (void)hipGetLastError();
+        // Without the record, no later check could see this call: wait for
+        // it, so the array is free when the next owner takes it.
+        (void)host_wait(s);
+        partials->owner = nullptr;
+        return TC_OK;
+    }
+    partials->owner = s;
+    return TC_OK;
 }
 
 // The moments of a whole buffer, in the manner of `total`: each block folds

@@ -211,3 +211,83 @@ def test_a_repeated_broadcast_program_runs_compiled_and_stays_exact(rows, cols):
         # which it writes without their multiply: at (1, 1) the transposed
         # matrix's column step is 1, so that shape compiles its own.
         assert compiled() == before + (1 if (rows, cols) in ((37, 70), (1, 1)) else 0)
+
+
+def _resident(limit=0):
+    import ctypes
+
+    resident, current = ctypes.c_uint64(), ctypes.c_uint64()
+    lib.call("tc_fused_resident", limit, ctypes.byref(resident), ctypes.byref(current))
+    return resident.value, current.value
+
+
+def _nine_place_program(scale):
+    """x[r, c] + x[r, c + 1] + ... + x[r, c + 8], times `scale`: nine places,
+    one more than kernel arguments carry, so the program runs from a device
+    copy."""
+    code = [(0, 0, 0, 0, lib.F32, 0, 0.0)]
+    for k in range(1, 9):
+        code += [(0, k, 1, 0, lib.F32, 0, 0.0), (2, lib.ADD, 0, 0, 1, 0, 0.0)]
+    code += [(1, 0, 2, 0, 0, 0, scale), (2, lib.MUL, 0, 0, 2, 0, 0.0), (5, 0, 0, 0, lib.F32, 0, 0.0)]
+    return code
+
+
+def test_large_programs_past_the_resident_limit_run_and_stay_exact():
+    # A program with more places than kernel arguments carry is kept on the
+    # device by its bytes, up to a limit; past it each run uploads its own
+    # copy and frees it once queued.  Runs with new constants and shapes on
+    # both sides of the limit, and a resident program run again, give the
+    # oracle's bits.
+    import ctypes
+
+    from tests.test_gpu_runtime import Graph
+
+    resident, limit = _resident()
+    try:
+        _resident(resident + 2)
+        rng = np.random.default_rng(21)
+        first = None
+        for i, (rows, cols) in enumerate([(5, 7), (33, 65), (5, 7), (64, 3), (17, 130), (1, 1)]):
+            scale = float(np.float32(1.0 + 0.25 * i))
+            code = _nine_place_program(scale)
+            places = [(k, 1, 1, [rows], [cols + 8]) for k in range(9)]
+            x = rng.standard_normal(rows * (cols + 8)).astype(np.float32)
+            want = np.zeros(rows * cols, np.float32)
+            oracle.fused(lib.F32, code, places, [x], [want], rows, cols)
+            dx, out = lib.Buffer.of(x), lib.Buffer(4 * rows * cols)
+            lib.fused(lib.F32, code, places, [(dx, x.size)], [(out, rows * cols)], rows, cols)
+            assert bits_equal(out.download(np.float32), want), (rows, cols)
+            if first is None:
+                first = (code, places, dx, x, want, rows, cols)
+        assert _resident()[0] == resident + 2
+        # The first program is resident: it runs from its kept copy, and may
+        # be captured into a graph.
+        code, places, dx, x, want, rows, cols = first
+        out = lib.Buffer(4 * rows * cols)
+        lib.fused(lib.F32, code, places, [(dx, x.size)], [(out, rows * cols)], rows, cols)
+        assert bits_equal(out.download(np.float32), want)
+        graph = Graph()
+        again = lib.Buffer(4 * rows * cols)
+        with graph:
+            lib.fused(lib.F32, code, places, [(dx, x.size)], [(again, rows * cols)], rows, cols)
+        for _ in range(2):
+            graph.replay()
+            lib.sync()
+            assert bits_equal(again.download(np.float32), want)
+        graph.destroy()
+        # A program never run before cannot be uploaded from inside a
+        # capture: refused, with nothing queued.
+        novel = _nine_place_program(9.5)
+        capture = Graph()
+        lib.sync()
+        assert capture.hip.hipStreamBeginCapture(capture.stream, 2) == 0
+        try:
+            with pytest.raises(lib.HipError, match="must run once before it is captured"):
+                lib.fused(lib.F32, novel, places, [(dx, x.size)], [(again, rows * cols)], rows, cols)
+        finally:
+            assert capture.hip.hipStreamEndCapture(capture.stream, ctypes.byref(capture.graph)) == 0
+            capture.hip.hipGraphDestroy(capture.graph)
+        lib.call("tc_release_graph_memory")
+        assert _resident()[0] == resident + 2
+    finally:
+        _resident(limit)

@@ -3,7 +3,8 @@ against `tc_vector_reduce` (Kernels::vector_reduce, kernels.rs:867), which
 runs the same kernels over storage from the cache: results must be the same
 bits, for every type and fold, on calls in a row whose second is smaller
 (the library's array then still holds the first call's partials past the
-ones the second writes)."""
+ones the second writes); and a call from a second stream while the array's
+last use is still queued is refused."""
 
 import ctypes
 
@@ -48,3 +49,49 @@ def test_the_noalloc_fold_over_nothing_is_the_identity():
     assert out.download(np.float32, 1)[0] == 0.0
     lib.call("tc_vector_reduce_noalloc", lib.F32, None, 0, lib.RMAX, out.ptr)
     assert out.download(np.float32, 1)[0] == -np.inf
+
+
+def test_a_call_from_another_stream_is_refused_while_the_array_is_in_use():
+    # The array belongs to the stream of its last call.  Another thread (its
+    # own stream) queues a fold behind about 4 ms of copies; while that fold
+    # is queued, a fold from this thread's stream is refused instead of
+    # racing on the array, and once the other stream has drained it runs
+    # and gives the allocating fold's bits.
+    import threading
+
+    n = 1 << 20
+    x = lib.Buffer.of(np.random.default_rng(5).standard_normal(n).astype(np.float32))
+    want = fold("tc_vector_reduce", lib.F32, x, n, lib.SUM)
+    big = 4 << 30
+    src, dst = lib.Buffer(big), lib.Buffer(big)
+    theirs, ours = lib.Buffer(4), lib.Buffer(4)
+    queued, go = threading.Event(), threading.Event()
+    failure = []
+
+    def other():
+        try:
+            for _ in range(3):
+                lib.call("tc_copy", dst.ptr, src.ptr, big)
+            lib.call("tc_vector_reduce_noalloc", lib.F32, x.ptr, n, lib.SUM, theirs.ptr)
+        except Exception as error:  # reported by the main thread
+            failure.append(error)
+        queued.set()
+        go.wait()
+        lib.call("tc_sync")
+
+    worker = threading.Thread(target=other)
+    worker.start()
+    try:
+        assert queued.wait(60)
+        assert not failure, failure
+        with pytest.raises(lib.HipError, match="in use by another stream"):
+            lib.call("tc_vector_reduce_noalloc", lib.F32, x.ptr, n, lib.SUM, ours.ptr)
+    finally:
+        go.set()
+        worker.join()
+    lib.call("tc_vector_reduce_noalloc", lib.F32, x.ptr, n, lib.SUM, ours.ptr)
+    for out in (theirs, ours):
+        got = out.download(np.float32, 1)[0]
+        assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32)
+    for buffer in (x, src, dst, theirs, ours):
+        buffer.free()
