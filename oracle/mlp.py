@@ -17,7 +17,12 @@ reference's tape runs for it, in the same order and the same element type:
   difference's pass-through, the bias through `matvec(adjoint, ones)`
   (:984), the product's `adjoint · Hᵀ` and `Wᵀ · adjoint` (:1199-1214), and
   the rectifier's ½-at-ties share `MaxShare(z, 0)` (:1122-1130, kernels.rs:138-153);
-- Adam: the program of optim.rs:1048-1100 with the corrections of :1106-1124.
+- Adam: the program of optim.rs:1048-1100 with the corrections of :1106-1124,
+  as the Host runs it under its default `Algebra::Reassociate`: the product
+  chain m' . c1 / d . rate regrouped as (m' . fl(c1 rate)) / d, the plan
+  `oracle/fusion.py`'s restatement of the reference's optimizer chooses for
+  it (fusion/src/rewrite.rs:324-399, optimize.rs:152-215); `algebra="exact"`
+  gives the construction order.
 
 `dtype` float32 gives the step as the f32 kernels compute it up to the
 order of each product's and sum's additions; float64 gives the tolerance
@@ -45,7 +50,10 @@ def powi(base, exponent: int, dtype=np.float32):
 class Adam:
     """`Adam` (optim.rs:1001-1136) over one array."""
 
-    def __init__(self, rate, dtype=np.float32):
+    def __init__(self, rate, dtype=np.float32, algebra="reassociate"):
+        if algebra not in ("exact", "reassociate"):
+            raise ValueError(f"no Algebra {algebra!r}")
+        self.algebra = algebra
         self.dtype = dtype
         self.rate = dtype(rate)
         self.b1, self.b2, self.eps = dtype(0.9), dtype(0.999), dtype(1e-8)
@@ -65,9 +73,11 @@ class Adam:
         else:
             m = self.m * self.b1 + fresh_first
             v = self.v * self.b2 + fresh_second
-        step = (m * c1) / (np.sqrt(v * c2) + self.eps)
+        denominator = np.sqrt(v * c2) + self.eps
         self.m, self.v = m, v
-        return p - step * self.rate
+        if self.algebra == "reassociate":
+            return p - (m * t(c1 * self.rate)) / denominator
+        return p - ((m * c1) / denominator) * self.rate
 
 
 def forward(weights, biases, x, y, dtype):
@@ -106,11 +116,11 @@ def gradients(weights, biases, x, y, dtype=np.float64):
     return loss, gw, gb
 
 
-def train(weights, biases, x, y, rate, steps, dtype=np.float32):
+def train(weights, biases, x, y, rate, steps, dtype=np.float32, algebra="reassociate"):
     """`steps` training steps; the loss before each, and the final parameters."""
     weights = [w.astype(dtype) for w in weights]
     biases = [b.astype(dtype) for b in biases]
-    rules = [(Adam(rate, dtype), Adam(rate, dtype)) for _ in weights]
+    rules = [(Adam(rate, dtype, algebra), Adam(rate, dtype, algebra)) for _ in weights]
     losses = []
     for _ in range(steps):
         loss, gw, gb = gradients(weights, biases, x, y, dtype)

@@ -1,15 +1,23 @@
 // The Adam rule over Hip storage: one fused program per step, run by
 // `tc_fused` (src/optim.rs:986-1136; `Kernels::fused`, kernels.rs:1077).
 //
-// `program` encodes the program `Adam::program` builds (optim.rs:1048-1100),
-// instruction for instruction in its construction order, with the uniforms
-// bound to their values: `1 - beta` folded into constants computed once in
-// the element type, and the bias corrections `1 / (1 - beta^t)` computed on
-// the host in the element type as `Adam::update` does (optim.rs:1106-1124),
-// with `powi` as square-and-multiply from the low bit, each product rounded
-// (compiler-rt's __powisf2, what Rust's f32::powi lowers to).  The first step
-// returns fresh moments; later steps update parameters and both moments in
-// place, reading and writing each once.
+// `program` encodes the program `Adam::program` builds (optim.rs:1048-1100)
+// as the Host runs it, with the uniforms bound to their values: `1 - beta`
+// folded into constants computed once in the element type, and the bias
+// corrections `1 / (1 - beta^t)` computed on the host in the element type as
+// `Adam::update` does (optim.rs:1106-1124), with `powi` as square-and-multiply
+// from the low bit, each product rounded (compiler-rt's __powisf2, what
+// Rust's f32::powi lowers to).  The first step returns fresh moments; later
+// steps update parameters and both moments in place, reading and writing
+// each once.
+//
+// The Host optimizes a built program under the thread's `Algebra`
+// (fused/mod.rs:2473-2491): `Exact` keeps the construction order,
+// ((m' c1) / d) rate; `Reassociate`, the default, regroups the product chain
+// m' . c1 / d . rate, whose inner links nothing else reads, and folds its two
+// constants into one in the element type: (m' fl(c1 rate)) / d
+// (fusion/src/rewrite.rs:324-399), the plan the optimizer's cost model picks
+// (fusion/src/optimize.rs:152-215).
 #pragma once
 
 #include <stdint.h>
@@ -37,11 +45,15 @@ inline float powi(float base, int exponent) {
     return exponent < 0 ? 1.0f / result : result;
 }
 
+// `Algebra` (fused/mod.rs:2473-2491).
+enum class Algebra { Exact, Reassociate };
+
 // `Adam` (optim.rs:1001-1136) for f32 parameters of one shape.
 class Adam {
    public:
-    // `Adam::new`: beta1 0.9, beta2 0.999, epsilon 1e-8 (optim.rs:1029-1041).
-    explicit Adam(float rate) : rate_(rate) {}
+    // `Adam::new`: beta1 0.9, beta2 0.999, epsilon 1e-8 (optim.rs:1029-1041);
+    // the algebra is fixed when the rule is made (optim.rs:727-733).
+    explicit Adam(float rate, Algebra algebra = Algebra::Reassociate) : rate_(rate), algebra_(algebra) {}
 
     size_t steps() const { return steps_; }
 
@@ -120,17 +132,25 @@ class Adam {
             first = 6;
             second = 8;
         }
-        const tc_encoded tail[] = {
-            op(CONST, 0, 10, 0, 0, 0, first_correction),
-            op(BINARY, TC_MUL, 11, first, 10, 0, 0.0f),    // corrected first
+        const bool regrouped = algebra_ == Algebra::Reassociate;
+        // Regrouped, c1 and the rate are one constant, folded in f32.
+        const float numerator_factor = regrouped ? first_correction * rate_ : first_correction;
+        const tc_encoded middle[] = {
+            op(CONST, 0, 10, 0, 0, 0, numerator_factor),
+            op(BINARY, TC_MUL, 11, first, 10, 0, 0.0f),    // m' c1, or m' fl(c1 rate)
             op(CONST, 0, 12, 0, 0, 0, second_correction),
             op(BINARY, TC_MUL, 13, second, 12, 0, 0.0f),   // corrected second
             op(UNARY, kSqrt, 13, 13, 0, 0, 0.0f),          // root
             op(CONST, 0, 14, 0, 0, 0, epsilon_),
             op(BINARY, TC_ADD, 13, 13, 14, 0, 0.0f),       // denominator
             op(BINARY, TC_DIV, 11, 11, 13, 0, 0.0f),       // step
-            op(CONST, 0, 15, 0, 0, 0, rate_),
-            op(BINARY, TC_MUL, 11, 11, 15, 0, 0.0f),       // step rate
+        };
+        code.insert(code.end(), std::begin(middle), std::end(middle));
+        if (!regrouped) {
+            code.push_back(op(CONST, 0, 15, 0, 0, 0, rate_));
+            code.push_back(op(BINARY, TC_MUL, 11, 11, 15, 0, 0.0f));  // step rate
+        }
+        const tc_encoded tail[] = {
             op(LOAD, 1, 7, 1, TC_F32, 0, 0.0f),            // r7 = p
             op(BINARY, TC_SUB, 7, 7, 11, 0, 0.0f),         // p - step rate
             op(STORE, 0, 0, 7, TC_F32, 0, 0.0f),
@@ -142,6 +162,7 @@ class Adam {
     }
 
     float rate_;
+    Algebra algebra_;
     float first_decay_ = 0.9f, second_decay_ = 0.999f, epsilon_ = 1e-8f;
     size_t steps_ = 0;
     std::optional<Storage<float>> first_, second_;

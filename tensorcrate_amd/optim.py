@@ -2,11 +2,26 @@
 per step (optim.rs:986-1136).
 
 ``adam_program`` encodes the program ``Adam::program`` builds
-(optim.rs:1048-1100), instruction for instruction in its construction order,
-with its uniforms bound to their values: the coefficients, ``1 - beta`` folded
-into constants computed once in the element type, and the bias corrections
-``1 / (1 - beta^t)`` computed on the host in the element type as ``update``
-does (optim.rs:1106-1124).  ``Adam.update`` runs it through ``tc_fused``.
+(optim.rs:1048-1100) as the Host runs it, with its uniforms bound to their
+values: the coefficients, ``1 - beta`` folded into constants computed once in
+the element type, and the bias corrections ``1 / (1 - beta^t)`` computed on
+the host in the element type as ``update`` does (optim.rs:1106-1124).
+``Adam.update`` runs it through ``tc_fused``.
+
+The Host optimizes every built program before it runs it, under the
+thread's ``Algebra`` (fused/mod.rs:2473-2491, optim.rs:716-745):
+
+- ``EXACT``: only rewrites that keep every result's bits, so the program runs
+  in its construction order: ``((m' c1) / (sqrt(v' c2) + eps)) rate``;
+- ``REASSOCIATE``, the default: the optimizer (fusion/src/rewrite.rs:324-399)
+  flattens the product chain ``m' . c1 / d . rate``, whose inner links nothing
+  else reads, gathers its two constants into one folded in the element type,
+  and rebuilds it as ``(m' . fl(c1 rate)) / d``, one instruction and one
+  constant fewer; under every cost model the reference defines that plan is
+  the cheapest (fusion/src/optimize.rs:152-215), so it is the one the Host
+  interprets.  The other chains of the step (``g g (1 - beta2)``,
+  ``m beta1 + g (1 - beta1)``, ``sqrt(.) + eps``, ``p - step``) rebuild as
+  built.
 """
 
 from __future__ import annotations
@@ -55,11 +70,17 @@ def identity_place(rows: int, cols: int):
     return (0, 1, 1, [rows], [cols])
 
 
-def adam_program(resumed: bool, dtype: int, rate, first_decay, second_decay, epsilon, step: int):
-    """The encoded Adam step (optim.rs:1048-1100) and its load places'
-    slots.  Inputs: 0 the gradient, 1 the parameters, then (resumed) 2 the
-    first moment and 3 the second; outputs: 0 the parameters, 1 the first
-    moment, 2 the second."""
+EXACT, REASSOCIATE = "exact", "reassociate"  # `Algebra` (fused/mod.rs:2473-2491)
+
+
+def adam_program(resumed: bool, dtype: int, rate, first_decay, second_decay, epsilon, step: int,
+                 algebra: str = REASSOCIATE):
+    """The encoded Adam step (optim.rs:1048-1100) as the Host runs it under
+    `algebra`, and its load places' slots.  Inputs: 0 the gradient, 1 the
+    parameters, then (resumed) 2 the first moment and 3 the second; outputs:
+    0 the parameters, 1 the first moment, 2 the second."""
+    if algebra not in (EXACT, REASSOCIATE):
+        raise ValueError(f"no Algebra {algebra!r}")
     t = lambda v: float(_in_type(dtype, v))
     one = np.float32(1.0)
     b1, b2 = _in_type(dtype, first_decay), _in_type(dtype, second_decay)
@@ -89,17 +110,26 @@ def adam_program(resumed: bool, dtype: int, rate, first_decay, second_decay, eps
         first, second = 6, 8
     else:
         first, second = 2, 5
-    code += [
-        (CONST, 0, 10, 0, 0, 0, float(first_correction)),
-        (BINARY, lib.MUL, 11, first, 10, 0, 0.0),     # corrected first
+    if algebra == REASSOCIATE:
+        # c1 and the rate gathered into one constant, folded in the type.
+        folded = t(np.float32(first_correction) * np.float32(t(rate)))
+        numerator = [(CONST, 0, 10, 0, 0, 0, folded),
+                     (BINARY, lib.MUL, 11, first, 10, 0, 0.0)]    # m' fl(c1 rate)
+    else:
+        numerator = [(CONST, 0, 10, 0, 0, 0, float(first_correction)),
+                     (BINARY, lib.MUL, 11, first, 10, 0, 0.0)]    # corrected first
+    code += numerator + [
         (CONST, 0, 12, 0, 0, 0, float(second_correction)),
         (BINARY, lib.MUL, 13, second, 12, 0, 0.0),    # corrected second
         (UNARY, SQRT, 13, 13, 0, 0, 0.0),             # root
         (CONST, 0, 14, 0, 0, 0, t(epsilon)),
         (BINARY, lib.ADD, 13, 13, 14, 0, 0.0),        # denominator
         (BINARY, lib.DIV, 11, 11, 13, 0, 0.0),        # step
-        (CONST, 0, 15, 0, 0, 0, t(rate)),
-        (BINARY, lib.MUL, 11, 11, 15, 0, 0.0),        # step rate
+    ]
+    if algebra == EXACT:
+        code += [(CONST, 0, 15, 0, 0, 0, t(rate)),
+                 (BINARY, lib.MUL, 11, 11, 15, 0, 0.0)]      # step rate
+    code += [
         (LOAD, 1, 7, 1, dtype, 0, 0.0),               # r7 = p
         (BINARY, lib.SUB, 7, 7, 11, 0, 0.0),          # p - step rate
         (STORE, 0, 0, 7, dtype, 0, 0.0),
@@ -113,10 +143,13 @@ def adam_program(resumed: bool, dtype: int, rate, first_decay, second_decay, eps
 class Adam:
     """`Adam` (optim.rs:1001-1136) over device buffers of `len` elements."""
 
-    def __init__(self, rate, dtype: int = lib.F32):
+    def __init__(self, rate, dtype: int = lib.F32, algebra: str = REASSOCIATE):
         self.rate = rate
         self.first_decay, self.second_decay, self.epsilon = 0.9, 0.999, 1e-8
         self.dtype = dtype
+        # Fixed when the rule is made, as `Step::default` takes the thread's
+        # algebra (optim.rs:727-733).
+        self.algebra = algebra
         self.steps = 0
         self.first = self.second = None
 
@@ -124,7 +157,7 @@ class Adam:
         self.steps += 1
         resumed = self.first is not None
         code, loads = adam_program(resumed, self.dtype, self.rate, self.first_decay, self.second_decay,
-                                   self.epsilon, self.steps)
+                                   self.epsilon, self.steps, self.algebra)
         n = rows * cols
         places = [identity_place(rows, cols)] * loads
         if not resumed:

@@ -8,8 +8,9 @@ import pytest
 from oracle import binding as oracle
 from oracle import mlp
 from tensorcrate_amd import lib
-from tensorcrate_amd.optim import Adam, adam_program, identity_place
+from tensorcrate_amd.optim import EXACT, REASSOCIATE, Adam, identity_place
 from tests.common import KINDS, bits_equal, same_bits, to_kind, widen
+from tests.host_programs import host_adam_program
 
 pytestmark = pytest.mark.gpu
 
@@ -70,14 +71,20 @@ def test_adams_first_step_is_the_rate(magnitude):
 # is infinite and the step does nothing; the reference's coefficients are
 # public fields (optim.rs:1001-1005), so bf16 runs with β₂ = 0.99, whose
 # bf16 value 0.98828125 keeps the update's arithmetic exercised.
+#
+# The checker's program is the Host's: `Adam::program` as built, run through
+# the restated optimizer under the rule's algebra, the chosen plan lowered
+# with each step's constants (tests/host_programs.py), and interpreted by
+# the oracle.
+@pytest.mark.parametrize("algebra", [REASSOCIATE, EXACT])
 @pytest.mark.parametrize("dtype,second_decay", [(lib.F32, 0.999), (lib.F16, 0.999), (lib.BF16, 0.99),
                                                 (lib.F32, 0.99)])
-def test_adam_steps_match_the_oracle_bit_for_bit(dtype, second_decay):
+def test_adam_steps_match_the_oracle_bit_for_bit(dtype, second_decay, algebra):
     rows, cols = 129, 257
     rng = np.random.default_rng(4)
     p0 = to_kind(rng.standard_normal((rows, cols)), dtype)
     grads = [to_kind(rng.standard_normal((rows, cols)), dtype) for _ in range(4)]
-    rule = Adam(1e-3, dtype)
+    rule = Adam(1e-3, dtype, algebra)
     rule.second_decay = second_decay
     p = lib.Buffer.of(p0)
     host_p = p0.copy().reshape(-1)
@@ -85,7 +92,8 @@ def test_adam_steps_match_the_oracle_bit_for_bit(dtype, second_decay):
     for step, grad in enumerate(grads, start=1):
         rule.update(p, lib.Buffer.of(grad), rows, cols)
         resumed = host_m is not None
-        code, loads = adam_program(resumed, dtype, 1e-3, 0.9, second_decay, 1e-8, step)
+        code, loads, _ = host_adam_program(resumed, dtype, 1e-3, 0.9, second_decay, 1e-8, step,
+                                           reassociate=algebra == REASSOCIATE)
         places = [identity_place(rows, cols)] * loads
         new_m = np.zeros_like(host_p) if not resumed else host_m
         new_v = np.zeros_like(host_p) if not resumed else host_v
@@ -119,7 +127,7 @@ def test_config5_adam_over_the_mlp_parameters():
     m = v = None
     for step in range(1, 4):
         resumed = m is not None
-        code, loads = adam_program(resumed, lib.F32, 1e-3, 0.9, 0.999, 1e-8, step)
+        code, loads, _ = host_adam_program(resumed, lib.F32, 1e-3, 0.9, 0.999, 1e-8, step)
         nm = np.zeros_like(host_p) if m is None else m
         nv = np.zeros_like(host_p) if v is None else v
         ins = [grad[:64].reshape(-1).copy(), host_p] + ([m, v] if resumed else [])
