@@ -569,6 +569,16 @@ int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, c
                        const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
                        void* const* outputs, const uint64_t* output_lens, uint32_t output_count);
 
+/* The source the runtime compiler builds `tc_matmul_epilogue`'s product
+ * kernels from for this program (after the product kernels' header, the
+ * epilogue type `CompiledStore`, its program as straight-line code), into
+ * `out` (NUL-terminated, cut at `capacity` - 1 bytes) with its full length
+ * in `*length`; `out` may be NULL to ask for the length.  Needs no device.
+ * No counterpart in the reference's interface: a diagnostic, so that tests
+ * can compile and inspect the very instances the runtime compiles. */
+int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                              uint32_t place_count, char* out, uint64_t capacity, uint64_t* length);
+
 /* How many fused programs this process has compiled into kernels of their
  * own.  A dense program (every load in element order, every load before any
  * store) is compiled on its second appearance and cached by its source, as

@@ -40,6 +40,10 @@
 
 #include <string.h>
 
+#include <algorithm>
+#include <mutex>
+#include <unordered_map>
+
 #include <type_traits>
 
 #include "common.hpp"
@@ -546,6 +550,45 @@ int matmul_typed(uint32_t transposed, bool accumulate, uint64_t m, uint64_t k, u
 // loads are in flight together.
 constexpr int kCompiledElems = 16;
 
+// The source the runtime compiler builds a program's product kernels from:
+// the epilogue type CompiledStore with the program as straight-line code,
+// after the product kernels' header; empty when the program has more
+// constants than the kernels' arguments carry.
+std::string epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* host_places,
+                            std::vector<float>* constants) {
+    const std::string body = epilogue_group(code, count, dtype, true, kCompiledElems, host_places, constants);
+    if (constants->size() > static_cast<size_t>(kInlineCode)) return std::string();
+    return "#include \"gemm_kernels.hpp\"\n"
+           "struct CompiledStore {\n"
+           "  static constexpr bool kProgram = true;\n"
+           "  static constexpr int kElems = " + std::to_string(kCompiledElems) + ";\n" +
+           compiled_members() +
+           "  __device__ __forceinline__ void group(const bool (&live)[kElems], const uint32_t (&row)[kElems],\n"
+           "      const uint32_t (&col)[kElems], uint32_t N, const float (&product)[kElems]) const {\n" +
+           body + "  }\n};\n";
+}
+
+// Whether a compiled kernel keeps anything in scratch memory (a private
+// segment), asked of the runtime once per function.  The four-wave kernel's
+// matrix-core steps are inline assembly on accumulators pinned in AGPRs, and
+// the code around them supplies their hazard cover; an instance whose
+// generated epilogue made the compiler spill, or move the accumulators to
+// scratch, breaks those assumptions, so such an instance is never launched
+// (the eight-wave kernels take the product instead).
+bool uses_scratch(hipFunction_t function) {
+    static std::mutex mutex;
+    static std::unordered_map<hipFunction_t, bool> known;
+    std::lock_guard<std::mutex> lock(mutex);
+    auto found = known.find(function);
+    if (found != known.end()) return found->second;
+    int bytes = 0;
+    if (hipFuncGetAttribute(&bytes, HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES, function) != hipSuccess) {
+        (void)hipGetLastError();
+        bytes = 1;  // unknown: treated as using scratch
+    }
+    return known.emplace(function, bytes != 0).first->second;
+}
+
 // The product kernels with `code` compiled into their epilogue, once the
 // program has been seen before: true when they were launched.
 bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, const void* a, const void* b,
@@ -554,16 +597,8 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
                            const void* const* inputs, uint32_t input_count, void* const* outputs,
                            uint32_t output_count, hipStream_t s, int* status) {
     std::vector<float> constants;
-    const std::string body = epilogue_group(code, count, dtype, true, kCompiledElems, host_places, &constants);
-    if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
-    std::string source = "#include \"gemm_kernels.hpp\"\n"
-                         "struct CompiledStore {\n"
-                         "  static constexpr bool kProgram = true;\n"
-                         "  static constexpr int kElems = " + std::to_string(kCompiledElems) + ";\n" +
-                         compiled_members() +
-                         "  __device__ __forceinline__ void group(const bool (&live)[kElems], const uint32_t (&row)[kElems],\n"
-                         "      const uint32_t (&col)[kElems], uint32_t N, const float (&product)[kElems]) const {\n" +
-                         body + "  }\n};\n";
+    const std::string source = epilogue_source(dtype, code, count, host_places, &constants);
+    if (source.empty()) return false;
     std::vector<std::string> kernels;
     uint32_t large = 0, small = 0, large_threads = 0, small_threads = 0;
     if (dtype == TC_F32) {
@@ -598,7 +633,7 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     // 16-bit products over whole step pairs take the persistent kernels, as
     // plain ones do (launch_tiled16): the four-wave one when K is a multiple
     // of 128, else the eight-wave one.
-    const bool wide = kernels.size() == 4 && use_large && k % 128 == 0;
+    const bool wide = kernels.size() == 4 && use_large && k % 128 == 0 && !uses_scratch(functions[3]);
     const bool persistent = kernels.size() == 4 && use_large && ((k + 63) / 64) % 2 == 0;
     hipFunction_t function = dtype == TC_F32 ? functions[0]
                              : wide          ? functions[3]
@@ -682,6 +717,29 @@ int matmul_program(uint32_t dtype, uint64_t m, uint64_t k, uint64_t n, const voi
 }  // namespace tc
 
 using namespace tc;
+
+extern "C" int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count,
+                                         const tc_place* places, uint32_t place_count, char* out, uint64_t capacity,
+                                         uint64_t* length) {
+    if (dtype != TC_F32 && dtype != TC_F16 && dtype != TC_BF16) {
+        return fail(TC_UNSUPPORTED, std::string("matmul epilogue source: no kernels for ") + dtype_name(dtype));
+    }
+    if (count > static_cast<uint32_t>(kInlineCode) || place_count > static_cast<uint32_t>(kInlinePlaces)) {
+        return fail(TC_UNSUPPORTED, "matmul epilogue source: the program is not compiled into the product kernels");
+    }
+    std::vector<float> constants;
+    const std::string source = epilogue_source(dtype, code, count, places, &constants);
+    if (source.empty()) {
+        return fail(TC_UNSUPPORTED, "matmul epilogue source: more constants than the kernels' arguments carry");
+    }
+    *length = source.size();
+    if (out != nullptr && capacity > 0) {
+        const size_t n = std::min<size_t>(source.size(), capacity - 1);
+        memcpy(out, source.data(), n);
+        out[n] = '\0';
+    }
+    return TC_OK;
+}
 
 extern "C" int tc_matmul(uint32_t in_dtype, uint32_t out_dtype, uint32_t transposed, int accumulate, uint64_t m,
                          uint64_t k, uint64_t n, const void* a, const void* b, void* c) {

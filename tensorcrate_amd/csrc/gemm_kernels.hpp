@@ -1420,6 +1420,16 @@ __device__ __forceinline__ void static_for(F&& f) {
 // What follows matrix-core step t (0-63) of a slice: fragment read r (even r
 // an A fragment, odd a B fragment, of block r / 2), direct load 100 + i, or
 // nothing.
+// The cache policy of the four-wave kernel's C stores: non-temporal (the
+// buffer instruction's nt bit), so C streams to memory instead of settling
+// in the XCD's L2, where the A and B panels the other tiles of the round are
+// still reading live.  A round's C is 4 MiB an XCD, the size of its L2.
+// Measured on MI355X (stand-alone harness, same bits): bf16 8192^3 1560-1585
+// against 1500-1505 TFLOP/s with plain stores; streaming the operand loads
+// instead measured 1285.  The f32 kernel's 4-byte stores measured 0.4-1.5%
+// slower streamed, so they stay plain.
+constexpr int kStreamStore = 2;
+
 template <int SLICE>
 __device__ constexpr int wide_op_at(int t) {
     if (SLICE == 0) return t % 2 == 1 && t < 32 ? t / 2 : -1;
@@ -1577,30 +1587,33 @@ __global__ void __launch_bounds__(256) gemm16x16_wide_kernel(const S* __restrict
             static_assert(16 % E == 0, "whole groups of a staged block's 16 rows");
             float* staged = reinterpret_cast<float*>(rows_lds + wave * kRegion);
             const int r = lane % 16, g = lane / 16;
+            // Blocks visited by compile-time index (static_for rather than
+            // an unroll hint), so the accumulators are never indexed at run
+            // time: a large program made the compiler stop unrolling and
+            // keep the whole accumulator array in scratch memory, where the
+            // in-place matrix-core steps would read it back unguarded.
+            static_for<0, (TN / 4) * TM>([&](auto x) __attribute__((always_inline)) {
+                constexpr int h = decltype(x)::value / TM, i = decltype(x)::value % TM;
+                static_for<0, 4>([&](auto y) __attribute__((always_inline)) {
+                    constexpr int jj = decltype(y)::value;
+                    *reinterpret_cast<f32x4*>(staged + r * 64 + (((4 * jj + g) ^ r) * 4)) = acc[i][4 * h + jj];
+                });
 #pragma unroll
-            for (int h = 0; h < TN / 4; h++) {
+                for (int v0 = 0; v0 < 16; v0 += E) {
+                    bool live[E];
+                    uint32_t row[E], col[E];
+                    float product[E];
 #pragma unroll
-                for (int i = 0; i < TM; i++) {
-#pragma unroll
-                    for (int jj = 0; jj < 4; jj++)
-                        *reinterpret_cast<f32x4*>(staged + r * 64 + (((4 * jj + g) ^ r) * 4)) = acc[i][4 * h + jj];
-#pragma unroll
-                    for (int v0 = 0; v0 < 16; v0 += E) {
-                        bool live[E];
-                        uint32_t row[E], col[E];
-                        float product[E];
-#pragma unroll
-                        for (int e = 0; e < E; e++) {
-                            const int v = v0 + e;
-                            product[e] = staged[v * 64 + (((lane / 4) ^ v) * 4) + lane % 4];
-                            row[e] = m0 + wm * (BM / WM) + 16 * i + v;
-                            col[e] = n0 + wn * (BN / WN) + 64 * h + lane;
-                            live[e] = row[e] < M && col[e] < N;
-                        }
-                        epi.group(live, row, col, N, product);
+                    for (int e = 0; e < E; e++) {
+                        const int v = v0 + e;
+                        product[e] = staged[v * 64 + (((lane / 4) ^ v) * 4) + lane % 4];
+                        row[e] = m0 + wm * (BM / WM) + 16 * i + v;
+                        col[e] = n0 + wn * (BN / WN) + 64 * h + lane;
+                        live[e] = row[e] < M && col[e] < N;
                     }
+                    epi.group(live, row, col, N, product);
                 }
-            }
+            });
         } else {
         const bool whole = m0 + BM <= M && n0 + BN <= N;
         const int g = lane / 16;
@@ -1638,13 +1651,13 @@ __global__ void __launch_bounds__(256) gemm16x16_wide_kernel(const S* __restrict
                 const uint32_t eight = __builtin_amdgcn_readfirstlane(8 * N * sizeof(O));
                 // Row 32 p + 8 e + lane / 8 of the wave's band.
                 const uint32_t row = row0 + 32 * p + lane / 8;
-                if (whole || (col_ok && row < M)) __builtin_amdgcn_raw_buffer_store_b128(v0, rc, row_off, first, 0);
+                if (whole || (col_ok && row < M)) __builtin_amdgcn_raw_buffer_store_b128(v0, rc, row_off, first, kStreamStore);
                 if (whole || (col_ok && row + 8 < M))
-                    __builtin_amdgcn_raw_buffer_store_b128(v1, rc, row_off, first + eight, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(v1, rc, row_off, first + eight, kStreamStore);
                 if (whole || (col_ok && row + 16 < M))
-                    __builtin_amdgcn_raw_buffer_store_b128(v2, rc, row_off, first + 2 * eight, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(v2, rc, row_off, first + 2 * eight, kStreamStore);
                 if (whole || (col_ok && row + 24 < M))
-                    __builtin_amdgcn_raw_buffer_store_b128(v3, rc, row_off, first + 3 * eight, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(v3, rc, row_off, first + 3 * eight, kStreamStore);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }

@@ -15,19 +15,26 @@ on three facts instead:
 
 This compiles every instance the library launches, and one with a program
 epilogue, to assembly with the library's own flags, and checks those facts
-(and that nothing spills) by a straight-line scan of each kernel.  A compiler
-that moved a register copy next to a step would fail here, on the CPU,
-rather than give wrong products on the GPU.  Runs on the CPU: hipcc
-cross-compiles for gfx950.
+(and that nothing spills) by a straight-line scan of each kernel.  The same
+scan runs over the instances the runtime compiler builds for product
+epilogues (`tc_matmul_epilogue` from a program's second appearance): their
+source is the library's own (`tc_matmul_epilogue_source`), compiled with the
+flags it hands the runtime compiler, for a dense layer's bias + relu and for
+a program with more inputs, places and outputs.  A compiler that moved a
+register copy next to a step would fail here, on the CPU, rather than give
+wrong products on the GPU.  Runs on the CPU: hipcc cross-compiles for
+gfx950.
 """
 
+import ctypes
 import re
 import subprocess
 from pathlib import Path
 
 import pytest
 
-from tensorcrate_amd import _build
+from tensorcrate_amd import _build, lib
+from tests.common import EXP, Code, column_broadcast, identity_place, row_broadcast
 
 CSRC = Path(__file__).resolve().parent.parent / "tensorcrate_amd" / "csrc"
 INSTANCES = [(t, f) for t in ("tc::bf16_t", "_Float16") for f in ("true, true", "true, false", "false, false")]
@@ -92,7 +99,7 @@ def scan(body):
                 for r in registers(parts[1], kind):
                     last[(kind, r)] = (position, "step", line)
             continue
-        if op.startswith("v_") or op.startswith(("ds_write", "buffer_store", "global_store")):
+        if op.startswith("v_") or op.startswith(("ds_write", "buffer_store", "global_store", "scratch_store")):
             sources = parts[2:] if op.startswith("v_") else parts[1:]
             for token in sources:
                 for kind in ("a", "v"):
@@ -166,3 +173,88 @@ def test_the_scan_finds_a_planted_hazard():
     ])
     steps, problems = scan(body)
     assert steps == 2 and len(problems) == 2
+
+
+# The runtime compiler's flags for generated kernels (csrc/fused.hip,
+# kCompileFlags).
+RUNTIME_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-Xclang", "-target-feature",
+                 "-Xclang", "-packed-fp32-ops"]
+
+
+def bias_relu(kind):
+    code = Code()
+    p = code.load(0, 0, kind)
+    b = code.load(1, 1, kind)
+    code.store(code.compare(lib.MAX, code.binary(lib.ADD, p, b), code.const(0.0)), kind, 0)
+    return code.code
+
+
+def scaled_two_outputs(kind):
+    # out0 = product * scale[row] + bias[col] (+ 0.5); out1 = exp(product) in
+    # f32: three places, two inputs, the product read twice, two outputs.
+    code = Code()
+    p = code.load(0, 0, kind)
+    s = code.load(2, 2, kind)
+    b = code.load(1, 1, kind)
+    shifted = code.binary(lib.ADD, code.binary(lib.ADD, code.binary(lib.MUL, p, s), b), code.const(0.5))
+    code.store(shifted, kind, 0)
+    code.store(code.unary(EXP, code.load(0, 0, kind)), lib.F32, 1)
+    return code.code
+
+
+def generated_source(kind, code, places):
+    enc, pl = lib._program(code, places)
+    length = ctypes.c_uint64()
+    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), None, 0, ctypes.byref(length))
+    out = ctypes.create_string_buffer(length.value + 1)
+    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), out, length.value + 1,
+             ctypes.byref(length))
+    return out.value.decode()
+
+
+@pytest.fixture(scope="module")
+def generated_assembly(tmp_path_factory):
+    try:
+        compiler = _build.hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc is not installed")
+    work = tmp_path_factory.mktemp("generated")
+    m = n = 8192
+    places = [identity_place(m, n), row_broadcast(n), column_broadcast(m)]
+    out = []
+    for name, program in (("bias_relu", bias_relu), ("scaled_two_outputs", scaled_two_outputs)):
+        for kind, t in ((lib.BF16, "tc::bf16_t"), (lib.F16, "_Float16")):
+            source = generated_source(kind, program(kind), places)
+            assert "struct CompiledStore" in source
+            # The library asks the runtime compiler for this instance by
+            # name; here it is instantiated explicitly.
+            text = ("#include <hip/hip_runtime.h>\n" + source +
+                    f"template __global__ void tc::gemm16x16_wide_kernel<{t}, {t}, true, false, CompiledStore>("
+                    f"const {t}*, const {t}*, {t}*, uint32_t, uint32_t, uint32_t, bool, CompiledStore);\n")
+            path = work / f"{name}_{kind}.hip"
+            path.write_text(text)
+            target = work / f"{name}_{kind}.s"
+            result = subprocess.run([compiler, *RUNTIME_FLAGS, f"-I{CSRC}", "--cuda-device-only", "-S", str(path),
+                                     "-o", str(target)], capture_output=True, text=True)
+            assert result.returncode == 0, result.stderr[-4000:]
+            out.append((name, kind, target.read_text()))
+    return out
+
+
+def test_generated_epilogue_instances_keep_the_hazard_cover(generated_assembly):
+    # A generated epilogue may hold more values than the registers the
+    # accumulators leave; what it spills must stay out of the matrix-core
+    # step sequence (no scratch access between its first and last step), and
+    # the hazard scan must pass with the spill stores counted as readers.
+    for name, kind, text in generated_assembly:
+        found = list(kernels(text))
+        assert len(found) == 1, (name, kind)
+        agprs = re.findall(r"\.agpr_count:\s+(\d+)", text)
+        assert agprs == ["256"], (name, kind, agprs)
+        lines = [line.split(";")[0].strip() for line in found[0][1].split("\n")]
+        steps_at = [i for i, line in enumerate(lines) if line.startswith("v_mfma")]
+        inside = [line for line in lines[steps_at[0]:steps_at[-1]] if line.startswith("scratch_")]
+        assert not inside, (name, kind, inside[:3])
+        steps, problems = scan(found[0][1])
+        assert steps == 256, (name, kind, steps)
+        assert not problems, (name, kind, problems[:5])
