@@ -579,6 +579,19 @@ int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, c
 int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
                               uint32_t place_count, char* out, uint64_t capacity, uint64_t* length);
 
+/* The source the runtime compiler builds `tc_fused_with_statistics`'s one
+ * kernel from for this program and these statistics (the arguments as that
+ * call takes them; `inputs` and the statistics' sources are only compared
+ * and checked for alignment, never read; outputs count as 16-byte aligned),
+ * into `out` as `tc_matmul_epilogue_source` does.
+ * TC_UNSUPPORTED when the program runs as the composition instead.  Needs no
+ * device.  No counterpart in the reference's interface: a diagnostic, so
+ * that tests can compile the very source the runtime compiles. */
+int tc_fused_with_statistics_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                                    uint32_t place_count, const void* const* inputs, uint32_t input_count,
+                                    uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
+                                    uint32_t statistic_count, char* out, uint64_t capacity, uint64_t* length);
+
 /* How many fused programs this process has compiled into kernels of their
  * own.  A dense program (every load in element order, every load before any
  * store) is compiled on its second appearance and cached by its source, as

@@ -99,4 +99,51 @@ __device__ __forceinline__ void store_as(void* base, uint32_t dtype, uint64_t in
     }
 }
 
+// `E` consecutive elements from `index` on, as `load_as` reads them one by
+// one, moved four at a time: 16 bytes for f32, 8 for the 16-bit types.
+// `index` is a multiple of 4 and `base` aligned to the piece.
+template <int E>
+__device__ __forceinline__ void load_run(const void* base, uint32_t dtype, uint64_t index, float (&out)[E]) {
+    static_assert(E % 4 == 0, "whole runs of four");
+#pragma unroll
+    for (int q = 0; q < E / 4; q++) {
+        if (dtype == tc_ops::F32) {
+            const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + index + 4 * q);
+            out[4 * q] = v.x, out[4 * q + 1] = v.y, out[4 * q + 2] = v.z, out[4 * q + 3] = v.w;
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + index + 4 * q);
+            const uint16_t h[4] = {static_cast<uint16_t>(v.x), static_cast<uint16_t>(v.x >> 16),
+                                   static_cast<uint16_t>(v.y), static_cast<uint16_t>(v.y >> 16)};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                out[4 * q + j] = dtype == tc_ops::F16 ? static_cast<float>(__builtin_bit_cast(_Float16, h[j]))
+                                                      : bf16_bits_to_f32(h[j]);
+            }
+        }
+    }
+}
+
+// `E` consecutive elements stored from `index` on, each converted as
+// `store_as` converts it, four at a time; the same alignment as `load_run`.
+template <int E>
+__device__ __forceinline__ void store_run(void* base, uint32_t dtype, uint64_t index, const float (&v)[E]) {
+    static_assert(E % 4 == 0, "whole runs of four");
+#pragma unroll
+    for (int q = 0; q < E / 4; q++) {
+        if (dtype == tc_ops::F32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(base) + index + 4 * q) =
+                make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        } else {
+            uint16_t h[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                h[j] = dtype == tc_ops::F16 ? __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[4 * q + j]))
+                                            : f32_to_bf16_bits(v[4 * q + j]);
+            }
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + index + 4 * q) =
+                make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+        }
+    }
+}
+
 }  // namespace tc

@@ -530,9 +530,16 @@ std::string place_index(const tc_place& place, const std::string& p, const std::
     return index;
 }
 
+// `held`, when given, marks the loads (by instruction index) whose values
+// the kernel already holds, rounded to the program's type: they read
+// `held[e]` instead of memory.  `runs`, when given, marks the loads and
+// stores that may move the group as one run: the kernel calls the group
+// with elements that are consecutive columns of one row, all live or none,
+// and these instructions' pieces are aligned (load_run / store_run).
 std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                        const tc_place* places, std::vector<float>* constants, bool sum_store = false,
-                       int stat_first = -1) {
+                       int stat_first = -1, const std::vector<bool>* held = nullptr,
+                       const std::vector<bool>* runs = nullptr) {
     static const char* const kBinary[] = {"+", "-", "*", "/"};
     const std::string round = "tc_round<" + std::to_string(dtype) + ">";
     std::ostringstream src;
@@ -544,6 +551,9 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
         if (in.kind == 5) {
             if (sum_store) {  // the one output, already in its type, summed in f32 in element order
                 src << each << "sum += live[e] ? " << at(in.a) << " : 0.0f;\n";
+            } else if (runs != nullptr && (*runs)[pc] && !reg[in.a].empty()) {
+                src << "    if (live[0]) tc::store_run<" << elems << ">(out[" << int(in.aux) << "], " << int(in.b)
+                    << "u, (uint64_t)row[0] * N + col[0], " << reg[in.a] << ");\n";
             } else {
                 src << each << "if (live[e]) tc::store_as(out[" << int(in.aux) << "], " << int(in.b)
                     << "u, (uint64_t)row[e] * N + col[e], " << at(in.a) << ");\n";
@@ -559,6 +569,15 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                 } else if (stat_first >= 0 && in.a >= stat_first) {
                     // A row statistic, one value a row, already in the type.
                     src << "stat[" << (in.a - stat_first) << "];\n";
+                } else if (held != nullptr && (*held)[pc]) {
+                    src << "held[e];\n";
+                } else if (runs != nullptr && (*runs)[pc]) {
+                    // The run from its first element's index, loaded only
+                    // when live; then each element rounded to the type.
+                    const std::string p = "places[" + std::to_string(in.op) + "]";
+                    src << "0.0f;\n    if (live[0]) tc::load_run<" << elems << ">(in[" << int(in.a) << "], "
+                        << int(in.b) << "u, " << place_index(places[in.op], p, "row[0]", "col[0]") << ", " << v
+                        << ");\n" << each << v << "[e] = " << round << "(" << v << "[e]);\n";
                 } else {
                     // Every lane loads, an element outside C at (0, 0), so
                     // no load waits on a branch; the place's row walk is
@@ -975,6 +994,204 @@ extern "C" int tc_fused_resident(uint64_t limit, uint64_t* resident, uint64_t* c
     return TC_OK;
 }
 
+namespace tc {
+namespace {
+
+// The moments' merge and the wave's fold, shared by both forms of the
+// statistics kernel's source.
+const char* const kMomentsSource =
+    "struct Moments { float n, mean, m2; };\n"
+    "// Chan's pairwise merge of two (count, mean, squared deviations).\n"
+    "__device__ __forceinline__ Moments merge(Moments a, Moments b) {\n"
+    "  if (b.n == 0.0f) return a;\n"
+    "  if (a.n == 0.0f) return b;\n"
+    "  const float n = a.n + b.n, delta = b.mean - a.mean, share = b.n / n;\n"
+    "  return Moments{n, a.mean + delta * share, a.m2 + b.m2 + delta * delta * (a.n * share)};\n"
+    "}\n"
+    "// Every lane ends with the same bits: each step merges the lower\n"
+    "// lane's moments with the higher lane's, on both lanes.\n"
+    "__device__ __forceinline__ Moments wave_merge(Moments m, uint32_t lane) {\n"
+    "  for (int offset = 1; offset < 64; offset <<= 1) {\n"
+    "    const Moments o{__shfl_xor(m.n, offset), __shfl_xor(m.mean, offset), __shfl_xor(m.m2, offset)};\n"
+    "    m = (lane & offset) == 0 ? merge(m, o) : merge(o, m);\n"
+    "  }\n"
+    "  return m;\n"
+    "}\n";
+
+// The statistics kernel for one source whose place is its own rows x cols
+// row-major matrix (a layer norm's x): a wave a row, the row loaded once as
+// 16-byte packs into registers (a lane holds packs lane, lane + 64, ...),
+// each lane's moments taken in two passes over its registers and the
+// wave's lanes merged by Chan's update, and the program then run over the
+// held packs, a pack's elements a call, its loads of that same matrix
+// reading the registers.  The row is read from memory once, where the
+// general form reads it again for the program.  Taken when the source is
+// 16-byte aligned, rows are whole packs and a lane holds at most 128 values
+// (cols up to 8192); false otherwise.
+bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                     const void* const* inputs, uint32_t input_count, void* const* outputs, uint64_t cols,
+                     const tc_row_stat& st, uint32_t sources, const tc_row_stat* statistics,
+                     uint32_t statistic_count, std::vector<float>* constants, std::string* out) {
+    if (sources != 1) return false;
+    const uint32_t size = st.source_dtype == TC_F32 ? 4 : (st.source_dtype == TC_F16 || st.source_dtype == TC_BF16) ? 2 : 0;
+    if (size == 0) return false;
+    const uint32_t per = 16 / size;
+    const tc_place& sp = st.place;
+    if (sp.offset != 0 || sp.col_step != 1 || sp.lead != 1 || sp.steps[0] != cols || cols % per != 0 ||
+        reinterpret_cast<uintptr_t>(st.source) % 16 != 0) {
+        return false;
+    }
+    const uint64_t packs = (cols + 64 * per - 1) / (64 * per);  // packs a lane holds
+    if (packs * per > 128) return false;
+    // The program's loads of the same elements: the same storage, type and
+    // place.
+    std::vector<bool> held(count, false);
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind != 0 || in.a >= input_count || inputs[in.a] != st.source || in.b != st.source_dtype) continue;
+        const tc_place& lp = places[in.op];
+        held[pc] = lp.offset == sp.offset && lp.col_step == sp.col_step && lp.lead == sp.lead &&
+                   lp.dims[0] == sp.dims[0] && lp.steps[0] == sp.steps[0];
+    }
+    // The other loads and the stores move a pack's elements as one run
+    // where their pieces are aligned: a store to an aligned output (its row
+    // of cols elements is whole pieces), a load through a place that walks
+    // columns one by one from an aligned input, offset and row step.
+    // `outputs` may be null (a diagnostic): outputs then count as aligned.
+    auto aligned = [](const void* pointer, uint32_t element_dtype) {
+        return reinterpret_cast<uintptr_t>(pointer) % (element_dtype == TC_F32 ? 16 : 8) == 0;
+    };
+    std::vector<bool> runs(count, false);
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind == 5) {
+            runs[pc] = outputs == nullptr || aligned(outputs[in.aux], in.b);
+        } else if (in.kind == 0 && !held[pc] && in.a < input_count) {
+            const tc_place& lp = places[in.op];
+            runs[pc] = lp.lead <= 1 && lp.col_step == 1 && lp.offset % 4 == 0 &&
+                       (lp.lead == 0 || lp.steps[0] % 4 == 0) && aligned(inputs[in.a], in.b);
+        }
+    }
+    const std::string body = group_body(code, count, dtype, false, static_cast<int>(per), places, constants, false,
+                                        static_cast<int>(input_count), &held, &runs);
+    if (constants->size() > static_cast<size_t>(kInlineCode)) return false;
+    const std::string P = std::to_string(per), K = std::to_string(packs), S = std::to_string(statistic_count),
+                      T = std::to_string(dtype);
+    // A pack's elements from its 16 bytes, rounded to the program's type as
+    // a load of them is.
+    std::string unpack;
+    if (st.source_dtype == TC_F32) {
+        unpack = "  const uint32_t bits[4] = {w.x, w.y, w.z, w.w};\n"
+                 "  for (int j = 0; j < 4; j++) x[j] = tc_round<" + T + ">(__builtin_bit_cast(float, bits[j]));\n";
+    } else {
+        const std::string widen = st.source_dtype == TC_F16
+                                      ? "static_cast<float>(__builtin_bit_cast(_Float16, h))"
+                                      : "tc::bf16_bits_to_f32(h)";
+        unpack = "  const uint32_t words[4] = {w.x, w.y, w.z, w.w};\n"
+                 "  for (int j = 0; j < 8; j++) {\n"
+                 "    const uint16_t h = static_cast<uint16_t>(words[j / 2] >> (16 * (j % 2)));\n"
+                 "    x[j] = tc_round<" + T + ">(" + widen + ");\n"
+                 "  }\n";
+    }
+    std::ostringstream src;
+    src << "#include \"device.hpp\"\n"
+           "struct Program {\n" << compiled_members()
+        << "  __device__ __forceinline__ void group(const bool (&live)[" << P << "], const uint32_t (&row)[" << P
+        << "],\n      const uint32_t (&col)[" << P << "], uint32_t N, const float (&stat)[" << S
+        << "], const float (&held)[" << P << "]) const {\n"
+        << body << "  }\n};\n"
+           "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
+        << kMomentsSource
+        << "__device__ __forceinline__ void unpack(const uint4 w, float (&x)[" << P << "]) {\n" << unpack << "}\n"
+           "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_row_statistics(Program p, Sources src,\n"
+           "    uint32_t rows, uint32_t cols) {\n"
+           "  // The wave, and so its row, said to be uniform: the row's buffer\n"
+           "  // resource then lives in scalar registers.\n"
+           "  const uint32_t lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);\n"
+           "  for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {\n"
+           "    // The row as a buffer of its own bytes: a pack past its end\n"
+           "    // loads zeros, with no branch, and every load's address is the\n"
+           "    // lane's offset plus a constant.\n"
+           "    const __amdgpu_buffer_rsrc_t line = __builtin_amdgcn_make_buffer_rsrc(\n"
+           "        const_cast<uint8_t*>(static_cast<const uint8_t*>(src.in[0]) + (uint64_t)r * cols * " << size
+        << "u), 0,\n        cols * " << size << "u, 0x00020000);\n"
+           "    // The row's packs as loaded (16-bit elements stay packed, two a\n"
+           "    // register), unpacked at each use.\n"
+           "    uint4 w[" << K << "];\n"
+           "#pragma unroll\n"
+           "    for (int k = 0; k < " << K << "; k++)\n"
+           "      w[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, lane * 16u, k * 1024u, 0));\n"
+           "    // The lane's values in two passes: their mean, then the squared\n"
+           "    // deviations from it; then the wave's lanes merged.\n"
+           "    // The row's first element, when finite, is subtracted first and\n"
+           "    // added back to the mean once: rows whose mean is large against\n"
+           "    // their spread keep their accuracy through the lanes' merges.\n"
+           "    float first[" << P << "];\n"
+           "    unpack(w[0], first);\n"
+           "    float shift = __shfl(first[0], 0, 64);\n"
+           "    if (!isfinite(shift)) shift = 0.0f;\n"
+           "    float n = 0.0f, sum = 0.0f;\n"
+           "#pragma unroll\n"
+           "    for (int k = 0; k < " << K << "; k++) {\n"
+           "      if ((lane + 64u * k) * " << P << "u < cols) {\n"
+           "        float x[" << P << "];\n"
+           "        unpack(w[k], x);\n"
+           "        for (int j = 0; j < " << P << "; j++) sum += x[j] - shift;\n"
+           "        n += " << per << ".0f;\n"
+           "      }\n"
+           "    }\n"
+           "    const float lane_mean = n > 0.0f ? sum / n : 0.0f;\n"
+           "    // The same value, made opaque: the second pass recomputes each\n"
+           "    // x - shift rather than keeping the first pass's in registers.\n"
+           "    asm volatile(\"\" : \"+v\"(shift));\n"
+           "    float q = 0.0f;\n"
+           "#pragma unroll\n"
+           "    for (int k = 0; k < " << K << "; k++) {\n"
+           "      if ((lane + 64u * k) * " << P << "u < cols) {\n"
+           "        float x[" << P << "];\n"
+           "        unpack(w[k], x);\n"
+           "        for (int j = 0; j < " << P << "; j++) {\n"
+           "          const float d = (x[j] - shift) - lane_mean;\n"
+           "          q += d * d;\n"
+           "        }\n"
+           "      }\n"
+           "    }\n"
+           "    const Moments m = wave_merge(Moments{n, lane_mean, q}, lane);\n"
+           "    float stat[" << S << "];\n";
+    for (uint32_t i = 0; i < statistic_count; i++) {
+        src << "    stat[" << i << "] = tc_round<" << T << ">("
+            << (statistics[i].which == TC_STAT_MEAN ? "m.mean + shift" : "m.m2") << ");\n";
+    }
+    src << "    // The lane's index made opaque here, so the columns of every pack\n"
+           "    // are computed where they are used rather than hoisted out of the\n"
+           "    // row loop, where they would hold a register each.\n"
+           "    uint32_t at_lane = lane;\n"
+           "    asm volatile(\"\" : \"+v\"(at_lane));\n"
+           "#pragma unroll\n"
+           "    for (int k = 0; k < " << K << "; k++) {\n"
+           "      uint32_t row[" << P << "], col[" << P << "];\n"
+           "      bool live[" << P << "];\n"
+           "      for (int j = 0; j < " << P << "; j++) {\n"
+           "        col[j] = (at_lane + 64u * k) * " << P << "u + j;\n"
+           "        row[j] = r;\n"
+           "        live[j] = col[j] < cols;\n"
+           "      }\n"
+           "      float x[" << P << "];\n"
+           "      unpack(w[k], x);\n"
+           "      p.group(live, row, col, cols, stat, x);\n"
+           "      // One pack's program at a time: hoisting every pack's loads\n"
+           "      // ahead of the others' arithmetic would spill the row.\n"
+           "      __builtin_amdgcn_sched_barrier(0);\n"
+           "    }\n"
+           "  }\n"
+           "}\n";
+    *out = src.str();
+    return true;
+}
+
+}  // namespace
+}  // namespace tc
+
 // `fused_with_statistics` (kernels.rs:1103-1113) as one compiled kernel, from
 // the program's second appearance: a wave a row.  For each distinct source
 // one pass over the row (through the source's place, rounded to the
@@ -985,12 +1202,24 @@ extern "C" int tc_fused_resident(uint64_t limit, uint64_t* resident, uint64_t* c
 // composed form stores them, and the program then runs over the row with
 // each statistic read from a register.  The row's second read, for the
 // program, mostly hits the caches.
-int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
-                             uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
-                             uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
-                             uint32_t output_count, uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
-                             uint32_t statistic_count, bool* done) {
-    *done = false;
+namespace tc {
+namespace {
+
+// The one-kernel form's plan: its source (empty when the program does not
+// take that form), its constants, and its distinct sources.
+struct RowStatisticsPlan {
+    std::string source;
+    std::vector<float> constants;
+    const tc_row_stat* first[4] = {};
+    uint32_t sources = 0;
+    bool held = false;  // the form that holds each row in registers
+};
+
+int plan_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                        uint32_t place_count, const void* const* inputs, uint32_t input_count,
+                        void* const* outputs, uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
+                        uint32_t statistic_count, RowStatisticsPlan* plan) {
+    plan->source.clear();
     constexpr uint32_t kMaxSources = 4;
     if (statistic_count == 0 || statistic_count > 8 || place_count > static_cast<uint32_t>(kInlinePlaces) ||
         rows == 0 || cols == 0 || rows * cols > (uint64_t{1} << 31)) {
@@ -1006,8 +1235,8 @@ int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
     }
     // The distinct sources, each with its place checked against its length.
     uint32_t source_of[8];
-    uint32_t sources = 0;
-    const tc_row_stat* first[kMaxSources];
+    uint32_t& sources = plan->sources;
+    const tc_row_stat** first = plan->first;
     for (uint32_t i = 0; i < statistic_count; i++) {
         const tc_row_stat& st = statistics[i];
         uint32_t j = 0;
@@ -1031,95 +1260,118 @@ int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
         }
         source_of[i] = j;
     }
-    std::vector<float> constants;
-    const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, &constants, false,
-                                        static_cast<int>(input_count));
-    if (constants.size() > static_cast<size_t>(kInlineCode)) return TC_OK;
-    const std::string E = std::to_string(kGeneralElems), S = std::to_string(statistic_count),
-                      T = std::to_string(dtype);
+    std::vector<float>& constants = plan->constants;
+    const std::string S = std::to_string(statistic_count), T = std::to_string(dtype);
     std::ostringstream src;
-    src << "#include \"device.hpp\"\n"
-           "struct Program {\n" << compiled_members()
-        << "  __device__ __forceinline__ void group(const bool (&live)[" << E << "], const uint32_t (&row)[" << E
-        << "],\n      const uint32_t (&col)[" << E << "], uint32_t N, const float (&stat)[" << S << "]) const {\n"
-        << body << "  }\n};\n"
-           "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
-           "struct Moments { float n, mean, m2; };\n"
-           "// Chan's pairwise merge of two (count, mean, squared deviations).\n"
-           "__device__ __forceinline__ Moments merge(Moments a, Moments b) {\n"
-           "  if (b.n == 0.0f) return a;\n"
-           "  if (a.n == 0.0f) return b;\n"
-           "  const float n = a.n + b.n, delta = b.mean - a.mean, share = b.n / n;\n"
-           "  return Moments{n, a.mean + delta * share, a.m2 + b.m2 + delta * delta * (a.n * share)};\n"
-           "}\n"
-           "// Every lane ends with the same bits: each step merges the lower\n"
-           "// lane's moments with the higher lane's, on both lanes.\n"
-           "__device__ __forceinline__ Moments wave_merge(Moments m, uint32_t lane) {\n"
-           "  for (int offset = 1; offset < 64; offset <<= 1) {\n"
-           "    const Moments o{__shfl_xor(m.n, offset), __shfl_xor(m.mean, offset), __shfl_xor(m.m2, offset)};\n"
-           "    m = (lane & offset) == 0 ? merge(m, o) : merge(o, m);\n"
-           "  }\n"
-           "  return m;\n"
-           "}\n"
-           "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_row_statistics(Program p, Sources src,\n"
-           "    uint32_t rows, uint32_t cols) {\n"
-           "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
-           "  for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {\n"
-           "    float stat[" << S << "];\n";
-    for (uint32_t j = 0; j < sources; j++) {
-        const std::string J = std::to_string(j), D = std::to_string(first[j]->source_dtype);
-        // Sixteen loads in flight a lane; each lane still adds its
-        // elements in column order.
-        const std::string value = "tc_round<" + T + ">(tc::load_as(src.in[" + J + "], " + D + "u, " +
-                                  place_index(first[j]->place, "src.places[" + J + "]", "r", "c") + "))";
-        const std::string batch = "      for (uint32_t c0 = lane; c0 < cols; c0 += 64u * 16u) {\n"
-                                  "        float x[16];\n"
-                                  "        for (int u = 0; u < 16; u++) {\n"
-                                  "          const uint32_t c = c0 + 64u * u;\n"
-                                  "          x[u] = c < cols ? " + value + " : 0.0f;\n"
-                                  "        }\n";
-        // One pass: each batch's own mean and squared deviations, merged
-        // into the lane's running moments, then the wave's lanes merged.
-        src << "    {\n"
-               "      Moments m{0.0f, 0.0f, 0.0f};\n" << batch <<
-               "        float bs = 0.0f, bn = 0.0f;\n"
-               "        for (int u = 0; u < 16; u++) if (c0 + 64u * u < cols) { bs += x[u]; bn += 1.0f; }\n"
-               "        const float bm = bn > 0.0f ? bs / bn : 0.0f;\n"
-               "        float bq = 0.0f;\n"
-               "        for (int u = 0; u < 16; u++) {\n"
-               "          const float d = x[u] - bm;\n"
-               "          if (c0 + 64u * u < cols) bq += d * d;\n"
-               "        }\n"
-               "        m = merge(m, Moments{bn, bm, bq});\n"
-               "      }\n"
-               "      m = wave_merge(m, lane);\n"
-               "      const float mean = m.mean, deviations = m.m2;\n";
-        for (uint32_t i = 0; i < statistic_count; i++) {
-            if (source_of[i] != j) continue;
-            src << "      stat[" << i << "] = tc_round<" << T << ">("
-                << (statistics[i].which == TC_STAT_MEAN ? "mean" : "deviations") << ");\n";
+    std::string held_source;
+    if (held_row_source(code, count, dtype, places, inputs, input_count, outputs, cols, *first[0], sources,
+                        statistics, statistic_count, &constants, &held_source)) {
+        src << held_source;
+        plan->held = true;
+    } else {
+        constants.clear();
+        const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, &constants, false,
+                                            static_cast<int>(input_count));
+        if (constants.size() > static_cast<size_t>(kInlineCode)) return TC_OK;
+        const std::string E = std::to_string(kGeneralElems);
+        src << "#include \"device.hpp\"\n"
+               "struct Program {\n" << compiled_members()
+            << "  __device__ __forceinline__ void group(const bool (&live)[" << E << "], const uint32_t (&row)[" << E
+            << "],\n      const uint32_t (&col)[" << E << "], uint32_t N, const float (&stat)[" << S << "]) const {\n"
+            << body << "  }\n};\n"
+               "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
+            << kMomentsSource <<
+               "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_row_statistics(Program p, Sources src,\n"
+               "    uint32_t rows, uint32_t cols) {\n"
+               "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
+               "  for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {\n"
+               "    float stat[" << S << "];\n";
+        for (uint32_t j = 0; j < sources; j++) {
+            const std::string J = std::to_string(j), D = std::to_string(first[j]->source_dtype);
+            // Sixteen loads in flight a lane; each lane still adds its
+            // elements in column order.
+            const std::string value = "tc_round<" + T + ">(tc::load_as(src.in[" + J + "], " + D + "u, " +
+                                      place_index(first[j]->place, "src.places[" + J + "]", "r", "c") + "))";
+            const std::string batch = "      for (uint32_t c0 = lane; c0 < cols; c0 += 64u * 16u) {\n"
+                                      "        float x[16];\n"
+                                      "        for (int u = 0; u < 16; u++) {\n"
+                                      "          const uint32_t c = c0 + 64u * u;\n"
+                                      "          x[u] = c < cols ? " + value + " : 0.0f;\n"
+                                      "        }\n";
+            // One pass: each batch's own mean and squared deviations, merged
+            // into the lane's running moments, then the wave's lanes merged.
+            // The row's first element, when finite, is subtracted before the
+            // moments are taken and added back to the mean once: rows whose
+            // mean is large against their spread keep the accuracy of two
+            // passes through the merges.
+            const std::string first_value = "tc_round<" + T + ">(tc::load_as(src.in[" + J + "], " + D + "u, " +
+                                            place_index(first[j]->place, "src.places[" + J + "]", "r", "0u") + "))";
+            src << "    {\n"
+                   "      float shift = " << first_value << ";\n"
+                   "      if (!isfinite(shift)) shift = 0.0f;\n"
+                   "      Moments m{0.0f, 0.0f, 0.0f};\n" << batch <<
+                   "        for (int u = 0; u < 16; u++) x[u] -= shift;\n"
+                   "        float bs = 0.0f, bn = 0.0f;\n"
+                   "        for (int u = 0; u < 16; u++) if (c0 + 64u * u < cols) { bs += x[u]; bn += 1.0f; }\n"
+                   "        const float bm = bn > 0.0f ? bs / bn : 0.0f;\n"
+                   "        float bq = 0.0f;\n"
+                   "        for (int u = 0; u < 16; u++) {\n"
+                   "          const float d = x[u] - bm;\n"
+                   "          if (c0 + 64u * u < cols) bq += d * d;\n"
+                   "        }\n"
+                   "        m = merge(m, Moments{bn, bm, bq});\n"
+                   "      }\n"
+                   "      m = wave_merge(m, lane);\n"
+                   "      const float mean = m.mean + shift, deviations = m.m2;\n";
+            for (uint32_t i = 0; i < statistic_count; i++) {
+                if (source_of[i] != j) continue;
+                src << "      stat[" << i << "] = tc_round<" << T << ">("
+                    << (statistics[i].which == TC_STAT_MEAN ? "mean" : "deviations") << ");\n";
+            }
+            src << "    }\n";
         }
-        src << "    }\n";
+        src << "    for (uint32_t c0 = 0; c0 < cols; c0 += 64u * " << E << ") {\n"
+               "      uint32_t row[" << E << "], col[" << E << "];\n"
+               "      bool live[" << E << "];\n"
+               "      for (int v = 0; v < " << E << "; v++) {\n"
+               "        col[v] = c0 + v * 64u + lane;\n"
+               "        row[v] = r;\n"
+               "        live[v] = col[v] < cols;\n"
+               "      }\n"
+               "      p.group(live, row, col, cols, stat);\n"
+               "    }\n"
+               "  }\n"
+               "}\n";
     }
-    src << "    for (uint32_t c0 = 0; c0 < cols; c0 += 64u * " << E << ") {\n"
-           "      uint32_t row[" << E << "], col[" << E << "];\n"
-           "      bool live[" << E << "];\n"
-           "      for (int v = 0; v < " << E << "; v++) {\n"
-           "        col[v] = c0 + v * 64u + lane;\n"
-           "        row[v] = r;\n"
-           "        live[v] = col[v] < cols;\n"
-           "      }\n"
-           "      p.group(live, row, col, cols, stat);\n"
-           "    }\n"
-           "  }\n"
-           "}\n";
+    plan->source = src.str();
+    return TC_OK;
+}
+
+}  // namespace
+}  // namespace tc
+
+int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                             uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                             uint32_t input_count, void* const* outputs, const uint64_t* output_lens,
+                             uint32_t output_count, uint64_t rows, uint64_t cols, const tc_row_stat* statistics,
+                             uint32_t statistic_count, bool* done) {
+    *done = false;
+    (void)input_lens;
+    (void)output_lens;
+    RowStatisticsPlan plan;
+    int status = plan_row_statistics(dtype, code, count, places, place_count, inputs, input_count, outputs, rows,
+                                     cols, statistics, statistic_count, &plan);
+    if (status != TC_OK || plan.source.empty()) return status;
+    const std::vector<float>& constants = plan.constants;
+    const uint32_t sources = plan.sources;
+    const tc_row_stat* const* first = plan.first;
     hipFunction_t function = nullptr;
-    if (!cached_kernels(src.str(), {"tc_fused_row_statistics"}, &function)) return TC_OK;
+    if (!cached_kernels(plan.source, {"tc_fused_row_statistics"}, &function)) return TC_OK;
     TC_STREAM(s);
     CompiledArgsOf args{};
     for (uint32_t k = 0; k < input_count; k++) args.in[k] = inputs[k];
     for (uint32_t k = 0; k < output_count; k++) args.out[k] = outputs[k];
-    int status = to_device_places(places, place_count, args.places);
+    status = to_device_places(places, place_count, args.places);
     if (status != TC_OK) return status;
     for (size_t c = 0; c < constants.size(); c++) args.constants[c] = constants[c];
     struct {
@@ -1133,17 +1385,44 @@ int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
     }
     uint32_t rows32 = static_cast<uint32_t>(rows), cols32 = static_cast<uint32_t>(cols);
     void* params[] = {&args, &where, &rows32, &cols32};
-    // Four workgroups a CU, each wave walking rows: enough loads in flight
-    // for HBM, while the rows in flight stay few enough that a row's second
-    // read, for the program, finds it in the caches (layer norm over
-    // 8192 x 8192 f32: 3.10 TB/s, against 2.91 at eight a CU; before the
-    // moments took one pass, 2.80 against 2.13 at two a CU and 2.65 with a
-    // wave for every row).
-    const uint64_t wanted = (rows + 3) / 4, cap = static_cast<uint64_t>(compute_units()) * 4;
+    // The general form: four workgroups a CU, each wave walking rows:
+    // enough loads in flight for HBM, while the rows in flight stay few
+    // enough that a row's second read, for the program, finds it in the
+    // caches (layer norm over 8192 x 8192 f32: 3.10 TB/s, against 2.91 at
+    // eight a CU).  The held form reads each row once, so it takes eight
+    // (the same layer norm: 4.97 TB/s at eight, 4.90 at four, 4.96 at two;
+    // streaming stores measured no faster).
+    const uint64_t wanted = (rows + 3) / 4,
+                   cap = static_cast<uint64_t>(compute_units()) * (plan.held ? 8 : 4);
     const uint32_t blocks = static_cast<uint32_t>(wanted < cap ? wanted : cap);
     count_dispatch();
     const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);
     if (error != hipSuccess) return fail(TC_DEVICE, std::string("fused with statistics: ") + hipGetErrorString(error));
     *done = true;
+    return TC_OK;
+}
+
+using tc::RowStatisticsPlan;
+using tc::plan_row_statistics;
+
+extern "C" int tc_fused_with_statistics_source(uint32_t dtype, const tc_encoded* code, uint32_t count,
+                                               const tc_place* places, uint32_t place_count,
+                                               const void* const* inputs, uint32_t input_count, uint64_t rows,
+                                               uint64_t cols, const tc_row_stat* statistics,
+                                               uint32_t statistic_count, char* out, uint64_t capacity,
+                                               uint64_t* length) {
+    RowStatisticsPlan plan;
+    const int status = plan_row_statistics(dtype, code, count, places, place_count, inputs, input_count, nullptr,
+                                           rows, cols, statistics, statistic_count, &plan);
+    if (status != TC_OK) return status;
+    if (plan.source.empty()) {
+        return fail(TC_UNSUPPORTED, "fused with statistics source: the program does not take the one-kernel form");
+    }
+    *length = plan.source.size();
+    if (out != nullptr && capacity > 0) {
+        const size_t n = plan.source.size() < capacity - 1 ? plan.source.size() : capacity - 1;
+        memcpy(out, plan.source.data(), n);
+        out[n] = '\0';
+    }
     return TC_OK;
 }

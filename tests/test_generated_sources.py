@@ -1,0 +1,100 @@
+"""The kernels the runtime compiler builds from a program, compiled on the
+CPU from the library's own generated source (hipcc cross-compiles for
+gfx950) with the flags it hands the runtime compiler: every instance must
+compile, and none may keep anything in scratch memory.
+
+`tc_fused_with_statistics` (Kernels::fused_with_statistics,
+kernels.rs:1103-1113) compiles a program with its row statistics into one
+kernel from the program's second appearance; for a statistic of a
+row-major matrix the kernel holds each row in registers, reads it once, and
+feeds the program's loads of that matrix from the registers.  These check
+the source of both forms."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from tensorcrate_amd import _build, lib
+from tests.common import Code, column_broadcast, identity_place
+
+CSRC = Path(__file__).resolve().parent.parent / "tensorcrate_amd" / "csrc"
+RUNTIME_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-Xclang", "-target-feature",
+                 "-Xclang", "-packed-fp32-ops"]
+
+
+def layer_norm(dtype, cols):
+    """(x - mean) / sqrt(deviations / cols + 1e-5) * gamma, gamma a row
+    vector: the bench's program."""
+    code = Code()
+    x = code.load(0, 0, dtype)
+    gamma = code.load(1, 1, dtype)
+    mean = code.load(2, 2, dtype)
+    deviations = code.load(2, 3, dtype)
+    variance = code.binary(lib.ADD, code.binary(lib.MUL, deviations, code.const(np.float32(1.0 / cols))),
+                           code.const(1e-5))
+    root = code.unary(13, variance)
+    code.store(code.binary(lib.MUL, code.binary(lib.DIV, code.binary(lib.SUB, x, mean), root), gamma), dtype, 0)
+    return code.code
+
+
+def statistics_source(dtype, code, places, rows, cols, source_ptr, stats):
+    enc, pl = lib._program(code, places)
+    inputs = (ctypes.c_void_p * 2)(source_ptr, 0x2000)
+    table = (lib.Statistic * len(stats))()
+    for i, (which, place) in enumerate(stats):
+        _, spl = lib._program([], [place])
+        table[i].source, table[i].source_len, table[i].source_dtype = source_ptr, rows * cols, dtype
+        table[i].which = which
+        table[i].place = spl[0]
+    length = ctypes.c_uint64()
+    lib.call("tc_fused_with_statistics_source", dtype, enc, len(code), pl, len(places), inputs, 2, rows, cols,
+             table, len(stats), None, 0, ctypes.byref(length))
+    out = ctypes.create_string_buffer(length.value + 1)
+    lib.call("tc_fused_with_statistics_source", dtype, enc, len(code), pl, len(places), inputs, 2, rows, cols,
+             table, len(stats), out, length.value + 1, ctypes.byref(length))
+    return out.value.decode()
+
+
+def compile_kernel(tmp_path, name, source):
+    try:
+        compiler = _build.hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc is not installed")
+    path = tmp_path / f"{name}.hip"
+    path.write_text("#include <hip/hip_runtime.h>\n" + source)
+    target = tmp_path / f"{name}.s"
+    result = subprocess.run([compiler, *RUNTIME_FLAGS, f"-I{CSRC}", "--cuda-device-only", "-S", str(path), "-o",
+                             str(target)], capture_output=True, text=True)
+    assert result.returncode == 0, result.stderr[-4000:]
+    return target.read_text()
+
+
+@pytest.mark.parametrize("dtype,cols,held", [(lib.F32, 8192, True), (lib.F32, 4100, True), (lib.BF16, 1024, True),
+                                             (lib.F16, 8192, True), (lib.F32, 777, False), (lib.F32, 8300, False)])
+def test_statistics_kernels_compile_without_scratch(tmp_path, dtype, cols, held):
+    rows = 64
+    places = [identity_place(rows, cols), (0, 1, 0, [], []), column_broadcast(rows)]
+    whole = identity_place(rows, cols)
+    source = statistics_source(dtype, layer_norm(dtype, cols), places, rows, cols, 0x10000,
+                               [(lib.STAT_MEAN, whole), (lib.STAT_DEVIATIONS, whole)])
+    # The held form reads the row as 16-byte packs and feeds the program's
+    # load of x from them.
+    assert ("const float (&held)" in source) == held
+    if held:
+        assert re.search(r"v\d+\[e\] = held\[e\];", source)
+    text = compile_kernel(tmp_path, "statistics", source)
+    assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
+
+
+def test_a_misaligned_or_offset_source_takes_the_general_form(tmp_path):
+    rows, cols = 16, 1024
+    places = [identity_place(rows, cols), (0, 1, 0, [], []), column_broadcast(rows)]
+    whole = identity_place(rows, cols)
+    stats = [(lib.STAT_MEAN, whole), (lib.STAT_DEVIATIONS, whole)]
+    aligned = statistics_source(lib.F32, layer_norm(lib.F32, cols), places, rows, cols, 0x10000, stats)
+    misaligned = statistics_source(lib.F32, layer_norm(lib.F32, cols), places, rows, cols, 0x10004, stats)
+    assert "const float (&held)" in aligned and "const float (&held)" not in misaligned

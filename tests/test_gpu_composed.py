@@ -188,7 +188,7 @@ def test_row_sums_of_a_repeated_program_run_as_one_compiled_kernel(dtype):
     assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
 
 
-@pytest.mark.parametrize("shape", [(300, 777), (40, 8300)])
+@pytest.mark.parametrize("shape", [(300, 777), (40, 8300), (300, 1024), (64, 8192), (33, 4100)])
 @pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
 def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # From the program's second appearance its statistics and the program run
@@ -198,9 +198,11 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # program; the moments fold in another order than the oracle's, which
     # moves the statistics by their last place at most.  Rows of 777 are
     # ragged against a wave's 64 lanes and its 16-load batches; rows of 8300
-    # take more than eight batches a pass.  The kernel's source does not
-    # depend on the shape, so the second shape may find it compiled already;
-    # either way the last call is one launch.
+    # take more than eight batches a pass: both take the general form.  Rows
+    # of 1024 and 8192 (and of 4100 in f32, whose last packs fall past the
+    # row on some lanes) take the form that holds the row in registers and
+    # feeds the program's load of x from them.  A shape may find its kernel
+    # compiled already; either way the last call is one launch.
     import ctypes
 
     rows, cols = shape
@@ -235,3 +237,47 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
         compiled.append(count.value)
     assert compiled[1] - compiled[0] in (0, 1) and compiled[2] == compiled[1]
     assert launches == 1
+
+
+@pytest.mark.parametrize("cols", [777, 1024, 8192])
+@pytest.mark.parametrize("offset", [1000.0, 10000.0])
+def test_row_statistics_of_offset_rows_keep_two_pass_accuracy(offset, cols):
+    # Rows whose mean is large against their spread (offset + U(-1, 1)): the
+    # one-kernel statistics, in either of their forms (the row held in
+    # registers for 1024 and 8192 columns, the batched walk for 777), shift
+    # each row by its first element, and are at least as close to the exact
+    # moments as the reference's own two passes (the oracle's sequential f32
+    # mean, then squared deviations from it, statistics/mod.rs:419-441), or
+    # within 1e-5 of them relative.  The composition's moments (the first
+    # call) come from the axis-reduction kernels' variance fold, which merges
+    # unshifted chunk moments: it is held to the f32 accumulation bound
+    # cols * 2^-24 of the deviations instead.
+    import ctypes
+
+    rows = 64
+    rng = np.random.default_rng(int(offset) + cols)
+    xs = (offset + rng.uniform(-1, 1, rows * cols)).astype(np.float32)
+    code = Code()
+    code.store(code.load(1, 1, lib.F32), lib.F32, 0)
+    code.store(code.load(1, 2, lib.F32), lib.F32, 1)
+    places = [identity_place(rows, cols), column_broadcast(rows)]
+    whole = identity_place(rows, cols)
+    dx = lib.Buffer.of(xs)
+    exact = xs.reshape(rows, cols).astype(np.float64)
+    exact_mean = exact.mean(axis=1)
+    exact_dev = ((exact - exact_mean[:, None]) ** 2).sum(axis=1)
+    ref_mean, ref_dev = oracle.row_moments(lib.F32, lib.F32, xs, whole, rows, cols)
+    ref_mean_err = np.abs(ref_mean.astype(np.float64) - exact_mean)
+    ref_dev_err = np.abs(ref_dev.astype(np.float64) - exact_dev)
+    for call in range(2):  # composed, then the compiled kernel
+        means, devs = lib.Buffer(rows * cols * 4), lib.Buffer(rows * cols * 4)
+        lib.fused_with_statistics(lib.F32, code.code, places, [(dx, xs.size)], [(means, rows * cols),
+                                                                               (devs, rows * cols)], rows, cols,
+                                  [(dx, xs.size, lib.F32, whole, "mean"), (dx, xs.size, lib.F32, whole, "deviations")])
+        got_mean = means.download(np.float32, rows * cols).reshape(rows, cols)[:, 0].astype(np.float64)
+        got_dev = devs.download(np.float32, rows * cols).reshape(rows, cols)[:, 0].astype(np.float64)
+        mean_err, dev_err = np.abs(got_mean - exact_mean), np.abs(got_dev - exact_dev)
+        assert np.all(mean_err <= np.maximum(2 * ref_mean_err, 4 * np.spacing(np.float32(offset)))), call
+        relative = 1e-5 if call else cols * 2.0 ** -24
+        assert np.all(dev_err <= np.maximum(2 * ref_dev_err, relative * exact_dev)), \
+            (call, dev_err.max(), ref_dev_err.max())
