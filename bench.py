@@ -292,39 +292,58 @@ def gemm(kind: str, m: int, k: int, n: int, seed: int, sigma, steps: int, warmup
     return Product(kind, m, k, n, seed, sigma).time(steps, warmup, cpu)
 
 
+class DenseLayer:
+    """relu(x . w + bias) over synthetic operands, as the calls the bench
+    times: the program in the product kernel's epilogue
+    (`tc_matmul_epilogue`, one kernel, the product never in HBM), unfused
+    (`tc_matmul`, then `tc_fused` over the stored product), and the product
+    alone."""
+
+    def __init__(self, kind: str, m: int, k: int, n: int):
+        rng = np.random.default_rng(11)
+        code = KIND[kind]
+        size = 4 if kind == "f32" else 2
+        self.hx = host_matrix(kind, m, k, rng, 1 / np.sqrt(k))
+        self.hw = host_matrix(kind, k, n, rng, 1 / np.sqrt(k))
+        self.hbias = host_matrix(kind, 1, n, rng).reshape(n)
+        x, w, bias = lib.Buffer.of(self.hx), lib.Buffer.of(self.hw), lib.Buffer.of(self.hbias)
+        out, product = lib.Buffer(m * n * size), lib.Buffer(m * n * size)
+        self.buffers = [x, w, bias, out, product]
+        self.program = [(0, 0, 0, 0, code, 0, 0.0), (0, 1, 1, 1, code, 0, 0.0), (2, lib.ADD, 2, 0, 1, 0, 0.0),
+                        (1, 0, 3, 0, 0, 0, 0.0), (4, lib.MAX, 4, 2, 3, 0, 0.0), (5, 0, 0, 4, code, 0, 0.0)]
+        program = self.program
+        enc, places = lib._program(program, [(0, 1, 1, [m], [n]), (0, 1, 0, [], [])])
+        bias_in, bias_len = lib._buffers([(bias, n)])
+        both_in, both_len = lib._buffers([(product, m * n), (bias, n)])
+        outs, out_lens = lib._buffers([(out, m * n)])
+
+        def fused():
+            lib.call("tc_matmul_epilogue", code, enc, len(program), places, 2, m, k, n, x.ptr, w.ptr, bias_in,
+                     bias_len, 1, outs, out_lens, 1)
+
+        def unfused():
+            lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, x.ptr, w.ptr, product.ptr)
+            lib.call("tc_fused", code, enc, len(program), places, 2, both_in, both_len, 2, outs, out_lens, 1, m, n)
+
+        def product_only():
+            lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, x.ptr, w.ptr, product.ptr)
+
+        self.fused, self.unfused, self.product_only = fused, unfused, product_only
+
+    def free(self) -> None:
+        for buffer in self.buffers:
+            buffer.free()
+
+
 def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> list[dict]:
-    """relu(x . w + bias) two ways: the program in the product kernel's
-    epilogue (`tc_matmul_epilogue`, one kernel, the product never in HBM)
-    and unfused (`tc_matmul`, then `tc_fused` over the stored product).
-    Both lines count the product's 2 m n k FLOP only."""
+    """relu(x . w + bias) two ways, and the product alone (`DenseLayer`).
+    Every line counts the product's 2 m n k FLOP only."""
     from oracle import binding as oracle  # the CPU baseline's restatement
 
-    rng = np.random.default_rng(11)
+    layer = DenseLayer(kind, m, k, n)
     code = KIND[kind]
-    size = 4 if kind == "f32" else 2
-    hx = host_matrix(kind, m, k, rng, 1 / np.sqrt(k))
-    hw = host_matrix(kind, k, n, rng, 1 / np.sqrt(k))
-    hbias = host_matrix(kind, 1, n, rng).reshape(n)
-    x, w, bias = lib.Buffer.of(hx), lib.Buffer.of(hw), lib.Buffer.of(hbias)
-    out, product = lib.Buffer(m * n * size), lib.Buffer(m * n * size)
-    program = [(0, 0, 0, 0, code, 0, 0.0), (0, 1, 1, 1, code, 0, 0.0), (2, lib.ADD, 2, 0, 1, 0, 0.0),
-               (1, 0, 3, 0, 0, 0, 0.0), (4, lib.MAX, 4, 2, 3, 0, 0.0), (5, 0, 0, 4, code, 0, 0.0)]
-    enc, places = lib._program(program, [(0, 1, 1, [m], [n]), (0, 1, 0, [], [])])
-    bias_in, bias_len = lib._buffers([(bias, n)])
-    both_in, both_len = lib._buffers([(product, m * n), (bias, n)])
-    outs, out_lens = lib._buffers([(out, m * n)])
-
-    def fused():
-        lib.call("tc_matmul_epilogue", code, enc, len(program), places, 2, m, k, n, x.ptr, w.ptr, bias_in, bias_len,
-                 1, outs, out_lens, 1)
-
-    def unfused():
-        lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, x.ptr, w.ptr, product.ptr)
-        lib.call("tc_fused", code, enc, len(program), places, 2, both_in, both_len, 2, outs, out_lens, 1, m, n)
-
-    def product_only():
-        lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, x.ptr, w.ptr, product.ptr)
-
+    hx, hw, hbias, program = layer.hx, layer.hw, layer.hbias, layer.program
+    fused, unfused, product_only = layer.fused, layer.unfused, layer.product_only
     flops = 2.0 * m * n * k
     # The CPU baseline: the oracle's product-then-program (the Host's
     # run_matmul, fused/mod.rs:1143-1215) over a band of rows of x.
@@ -349,9 +368,55 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
                       "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind],
                                    "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK[kind], "traffic": None},
                       "cpu_baseline": baseline})
-    for buffer in (x, w, bias, out, product):
-        buffer.free()
+    layer.free()
     return lines
+
+
+class LayerNorm:
+    """(x - mean) / sqrt(deviations / cols + 1e-5) * gamma over the rows of an
+    f32 rows x cols matrix x, as the two calls the bench times on a given x:
+    `one_kernel` (`tc_fused_with_statistics`, one compiled kernel from the
+    program's second appearance) and `composed` (`tc_row_moments`, then
+    `tc_fused`)."""
+
+    def __init__(self, rows: int, cols: int, rng):
+        self.hgamma = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+        gamma = lib.Buffer.of(self.hgamma)
+        nbytes = rows * cols * 4
+        out, means, devs = lib.Buffer(nbytes), lib.Buffer(rows * 4), lib.Buffer(rows * 4)
+        self.buffers = [gamma, out, means, devs]
+        f32 = lib.F32
+        self.program = program = [
+            (0, 0, 0, 0, f32, 0, 0.0), (0, 1, 1, 1, f32, 0, 0.0), (0, 2, 2, 2, f32, 0, 0.0),
+            (0, 2, 3, 3, f32, 0, 0.0), (1, 0, 4, 0, 0, 0, float(np.float32(1.0 / cols))),
+            (2, lib.MUL, 3, 3, 4, 0, 0.0), (1, 0, 4, 0, 0, 0, 1e-5), (2, lib.ADD, 3, 3, 4, 0, 0.0),
+            (3, 13, 3, 3, 0, 0, 0.0), (2, lib.SUB, 0, 0, 2, 0, 0.0), (2, lib.DIV, 0, 0, 3, 0, 0.0),
+            (2, lib.MUL, 0, 0, 1, 0, 0.0), (5, 0, 0, 0, f32, 0, 0.0)]
+        whole = (0, 1, 1, [rows], [cols])
+        place_list = [whole, (0, 1, 0, [], []), (0, 0, 1, [rows], [1])]
+        enc, places = lib._program(program, place_list)
+        _, whole_place = lib._program([], [whole])
+        outs, out_lens = lib._buffers([(out, rows * cols)])
+
+        def one_kernel(x):
+            ins, in_lens = lib._buffers([(x, rows * cols), (gamma, cols)])
+            stats = (lib.Statistic * 2)()
+            for i, which in enumerate((lib.STAT_MEAN, lib.STAT_DEVIATIONS)):
+                stats[i].source, stats[i].source_len, stats[i].source_dtype = x.ptr, rows * cols, f32
+                stats[i].which, stats[i].place = which, whole_place[0]
+            lib.call("tc_fused_with_statistics", f32, enc, len(program), places, 3, ins, in_lens, 2, outs, out_lens,
+                     1, rows, cols, stats, 2)
+
+        def composed(x):
+            lib.call("tc_row_moments", f32, f32, x.ptr, rows * cols, whole_place, rows, cols, means.ptr, devs.ptr)
+            ins, in_lens = lib._buffers([(x, rows * cols), (gamma, cols), (means, rows), (devs, rows)])
+            lib.call("tc_fused", f32, enc, len(program), places, 3, ins, in_lens, 4, outs, out_lens, 1, rows, cols)
+
+        self.one_kernel, self.composed = one_kernel, composed
+
+    def free(self) -> None:
+        for buffer in self.buffers:
+            buffer.free()
 
 
 def layer_norm(rows: int, cols: int, steps: int, warmup: int) -> list[dict]:
@@ -364,37 +429,13 @@ def layer_norm(rows: int, cols: int, steps: int, warmup: int) -> list[dict]:
     the result written once; inputs rotate past the Infinity Cache."""
     from oracle import binding as oracle  # the CPU baseline's restatement
 
+    f32 = lib.F32
     rng = np.random.default_rng(17)
     nbytes = rows * cols * 4
     xs = rotation(lambda: lib.Buffer.of(rng.uniform(-3, 3, rows * cols).astype(np.float32)), nbytes)
-    hgamma = rng.uniform(0.5, 1.5, cols).astype(np.float32)
-    gamma = lib.Buffer.of(hgamma)
-    out, means, devs = lib.Buffer(nbytes), lib.Buffer(rows * 4), lib.Buffer(rows * 4)
-    f32 = lib.F32
-    program = [(0, 0, 0, 0, f32, 0, 0.0), (0, 1, 1, 1, f32, 0, 0.0), (0, 2, 2, 2, f32, 0, 0.0),
-               (0, 2, 3, 3, f32, 0, 0.0), (1, 0, 4, 0, 0, 0, float(np.float32(1.0 / cols))),
-               (2, lib.MUL, 3, 3, 4, 0, 0.0), (1, 0, 4, 0, 0, 0, 1e-5), (2, lib.ADD, 3, 3, 4, 0, 0.0),
-               (3, 13, 3, 3, 0, 0, 0.0), (2, lib.SUB, 0, 0, 2, 0, 0.0), (2, lib.DIV, 0, 0, 3, 0, 0.0),
-               (2, lib.MUL, 0, 0, 1, 0, 0.0), (5, 0, 0, 0, f32, 0, 0.0)]
-    whole = (0, 1, 1, [rows], [cols])
-    place_list = [whole, (0, 1, 0, [], []), (0, 0, 1, [rows], [1])]
-    enc, places = lib._program(program, place_list)
-    _, whole_place = lib._program([], [whole])
-    outs, out_lens = lib._buffers([(out, rows * cols)])
-
-    def one_kernel(x):
-        ins, in_lens = lib._buffers([(x, rows * cols), (gamma, cols)])
-        stats = (lib.Statistic * 2)()
-        for i, which in enumerate((lib.STAT_MEAN, lib.STAT_DEVIATIONS)):
-            stats[i].source, stats[i].source_len, stats[i].source_dtype = x.ptr, rows * cols, f32
-            stats[i].which, stats[i].place = which, whole_place[0]
-        lib.call("tc_fused_with_statistics", f32, enc, len(program), places, 3, ins, in_lens, 2, outs, out_lens, 1,
-                 rows, cols, stats, 2)
-
-    def composed(x):
-        lib.call("tc_row_moments", f32, f32, x.ptr, rows * cols, whole_place, rows, cols, means.ptr, devs.ptr)
-        ins, in_lens = lib._buffers([(x, rows * cols), (gamma, cols), (means, rows), (devs, rows)])
-        lib.call("tc_fused", f32, enc, len(program), places, 3, ins, in_lens, 4, outs, out_lens, 1, rows, cols)
+    norm = LayerNorm(rows, cols, rng)
+    program, hgamma = norm.program, norm.hgamma
+    one_kernel, composed = norm.one_kernel, norm.composed
 
     # The CPU baseline: the oracle's row moments, then its program, over a
     # band of rows.
@@ -416,8 +457,9 @@ def layer_norm(rows: int, cols: int, steps: int, warmup: int) -> list[dict]:
         ms = timed_graph(rotating(xs, fn), steps, warmup)
         lines.append(with_cpu(hbm_line(f"layer norm f32 [{rows}x{cols}] (fused_with_statistics), {name}",
                                        2.0 * nbytes, ms, f"layernorm {short}"), baseline))
-    for buffer in xs + [gamma, out, means, devs]:
+    for buffer in xs:
         buffer.free()
+    norm.free()
     return lines
 
 
@@ -846,8 +888,9 @@ def traffic_probe() -> None:
     1 GiB read and 1 GiB written each, the counters' calibration), three
     launches of the headline product, three of the f16 16384 x 1024 x 4096
     product, three each of the f32 4096^3 product in its PLAIN, LEFT and
-    RIGHT forms, then one call of every bandwidth workload in the order
-    ``traffic_workloads`` lists them."""
+    RIGHT forms, then one call of every bandwidth, fused and training
+    workload in the order ``traffic_workloads`` lists them, each between two
+    marker launches (a 1 x 1 ``tc_flip``) after its untimed calls."""
     n = 1 << 28
     src, dst = lib.Buffer(4 * n), lib.Buffer(4 * n)
     lib.call("tc_fill", src.ptr, n, 4, ctypes.byref(ctypes.c_float(1.0)))
@@ -890,16 +933,30 @@ def traffic_probe() -> None:
     lib.sync()
     for buffer in (a, b, c):
         buffer.free()
-    for workload, run in traffic_workloads():
+    # Each workload's dispatches between two markers (a 1 x 1 flip, a kernel
+    # none of them uses), after its untimed calls: a workload of several
+    # kernels (the MLP step, the composed layer norm) is the sum between.
+    one, flipped = lib.Buffer(16), lib.Buffer(16)
+
+    def marker():
+        lib.call("tc_flip", 4, one.ptr, 1, 1, flipped.ptr)
+        lib.sync()
+    for workload, run, untimed in traffic_workloads():
         log(f"probe: {workload}")
+        for _ in range(untimed):
+            run()
+        lib.sync()
+        marker()
         run()
         lib.sync()
+        marker()
     log("traffic probe done")
 
 
 def traffic_workloads():
-    """(workload, call) for every bandwidth line, in a fixed order, each call
-    on inputs made beforehand (so the probe's dispatches are the calls')."""
+    """(workload, call, untimed calls first) for every bandwidth line and the
+    fused and training lines, in a fixed order, each call on inputs made
+    beforehand (so the probe's dispatches are the calls')."""
     rng = np.random.default_rng(2)
     x = Tensor.from_numpy(rng.standard_normal((256, 512, 512), dtype=np.float32))
     y = Tensor.from_numpy(rng.uniform(-1, 1, (1, 512, 1)).astype(np.float32))
@@ -955,6 +1012,36 @@ def traffic_workloads():
          lambda: lib.call("tc_vecmat", lib.F32, 8192, 8192, vec.ptr, mat.ptr, yv.ptr)),
         ("dot, f32 64 Mi elements", lambda: lib.call("tc_dot", lib.F32, da.ptr, db.ptr, 64 << 20, dot_out.ptr)),
         ("transpose, f32 [4096x4096]", lambda: lib.call("tc_transpose", 4, 4096, 4096, sq.ptr, sq_t.ptr)),
+    ]
+    # The workloads of several kernels or compiled programs, each run untimed
+    # first as many times as its timed line's warmup needs (the programs
+    # compile on their second appearance).
+    norm = LayerNorm(8192, 8192, np.random.default_rng(17))
+    ln_x = lib.Buffer.of(rng.uniform(-3, 3, 8192 * 8192).astype(np.float32))
+    dense_bf16, dense_f32 = DenseLayer("bf16", 8192, 8192, 8192), DenseLayer("f32", 4096, 1024, 4096)
+    from oracle import mlp  # the synthetic network's generator only
+
+    widths = (1024, 4096, 4096, 1024)
+    weights, biases = mlp.he_init(widths, 4)
+    mx, my = mlp.batch_of(widths, 4096, 4)
+    net = lib.Mlp(widths, 4096, weights, biases, mx, my, 1e-3)
+    count = sum(widths[l] * widths[l + 1] + widths[l + 1] for l in range(3))
+    params, grads = lib.Buffer(4 * count), lib.Buffer(4 * count)
+    lib.call("tc_fill", params.ptr, count, 4, ctypes.byref(ctypes.c_float(0.5)))
+    lib.call("tc_fill", grads.ptr, count, 4, ctypes.byref(ctypes.c_float(0.25)))
+    rule = Adam(1e-3)
+    keep += (norm, ln_x, dense_bf16, dense_f32, net, params, grads, rule)
+    calls = [(name, call, 0) for name, call in calls] + [
+        ("layer norm f32 [8192x8192] (fused_with_statistics), statistics and program in one kernel",
+         lambda: norm.one_kernel(ln_x), 2),
+        ("layer norm f32 [8192x8192] (fused_with_statistics), composed: row moments, then the program",
+         lambda: norm.composed(ln_x), 2),
+        ("Adam update, 25175040 f32 parameters (fused program)", lambda: rule.update(params, grads, 1, count), 3),
+        ("MLP training step 1024-4096-4096-1024, batch 4096, f32, tape + Adam (configs[4])", net.step, 3),
+        ("bf16 dense layer relu(x w + b) 8192x8192x8192, in the product's epilogue", dense_bf16.fused, 2),
+        ("bf16 dense layer relu(x w + b) 8192x8192x8192, unfused: product, then program", dense_bf16.unfused, 2),
+        ("f32 dense layer relu(x w + b) 4096x1024x4096, in the product's epilogue", dense_f32.fused, 2),
+        ("f32 dense layer relu(x w + b) 4096x1024x4096, unfused: product, then program", dense_f32.unfused, 2),
     ]
     traffic_workloads.keep = keep
     return calls

@@ -92,7 +92,8 @@ int vector_product(uint32_t dtype, bool row_vector, bool accumulate, uint64_t ro
 // does not compile).
 std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                            const tc_place* places, std::vector<float>* constants);
-bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out);
+bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,
+                      uint32_t* scratch = nullptr);
 // Whether hiprtc in this process compiles with the code-object compiler of
 // the ROCm the library was built against (fused.hip).
 bool runtime_compiler_is_ours();

@@ -29,6 +29,7 @@
 #include <mutex>
 #include <sstream>
 #include <unordered_map>
+#include <utility>
 
 #include "common.hpp"
 #include "program.hpp"
@@ -314,6 +315,15 @@ struct Compiled {
     bool failed = false;
     hipModule_t module = nullptr;
     std::vector<hipFunction_t> functions;
+    // Each function's scratch memory a lane, from the compiler's resource
+    // report (UINT32_MAX when it named none for the function).
+    std::vector<uint32_t> scratch;
+    // The code object the module was loaded from.  The loader reports this
+    // buffer to tools (profilers, debuggers) as the loaded code object's
+    // storage and they read it back while the module lives, so it lives as
+    // long as the module: for the process, as cached modules are never
+    // unloaded.
+    std::vector<char> image;
 };
 
 // Programs too large for kernel arguments, resident on the device for the
@@ -436,9 +446,37 @@ std::mutex compiled_mutex;
 std::unordered_map<std::string, Compiled> compiled_programs;
 uint64_t compiled_count = 0;
 
-// hiprtc's flags: the library's own (see _build.py).
+// hiprtc's flags: the library's own (see _build.py), and the compiler's
+// per-function resource report into the compile log, where each kernel's
+// scratch use is read (`scratch_by_function`).
 const char* const kCompileFlags[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
-                                     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+                                     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                                     "-Rpass-analysis=kernel-resource-usage"};
+
+// The scratch bytes a lane each function of a compile log uses: the log's
+// resource remarks name a function ("Function Name: <mangled>") and then
+// report its "ScratchSize [bytes/lane]: <n>".
+std::unordered_map<std::string, uint32_t> scratch_by_function(const std::string& log) {
+    std::unordered_map<std::string, uint32_t> out;
+    static const std::string kName = "remark: Function Name: ", kScratch = "ScratchSize [bytes/lane]: ";
+    std::string current;
+    size_t at = 0;
+    while (at < log.size()) {
+        size_t end = log.find('\n', at);
+        if (end == std::string::npos) end = log.size();
+        const std::string line = log.substr(at, end - at);
+        size_t found = line.find(kName);
+        if (found != std::string::npos) {
+            const size_t first = found + kName.size();
+            current = line.substr(first, line.find(' ', first) - first);
+        } else if ((found = line.find(kScratch)) != std::string::npos && !current.empty()) {
+            out[current] = static_cast<uint32_t>(strtoul(line.c_str() + found + kScratch.size(), nullptr, 10));
+            current.clear();
+        }
+        at = end + 1;
+    }
+    return out;
+}
 
 // Compile `source` with the embedded headers and look up `kernels`, each an
 // extern "C" name or a template-id whose lowered name hiprtc reports.
@@ -456,7 +494,13 @@ bool compile_program(const std::string& source, const std::vector<std::string>& 
               HIPRTC_SUCCESS;
     std::vector<char> binary;
     std::vector<std::string> lowered;
+    std::unordered_map<std::string, uint32_t> scratch;
     if (ok) {
+        size_t log_size = 0;
+        if (hiprtcGetProgramLogSize(program, &log_size) == HIPRTC_SUCCESS && log_size > 0) {
+            std::string log(log_size, '\0');
+            if (hiprtcGetProgramLog(program, &log[0]) == HIPRTC_SUCCESS) scratch = scratch_by_function(log);
+        }
         size_t size = 0;
         ok = hiprtcGetCodeSize(program, &size) == HIPRTC_SUCCESS && size > 0;
         if (ok) {
@@ -473,7 +517,8 @@ bool compile_program(const std::string& source, const std::vector<std::string>& 
     }
     hiprtcDestroyProgram(&program);
     if (!ok) return false;
-    if (hipModuleLoadData(&out->module, binary.data()) != hipSuccess) {
+    out->image = std::move(binary);
+    if (hipModuleLoadData(&out->module, out->image.data()) != hipSuccess) {
         (void)hipGetLastError();
         return false;
     }
@@ -484,6 +529,8 @@ bool compile_program(const std::string& source, const std::vector<std::string>& 
             return false;
         }
         out->functions.push_back(function);
+        const auto known = scratch.find(name);
+        out->scratch.push_back(known == scratch.end() ? UINT32_MAX : known->second);
     }
     return true;
 }
@@ -491,7 +538,8 @@ bool compile_program(const std::string& source, const std::vector<std::string>& 
 // The cached kernels of `source` for this device, compiled on the source's
 // second request; false (run something else) before that or if it does not
 // compile.
-bool cached_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out) {
+bool cached_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,
+                    uint32_t* scratch = nullptr) {
     int device = 0;
     (void)hipGetDevice(&device);
     std::lock_guard<std::mutex> lock(compiled_mutex);
@@ -505,7 +553,10 @@ bool cached_kernels(const std::string& source, const std::vector<std::string>& k
         }
         compiled_count++;
     }
-    for (size_t k = 0; k < entry.functions.size(); k++) out[k] = entry.functions[k];
+    for (size_t k = 0; k < entry.functions.size(); k++) {
+        out[k] = entry.functions[k];
+        if (scratch != nullptr) scratch[k] = entry.scratch[k];
+    }
     return true;
 }
 
@@ -804,8 +855,9 @@ std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtyp
     return group_body(code, count, dtype, product_input, elems, places, constants);
 }
 
-bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out) {
-    return cached_kernels(source, kernels, out);
+bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,
+                      uint32_t* scratch) {
+    return cached_kernels(source, kernels, out, scratch);
 }
 
 // hiprtc hands the compile to the code-object compiler library (comgr) that

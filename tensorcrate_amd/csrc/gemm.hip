@@ -41,8 +41,6 @@
 #include <string.h>
 
 #include <algorithm>
-#include <mutex>
-#include <unordered_map>
 
 #include <type_traits>
 
@@ -568,27 +566,6 @@ std::string epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t cou
            body + "  }\n};\n";
 }
 
-// Whether a compiled kernel keeps anything in scratch memory (a private
-// segment), asked of the runtime once per function.  The four-wave kernel's
-// matrix-core steps are inline assembly on accumulators pinned in AGPRs, and
-// the code around them supplies their hazard cover; an instance whose
-// generated epilogue made the compiler spill, or move the accumulators to
-// scratch, breaks those assumptions, so such an instance is never launched
-// (the eight-wave kernels take the product instead).
-bool uses_scratch(hipFunction_t function) {
-    static std::mutex mutex;
-    static std::unordered_map<hipFunction_t, bool> known;
-    std::lock_guard<std::mutex> lock(mutex);
-    auto found = known.find(function);
-    if (found != known.end()) return found->second;
-    int bytes = 0;
-    if (hipFuncGetAttribute(&bytes, HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES, function) != hipSuccess) {
-        (void)hipGetLastError();
-        bytes = 1;  // unknown: treated as using scratch
-    }
-    return known.emplace(function, bytes != 0).first->second;
-}
-
 // The product kernels with `code` compiled into their epilogue, once the
 // program has been seen before: true when they were launched.
 bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, const void* a, const void* b,
@@ -619,7 +596,8 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     }
     small = ((m + 127) / 128) * ((n + 127) / 128);
     hipFunction_t functions[4] = {};
-    if (!compiled_kernels(source, kernels, functions)) return false;
+    uint32_t scratch[4] = {};
+    if (!compiled_kernels(source, kernels, functions, scratch)) return false;
     CompiledArgsOf args{};
     for (uint32_t slot = 1; slot < input_count; slot++) args.in[slot] = inputs[slot];
     for (uint32_t slot = 0; slot < output_count; slot++) args.out[slot] = outputs[slot];
@@ -633,7 +611,13 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     // 16-bit products over whole step pairs take the persistent kernels, as
     // plain ones do (launch_tiled16): the four-wave one when K is a multiple
     // of 128, else the eight-wave one.
-    const bool wide = kernels.size() == 4 && use_large && k % 128 == 0 && !uses_scratch(functions[3]);
+    // The four-wave kernel's matrix-core steps are inline assembly on
+    // accumulators pinned in AGPRs, with their hazard cover written around
+    // them; an instance whose epilogue made the compiler spill or move the
+    // accumulators to scratch memory (the compile's resource report says
+    // so) breaks those assumptions and is never launched: the eight-wave
+    // kernels take the product instead.
+    const bool wide = kernels.size() == 4 && use_large && k % 128 == 0 && scratch[3] == 0;
     const bool persistent = kernels.size() == 4 && use_large && ((k + 63) / 64) % 2 == 0;
     hipFunction_t function = dtype == TC_F32 ? functions[0]
                              : wide          ? functions[3]
