@@ -45,26 +45,29 @@ from tensorcrate_amd.tensor import Tensor  # noqa: E402
 
 HBM_PEAK = 8000.0  # GB/s, MI355X HBM3E
 # HBM bytes per launch of the headline product, from `rocprofv3 --pmc
-# FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --traffic-probe`,
-# scaled by what the counters read for a plain 1 GiB copy (fetch x 2.0,
-# write x 0.998): 2.017 GB read + 0.134 GB written (profiles/gemm_bf16_8192_traffic.md).
-HEADLINE_TRAFFIC = 2.151e9
-# HBM bytes per call of each bandwidth workload and of the other products,
-# from the same two counters over `bench.py --traffic-probe` with the same
-# calibration (profiles/bandwidth_traffic.md, profiles/gemm_bf16_8192_traffic.md):
-# the bandwidth workloads within 5% of their algorithmic bytes.
+# FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --traffic-probe
+# kernels`, scaled by what the counters read for a plain 1 GiB copy (fetch
+# x 2.0, write x 0.998): the back-to-back launches' 1.617 GB read + 0.134 GB
+# written (profiles/gemm_bf16_8192_traffic.md).
+HEADLINE_TRAFFIC = 1.751e9
+# HBM bytes per call of each other product, bandwidth workload (part
+# "kernels" of the probe) and fused or training workload (part "programs"),
+# from the same two counters with the same calibration
+# (profiles/gemm_bf16_8192_traffic.md, profiles/bandwidth_traffic.md,
+# profiles/fused_programs_traffic.md): the bandwidth workloads within 5% of
+# their algorithmic bytes.
 MEASURED_TRAFFIC = {
     "f16 GEMM 16384x1024x4096": 3.419e+08,
-    "f32 GEMM 4096x4096x4096": 8.246e+08,
-    "x*y, f32 [256,512,512] x [1,512,1]": 5.365e+08,
-    "t+z, f32 [256,512,512] + [256,1,512]": 5.407e+08,
-    "permute(0,2,1).contiguous, f32 [256,512,512]": 5.365e+08,
-    "slice [:,128:384,:].contiguous, f32": 2.683e+08,
+    "f32 GEMM 4096x4096x4096": 6.041e+08,
+    "x*y, f32 [256,512,512] x [1,512,1]": 5.364e+08,
+    "t+z, f32 [256,512,512] + [256,1,512]": 5.406e+08,
+    "permute(0,2,1).contiguous, f32 [256,512,512]": 5.364e+08,
+    "slice [:,128:384,:].contiguous, f32": 2.682e+08,
     "concat of two [256,256,512] halves on axis 1, f32": 5.366e+08,
-    "same-shape add, f32 64 Mi elements": 8.049e+08,
-    "sum_axes [2] of f32 [64x128x1024]": 3.367e+07,
+    "same-shape add, f32 64 Mi elements": 8.048e+08,
+    "sum_axes [2] of f32 [64x128x1024]": 3.366e+07,
     "var_axes [2] of f32 [64x128x1024]": 3.366e+07,
-    "sum_axes [0, 1] of f32 [64x128x1024]": 3.416e+07,
+    "sum_axes [0, 1] of f32 [64x128x1024]": 3.415e+07,
     "var_axes [0, 1] of f32 [64x128x1024]": 3.523e+07,
     "argmax axis 1 of f32 [64x128x1024]": 3.387e+07,
     "sum_axes [2] of f32 [1024x128x1024]": 5.38e+08,
@@ -76,6 +79,14 @@ MEASURED_TRAFFIC = {
     "vecmat, f32 [8192] . [8192x8192]": 2.71e+08,
     "dot, f32 64 Mi elements": 5.37e+08,
     "transpose, f32 [4096x4096]": 1.342e+08,
+    "layer norm f32 [8192x8192] (fused_with_statistics), statistics and program in one kernel": 5.379e+08,
+    "layer norm f32 [8192x8192] (fused_with_statistics), composed: row moments, then the program": 8.058e+08,
+    "Adam update, 25175040 f32 parameters (fused program)": 7.043e+08,
+    "MLP training step 1024-4096-4096-1024, batch 4096, f32, tape + Adam (configs[4])": 8.091e+09,
+    "bf16 dense layer relu(x w + b) 8192x8192x8192, in the product's epilogue": 1.854e+09,
+    "bf16 dense layer relu(x w + b) 8192x8192x8192, unfused: product, then program": 2.094e+09,
+    "f32 dense layer relu(x w + b) 4096x1024x4096, in the product's epilogue": 2.015e+08,
+    "f32 dense layer relu(x w + b) 4096x1024x4096, unfused: product, then program": 3.357e+08,
 }
 MFMA_PEAK = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}  # dense TFLOP/s
 KIND = {"bf16": lib.BF16, "f16": lib.F16, "f32": lib.F32}
@@ -356,17 +367,20 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
                         2.0 * band * k * n, "TFLOP/s",
                         f"rows 0..{band} of x: the oracle's single-thread product, then the program, linear in M",
                         1e12, min_seconds=1.0)
+    # x, w and the bias read once, relu(x w + b) written once.
+    algorithmic = (m * k + k * n + n + m * n) * (4 if kind == "f32" else 2)
     lines = []
     for name, short, fn in (("in the product's epilogue", "epilogue", fused),
                             ("unfused: product, then program", "unfused", unfused),
                             ("the product alone", "product", product_only)):
         ms = timed(fn, steps, warmup)
         achieved = flops / (ms * 1e-3) / 1e12
-        lines.append({"workload": f"{kind} dense layer relu(x w + b) {m}x{k}x{n}, {name}",
-                      "key": f"dense {kind} {m}x{k}x{n} {short}", "spread": spread(ms),
+        workload = f"{kind} dense layer relu(x w + b) {m}x{k}x{n}, {name}"
+        lines.append({"workload": workload, "key": f"dense {kind} {m}x{k}x{n} {short}", "spread": spread(ms),
                       "value": achieved, "unit": "TFLOP/s", "ms": ms,
                       "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK[kind],
-                                   "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK[kind], "traffic": None},
+                                   "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK[kind],
+                                   "traffic": MEASURED_TRAFFIC.get(workload), "bytes": algorithmic},
                       "cpu_baseline": baseline})
     layer.free()
     return lines
@@ -844,7 +858,9 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
               "key": "mlp step", "spread": spread(ms),
               "value": 1e3 / ms, "unit": "steps/s", "ms": ms,
               "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK["f32"], "unit": "TFLOP/s",
-                           "frac": achieved / MFMA_PEAK["f32"], "traffic": None},
+                           "frac": achieved / MFMA_PEAK["f32"],
+                           "traffic": MEASURED_TRAFFIC.get("MLP training step 1024-4096-4096-1024, batch 4096, f32, "
+                                                           "tape + Adam (configs[4])")},
               "cpu_baseline": baseline}]
     # The Adam step over all 25,175,040 parameters as one tensor: reads the
     # gradient, parameters and both moments, writes the last three.
@@ -881,16 +897,18 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
     return lines
 
 
-def traffic_probe() -> None:
+def traffic_probe(part: str = "all") -> None:
     """A short run for ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``, each
     kernel launched eagerly so every dispatch is one workload's: three plain
     contiguous copies of 1 GiB through ``tc_strided_copy`` (the rows kernel;
-    1 GiB read and 1 GiB written each, the counters' calibration), three
-    launches of the headline product, three of the f16 16384 x 1024 x 4096
-    product, three each of the f32 4096^3 product in its PLAIN, LEFT and
-    RIGHT forms, then one call of every bandwidth, fused and training
-    workload in the order ``traffic_workloads`` lists them, each between two
-    marker launches (a 1 x 1 ``tc_flip``) after its untimed calls."""
+    1 GiB read and 1 GiB written each, the counters' calibration), then
+    (part "kernels" or "all") three launches of the headline product, three
+    of the f16 16384 x 1024 x 4096 product, three each of the f32 4096^3
+    product in its PLAIN, LEFT and RIGHT forms and one call of every
+    bandwidth workload, then (part "programs" or "all") one call of every
+    fused and training workload, in the order ``traffic_workloads`` lists
+    them, each between two marker launches (a 1 x 1 ``tc_flip``) after its
+    untimed calls.  The parts split the probe into two processes."""
     n = 1 << 28
     src, dst = lib.Buffer(4 * n), lib.Buffer(4 * n)
     lib.call("tc_fill", src.ptr, n, 4, ctypes.byref(ctypes.c_float(1.0)))
@@ -901,6 +919,27 @@ def traffic_probe() -> None:
     lib.sync()
     src.free()
     dst.free()
+    if part != "programs":
+        product_probe()
+    one, flipped = lib.Buffer(16), lib.Buffer(16)
+
+    def marker():
+        lib.call("tc_flip", 4, one.ptr, 1, 1, flipped.ptr)
+        lib.sync()
+    for workload, run, untimed in traffic_workloads(part):
+        log(f"probe: {workload}")
+        for _ in range(untimed):
+            run()
+        lib.sync()
+        marker()
+        run()
+        lib.sync()
+        marker()
+    log("traffic probe done")
+
+
+def product_probe() -> None:
+    """The traffic probe's products, three eager launches each."""
     m = k = n = 8192
     rng = np.random.default_rng(3)
     a = lib.Buffer.of(host_matrix("bf16", m, k, rng, 1 / np.sqrt(k)))
@@ -933,30 +972,26 @@ def traffic_probe() -> None:
     lib.sync()
     for buffer in (a, b, c):
         buffer.free()
-    # Each workload's dispatches between two markers (a 1 x 1 flip, a kernel
-    # none of them uses), after its untimed calls: a workload of several
-    # kernels (the MLP step, the composed layer norm) is the sum between.
-    one, flipped = lib.Buffer(16), lib.Buffer(16)
-
-    def marker():
-        lib.call("tc_flip", 4, one.ptr, 1, 1, flipped.ptr)
-        lib.sync()
-    for workload, run, untimed in traffic_workloads():
-        log(f"probe: {workload}")
-        for _ in range(untimed):
-            run()
-        lib.sync()
-        marker()
-        run()
-        lib.sync()
-        marker()
-    log("traffic probe done")
 
 
-def traffic_workloads():
-    """(workload, call, untimed calls first) for every bandwidth line and the
-    fused and training lines, in a fixed order, each call on inputs made
-    beforehand (so the probe's dispatches are the calls')."""
+# Each workload's dispatches lie between two markers (a 1 x 1 flip, a kernel
+# none of them uses), after its untimed calls: a workload of several kernels
+# (the MLP step, the composed layer norm) is the sum between.
+def traffic_workloads(part: str = "all"):
+    """(workload, call, untimed calls first) for every bandwidth line (part
+    "kernels") and the fused and training lines (part "programs"), in a
+    fixed order, each call on inputs made beforehand (so the probe's
+    dispatches are the calls')."""
+    calls = []
+    if part != "programs":
+        calls += bandwidth_workloads()
+    if part != "kernels":
+        calls += program_workloads()
+    return calls
+
+
+def bandwidth_workloads():
+    """The bandwidth lines' calls for the traffic probe."""
     rng = np.random.default_rng(2)
     x = Tensor.from_numpy(rng.standard_normal((256, 512, 512), dtype=np.float32))
     y = Tensor.from_numpy(rng.uniform(-1, 1, (1, 512, 1)).astype(np.float32))
@@ -1013,9 +1048,15 @@ def traffic_workloads():
         ("dot, f32 64 Mi elements", lambda: lib.call("tc_dot", lib.F32, da.ptr, db.ptr, 64 << 20, dot_out.ptr)),
         ("transpose, f32 [4096x4096]", lambda: lib.call("tc_transpose", 4, 4096, 4096, sq.ptr, sq_t.ptr)),
     ]
-    # The workloads of several kernels or compiled programs, each run untimed
-    # first as many times as its timed line's warmup needs (the programs
-    # compile on their second appearance).
+    bandwidth_workloads.keep = keep
+    return [(name, call, 0) for name, call in calls]
+
+
+def program_workloads():
+    """The workloads of several kernels or compiled programs, each run
+    untimed first as many times as its timed line's warmup needs (the
+    programs compile on their second appearance)."""
+    rng = np.random.default_rng(2)
     norm = LayerNorm(8192, 8192, np.random.default_rng(17))
     ln_x = lib.Buffer.of(rng.uniform(-3, 3, 8192 * 8192).astype(np.float32))
     dense_bf16, dense_f32 = DenseLayer("bf16", 8192, 8192, 8192), DenseLayer("f32", 4096, 1024, 4096)
@@ -1030,8 +1071,8 @@ def traffic_workloads():
     lib.call("tc_fill", params.ptr, count, 4, ctypes.byref(ctypes.c_float(0.5)))
     lib.call("tc_fill", grads.ptr, count, 4, ctypes.byref(ctypes.c_float(0.25)))
     rule = Adam(1e-3)
-    keep += (norm, ln_x, dense_bf16, dense_f32, net, params, grads, rule)
-    calls = [(name, call, 0) for name, call in calls] + [
+    program_workloads.keep = (norm, ln_x, dense_bf16, dense_f32, net, params, grads, rule)
+    return [
         ("layer norm f32 [8192x8192] (fused_with_statistics), statistics and program in one kernel",
          lambda: norm.one_kernel(ln_x), 2),
         ("layer norm f32 [8192x8192] (fused_with_statistics), composed: row moments, then the program",
@@ -1043,8 +1084,6 @@ def traffic_workloads():
         ("f32 dense layer relu(x w + b) 4096x1024x4096, in the product's epilogue", dense_f32.fused, 2),
         ("f32 dense layer relu(x w + b) 4096x1024x4096, unfused: product, then program", dense_f32.unfused, 2),
     ]
-    traffic_workloads.keep = keep
-    return calls
 
 
 def cpu_baseline(m: int, k: int, n: int) -> dict:
@@ -1124,8 +1163,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=30)
     parser.add_argument("--quick", action="store_true", help="headline only, no secondary workloads or CPU baseline")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    parser.add_argument("--traffic-probe", action="store_true",
-                        help="only the short copy + product run that HBM-traffic counters are read over")
+    parser.add_argument("--traffic-probe", nargs="?", const="all", choices=["all", "kernels", "programs"],
+                        help="only the short run that HBM-traffic counters are read over (optionally one part: "
+                             "the kernels' workloads or the compiled programs')")
     parser.add_argument("--only", default="",
                         help="comma-separated secondary groups to run alone (gemm, reductions, copies, vectors, fusion, transfer, mlp); "
                              "prints their lines as a JSON list instead of the headline line")
@@ -1137,7 +1177,7 @@ def main() -> int:
     name, arch = lib.device_info()
     log(f"device {name} {arch}")
     if args.traffic_probe:
-        traffic_probe()
+        traffic_probe(args.traffic_probe)
         return 0
 
     if args.only:
