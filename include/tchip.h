@@ -573,11 +573,14 @@ int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, c
  * kernels from for this program (after the product kernels' header, the
  * epilogue type `CompiledStore`, its program as straight-line code), into
  * `out` (NUL-terminated, cut at `capacity` - 1 bytes) with its full length
- * in `*length`; `out` may be NULL to ask for the length.  Needs no device.
+ * in `*length`; `out` may be NULL to ask for the length.  `runs` nonzero
+ * asks for the source of a launch whose operands allow the four-wave
+ * kernel's run form (N a multiple of 8, 16-byte aligned operands), which it
+ * contains when the program's places allow it too.  Needs no device.
  * No counterpart in the reference's interface: a diagnostic, so that tests
  * can compile and inspect the very instances the runtime compiles. */
 int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
-                              uint32_t place_count, char* out, uint64_t capacity, uint64_t* length);
+                              uint32_t place_count, uint32_t runs, char* out, uint64_t capacity, uint64_t* length);
 
 /* The source the runtime compiler builds `tc_fused_with_statistics`'s one
  * kernel from for this program and these statistics (the arguments as that

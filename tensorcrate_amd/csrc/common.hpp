@@ -92,6 +92,16 @@ int vector_product(uint32_t dtype, bool row_vector, bool accumulate, uint64_t ro
 // does not compile).
 std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                            const tc_place* places, std::vector<float>* constants);
+// The run form of the same program, for a kernel that hands it whole runs
+// of kEpilogueRun consecutive columns of one row (all inside C or none) and
+// loads what every row shares once: the members `Invariant`,
+// `invariant(inv, live, col)` (the runs starting at column `col`, loaded
+// when `live`) and `run(inv, live, row, col, N, product)`.  Loads of
+// contiguous columns and stores move 16-byte pieces, the stores
+// non-temporal; the caller checks their alignment.  Empty when a load's
+// place steps through its columns other than by 0 or 1, or folds rows.
+std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                          std::vector<float>* constants);
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,
                       uint32_t* scratch = nullptr);
 // Whether hiprtc in this process compiles with the code-object compiler of

@@ -56,6 +56,10 @@ struct Elem<bf16_t> {
 
 constexpr int kPlaceLead = 5;  // a place's folded row axes (TC_FUSED_LEAD)
 
+// The consecutive columns of one row a product epilogue's run form (`run`)
+// takes at a time: 16 bytes of a 16-bit C.
+constexpr int kEpilogueRun = 8;
+
 // A load's place in device form (`Place`, fused/mod.rs:3230-3268): element
 // (row, col) reads offset + col * col_step plus the row index spread over
 // up to five folded axes.
@@ -143,6 +147,72 @@ __device__ __forceinline__ void store_run(void* base, uint32_t dtype, uint64_t i
             *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + index + 4 * q) =
                 make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
         }
+    }
+}
+
+// As `load_run`, in 16-byte pieces for every type: eight 16-bit elements or
+// four f32 a piece.  `index` is a multiple of a piece's elements and `base`
+// 16-byte aligned.
+template <int E>
+__device__ __forceinline__ void load_wide(const void* base, uint32_t dtype, uint64_t index, float (&out)[E]) {
+    static_assert(E % 8 == 0, "whole runs of eight");
+    if (dtype == tc_ops::F32) {
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + index + 4 * q);
+            out[4 * q] = v.x, out[4 * q + 1] = v.y, out[4 * q + 2] = v.z, out[4 * q + 3] = v.w;
+        }
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < E / 8; q++) {
+        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + index + 8 * q);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint16_t h = static_cast<uint16_t>(w[j / 2] >> (16 * (j % 2)));
+            out[8 * q + j] = dtype == tc_ops::F16 ? static_cast<float>(__builtin_bit_cast(_Float16, h))
+                                                  : bf16_bits_to_f32(h);
+        }
+    }
+}
+
+// As `store_run`, in 16-byte pieces for every type (the alignment of
+// `load_wide`); with NT the stores are non-temporal, streaming past the
+// caches, for results no kernel of the same launch reads back.
+template <int E, bool NT>
+__device__ __forceinline__ void store_wide(void* base, uint32_t dtype, uint64_t index, const float (&v)[E]) {
+    static_assert(E % 8 == 0, "whole runs of eight");
+    typedef uint32_t words __attribute__((ext_vector_type(4)));
+    auto put = [](uint4* at, uint4 value) {
+        if (NT) {
+            __builtin_nontemporal_store(words{value.x, value.y, value.z, value.w}, reinterpret_cast<words*>(at));
+        } else {
+            *at = value;
+        }
+    };
+    if (dtype == tc_ops::F32) {
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            put(reinterpret_cast<uint4*>(static_cast<float*>(base) + index + 4 * q),
+                make_uint4(__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
+                           __float_as_uint(v[4 * q + 3])));
+        }
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < E / 8; q++) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float lo = v[8 * q + 2 * j], hi = v[8 * q + 2 * j + 1];
+            const uint16_t a = dtype == tc_ops::F16 ? __builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))
+                                                    : f32_to_bf16_bits(lo);
+            const uint16_t b = dtype == tc_ops::F16 ? __builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))
+                                                    : f32_to_bf16_bits(hi);
+            w[j] = a | (static_cast<uint32_t>(b) << 16);
+        }
+        put(reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + index + 8 * q), make_uint4(w[0], w[1], w[2], w[3]));
     }
 }
 

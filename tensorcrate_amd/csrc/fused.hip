@@ -586,11 +586,15 @@ std::string place_index(const tc_place& place, const std::string& p, const std::
 // `held[e]` instead of memory.  `runs`, when given, marks the loads and
 // stores that may move the group as one run: the kernel calls the group
 // with elements that are consecutive columns of one row, all live or none,
-// and these instructions' pieces are aligned (load_run / store_run).
+// and these instructions' pieces are aligned (load_run / store_run; with
+// `wide`, 16-byte pieces, load_wide / store_wide with non-temporal stores).
+// `invariant`, when given, marks loads whose run is the same for every row
+// of the kernel's runs: they read `inv.i<pc>[e]`, loaded before the runs.
 std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                        const tc_place* places, std::vector<float>* constants, bool sum_store = false,
                        int stat_first = -1, const std::vector<bool>* held = nullptr,
-                       const std::vector<bool>* runs = nullptr) {
+                       const std::vector<bool>* runs = nullptr, const std::vector<bool>* invariant = nullptr,
+                       bool wide = false) {
     static const char* const kBinary[] = {"+", "-", "*", "/"};
     const std::string round = "tc_round<" + std::to_string(dtype) + ">";
     std::ostringstream src;
@@ -603,7 +607,8 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
             if (sum_store) {  // the one output, already in its type, summed in f32 in element order
                 src << each << "sum += live[e] ? " << at(in.a) << " : 0.0f;\n";
             } else if (runs != nullptr && (*runs)[pc] && !reg[in.a].empty()) {
-                src << "    if (live[0]) tc::store_run<" << elems << ">(out[" << int(in.aux) << "], " << int(in.b)
+                src << "    if (live[0]) tc::" << (wide ? "store_wide<" : "store_run<") << elems
+                    << (wide ? ", true" : "") << ">(out[" << int(in.aux) << "], " << int(in.b)
                     << "u, (uint64_t)row[0] * N + col[0], " << reg[in.a] << ");\n";
             } else {
                 src << each << "if (live[e]) tc::store_as(out[" << int(in.aux) << "], " << int(in.b)
@@ -622,11 +627,14 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                     src << "stat[" << (in.a - stat_first) << "];\n";
                 } else if (held != nullptr && (*held)[pc]) {
                     src << "held[e];\n";
+                } else if (invariant != nullptr && (*invariant)[pc]) {
+                    src << "inv.i" << pc << "[e];\n";
                 } else if (runs != nullptr && (*runs)[pc]) {
                     // The run from its first element's index, loaded only
                     // when live; then each element rounded to the type.
                     const std::string p = "places[" + std::to_string(in.op) + "]";
-                    src << "0.0f;\n    if (live[0]) tc::load_run<" << elems << ">(in[" << int(in.a) << "], "
+                    src << "0.0f;\n    if (live[0]) tc::" << (wide ? "load_wide<" : "load_run<") << elems << ">(in["
+                        << int(in.a) << "], "
                         << int(in.b) << "u, " << place_index(places[in.op], p, "row[0]", "col[0]") << ", " << v
                         << ");\n" << each << v << "[e] = " << round << "(" << v << "[e]);\n";
                 } else {
@@ -853,6 +861,54 @@ int check_program(const tc_encoded* code, uint32_t count, uint32_t place_count, 
 std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                            const tc_place* places, std::vector<float>* constants) {
     return group_body(code, count, dtype, product_input, elems, places, constants);
+}
+
+std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                          std::vector<float>* constants) {
+    constexpr int E = kEpilogueRun;
+    const std::string round = "tc_round<" + std::to_string(dtype) + ">";
+    const std::string each = "    for (int e = 0; e < " + std::to_string(E) + "; e++) ";
+    std::vector<bool> runs(count, false), invariant(count, false);
+    std::ostringstream members, loader;
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind == 5) {
+            runs[pc] = true;
+            continue;
+        }
+        if (in.kind != 0 || in.a == 0) continue;  // input 0 is the product
+        const tc_place& place = places[in.op];
+        if (place.lead > 1) return std::string();
+        const bool same_rows = place.lead == 0 || place.steps[0] == 0;
+        const std::string p = "places[" + std::to_string(in.op) + "]", name = "inv.i" + std::to_string(pc);
+        if (same_rows && (place.col_step == 1 || place.col_step == 0)) {
+            invariant[pc] = true;
+            members << "    float i" << pc << "[" << E << "];\n";
+            if (place.col_step == 1) {
+                loader << each << name << "[e] = 0.0f;\n    if (live) tc::load_wide<" << E << ">(in[" << int(in.a)
+                       << "], " << int(in.b) << "u, " << place_index(place, p, "0u", "col") << ", " << name
+                       << ");\n" << each << name << "[e] = " << round << "(" << name << "[e]);\n";
+            } else {
+                loader << "    {\n      const float x = live ? " << round << "(tc::load_as(in[" << int(in.a) << "], "
+                       << int(in.b) << "u, " << place_index(place, p, "0u", "0u") << ")) : 0.0f;\n  " << each
+                       << name << "[e] = x;\n    }\n";
+            }
+        } else if (place.col_step == 1) {
+            runs[pc] = true;
+        } else if (place.col_step != 0) {
+            return std::string();
+        }
+    }
+    const std::string body =
+        group_body(code, count, dtype, true, E, places, constants, false, -1, nullptr, &runs, &invariant, true);
+    const std::string e = std::to_string(E);
+    return "  struct Invariant {\n" + members.str() + "  };\n"
+           "  __device__ __forceinline__ void invariant(Invariant& inv, bool live, uint32_t col) const {\n" +
+           loader.str() + "  }\n"
+           "  __device__ __forceinline__ void run(const Invariant& inv, bool alive, uint32_t r, uint32_t c, uint32_t N,\n"
+           "      const float (&product)[" + e + "]) const {\n"
+           "    bool live[" + e + "];\n    uint32_t row[" + e + "], col[" + e + "];\n" + each +
+           "live[e] = alive, row[e] = r, col[e] = c + e;\n" + body + "  }\n";
 }
 
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,

@@ -553,17 +553,45 @@ constexpr int kCompiledElems = 16;
 // after the product kernels' header; empty when the program has more
 // constants than the kernels' arguments carry.
 std::string epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* host_places,
-                            std::vector<float>* constants) {
+                            std::vector<float>* constants, bool runs) {
     const std::string body = epilogue_group(code, count, dtype, true, kCompiledElems, host_places, constants);
+    // The run form, which the four-wave kernel takes, for 16-bit products
+    // whose operands allow it (the caller's `runs`).
+    const std::string run_members =
+        runs && dtype != TC_F32 ? epilogue_runs(code, count, dtype, host_places, constants) : std::string();
     if (constants->size() > static_cast<size_t>(kInlineCode)) return std::string();
     return "#include \"gemm_kernels.hpp\"\n"
            "struct CompiledStore {\n"
            "  static constexpr bool kProgram = true;\n"
+           "  static constexpr bool kRuns = " + std::string(run_members.empty() ? "false" : "true") + ";\n"
            "  static constexpr int kElems = " + std::to_string(kCompiledElems) + ";\n" +
            compiled_members() +
            "  __device__ __forceinline__ void group(const bool (&live)[kElems], const uint32_t (&row)[kElems],\n"
            "      const uint32_t (&col)[kElems], uint32_t N, const float (&product)[kElems]) const {\n" +
-           body + "  }\n};\n";
+           body + "  }\n" + run_members + "};\n";
+}
+
+// Whether the run form's 16-byte pieces are aligned for this launch: runs
+// of kEpilogueRun columns never straddle C's edge (N a multiple of the run),
+// every output and every contiguous load starts on 16 bytes and a load's
+// rows step by whole 16-byte pieces.
+bool runs_aligned(uint64_t n, const tc_encoded* code, uint32_t count, const tc_place* places,
+                  const void* const* inputs, void* const* outputs, uint32_t output_count) {
+    auto aligned = [](uintptr_t at) { return at % 16 == 0; };
+    if (n % kEpilogueRun != 0) return false;
+    for (uint32_t slot = 0; slot < output_count; slot++) {
+        if (!aligned(reinterpret_cast<uintptr_t>(outputs[slot]))) return false;
+    }
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind != 0 || in.a == 0) continue;
+        const tc_place& place = places[in.op];
+        if (place.col_step != 1) continue;
+        const uint64_t size = in.b == TC_F32 ? 4 : 2;
+        if (!aligned(reinterpret_cast<uintptr_t>(inputs[in.a]) + place.offset * size)) return false;
+        if (place.lead == 1 && (place.steps[0] * size) % 16 != 0) return false;
+    }
+    return true;
 }
 
 // The product kernels with `code` compiled into their epilogue, once the
@@ -574,7 +602,8 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
                            const void* const* inputs, uint32_t input_count, void* const* outputs,
                            uint32_t output_count, hipStream_t s, int* status) {
     std::vector<float> constants;
-    const std::string source = epilogue_source(dtype, code, count, host_places, &constants);
+    const bool runs = runs_aligned(n, code, count, host_places, inputs, outputs, output_count);
+    const std::string source = epilogue_source(dtype, code, count, host_places, &constants, runs);
     if (source.empty()) return false;
     std::vector<std::string> kernels;
     uint32_t large = 0, small = 0, large_threads = 0, small_threads = 0;
@@ -703,8 +732,8 @@ int matmul_program(uint32_t dtype, uint64_t m, uint64_t k, uint64_t n, const voi
 using namespace tc;
 
 extern "C" int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count,
-                                         const tc_place* places, uint32_t place_count, char* out, uint64_t capacity,
-                                         uint64_t* length) {
+                                         const tc_place* places, uint32_t place_count, uint32_t runs, char* out,
+                                         uint64_t capacity, uint64_t* length) {
     if (dtype != TC_F32 && dtype != TC_F16 && dtype != TC_BF16) {
         return fail(TC_UNSUPPORTED, std::string("matmul epilogue source: no kernels for ") + dtype_name(dtype));
     }
@@ -712,7 +741,7 @@ extern "C" int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code,
         return fail(TC_UNSUPPORTED, "matmul epilogue source: the program is not compiled into the product kernels");
     }
     std::vector<float> constants;
-    const std::string source = epilogue_source(dtype, code, count, places, &constants);
+    const std::string source = epilogue_source(dtype, code, count, places, &constants, runs != 0);
     if (source.empty()) {
         return fail(TC_UNSUPPORTED, "matmul epilogue source: more constants than the kernels' arguments carry");
     }

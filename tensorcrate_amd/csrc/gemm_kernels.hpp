@@ -132,6 +132,13 @@ struct PlainStore {
     static constexpr bool kProgram = false;
 };
 
+// Whether an epilogue type also has the run form (`kRuns`, with
+// `Invariant`, `invariant` and `run`); a type without the member has not.
+template <class EPI, class = void>
+struct HasRuns : std::false_type {};
+template <class EPI>
+struct HasRuns<EPI, std::void_t<decltype(EPI::kRuns)>> : std::integral_constant<bool, EPI::kRuns> {};
+
 // A workgroup barrier ordering LDS alone: fences scoped to the workgroup and
 // to LDS ("local") around the barrier, so LDS accesses stay on their side
 // and only LDS traffic is waited for.  Unlike __syncthreads it does not wait
@@ -1579,7 +1586,43 @@ __global__ void __launch_bounds__(256) gemm16x16_wide_kernel(const S* __restrict
         __builtin_amdgcn_sched_barrier(0);
         // lane's accumulators of block (i, j): C[row][col .. col + 3] for row =
         // m0 + wm*128 + 16 i + lane % 16, col = n0 + wn*128 + 16 j + 4 (lane / 16).
-        if constexpr (EPI::kProgram) {
+        if constexpr (EPI::kProgram && HasRuns<EPI>::value) {
+            // The program over runs: each 16-row block of a 64-column half,
+            // staged in f32 in the wave's own 4 KiB as below, is read back
+            // eight consecutive columns of one row a lane (lane / 8 picks
+            // the row, lane % 8 the eight columns), the same columns in
+            // every block of the half, so what the program loads for every
+            // row alike (a bias) is loaded once a half, for both halves
+            // before the tile's first store: no load then waits behind the
+            // tile's stores.  Each run leaves as one 16-byte store.
+            constexpr int R = kEpilogueRun;
+            static_assert(R == 8, "a lane's eight columns: two staged 16-byte chunks");
+            float* staged = reinterpret_cast<float*>(rows_lds + wave * kRegion);
+            const int r = lane % 16, g = lane / 16;
+            typename EPI::Invariant inv[TN / 4];
+            static_for<0, TN / 4>([&](auto x) __attribute__((always_inline)) {
+                constexpr int h = decltype(x)::value;
+                const uint32_t col = n0 + wn * (BN / WN) + 64 * h + 8 * (lane % 8);
+                epi.invariant(inv[h], col < N, col);
+            });
+            static_for<0, (TN / 4) * TM>([&](auto x) __attribute__((always_inline)) {
+                constexpr int h = decltype(x)::value / TM, i = decltype(x)::value % TM;
+                static_for<0, 4>([&](auto y) __attribute__((always_inline)) {
+                    constexpr int jj = decltype(y)::value;
+                    *reinterpret_cast<f32x4*>(staged + r * 64 + (((4 * jj + g) ^ r) * 4)) = acc[i][4 * h + jj];
+                });
+                const uint32_t col = n0 + wn * (BN / WN) + 64 * h + 8 * (lane % 8);
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const int rr = 8 * half + lane / 8, c0 = 2 * (lane % 8);
+                    const f32x4 lo = *reinterpret_cast<const f32x4*>(staged + rr * 64 + ((c0 ^ rr) * 4));
+                    const f32x4 hi = *reinterpret_cast<const f32x4*>(staged + rr * 64 + (((c0 + 1) ^ rr) * 4));
+                    const float product[R] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    const uint32_t row = m0 + wm * (BM / WM) + 16 * i + rr;
+                    epi.run(inv[h], row < M && col < N, row, col, N, product);
+                }
+            });
+        } else if constexpr (EPI::kProgram) {
             // As in the persistent kernel, per 64-column half of the wave's
             // tile: one 16-row block of f32 results at a time in the wave's
             // own 4 KiB, handed to the program EPI::kElems rows a lane.

@@ -202,12 +202,13 @@ def scaled_two_outputs(kind):
     return code.code
 
 
-def generated_source(kind, code, places):
+def generated_source(kind, code, places, runs):
     enc, pl = lib._program(code, places)
     length = ctypes.c_uint64()
-    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), None, 0, ctypes.byref(length))
+    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), runs, None, 0,
+             ctypes.byref(length))
     out = ctypes.create_string_buffer(length.value + 1)
-    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), out, length.value + 1,
+    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), runs, out, length.value + 1,
              ctypes.byref(length))
     return out.value.decode()
 
@@ -222,10 +223,13 @@ def generated_assembly(tmp_path_factory):
     m = n = 8192
     places = [identity_place(m, n), row_broadcast(n), column_broadcast(m)]
     out = []
-    for name, program in (("bias_relu", bias_relu), ("scaled_two_outputs", scaled_two_outputs)):
+    for name, program, runs in (("bias_relu", bias_relu, 0), ("scaled_two_outputs", scaled_two_outputs, 0),
+                                ("bias_relu_runs", bias_relu, 1), ("scaled_two_outputs_runs", scaled_two_outputs, 1)):
         for kind, t in ((lib.BF16, "tc::bf16_t"), (lib.F16, "_Float16")):
-            source = generated_source(kind, program(kind), places)
+            source = generated_source(kind, program(kind), places, runs)
             assert "struct CompiledStore" in source
+            # Both programs' places allow the run form.
+            assert ("kRuns = true" in source) == bool(runs), (name, kind)
             # The library asks the runtime compiler for this instance by
             # name; here it is instantiated explicitly.
             text = ("#include <hip/hip_runtime.h>\n" + source +

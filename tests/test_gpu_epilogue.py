@@ -164,3 +164,55 @@ def test_a_repeated_program_runs_compiled_with_the_same_bits(kind, m, k, n):
     want = plain.download(HOST[kind], m * n)
     for got in results:
         assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def residual_scaled(kind):
+    # out0 = max(product * scale[row] + bias[col], 0) + residual[row, col];
+    # out1 = the product in f32.  Every kind of load the four-wave kernel's
+    # run form takes: a row-invariant run (the bias), one value a row (the
+    # scale), a run a row (the residual), and a second output of another type.
+    code = Code()
+    p = code.load(0, 0, kind)
+    s = code.load(2, 2, kind)
+    b = code.load(1, 1, kind)
+    r = code.load(3, 3, kind)
+    y = code.compare(lib.MAX, code.binary(lib.ADD, code.binary(lib.MUL, p, s), b), code.const(0.0))
+    code.store(code.binary(lib.ADD, y, r), kind, 0)
+    code.store(code.load(0, 0, kind), lib.F32, 1)
+    return code.code
+
+
+@pytest.mark.parametrize("kind", [lib.BF16, lib.F16])
+@pytest.mark.parametrize("m,k,n,skew", [(4100, 256, 4104, 0), (4100, 256, 4100, 0), (4100, 256, 4104, 1)],
+                         ids=["runs", "columns-not-whole-runs", "misaligned-bias"])
+def test_four_wave_epilogue_forms_give_the_unfused_bits(kind, m, k, n, skew):
+    # With N a multiple of 8 and every operand 16-byte aligned the compiled
+    # four-wave epilogue takes whole runs of eight columns (the bias loaded
+    # once a half tile, 16-byte loads and stores); with N not a multiple of 8,
+    # or a bias one element off 16 bytes, it takes the element form.  Both
+    # give the unfused bits on every call, ragged tiles on both edges
+    # included (17 x 17 tiles of 256).
+    rng = np.random.default_rng(kind * 10 + skew + n)
+    a = to_kind(rng.uniform(-1, 1, (m, k)).astype(np.float32), kind)
+    w = to_kind(rng.uniform(-1, 1, (k, n)).astype(np.float32), kind)
+    bias = to_kind(rng.uniform(-1, 1, n + skew).astype(np.float32), kind)
+    scale = to_kind(rng.uniform(0.5, 2, m).astype(np.float32), kind)
+    residual = to_kind(rng.uniform(-1, 1, (m, n)).astype(np.float32), kind)
+    code = residual_scaled(kind)
+    places = [identity_place(m, n), (skew, 1, 0, [], []), column_broadcast(m), identity_place(m, n)]
+    da, dw, db, ds, dr = (lib.Buffer.of(x) for x in (a, w, bias, scale, residual))
+    inputs = [(db, n + skew), (ds, m), (dr, m * n)]
+    width = HOST[kind](0).itemsize
+    results = []
+    for _ in range(3):  # the interpreter, then compiled from the second call
+        outs = [lib.Buffer(m * n * width), lib.Buffer(m * n * 4)]
+        lib.matmul_epilogue(kind, code, places, da, dw, m, k, n, inputs, [(o, m * n) for o in outs])
+        results.append((outs[0].download(HOST[kind], m * n), outs[1].download(np.float32, m * n)))
+    product = lib.Buffer(m * n * width)
+    lib.call("tc_matmul", kind, kind, lib.PLAIN, 0, m, k, n, da.ptr, dw.ptr, product.ptr)
+    plain = [lib.Buffer(m * n * width), lib.Buffer(m * n * 4)]
+    lib.fused(kind, code, places, [(product, m * n)] + inputs, [(p, m * n) for p in plain], m, n)
+    want = (plain[0].download(HOST[kind], m * n), plain[1].download(np.float32, m * n))
+    for call, got in enumerate(results):
+        for g, wt in zip(got, want):
+            assert np.array_equal(g.view(np.uint8), wt.view(np.uint8)), call
