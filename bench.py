@@ -182,6 +182,25 @@ class _Marks:
             self.hip.hipEventDestroy(event)
 
 
+# How long a matrix-core line runs its call back to back before it is timed.
+# The part runs its first dense products of a burst fast and then slows for
+# a few dozen launches while its power controller settles the clock (an
+# 8192^3 product: 0.74, then 0.95, then a steady 0.72 ms); 50 ms of the
+# call covers that, so no line is timed inside the ramp.
+SETTLE_SECONDS = 0.05
+
+
+def settle(fn, seconds: float = SETTLE_SECONDS) -> None:
+    """`fn` called back to back, untimed, for at least `seconds`."""
+    start = time.perf_counter()
+    while True:
+        for _ in range(4):
+            fn()
+        lib.sync()
+        if time.perf_counter() - start >= seconds:
+            return
+
+
 def timed(fn, steps: int, warmup: int) -> Timing:
     """`fn` called `warmup` times untimed, then exactly `steps` times between
     HIP events on the library's stream, with the stream synchronised before
@@ -266,6 +285,7 @@ class Product:
         kind, m, k, n = self.kind, self.m, self.k, self.n
         a, b, c, code = self.a, self.b, self.c, KIND[kind]
         op = lambda: lib.call("tc_matmul", code, code, lib.PLAIN, 0, m, k, n, a.ptr, b.ptr, c.ptr)
+        settle(op)
         ms = timed(op, steps, warmup)
         # The product is one kernel launch, so the call's event time is the
         # kernel's.
@@ -369,10 +389,18 @@ def dense_layer(kind: str, m: int, k: int, n: int, steps: int, warmup: int) -> l
                         1e12, min_seconds=1.0)
     # x, w and the bias read once, relu(x w + b) written once.
     algorithmic = (m * k + k * n + n + m * n) * (4 if kind == "f32" else 2)
+    # The programs compile on their second appearance; both compiles come
+    # first, so that the idle time they take does not undo the clock's
+    # settling, and each line is then timed after its call ran back to back.
+    for _ in range(2):
+        fused()
+        unfused()
+    lib.sync()
     lines = []
     for name, short, fn in (("in the product's epilogue", "epilogue", fused),
                             ("unfused: product, then program", "unfused", unfused),
                             ("the product alone", "product", product_only)):
+        settle(fn)
         ms = timed(fn, steps, warmup)
         achieved = flops / (ms * 1e-3) / 1e12
         workload = f"{kind} dense layer relu(x w + b) {m}x{k}x{n}, {name}"
@@ -839,6 +867,12 @@ def mlp_step(steps: int, warmup: int) -> list[dict]:
     weights, biases = mlp.he_init(widths, 4)
     x, y = mlp.batch_of(widths, batch, 4)
     net = lib.Mlp(widths, batch, weights, biases, x, y, 1e-3)
+    # Three steps compile the step's Adam programs (each on its second
+    # appearance), then the step runs back to back until the clock settles.
+    for _ in range(3):
+        net.step()
+    lib.sync()
+    settle(net.step)
     ms = timed(net.step, steps, warmup)
     flops = sum(2.0 * widths[l] * widths[l + 1] * batch for l in range(3)) * 3
     net.close()

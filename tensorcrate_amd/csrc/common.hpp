@@ -102,8 +102,14 @@ std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtyp
 // place steps through its columns other than by 0 or 1, or folds rows.
 std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                           std::vector<float>* constants);
+// What the compiler's resource report says of a compiled kernel: scratch
+// bytes a lane and architectural VGPRs (UINT32_MAX where it said nothing).
+struct KernelResources {
+    uint32_t scratch = UINT32_MAX;
+    uint32_t vgprs = UINT32_MAX;
+};
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,
-                      uint32_t* scratch = nullptr);
+                      KernelResources* resources = nullptr);
 // Whether hiprtc in this process compiles with the code-object compiler of
 // the ROCm the library was built against (fused.hip).
 bool runtime_compiler_is_ours();

@@ -200,17 +200,22 @@ __device__ __forceinline__ void store_wide(void* base, uint32_t dtype, uint64_t 
         }
         return;
     }
+    typedef float pair_f32 __attribute__((ext_vector_type(2)));
+    typedef __bf16 pair_bf16 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int q = 0; q < E / 8; q++) {
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const float lo = v[8 * q + 2 * j], hi = v[8 * q + 2 * j + 1];
-            const uint16_t a = dtype == tc_ops::F16 ? __builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))
-                                                    : f32_to_bf16_bits(lo);
-            const uint16_t b = dtype == tc_ops::F16 ? __builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))
-                                                    : f32_to_bf16_bits(hi);
-            w[j] = a | (static_cast<uint32_t>(b) << 16);
+            if (dtype == tc_ops::F16) {
+                w[j] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(lo)) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+            } else {
+                // Both halves in one conversion (v_cvt_pk_bf16_f32, the
+                // rounding f32_to_bf16_bits does), `lo` in the low half.
+                w[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pair_f32{lo, hi}, pair_bf16));
+            }
         }
         put(reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + index + 8 * q), make_uint4(w[0], w[1], w[2], w[3]));
     }

@@ -315,9 +315,8 @@ struct Compiled {
     bool failed = false;
     hipModule_t module = nullptr;
     std::vector<hipFunction_t> functions;
-    // Each function's scratch memory a lane, from the compiler's resource
-    // report (UINT32_MAX when it named none for the function).
-    std::vector<uint32_t> scratch;
+    // Each function's resources, from the compiler's resource report.
+    std::vector<KernelResources> resources;
     // The code object the module was loaded from.  The loader reports this
     // buffer to tools (profilers, debuggers) as the loaded code object's
     // storage and they read it back while the module lives, so it lives as
@@ -448,17 +447,19 @@ uint64_t compiled_count = 0;
 
 // hiprtc's flags: the library's own (see _build.py), and the compiler's
 // per-function resource report into the compile log, where each kernel's
-// scratch use is read (`scratch_by_function`).
+// scratch and register use is read (`resources_by_function`).
 const char* const kCompileFlags[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
                                      "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                                      "-Rpass-analysis=kernel-resource-usage"};
 
-// The scratch bytes a lane each function of a compile log uses: the log's
-// resource remarks name a function ("Function Name: <mangled>") and then
-// report its "ScratchSize [bytes/lane]: <n>".
-std::unordered_map<std::string, uint32_t> scratch_by_function(const std::string& log) {
-    std::unordered_map<std::string, uint32_t> out;
-    static const std::string kName = "remark: Function Name: ", kScratch = "ScratchSize [bytes/lane]: ";
+// The resources each function of a compile log uses: the log's resource
+// remarks name a function ("Function Name: <mangled>") and then report,
+// among others, its "VGPRs: <n>" (indented, unlike "TotalSGPRs" and
+// "VGPRs Spill") and "ScratchSize [bytes/lane]: <n>".
+std::unordered_map<std::string, KernelResources> resources_by_function(const std::string& log) {
+    std::unordered_map<std::string, KernelResources> out;
+    static const std::string kName = "remark: Function Name: ", kScratch = "ScratchSize [bytes/lane]: ",
+                             kVgprs = " VGPRs: ";
     std::string current;
     size_t at = 0;
     while (at < log.size()) {
@@ -469,9 +470,10 @@ std::unordered_map<std::string, uint32_t> scratch_by_function(const std::string&
         if (found != std::string::npos) {
             const size_t first = found + kName.size();
             current = line.substr(first, line.find(' ', first) - first);
-        } else if ((found = line.find(kScratch)) != std::string::npos && !current.empty()) {
-            out[current] = static_cast<uint32_t>(strtoul(line.c_str() + found + kScratch.size(), nullptr, 10));
-            current.clear();
+        } else if (!current.empty() && (found = line.find(kScratch)) != std::string::npos) {
+            out[current].scratch = static_cast<uint32_t>(strtoul(line.c_str() + found + kScratch.size(), nullptr, 10));
+        } else if (!current.empty() && (found = line.find(kVgprs)) != std::string::npos) {
+            out[current].vgprs = static_cast<uint32_t>(strtoul(line.c_str() + found + kVgprs.size(), nullptr, 10));
         }
         at = end + 1;
     }
@@ -494,12 +496,12 @@ bool compile_program(const std::string& source, const std::vector<std::string>& 
               HIPRTC_SUCCESS;
     std::vector<char> binary;
     std::vector<std::string> lowered;
-    std::unordered_map<std::string, uint32_t> scratch;
+    std::unordered_map<std::string, KernelResources> resources;
     if (ok) {
         size_t log_size = 0;
         if (hiprtcGetProgramLogSize(program, &log_size) == HIPRTC_SUCCESS && log_size > 0) {
             std::string log(log_size, '\0');
-            if (hiprtcGetProgramLog(program, &log[0]) == HIPRTC_SUCCESS) scratch = scratch_by_function(log);
+            if (hiprtcGetProgramLog(program, &log[0]) == HIPRTC_SUCCESS) resources = resources_by_function(log);
         }
         size_t size = 0;
         ok = hiprtcGetCodeSize(program, &size) == HIPRTC_SUCCESS && size > 0;
@@ -529,8 +531,8 @@ bool compile_program(const std::string& source, const std::vector<std::string>& 
             return false;
         }
         out->functions.push_back(function);
-        const auto known = scratch.find(name);
-        out->scratch.push_back(known == scratch.end() ? UINT32_MAX : known->second);
+        const auto known = resources.find(name);
+        out->resources.push_back(known == resources.end() ? KernelResources{} : known->second);
     }
     return true;
 }
@@ -539,7 +541,7 @@ bool compile_program(const std::string& source, const std::vector<std::string>& 
 // second request; false (run something else) before that or if it does not
 // compile.
 bool cached_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,
-                    uint32_t* scratch = nullptr) {
+                    KernelResources* resources = nullptr) {
     int device = 0;
     (void)hipGetDevice(&device);
     std::lock_guard<std::mutex> lock(compiled_mutex);
@@ -555,7 +557,7 @@ bool cached_kernels(const std::string& source, const std::vector<std::string>& k
     }
     for (size_t k = 0; k < entry.functions.size(); k++) {
         out[k] = entry.functions[k];
-        if (scratch != nullptr) scratch[k] = entry.scratch[k];
+        if (resources != nullptr) resources[k] = entry.resources[k];
     }
     return true;
 }
@@ -581,6 +583,22 @@ std::string place_index(const tc_place& place, const std::string& p, const std::
     return index;
 }
 
+// Whether `value` is a value of `dtype` (rounding it to the type changes no
+// bit): every f32 is; for the 16-bit types, on the host's conversions.
+bool holds_exactly(uint32_t dtype, float value) {
+    uint32_t bits = 0, back = 0;
+    memcpy(&bits, &value, 4);
+    if (dtype == TC_BF16) {
+        back = static_cast<uint32_t>(tc_f32_to_bf16(value)) << 16;
+    } else if (dtype == TC_F16) {
+        const float wide = static_cast<float>(static_cast<_Float16>(value));
+        memcpy(&back, &wide, 4);
+    } else {
+        return true;
+    }
+    return bits == back;
+}
+
 // `held`, when given, marks the loads (by instruction index) whose values
 // the kernel already holds, rounded to the program's type: they read
 // `held[e]` instead of memory.  `runs`, when given, marks the loads and
@@ -596,9 +614,15 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                        const std::vector<bool>* runs = nullptr, const std::vector<bool>* invariant = nullptr,
                        bool wide = false) {
     static const char* const kBinary[] = {"+", "-", "*", "/"};
-    const std::string round = "tc_round<" + std::to_string(dtype) + ">";
+    const std::string round_run = "    tc_round_run<" + std::to_string(dtype) + ">(";
     std::ostringstream src;
     std::string reg[TC_FUSED_REGISTERS];
+    // Whether a register's every element is already a value of the type
+    // (rounding it again changes no bit): what a rounding wrote, a constant
+    // the type holds exactly, a predicate's 0, 1/2 or 1.  An unwritten
+    // register reads 0.
+    bool exact[TC_FUSED_REGISTERS];
+    for (bool& e : exact) e = true;
     auto at = [&](uint8_t r) { return reg[r].empty() ? std::string("0.0f") : reg[r] + "[e]"; };
     const std::string each = "    for (int e = 0; e < " + std::to_string(elems) + "; e++) ";
     for (uint32_t pc = 0; pc < count; pc++) {
@@ -617,26 +641,32 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
             continue;
         }
         const std::string v = "v" + std::to_string(pc);
+        // Each value is computed in f32 and the array then rounded to the
+        // type (tc_round_run, as tc_round rounds one value) unless `rounded`
+        // is left false because the rounding could change no bit.
+        bool rounded = true;
         src << "    float " << v << "[" << elems << "];\n" << each << v << "[e] = ";
         switch (in.kind) {
             case 0:
                 if (product_input && in.a == 0) {
-                    src << "live[e] ? " << round << "(product[e]) : 0.0f;\n";
+                    src << "live[e] ? product[e] : 0.0f;\n";
                 } else if (stat_first >= 0 && in.a >= stat_first) {
                     // A row statistic, one value a row, already in the type.
                     src << "stat[" << (in.a - stat_first) << "];\n";
+                    rounded = false;
                 } else if (held != nullptr && (*held)[pc]) {
                     src << "held[e];\n";
+                    rounded = false;
                 } else if (invariant != nullptr && (*invariant)[pc]) {
                     src << "inv.i" << pc << "[e];\n";
+                    rounded = false;
                 } else if (runs != nullptr && (*runs)[pc]) {
                     // The run from its first element's index, loaded only
-                    // when live; then each element rounded to the type.
+                    // when live.
                     const std::string p = "places[" + std::to_string(in.op) + "]";
                     src << "0.0f;\n    if (live[0]) tc::" << (wide ? "load_wide<" : "load_run<") << elems << ">(in["
-                        << int(in.a) << "], "
-                        << int(in.b) << "u, " << place_index(places[in.op], p, "row[0]", "col[0]") << ", " << v
-                        << ");\n" << each << v << "[e] = " << round << "(" << v << "[e]);\n";
+                        << int(in.a) << "], " << int(in.b) << "u, "
+                        << place_index(places[in.op], p, "row[0]", "col[0]") << ", " << v << ");\n";
                 } else {
                     // Every lane loads, an element outside C at (0, 0), so
                     // no load waits on a branch; the place's row walk is
@@ -644,29 +674,39 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                     const std::string p = "places[" + std::to_string(in.op) + "]";
                     const std::string r = "(live[e] ? row[e] : 0u)", c = "(live[e] ? col[e] : 0u)";
                     std::string index = place_index(places[in.op], p, r, c);
-                    src << "live[e] ? " << round << "(tc::load_as(in[" << int(in.a) << "], " << int(in.b) << "u, "
-                        << index << ")) : 0.0f;\n";
+                    src << "live[e] ? tc::load_as(in[" << int(in.a) << "], " << int(in.b) << "u, " << index
+                        << ") : 0.0f;\n";
                 }
                 break;
             case 1:
+                // Constants are used as given; one the type holds exactly
+                // counts as rounded.
                 src << "constants[" << constants->size() << "];\n";
                 constants->push_back(in.value);
+                rounded = false;
+                exact[in.dst] = holds_exactly(dtype, in.value);
                 break;
             case 2:
                 if (in.op == TC_REM) {
-                    src << round << "(fmodf(" << at(in.a) << ", " << at(in.b) << "));\n";
+                    src << "fmodf(" << at(in.a) << ", " << at(in.b) << ");\n";
                 } else {
-                    src << round << "(" << at(in.a) << " " << kBinary[in.op] << " " << at(in.b) << ");\n";
+                    src << at(in.a) << " " << kBinary[in.op] << " " << at(in.b) << ";\n";
                 }
                 break;
             case 3:
-                src << round << "(tc_analytic(" << int(in.op) << "u, " << at(in.a) << "));\n";
+                src << "tc_analytic(" << int(in.op) << "u, " << at(in.a) << ");\n";
                 break;
             default:
-                src << round << "(tc_compare(" << int(in.op) << "u, " << at(in.a) << ", " << at(in.b) << "));\n";
+                src << "tc_compare(" << int(in.op) << "u, " << at(in.a) << ", " << at(in.b) << ");\n";
+                // A predicate is 0, 1/2 or 1; the minimum or maximum of two
+                // values of the type is one of them (or a quiet NaN the type
+                // holds).
+                rounded = (in.op == TC_MIN || in.op == TC_MAX) && !(exact[in.a] && exact[in.b]);
                 break;
         }
+        if (rounded) src << round_run << v << ");\n";
         reg[in.dst] = v;
+        if (in.kind != 1) exact[in.dst] = true;
     }
     return src.str();
 }
@@ -912,8 +952,8 @@ std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype
 }
 
 bool compiled_kernels(const std::string& source, const std::vector<std::string>& kernels, hipFunction_t* out,
-                      uint32_t* scratch) {
-    return cached_kernels(source, kernels, out, scratch);
+                      KernelResources* resources) {
+    return cached_kernels(source, kernels, out, resources);
 }
 
 // hiprtc hands the compile to the code-object compiler library (comgr) that

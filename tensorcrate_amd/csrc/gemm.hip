@@ -553,13 +553,14 @@ constexpr int kCompiledElems = 16;
 // after the product kernels' header; empty when the program has more
 // constants than the kernels' arguments carry.
 std::string epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* host_places,
-                            std::vector<float>* constants, bool runs) {
+                            std::vector<float>* constants, bool runs, bool* has_runs = nullptr) {
     const std::string body = epilogue_group(code, count, dtype, true, kCompiledElems, host_places, constants);
     // The run form, which the four-wave kernel takes, for 16-bit products
     // whose operands allow it (the caller's `runs`).
     const std::string run_members =
         runs && dtype != TC_F32 ? epilogue_runs(code, count, dtype, host_places, constants) : std::string();
     if (constants->size() > static_cast<size_t>(kInlineCode)) return std::string();
+    if (has_runs != nullptr) *has_runs = !run_members.empty();
     return "#include \"gemm_kernels.hpp\"\n"
            "struct CompiledStore {\n"
            "  static constexpr bool kProgram = true;\n"
@@ -594,6 +595,12 @@ bool runs_aligned(uint64_t n, const tc_encoded* code, uint32_t count, const tc_p
     return true;
 }
 
+// The most architectural VGPRs a four-wave instance with a compiled
+// epilogue may use: a margin of 32 under the 256 a wave has, so spilled
+// scalars find a free VGPR rather than an accumulator's AGPR (the library's
+// own instances use 165-200).
+constexpr uint32_t kWideVgprLimit = 224;
+
 // The product kernels with `code` compiled into their epilogue, once the
 // program has been seen before: true when they were launched.
 bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, const void* a, const void* b,
@@ -603,7 +610,8 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
                            uint32_t output_count, hipStream_t s, int* status) {
     std::vector<float> constants;
     const bool runs = runs_aligned(n, code, count, host_places, inputs, outputs, output_count);
-    const std::string source = epilogue_source(dtype, code, count, host_places, &constants, runs);
+    bool has_runs = false;
+    const std::string source = epilogue_source(dtype, code, count, host_places, &constants, runs, &has_runs);
     if (source.empty()) return false;
     std::vector<std::string> kernels;
     uint32_t large = 0, small = 0, large_threads = 0, small_threads = 0;
@@ -617,7 +625,12 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
                    "tc::direct16_kernel<" + type + ", " + type + ", true, false, 128, 128, 2, 2, 64, 2, CompiledStore>"};
         if (runtime_compiler_is_ours()) {
             kernels.push_back("tc::gemm16x16_persistent_kernel<" + type + ", " + type + ", true, false, CompiledStore>");
-            kernels.push_back("tc::gemm16x16_wide_kernel<" + type + ", " + type + ", true, false, CompiledStore>");
+            // The four-wave kernel takes only the run form: the element
+            // form's per-element addresses and stores cost it more than the
+            // eight-wave kernel loses, and crowd its registers.
+            if (has_runs) {
+                kernels.push_back("tc::gemm16x16_wide_kernel<" + type + ", " + type + ", true, false, CompiledStore>");
+            }
         }
         large = ((m + 255) / 256) * ((n + 255) / 256);
         large_threads = 512;
@@ -625,8 +638,8 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     }
     small = ((m + 127) / 128) * ((n + 127) / 128);
     hipFunction_t functions[4] = {};
-    uint32_t scratch[4] = {};
-    if (!compiled_kernels(source, kernels, functions, scratch)) return false;
+    KernelResources resources[4];
+    if (!compiled_kernels(source, kernels, functions, resources)) return false;
     CompiledArgsOf args{};
     for (uint32_t slot = 1; slot < input_count; slot++) args.in[slot] = inputs[slot];
     for (uint32_t slot = 0; slot < output_count; slot++) args.out[slot] = outputs[slot];
@@ -642,11 +655,15 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
     // of 128, else the eight-wave one.
     // The four-wave kernel's matrix-core steps are inline assembly on
     // accumulators pinned in AGPRs, with their hazard cover written around
-    // them; an instance whose epilogue made the compiler spill or move the
-    // accumulators to scratch memory (the compile's resource report says
-    // so) breaks those assumptions and is never launched: the eight-wave
-    // kernels take the product instead.
-    const bool wide = kernels.size() == 4 && use_large && k % 128 == 0 && scratch[3] == 0;
+    // them.  An epilogue that crowds the registers breaks those assumptions:
+    // with the architectural VGPRs nearly full the compiler parks spilled
+    // values in AGPRs and moves accumulators out of them inside the main
+    // loop (seen at 250 VGPRs), and past that it spills to scratch memory.
+    // So an instance is launched only when the compile's resource report
+    // shows no scratch and at most kWideVgprLimit VGPRs; otherwise the
+    // eight-wave kernels take the product.
+    const bool wide = kernels.size() == 4 && use_large && k % 128 == 0 && resources[3].scratch == 0 &&
+                      resources[3].vgprs <= kWideVgprLimit;
     const bool persistent = kernels.size() == 4 && use_large && ((k + 63) / 64) % 2 == 0;
     hipFunction_t function = dtype == TC_F32 ? functions[0]
                              : wide          ? functions[3]

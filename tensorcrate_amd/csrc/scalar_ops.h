@@ -17,7 +17,7 @@ enum : unsigned { SQRT = 13 };
 
 // bf16 is the top half of an f32, so widening is a shift.
 __host__ __device__ inline float tc_bf16_to_f32(unsigned short bits) {
-    return __uint_as_float(static_cast<unsigned>(bits) << 16);
+    return __builtin_bit_cast(float, static_cast<unsigned>(bits) << 16);
 }
 
 // Round to nearest, ties to even, with NaNs quieted: the rule of
@@ -31,7 +31,7 @@ __host__ __device__ inline unsigned short tc_f32_to_bf16(float value) {
 #if defined(__HIP_DEVICE_COMPILE__)
     return __builtin_bit_cast(unsigned short, static_cast<__bf16>(value));
 #else
-    const unsigned x = __float_as_uint(value);
+    const unsigned x = __builtin_bit_cast(unsigned, value);
     const unsigned rounded = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
     const unsigned quiet = (x >> 16) | 0x0040u;
     return static_cast<unsigned short>((x & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
@@ -91,4 +91,24 @@ __device__ inline float tc_round(float v) {
     if (T == tc_ops::F16) return static_cast<float>(static_cast<_Float16>(v));
     if (T == tc_ops::BF16) return tc_bf16_to_f32(tc_f32_to_bf16(v));
     return v;
+}
+
+// Each element of `v` rounded as tc_round<T> rounds it.  bf16 rounds two at
+// a time: gfx950's pair conversion (v_cvt_pk_bf16_f32, the same rule as the
+// one-value conversion) and one shift or mask each back to f32.
+template <int T, int E>
+__device__ inline void tc_round_run(float (&v)[E]) {
+    if constexpr (T == tc_ops::BF16) {
+        typedef float pair_f32 __attribute__((ext_vector_type(2)));
+        typedef __bf16 pair_bf16 __attribute__((ext_vector_type(2)));
+        int e = 0;
+        for (; e + 1 < E; e += 2) {
+            const unsigned w = __builtin_bit_cast(unsigned, __builtin_convertvector(pair_f32{v[e], v[e + 1]}, pair_bf16));
+            v[e] = __uint_as_float(w << 16);
+            v[e + 1] = __uint_as_float(w & 0xffff0000u);
+        }
+        if (e < E) v[e] = tc_round<T>(v[e]);
+    } else if constexpr (T == tc_ops::F16) {
+        for (int e = 0; e < E; e++) v[e] = tc_round<T>(v[e]);
+    }
 }
