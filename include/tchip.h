@@ -582,6 +582,18 @@ int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, c
 int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
                               uint32_t place_count, uint32_t runs, char* out, uint64_t capacity, uint64_t* length);
 
+/* The source the runtime compiler builds for `tc_fused` with this program
+ * over rows x cols (the arguments as that call takes them; `inputs` are
+ * only checked for alignment, never read; outputs count as 16-byte
+ * aligned): the dense form, the run form or the general form, as the call
+ * would pick, into `out` as `tc_matmul_epilogue_source` does.
+ * TC_UNSUPPORTED when the program runs interpreted.  Needs no device.  No
+ * counterpart in the reference's interface: a diagnostic, so that tests can
+ * compile the very source the runtime compiles. */
+int tc_fused_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                    uint32_t place_count, const void* const* inputs, uint32_t input_count, uint64_t rows,
+                    uint64_t cols, char* out, uint64_t capacity, uint64_t* length);
+
 /* The source the runtime compiler builds `tc_fused_with_statistics`'s one
  * kernel from for this program and these statistics (the arguments as that
  * call takes them; `inputs` and the statistics' sources are only compared

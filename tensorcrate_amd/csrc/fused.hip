@@ -605,14 +605,15 @@ bool holds_exactly(uint32_t dtype, float value) {
 // stores that may move the group as one run: the kernel calls the group
 // with elements that are consecutive columns of one row, all live or none,
 // and these instructions' pieces are aligned (load_run / store_run; with
-// `wide`, 16-byte pieces, load_wide / store_wide with non-temporal stores).
+// `wide`, 16-byte pieces, load_wide / store_wide, the stores non-temporal
+// with `stream`).
 // `invariant`, when given, marks loads whose run is the same for every row
 // of the kernel's runs: they read `inv.i<pc>[e]`, loaded before the runs.
 std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                        const tc_place* places, std::vector<float>* constants, bool sum_store = false,
                        int stat_first = -1, const std::vector<bool>* held = nullptr,
                        const std::vector<bool>* runs = nullptr, const std::vector<bool>* invariant = nullptr,
-                       bool wide = false) {
+                       bool wide = false, bool stream = false) {
     static const char* const kBinary[] = {"+", "-", "*", "/"};
     const std::string round_run = "    tc_round_run<" + std::to_string(dtype) + ">(";
     std::ostringstream src;
@@ -632,7 +633,7 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                 src << each << "sum += live[e] ? " << at(in.a) << " : 0.0f;\n";
             } else if (runs != nullptr && (*runs)[pc] && !reg[in.a].empty()) {
                 src << "    if (live[0]) tc::" << (wide ? "store_wide<" : "store_run<") << elems
-                    << (wide ? ", true" : "") << ">(out[" << int(in.aux) << "], " << int(in.b)
+                    << (wide ? (stream ? ", true" : ", false") : "") << ">(out[" << int(in.aux) << "], " << int(in.b)
                     << "u, (uint64_t)row[0] * N + col[0], " << reg[in.a] << ");\n";
             } else {
                 src << each << "if (live[e]) tc::store_as(out[" << int(in.aux) << "], " << int(in.b)
@@ -735,6 +736,109 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
     return true;
 }
 
+}  // namespace
+
+bool runs_allowed(uint64_t cols, const tc_encoded* code, uint32_t count, const tc_place* places,
+                  const void* const* inputs, void* const* outputs, uint32_t output_count, bool product_input) {
+    auto aligned = [](uintptr_t at) { return at % 16 == 0; };
+    if (cols % kEpilogueRun != 0) return false;
+    for (uint32_t slot = 0; slot < output_count; slot++) {
+        if (!aligned(reinterpret_cast<uintptr_t>(outputs[slot]))) return false;
+    }
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind != 0 || (product_input && in.a == 0)) continue;
+        const tc_place& place = places[in.op];
+        if (place.lead > 1 || (place.col_step != 0 && place.col_step != 1)) return false;
+        if (place.col_step != 1) continue;
+        const uint64_t size = in.b == TC_F32 ? 4 : 2;
+        if (!aligned(reinterpret_cast<uintptr_t>(inputs[in.a]) + place.offset * size)) return false;
+        if (place.lead == 1 && (place.steps[0] * size) % 16 != 0) return false;
+    }
+    return true;
+}
+
+namespace {
+
+// A program over whole runs (`runs_allowed`): a kernel over the rows x cols
+// space in runs of kEpilogueRun consecutive columns of one row, a run a
+// thread, consecutive threads on consecutive runs.  Each load of contiguous
+// columns moves 16-byte pieces (a row-invariant one, a bias, from the
+// cache), a load of one value a row loads it once a run, and each store is
+// 16-byte pieces, non-temporal when the program moves more than
+// kStreamBytes.  From the program's second appearance, like the other
+// compiled forms.
+std::string general_runs_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                                uint64_t rows, uint64_t cols, std::vector<float>* constants) {
+    constexpr int E = kEpilogueRun;
+    const uint64_t runs = rows * cols / E;
+    std::vector<bool> marks(count, false);
+    uint64_t bytes = 0;  // a run's, loads of contiguous columns and stores
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        const uint64_t size = in.b == TC_F32 ? 4 : 2;
+        if (in.kind == 5 || (in.kind == 0 && places[in.op].col_step == 1)) {
+            marks[pc] = true;
+            bytes += size * E;
+        }
+    }
+    const bool stream = runs * bytes > kStreamBytes;
+    const std::string body =
+        group_body(code, count, dtype, false, E, places, constants, false, -1, nullptr, &marks, nullptr, true, stream);
+    if (constants->size() > static_cast<size_t>(kInlineCode)) return std::string();
+    const std::string e = std::to_string(E);
+    return "#include \"device.hpp\"\n"
+           "struct Program {\n" + std::string(compiled_members()) +
+           "  __device__ __forceinline__ void run(uint32_t r, uint32_t c, uint32_t N) const {\n"
+           "    bool live[" + e + "];\n    uint32_t row[" + e + "], col[" + e + "];\n"
+           "    for (int e = 0; e < " + e + "; e++) live[e] = true, row[e] = r, col[e] = c + e;\n" + body + "  }\n};\n"
+           "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_runs(Program p, uint32_t cols, uint32_t per_row,\n"
+           "                                                                 uint32_t runs) {\n"
+           "  const uint32_t stride = gridDim.x * 256u;\n"
+           "  uint32_t at = blockIdx.x * 256u + threadIdx.x;\n"
+           "  if (at >= runs) return;\n"
+           "  // The run's row and its place in the row, then stepped by the grid's\n"
+           "  // stride without a division.\n"
+           "  uint32_t r = at / per_row, c = at - r * per_row;\n"
+           "  const uint32_t step_rows = stride / per_row, step_runs = stride - step_rows * per_row;\n"
+           "  for (; at < runs; at += stride) {\n"
+           "    p.run(r, c * " + e + "u, cols);\n"
+           "    r += step_rows;\n"
+           "    c += step_runs;\n"
+           "    if (c >= per_row) { c -= per_row; r++; }\n"
+           "  }\n"
+           "}\n";
+}
+
+bool run_general_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                      uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, hipStream_t s,
+                      int* status) {
+    constexpr int E = kEpilogueRun;
+    const uint64_t runs = rows * cols / E;
+    std::vector<float> constants;
+    const std::string source = general_runs_source(code, count, dtype, places, rows, cols, &constants);
+    if (source.empty()) return false;
+    hipFunction_t function = nullptr;
+    if (!cached_kernels(source, {"tc_fused_runs"}, &function)) return false;
+    CompiledArgsOf args{};
+    for (int k = 0; k < TC_FUSED_MAX_INPUTS; k++) args.in[k] = buffers.inputs[k];
+    for (int k = 0; k < TC_FUSED_MAX_OUTPUTS; k++) args.out[k] = buffers.outputs[k];
+    int place_status = to_device_places(places, place_count, args.places);
+    if (place_status != TC_OK) {
+        *status = place_status;
+        return true;
+    }
+    for (size_t c = 0; c < constants.size(); c++) args.constants[c] = constants[c];
+    uint32_t cols32 = static_cast<uint32_t>(cols), per_row = static_cast<uint32_t>(cols / E),
+             runs32 = static_cast<uint32_t>(runs);
+    void* params[] = {&args, &cols32, &per_row, &runs32};
+    const uint32_t blocks = grid_for(runs, 256, 8);
+    count_dispatch();
+    const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);
+    *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused program: ") + hipGetErrorString(error));
+    return true;
+}
+
 // A program whose loads do not all walk in element order (a broadcast
 // operand, a transposed view) runs compiled too, from its second
 // appearance: a kernel over the rows x cols space, 16 elements a thread 64
@@ -744,17 +848,35 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
 // straight-line code a product epilogue runs.
 constexpr int kGeneralElems = 16;
 
+std::string general_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                           std::vector<float>* constants);
+bool launch_general(hipFunction_t function, const std::vector<float>& constants, const tc_place* places,
+                    uint32_t place_count, const Buffers& buffers, uint64_t total, uint64_t cols, hipStream_t s,
+                    int* status);
+
 bool run_general_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                           uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, hipStream_t s,
                           int* status) {
     const uint64_t total = rows * cols;
     // 32-bit element indices: below 2^31, so no index of the last pass wraps.
     if (place_count > static_cast<uint32_t>(kInlinePlaces) || total > (uint64_t{1} << 31)) return false;
+    if (runs_allowed(cols, code, count, places, buffers.inputs, buffers.outputs, TC_FUSED_MAX_OUTPUTS, false)) {
+        return run_general_runs(code, count, dtype, places, place_count, buffers, rows, cols, s, status);
+    }
     std::vector<float> constants;
-    const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, &constants);
-    if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
+    const std::string source = general_source(code, count, dtype, places, &constants);
+    if (source.empty()) return false;
+    hipFunction_t function = nullptr;
+    if (!cached_kernels(source, {"tc_fused_general"}, &function)) return false;
+    return launch_general(function, constants, places, place_count, buffers, rows * cols, cols, s, status);
+}
+
+std::string general_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                           std::vector<float>* constants) {
+    const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, constants);
+    if (constants->size() > static_cast<size_t>(kInlineCode)) return std::string();
     const std::string E = std::to_string(kGeneralElems);
-    const std::string source =
+    return
         "#include \"device.hpp\"\n"
         "struct Program {\n" + std::string(compiled_members()) +
         "  __device__ __forceinline__ void group(const bool (&live)[" + E + "], const uint32_t (&row)[" + E + "],\n"
@@ -787,8 +909,11 @@ bool run_general_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype
         "    p.group(live, row, col, cols);\n"
         "  }\n"
         "}\n";
-    hipFunction_t function = nullptr;
-    if (!cached_kernels(source, {"tc_fused_general"}, &function)) return false;
+}
+
+bool launch_general(hipFunction_t function, const std::vector<float>& constants, const tc_place* places,
+                    uint32_t place_count, const Buffers& buffers, uint64_t total, uint64_t cols, hipStream_t s,
+                    int* status) {
     CompiledArgsOf args{};
     for (int k = 0; k < TC_FUSED_MAX_INPUTS; k++) args.in[k] = buffers.inputs[k];
     for (int k = 0; k < TC_FUSED_MAX_OUTPUTS; k++) args.out[k] = buffers.outputs[k];
@@ -940,7 +1065,7 @@ std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype
         }
     }
     const std::string body =
-        group_body(code, count, dtype, true, E, places, constants, false, -1, nullptr, &runs, &invariant, true);
+        group_body(code, count, dtype, true, E, places, constants, false, -1, nullptr, &runs, &invariant, true, true);
     const std::string e = std::to_string(E);
     return "  struct Invariant {\n" + members.str() + "  };\n"
            "  __device__ __forceinline__ void invariant(Invariant& inv, bool live, uint32_t col) const {\n" +
@@ -1570,6 +1695,38 @@ extern "C" int tc_fused_with_statistics_source(uint32_t dtype, const tc_encoded*
     if (out != nullptr && capacity > 0) {
         const size_t n = plan.source.size() < capacity - 1 ? plan.source.size() : capacity - 1;
         memcpy(out, plan.source.data(), n);
+        out[n] = '\0';
+    }
+    return TC_OK;
+}
+
+extern "C" int tc_fused_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                               uint32_t place_count, const void* const* inputs, uint32_t input_count, uint64_t rows,
+                               uint64_t cols, char* out, uint64_t capacity, uint64_t* length) {
+    if (dtype > TC_BF16) return fail(TC_UNSUPPORTED, std::string("fused source: no kernels for ") + dtype_name(dtype));
+    if (input_count > TC_FUSED_MAX_INPUTS || rows == 0 || cols == 0) {
+        return fail(TC_INVALID, "fused source: inputs, rows and columns as tc_fused takes them");
+    }
+    const void* in[TC_FUSED_MAX_INPUTS] = {};
+    for (uint32_t k = 0; k < input_count; k++) in[k] = inputs[k];
+    void* const outs[TC_FUSED_MAX_OUTPUTS] = {};  // outputs count as 16-byte aligned
+    std::vector<float> constants;
+    std::string source;
+    tc::DenseLoads dense{};
+    uint32_t dense_loads = 0;
+    if (tc::dense_plan(code, count, places, in, outs, rows, cols, &dense, &dense_loads)) {
+        const bool stream = rows * cols / 4 * tc::dense_chunk_bytes(code, count) > kStreamBytes;
+        source = tc::dense_source(code, count, dtype, stream, &constants);
+    } else if (place_count <= static_cast<uint32_t>(kInlinePlaces) && rows * cols <= (uint64_t{1} << 31)) {
+        source = tc::runs_allowed(cols, code, count, places, in, outs, TC_FUSED_MAX_OUTPUTS, false)
+                     ? tc::general_runs_source(code, count, dtype, places, rows, cols, &constants)
+                     : tc::general_source(code, count, dtype, places, &constants);
+    }
+    if (source.empty()) return fail(TC_UNSUPPORTED, "fused source: the program runs interpreted");
+    *length = source.size();
+    if (out != nullptr && capacity > 0) {
+        const size_t n = source.size() < capacity - 1 ? source.size() : capacity - 1;
+        memcpy(out, source.data(), n);
         out[n] = '\0';
     }
     return TC_OK;

@@ -572,29 +572,6 @@ std::string epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t cou
            body + "  }\n" + run_members + "};\n";
 }
 
-// Whether the run form's 16-byte pieces are aligned for this launch: runs
-// of kEpilogueRun columns never straddle C's edge (N a multiple of the run),
-// every output and every contiguous load starts on 16 bytes and a load's
-// rows step by whole 16-byte pieces.
-bool runs_aligned(uint64_t n, const tc_encoded* code, uint32_t count, const tc_place* places,
-                  const void* const* inputs, void* const* outputs, uint32_t output_count) {
-    auto aligned = [](uintptr_t at) { return at % 16 == 0; };
-    if (n % kEpilogueRun != 0) return false;
-    for (uint32_t slot = 0; slot < output_count; slot++) {
-        if (!aligned(reinterpret_cast<uintptr_t>(outputs[slot]))) return false;
-    }
-    for (uint32_t pc = 0; pc < count; pc++) {
-        const tc_encoded& in = code[pc];
-        if (in.kind != 0 || in.a == 0) continue;
-        const tc_place& place = places[in.op];
-        if (place.col_step != 1) continue;
-        const uint64_t size = in.b == TC_F32 ? 4 : 2;
-        if (!aligned(reinterpret_cast<uintptr_t>(inputs[in.a]) + place.offset * size)) return false;
-        if (place.lead == 1 && (place.steps[0] * size) % 16 != 0) return false;
-    }
-    return true;
-}
-
 // The most architectural VGPRs a four-wave instance with a compiled
 // epilogue may use: a margin of 32 under the 256 a wave has, so spilled
 // scalars find a free VGPR rather than an accumulator's AGPR (the library's
@@ -609,7 +586,7 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
                            const void* const* inputs, uint32_t input_count, void* const* outputs,
                            uint32_t output_count, hipStream_t s, int* status) {
     std::vector<float> constants;
-    const bool runs = runs_aligned(n, code, count, host_places, inputs, outputs, output_count);
+    const bool runs = runs_allowed(n, code, count, host_places, inputs, outputs, output_count, true);
     bool has_runs = false;
     const std::string source = epilogue_source(dtype, code, count, host_places, &constants, runs, &has_runs);
     if (source.empty()) return false;

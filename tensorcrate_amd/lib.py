@@ -187,6 +187,7 @@ SIGNATURES = {
     "tc_fused_compiled": [ctypes.POINTER(u64)],
     "tc_fused_resident": [u64, ctypes.POINTER(u64), ctypes.POINTER(u64)],
     "tc_matmul_epilogue_source": [u32, vp, u32, vp, u32, u32, ctypes.c_char_p, u64, ctypes.POINTER(u64)],
+    "tc_fused_source": [u32, vp, u32, vp, u32, vp, u32, u64, u64, ctypes.c_char_p, u64, ctypes.POINTER(u64)],
     "tc_fused_with_statistics_source": [u32, vp, u32, vp, u32, ctypes.POINTER(vp), u32, u64, u64, vp, u32,
                                         ctypes.c_char_p, u64, ctypes.POINTER(u64)],
     "tc_row_moments": [u32, u32, vp, u64, ctypes.POINTER(Place), u64, u64, vp, vp],

@@ -221,3 +221,19 @@ def ulps(got: np.ndarray, want: np.ndarray) -> np.ndarray:
         nan_g, nan_w = np.isnan(wide_got), np.isnan(want.astype(np.float32))
     gap = np.where(nan_g & nan_w, 0, gap)
     return np.where(nan_g != nan_w, 1 << 40, gap)
+
+
+def run_form_program(rows, skew=0):
+    """max(scale[row] * x + bias[col] - s, 0) as bf16 and (that sum > bias)
+    as f32: a row-broadcast f16 vector `bias` (its place `skew` elements
+    on), one bf16 value a row, a contiguous f32 matrix and an f32 scalar,
+    each a kind of load the run form takes.  Returns (code, places) with
+    places for `rows` rows."""
+    from tensorcrate_amd import lib
+
+    code = [(0, 0, 0, 0, lib.F16, 0, 0.0), (0, 1, 1, 1, lib.BF16, 0, 0.0), (0, 2, 2, 2, lib.F32, 0, 0.0),
+            (0, 3, 4, 3, lib.F32, 0, 0.0), (2, lib.MUL, 3, 1, 2, 0, 0.0), (2, lib.ADD, 3, 3, 0, 0, 0.0),
+            (2, lib.SUB, 3, 3, 4, 0, 0.0), (1, 0, 6, 0, 0, 0, 0.0), (4, lib.MAX, 7, 3, 6, 0, 0.0),
+            (4, lib.GREATER, 5, 3, 0, 0, 0.0), (5, 0, 0, 7, lib.BF16, 0, 0.0), (5, 0, 0, 5, lib.F32, 1, 0.0)]
+    places = [(skew, 1, 0, [], []), (0, 0, 1, [rows], [1]), None, (0, 0, 0, [], [])]
+    return code, places

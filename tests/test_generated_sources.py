@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from tensorcrate_amd import _build, lib
-from tests.common import Code, column_broadcast, identity_place
+from tests.common import Code, column_broadcast, identity_place, run_form_program
 
 CSRC = Path(__file__).resolve().parent.parent / "tensorcrate_amd" / "csrc"
 RUNTIME_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-Xclang", "-target-feature",
@@ -98,3 +98,46 @@ def test_a_misaligned_or_offset_source_takes_the_general_form(tmp_path):
     aligned = statistics_source(lib.F32, layer_norm(lib.F32, cols), places, rows, cols, 0x10000, stats)
     misaligned = statistics_source(lib.F32, layer_norm(lib.F32, cols), places, rows, cols, 0x10004, stats)
     assert "const float (&held)" in aligned and "const float (&held)" not in misaligned
+
+
+def fused_source(dtype, code, places, rows, cols, pointers):
+    enc, pl = lib._program(code, places)
+    inputs = (ctypes.c_void_p * len(pointers))(*pointers)
+    length = ctypes.c_uint64()
+    lib.call("tc_fused_source", dtype, enc, len(code), pl, len(places), inputs, len(pointers), rows, cols, None, 0,
+             ctypes.byref(length))
+    out = ctypes.create_string_buffer(length.value + 1)
+    lib.call("tc_fused_source", dtype, enc, len(code), pl, len(places), inputs, len(pointers), rows, cols, out,
+             length.value + 1, ctypes.byref(length))
+    return out.value.decode()
+
+
+@pytest.mark.parametrize("dtype", [lib.F32, lib.F16, lib.BF16])
+@pytest.mark.parametrize("cols,skew,form", [(1000, 0, "tc_fused_runs"), (70, 0, "tc_fused_general"),
+                                            (1000, 1, "tc_fused_general")],
+                         ids=["runs", "cols-not-whole-runs", "misaligned-bias"])
+def test_broadcast_programs_compile_in_the_form_their_operands_allow(tmp_path, dtype, cols, skew, form):
+    # A program with broadcast operands runs in runs of eight columns when
+    # cols is a multiple of 8 and its operands are 16-byte aligned (here the
+    # f16 bias one element off makes it misaligned), else in the general
+    # form; both compile, without scratch.
+    rows = 4099
+    code, places = run_form_program(rows, skew)
+    places[2] = identity_place(rows, cols)
+    source = fused_source(dtype, code, places, rows, cols, [0x10000, 0x20000, 0x30000, 0x40000])
+    assert f"void __launch_bounds__(256) {form}(" in source
+    if form == "tc_fused_runs":
+        assert "tc::load_wide<8>(in[2]" in source and "tc::store_wide<8" in source
+    text = compile_kernel(tmp_path, form, source)
+    assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
+
+
+def test_the_composed_layer_norm_program_runs_in_runs(tmp_path):
+    # The program pass of the composed layer norm: x and gamma in runs, the
+    # row's two statistics one load a run.
+    rows, cols = 8192, 8192
+    places = [identity_place(rows, cols), (0, 1, 0, [], []), column_broadcast(rows)]
+    source = fused_source(lib.F32, layer_norm(lib.F32, cols), places, rows, cols, [0x10000, 0x20000, 0x30000, 0x40000])
+    assert "tc_fused_runs(" in source
+    text = compile_kernel(tmp_path, "layer_norm_runs", source)
+    assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
