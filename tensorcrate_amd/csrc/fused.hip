@@ -1316,6 +1316,13 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
     }
     const uint64_t packs = (cols + 64 * per - 1) / (64 * per);  // packs a lane holds
     if (packs * per > 128) return false;
+    // Three waves a SIMD for long f32 rows: a wave holding a whole
+    // 8192-element f32 row takes 169 VGPRs unprompted, one past the 168
+    // three waves can have (154 when asked, nothing spilled), and the third
+    // row in flight on each SIMD hides more of the others' loads.  Shorter
+    // or 16-bit rows fit three waves anyway (asked, an f16 row of 8192
+    // spilled).
+    const std::string occupancy = size == 4 && packs > 24 ? " __attribute__((amdgpu_waves_per_eu(3)))" : "";
     // The program's loads of the same elements: the same storage, type and
     // place.
     std::vector<bool> held(count, false);
@@ -1376,7 +1383,8 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
         << kMomentsSource
         << "__device__ __forceinline__ void unpack(const uint4 w, float (&x)[" << P << "]) {\n" << unpack << "}\n"
-           "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_row_statistics(Program p, Sources src,\n"
+           "extern \"C\" __global__ void __launch_bounds__(256)" << occupancy << "\n"
+           "tc_fused_row_statistics(Program p, Sources src,\n"
            "    uint32_t rows, uint32_t cols) {\n"
            "  // The wave, and so its row, said to be uniform: the row's buffer\n"
            "  // resource then lives in scalar registers.\n"
