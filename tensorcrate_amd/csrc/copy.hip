@@ -422,7 +422,13 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
         if (wide) {
             const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
             uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-            const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>(blocks, 8 * compute_units()));
+            // As many blocks as are resident at once (the tile's 32 KiB of
+            // LDS leaves room for five a CU), each walking the same number of
+            // tiles, so no second round runs part-empty: 2048 tiles take
+            // 1024 blocks of two rather than 1280 blocks and then 768.
+            const uint64_t resident = 5 * static_cast<uint64_t>(compute_units());
+            const uint64_t per_block = (blocks + resident - 1) / resident;
+            const uint32_t grid = static_cast<uint32_t>((blocks + per_block - 1) / per_block);
             if (stream_tiles) {
                 tile4_kernel<I, true, TA, TB><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
             } else {
