@@ -351,6 +351,17 @@ template <typename O, bool A_KC, bool B_KC, class EPI = PlainStore>
 void launch_inplace32(const float* a, const float* b, O* c, uint32_t m, uint32_t k, uint32_t n, bool accumulate,
                       hipStream_t s, const EPI& epi = EPI{}) {
     const uint32_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+    // Too few 128 x 128 tiles for two blocks on every CU (a 4096 x 1024
+    // product has 256): 128 x 64 tiles, twice the blocks, so the two-blocks-
+    // a-CU overlap still happens.
+    if constexpr (!EPI::kProgram) {
+        if (tiles < 2 * static_cast<uint32_t>(compute_units())) {
+            const uint32_t narrow = ((m + 127) / 128) * ((n + 63) / 64);
+            inplace32_kernel<O, A_KC, B_KC, 128, 64, EPI><<<narrow, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate,
+                                                                                     epi);
+            return;
+        }
+    }
     inplace32_kernel<O, A_KC, B_KC, 128, 128, EPI><<<tiles, kThreads, 0, s>>>(a, b, c, m, n, k, accumulate, epi);
 }
 
