@@ -1292,19 +1292,23 @@ const char* const kMomentsSource =
     "}\n";
 
 // The statistics kernel for one source whose place is its own rows x cols
-// row-major matrix (a layer norm's x): a wave a row, the row loaded once as
-// 16-byte packs into registers (a lane holds packs lane, lane + 64, ...),
-// each lane's moments taken in two passes over its registers and the
-// wave's lanes merged by Chan's update, and the program then run over the
-// held packs, a pack's elements a call, its loads of that same matrix
-// reading the registers.  The row is read from memory once, where the
-// general form reads it again for the program.  Taken when the source is
-// 16-byte aligned, rows are whole packs and a lane holds at most 128 values
-// (cols up to 8192); false otherwise.
+// row-major matrix (a layer norm's x): one to four waves a row (`waves`),
+// the row loaded once as 16-byte packs into registers (the row's lane t
+// holds packs t, t + 64 waves, ...), each lane's moments taken in two passes
+// over its registers, the wave's lanes merged by Chan's update in a fixed
+// shuffle tree and the row's waves through LDS in a fixed tree, and the
+// program then run over the held packs, a pack's elements a call, its
+// loads of that same matrix reading the registers.  The row is read from
+// memory once, where the general form reads it again for the program.
+// Long rows take more waves, so a lane holds at most 32 values where it
+// can: a wave per row of up to 2048 elements, two up to 4096, else four.
+// Taken when the source is 16-byte aligned, rows are whole packs and a
+// lane holds at most 128 values (cols up to 32768); false otherwise.
 bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                      const void* const* inputs, uint32_t input_count, void* const* outputs, uint64_t cols,
                      const tc_row_stat& st, uint32_t sources, const tc_row_stat* statistics,
-                     uint32_t statistic_count, std::vector<float>* constants, std::string* out) {
+                     uint32_t statistic_count, std::vector<float>* constants, std::string* out,
+                     uint32_t* waves_out) {
     if (sources != 1) return false;
     const uint32_t size = st.source_dtype == TC_F32 ? 4 : (st.source_dtype == TC_F16 || st.source_dtype == TC_BF16) ? 2 : 0;
     if (size == 0) return false;
@@ -1314,15 +1318,10 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
         reinterpret_cast<uintptr_t>(st.source) % 16 != 0) {
         return false;
     }
-    const uint64_t packs = (cols + 64 * per - 1) / (64 * per);  // packs a lane holds
+    const uint32_t waves = cols <= 2048 ? 1 : cols <= 4096 ? 2 : 4;  // waves a row
+    const uint64_t lanes = 64 * waves;
+    const uint64_t packs = (cols + lanes * per - 1) / (lanes * per);  // packs a lane holds
     if (packs * per > 128) return false;
-    // Three waves a SIMD for long f32 rows: a wave holding a whole
-    // 8192-element f32 row takes 169 VGPRs unprompted, one past the 168
-    // three waves can have (154 when asked, nothing spilled), and the third
-    // row in flight on each SIMD hides more of the others' loads.  Shorter
-    // or 16-bit rows fit three waves anyway (asked, an f16 row of 8192
-    // spilled).
-    const std::string occupancy = size == 4 && packs > 24 ? " __attribute__((amdgpu_waves_per_eu(3)))" : "";
     // The program's loads of the same elements: the same storage, type and
     // place.
     std::vector<bool> held(count, false);
@@ -1373,6 +1372,8 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
                  "    x[j] = tc_round<" + T + ">(" + widen + ");\n"
                  "  }\n";
     }
+    const std::string W = std::to_string(waves), L = std::to_string(lanes),
+                      B = std::to_string(lanes * 16), R = std::to_string(4 / waves);
     std::ostringstream src;
     src << "#include \"device.hpp\"\n"
            "struct Program {\n" << compiled_members()
@@ -1383,13 +1384,27 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
         << kMomentsSource
         << "__device__ __forceinline__ void unpack(const uint4 w, float (&x)[" << P << "]) {\n" << unpack << "}\n"
-           "extern \"C\" __global__ void __launch_bounds__(256)" << occupancy << "\n"
+           "extern \"C\" __global__ void __launch_bounds__(256)\n"
            "tc_fused_row_statistics(Program p, Sources src,\n"
            "    uint32_t rows, uint32_t cols) {\n"
-           "  // The wave, and so its row, said to be uniform: the row's buffer\n"
-           "  // resource then lives in scalar registers.\n"
+           "  // " << W << " wave(s) a row, " << R << " row(s) a block: the wave, its row\n"
+           "  // and its part of the row are uniform, so the row's buffer\n"
+           "  // resource lives in scalar registers.  Every wave of the block\n"
+           "  // runs every turn of the loop (one past the last row repeats the\n"
+           "  // last row's work and stores nothing), so the block's barriers\n"
+           "  // are met by all of its waves.\n"
            "  const uint32_t lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);\n"
-           "  for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {\n"
+           "  const uint32_t part = wave % " << W << "u, at = part * 64u + lane;\n";
+    if (waves > 1) {
+        src << "  // Each wave's merged moments, a slot per turn parity: a turn's\n"
+               "  // writes follow the previous turn's barrier, which every wave\n"
+               "  // passed only after reading the slot of the turn before.\n"
+               "  __shared__ float parts[2][4][3];\n";
+    }
+    src << "  uint32_t turn = 0;\n"
+           "  for (uint32_t base = blockIdx.x * " << R << "u; base < rows; base += gridDim.x * " << R << "u, turn++) {\n"
+           "    const bool on = base + wave / " << W << "u < rows;\n"
+           "    const uint32_t r = on ? base + wave / " << W << "u : rows - 1;\n"
            "    // The row as a buffer of its own bytes: a pack past its end\n"
            "    // loads zeros, with no branch, and every load's address is the\n"
            "    // lane's offset plus a constant.\n"
@@ -1401,20 +1416,27 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "    uint4 w[" << K << "];\n"
            "#pragma unroll\n"
            "    for (int k = 0; k < " << K << "; k++)\n"
-           "      w[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, lane * 16u, k * 1024u, 0));\n"
+           "      w[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, at * 16u, k * " << B
+        << "u, 0));\n"
            "    // The lane's values in two passes: their mean, then the squared\n"
            "    // deviations from it; then the wave's lanes merged.\n"
            "    // The row's first element, when finite, is subtracted first and\n"
            "    // added back to the mean once: rows whose mean is large against\n"
            "    // their spread keep their accuracy through the lanes' merges.\n"
-           "    float first[" << P << "];\n"
-           "    unpack(w[0], first);\n"
-           "    float shift = __shfl(first[0], 0, 64);\n"
-           "    if (!isfinite(shift)) shift = 0.0f;\n"
+           "    float first[" << P << "];\n";
+    if (waves == 1) {
+        src << "    unpack(w[0], first);\n"
+               "    float shift = __shfl(first[0], 0, 64);\n";
+    } else {
+        src << "    // (Lane 0 of the row's first wave holds it; the others load it.)\n"
+               "    unpack(__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, 0u, 0u, 0)), first);\n"
+               "    float shift = first[0];\n";
+    }
+    src << "    if (!isfinite(shift)) shift = 0.0f;\n"
            "    float n = 0.0f, sum = 0.0f;\n"
            "#pragma unroll\n"
            "    for (int k = 0; k < " << K << "; k++) {\n"
-           "      if ((lane + 64u * k) * " << P << "u < cols) {\n"
+           "      if ((at + " << L << "u * k) * " << P << "u < cols) {\n"
            "        float x[" << P << "];\n"
            "        unpack(w[k], x);\n"
            "        for (int j = 0; j < " << P << "; j++) sum += x[j] - shift;\n"
@@ -1428,7 +1450,7 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "    float q = 0.0f;\n"
            "#pragma unroll\n"
            "    for (int k = 0; k < " << K << "; k++) {\n"
-           "      if ((lane + 64u * k) * " << P << "u < cols) {\n"
+           "      if ((at + " << L << "u * k) * " << P << "u < cols) {\n"
            "        float x[" << P << "];\n"
            "        unpack(w[k], x);\n"
            "        for (int j = 0; j < " << P << "; j++) {\n"
@@ -1436,9 +1458,30 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "          q += d * d;\n"
            "        }\n"
            "      }\n"
-           "    }\n"
-           "    const Moments m = wave_merge(Moments{n, lane_mean, q}, lane);\n"
-           "    float stat[" << S << "];\n";
+           "    }\n";
+    if (waves == 1) {
+        src << "    const Moments m = wave_merge(Moments{n, lane_mean, q}, lane);\n";
+    } else {
+        src << "    const Moments mine = wave_merge(Moments{n, lane_mean, q}, lane);\n"
+               "    if (lane == 0) {\n"
+               "      parts[turn & 1u][wave][0] = mine.n;\n"
+               "      parts[turn & 1u][wave][1] = mine.mean;\n"
+               "      parts[turn & 1u][wave][2] = mine.m2;\n"
+               "    }\n"
+               "    __syncthreads();\n"
+               "    // The row's waves in a fixed tree, the same bits on each.\n"
+               "    Moments each[" << W << "];\n"
+               "    for (uint32_t v = 0; v < " << W << "u; v++) {\n"
+               "      const float* slot = parts[turn & 1u][wave - part + v];\n"
+               "      each[v] = Moments{slot[0], slot[1], slot[2]};\n"
+               "    }\n";
+        if (waves == 2) {
+            src << "    const Moments m = merge(each[0], each[1]);\n";
+        } else {
+            src << "    const Moments m = merge(merge(each[0], each[1]), merge(each[2], each[3]));\n";
+        }
+    }
+    src << "    float stat[" << S << "];\n";
     for (uint32_t i = 0; i < statistic_count; i++) {
         src << "    stat[" << i << "] = tc_round<" << T << ">("
             << (statistics[i].which == TC_STAT_MEAN ? "m.mean + shift" : "m.m2") << ");\n";
@@ -1446,16 +1489,16 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
     src << "    // The lane's index made opaque here, so the columns of every pack\n"
            "    // are computed where they are used rather than hoisted out of the\n"
            "    // row loop, where they would hold a register each.\n"
-           "    uint32_t at_lane = lane;\n"
+           "    uint32_t at_lane = at;\n"
            "    asm volatile(\"\" : \"+v\"(at_lane));\n"
            "#pragma unroll\n"
            "    for (int k = 0; k < " << K << "; k++) {\n"
            "      uint32_t row[" << P << "], col[" << P << "];\n"
            "      bool live[" << P << "];\n"
            "      for (int j = 0; j < " << P << "; j++) {\n"
-           "        col[j] = (at_lane + 64u * k) * " << P << "u + j;\n"
+           "        col[j] = (at_lane + " << L << "u * k) * " << P << "u + j;\n"
            "        row[j] = r;\n"
-           "        live[j] = col[j] < cols;\n"
+           "        live[j] = on && col[j] < cols;\n"
            "      }\n"
            "      float x[" << P << "];\n"
            "      unpack(w[k], x);\n"
@@ -1466,6 +1509,7 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "    }\n"
            "  }\n"
            "}\n";
+    *waves_out = waves;
     *out = src.str();
     return true;
 }
@@ -1493,7 +1537,8 @@ struct RowStatisticsPlan {
     std::vector<float> constants;
     const tc_row_stat* first[4] = {};
     uint32_t sources = 0;
-    bool held = false;  // the form that holds each row in registers
+    bool held = false;    // the form that holds each row in registers
+    uint32_t waves = 1;   // the held form's waves a row (1, 2 or 4)
 };
 
 int plan_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
@@ -1546,7 +1591,7 @@ int plan_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t count, 
     std::ostringstream src;
     std::string held_source;
     if (held_row_source(code, count, dtype, places, inputs, input_count, outputs, cols, *first[0], sources,
-                        statistics, statistic_count, &constants, &held_source)) {
+                        statistics, statistic_count, &constants, &held_source, &plan->waves)) {
         src << held_source;
         plan->held = true;
     } else {
@@ -1670,11 +1715,15 @@ int tc::fused_row_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
     // enough loads in flight for HBM, while the rows in flight stay few
     // enough that a row's second read, for the program, finds it in the
     // caches (layer norm over 8192 x 8192 f32: 3.10 TB/s, against 2.91 at
-    // eight a CU).  The held form reads each row once, so it takes eight
-    // (the same layer norm: 4.97 TB/s at eight, 4.90 at four, 4.96 at two;
-    // streaming stores measured no faster).
-    const uint64_t wanted = (rows + 3) / 4,
-                   cap = static_cast<uint64_t>(compute_units()) * (plan.held ? 8 : 4);
+    // eight a CU).  The held form reads each row once and takes a workgroup
+    // for each 4 / waves rows, as many as there are: the rows of a launch
+    // spread over every CU as workgroups end, where a grid of eight a CU
+    // looping over them ends on a few CUs still at their last rows (the
+    // same layer norm, four waves a row: 5.16 TB/s, against 5.00 at eight a
+    // CU; a wave a row, 4.70 at eight a CU).
+    const uint64_t per_block = plan.held ? 4 / plan.waves : 4;
+    const uint64_t wanted = (rows + per_block - 1) / per_block,
+                   cap = plan.held ? wanted : static_cast<uint64_t>(compute_units()) * 4;
     const uint32_t blocks = static_cast<uint32_t>(wanted < cap ? wanted : cap);
     count_dispatch();
     const hipError_t error = hipModuleLaunchKernel(function, blocks, 1, 1, 256, 1, 1, 0, s, params, nullptr);

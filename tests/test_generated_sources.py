@@ -73,9 +73,14 @@ def compile_kernel(tmp_path, name, source):
     return target.read_text()
 
 
-@pytest.mark.parametrize("dtype,cols,held", [(lib.F32, 8192, True), (lib.F32, 4100, True), (lib.BF16, 1024, True),
-                                             (lib.F16, 8192, True), (lib.F32, 777, False), (lib.F32, 8300, False)])
-def test_statistics_kernels_compile_without_scratch(tmp_path, dtype, cols, held):
+@pytest.mark.parametrize("dtype,cols,held,waves", [
+    (lib.F32, 8192, True, 4), (lib.F32, 4100, True, 4), (lib.BF16, 1024, True, 1), (lib.F16, 8192, True, 4),
+    (lib.F32, 3000, True, 2), (lib.F32, 8300, True, 4), (lib.F32, 32768, True, 4), (lib.F32, 777, False, 0),
+    (lib.F32, 33000, False, 0)])
+def test_statistics_kernels_compile_without_scratch(tmp_path, dtype, cols, held, waves):
+    # Rows of up to 2048 elements take a wave each, up to 4096 two, longer
+    # ones four, up to 128 values a lane (32768 elements); rows not whole
+    # 16-byte packs, or longer, take the general form.
     rows = 64
     places = [identity_place(rows, cols), (0, 1, 0, [], []), column_broadcast(rows)]
     whole = identity_place(rows, cols)
@@ -86,6 +91,8 @@ def test_statistics_kernels_compile_without_scratch(tmp_path, dtype, cols, held)
     assert ("const float (&held)" in source) == held
     if held:
         assert re.search(r"v\d+\[e\] = held\[e\];", source)
+        assert f"// {waves} wave(s) a row, {4 // waves} row(s) a block" in source
+        assert ("__syncthreads();" in source) == (waves > 1)
     text = compile_kernel(tmp_path, "statistics", source)
     assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
 

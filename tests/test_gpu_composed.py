@@ -188,7 +188,8 @@ def test_row_sums_of_a_repeated_program_run_as_one_compiled_kernel(dtype):
     assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
 
 
-@pytest.mark.parametrize("shape", [(300, 777), (40, 8300), (300, 1024), (64, 8192), (33, 4100)])
+@pytest.mark.parametrize("shape", [(300, 777), (40, 8300), (301, 1024), (64, 8192), (33, 4100), (41, 3000),
+                                   (8, 33000)])
 @pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
 def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # From the program's second appearance its statistics and the program run
@@ -197,12 +198,15 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # oracle.  (x - mean) / (deviations / cols + 1) is this test's own
     # program; the moments fold in another order than the oracle's, which
     # moves the statistics by their last place at most.  Rows of 777 are
-    # ragged against a wave's 64 lanes and its 16-load batches; rows of 8300
-    # take more than eight batches a pass: both take the general form.  Rows
-    # of 1024 and 8192 (and of 4100 in f32, whose last packs fall past the
-    # row on some lanes) take the form that holds the row in registers and
-    # feeds the program's load of x from them.  A shape may find its kernel
-    # compiled already; either way the last call is one launch.
+    # not whole 16-byte packs in f32, and rows of 33000 hold more than 128
+    # values a lane over four waves: both take the general form.  The others
+    # take the form that holds the row in registers and feeds the program's
+    # load of x from them: a wave a row for 1024 (301 rows: the last
+    # workgroup's four waves have one row), two for 3000 (41 rows: the last
+    # workgroup's second pair of waves has none), four for 4100, 8192 and
+    # 8300 (whose last packs fall past the row on some lanes).  A shape may
+    # find its kernel compiled already; either way the last call is one
+    # launch.
     import ctypes
 
     rows, cols = shape
@@ -239,12 +243,13 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     assert launches == 1
 
 
-@pytest.mark.parametrize("cols", [777, 1024, 8192])
+@pytest.mark.parametrize("cols", [777, 1024, 3000, 8192])
 @pytest.mark.parametrize("offset", [1000.0, 10000.0])
 def test_row_statistics_of_offset_rows_keep_two_pass_accuracy(offset, cols):
     # Rows whose mean is large against their spread (offset + U(-1, 1)): the
     # one-kernel statistics, in either of their forms (the row held in
-    # registers for 1024 and 8192 columns, the batched walk for 777), shift
+    # registers by one, two or four waves for 1024, 3000 and 8192 columns,
+    # the batched walk for 777), shift
     # each row by its first element, and are at least as close to the exact
     # moments as the reference's own two passes (the oracle's sequential f32
     # mean, then squared deviations from it, statistics/mod.rs:419-441), or
