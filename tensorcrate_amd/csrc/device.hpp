@@ -221,4 +221,30 @@ __device__ __forceinline__ void store_wide(void* base, uint32_t dtype, uint64_t 
     }
 }
 
+// q[e] = x[e] / d, each the IEEE f32 quotient, for a divisor the same for
+// every element (a function of a row's statistics and constants), at about
+// half the cost of E f32 divisions: one f64 reciprocal, then a product a
+// quotient.  r = RN64(1/d) and RN64(x r) are within 2^-52 of x / d
+// relatively, while x / d, a quotient of two 24-bit significands, lies at
+// least 2^-49 from every midpoint between two normal floats (or the
+// overflow threshold) unless it is one, which takes a 25-bit significand
+// that no 24-bit x has: so rounding the product to f32 gives the
+// correctly rounded quotient whenever that is a normal float.  Any other
+// result (zero, subnormal, infinite, NaN; so any zero, infinite or NaN
+// operand) is recomputed by the f32 division itself.
+template <int E>
+__device__ __forceinline__ void div_uniform(float (&q)[E], const float (&x)[E], float d) {
+    const double r = 1.0 / static_cast<double>(d);
+    bool other = false;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        q[e] = static_cast<float>(static_cast<double>(x[e]) * r);
+        other |= !__builtin_amdgcn_classf(q[e], 0x108);  // not a normal float (class bits 3 and 8)
+    }
+    if (other) {
+#pragma unroll
+        for (int e = 0; e < E; e++) q[e] = x[e] / d;
+    }
+}
+
 }  // namespace tc

@@ -624,6 +624,11 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
     // register reads 0.
     bool exact[TC_FUSED_REGISTERS];
     for (bool& e : exact) e = true;
+    // Whether a register holds the same value for every element of a group
+    // (a function of constants and the row's statistics, whose groups lie
+    // in one row): a division by such a value takes tc::div_uniform.
+    bool uniform[TC_FUSED_REGISTERS];
+    for (bool& u : uniform) u = true;
     auto at = [&](uint8_t r) { return reg[r].empty() ? std::string("0.0f") : reg[r] + "[e]"; };
     const std::string each = "    for (int e = 0; e < " + std::to_string(elems) + "; e++) ";
     for (uint32_t pc = 0; pc < count; pc++) {
@@ -646,6 +651,22 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
         // type (tc_round_run, as tc_round rounds one value) unless `rounded`
         // is left false because the rounding could change no bit.
         bool rounded = true;
+        bool same = true;  // the value is uniform, as defined above
+        switch (in.kind) {
+            case 0: same = stat_first >= 0 && in.a >= stat_first; break;
+            case 1: break;
+            case 3: same = uniform[in.a]; break;
+            default: same = uniform[in.a] && uniform[in.b]; break;
+        }
+        if (in.kind == 2 && in.op == TC_DIV && uniform[in.b] && !same && !reg[in.a].empty()) {
+            src << "    float " << v << "[" << elems << "];\n    tc::div_uniform<" << elems << ">(" << v << ", "
+                << reg[in.a] << ", " << (reg[in.b].empty() ? std::string("0.0f") : reg[in.b] + "[0]") << ");\n"
+                << round_run << v << ");\n";
+            reg[in.dst] = v;
+            exact[in.dst] = true;
+            uniform[in.dst] = false;
+            continue;
+        }
         src << "    float " << v << "[" << elems << "];\n" << each << v << "[e] = ";
         switch (in.kind) {
             case 0:
@@ -708,6 +729,7 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
         if (rounded) src << round_run << v << ");\n";
         reg[in.dst] = v;
         if (in.kind != 1) exact[in.dst] = true;
+        uniform[in.dst] = same;
     }
     return src.str();
 }
@@ -1302,8 +1324,14 @@ const char* const kMomentsSource =
 // memory once, where the general form reads it again for the program.
 // Long rows take more waves, so a lane holds at most 32 values where it
 // can: a wave per row of up to 2048 elements, two up to 4096, else four.
-// Taken when the source is 16-byte aligned, rows are whole packs and a
-// lane holds at most 128 values (cols up to 32768); false otherwise.
+// The program's loads of what every row reads alike (a row vector, a
+// scalar) are issued once for each of the lane's packs, behind the row's
+// loads: left inside the program, each would wait for the stores before
+// it, loads and stores retiring in order.  A workgroup takes one group of
+// rows, and the launch as many workgroups as there are groups.  Taken when
+// the source is 16-byte aligned, rows are whole packs and a lane holds at
+// most 64 values (cols up to 16384; the row and a row vector then take
+// about 150 registers); false otherwise.
 bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                      const void* const* inputs, uint32_t input_count, void* const* outputs, uint64_t cols,
                      const tc_row_stat& st, uint32_t sources, const tc_row_stat* statistics,
@@ -1321,7 +1349,7 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
     const uint32_t waves = cols <= 2048 ? 1 : cols <= 4096 ? 2 : 4;  // waves a row
     const uint64_t lanes = 64 * waves;
     const uint64_t packs = (cols + lanes * per - 1) / (lanes * per);  // packs a lane holds
-    if (packs * per > 128) return false;
+    if (packs * per > 64) return false;
     // The program's loads of the same elements: the same storage, type and
     // place.
     std::vector<bool> held(count, false);
@@ -1351,8 +1379,36 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
                        (lp.lead == 0 || lp.steps[0] % 4 == 0) && aligned(inputs[in.a], in.b);
         }
     }
+    // Loads that read the same elements in every row (a row vector such as
+    // a layer norm's gamma, a scalar) are loaded for every pack of the lane
+    // once, before the loop over rows: a load inside the program would wait
+    // for the stores before it, as loads and stores retire in order.
+    std::vector<bool> invariant(count, false);
+    const std::string round = "tc_round<" + std::to_string(dtype) + ">";
+    const std::string each_pack = "    for (int e = 0; e < " + std::to_string(per) + "; e++) ";
+    std::ostringstream members, loader;
+    for (uint32_t pc = 0; pc < count; pc++) {
+        const tc_encoded& in = code[pc];
+        if (in.kind != 0 || held[pc] || in.a >= input_count) continue;
+        const tc_place& lp = places[in.op];
+        const bool same_rows = lp.lead == 0 || (lp.lead == 1 && lp.steps[0] == 0);
+        if (!same_rows || (lp.col_step != 0 && !runs[pc])) continue;
+        invariant[pc] = true;
+        runs[pc] = false;
+        const std::string name = "inv.i" + std::to_string(pc), pl = "places[" + std::to_string(in.op) + "]";
+        members << "    float i" << pc << "[" << per << "];\n";
+        if (lp.col_step == 1) {
+            loader << each_pack << name << "[e] = 0.0f;\n    if (live) tc::load_run<" << per << ">(in["
+                   << int(in.a) << "], " << int(in.b) << "u, " << place_index(lp, pl, "0u", "col") << ", " << name
+                   << ");\n" << each_pack << name << "[e] = " << round << "(" << name << "[e]);\n";
+        } else {
+            loader << "    {\n      const float x = live ? " << round << "(tc::load_as(in[" << int(in.a) << "], "
+                   << int(in.b) << "u, " << place_index(lp, pl, "0u", "0u") << ")) : 0.0f;\n  " << each_pack
+                   << name << "[e] = x;\n    }\n";
+        }
+    }
     const std::string body = group_body(code, count, dtype, false, static_cast<int>(per), places, constants, false,
-                                        static_cast<int>(input_count), &held, &runs);
+                                        static_cast<int>(input_count), &held, &runs, &invariant);
     if (constants->size() > static_cast<size_t>(kInlineCode)) return false;
     const std::string P = std::to_string(per), K = std::to_string(packs), S = std::to_string(statistic_count),
                       T = std::to_string(dtype);
@@ -1377,9 +1433,12 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
     std::ostringstream src;
     src << "#include \"device.hpp\"\n"
            "struct Program {\n" << compiled_members()
-        << "  __device__ __forceinline__ void group(const bool (&live)[" << P << "], const uint32_t (&row)[" << P
+        << "  struct Invariant {\n" << members.str() << "  };\n"
+           "  __device__ __forceinline__ void invariant(Invariant& inv, bool live, uint32_t col) const {\n"
+        << loader.str() << "  }\n"
+           "  __device__ __forceinline__ void group(const bool (&live)[" << P << "], const uint32_t (&row)[" << P
         << "],\n      const uint32_t (&col)[" << P << "], uint32_t N, const float (&stat)[" << S
-        << "], const float (&held)[" << P << "]) const {\n"
+        << "], const float (&held)[" << P << "],\n      const Invariant& inv) const {\n"
         << body << "  }\n};\n"
            "struct Sources { const void* in[4]; tc::DevicePlace places[4]; };\n"
         << kMomentsSource
@@ -1389,35 +1448,46 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "    uint32_t rows, uint32_t cols) {\n"
            "  // " << W << " wave(s) a row, " << R << " row(s) a block: the wave, its row\n"
            "  // and its part of the row are uniform, so the row's buffer\n"
-           "  // resource lives in scalar registers.  Every wave of the block\n"
-           "  // runs every turn of the loop (one past the last row repeats the\n"
-           "  // last row's work and stores nothing), so the block's barriers\n"
-           "  // are met by all of its waves.\n"
+           "  // resource lives in scalar registers.\n"
            "  const uint32_t lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);\n"
            "  const uint32_t part = wave % " << W << "u, at = part * 64u + lane;\n";
     if (waves > 1) {
-        src << "  // Each wave's merged moments, a slot per turn parity: a turn's\n"
-               "  // writes follow the previous turn's barrier, which every wave\n"
-               "  // passed only after reading the slot of the turn before.\n"
-               "  __shared__ float parts[2][4][3];\n";
+        src << "  // Each wave's merged moments.\n"
+               "  __shared__ float parts[4][3];\n";
     }
-    src << "  uint32_t turn = 0;\n"
-           "  for (uint32_t base = blockIdx.x * " << R << "u; base < rows; base += gridDim.x * " << R << "u, turn++) {\n"
-           "    const bool on = base + wave / " << W << "u < rows;\n"
-           "    const uint32_t r = on ? base + wave / " << W << "u : rows - 1;\n"
-           "    // The row as a buffer of its own bytes: a pack past its end\n"
-           "    // loads zeros, with no branch, and every load's address is the\n"
-           "    // lane's offset plus a constant.\n"
-           "    const __amdgpu_buffer_rsrc_t line = __builtin_amdgcn_make_buffer_rsrc(\n"
-           "        const_cast<uint8_t*>(static_cast<const uint8_t*>(src.in[0]) + (uint64_t)r * cols * " << size
-        << "u), 0,\n        cols * " << size << "u, 0x00020000);\n"
-           "    // The row's packs as loaded (16-bit elements stay packed, two a\n"
-           "    // register), unpacked at each use.\n"
-           "    uint4 w[" << K << "];\n"
+    src << "  // The workgroup's row for this wave (one past the last row repeats\n"
+           "  // the last row's work and stores nothing, so the workgroup's\n"
+           "  // barrier is met by all of its waves).\n"
+           "  const uint32_t first_row = blockIdx.x * " << R << "u + wave / " << W << "u;\n"
+           "  const bool on = first_row < rows;\n"
+           "  const uint32_t r = on ? first_row : rows - 1;\n"
+           "  // The row as a buffer of its own bytes: a pack past its end loads\n"
+           "  // zeros, with no branch, and every load's address is the lane's\n"
+           "  // offset plus a constant.\n"
+           "  const __amdgpu_buffer_rsrc_t line = __builtin_amdgcn_make_buffer_rsrc(\n"
+           "      const_cast<uint8_t*>(static_cast<const uint8_t*>(src.in[0]) + (uint64_t)r * cols * " << size
+        << "u), 0,\n      cols * " << size << "u, 0x00020000);\n"
+           "  // The row's packs as loaded (16-bit elements stay packed, two a\n"
+           "  // register), unpacked at each use.\n"
+           "  uint4 w[" << K << "];\n"
            "#pragma unroll\n"
-           "    for (int k = 0; k < " << K << "; k++)\n"
-           "      w[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, at * 16u, k * " << B
-        << "u, 0));\n"
+           "  for (int k = 0; k < " << K << "; k++)\n"
+           "    w[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, at * 16u, k * " << B
+        << "u, 0));\n";
+    if (waves > 1) {
+        src << "  // The row's first pack, which every lane loads (lane 0 of the\n"
+               "  // row's first wave holds it in w[0] as well).\n"
+               "  const uint4 head = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, 0u, 0u, 0));\n";
+    }
+    src << "  // The program's loads of what every row reads alike, for each of\n"
+           "  // the lane's packs, issued behind the row's.\n"
+           "  typename Program::Invariant inv[" << K << "];\n"
+           "#pragma unroll\n"
+           "  for (int k = 0; k < " << K << "; k++) {\n"
+           "    const uint32_t col = (at + " << L << "u * k) * " << P << "u;\n"
+           "    p.invariant(inv[k], col < cols, col);\n"
+           "  }\n"
+           "  {\n"
            "    // The lane's values in two passes: their mean, then the squared\n"
            "    // deviations from it; then the wave's lanes merged.\n"
            "    // The row's first element, when finite, is subtracted first and\n"
@@ -1428,8 +1498,7 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
         src << "    unpack(w[0], first);\n"
                "    float shift = __shfl(first[0], 0, 64);\n";
     } else {
-        src << "    // (Lane 0 of the row's first wave holds it; the others load it.)\n"
-               "    unpack(__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(line, 0u, 0u, 0)), first);\n"
+        src << "    unpack(head, first);\n"
                "    float shift = first[0];\n";
     }
     src << "    if (!isfinite(shift)) shift = 0.0f;\n"
@@ -1464,15 +1533,15 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
     } else {
         src << "    const Moments mine = wave_merge(Moments{n, lane_mean, q}, lane);\n"
                "    if (lane == 0) {\n"
-               "      parts[turn & 1u][wave][0] = mine.n;\n"
-               "      parts[turn & 1u][wave][1] = mine.mean;\n"
-               "      parts[turn & 1u][wave][2] = mine.m2;\n"
+               "      parts[wave][0] = mine.n;\n"
+               "      parts[wave][1] = mine.mean;\n"
+               "      parts[wave][2] = mine.m2;\n"
                "    }\n"
                "    __syncthreads();\n"
                "    // The row's waves in a fixed tree, the same bits on each.\n"
                "    Moments each[" << W << "];\n"
                "    for (uint32_t v = 0; v < " << W << "u; v++) {\n"
-               "      const float* slot = parts[turn & 1u][wave - part + v];\n"
+               "      const float* slot = parts[wave - part + v];\n"
                "      each[v] = Moments{slot[0], slot[1], slot[2]};\n"
                "    }\n";
         if (waves == 2) {
@@ -1502,7 +1571,7 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
            "      }\n"
            "      float x[" << P << "];\n"
            "      unpack(w[k], x);\n"
-           "      p.group(live, row, col, cols, stat, x);\n"
+           "      p.group(live, row, col, cols, stat, x, inv[k]);\n"
            "      // One pack's program at a time: hoisting every pack's loads\n"
            "      // ahead of the others' arithmetic would spill the row.\n"
            "      __builtin_amdgcn_sched_barrier(0);\n"

@@ -75,12 +75,14 @@ def compile_kernel(tmp_path, name, source):
 
 @pytest.mark.parametrize("dtype,cols,held,waves", [
     (lib.F32, 8192, True, 4), (lib.F32, 4100, True, 4), (lib.BF16, 1024, True, 1), (lib.F16, 8192, True, 4),
-    (lib.F32, 3000, True, 2), (lib.F32, 8300, True, 4), (lib.F32, 32768, True, 4), (lib.F32, 777, False, 0),
-    (lib.F32, 33000, False, 0)])
+    (lib.F32, 3000, True, 2), (lib.F32, 8300, True, 4), (lib.F32, 16384, True, 4), (lib.F32, 777, False, 0),
+    (lib.F32, 16400, False, 0)])
 def test_statistics_kernels_compile_without_scratch(tmp_path, dtype, cols, held, waves):
     # Rows of up to 2048 elements take a wave each, up to 4096 two, longer
-    # ones four, up to 128 values a lane (32768 elements); rows not whole
-    # 16-byte packs, or longer, take the general form.
+    # ones four, up to 64 values a lane (16384 elements); rows not whole
+    # 16-byte packs, or longer, take the general form.  The held form reads
+    # gamma, which every row reads alike, once for each of a lane's packs
+    # before the program.
     rows = 64
     places = [identity_place(rows, cols), (0, 1, 0, [], []), column_broadcast(rows)]
     whole = identity_place(rows, cols)
@@ -93,6 +95,7 @@ def test_statistics_kernels_compile_without_scratch(tmp_path, dtype, cols, held,
         assert re.search(r"v\d+\[e\] = held\[e\];", source)
         assert f"// {waves} wave(s) a row, {4 // waves} row(s) a block" in source
         assert ("__syncthreads();" in source) == (waves > 1)
+        assert "p.invariant(inv[k], col < cols, col);" in source and re.search(r"v\d+\[e\] = inv\.i\d+\[e\];", source)
     text = compile_kernel(tmp_path, "statistics", source)
     assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
 

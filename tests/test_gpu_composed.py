@@ -198,7 +198,7 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # oracle.  (x - mean) / (deviations / cols + 1) is this test's own
     # program; the moments fold in another order than the oracle's, which
     # moves the statistics by their last place at most.  Rows of 777 are
-    # not whole 16-byte packs in f32, and rows of 33000 hold more than 128
+    # not whole 16-byte packs in f32, and rows of 33000 hold more than 64
     # values a lane over four waves: both take the general form.  The others
     # take the form that holds the row in registers and feeds the program's
     # load of x from them: a wave a row for 1024 (301 rows: the last
@@ -286,3 +286,40 @@ def test_row_statistics_of_offset_rows_keep_two_pass_accuracy(offset, cols):
         relative = 1e-5 if call else cols * 2.0 ** -24
         assert np.all(dev_err <= np.maximum(2 * ref_dev_err, relative * exact_dev)), \
             (call, dev_err.max(), ref_dev_err.max())
+
+
+@pytest.mark.parametrize("cols", [1024, 3000, 8192])
+@pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
+def test_a_division_by_a_statistic_keeps_the_divisions_bits(dtype, cols):
+    # The one-kernel form divides by a function of the row's statistics with
+    # one reciprocal a row and a product an element (the f32 division kept
+    # for any quotient not a normal float).  The program also stores the
+    # statistics it read, so the oracle can run the same program on them:
+    # every quotient must be its bits, for one, two and four waves a row,
+    # and from the composed first call too.
+    rows = 33
+    code = Code()
+    x = code.load(0, 0, dtype)
+    mean = code.load(1, 1, dtype)
+    deviations = code.load(1, 2, dtype)
+    scale = code.binary(lib.MUL, deviations, code.const(np.float32(1.0 / cols)))
+    code.store(code.binary(lib.DIV, code.binary(lib.SUB, x, mean), scale), dtype, 0)
+    code.store(mean, dtype, 1)
+    code.store(deviations, dtype, 2)
+    places = [identity_place(rows, cols), column_broadcast(rows)]
+    whole = identity_place(rows, cols)
+    xs = to_kind(np.random.default_rng(cols).uniform(-3, 3, rows * cols).astype(np.float32), dtype)
+    dx = lib.Buffer.of(xs)
+    host = np.float32 if dtype == lib.F32 else np.uint16
+    for call in range(3):
+        out = [lib.Buffer(rows * cols * np.dtype(host).itemsize) for _ in range(3)]
+        lib.fused_with_statistics(dtype, code.code, places, [(dx, xs.size)], [(o, rows * cols) for o in out],
+                                  rows, cols,
+                                  [(dx, xs.size, dtype, whole, "mean"), (dx, xs.size, dtype, whole, "deviations")])
+        got = [o.download(host, rows * cols) for o in out]
+        means = got[1].reshape(rows, cols)[:, 0].copy()
+        devs = got[2].reshape(rows, cols)[:, 0].copy()
+        want = np.zeros(rows * cols, host)
+        oracle.fused(dtype, code.code[:-2], places, [xs, means, devs], [want], rows, cols)
+        assert np.array_equal(got[0].view(np.uint32 if dtype == lib.F32 else np.uint16),
+                              want.view(np.uint32 if dtype == lib.F32 else np.uint16)), call

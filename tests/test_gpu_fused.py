@@ -9,7 +9,7 @@ from oracle import binding as oracle
 from oracle import mlp
 from tensorcrate_amd import lib
 from tensorcrate_amd.optim import EXACT, REASSOCIATE, Adam, identity_place
-from tests.common import KINDS, bits_equal, run_form_program, same_bits, to_kind, widen
+from tests.common import KINDS, Code, bits_equal, row_broadcast, run_form_program, same_bits, to_kind, widen
 from tests.host_programs import host_adam_program
 
 pytestmark = pytest.mark.gpu
@@ -329,3 +329,47 @@ def test_a_broadcast_program_in_runs_stays_exact(rows, cols, skew):
                       [(g0, rows * cols), (g1, rows * cols)], rows, cols)
             assert same_bits(g0.download(np.uint16), out0, lib.BF16), dtype
             assert bits_equal(g1.download(np.float32), out1), dtype
+
+
+def _every_kind_of_f32(n, seed):
+    """Random bit patterns (every binade, subnormals, infinities, NaNs)
+    with zeros, extremes and the smallest subnormals among them."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32).copy()
+    x[:10] = [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-40, 3.4e38, -1.1754944e-38, 1.0]
+    return x
+
+
+@pytest.mark.parametrize("divisor", [3.0, 0.1, -7.0, 1e-39, 3e38, 1.0, 0.0])
+@pytest.mark.parametrize("rows,cols,form", [(3, 4096, "dense"), (64, 1000, "runs"), (37, 70, "elements")])
+def test_a_division_by_a_constant_keeps_the_divisions_bits(rows, cols, form, divisor):
+    # A division by a value the same for every element (here a constant)
+    # compiles to one reciprocal and a product an element, with the f32
+    # division kept for every quotient that is not a normal float; every
+    # call (interpreted, then compiled), in every type and compiled form,
+    # gives the oracle's bits, over operands of every kind: quotients that
+    # overflow, land subnormal or are zero, infinities, NaNs, subnormal and
+    # zero divisors.  A second output of a row vector makes the program
+    # broadcast (the run form, or the element form for cols not a multiple
+    # of 8).
+    x = _every_kind_of_f32(rows * cols, cols)
+    code = Code()
+    q = code.binary(lib.DIV, code.load(0, 0, lib.F32), code.const(np.float32(divisor)))
+    code.store(q, lib.F32, 0)
+    places = [identity_place(rows, cols)]
+    inputs, device = [x], [lib.Buffer.of(x)]
+    if form != "dense":
+        vector = np.arange(cols, dtype=np.float32)
+        code.store(code.load(1, 1, lib.F32), lib.F32, 1)
+        places.append(row_broadcast(cols))
+        inputs.append(vector)
+        device.append(lib.Buffer.of(vector))
+    outputs = 1 if form == "dense" else 2
+    for dtype in KINDS:
+        want = [np.zeros(rows * cols, np.float32) for _ in range(outputs)]
+        oracle.fused(dtype, code.code, places, inputs, want, rows, cols)
+        for call in range(3):
+            got = [lib.Buffer(rows * cols * 4) for _ in range(outputs)]
+            lib.fused(dtype, code.code, places, [(d, a.size) for d, a in zip(device, inputs)],
+                      [(g, rows * cols) for g in got], rows, cols)
+            assert same_bits(got[0].download(np.float32), want[0], lib.F32), (dtype, call)
