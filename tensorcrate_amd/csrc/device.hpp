@@ -129,14 +129,23 @@ __device__ __forceinline__ void load_run(const void* base, uint32_t dtype, uint6
 
 // `E` consecutive elements stored from `index` on, each converted as
 // `store_as` converts it, four at a time; the same alignment as `load_run`.
-template <int E>
+// With NT the stores are non-temporal, as in `store_wide`.
+template <int E, bool NT = false>
 __device__ __forceinline__ void store_run(void* base, uint32_t dtype, uint64_t index, const float (&v)[E]) {
     static_assert(E % 4 == 0, "whole runs of four");
+    typedef uint32_t words4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t words2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int q = 0; q < E / 4; q++) {
         if (dtype == tc_ops::F32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(base) + index + 4 * q) =
-                make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            float* at = static_cast<float*>(base) + index + 4 * q;
+            const words4 w = {__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
+                              __float_as_uint(v[4 * q + 3])};
+            if (NT) {
+                __builtin_nontemporal_store(w, reinterpret_cast<words4*>(at));
+            } else {
+                *reinterpret_cast<words4*>(at) = w;
+            }
         } else {
             uint16_t h[4];
 #pragma unroll
@@ -144,8 +153,13 @@ __device__ __forceinline__ void store_run(void* base, uint32_t dtype, uint64_t i
                 h[j] = dtype == tc_ops::F16 ? __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[4 * q + j]))
                                             : f32_to_bf16_bits(v[4 * q + j]);
             }
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + index + 4 * q) =
-                make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+            uint16_t* at = static_cast<uint16_t*>(base) + index + 4 * q;
+            const words2 w = {h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16)};
+            if (NT) {
+                __builtin_nontemporal_store(w, reinterpret_cast<words2*>(at));
+            } else {
+                *reinterpret_cast<words2*>(at) = w;
+            }
         }
     }
 }

@@ -638,7 +638,7 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                 src << each << "sum += live[e] ? " << at(in.a) << " : 0.0f;\n";
             } else if (runs != nullptr && (*runs)[pc] && !reg[in.a].empty()) {
                 src << "    if (live[0]) tc::" << (wide ? "store_wide<" : "store_run<") << elems
-                    << (wide ? (stream ? ", true" : ", false") : "") << ">(out[" << int(in.aux) << "], " << int(in.b)
+                    << (stream ? ", true" : ", false") << ">(out[" << int(in.aux) << "], " << int(in.b)
                     << "u, (uint64_t)row[0] * N + col[0], " << reg[in.a] << ");\n";
             } else {
                 src << each << "if (live[e]) tc::store_as(out[" << int(in.aux) << "], " << int(in.b)
@@ -782,17 +782,29 @@ bool runs_allowed(uint64_t cols, const tc_encoded* code, uint32_t count, const t
 
 namespace {
 
+// The columns a thread of the run form takes: four when the program stores
+// f32 (each store one 16-byte piece, so a wave's store instruction writes
+// one contiguous kilobyte), else kEpilogueRun (16 bytes of a 16-bit type).
+// Eight f32 a thread stored as two pieces left each instruction half of
+// every line it touched, and the non-temporal halves reached HBM as 1.56
+// times the output's bytes.
+int run_elems(const tc_encoded* code, uint32_t count) {
+    for (uint32_t pc = 0; pc < count; pc++) {
+        if (code[pc].kind == 5 && code[pc].b == TC_F32) return 4;
+    }
+    return kEpilogueRun;
+}
+
 // A program over whole runs (`runs_allowed`): a kernel over the rows x cols
-// space in runs of kEpilogueRun consecutive columns of one row, a run a
+// space in runs of `run_elems` consecutive columns of one row, a run a
 // thread, consecutive threads on consecutive runs.  Each load of contiguous
-// columns moves 16-byte pieces (a row-invariant one, a bias, from the
+// columns moves the run's pieces (a row-invariant one, a bias, from the
 // cache), a load of one value a row loads it once a run, and each store is
-// 16-byte pieces, non-temporal when the program moves more than
-// kStreamBytes.  From the program's second appearance, like the other
-// compiled forms.
+// whole pieces, non-temporal when the program moves more than kStreamBytes.
+// From the program's second appearance, like the other compiled forms.
 std::string general_runs_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                                 uint64_t rows, uint64_t cols, std::vector<float>* constants) {
-    constexpr int E = kEpilogueRun;
+    const int E = run_elems(code, count);
     const uint64_t runs = rows * cols / E;
     std::vector<bool> marks(count, false);
     uint64_t bytes = 0;  // a run's, loads of contiguous columns and stores
@@ -805,8 +817,8 @@ std::string general_runs_source(const tc_encoded* code, uint32_t count, uint32_t
         }
     }
     const bool stream = runs * bytes > kStreamBytes;
-    const std::string body =
-        group_body(code, count, dtype, false, E, places, constants, false, -1, nullptr, &marks, nullptr, true, stream);
+    const std::string body = group_body(code, count, dtype, false, E, places, constants, false, -1, nullptr, &marks,
+                                        nullptr, E % 8 == 0, stream);
     if (constants->size() > static_cast<size_t>(kInlineCode)) return std::string();
     const std::string e = std::to_string(E);
     return "#include \"device.hpp\"\n"
@@ -835,7 +847,7 @@ std::string general_runs_source(const tc_encoded* code, uint32_t count, uint32_t
 bool run_general_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                       uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, hipStream_t s,
                       int* status) {
-    constexpr int E = kEpilogueRun;
+    const int E = run_elems(code, count);
     const uint64_t runs = rows * cols / E;
     std::vector<float> constants;
     const std::string source = general_runs_source(code, count, dtype, places, rows, cols, &constants);

@@ -137,8 +137,22 @@ def test_broadcast_programs_compile_in_the_form_their_operands_allow(tmp_path, d
     source = fused_source(dtype, code, places, rows, cols, [0x10000, 0x20000, 0x30000, 0x40000])
     assert f"void __launch_bounds__(256) {form}(" in source
     if form == "tc_fused_runs":
-        assert "tc::load_wide<8>(in[2]" in source and "tc::store_wide<8" in source
+        # The program stores an f32 output, so a thread takes four columns:
+        # each f32 store one 16-byte piece.
+        assert "tc::load_run<4>(in[2]" in source and "tc::store_run<4, false>(out[1], 0u" in source
     text = compile_kernel(tmp_path, form, source)
+    assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
+
+
+def test_a_program_storing_only_16_bit_outputs_runs_eight_columns_a_thread(tmp_path):
+    # Without an f32 store, a thread of the run form takes eight columns:
+    # 16-byte loads and stores of the 16-bit operands.
+    rows, cols = 4099, 1000
+    code, places = run_form_program(rows, 0)
+    places[2] = identity_place(rows, cols)
+    source = fused_source(lib.BF16, code[:-1], places, rows, cols, [0x10000, 0x20000, 0x30000, 0x40000])
+    assert "tc::load_wide<8>(in[0]" in source and "tc::store_wide<8, false>(out[0]" in source
+    text = compile_kernel(tmp_path, "runs_eight", source)
     assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
 
 
