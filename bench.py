@@ -79,14 +79,14 @@ MEASURED_TRAFFIC = {
     "vecmat, f32 [8192] . [8192x8192]": 2.71e+08,
     "dot, f32 64 Mi elements": 5.37e+08,
     "transpose, f32 [4096x4096]": 1.342e+08,
-    "layer norm f32 [8192x8192] (fused_with_statistics), statistics and program in one kernel": 5.379e+08,
-    "layer norm f32 [8192x8192] (fused_with_statistics), composed: row moments, then the program": 8.058e+08,
+    "layer norm f32 [8192x8192] (fused_with_statistics), statistics and program in one kernel": 5.368e+08,
+    "layer norm f32 [8192x8192] (fused_with_statistics), composed: row moments, then the program": 8.059e+08,
     "Adam update, 25175040 f32 parameters (fused program)": 7.043e+08,
-    "MLP training step 1024-4096-4096-1024, batch 4096, f32, tape + Adam (configs[4])": 8.091e+09,
-    "bf16 dense layer relu(x w + b) 8192x8192x8192, in the product's epilogue": 1.854e+09,
-    "bf16 dense layer relu(x w + b) 8192x8192x8192, unfused: product, then program": 2.094e+09,
+    "MLP training step 1024-4096-4096-1024, batch 4096, f32, tape + Adam (configs[4])": 8.402e+09,
+    "bf16 dense layer relu(x w + b) 8192x8192x8192, in the product's epilogue": 1.752e+09,
+    "bf16 dense layer relu(x w + b) 8192x8192x8192, unfused: product, then program": 2.318e+09,
     "f32 dense layer relu(x w + b) 4096x1024x4096, in the product's epilogue": 2.015e+08,
-    "f32 dense layer relu(x w + b) 4096x1024x4096, unfused: product, then program": 3.357e+08,
+    "f32 dense layer relu(x w + b) 4096x1024x4096, unfused: product, then program": 3.356e+08,
 }
 MFMA_PEAK = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}  # dense TFLOP/s
 KIND = {"bf16": lib.BF16, "f16": lib.F16, "f32": lib.F32}
