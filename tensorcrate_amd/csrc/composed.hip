@@ -317,6 +317,13 @@ int tc_matmul_epilogue(uint32_t dtype, const tc_encoded* code, uint32_t count, c
         }
     }
     if (m == 0 || n == 0) return TC_OK;
+    if (k != 0 && (a == nullptr || b == nullptr)) return fail(TC_INVALID, "fused matmul: a null operand");
+    for (uint32_t s = 0; s < input_count; s++) {
+        if (inputs[s] == nullptr && input_lens[s] != 0) return fail(TC_INVALID, "fused matmul: a null input");
+    }
+    for (uint32_t s = 0; s < output_count; s++) {
+        if (outputs[s] == nullptr && output_lens[s] != 0) return fail(TC_INVALID, "fused matmul: a null output");
+    }
     const uint64_t cells = m * n;
     {
         const void* all[TC_FUSED_MAX_INPUTS] = {};

@@ -762,6 +762,9 @@ extern "C" int tc_matmul_epilogue_source(uint32_t dtype, const tc_encoded* code,
 extern "C" int tc_matmul(uint32_t in_dtype, uint32_t out_dtype, uint32_t transposed, int accumulate, uint64_t m,
                          uint64_t k, uint64_t n, const void* a, const void* b, void* c) {
     if (transposed > TC_RIGHT) return fail(TC_INVALID, "matmul: no Transposed " + std::to_string(transposed));
+    if (m != 0 && n != 0 && (c == nullptr || (k != 0 && (a == nullptr || b == nullptr)))) {
+        return fail(TC_INVALID, "matmul: a null operand");
+    }
     const bool acc = accumulate != 0;
     if (in_dtype == TC_F32 && out_dtype == TC_F32) return matmul_typed<float, float>(transposed, acc, m, k, n, a, b, c);
     if (in_dtype == TC_BF16 && out_dtype == TC_BF16) return matmul_typed<bf16_t, bf16_t>(transposed, acc, m, k, n, a, b, c);

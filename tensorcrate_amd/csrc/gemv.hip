@@ -303,11 +303,17 @@ extern "C" {
 
 int tc_matvec(uint32_t dtype, int accumulate, uint64_t rows, uint64_t cols, const void* matrix, const void* vector,
               void* out) {
+    if (rows != 0 && (out == nullptr || (cols != 0 && (matrix == nullptr || vector == nullptr)))) {
+        return fail(TC_INVALID, "matvec: a null operand");
+    }
     TC_DISPATCH_FLOAT(dtype, "matvec", S, return matvec_typed<S>(accumulate != 0, rows, cols, matrix, vector, out));
     return TC_OK;
 }
 
 int tc_vecmat(uint32_t dtype, uint64_t rows, uint64_t cols, const void* vector, const void* matrix, void* out) {
+    if (cols != 0 && (out == nullptr || (rows != 0 && (matrix == nullptr || vector == nullptr)))) {
+        return fail(TC_INVALID, "vecmat: a null operand");
+    }
     TC_DISPATCH_FLOAT(dtype, "vecmat", S, return vecmat_typed<S>(false, rows, cols, vector, matrix, out));
     return TC_OK;
 }

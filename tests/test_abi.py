@@ -71,3 +71,16 @@ def test_errors_are_reported_not_raised_on_the_device():
     assert status == lib.INVALID
     assert loaded.tc_last_error().decode() == (
         "strided copy: shape [2, 3] with strides [3, 1] from offset 5 reaches past 10 elements")
+
+
+def test_null_operands_are_refused_before_any_device_work():
+    # A product or matrix-vector call with work to do and a null operand is
+    # refused on the host, before any device work (a kernel would read
+    # address 0).
+    loaded = lib.load()
+    assert loaded.tc_matmul(lib.F32, lib.F32, lib.PLAIN, 0, 4, 4, 4, None, None, None) == lib.INVALID
+    assert loaded.tc_last_error().decode() == "matmul: a null operand"
+    assert loaded.tc_matvec(lib.F32, 0, 8, 8, None, None, None) == lib.INVALID
+    assert loaded.tc_last_error().decode() == "matvec: a null operand"
+    assert loaded.tc_vecmat(lib.F32, 8, 8, None, None, None) == lib.INVALID
+    assert loaded.tc_last_error().decode() == "vecmat: a null operand"
