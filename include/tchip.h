@@ -13,7 +13,9 @@
  *    a message for the calling thread, worded like the reference's panic for
  *    the same mistake ("strided copy: shape [..] ... reaches past N
  *    elements").  Layout checks run on the host before any launch, so a bad
- *    layout never reaches the GPU.
+ *    layout never reaches the GPU.  A call with elements to read or write
+ *    refuses a null device pointer the same way (TC_INVALID, "<operation>: a
+ *    null operand"); an empty call may pass null.
  *  - All work is queued asynchronously on one HIP stream per host thread and
  *    ordered on it; `tc_sync` waits for it.  Host pointers passed to
  *    `tc_upload` / `tc_download` are done with when the call returns.

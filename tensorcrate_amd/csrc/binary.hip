@@ -494,6 +494,7 @@ using namespace tc;
 extern "C" {
 
 int tc_elementwise(uint32_t dtype, uint32_t op, const void* a, const void* b, void* out, uint64_t n) {
+    if (n != 0 && any_null({a, b, out})) return null_operand("elementwise");
     TC_DISPATCH_FLOAT(dtype, "elementwise", S,
                       return map_pair<S>(TC_PAIR_ARITHMETIC, op, a, b, out, n, "elementwise"));
     return TC_OK;
@@ -501,6 +502,7 @@ int tc_elementwise(uint32_t dtype, uint32_t op, const void* a, const void* b, vo
 
 int tc_broadcast(uint32_t dtype, uint32_t op, const void* a, float scalar, int scalar_left, void* out,
                  uint64_t n) {
+    if (n != 0 && any_null({a, out})) return null_operand("broadcast");
     TC_DISPATCH_FLOAT(dtype, "broadcast", S,
                       return map_scalar<S>(TC_PAIR_ARITHMETIC, op, a, scalar, scalar_left != 0, out, n,
                                            "broadcast"));
@@ -508,6 +510,7 @@ int tc_broadcast(uint32_t dtype, uint32_t op, const void* a, float scalar, int s
 }
 
 int tc_compare(uint32_t dtype, uint32_t op, const void* a, const void* b, void* out, uint64_t n) {
+    if (n != 0 && any_null({a, b, out})) return null_operand("compare");
     TC_DISPATCH_FLOAT(dtype, "compare", S,
                       return map_pair<S>(TC_PAIR_COMPARE, op, a, b, out, n, "compare"));
     return TC_OK;
@@ -515,6 +518,7 @@ int tc_compare(uint32_t dtype, uint32_t op, const void* a, const void* b, void* 
 
 int tc_compare_scalar(uint32_t dtype, uint32_t op, const void* a, float scalar, int scalar_left,
                       void* out, uint64_t n) {
+    if (n != 0 && any_null({a, out})) return null_operand("compare_scalar");
     TC_DISPATCH_FLOAT(dtype, "compare_scalar", S,
                       return map_scalar<S>(TC_PAIR_COMPARE, op, a, scalar, scalar_left != 0, out, n,
                                            "compare_scalar"));
@@ -523,6 +527,7 @@ int tc_compare_scalar(uint32_t dtype, uint32_t op, const void* a, float scalar, 
 
 int tc_unary(uint32_t dtype, uint32_t op, const void* a, void* out, uint64_t n) {
     if (op > 13) return fail(TC_INVALID, "no Analytic " + std::to_string(op));
+    if (n != 0 && any_null({a, out})) return null_operand("unary");
     TC_STREAM(s);
     TC_DISPATCH_FLOAT(dtype, "unary", S, return launch_map<S>(a, nullptr, out, n, UnaryOf<S>{op}, s, "unary"));
     return TC_OK;
@@ -531,16 +536,19 @@ int tc_unary(uint32_t dtype, uint32_t op, const void* a, void* out, uint64_t n) 
 int tc_unary_dual(uint32_t dtype, uint32_t op, const void* value, const void* tangent, void* out_value,
                   void* out_tangent, uint64_t n) {
     if (op > 13) return fail(TC_INVALID, "no Analytic " + std::to_string(op));
+    if (n != 0 && any_null({value, tangent, out_value, out_tangent})) return null_operand("unary_dual");
     TC_DISPATCH_FLOAT(dtype, "unary_dual", S, return launch_dual<S>(value, tangent, out_value, out_tangent, n, op));
     return TC_OK;
 }
 
 int tc_power(uint32_t dtype, const void* a, const void* b, void* out, uint64_t n) {
+    if (n != 0 && any_null({a, b, out})) return null_operand("power");
     TC_DISPATCH_FLOAT(dtype, "power", S, return map_pair<S>(TC_PAIR_POWER, 0, a, b, out, n, "power"));
     return TC_OK;
 }
 
 int tc_power_scalar(uint32_t dtype, const void* a, float scalar, int scalar_left, void* out, uint64_t n) {
+    if (n != 0 && any_null({a, out})) return null_operand("power");
     if (scalar_left) {
         TC_DISPATCH_FLOAT(dtype, "power", S,
                           return map_scalar<S>(TC_PAIR_POWER, 0, a, scalar, true, out, n, "power"));
@@ -557,6 +565,7 @@ int tc_clamp(uint32_t dtype, const void* a, float low, float high, void* out, ui
     // Only an ordered pair the wrong way round is refused: a NaN bound is
     // inert, since max(x, NaN) and min(x, NaN) are x (shape.rs:30-43).
     if (low > high) return fail(TC_INVALID, "clamp: the lower bound exceeds the upper one");
+    if (n != 0 && any_null({a, out})) return null_operand("clamp");
     TC_STREAM(s);
     TC_DISPATCH_FLOAT(dtype, "clamp", S, return launch_map<S>(a, nullptr, out, n, ClampTo{low, high}, s, "clamp"));
     return TC_OK;
@@ -571,6 +580,7 @@ int tc_strided_binary(uint32_t dtype, uint32_t kind, uint32_t op, uint32_t rank,
     status = check_strided(b_len, rank, shape, b_at->offset, b_at->strides, "strided binary", &count);
     if (status != TC_OK) return status;
     if (count == 0) return TC_OK;
+    if (any_null({a, b, out})) return null_operand("strided binary");
     uint64_t out_strides[kMaxRank] = {};
     uint64_t step = 1;
     for (int k = static_cast<int>(rank) - 1; k >= 0; k--) {

@@ -45,6 +45,24 @@ void count_dispatch();
 // Wait for the stream or an event on the host, counted as a host wait.
 hipError_t host_wait(hipStream_t s);
 hipError_t host_wait(hipEvent_t e);
+// A call with work to do refuses a null device pointer on the host, before
+// any device work: a kernel would read or write address 0.  `null_operand`
+// records the refusal under `what`; `null_slot` is true when a slot of an
+// input or output array has elements but no storage.
+inline bool any_null(std::initializer_list<const void*> pointers) {
+    for (const void* p : pointers) {
+        if (p == nullptr) return true;
+    }
+    return false;
+}
+inline int null_operand(const char* what) { return fail(TC_INVALID, std::string(what) + ": a null operand"); }
+inline bool null_slot(const void* const* pointers, const uint64_t* lens, uint32_t count) {
+    for (uint32_t k = 0; k < count; k++) {
+        if (lens[k] != 0 && pointers[k] == nullptr) return true;
+    }
+    return false;
+}
+
 // Shorthand: set up the thread's stream or return its failure.
 #define TC_STREAM(var)                                \
     hipStream_t var = ::tc::stream();                 \

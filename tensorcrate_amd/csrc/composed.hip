@@ -108,6 +108,9 @@ int tc_row_moments(uint32_t dtype, uint32_t input_dtype, const void* input, uint
     }
     if (place->lead > TC_FUSED_LEAD) return fail(TC_INVALID, "row_moments: a place folds more than 5 axes");
     if (rows == 0) return TC_OK;
+    if (any_null({means, deviations}) || (cols != 0 && input_len != 0 && input == nullptr)) {
+        return null_operand("row_moments");
+    }
     if (cols == 0) {  // moments of nothing (statistics/mod.rs:428-434)
         int status = fill_nan(dtype, means, rows);
         return status == TC_OK ? fill_nan(dtype, deviations, rows) : status;
@@ -157,6 +160,10 @@ int tc_fused_with_statistics(uint32_t dtype, const tc_encoded* code, uint32_t co
         if (st.which > TC_STAT_DEVIATIONS || !is_float(st.source_dtype) || st.place.lead > TC_FUSED_LEAD) {
             return fail(TC_INVALID, "fused with statistics: statistic " + std::to_string(i) + " is malformed");
         }
+        if (st.source == nullptr && st.source_len != 0) return null_operand("fused with statistics");
+    }
+    if (null_slot(inputs, input_lens, input_count) || null_slot(outputs, output_lens, output_count)) {
+        return null_operand("fused with statistics");
     }
     const void* all[TC_FUSED_MAX_INPUTS] = {};
     uint64_t all_lens[TC_FUSED_MAX_INPUTS] = {};
@@ -250,6 +257,7 @@ int tc_fused_sum(uint32_t dtype, const tc_encoded* code, uint32_t count, const t
     const uint64_t results = axis == TC_AXIS_ROWS ? rows : cols;
     const uint64_t depth = axis == TC_AXIS_ROWS ? cols : rows;
     if (results == 0) return TC_OK;
+    if (out == nullptr || null_slot(inputs, input_lens, input_count)) return null_operand("fused sum");
     if (depth == 0) {  // sums of nothing
         const uint32_t zero = 0;
         return tc_fill(out, results, static_cast<uint32_t>(dtype_size(dtype)), &zero);

@@ -507,6 +507,7 @@ int tc_strided_copy(uint32_t width, const void* src, uint64_t src_len, uint32_t 
     uint64_t count = 0;
     int status = check_strided(src_len, rank, shape, from->offset, from->strides, "strided copy", &count);
     if (status != TC_OK) return status;
+    if (count != 0 && any_null({src, dst})) return null_operand("strided copy");
     // The target is the row-major layout of `shape`.
     tc_strided to{};
     uint64_t step = 1;
@@ -533,6 +534,7 @@ int tc_assemble(uint32_t width, void* dst, uint64_t len, const tc_region* region
         status = check_strided(len, region.rank, region.shape, region.to.offset, region.to.strides,
                                "assemble", &elements);
         if (status != TC_OK) return status;
+        if (elements != 0 && any_null({region.source, dst})) return null_operand("assemble");
         traffic += 2 * elements * width;
     }
     for (uint32_t r = 0; r < count; r++) {

@@ -1219,6 +1219,9 @@ extern "C" int tc_fused(uint32_t dtype, const tc_encoded* code, uint32_t count, 
     int status = check_fused(dtype, code, count, places, place_count, input_lens, input_count, output_lens,
                              output_count, rows, cols);
     if (status != TC_OK) return status;
+    if (null_slot(inputs, input_lens, input_count) || null_slot(outputs, output_lens, output_count)) {
+        return null_operand("fused program");
+    }
     TC_STREAM(s);
     if (rows == 0 || cols == 0 || count == 0) return TC_OK;
     Buffers buffers{};

@@ -1066,10 +1066,27 @@ int reduce_moments(uint32_t dtype, const void* input, uint64_t input_len, const 
 
 using namespace tc;
 
+namespace tc {
+namespace {
+
+// How many results a split keeps (the product of its kept extents; one for
+// a full reduction).
+uint64_t split_results(const tc_split* split) {
+    uint64_t results = 1;
+    for (uint32_t k = 0; k < split->kept_rank && k < static_cast<uint32_t>(kMaxRank); k++) results *= split->kept[k];
+    return results;
+}
+
+}  // namespace
+}  // namespace tc
+
 extern "C" {
 
 int tc_reduce_axes(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split,
                    uint32_t kind, uint32_t op, uint64_t divisor, void* out) {
+    if ((input_len != 0 && input == nullptr) || (split_results(split) != 0 && out == nullptr)) {
+        return null_operand("reduce_axes");
+    }
     TC_DISPATCH_FLOAT(dtype, "reduce_axes", S,
                       return reduce_axes_typed<S>(input, input_len, split, kind, op, divisor, out));
     return TC_OK;
@@ -1077,11 +1094,15 @@ int tc_reduce_axes(uint32_t dtype, const void* input, uint64_t input_len, const 
 
 int tc_arg_reduce(uint32_t dtype, const void* input, uint64_t input_len, const tc_split* split,
                   uint32_t op, uint32_t* out) {
+    if ((input_len != 0 && input == nullptr) || (split_results(split) != 0 && out == nullptr)) {
+        return null_operand("arg_reduce");
+    }
     TC_DISPATCH_FLOAT(dtype, "arg_reduce", S, return arg_reduce_typed<S>(input, input_len, split, op, out));
     return TC_OK;
 }
 
 int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result) {
+    if (result == nullptr || (n != 0 && a == nullptr)) return null_operand("vector_reduce");
     switch (op) {
         case TC_REDUCE_SUM:
             TC_DISPATCH_FLOAT(dtype, "vector_reduce", S,
@@ -1102,11 +1123,13 @@ int tc_vector_reduce(uint32_t dtype, const void* a, uint64_t n, uint32_t op, flo
 }
 
 int tc_moments(uint32_t dtype, const void* a, uint64_t n, float* result) {
+    if (result == nullptr || (n != 0 && a == nullptr)) return null_operand("moments");
     TC_DISPATCH_FLOAT(dtype, "moments", S, return total_moments<S>(a, n, result));
     return TC_OK;
 }
 
 int tc_vector_reduce_noalloc(uint32_t dtype, const void* a, uint64_t n, uint32_t op, float* result) {
+    if (result == nullptr || (n != 0 && a == nullptr)) return null_operand("vector_reduce_noalloc");
     switch (op) {
         case TC_REDUCE_SUM:
             TC_DISPATCH_FLOAT(dtype, "vector_reduce_noalloc", S, return total_noalloc<S, TC_REDUCE_SUM>(a, n, result));
@@ -1123,6 +1146,7 @@ int tc_vector_reduce_noalloc(uint32_t dtype, const void* a, uint64_t n, uint32_t
 }
 
 int tc_dot(uint32_t dtype, const void* a, const void* b, uint64_t n, float* result) {
+    if (result == nullptr || (n != 0 && any_null({a, b}))) return null_operand("dot");
     TC_DISPATCH_FLOAT(dtype, "dot", S, return total<S, TC_REDUCE_SUM, true>(a, b, n, result, "dot"));
     return TC_OK;
 }

@@ -84,3 +84,22 @@ def test_null_operands_are_refused_before_any_device_work():
     assert loaded.tc_last_error().decode() == "matvec: a null operand"
     assert loaded.tc_vecmat(lib.F32, 8, 8, None, None, None) == lib.INVALID
     assert loaded.tc_last_error().decode() == "vecmat: a null operand"
+    # The same refusal across the other compute entry points that read or
+    # write device memory.
+    assert loaded.tc_elementwise(lib.F32, lib.ADD, None, None, None, 16) == lib.INVALID
+    assert loaded.tc_last_error().decode() == "elementwise: a null operand"
+    assert loaded.tc_unary(lib.F32, 0, None, None, 16) == lib.INVALID
+    result = ctypes.c_float()
+    assert loaded.tc_dot(lib.F32, None, None, 16, ctypes.byref(result)) == lib.INVALID
+    assert loaded.tc_vector_reduce(lib.F32, None, 16, 0, ctypes.byref(result)) == lib.INVALID
+    shape = lib.dims([2, 3])
+    at = lib.strided(0, [3, 1])
+    assert loaded.tc_strided_copy(4, None, 6, 2, shape, ctypes.byref(at), None) == lib.INVALID
+    assert loaded.tc_last_error().decode() == "strided copy: a null operand"
+    code = [(0, 0, 0, 0, lib.F32, 0, 0.0), (5, 0, 0, 0, lib.F32, 0, 0.0)]
+    enc, places = lib._program(code, [(0, 1, 1, [2], [3])])
+    ins = (ctypes.c_void_p * 1)(None)
+    outs = (ctypes.c_void_p * 1)(None)
+    lens = (ctypes.c_uint64 * 1)(6)
+    assert loaded.tc_fused(lib.F32, enc, 2, places, 1, ins, lens, 1, outs, lens, 1, 2, 3) == lib.INVALID
+    assert loaded.tc_last_error().decode() == "fused program: a null operand"
