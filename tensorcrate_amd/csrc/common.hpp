@@ -147,6 +147,12 @@ bool runtime_compiler_is_ours();
 int fused_row_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
                    uint32_t place_count, const void* const* inputs, const uint64_t* input_lens, uint32_t input_count,
                    uint64_t rows, uint64_t cols, void* out, bool* done);
+// The same along columns: the output summed per column, the rows split
+// over workgroups when there are few columns, the splits' sums added by a
+// second kernel in split order.
+int fused_column_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                      uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                      uint32_t input_count, uint64_t rows, uint64_t cols, void* out, bool* done);
 
 // `fused_with_statistics` as one compiled kernel (fused.hip), for a checked
 // program: each row's statistics computed in registers and the program run

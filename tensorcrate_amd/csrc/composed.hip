@@ -262,10 +262,13 @@ int tc_fused_sum(uint32_t dtype, const tc_encoded* code, uint32_t count, const t
         const uint32_t zero = 0;
         return tc_fill(out, results, static_cast<uint32_t>(dtype_size(dtype)), &zero);
     }
-    if (axis == TC_AXIS_ROWS) {
+    {
         bool done = false;
-        int status = fused_row_sums(dtype, code, count, places, place_count, inputs, input_lens, input_count, rows,
-                                    cols, out, &done);
+        int status = axis == TC_AXIS_ROWS
+                         ? fused_row_sums(dtype, code, count, places, place_count, inputs, input_lens, input_count,
+                                          rows, cols, out, &done)
+                         : fused_column_sums(dtype, code, count, places, place_count, inputs, input_lens,
+                                             input_count, rows, cols, out, &done);
         if (status != TC_OK || done) return status;
     }
     const uint64_t n = rows * cols;

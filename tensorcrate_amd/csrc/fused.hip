@@ -613,7 +613,7 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
                        const tc_place* places, std::vector<float>* constants, bool sum_store = false,
                        int stat_first = -1, const std::vector<bool>* held = nullptr,
                        const std::vector<bool>* runs = nullptr, const std::vector<bool>* invariant = nullptr,
-                       bool wide = false, bool stream = false) {
+                       bool wide = false, bool stream = false, bool sum_each = false) {
     static const char* const kBinary[] = {"+", "-", "*", "/"};
     const std::string round_run = "    tc_round_run<" + std::to_string(dtype) + ">(";
     std::ostringstream src;
@@ -634,7 +634,9 @@ std::string group_body(const tc_encoded* code, uint32_t count, uint32_t dtype, b
     for (uint32_t pc = 0; pc < count; pc++) {
         const tc_encoded& in = code[pc];
         if (in.kind == 5) {
-            if (sum_store) {  // the one output, already in its type, summed in f32 in element order
+            if (sum_store && sum_each) {  // each element's own running sum, in f32
+                src << each << "sum[e] += live[e] ? " << at(in.a) << " : 0.0f;\n";
+            } else if (sum_store) {  // the one output, already in its type, summed in f32 in element order
                 src << each << "sum += live[e] ? " << at(in.a) << " : 0.0f;\n";
             } else if (runs != nullptr && (*runs)[pc] && !reg[in.a].empty()) {
                 src << "    if (live[0]) tc::" << (wide ? "store_wide<" : "store_run<") << elems
@@ -1031,6 +1033,144 @@ bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtyp
     return true;
 }
 
+// A program's one output summed along its columns (`fused_sum` over
+// `Axis::Columns`, kernels.rs:1120-1135) from the program's second
+// appearance, the output never stored: a workgroup takes 256 columns, four
+// consecutive ones a lane (the program's contiguous loads one 16-byte run of
+// f32, 8 bytes of a 16-bit type), over a split of the rows, its four waves
+// consecutive quarters of the split, each lane summing its columns in f32 in
+// row order, eight rows' programs at a time; the waves' sums are added in
+// order, and the splits' (when the rows are split to fill the GPU) by a
+// second kernel in split order.  Taken when the program's operands allow
+// the run form (`runs_allowed`).
+bool run_compiled_column_sums(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
+                              uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, void* out,
+                              hipStream_t s, int* status) {
+    constexpr int E = 4;
+    if (place_count > static_cast<uint32_t>(kInlinePlaces) || rows * cols > (uint64_t{1} << 31)) return false;
+    if (!runs_allowed(cols, code, count, places, buffers.inputs, nullptr, 0, false)) return false;
+    std::vector<bool> runs(count, false);
+    for (uint32_t pc = 0; pc < count; pc++) {
+        runs[pc] = code[pc].kind == 0 && places[code[pc].op].col_step == 1;
+    }
+    std::vector<float> constants;
+    const std::string body = group_body(code, count, dtype, false, E, places, &constants, true, -1, nullptr, &runs,
+                                        nullptr, false, false, true);
+    if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
+    const std::string T = std::to_string(dtype);
+    const std::string source =
+        "#include \"device.hpp\"\n"
+        "struct Program {\n" + std::string(compiled_members()) +
+        "  __device__ __forceinline__ void group(const bool (&live)[4], const uint32_t (&row)[4],\n"
+        "      const uint32_t (&col)[4], uint32_t N, float (&sum)[4]) const {\n" + body + "  }\n};\n"
+        "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_column_sums(Program p, uint32_t rows,\n"
+        "    uint32_t cols, uint32_t tiles, uint32_t per_split, uint32_t splits, void* sums, float* partial) {\n"
+        "  __shared__ float quarter[4][256];\n"
+        "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
+        "  const uint32_t tile = blockIdx.x % tiles, split = blockIdx.x / tiles;\n"
+        "  const uint32_t c = (tile * 64u + lane) * 4u;\n"
+        "  const bool alive = c < cols;\n"
+        "  const uint32_t begin = split * per_split;\n"
+        "  const uint32_t end = min(begin + per_split, rows);\n"
+        "  const uint32_t per_wave = (end - begin + 3u) / 4u;\n"
+        "  const uint32_t first = min(begin + wave * per_wave, end), last = min(first + per_wave, end);\n"
+        "  float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};\n"
+        "  auto one = [&](uint32_t r) {\n"
+        "    bool live[4];\n"
+        "    uint32_t row[4], col[4];\n"
+        "    for (int e = 0; e < 4; e++) live[e] = alive, row[e] = r, col[e] = c + e;\n"
+        "    p.group(live, row, col, cols, sum);\n"
+        "  };\n"
+        "  uint32_t r = first;\n"
+        "  for (; r + 8u <= last; r += 8u) {\n"
+        "#pragma unroll\n"
+        "    for (int u = 0; u < 8; u++) one(r + u);\n"
+        "  }\n"
+        "  for (; r < last; r++) one(r);\n"
+        "  for (int e = 0; e < 4; e++) quarter[wave][lane * 4u + e] = sum[e];\n"
+        "  __syncthreads();\n"
+        "  if (wave == 0 && alive) {\n"
+        "    for (int e = 0; e < 4; e++) {\n"
+        "      const uint32_t at = lane * 4u + e;\n"
+        "      const float total = ((quarter[0][at] + quarter[1][at]) + quarter[2][at]) + quarter[3][at];\n"
+        "      if (splits == 1u) tc::store_as(sums, " + T + "u, c + e, total);\n"
+        "      else partial[(uint64_t)split * cols + c + e] = total;\n"
+        "    }\n"
+        "  }\n"
+        "}\n"
+        "// The splits' sums of 64 columns a workgroup: lane = column, each wave\n"
+        "// adding a quarter of the splits in order (eight loads in flight), then\n"
+        "// the quarters in order.\n"
+        "extern \"C\" __global__ void __launch_bounds__(256) tc_fused_column_sums_combine(uint32_t cols,\n"
+        "    uint32_t splits, const float* partial, void* sums) {\n"
+        "  __shared__ float quarter[4][64];\n"
+        "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
+        "  const uint32_t c = blockIdx.x * 64u + lane;\n"
+        "  const uint32_t per_wave = (splits + 3u) / 4u;\n"
+        "  const uint32_t k0 = min(wave * per_wave, splits), k1 = min(k0 + per_wave, splits);\n"
+        "  float total = 0.0f;\n"
+        "  if (c < cols) {\n"
+        "    uint32_t k = k0;\n"
+        "    for (; k + 8u <= k1; k += 8u) {\n"
+        "      float x[8];\n"
+        "      for (int u = 0; u < 8; u++) x[u] = partial[(uint64_t)(k + u) * cols + c];\n"
+        "      for (int u = 0; u < 8; u++) total += x[u];\n"
+        "    }\n"
+        "    for (; k < k1; k++) total += partial[(uint64_t)k * cols + c];\n"
+        "  }\n"
+        "  quarter[wave][lane] = total;\n"
+        "  __syncthreads();\n"
+        "  if (wave == 0 && c < cols) {\n"
+        "    tc::store_as(sums, " + T + "u, c, ((quarter[0][lane] + quarter[1][lane]) + quarter[2][lane]) + quarter[3][lane]);\n"
+        "  }\n"
+        "}\n";
+    hipFunction_t functions[2] = {};
+    if (!cached_kernels(source, {"tc_fused_column_sums", "tc_fused_column_sums_combine"}, functions)) return false;
+    CompiledArgsOf args{};
+    for (int k = 0; k < TC_FUSED_MAX_INPUTS; k++) args.in[k] = buffers.inputs[k];
+    int place_status = to_device_places(places, place_count, args.places);
+    if (place_status != TC_OK) {
+        *status = place_status;
+        return true;
+    }
+    for (size_t c = 0; c < constants.size(); c++) args.constants[c] = constants[c];
+    // The rows split until there are four workgroups a CU, each wave keeping
+    // at least sixteen rows.
+    const uint64_t tiles = (cols + 255) / 256;
+    const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
+    uint64_t splits = 1;
+    if (tiles < want) {
+        splits = (want + tiles - 1) / tiles;
+        const uint64_t most = rows / (4 * 16);
+        if (splits > most) splits = most;
+        if (splits < 1) splits = 1;
+    }
+    const uint64_t per_split = (rows + splits - 1) / splits;
+    splits = (rows + per_split - 1) / per_split;
+    void* partial = nullptr;
+    if (splits > 1) {
+        *status = tc_alloc(splits * cols * sizeof(float), &partial);
+        if (*status != TC_OK) return true;
+    }
+    uint32_t rows32 = static_cast<uint32_t>(rows), cols32 = static_cast<uint32_t>(cols),
+             tiles32 = static_cast<uint32_t>(tiles), per32 = static_cast<uint32_t>(per_split),
+             splits32 = static_cast<uint32_t>(splits);
+    void* params[] = {&args, &rows32, &cols32, &tiles32, &per32, &splits32, &out, &partial};
+    count_dispatch();
+    hipError_t error = hipModuleLaunchKernel(functions[0], static_cast<uint32_t>(tiles * splits), 1, 1, 256, 1, 1, 0,
+                                             s, params, nullptr);
+    if (error == hipSuccess && splits > 1) {
+        void* finish[] = {&cols32, &splits32, &partial, &out};
+        count_dispatch();
+        error = hipModuleLaunchKernel(functions[1], static_cast<uint32_t>((cols + 63) / 64), 1, 1, 256, 1, 1, 0, s,
+                                      finish, nullptr);
+    }
+    // Stream order keeps the partial sums alive until both kernels have run.
+    if (partial != nullptr) tc_free(partial);
+    *status = error == hipSuccess ? TC_OK : fail(TC_DEVICE, std::string("fused sum: ") + hipGetErrorString(error));
+    return true;
+}
+
 // Host-side validation of what the kernel would otherwise trust.
 int check_program(const tc_encoded* code, uint32_t count, uint32_t place_count, uint32_t input_count,
                   uint32_t output_count) {
@@ -1159,6 +1299,20 @@ int fused_row_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const
     Buffers buffers{};
     for (uint32_t k = 0; k < input_count; k++) buffers.inputs[k] = inputs[k];
     *done = run_compiled_row_sums(code, count, dtype, places, place_count, buffers, rows, cols, out, s, &status);
+    return status;
+}
+
+int fused_column_sums(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* places,
+                      uint32_t place_count, const void* const* inputs, const uint64_t* input_lens,
+                      uint32_t input_count, uint64_t rows, uint64_t cols, void* out, bool* done) {
+    *done = false;
+    const uint64_t lens[1] = {rows * cols};
+    int status = check_fused(dtype, code, count, places, place_count, input_lens, input_count, lens, 1, rows, cols);
+    if (status != TC_OK) return status;
+    TC_STREAM(s);
+    Buffers buffers{};
+    for (uint32_t k = 0; k < input_count; k++) buffers.inputs[k] = inputs[k];
+    *done = run_compiled_column_sums(code, count, dtype, places, place_count, buffers, rows, cols, out, s, &status);
     return status;
 }
 

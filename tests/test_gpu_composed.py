@@ -188,6 +188,46 @@ def test_row_sums_of_a_repeated_program_run_as_one_compiled_kernel(dtype):
     assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
 
 
+@pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
+@pytest.mark.parametrize("rows,cols", [(300, 5000), (5000, 64), (33, 70), (7, 100000)],
+                         ids=["wide", "tall-split-rows", "ragged", "few-rows"])
+def test_column_sums_of_a_repeated_program_run_compiled(dtype, rows, cols):
+    # From the program's second appearance its column sums are computed
+    # without storing the output: a kernel over 64-column tiles, the rows
+    # split over workgroups when the columns are few (5000 x 64), the splits'
+    # sums added by a second kernel; every run agrees with the oracle to the
+    # summation bound.
+    import ctypes
+
+    code = Code()
+    x = code.load(0, 0, dtype)
+    y = code.binary(lib.ADD, code.binary(lib.MUL, code.unary(EXP, x), code.const(0.5)), code.const(0.25))
+    # A product by 1 per case (exact in every type), so each case's program
+    # is its own source and compiles on its own second appearance.
+    for _ in range([(300, 5000), (5000, 64), (33, 70), (7, 100000)].index((rows, cols))):
+        y = code.binary(lib.MUL, y, code.const(1.0))
+    code.store(y, dtype, 0)
+    rng = np.random.default_rng(dtype + rows)
+    values = to_kind(rng.uniform(-1, 1, rows * cols).astype(np.float32), dtype)
+    want = widen(dtype, oracle.fused_sum(dtype, code.code, [identity_place(rows, cols)], [values], rows, cols, 1))
+    exact = (np.exp(widen(dtype, values).astype(np.float64)) * 0.5 + 0.25).reshape(rows, cols).sum(0)
+    unit = 2.0 ** -24 if dtype == lib.F32 else 2.0 ** -8
+    counts = []
+    for _ in range(3):
+        got = widen(dtype, device_fused_sum(dtype, code.code, [identity_place(rows, cols)], [values], rows, cols, 1))
+        # Per element: three operations rounded to the type (and exp's own
+        # error); per sum: at most `rows` additions in f32, then the result
+        # rounded to the type.  The oracle sums in its own order, within
+        # rows 2^-24 of the exact sum.
+        bound = (4 * unit + 2 * (rows + 8) * 2.0 ** -24) * exact + unit * exact
+        assert np.all(np.abs(got - exact) <= bound)
+        assert np.all(np.abs(got - want) <= bound + (4 * unit + rows * 2.0 ** -24) * exact)
+        count = ctypes.c_uint64()
+        lib.call("tc_fused_compiled", ctypes.byref(count))
+        counts.append(count.value)
+    assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
+
+
 @pytest.mark.parametrize("shape", [(300, 777), (40, 8300), (301, 1024), (64, 8192), (33, 4100), (41, 3000),
                                    (8, 33000)])
 @pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
