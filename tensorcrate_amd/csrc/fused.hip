@@ -985,10 +985,43 @@ bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtyp
                            uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, void* out,
                            hipStream_t s, int* status) {
     if (place_count > static_cast<uint32_t>(kInlinePlaces) || rows * cols > (uint64_t{1} << 31)) return false;
+    // Where the operands allow the run form, a lane takes four consecutive
+    // columns at a time (the program's contiguous loads one 16-byte run of
+    // f32), four runs 256 columns apart in flight; otherwise 16 elements 64
+    // apart.  Either way each lane adds its elements in the order it takes
+    // them, cols / 64 of them.
+    const bool runs = runs_allowed(cols, code, count, places, buffers.inputs, nullptr, 0, false);
+    std::vector<bool> marks(count, false);
+    for (uint32_t pc = 0; runs && pc < count; pc++) {
+        marks[pc] = code[pc].kind == 0 && places[code[pc].op].col_step == 1;
+    }
+    const int elems = runs ? 4 : kGeneralElems;
     std::vector<float> constants;
-    const std::string body = group_body(code, count, dtype, false, kGeneralElems, places, &constants, true);
+    const std::string body =
+        group_body(code, count, dtype, false, elems, places, &constants, true, -1, nullptr, runs ? &marks : nullptr);
     if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
-    const std::string E = std::to_string(kGeneralElems);
+    const std::string E = std::to_string(elems);
+    const std::string walk =
+        runs ? "    for (uint32_t c0 = 0; c0 < cols; c0 += 1024u) {\n"
+               "#pragma unroll\n"
+               "      for (uint32_t u = 0; u < 4u; u++) {\n"
+               "        uint32_t row[4], col[4];\n"
+               "        bool live[4];\n"
+               "        const uint32_t c = c0 + u * 256u + lane * 4u;\n"
+               "        for (int v = 0; v < 4; v++) col[v] = c + v, row[v] = r, live[v] = c < cols;\n"
+               "        p.group(live, row, col, cols, sum);\n"
+               "      }\n"
+               "    }\n"
+             : "    for (uint32_t c0 = 0; c0 < cols; c0 += 64u * " + E + ") {\n"
+               "      uint32_t row[" + E + "], col[" + E + "];\n"
+               "      bool live[" + E + "];\n"
+               "      for (int v = 0; v < " + E + "; v++) {\n"
+               "        col[v] = c0 + v * 64u + lane;\n"
+               "        row[v] = r;\n"
+               "        live[v] = col[v] < cols;\n"
+               "      }\n"
+               "      p.group(live, row, col, cols, sum);\n"
+               "    }\n";
     const std::string source =
         "#include \"device.hpp\"\n"
         "struct Program {\n" + std::string(compiled_members()) +
@@ -998,17 +1031,7 @@ bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtyp
         "    uint32_t cols, void* sums) {\n"
         "  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;\n"
         "  for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {\n"
-        "    float sum = 0.0f;\n"
-        "    for (uint32_t c0 = 0; c0 < cols; c0 += 64u * " + E + ") {\n"
-        "      uint32_t row[" + E + "], col[" + E + "];\n"
-        "      bool live[" + E + "];\n"
-        "      for (int v = 0; v < " + E + "; v++) {\n"
-        "        col[v] = c0 + v * 64u + lane;\n"
-        "        row[v] = r;\n"
-        "        live[v] = col[v] < cols;\n"
-        "      }\n"
-        "      p.group(live, row, col, cols, sum);\n"
-        "    }\n"
+        "    float sum = 0.0f;\n" + walk +
         "    for (int offset = 32; offset > 0; offset >>= 1) sum += __shfl_xor(sum, offset);\n"
         "    if (lane == 0) tc::store_as(sums, " + std::to_string(dtype) + "u, r, sum);\n"
         "  }\n"
