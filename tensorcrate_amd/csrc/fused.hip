@@ -978,9 +978,9 @@ bool launch_general(hipFunction_t function, const std::vector<float>& constants,
 
 // A program's one output summed along its rows (`fused_sum` over
 // `Axis::Rows`, kernels.rs:1120-1135) in one kernel, from the program's second
-// appearance: a wave a row, 16 elements a lane 64 apart, each lane summing in
-// element order and the wave in a fixed shuffle tree, so the output itself is
-// never stored.
+// appearance: a wave a row, each lane summing its elements in the order it
+// takes them (runs of four columns, or 16 elements 64 apart) and the wave in
+// a fixed shuffle tree, so the output itself is never stored.
 bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                            uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, void* out,
                            hipStream_t s, int* status) {
@@ -1787,7 +1787,9 @@ bool held_row_source(const tc_encoded* code, uint32_t count, uint32_t dtype, con
 }  // namespace tc
 
 // `fused_with_statistics` (kernels.rs:1103-1113) as one compiled kernel, from
-// the program's second appearance: a wave a row.  For each distinct source
+// the program's second appearance.  The held form (`held_row_source`) keeps
+// each row in registers; the general form here runs a wave a row.  For each
+// distinct source
 // one pass over the row (through the source's place, rounded to the
 // program's type) takes each lane's batches of 16 elements, their mean and
 // squared deviations from it, and merges them into the lane's running
