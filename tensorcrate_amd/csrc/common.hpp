@@ -120,14 +120,16 @@ std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtyp
 // place steps through its columns other than by 0 or 1, or folds rows.
 std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                           std::vector<float>* constants);
-// Whether a program over `cols` columns may run in runs of kEpilogueRun
-// columns with 16-byte pieces: `cols` a multiple of the run, every output
-// and every load of contiguous columns starting on 16 bytes, every load's
-// rows stepping by whole pieces, and no place stepping through its columns
-// other than by 0 or 1 or folding more than one row axis.  With
+// Whether a program over `cols` columns may run in runs of `width` columns
+// moved in 16-byte pieces, or as one piece when the run is shorter (four
+// 16-bit elements: 8 bytes): `cols` a multiple of the run, every output
+// it stores and every load of contiguous columns starting on a piece, every
+// load's rows stepping by whole pieces, and no place stepping through its
+// columns other than by 0 or 1 or folding more than one row axis.  With
 // `product_input`, input 0 is a product kernel's own result and not checked.
 bool runs_allowed(uint64_t cols, const tc_encoded* code, uint32_t count, const tc_place* places,
-                  const void* const* inputs, void* const* outputs, uint32_t output_count, bool product_input);
+                  const void* const* inputs, void* const* outputs, uint32_t output_count, bool product_input,
+                  int width = kEpilogueRun);
 // What the compiler's resource report says of a compiled kernel: scratch
 // bytes a lane and architectural VGPRs (UINT32_MAX where it said nothing).
 struct KernelResources {

@@ -763,38 +763,50 @@ bool run_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype, const 
 }  // namespace
 
 bool runs_allowed(uint64_t cols, const tc_encoded* code, uint32_t count, const tc_place* places,
-                  const void* const* inputs, void* const* outputs, uint32_t output_count, bool product_input) {
-    auto aligned = [](uintptr_t at) { return at % 16 == 0; };
-    if (cols % kEpilogueRun != 0) return false;
-    for (uint32_t slot = 0; slot < output_count; slot++) {
-        if (!aligned(reinterpret_cast<uintptr_t>(outputs[slot]))) return false;
-    }
+                  const void* const* inputs, void* const* outputs, uint32_t output_count, bool product_input,
+                  int width) {
+    // A piece is 16 bytes of the run, or the whole run when that is shorter,
+    // and it starts on its own size.
+    auto piece = [&](uint32_t element_dtype) -> uint64_t {
+        const uint64_t size = element_dtype == TC_F32 ? 4 : 2;
+        return width * size < 16 ? width * size : 16;
+    };
+    if (width <= 0 || cols % static_cast<uint64_t>(width) != 0) return false;
     for (uint32_t pc = 0; pc < count; pc++) {
         const tc_encoded& in = code[pc];
+        if (in.kind == 5) {
+            if (in.aux < output_count && reinterpret_cast<uintptr_t>(outputs[in.aux]) % piece(in.b) != 0) return false;
+            continue;
+        }
         if (in.kind != 0 || (product_input && in.a == 0)) continue;
         const tc_place& place = places[in.op];
         if (place.lead > 1 || (place.col_step != 0 && place.col_step != 1)) return false;
         if (place.col_step != 1) continue;
-        const uint64_t size = in.b == TC_F32 ? 4 : 2;
-        if (!aligned(reinterpret_cast<uintptr_t>(inputs[in.a]) + place.offset * size)) return false;
-        if (place.lead == 1 && (place.steps[0] * size) % 16 != 0) return false;
+        const uint64_t size = in.b == TC_F32 ? 4 : 2, align = piece(in.b);
+        if ((reinterpret_cast<uintptr_t>(inputs[in.a]) + place.offset * size) % align != 0) return false;
+        if (place.lead == 1 && (place.steps[0] * size) % align != 0) return false;
     }
     return true;
 }
 
 namespace {
 
-// The columns a thread of the run form takes: four when the program stores
-// f32 (each store one 16-byte piece, so a wave's store instruction writes
-// one contiguous kilobyte), else kEpilogueRun (16 bytes of a 16-bit type).
-// Eight f32 a thread stored as two pieces left each instruction half of
-// every line it touched, and the non-temporal halves reached HBM as 1.56
-// times the output's bytes.
-int run_elems(const tc_encoded* code, uint32_t count) {
-    for (uint32_t pc = 0; pc < count; pc++) {
-        if (code[pc].kind == 5 && code[pc].b == TC_F32) return 4;
+// The columns a thread of the run form takes (`runs_allowed` at that
+// width), or 0 for the element form: eight (16 bytes of a 16-bit type)
+// unless the program stores f32 or its operands allow only runs of four,
+// then four (each f32 store one 16-byte piece, so a wave's store
+// instruction writes one contiguous kilobyte; 8-byte pieces of the 16-bit
+// types).  Eight f32 a thread stored as two pieces left each instruction
+// half of every line it touched, and the non-temporal halves reached HBM as
+// 1.56 times the output's bytes.
+int run_width(const tc_encoded* code, uint32_t count, const tc_place* places, const void* const* inputs,
+              void* const* outputs, uint64_t cols) {
+    bool f32_store = false;
+    for (uint32_t pc = 0; pc < count; pc++) f32_store |= code[pc].kind == 5 && code[pc].b == TC_F32;
+    if (!f32_store && runs_allowed(cols, code, count, places, inputs, outputs, TC_FUSED_MAX_OUTPUTS, false)) {
+        return kEpilogueRun;
     }
-    return kEpilogueRun;
+    return runs_allowed(cols, code, count, places, inputs, outputs, TC_FUSED_MAX_OUTPUTS, false, 4) ? 4 : 0;
 }
 
 // A program over whole runs (`runs_allowed`): a kernel over the rows x cols
@@ -805,8 +817,7 @@ int run_elems(const tc_encoded* code, uint32_t count) {
 // whole pieces, non-temporal when the program moves more than kStreamBytes.
 // From the program's second appearance, like the other compiled forms.
 std::string general_runs_source(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
-                                uint64_t rows, uint64_t cols, std::vector<float>* constants) {
-    const int E = run_elems(code, count);
+                                uint64_t rows, uint64_t cols, int E, std::vector<float>* constants) {
     const uint64_t runs = rows * cols / E;
     std::vector<bool> marks(count, false);
     uint64_t bytes = 0;  // a run's, loads of contiguous columns and stores
@@ -847,12 +858,11 @@ std::string general_runs_source(const tc_encoded* code, uint32_t count, uint32_t
 }
 
 bool run_general_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
-                      uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, hipStream_t s,
-                      int* status) {
-    const int E = run_elems(code, count);
+                      uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, int E,
+                      hipStream_t s, int* status) {
     const uint64_t runs = rows * cols / E;
     std::vector<float> constants;
-    const std::string source = general_runs_source(code, count, dtype, places, rows, cols, &constants);
+    const std::string source = general_runs_source(code, count, dtype, places, rows, cols, E, &constants);
     if (source.empty()) return false;
     hipFunction_t function = nullptr;
     if (!cached_kernels(source, {"tc_fused_runs"}, &function)) return false;
@@ -901,9 +911,8 @@ bool run_general_compiled(const tc_encoded* code, uint32_t count, uint32_t dtype
     const uint64_t total = rows * cols;
     // 32-bit element indices: below 2^31, so no index of the last pass wraps.
     if (place_count > static_cast<uint32_t>(kInlinePlaces) || total > (uint64_t{1} << 31)) return false;
-    if (runs_allowed(cols, code, count, places, buffers.inputs, buffers.outputs, TC_FUSED_MAX_OUTPUTS, false)) {
-        return run_general_runs(code, count, dtype, places, place_count, buffers, rows, cols, s, status);
-    }
+    const int E = run_width(code, count, places, buffers.inputs, buffers.outputs, cols);
+    if (E != 0) return run_general_runs(code, count, dtype, places, place_count, buffers, rows, cols, E, s, status);
     std::vector<float> constants;
     const std::string source = general_source(code, count, dtype, places, &constants);
     if (source.empty()) return false;
@@ -990,7 +999,7 @@ bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtyp
     // f32), four runs 256 columns apart in flight; otherwise 16 elements 64
     // apart.  Either way each lane adds its elements in the order it takes
     // them, cols / 64 of them.
-    const bool runs = runs_allowed(cols, code, count, places, buffers.inputs, nullptr, 0, false);
+    const bool runs = runs_allowed(cols, code, count, places, buffers.inputs, nullptr, 0, false, 4);
     std::vector<bool> marks(count, false);
     for (uint32_t pc = 0; runs && pc < count; pc++) {
         marks[pc] = code[pc].kind == 0 && places[code[pc].op].col_step == 1;
@@ -1071,7 +1080,7 @@ bool run_compiled_column_sums(const tc_encoded* code, uint32_t count, uint32_t d
                               hipStream_t s, int* status) {
     constexpr int E = 4;
     if (place_count > static_cast<uint32_t>(kInlinePlaces) || rows * cols > (uint64_t{1} << 31)) return false;
-    if (!runs_allowed(cols, code, count, places, buffers.inputs, nullptr, 0, false)) return false;
+    if (!runs_allowed(cols, code, count, places, buffers.inputs, nullptr, 0, false, 4)) return false;
     std::vector<bool> runs(count, false);
     for (uint32_t pc = 0; pc < count; pc++) {
         runs[pc] = code[pc].kind == 0 && places[code[pc].op].col_step == 1;
@@ -2046,9 +2055,9 @@ extern "C" int tc_fused_source(uint32_t dtype, const tc_encoded* code, uint32_t 
         const bool stream = rows * cols / 4 * tc::dense_chunk_bytes(code, count) > kStreamBytes;
         source = tc::dense_source(code, count, dtype, stream, &constants);
     } else if (place_count <= static_cast<uint32_t>(kInlinePlaces) && rows * cols <= (uint64_t{1} << 31)) {
-        source = tc::runs_allowed(cols, code, count, places, in, outs, TC_FUSED_MAX_OUTPUTS, false)
-                     ? tc::general_runs_source(code, count, dtype, places, rows, cols, &constants)
-                     : tc::general_source(code, count, dtype, places, &constants);
+        const int width = tc::run_width(code, count, places, in, outs, cols);
+        source = width != 0 ? tc::general_runs_source(code, count, dtype, places, rows, cols, width, &constants)
+                            : tc::general_source(code, count, dtype, places, &constants);
     }
     if (source.empty()) return fail(TC_UNSUPPORTED, "fused source: the program runs interpreted");
     *length = source.size();

@@ -123,14 +123,14 @@ def fused_source(dtype, code, places, rows, cols, pointers):
 
 
 @pytest.mark.parametrize("dtype", [lib.F32, lib.F16, lib.BF16])
-@pytest.mark.parametrize("cols,skew,form", [(1000, 0, "tc_fused_runs"), (70, 0, "tc_fused_general"),
-                                            (1000, 1, "tc_fused_general")],
-                         ids=["runs", "cols-not-whole-runs", "misaligned-bias"])
+@pytest.mark.parametrize("cols,skew,form", [(1000, 0, "tc_fused_runs"), (1004, 0, "tc_fused_runs"),
+                                            (70, 0, "tc_fused_general"), (1000, 1, "tc_fused_general")],
+                         ids=["runs", "runs-of-four", "cols-not-whole-runs", "misaligned-bias"])
 def test_broadcast_programs_compile_in_the_form_their_operands_allow(tmp_path, dtype, cols, skew, form):
-    # A program with broadcast operands runs in runs of eight columns when
-    # cols is a multiple of 8 and its operands are 16-byte aligned (here the
-    # f16 bias one element off makes it misaligned), else in the general
-    # form; both compile, without scratch.
+    # A program with broadcast operands runs in runs of columns when cols is
+    # a multiple of 4 and its operands start on whole pieces (here the f16
+    # bias one element off does not), else in the general form; both
+    # compile, without scratch.
     rows = 4099
     code, places = run_form_program(rows, skew)
     places[2] = identity_place(rows, cols)
@@ -144,15 +144,20 @@ def test_broadcast_programs_compile_in_the_form_their_operands_allow(tmp_path, d
     assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
 
 
-def test_a_program_storing_only_16_bit_outputs_runs_eight_columns_a_thread(tmp_path):
+@pytest.mark.parametrize("cols,width", [(1000, 8), (1004, 4)])
+def test_a_program_storing_only_16_bit_outputs_runs_eight_columns_a_thread(tmp_path, cols, width):
     # Without an f32 store, a thread of the run form takes eight columns:
-    # 16-byte loads and stores of the 16-bit operands.
-    rows, cols = 4099, 1000
+    # 16-byte loads and stores of the 16-bit operands; four (8-byte pieces)
+    # when cols is a multiple of 4 but not of 8.
+    rows = 4099
     code, places = run_form_program(rows, 0)
     places[2] = identity_place(rows, cols)
     source = fused_source(lib.BF16, code[:-1], places, rows, cols, [0x10000, 0x20000, 0x30000, 0x40000])
-    assert "tc::load_wide<8>(in[0]" in source and "tc::store_wide<8, false>(out[0]" in source
-    text = compile_kernel(tmp_path, "runs_eight", source)
+    if width == 8:
+        assert "tc::load_wide<8>(in[0]" in source and "tc::store_wide<8, false>(out[0]" in source
+    else:
+        assert "tc::load_run<4>(in[0]" in source and "tc::store_run<4, false>(out[0]" in source
+    text = compile_kernel(tmp_path, f"runs_{width}", source)
     assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
 
 

@@ -302,17 +302,19 @@ def test_large_programs_past_the_resident_limit_run_and_stay_exact():
 
 
 @pytest.mark.parametrize("f32_store", [True, False], ids=["f32-store", "16-bit-stores"])
-@pytest.mark.parametrize("rows,cols,skew", [(4099, 1000, 0), (37, 72, 0), (1, 8, 0), (37, 70, 0), (4099, 1000, 1)],
-                         ids=["runs", "runs-small", "runs-one-row", "cols-not-whole-runs", "misaligned-bias"])
+@pytest.mark.parametrize("rows,cols,skew", [(4099, 1000, 0), (37, 72, 0), (1, 8, 0), (37, 1004, 0), (37, 70, 0),
+                                            (4099, 1000, 1)],
+                         ids=["runs", "runs-small", "runs-one-row", "runs-of-four", "cols-not-whole-runs",
+                              "misaligned-bias"])
 def test_a_broadcast_program_in_runs_stays_exact(rows, cols, skew, f32_store):
     # A program whose places step their columns by 0 or 1 (a contiguous
     # matrix, a row-broadcast vector, one value a row, a scalar) runs
-    # compiled in runs of one row when cols is a multiple of 8 and its
-    # operands are 16-byte aligned: eight columns a thread (16-byte pieces)
-    # when it stores only 16-bit outputs, four when it stores f32; one load a
-    # run for the value a row.  A cols not a multiple of 8, or a bias one
-    # element off 16 bytes, takes the element form.  Every call, in every
-    # type, gives the oracle's bits.
+    # compiled in runs of one row when cols is a multiple of 4 and its
+    # operands start on whole pieces: eight columns a thread (16-byte
+    # pieces) when it stores only 16-bit outputs and cols is a multiple of 8,
+    # else four; one load a run for the value a row.  A cols not a multiple
+    # of 4, or a bias one element off its piece, takes the element form.
+    # Every call, in every type, gives the oracle's bits.
     rng = np.random.default_rng(rows + cols + skew)
     bias = to_kind(rng.standard_normal(cols + skew), lib.F16)
     scale = to_kind(rng.uniform(0.5, 2, rows), lib.BF16)
