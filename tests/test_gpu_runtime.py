@@ -182,3 +182,73 @@ def test_a_split_reduction_replays_from_a_graph_like_its_eager_run():
     graph.destroy()
     del out
     lib.call("tc_release_graph_memory")
+
+
+def test_compiled_programs_replay_from_a_graph_like_their_eager_runs():
+    # The compiled forms of a program, captured once compiled: column sums
+    # with their rows split (partial sums in memory the runtime allocates,
+    # added by a second launch), row sums in runs, the one-kernel layer norm
+    # (four waves a row, gamma loaded ahead) and a run-form program storing
+    # f32.  Replays, with eager work between them, must each give the eager
+    # result, bit for bit.
+    from tests.common import EXP, Code, column_broadcast, identity_place, row_broadcast
+
+    rng = np.random.default_rng(23)
+    f32 = lib.F32
+    # exp(x) * 0.5 + 0.25, summed along either axis of a 5000 x 64 matrix.
+    code = Code()
+    y = code.binary(lib.ADD, code.binary(lib.MUL, code.unary(EXP, code.load(0, 0, f32)), code.const(0.5)),
+                    code.const(0.25))
+    code.store(y, f32, 0)
+    rows, cols = 5000, 64
+    x = lib.Buffer.of(rng.uniform(-1, 1, rows * cols).astype(np.float32))
+    place = [identity_place(rows, cols)]
+    column_sums, row_sums = lib.Buffer(4 * cols), lib.Buffer(4 * rows)
+    # (x - mean) / (deviations / cols + 1e-5) * gamma over 64 rows of 8192.
+    ln_rows, ln_cols = 64, 8192
+    ln = Code()
+    centered = ln.binary(lib.SUB, ln.load(0, 0, f32), ln.load(1, 2, f32))
+    scale = ln.binary(lib.ADD, ln.binary(lib.MUL, ln.load(1, 3, f32), ln.const(np.float32(1.0 / ln_cols))),
+                      ln.const(1e-5))
+    ln.store(ln.binary(lib.MUL, ln.binary(lib.DIV, centered, scale), ln.load(2, 1, f32)), f32, 0)
+    ln_places = [identity_place(ln_rows, ln_cols), column_broadcast(ln_rows), row_broadcast(ln_cols)]
+    whole = identity_place(ln_rows, ln_cols)
+    lx = lib.Buffer.of(rng.uniform(-3, 3, ln_rows * ln_cols).astype(np.float32))
+    gamma = lib.Buffer.of(rng.uniform(0.5, 1.5, ln_cols).astype(np.float32))
+    normed = lib.Buffer(4 * ln_rows * ln_cols)
+    stats = [(lx, ln_rows * ln_cols, f32, whole, "mean"), (lx, ln_rows * ln_cols, f32, whole, "deviations")]
+
+    def run_all():
+        lib.fused_sum(f32, code.code, place, [(x, rows * cols)], rows, cols, 1, column_sums)
+        lib.fused_sum(f32, code.code, place, [(x, rows * cols)], rows, cols, 0, row_sums)
+        lib.fused_with_statistics(f32, ln.code, ln_places, [(lx, ln_rows * ln_cols), (gamma, ln_cols)],
+                                  [(normed, ln_rows * ln_cols)], ln_rows, ln_cols, stats)
+
+    def read():
+        return [column_sums.download(np.float32, cols), row_sums.download(np.float32, rows),
+                normed.download(np.float32, ln_rows * ln_cols)]
+
+    compiled = ctypes.c_uint64()
+    run_all()
+    run_all()  # the second appearance compiles each form
+    lib.call("tc_fused_compiled", ctypes.byref(compiled))
+    eager = read()
+    for buffer, n in ((column_sums, cols), (row_sums, rows), (normed, ln_rows * ln_cols)):
+        lib.call("tc_fill", buffer.ptr, n, 4, ctypes.byref(ctypes.c_float(0.0)))
+    lib.call("tc_release_graph_memory")
+    with Graph() as graph:
+        run_all()
+    for replay in range(3):
+        graph.replay()
+        lib.sync()
+        got = read()
+        for name, a, b in zip(("column sums", "row sums", "layer norm"), got, eager):
+            assert np.array_equal(a, b), (name, replay)
+        # Eager work between the replays, allocating partial sums of its own.
+        lib.fused_sum(f32, code.code, place, [(x, rows * cols)], rows, cols, 1, column_sums)
+        assert np.array_equal(column_sums.download(np.float32, cols), eager[0])
+    after = ctypes.c_uint64()
+    lib.call("tc_fused_compiled", ctypes.byref(after))
+    assert after.value == compiled.value  # nothing compiled anew under capture
+    graph.destroy()
+    lib.call("tc_release_graph_memory")
