@@ -111,15 +111,16 @@ int vector_product(uint32_t dtype, bool row_vector, bool accumulate, uint64_t ro
 std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtype, bool product_input, int elems,
                            const tc_place* places, std::vector<float>* constants);
 // The run form of the same program, for a kernel that hands it whole runs
-// of kEpilogueRun consecutive columns of one row (all inside C or none) and
-// loads what every row shares once: the members `Invariant`,
-// `invariant(inv, live, col)` (the runs starting at column `col`, loaded
-// when `live`) and `run(inv, live, row, col, N, product)`.  Loads of
-// contiguous columns and stores move 16-byte pieces, the stores
-// non-temporal; the caller checks their alignment.  Empty when a load's
-// place steps through its columns other than by 0 or 1, or folds rows.
+// of E consecutive columns of one row (all inside C or none) and loads what
+// every row shares once: the members `Invariant`, `invariant(inv, live,
+// col)` (the runs starting at column `col`, loaded when `live`) and
+// `run(inv, live, row, col, N, product)`.  Loads of contiguous columns and
+// stores move 16-byte pieces: E = kEpilogueRun (16-bit products) streams its
+// stores past the caches, E = 4 (f32 products, one piece a run) stores
+// plainly; the caller checks their alignment.  Empty when a load's place
+// steps through its columns other than by 0 or 1, or folds rows.
 std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
-                          std::vector<float>* constants);
+                          std::vector<float>* constants, int E = kEpilogueRun);
 // Whether a program over `cols` columns may run in runs of `width` columns
 // moved in 16-byte pieces, or as one piece when the run is shorter (four
 // 16-bit elements: 8 bytes): `cols` a multiple of the run, every output

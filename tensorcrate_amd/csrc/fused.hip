@@ -1243,8 +1243,11 @@ std::string epilogue_group(const tc_encoded* code, uint32_t count, uint32_t dtyp
 }
 
 std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
-                          std::vector<float>* constants) {
-    constexpr int E = kEpilogueRun;
+                          std::vector<float>* constants, int E) {
+    // Runs of eight (16-bit products) move 16-byte pieces and stream their
+    // stores; runs of four (f32 products) move one 16-byte piece, stored
+    // plainly as the f32 kernel's own stores are.
+    const bool wide = E % 8 == 0;
     const std::string round = "tc_round<" + std::to_string(dtype) + ">";
     const std::string each = "    for (int e = 0; e < " + std::to_string(E) + "; e++) ";
     std::vector<bool> runs(count, false), invariant(count, false);
@@ -1264,9 +1267,9 @@ std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype
             invariant[pc] = true;
             members << "    float i" << pc << "[" << E << "];\n";
             if (place.col_step == 1) {
-                loader << each << name << "[e] = 0.0f;\n    if (live) tc::load_wide<" << E << ">(in[" << int(in.a)
-                       << "], " << int(in.b) << "u, " << place_index(place, p, "0u", "col") << ", " << name
-                       << ");\n" << each << name << "[e] = " << round << "(" << name << "[e]);\n";
+                loader << each << name << "[e] = 0.0f;\n    if (live) tc::" << (wide ? "load_wide<" : "load_run<") << E
+                       << ">(in[" << int(in.a) << "], " << int(in.b) << "u, " << place_index(place, p, "0u", "col")
+                       << ", " << name << ");\n" << each << name << "[e] = " << round << "(" << name << "[e]);\n";
             } else {
                 loader << "    {\n      const float x = live ? " << round << "(tc::load_as(in[" << int(in.a) << "], "
                        << int(in.b) << "u, " << place_index(place, p, "0u", "0u") << ")) : 0.0f;\n  " << each
@@ -1279,7 +1282,7 @@ std::string epilogue_runs(const tc_encoded* code, uint32_t count, uint32_t dtype
         }
     }
     const std::string body =
-        group_body(code, count, dtype, true, E, places, constants, false, -1, nullptr, &runs, &invariant, true, true);
+        group_body(code, count, dtype, true, E, places, constants, false, -1, nullptr, &runs, &invariant, wide, wide);
     const std::string e = std::to_string(E);
     return "  struct Invariant {\n" + members.str() + "  };\n"
            "  __device__ __forceinline__ void invariant(Invariant& inv, bool live, uint32_t col) const {\n" +

@@ -566,10 +566,12 @@ constexpr int kCompiledElems = 16;
 std::string epilogue_source(uint32_t dtype, const tc_encoded* code, uint32_t count, const tc_place* host_places,
                             std::vector<float>* constants, bool runs, bool* has_runs = nullptr) {
     const std::string body = epilogue_group(code, count, dtype, true, kCompiledElems, host_places, constants);
-    // The run form, which the four-wave kernel takes, for 16-bit products
-    // whose operands allow it (the caller's `runs`).
+    // The run form, where the operands allow it (the caller's `runs`): runs
+    // of eight for the four-wave kernel's 16-bit products, of four for the
+    // f32 kernel.
     const std::string run_members =
-        runs && dtype != TC_F32 ? epilogue_runs(code, count, dtype, host_places, constants) : std::string();
+        runs ? epilogue_runs(code, count, dtype, host_places, constants, dtype == TC_F32 ? 4 : kEpilogueRun)
+             : std::string();
     if (constants->size() > static_cast<size_t>(kInlineCode)) return std::string();
     if (has_runs != nullptr) *has_runs = !run_members.empty();
     return "#include \"gemm_kernels.hpp\"\n"
@@ -597,7 +599,8 @@ bool run_compiled_epilogue(uint32_t dtype, uint32_t m, uint32_t k, uint32_t n, c
                            const void* const* inputs, uint32_t input_count, void* const* outputs,
                            uint32_t output_count, hipStream_t s, int* status) {
     std::vector<float> constants;
-    const bool runs = runs_allowed(n, code, count, host_places, inputs, outputs, output_count, true);
+    const bool runs = runs_allowed(n, code, count, host_places, inputs, outputs, output_count, true,
+                                   dtype == TC_F32 ? 4 : kEpilogueRun);
     bool has_runs = false;
     const std::string source = epilogue_source(dtype, code, count, host_places, &constants, runs, &has_runs);
     if (source.empty()) return false;

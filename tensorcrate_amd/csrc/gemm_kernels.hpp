@@ -138,6 +138,15 @@ template <class EPI, class = void>
 struct HasRuns : std::false_type {};
 template <class EPI>
 struct HasRuns<EPI, std::void_t<decltype(EPI::kRuns)>> : std::integral_constant<bool, EPI::kRuns> {};
+// The run form's invariant state where the epilogue has one, else nothing.
+template <class EPI, bool = HasRuns<EPI>::value>
+struct RunState {
+    struct Invariant {};
+};
+template <class EPI>
+struct RunState<EPI, true> {
+    using Invariant = typename EPI::Invariant;
+};
 
 // A workgroup barrier ordering LDS alone: fences scoped to the workgroup and
 // to LDS ("local") around the barrier, so LDS accesses stay on their side
@@ -203,6 +212,27 @@ __device__ __forceinline__ void program_pass(const EPI& epi, float* r0, float* r
             live[v] = inside && row[v] < M && col[v] < N;
         }
         epi.group(live, row, col, N, product);
+    }
+}
+
+// The run form of the same epilogue (EPI::run, runs of four columns): the
+// staged rows read back one 16-byte run a thread, consecutive threads on
+// consecutive runs, each thread on the same four columns in every round
+// (BN / 4 divides the workgroup), whose row-invariant loads `inv` holds.
+template <int BN, int G, int REGION_ROWS, int H, int WAVE_ROWS, class EPI>
+__device__ __forceinline__ void program_runs(const EPI& epi, const typename EPI::Invariant& inv, float* region,
+                                             uint32_t rows, uint32_t pass, uint32_t row_base, uint32_t col_base,
+                                             uint32_t M, uint32_t N) {
+    constexpr uint32_t kPerRow = BN / 4;
+    const uint32_t runs = rows * kPerRow;
+    for (uint32_t q = threadIdx.x; q < runs; q += blockDim.x) {
+        const uint32_t rr = q / kPerRow, cc = (q % kPerRow) * 4;
+        const float4 v =
+            *reinterpret_cast<const float4*>(staged_at<BN, G, REGION_ROWS>(region, region, region, region, rr, cc));
+        const float product[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t row = row_base + (rr / H) * WAVE_ROWS + pass * H + rr % H;
+        const uint32_t col = col_base + cc;
+        epi.run(inv, row < M && col < N, row, col, N, product);
     }
 }
 
@@ -359,6 +389,14 @@ __global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __rest
         constexpr int kPass = kFit >= 128 ? 128 : 64;
         constexpr int kPasses = BM / kPass, H = BM / 2 / kPasses;
         static_assert(kFit >= kPass && BM % kPass == 0 && H % 16 == 0, "a pass fits in LDS");
+        // The run form loads what every row reads alike for the thread's
+        // four columns before any store, so no load waits behind one.
+        typename RunState<EPI>::Invariant inv{};
+        if constexpr (HasRuns<EPI>::value) {
+            static_assert(kThreads % (BN / 4) == 0, "a thread keeps its columns in every round");
+            const uint32_t col = n0 + (threadIdx.x % (BN / 4)) * 4;
+            epi.invariant(inv, col < N, col);
+        }
 #pragma unroll
         for (int pass = 0; pass < kPasses; pass++) {
             lds_barrier();  // every wave is done with LDS
@@ -375,7 +413,11 @@ __global__ void __launch_bounds__(kThreads) inplace32_kernel(const float* __rest
                 }
             }
             lds_barrier();
-            program_pass<BN, 16, kPass, H, BM / 2>(epi, lds_a, lds_a, lds_a, lds_a, kPass, pass, m0, n0, M, N);
+            if constexpr (HasRuns<EPI>::value) {
+                program_runs<BN, 16, kPass, H, BM / 2>(epi, inv, lds_a, kPass, pass, m0, n0, M, N);
+            } else {
+                program_pass<BN, 16, kPass, H, BM / 2>(epi, lds_a, lds_a, lds_a, lds_a, kPass, pass, m0, n0, M, N);
+            }
         }
     } else {
 #pragma unroll

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from tensorcrate_amd import _build, lib
-from tests.common import Code, column_broadcast, identity_place, run_form_program
+from tests.common import Code, column_broadcast, identity_place, row_broadcast, run_form_program
 
 CSRC = Path(__file__).resolve().parent.parent / "tensorcrate_amd" / "csrc"
 RUNTIME_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-Xclang", "-target-feature",
@@ -169,4 +169,35 @@ def test_the_composed_layer_norm_program_runs_in_runs(tmp_path):
     source = fused_source(lib.F32, layer_norm(lib.F32, cols), places, rows, cols, [0x10000, 0x20000, 0x30000, 0x40000])
     assert "tc_fused_runs(" in source
     text = compile_kernel(tmp_path, "layer_norm_runs", source)
+    assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
+
+
+def epilogue_source(kind, code, places, runs):
+    enc, pl = lib._program(code, places)
+    length = ctypes.c_uint64()
+    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), runs, None, 0, ctypes.byref(length))
+    out = ctypes.create_string_buffer(length.value + 1)
+    lib.call("tc_matmul_epilogue_source", kind, enc, len(code), pl, len(places), runs, out, length.value + 1,
+             ctypes.byref(length))
+    return out.value.decode()
+
+
+@pytest.mark.parametrize("runs", [1, 0])
+def test_the_f32_product_epilogue_compiles_in_runs_of_four(tmp_path, runs):
+    # relu(x w + b) over an f32 product: in the run form the f32 kernel hands
+    # the program runs of four columns (one 16-byte piece, stored plainly),
+    # the bias loaded once for a thread's columns; both forms compile into
+    # the f32 kernel without scratch.
+    m, n = 64, 96
+    code = Code()
+    total = code.binary(lib.ADD, code.load(0, 0, lib.F32), code.load(1, 1, lib.F32))
+    code.store(code.compare(lib.MAX, total, code.const(0.0)), lib.F32, 0)
+    places = [identity_place(m, n), row_broadcast(n)]
+    source = epilogue_source(lib.F32, code.code, places, runs)
+    assert f"static constexpr bool kRuns = {'true' if runs else 'false'};" in source
+    if runs:
+        assert "tc::load_run<4>(in[1]" in source and "tc::store_run<4, false>(out[0]" in source
+    text = compile_kernel(tmp_path, f"f32_epilogue_{runs}", source +
+                          "template __global__ void tc::inplace32_kernel<float, true, false, 128, 128, CompiledStore>("
+                          "const float*, const float*, float*, uint32_t, uint32_t, uint32_t, bool, CompiledStore);\n")
     assert re.findall(r"\.private_segment_fixed_size:\s+(\d+)", text) == ["0"]
