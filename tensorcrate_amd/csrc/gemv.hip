@@ -5,6 +5,9 @@
 //  - matvec: one wave per row, lanes reading 16 bytes of the row at a time
 //    (eight such reads in flight per lane),
 //    a 64-lane shuffle tree for the dot product.  The vector stays hot in L2.
+// A matrix as large as the Infinity Cache is read with non-temporal loads,
+// streaming past the caches so they keep the vector (measured at 8192 x 8192
+// f32: matvec 72.7% -> 80.3% of HBM, vecmat 69.3% -> 74.2%).
 //  - vecmat: lanes on neighbouring columns, 16 bytes of a row each, so
 //    every row read is one coalesced run; four row groups split the rows
 //    inside a block, and tall matrices split their rows across blocks,
@@ -29,7 +32,7 @@ __device__ inline float wave_sum(float v) {
     return v;
 }
 
-template <typename S, bool PACKED>
+template <typename S, bool PACKED, bool NT>
 __global__ void __launch_bounds__(256) matvec_kernel(const S* __restrict__ m, const S* __restrict__ v,
                                                      S* __restrict__ y, uint64_t rows, uint64_t cols,
                                                      bool accumulate) {
@@ -52,7 +55,8 @@ __global__ void __launch_bounds__(256) matvec_kernel(const S* __restrict__ m, co
                 Pack<S> a[8], b[8];
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    a[u] = pr[p + u * 64];
+                    const uint4 w = load_word<NT>(pr + p + u * 64);
+                    __builtin_memcpy(&a[u], &w, 16);
                     b[u] = pv[p + u * 64];
                 }
 #pragma unroll
@@ -84,7 +88,7 @@ constexpr int kGroups = 4;
 // for f32 at V = W = 4); `split` picks the rows.  With one split the block
 // finishes its columns; otherwise it writes f32 partial sums to
 // `partial[split][col]`.
-template <typename S, int V, int W>
+template <typename S, int V, int W, bool NT>
 __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, const S* __restrict__ m,
                                                      S* __restrict__ y, float* __restrict__ partial,
                                                      uint64_t rows, uint64_t cols, uint64_t tiles,
@@ -128,7 +132,10 @@ __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, co
                 w[q] = E::widen(v[r + q]);
 #pragma unroll
                 for (int u = 0; u < W; u++) {
-                    if (live[u]) p[q][u] = *reinterpret_cast<const Pack<S>*>(m + (r + q) * cols + base + u * 64 * V);
+                    if (live[u]) {
+                        const uint4 word = load_word<NT>(m + (r + q) * cols + base + u * 64 * V);
+                        __builtin_memcpy(&p[q][u], &word, 16);
+                    }
                 }
             }
 #pragma unroll
@@ -148,7 +155,9 @@ __global__ void __launch_bounds__(256) vecmat_kernel(const S* __restrict__ v, co
         for (int u = 0; u < W; u++) {
             if (!live[u]) continue;
             if (V > 1) {
-                Pack<S> p = *reinterpret_cast<const Pack<S>*>(m + r * cols + base + u * 64 * V);
+                const uint4 word = load_word<NT>(m + r * cols + base + u * 64 * V);
+                Pack<S> p;
+                __builtin_memcpy(&p, &word, 16);
 #pragma unroll
                 for (int k = 0; k < V; k++) acc[u][k] += w * E::widen(p.v[k]);
             } else {
@@ -227,19 +236,25 @@ int matvec_typed(bool accumulate, uint64_t rows, uint64_t cols, const void* m, c
     const S* pv = static_cast<const S*>(v);
     S* py = static_cast<S*>(y);
     const bool packed = cols % Pack<S>::N == 0 && aligned16(m) && aligned16(v);
+    const bool stream = rows * cols * sizeof(S) >= kStreamBytes;
     const uint32_t blocks = grid_for(rows, 4, 32);
-    if (packed) {
-        matvec_kernel<S, true><<<blocks, 256, 0, s>>>(pm, pv, py, rows, cols, accumulate);
+    if (packed && stream) {
+        matvec_kernel<S, true, true><<<blocks, 256, 0, s>>>(pm, pv, py, rows, cols, accumulate);
+    } else if (packed) {
+        matvec_kernel<S, true, false><<<blocks, 256, 0, s>>>(pm, pv, py, rows, cols, accumulate);
     } else {
-        matvec_kernel<S, false><<<blocks, 256, 0, s>>>(pm, pv, py, rows, cols, accumulate);
+        matvec_kernel<S, false, false><<<blocks, 256, 0, s>>>(pm, pv, py, rows, cols, accumulate);
     }
     return check_launch("matvec");
 }
 
-template <typename S, int V, int W>
-int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, bool accumulate, hipStream_t s) {
+// `per_cu`: the blocks a CU that row splits fill, when the column tiles
+// alone do not.
+template <typename S, int V, int W, bool NT>
+int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, bool accumulate, uint64_t per_cu,
+                  hipStream_t s) {
     const uint64_t tiles = (cols + 64 * V * W - 1) / (64 * V * W);
-    const uint64_t want = static_cast<uint64_t>(compute_units()) * 4;
+    const uint64_t want = static_cast<uint64_t>(compute_units()) * per_cu;
     uint64_t splits = 1;
     if (tiles < want) {
         splits = (want + tiles - 1) / tiles;
@@ -256,7 +271,7 @@ int launch_vecmat(const S* v, const S* m, S* y, uint64_t rows, uint64_t cols, bo
         if (status != TC_OK) return status;
         partial = static_cast<float*>(scratch);
     }
-    vecmat_kernel<S, V, W><<<static_cast<uint32_t>(tiles * splits), 256, 0, s>>>(v, m, y, partial, rows, cols,
+    vecmat_kernel<S, V, W, NT><<<static_cast<uint32_t>(tiles * splits), 256, 0, s>>>(v, m, y, partial, rows, cols,
                                                                                  tiles, splits, per_split, accumulate);
     int status = check_launch("vecmat");
     if (status == TC_OK && splits > 1) {
@@ -275,12 +290,19 @@ int vecmat_typed(bool accumulate, uint64_t rows, uint64_t cols, const void* v, c
     const S* pm = static_cast<const S*>(m);
     S* py = static_cast<S*>(y);
     constexpr int V = Pack<S>::N;
-    // One pack a lane: measured at 8192 x 8192 f32, two or four packs a lane
-    // (2 or 4 KiB runs of a row per wave) were slower, 68% and 66% of HBM
-    // against 70%, their extra row splits costing more than the longer runs
-    // gain.
-    if (cols % V == 0 && aligned16(m)) return launch_vecmat<S, V, 1>(pv, pm, py, rows, cols, accumulate, s);
-    return launch_vecmat<S, 1, 1>(pv, pm, py, rows, cols, accumulate, s);
+    if (cols % V == 0 && aligned16(m)) {
+        // Streamed: two packs a lane on two blocks a CU.  Measured at 8192 x
+        // 8192 f32 with non-temporal loads, as a share of HBM: 78% against
+        // 74% for one pack a lane on four blocks a CU (one pack on two: 65%;
+        // four packs on two: 77%; two packs on one, four or eight: 60%,
+        // 77% and 71%).  Before streaming, one pack a lane on four blocks a
+        // CU led (70%, against 68% and 66% for two and four packs).
+        if (rows * cols * sizeof(S) >= kStreamBytes) {
+            return launch_vecmat<S, V, 2, true>(pv, pm, py, rows, cols, accumulate, 2, s);
+        }
+        return launch_vecmat<S, V, 1, false>(pv, pm, py, rows, cols, accumulate, 4, s);
+    }
+    return launch_vecmat<S, 1, 1, false>(pv, pm, py, rows, cols, accumulate, 4, s);
 }
 
 }  // namespace

@@ -117,32 +117,46 @@ def test_an_empty_inner_dimension_gives_zeros_or_the_addend():
     assert np.array_equal(product(lib.F32, lib.F32, lib.PLAIN, a, b, 3, 0, 4, addend=c), c)
 
 
+def check_matvec_vecmat(kind, rows, cols, rng):
+    """matvec, matvec with an addend and vecmat of one matrix against f64."""
+    m = to_kind(rng.uniform(-1, 1, (rows, cols)).astype(np.float32), kind)
+    v = to_kind(rng.uniform(-1, 1, cols), kind)
+    w = to_kind(rng.uniform(-1, 1, rows), kind)
+    dm, dv, dw = lib.Buffer.of(m), lib.Buffer.of(v), lib.Buffer.of(w)
+    out = lib.Buffer(rows * 4)
+    lib.call("tc_matvec", kind, 0, rows, cols, dm.ptr, dv.ptr, out.ptr)
+    got = widen(kind, out.download(HOST[kind], rows))
+    wm, wv, ww = widen(kind, m), widen(kind, v), widen(kind, w)
+    want = wm.astype(np.float64) @ wv
+    scale = np.abs(wm).astype(np.float64) @ np.abs(wv)
+    unit = 2.0 ** -24 if kind == lib.F32 else (2.0 ** -11 if kind == lib.F16 else 2.0 ** -8)
+    assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(cols) * scale + unit * np.abs(want) + 1e-30)
+    lib.call("tc_matvec", kind, 1, rows, cols, dm.ptr, dv.ptr, dw.ptr)
+    got = widen(kind, dw.download(HOST[kind], rows))
+    assert np.all(np.abs(got - (want + ww)) <= 1e-5 * np.sqrt(cols) * scale + unit * (np.abs(want) + 1) + 1e-30)
+    out = lib.Buffer(cols * 4)
+    lib.call("tc_vecmat", kind, rows, cols, dw.ptr, dm.ptr, out.ptr)
+    got = widen(kind, out.download(HOST[kind], cols))
+    w2 = widen(kind, dw.download(HOST[kind], rows))
+    want = w2.astype(np.float64) @ wm
+    scale = np.abs(w2).astype(np.float64) @ np.abs(wm)
+    assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(rows) * scale + unit * np.abs(want) + 1e-30)
+
+
 def test_matvec_vecmat():
     rng = np.random.default_rng(13)
     for kind in [lib.F32, lib.BF16, lib.F16]:
         for rows, cols in [(1, 1), (37, 53), (1000, 64), (8, 8192), (513, 1031), (300, 5000), (64, 8200), (2000, 4096)]:
-            m = to_kind(rng.uniform(-1, 1, (rows, cols)), kind)
-            v = to_kind(rng.uniform(-1, 1, cols), kind)
-            w = to_kind(rng.uniform(-1, 1, rows), kind)
-            dm, dv, dw = lib.Buffer.of(m), lib.Buffer.of(v), lib.Buffer.of(w)
-            out = lib.Buffer(rows * 4)
-            lib.call("tc_matvec", kind, 0, rows, cols, dm.ptr, dv.ptr, out.ptr)
-            got = widen(kind, out.download(HOST[kind], rows))
-            wm, wv, ww = widen(kind, m), widen(kind, v), widen(kind, w)
-            want = wm.astype(np.float64) @ wv
-            scale = np.abs(wm).astype(np.float64) @ np.abs(wv)
-            unit = 2.0 ** -24 if kind == lib.F32 else (2.0 ** -11 if kind == lib.F16 else 2.0 ** -8)
-            assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(cols) * scale + unit * np.abs(want) + 1e-30)
-            lib.call("tc_matvec", kind, 1, rows, cols, dm.ptr, dv.ptr, dw.ptr)
-            got = widen(kind, dw.download(HOST[kind], rows))
-            assert np.all(np.abs(got - (want + ww)) <= 1e-5 * np.sqrt(cols) * scale + unit * (np.abs(want) + 1) + 1e-30)
-            out = lib.Buffer(cols * 4)
-            lib.call("tc_vecmat", kind, rows, cols, dw.ptr, dm.ptr, out.ptr)
-            got = widen(kind, out.download(HOST[kind], cols))
-            w2 = widen(kind, dw.download(HOST[kind], rows))
-            want = w2.astype(np.float64) @ wm
-            scale = np.abs(w2).astype(np.float64) @ np.abs(wm)
-            assert np.all(np.abs(got - want) <= 1e-5 * np.sqrt(rows) * scale + unit * np.abs(want) + 1e-30)
+            check_matvec_vecmat(kind, rows, cols, rng)
+
+
+@pytest.mark.parametrize("kind,rows,cols", [(lib.F32, 8192, 8192), (lib.F32, 8191, 8196), (lib.BF16, 8192, 16384),
+                                            (lib.F16, 16390, 8196)])
+def test_matvec_vecmat_of_matrices_as_large_as_the_infinity_cache(kind, rows, cols):
+    # Matrices of 256 MiB and more are read with non-temporal loads, and
+    # vecmat takes two packs a lane there: whole and ragged column tiles,
+    # ragged row splits.
+    check_matvec_vecmat(kind, rows, cols, np.random.default_rng(rows + cols))
 
 
 def test_config1_f32_512_cubed():
