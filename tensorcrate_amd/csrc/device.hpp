@@ -103,19 +103,33 @@ __device__ __forceinline__ void store_as(void* base, uint32_t dtype, uint64_t in
     }
 }
 
+// A 16-byte or 8-byte piece, with NT a non-temporal load (streaming past
+// the caches, for data read once).
+template <bool NT, typename W>
+__device__ __forceinline__ W load_piece(const W* at) {
+    if (NT) return __builtin_nontemporal_load(at);
+    return *at;
+}
+
 // `E` consecutive elements from `index` on, as `load_as` reads them one by
 // one, moved four at a time: 16 bytes for f32, 8 for the 16-bit types.
-// `index` is a multiple of 4 and `base` aligned to the piece.
-template <int E>
+// `index` is a multiple of 4 and `base` aligned to the piece.  With NT the
+// loads are non-temporal.
+template <int E, bool NT = false>
 __device__ __forceinline__ void load_run(const void* base, uint32_t dtype, uint64_t index, float (&out)[E]) {
     static_assert(E % 4 == 0, "whole runs of four");
+    typedef uint32_t words4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t words2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int q = 0; q < E / 4; q++) {
         if (dtype == tc_ops::F32) {
-            const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + index + 4 * q);
-            out[4 * q] = v.x, out[4 * q + 1] = v.y, out[4 * q + 2] = v.z, out[4 * q + 3] = v.w;
+            const words4 v =
+                load_piece<NT>(reinterpret_cast<const words4*>(static_cast<const float*>(base) + index + 4 * q));
+            out[4 * q] = __uint_as_float(v.x), out[4 * q + 1] = __uint_as_float(v.y);
+            out[4 * q + 2] = __uint_as_float(v.z), out[4 * q + 3] = __uint_as_float(v.w);
         } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + index + 4 * q);
+            const words2 v =
+                load_piece<NT>(reinterpret_cast<const words2*>(static_cast<const uint16_t*>(base) + index + 4 * q));
             const uint16_t h[4] = {static_cast<uint16_t>(v.x), static_cast<uint16_t>(v.x >> 16),
                                    static_cast<uint16_t>(v.y), static_cast<uint16_t>(v.y >> 16)};
 #pragma unroll
@@ -167,20 +181,24 @@ __device__ __forceinline__ void store_run(void* base, uint32_t dtype, uint64_t i
 // As `load_run`, in 16-byte pieces for every type: eight 16-bit elements or
 // four f32 a piece.  `index` is a multiple of a piece's elements and `base`
 // 16-byte aligned.
-template <int E>
+template <int E, bool NT = false>
 __device__ __forceinline__ void load_wide(const void* base, uint32_t dtype, uint64_t index, float (&out)[E]) {
     static_assert(E % 8 == 0, "whole runs of eight");
+    typedef uint32_t words4 __attribute__((ext_vector_type(4)));
     if (dtype == tc_ops::F32) {
 #pragma unroll
         for (int q = 0; q < E / 4; q++) {
-            const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + index + 4 * q);
-            out[4 * q] = v.x, out[4 * q + 1] = v.y, out[4 * q + 2] = v.z, out[4 * q + 3] = v.w;
+            const words4 v =
+                load_piece<NT>(reinterpret_cast<const words4*>(static_cast<const float*>(base) + index + 4 * q));
+            out[4 * q] = __uint_as_float(v.x), out[4 * q + 1] = __uint_as_float(v.y);
+            out[4 * q + 2] = __uint_as_float(v.z), out[4 * q + 3] = __uint_as_float(v.w);
         }
         return;
     }
 #pragma unroll
     for (int q = 0; q < E / 8; q++) {
-        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + index + 8 * q);
+        const words4 v =
+            load_piece<NT>(reinterpret_cast<const words4*>(static_cast<const uint16_t*>(base) + index + 8 * q));
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int j = 0; j < 8; j++) {

@@ -247,9 +247,22 @@ def test_fused_with_statistics_runs_as_one_compiled_kernel(dtype, shape):
     # 8300 (whose last packs fall past the row on some lanes).  A shape may
     # find its kernel compiled already; either way the last call is one
     # launch.
+    check_one_kernel_statistics(dtype, *shape)
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(lib.F32, 8192, 8192), (lib.BF16, 8192, 16384)])
+def test_one_kernel_statistics_of_a_source_as_large_as_the_infinity_cache(dtype, rows, cols):
+    # A source of 256 MiB or more is read with non-temporal loads, each row
+    # once, and meets the same bound.
+    check_one_kernel_statistics(dtype, rows, cols)
+
+
+def check_one_kernel_statistics(dtype, rows, cols):
+    """(x - mean) / (deviations / cols + 1) through fused_with_statistics,
+    three calls, each within the statistics' rounding of the oracle; the
+    last one launch."""
     import ctypes
 
-    rows, cols = shape
     code = Code()
     x = code.load(0, 0, dtype)
     mean = code.load(1, 1, dtype)

@@ -303,9 +303,9 @@ def test_large_programs_past_the_resident_limit_run_and_stay_exact():
 
 @pytest.mark.parametrize("f32_store", [True, False], ids=["f32-store", "16-bit-stores"])
 @pytest.mark.parametrize("rows,cols,skew", [(4099, 1000, 0), (37, 72, 0), (1, 8, 0), (37, 1004, 0), (37, 70, 0),
-                                            (4099, 1000, 1)],
+                                            (4099, 1000, 1), (8192, 8192, 0)],
                          ids=["runs", "runs-small", "runs-one-row", "runs-of-four", "cols-not-whole-runs",
-                              "misaligned-bias"])
+                              "misaligned-bias", "runs-streamed"])
 def test_a_broadcast_program_in_runs_stays_exact(rows, cols, skew, f32_store):
     # A program whose places step their columns by 0 or 1 (a contiguous
     # matrix, a row-broadcast vector, one value a row, a scalar) runs
@@ -314,6 +314,8 @@ def test_a_broadcast_program_in_runs_stays_exact(rows, cols, skew, f32_store):
     # pieces) when it stores only 16-bit outputs and cols is a multiple of 8,
     # else four; one load a run for the value a row.  A cols not a multiple
     # of 4, or a bias one element off its piece, takes the element form.
+    # Past 256 MiB of traffic (8192 x 8192) the program streams: its stores
+    # and the matrix's loads are non-temporal, the bias's loads not.
     # Every call, in every type, gives the oracle's bits.
     rng = np.random.default_rng(rows + cols + skew)
     bias = to_kind(rng.standard_normal(cols + skew), lib.F16)
