@@ -994,6 +994,18 @@ bool launch_general(hipFunction_t function, const std::vector<float>& constants,
 // appearance: a wave a row, each lane summing its elements in the order it
 // takes them (runs of four columns, or 16 elements 64 apart) and the wave in
 // a fixed shuffle tree, so the output itself is never stored.
+// The bytes an element the program's loads read through places that walk
+// rows (a row-invariant place reads the same run in every row).
+uint64_t walked_bytes(const tc_encoded* code, uint32_t count, const tc_place* places) {
+    uint64_t bytes = 0;
+    for (uint32_t pc = 0; pc < count; pc++) {
+        if (code[pc].kind != 0) continue;
+        const tc_place& p = places[code[pc].op];
+        if (p.lead > 1 || (p.lead == 1 && p.steps[0] != 0)) bytes += code[pc].b == TC_F32 ? 4 : 2;
+    }
+    return bytes;
+}
+
 bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtype, const tc_place* places,
                            uint32_t place_count, const Buffers& buffers, uint64_t rows, uint64_t cols, void* out,
                            hipStream_t s, int* status) {
@@ -1009,9 +1021,11 @@ bool run_compiled_row_sums(const tc_encoded* code, uint32_t count, uint32_t dtyp
         marks[pc] = code[pc].kind == 0 && places[code[pc].op].col_step == 1;
     }
     const int elems = runs ? 4 : kGeneralElems;
+    // Runs over 256 MiB or more are read with non-temporal loads.
+    const bool stream = runs && rows * cols * walked_bytes(code, count, places) >= kStreamBytes;
     std::vector<float> constants;
-    const std::string body =
-        group_body(code, count, dtype, false, elems, places, &constants, true, -1, nullptr, runs ? &marks : nullptr);
+    const std::string body = group_body(code, count, dtype, false, elems, places, &constants, true, -1, nullptr,
+                                        runs ? &marks : nullptr, nullptr, false, stream);
     if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
     const std::string E = std::to_string(elems);
     const std::string walk =
@@ -1089,9 +1103,11 @@ bool run_compiled_column_sums(const tc_encoded* code, uint32_t count, uint32_t d
     for (uint32_t pc = 0; pc < count; pc++) {
         runs[pc] = code[pc].kind == 0 && places[code[pc].op].col_step == 1;
     }
+    // Runs over 256 MiB or more are read with non-temporal loads.
+    const bool stream = rows * cols * walked_bytes(code, count, places) >= kStreamBytes;
     std::vector<float> constants;
     const std::string body = group_body(code, count, dtype, false, E, places, &constants, true, -1, nullptr, &runs,
-                                        nullptr, false, false, true);
+                                        nullptr, false, stream, true);
     if (constants.size() > static_cast<size_t>(kInlineCode)) return false;
     const std::string T = std::to_string(dtype);
     const std::string source =

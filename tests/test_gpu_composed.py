@@ -188,6 +188,35 @@ def test_row_sums_of_a_repeated_program_run_as_one_compiled_kernel(dtype):
     assert counts[1] == counts[0] + 1 and counts[2] == counts[1]
 
 
+@pytest.mark.parametrize("axis", [0, 1], ids=["row-sums", "column-sums"])
+@pytest.mark.parametrize("dtype,rows,cols", [(lib.F32, 8192, 8192), (lib.BF16, 8192, 16384)])
+def test_sums_of_a_program_over_256_mib_of_runs(dtype, rows, cols, axis):
+    # Compiled row or column sums whose runs read 256 MiB or more load them
+    # non-temporally; every call (the first may compose, later ones run
+    # compiled) agrees with the oracle to the summation bound.
+    # exp(x) * 0.5 - 0.25 is this test's own program.
+    code = Code()
+    x = code.load(0, 0, dtype)
+    y = code.binary(lib.SUB, code.binary(lib.MUL, code.unary(EXP, x), code.const(0.5)), code.const(0.25))
+    code.store(y, dtype, 0)
+    rng = np.random.default_rng(dtype + axis)
+    values = to_kind(rng.uniform(-1, 1, rows * cols).astype(np.float32), dtype)
+    want = widen(dtype, oracle.fused_sum(dtype, code.code, [identity_place(rows, cols)], [values], rows, cols, axis))
+    exact = (np.exp(widen(dtype, values).astype(np.float64)) * 0.5 - 0.25).reshape(rows, cols).sum(1 - axis)
+    magnitude = (np.exp(widen(dtype, values).astype(np.float64)) * 0.5 + 0.25).reshape(rows, cols).sum(1 - axis)
+    unit = 2.0 ** -24 if dtype == lib.F32 else 2.0 ** -8
+    depth = cols if axis == 0 else rows
+    # Per element: three operations rounded to the type (and exp's own
+    # error); per sum: at most `depth` additions in f32, then the result
+    # rounded to the type; the oracle within depth 2^-24 of the exact sum.
+    bound = (4 * unit + 2 * (depth + 8) * 2.0 ** -24) * magnitude + unit * np.abs(exact)
+    for _ in range(3):
+        got = widen(dtype, device_fused_sum(dtype, code.code, [identity_place(rows, cols)], [values], rows, cols,
+                                            axis))
+        assert np.all(np.abs(got - exact) <= bound)
+        assert np.all(np.abs(got - want) <= bound + (4 * unit + depth * 2.0 ** -24) * magnitude)
+
+
 @pytest.mark.parametrize("dtype", [lib.F32, lib.BF16])
 @pytest.mark.parametrize("rows,cols", [(300, 5000), (5000, 64), (33, 70), (7, 100000)],
                          ids=["wide", "tall-split-rows", "ragged", "few-rows"])
