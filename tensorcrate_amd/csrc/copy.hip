@@ -210,9 +210,12 @@ __global__ void __launch_bounds__(256) tile_kernel(const T* __restrict__ src, T*
 // exchange would, and no padding: the 16-byte chunks of tile row r sit at
 // chunk ^ ((r / 4) % 16), which puts the 16 rows a quarter-wave reads on
 // distinct bank groups in the second phase and permutes a row's chunks in
-// the first (the period is the smaller of a row's chunks and TB / 4).  Needs every extent, offset and stride that steps along a
-// vector to be a multiple of 4, which the host checks; NT marks a transpose
-// that streams past the Infinity Cache.
+// the first (the period is the smaller of a row's chunks and TB / 4).
+// Needs every extent, offset and stride that steps along a vector to be a
+// multiple of 4, which the host checks.  NT marks a transpose that streams
+// past the Infinity Cache: its loads are non-temporal, its stores plain
+// (config-3 permute of [256, 512, 512] f32: 5.99 TB/s with both streamed,
+// 6.50 with plain stores).
 template <typename I, bool NT, int TA, int TB>
 __global__ void __launch_bounds__(256) tile4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
                                                     TileLayout<I> t, I tiles) {
@@ -296,10 +299,10 @@ __global__ void __launch_bounds__(256) tile4_kernel(const uint32_t* __restrict__
             const I aa = here.a0 + ca * 4;
             uint32_t* out = dst + here.to + b + aa * t.dst_a;
             if (b < t.extent_b) {
-                if (aa < t.extent_a) store_word<NT>(out, uint4{q[0].x, q[1].x, q[2].x, q[3].x});
-                if (aa + 1 < t.extent_a) store_word<NT>(out + t.dst_a, uint4{q[0].y, q[1].y, q[2].y, q[3].y});
-                if (aa + 2 < t.extent_a) store_word<NT>(out + 2 * t.dst_a, uint4{q[0].z, q[1].z, q[2].z, q[3].z});
-                if (aa + 3 < t.extent_a) store_word<NT>(out + 3 * t.dst_a, uint4{q[0].w, q[1].w, q[2].w, q[3].w});
+                if (aa < t.extent_a) store_word<false>(out, uint4{q[0].x, q[1].x, q[2].x, q[3].x});
+                if (aa + 1 < t.extent_a) store_word<false>(out + t.dst_a, uint4{q[0].y, q[1].y, q[2].y, q[3].y});
+                if (aa + 2 < t.extent_a) store_word<false>(out + 2 * t.dst_a, uint4{q[0].z, q[1].z, q[2].z, q[3].z});
+                if (aa + 3 < t.extent_a) store_word<false>(out + 3 * t.dst_a, uint4{q[0].w, q[1].w, q[2].w, q[3].w});
             }
         }
         if (next >= tiles) break;
@@ -407,11 +410,12 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
         // measured on MI355X over ten shapes from 2048^2 to [1024, 256, 256],
         // streaming, with inputs and outputs both cold, they averaged 5.55
         // TB/s against 5.46 for 128 x 64 and 5.49 for 256 x 32 (the config-3
-        // permute 5.89 against 5.69).  Streaming beat plain accesses on every
-        // shape there, but writing into a target that is still in the
-        // Infinity Cache it loses (a 4096^2 transpose into one reused target:
-        // 4.86 against 5.18 TB/s), so, as for every copy, only traffic past
-        // that cache streams.
+        // permute 5.89 against 5.69).  Streaming both sides beat plain
+        // accesses on every shape there, but writing into a target that is
+        // still in the Infinity Cache it loses (a 4096^2 transpose into one
+        // reused target: 4.86 against 5.18 TB/s), and streamed loads with
+        // plain stores beat both (the kernel's stores are now always plain);
+        // as for every copy, only traffic past that cache streams.
         constexpr int TA = 64, TB = 128;
         const bool stream_tiles = stream;
         uint64_t blocks = tiled(TA, TB);
