@@ -227,7 +227,9 @@ uint64_t dense_chunk_bytes(const tc_encoded* code, uint32_t count) {
 
 // The generated source of a dense program, and the order its constants
 // take in `CompiledArgs::constants`.  A streaming program (one whose traffic
-// exceeds the Infinity Cache) loads and stores with nontemporal hints.
+// exceeds the Infinity Cache) loads with nontemporal hints and stores
+// plainly (the Adam update over 25 M f32 parameters: 6.06 -> 6.64 TB/s
+// against nontemporal stores).
 std::string dense_source(const tc_encoded* code, uint32_t count, uint32_t dtype, bool stream,
                          std::vector<float>* constants) {
     static const char* const kRound[] = {"tc_round<0>", "tc_round<1>", "tc_round<2>"};
@@ -237,7 +239,7 @@ std::string dense_source(const tc_encoded* code, uint32_t count, uint32_t dtype,
     src << "#include \"scalar_ops.h\"\n"
         << "typedef float tc_f4 __attribute__((ext_vector_type(4)));\n"
         << "typedef unsigned tc_u2 __attribute__((ext_vector_type(2)));\n"
-        << (stream ? "#define TC_LD(p) __builtin_nontemporal_load(p)\n#define TC_ST(v, p) __builtin_nontemporal_store(v, p)\n"
+        << (stream ? "#define TC_LD(p) __builtin_nontemporal_load(p)\n#define TC_ST(v, p) (*(p) = (v))\n"
                    : "#define TC_LD(p) (*(p))\n#define TC_ST(v, p) (*(p) = (v))\n")
         << "struct Args { const void* in[" << kDenseLoads << "]; void* out[" << TC_FUSED_MAX_OUTPUTS
         << "]; float constants[" << kCompiledConstants << "]; unsigned long long chunks; };\n"

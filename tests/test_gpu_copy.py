@@ -109,6 +109,15 @@ def test_transpose_of_every_width():
             assert bits_equal(dst.download(dtype, x.size).reshape(cols, rows), oracle.transpose(x))
 
 
+def test_a_transpose_past_the_infinity_cache():
+    # 8192 x 8192 f32 moves 512 MiB: the tiled kernel streams its loads and
+    # stores plainly; the bits are numpy's transpose.
+    x = np.random.default_rng(8).standard_normal((8192, 8192), dtype=np.float32)
+    src, dst = lib.Buffer.of(x), lib.Buffer(x.nbytes)
+    lib.call("tc_transpose", 4, 8192, 8192, src.ptr, dst.ptr)
+    assert bits_equal(dst.download(np.float32, x.size).reshape(8192, 8192), x.T)
+
+
 def test_a_layout_past_its_storage_is_refused():
     x = Tensor.from_numpy(np.zeros(10, np.float32))
     with pytest.raises(lib.HipError, match="reaches past 10 elements"):

@@ -52,6 +52,18 @@ def test_same_shape_operations_are_bit_exact(kind, n):
     assert same(widen(kind, out.download(host, n)), widen(kind, oracle.clamp(kind, a, -1.0, 2.0)))
 
 
+@pytest.mark.parametrize("kind,n", [(lib.F32, (24 << 20) + 3), (lib.BF16, (48 << 20) + 5)])
+def test_same_shape_operations_past_the_infinity_cache(kind, n):
+    # Three operands of 96 MiB or more stream (non-temporal loads, plain
+    # stores); the bits are the oracle's, tail elements included.
+    a, b = inputs(kind, n, 3)
+    da, db = lib.Buffer.of(a), lib.Buffer.of(b)
+    out = lib.Buffer(a.nbytes)
+    for op in ARITH:
+        lib.call("tc_elementwise", kind, op, da.ptr, db.ptr, out.ptr, n)
+        assert same_bits(out.download(a.dtype, n), oracle.elementwise(kind, lib.ARITHMETIC, op, a, b), kind), op
+
+
 def test_unaligned_operands():
     # Views into the middle of a buffer: the element path, still exact.
     a, b = inputs(lib.F32, 1000, 5)
