@@ -403,8 +403,8 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
             return tiles_a * tiles_b * batches;
         };
         // Four-byte elements whose rows start on 16-byte boundaries move 16
-        // bytes a lane; a block walks several tiles, at most eight blocks a
-        // CU.  64 x 128 tiles (256-byte reads and 512-byte writes per row):
+        // bytes a lane; a block walks several tiles.  Streaming transposes
+        // take 64 x 128 tiles (256-byte reads and 512-byte writes per row):
         // measured on MI355X over ten shapes from 2048^2 to [1024, 256, 256],
         // streaming, with inputs and outputs both cold, they averaged 5.55
         // TB/s against 5.46 for 128 x 64 and 5.49 for 256 x 32 (the config-3
@@ -413,10 +413,13 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
         // still in the Infinity Cache it loses (a 4096^2 transpose into one
         // reused target: 4.86 against 5.18 TB/s), and streamed loads with
         // plain stores beat both (the kernel's stores are now always plain);
-        // as for every copy, only traffic past that cache streams.
-        constexpr int TA = 64, TB = 128;
+        // as for every copy, only traffic past that cache streams.  Smaller
+        // transposes take 64 x 64 tiles, twice the blocks for the same work:
+        // 4096^2 5.22 -> 5.55 TB/s, 2048^2 4.05 -> 4.29, 2048 x 8192 5.55 ->
+        // 5.42; 32 x 128 and 128 x 64 measured slower than both.
         const bool stream_tiles = stream;
-        uint64_t blocks = tiled(TA, TB);
+        const int ta = 64, tb = stream_tiles ? 128 : 64;
+        uint64_t blocks = tiled(ta, tb);
         bool wide = sizeof(T) == 4 && blocks <= UINT32_MAX && walk.shape[axis_a] % 4 == 0 &&
                     walk.shape[axis_b] % 4 == 0 && walk.strides[0][axis_b] % 4 == 0 &&
                     walk.strides[1][axis_a] % 4 == 0 && aligned16(src) && aligned16(dst);
@@ -424,17 +427,19 @@ int launch_copy(const T* src, T* dst, const Walk<2>& walk, uint64_t count, bool 
         if (wide) {
             const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
             uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-            // As many blocks as are resident at once (the tile's 32 KiB of
-            // LDS leaves room for five a CU), each walking the same number of
-            // tiles, so no second round runs part-empty: 2048 tiles take
-            // 1024 blocks of two rather than 1280 blocks and then 768.
-            const uint64_t resident = 5 * static_cast<uint64_t>(compute_units());
+            // At most four blocks a CU for the 64 x 128 tiles (32 KiB of LDS
+            // each), eight for 64 x 64 (16 KiB), each block walking the same
+            // number of tiles, so no second round runs part-empty.  Four
+            // rather than the five that fit: 8192^2 transpose 6.44 -> 6.70
+            // TB/s, config-3 permute 6.52 -> 6.67 (8192 tiles: 1024 blocks of
+            // eight, four on every CU, rather than 1171 of seven).
+            const uint64_t resident = (stream_tiles ? 4 : 8) * static_cast<uint64_t>(compute_units());
             const uint64_t per_block = (blocks + resident - 1) / resident;
             const uint32_t grid = static_cast<uint32_t>((blocks + per_block - 1) / per_block);
             if (stream_tiles) {
-                tile4_kernel<I, true, TA, TB><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
+                tile4_kernel<I, true, 64, 128><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
             } else {
-                tile4_kernel<I, false, TA, TB><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
+                tile4_kernel<I, false, 64, 64><<<grid, 256, 0, s>>>(s32, d32, t, static_cast<I>(blocks));
             }
             return check_launch("strided copy");
         }
